@@ -1,0 +1,363 @@
+/*
+ * race_oracle.c -- CPU fp64 restatement of the RACE attention operator ("F1",
+ * per-bucket normalised) and of the reference CPU prefix-mean kernel.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP path of
+ * race_attention_amd is compared against.  Only tests/, __graft_entry__.smoke()
+ * and the cpu_baseline leg of bench.py may load it.  The product never links,
+ * imports or falls back to it.
+ *
+ * Reference semantics restated (paths relative to the reference repository):
+ *   misc/race.py:63-142      causal BatchedACE.forward
+ *   misc/vit.py:918-978      non-causal BatchedACE.forward
+ *   misc/race.py:54-58       corner prototypes = itertools.product([-1,+1], K)
+ *   misc/race.py:101-105     logits = (tanh(proj)/scale) @ protos_T ; softmax over R
+ *   misc/race.py:107-110     A = cumsum P_K ; B = cumsum P_K*v ; E = B/(A+1e-6)
+ *   misc/race.py:135-138     out_t = sum over all S=L*R buckets of P_Q * E
+ *   kernels/cpu/race_pref.cpp:36-101   prefix mean forward (fp64 accumulators)
+ *   kernels/cpu/race_pref.cpp:104-220  prefix mean backward (two passes)
+ *
+ * Layout used here: streams are independent; every per-stream tensor is
+ * [T][D] row-major double.  planes are [NP][L][K][D]; stream n uses planes
+ * block plane_of[n].  All arithmetic is double.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ORACLE_MAX_K 16
+
+/* Corner r of {-1,+1}^K in itertools.product order: the last coordinate
+ * varies fastest, so coordinate k is +1 iff bit (K-1-k) of r is set
+ * (misc/race.py:54-58). */
+static inline double corner_sign(int r, int k, int K)
+{
+    return ((r >> (K - 1 - k)) & 1) ? 1.0 : -1.0;
+}
+
+/* Soft hash of one token (misc/race.py:79-105): th[l*K+k] = tanh(<x, w_lk>),
+ * u = th*inv_temp, P[l*R+r] = softmax_r(sum_k c[r,k] u_k).  The softmax is the
+ * max-subtracted exponential form of F.softmax. */
+static void soft_hash(const double *x, const double *pl, int64_t D, int L, int K,
+                      double inv_temp, double *th, double *P)
+{
+    const int R = 1 << K;
+    for (int l = 0; l < L; ++l) {
+        double u[ORACLE_MAX_K];
+        for (int k = 0; k < K; ++k) {
+            const double *w = pl + ((int64_t)l * K + k) * D;
+            double acc = 0.0;
+            for (int64_t d = 0; d < D; ++d)
+                acc += x[d] * w[d];
+            th[l * K + k] = tanh(acc);
+            u[k] = th[l * K + k] * inv_temp;
+        }
+        double mx = -INFINITY;
+        for (int r = 0; r < R; ++r) {
+            double z = 0.0;
+            for (int k = 0; k < K; ++k)
+                z += corner_sign(r, k, K) * u[k];
+            P[l * R + r] = z;
+            if (z > mx)
+                mx = z;
+        }
+        double sum = 0.0;
+        for (int r = 0; r < R; ++r) {
+            P[l * R + r] = exp(P[l * R + r] - mx);
+            sum += P[l * R + r];
+        }
+        for (int r = 0; r < R; ++r)
+            P[l * R + r] /= sum;
+    }
+}
+
+/* Backward of soft_hash given dP: softmax backward, corner matmul backward,
+ * tanh backward, projection backward.  Adds into dx[D]; adds
+ * sum(du * th) into *g_inv_temp (du/d inv_temp = th). */
+static void soft_hash_bwd(const double *P, const double *th, const double *dP,
+                          const double *pl, int64_t D, int L, int K,
+                          double inv_temp, double *dx, double *g_inv_temp)
+{
+    const int R = 1 << K;
+    for (int l = 0; l < L; ++l) {
+        double dot = 0.0;
+        for (int r = 0; r < R; ++r)
+            dot += P[l * R + r] * dP[l * R + r];
+        for (int k = 0; k < K; ++k) {
+            double du = 0.0;
+            for (int r = 0; r < R; ++r)
+                du += P[l * R + r] * (dP[l * R + r] - dot) * corner_sign(r, k, K);
+            const double t = th[l * K + k];
+            *g_inv_temp += du * t;
+            const double dproj = du * inv_temp * (1.0 - t * t);
+            const double *w = pl + ((int64_t)l * K + k) * D;
+            for (int64_t d = 0; d < D; ++d)
+                dx[d] += dproj * w[d];
+        }
+    }
+}
+
+/* Forward of one stream.  Causal: per-token prefix state (misc/race.py:107-110,
+ * kernels/cpu/race_pref.cpp:82-98).  Non-causal: full-sequence state
+ * (misc/vit.py:962-975). */
+static void stream_forward(const double *q, const double *k, const double *v,
+                           const double *pl, int64_t T, int64_t D, int L, int K,
+                           int causal, double eps, double inv_temp, double *o)
+{
+    const int R = 1 << K;
+    const int64_t S = (int64_t)L * R;
+    double *A = calloc((size_t)S, sizeof(double));
+    double *B = calloc((size_t)(S * D), sizeof(double));
+    double *th = malloc(sizeof(double) * (size_t)(L * K));
+    double *PK = malloc(sizeof(double) * (size_t)S);
+    double *PQ = malloc(sizeof(double) * (size_t)S);
+
+    if (!causal) {
+        for (int64_t t = 0; t < T; ++t) {
+            soft_hash(k + t * D, pl, D, L, K, inv_temp, th, PK);
+            for (int64_t s = 0; s < S; ++s) {
+                A[s] += PK[s];
+                for (int64_t d = 0; d < D; ++d)
+                    B[s * D + d] += PK[s] * v[t * D + d];
+            }
+        }
+    }
+    for (int64_t t = 0; t < T; ++t) {
+        if (causal) {
+            soft_hash(k + t * D, pl, D, L, K, inv_temp, th, PK);
+            for (int64_t s = 0; s < S; ++s) {
+                A[s] += PK[s];
+                for (int64_t d = 0; d < D; ++d)
+                    B[s * D + d] += PK[s] * v[t * D + d];
+            }
+        }
+        soft_hash(q + t * D, pl, D, L, K, inv_temp, th, PQ);
+        double *ot = o + t * D;
+        for (int64_t d = 0; d < D; ++d)
+            ot[d] = 0.0;
+        for (int64_t s = 0; s < S; ++s) {
+            const double w = PQ[s] / (A[s] + eps);
+            for (int64_t d = 0; d < D; ++d)
+                ot[d] += w * B[s * D + d];
+        }
+    }
+    free(A); free(B); free(th); free(PK); free(PQ);
+}
+
+/* Backward of one stream.  With W = P_Q/(A+eps) and G[t,s] = g_t . B_s(t):
+ *   dP_Q[t,s] = G/(A+eps)
+ *   dA[t,s]   = -W G/(A+eps)
+ *   alpha_s(tau) = sum_{t>=tau} dA[t,s],  U_s(tau) = sum_{t>=tau} W[t,s] g_t
+ *   dP_K[tau,s]  = alpha_s(tau) + v_tau . U_s(tau)
+ *   dv_tau       = sum_s P_K[tau,s] U_s(tau)
+ * (the two-pass alpha/beta scheme of kernels/cpu/race_pref.cpp:154-216 applied
+ * to every bucket; non-causal sums run over the whole sequence). */
+static void stream_backward(const double *q, const double *k, const double *v,
+                            const double *g, const double *pl, int64_t T,
+                            int64_t D, int L, int K, int causal, double eps,
+                            double inv_temp, double *dq, double *dk, double *dv,
+                            double *g_it)
+{
+    const int R = 1 << K;
+    const int64_t S = (int64_t)L * R;
+    double *A = calloc((size_t)S, sizeof(double));
+    double *B = calloc((size_t)(S * D), sizeof(double));
+    double *dA = malloc(sizeof(double) * (size_t)(T * S));
+    double *W = malloc(sizeof(double) * (size_t)(T * S));
+    double *th = malloc(sizeof(double) * (size_t)(L * K));
+    double *PK = malloc(sizeof(double) * (size_t)S);
+    double *PQ = malloc(sizeof(double) * (size_t)S);
+    double *dP = malloc(sizeof(double) * (size_t)S);
+    double *alpha = calloc((size_t)S, sizeof(double));
+    double *U = calloc((size_t)(S * D), sizeof(double));
+
+    memset(dq, 0, sizeof(double) * (size_t)(T * D));
+    memset(dk, 0, sizeof(double) * (size_t)(T * D));
+    memset(dv, 0, sizeof(double) * (size_t)(T * D));
+
+    if (!causal) {
+        for (int64_t t = 0; t < T; ++t) {
+            soft_hash(k + t * D, pl, D, L, K, inv_temp, th, PK);
+            for (int64_t s = 0; s < S; ++s) {
+                A[s] += PK[s];
+                for (int64_t d = 0; d < D; ++d)
+                    B[s * D + d] += PK[s] * v[t * D + d];
+            }
+        }
+    }
+    /* pass 1 (forward in t): state, dP_Q -> dq, dA and W per token */
+    for (int64_t t = 0; t < T; ++t) {
+        if (causal) {
+            soft_hash(k + t * D, pl, D, L, K, inv_temp, th, PK);
+            for (int64_t s = 0; s < S; ++s) {
+                A[s] += PK[s];
+                for (int64_t d = 0; d < D; ++d)
+                    B[s * D + d] += PK[s] * v[t * D + d];
+            }
+        }
+        soft_hash(q + t * D, pl, D, L, K, inv_temp, th, PQ);
+        const double *gt = g + t * D;
+        for (int64_t s = 0; s < S; ++s) {
+            const double inv = 1.0 / (A[s] + eps);
+            double G = 0.0;
+            for (int64_t d = 0; d < D; ++d)
+                G += gt[d] * B[s * D + d];
+            dP[s] = G * inv;
+            W[t * S + s] = PQ[s] * inv;
+            dA[t * S + s] = -PQ[s] * inv * G * inv;
+        }
+        soft_hash_bwd(PQ, th, dP, pl, D, L, K, inv_temp, dq + t * D, g_it);
+    }
+    if (!causal) {
+        for (int64_t t = 0; t < T; ++t) {
+            const double *gt = g + t * D;
+            for (int64_t s = 0; s < S; ++s) {
+                alpha[s] += dA[t * S + s];
+                for (int64_t d = 0; d < D; ++d)
+                    U[s * D + d] += W[t * S + s] * gt[d];
+            }
+        }
+    }
+    /* pass 2 (reverse in t): suffix sums alpha, U -> dP_K -> dk, dv */
+    for (int64_t t = T - 1; t >= 0; --t) {
+        const double *gt = g + t * D;
+        const double *vt = v + t * D;
+        if (causal) {
+            for (int64_t s = 0; s < S; ++s) {
+                alpha[s] += dA[t * S + s];
+                for (int64_t d = 0; d < D; ++d)
+                    U[s * D + d] += W[t * S + s] * gt[d];
+            }
+        }
+        soft_hash(k + t * D, pl, D, L, K, inv_temp, th, PK);
+        double *dvt = dv + t * D;
+        for (int64_t s = 0; s < S; ++s) {
+            double vu = 0.0;
+            for (int64_t d = 0; d < D; ++d) {
+                vu += vt[d] * U[s * D + d];
+                dvt[d] += PK[s] * U[s * D + d];
+            }
+            dP[s] = alpha[s] + vu;
+        }
+        soft_hash_bwd(PK, th, dP, pl, D, L, K, inv_temp, dk + t * D, g_it);
+    }
+    free(A); free(B); free(dA); free(W); free(th); free(PK); free(PQ);
+    free(dP); free(alpha); free(U);
+}
+
+/* ---------------------------------------------------------------- exports */
+
+int oracle_race_forward(const double *q, const double *k, const double *v,
+                        const double *planes, const int64_t *plane_of,
+                        int64_t N, int64_t T, int64_t D, int L, int K,
+                        int causal, double eps, double inv_temp, double *out)
+{
+    if (K < 1 || K > ORACLE_MAX_K || L < 1 || N < 0 || T < 0 || D < 1)
+        return -1;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t n = 0; n < N; ++n) {
+        const double *pl = planes + plane_of[n] * (int64_t)L * K * D;
+        stream_forward(q + n * T * D, k + n * T * D, v + n * T * D, pl, T, D,
+                       L, K, causal, eps, inv_temp, out + n * T * D);
+    }
+    return 0;
+}
+
+int oracle_race_backward(const double *q, const double *k, const double *v,
+                         const double *dout, const double *planes,
+                         const int64_t *plane_of, int64_t N, int64_t T,
+                         int64_t D, int L, int K, int causal, double eps,
+                         double inv_temp, double *dq, double *dk, double *dv,
+                         double *grad_inv_temp)
+{
+    if (K < 1 || K > ORACLE_MAX_K || L < 1 || N < 0 || T < 0 || D < 1)
+        return -1;
+    double *part = calloc((size_t)(N > 0 ? N : 1), sizeof(double));
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t n = 0; n < N; ++n) {
+        const double *pl = planes + plane_of[n] * (int64_t)L * K * D;
+        const int64_t o = n * T * D;
+        stream_backward(q + o, k + o, v + o, dout + o, pl, T, D, L, K, causal,
+                        eps, inv_temp, dq + o, dk + o, dv + o, &part[n]);
+    }
+    double tot = 0.0;
+    for (int64_t n = 0; n < N; ++n)
+        tot += part[n];
+    if (grad_inv_temp)
+        *grad_inv_temp = tot;
+    free(part);
+    return 0;
+}
+
+/* Restatement of race_prefix_mean_flat (kernels/cpu/race_pref.cpp:36-101):
+ * w [NS][T], v [NS][T][D] float; E[ns,t,:] = B_t/(A_t+eps) with fp64 running
+ * sums A_t = sum_{tau<=t} w, B_t = sum_{tau<=t} w v. */
+void oracle_prefix_mean_flat(const float *w, const float *v, int64_t NS,
+                             int64_t T, int64_t D, double eps, float *E)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t ns = 0; ns < NS; ++ns) {
+        double A = 0.0;
+        double *B = calloc((size_t)D, sizeof(double));
+        const float *wn = w + ns * T;
+        const float *vn = v + ns * T * D;
+        float *en = E + ns * T * D;
+        for (int64_t t = 0; t < T; ++t) {
+            const double wt = (double)wn[t];
+            A += wt;
+            const double inv = 1.0 / (A + eps);
+            for (int64_t d = 0; d < D; ++d) {
+                B[d] += wt * (double)vn[t * D + d];
+                en[t * D + d] = (float)(B[d] * inv);
+            }
+        }
+        free(B);
+    }
+}
+
+/* Restatement of race_prefix_mean_flat_bw (kernels/cpu/race_pref.cpp:104-220):
+ * pass 1 forward builds invA[t] and alpha[t] = -invA^2 (g_t . B_t); pass 2
+ * reverse keeps suffix sums beta = sum g invA and a = sum alpha, giving
+ * gW[t] = a + beta . v_t and gV[t] = w_t beta. */
+void oracle_prefix_mean_flat_bw(const float *w, const float *v, const float *gE,
+                                int64_t NS, int64_t T, int64_t D, double eps,
+                                float *gW, float *gV)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t ns = 0; ns < NS; ++ns) {
+        const float *wn = w + ns * T;
+        const float *vn = v + ns * T * D;
+        const float *gn = gE + ns * T * D;
+        double *invA = malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
+        double *al = malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
+        double *B = calloc((size_t)D, sizeof(double));
+        double *beta = calloc((size_t)D, sizeof(double));
+        double A = 0.0;
+        for (int64_t t = 0; t < T; ++t) {
+            const double wt = (double)wn[t];
+            A += wt;
+            double gb = 0.0;
+            for (int64_t d = 0; d < D; ++d) {
+                B[d] += wt * (double)vn[t * D + d];
+                gb += (double)gn[t * D + d] * B[d];
+            }
+            invA[t] = 1.0 / (A + eps);
+            al[t] = -invA[t] * invA[t] * gb;
+        }
+        double asuf = 0.0;
+        for (int64_t t = T - 1; t >= 0; --t) {
+            double bv = 0.0;
+            for (int64_t d = 0; d < D; ++d) {
+                beta[d] += (double)gn[t * D + d] * invA[t];
+                bv += beta[d] * (double)vn[t * D + d];
+            }
+            asuf += al[t];
+            gW[ns * T + t] = (float)(asuf + bv);
+            const double wt = (double)wn[t];
+            for (int64_t d = 0; d < D; ++d)
+                gV[(ns * T + t) * D + d] = (float)(wt * beta[d]);
+        }
+        free(invA); free(al); free(B); free(beta);
+    }
+}
