@@ -1,0 +1,279 @@
+#!/usr/bin/env python3
+"""Benchmark: causal RACE layer forward+backward tokens/s on one MI355X.
+
+Workload (the metric's "N=1M causal" case): one RACE
+attention layer core, B=1, H=8, N=2^20 tokens, d=64, bf16 inputs/outputs with
+fp32 accumulation, K=4 hash bits (16 buckets per table), L=8 tables, M=1,
+temperature sqrt(d).  Inputs are synthetic: Q, K, V ~ N(0,1) row-normalised to
+unit L2 norm, dO ~ N(0,1), hyperplanes ~ N(0,1) (seeds 0 and 1234), resident in
+HBM before the timed region.
+
+A step is one race_fwd + race_bwd through the C ABI (six kernels: forward
+segment reduce, scan, output; backward reduce, scan, output).  Every kernel is
+enqueued on torch's current stream with HIP events between them, so the
+per-kernel average durations (and the roofline of the dominant kernel) come
+from the timed region itself.  The CPU baseline times the reference's own CPU
+path (aten + kernels/cpu/race_pref.cpp compiled from source) on a bounded
+sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--seq N] [--no-cpu-baseline] [--max-n]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "RACE layer fwd+bwd tokens/s at N=1M causal; % of HBM/MFMA roofline"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
+
+PHASES = (("fwd_reduce", "fwd", 1), ("fwd_scan", "fwd", 2), ("fwd_out", "fwd", 4),
+          ("bwd_reduce", "bwd", 1), ("bwd_scan", "bwd", 2), ("bwd_out", "bwd", 4))
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--seq", type=int, default=1 << 20, help="tokens per sequence (default 2^20)")
+    ap.add_argument("--heads", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=65536, help="tokens of one head timed on the CPU")
+    ap.add_argument("--max-n", action="store_true", help="also bisect the longest sequence that fits in HBM")
+    return ap.parse_args()
+
+
+def make_inputs(B, T, H, D, L, K, dev, seed=0):
+    import torch
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    out = []
+    for _ in range(3):  # Q, K, V generated in chunks to bound host memory
+        x = torch.empty(B, T, H, D, dtype=torch.bfloat16, device=dev)
+        step = 1 << 18
+        for t0 in range(0, T, step):
+            t1 = min(T, t0 + step)
+            c = torch.randn(B, t1 - t0, H, D, generator=g)
+            x[:, t0:t1] = torch.nn.functional.normalize(c, dim=-1).to(torch.bfloat16).to(dev)
+        out.append(x.unsqueeze(0))
+    do = torch.empty(1, B, T, H, D, dtype=torch.bfloat16, device=dev)
+    step = 1 << 18
+    for t0 in range(0, T, step):
+        t1 = min(T, t0 + step)
+        do[0, :, t0:t1] = torch.randn(B, t1 - t0, H, D, generator=g).to(torch.bfloat16).to(dev)
+    gp = torch.Generator(device="cpu").manual_seed(1234)
+    planes = torch.randn(1, L, K, D, generator=gp).to(dev)
+    return out[0], out[1], out[2], do, planes
+
+
+class Step:
+    """Pre-allocated buffers and descriptors for one fwd+bwd through the C ABI."""
+
+    def __init__(self, q, k, v, do, planes, L, K):
+        import torch
+        from race_attention_amd import _lib
+        from race_attention_amd.functional import make_desc, _strides4
+        self.lib = _lib.load()
+        self.q, self.k, self.v, self.do, self.planes = q, k, v, do, planes.float().contiguous()
+        self.d = make_desc(q, k, v, self.planes, L=L, K=K, causal=True, eps=1e-6, inv_temp=1.0 / math.sqrt(q.shape[-1]))
+        self.out = torch.empty_like(q)
+        self.dq, self.dk, self.dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+        self.d.o_stride = _strides4(self.out)
+        self.d.do_stride = _strides4(do)
+        self.d.g_stride = _strides4(self.dq)
+        ref = ctypes.byref(self.d)
+        sb, fw, bw = (self.lib.race_state_bytes(ref), self.lib.race_fwd_workspace_bytes(ref),
+                      self.lib.race_bwd_workspace_bytes(ref))
+        if sb == 0:
+            _lib.check(-1, "race_state_bytes")
+        self.state = torch.empty(sb, dtype=torch.uint8, device=q.device)
+        self.ws = torch.empty(max(fw, bw), dtype=torch.uint8, device=q.device)
+        self.git = torch.empty((), dtype=torch.float32, device=q.device)
+        self.check = _lib.check
+        P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        self.fargs = (P(q), P(k), P(v), P(self.planes), P(self.out), P(self.state), P(self.ws),
+                      ctypes.c_size_t(self.ws.numel()))
+        self.bargs = (P(q), P(k), P(v), P(self.planes), P(do), P(self.state), P(self.dq), P(self.dk), P(self.dv),
+                      P(self.git), P(self.ws), ctypes.c_size_t(self.ws.numel()))
+
+    def run(self, phases=0, which="both"):
+        import torch
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        self.d.phases = phases
+        if which in ("both", "fwd"):
+            self.check(self.lib.race_fwd(ctypes.byref(self.d), *self.fargs, st), "race_fwd")
+        if which in ("both", "bwd"):
+            self.check(self.lib.race_bwd(ctypes.byref(self.d), *self.bargs, st), "race_bwd")
+        self.d.phases = 0
+
+
+def algorithmic_bytes(name, tok_heads, D, esize):
+    """Compulsory HBM bytes of each kernel: token tensors it must read/write."""
+    unit = tok_heads * D * esize
+    return {"fwd_reduce": 2, "fwd_out": 4, "bwd_reduce": 5, "bwd_out": 6}.get(name, 0) * unit
+
+
+def cpu_baseline(sample_T, H_full, D=64, L=8, K=4, reps=3):
+    """Reference CPU path (aten + race_pref.cpp from source) on one head of
+    sample_T tokens of the same workload; reported as tokens/s of the full
+    H-head layer.  Falls back to the fp64 C restatement if oracle/_ref is absent."""
+    import torch
+    from oracle import race_oracle
+    q, k, v, do, planes = make_inputs(1, sample_T, 1, D, L, K, "cpu", seed=7)
+    threads = torch.get_num_threads()
+    ext = race_oracle.ref_race_pref()
+    times = []
+    if ext is not None:
+        from oracle import ref_cpu_path
+        planes_T = planes[0].reshape(L * K, D).T.contiguous().float()
+        Kf, Vf, Qf = [x.float().requires_grad_(True) for x in (k, v, q)]
+        for r in range(reps + 1):
+            for x in (Kf, Vf, Qf):
+                x.grad = None
+            t0 = time.perf_counter()
+            out = ref_cpu_path.causal_forward(Kf, Vf, Qf, planes_T, K, L, ext=ext)
+            out.backward(do.float())
+            if r > 0:
+                times.append(time.perf_counter() - t0)
+        kind = "reference"
+        what = "misc/race.py CPU path: aten projection/softmax/readout + kernels/cpu/race_pref.cpp (built from source)"
+    else:
+        from oracle import race_oracle as ro
+        import numpy as np
+        arrs = [x.double().numpy() for x in (q, k, v, do)]
+        pl = planes.double().numpy()
+        for r in range(reps + 1):
+            t0 = time.perf_counter()
+            ro.race_forward(arrs[0], arrs[1], arrs[2], pl, causal=True, inv_temp=1 / math.sqrt(D))
+            ro.race_backward(*arrs, pl, causal=True, inv_temp=1 / math.sqrt(D))
+            if r > 0:
+                times.append(time.perf_counter() - t0)
+        kind = "port"
+        what = "fp64 C restatement (oracle/race_oracle.c), one thread per stream"
+        threads = 1
+    t = statistics.median(times)
+    return {"value": sample_T / t / H_full, "unit": "tokens/s", "cores": threads, "kind": kind,
+            "sample": f"1 of {H_full} heads x {sample_T} tokens of the same causal K=4 L=8 d=64 workload, "
+                      f"fwd+bwd, median of {reps} after 1 warm-up ({what}); {t:.2f} s per sample; "
+                      f"value scaled to tokens of the {H_full}-head layer",
+            "host_cpus": os.cpu_count()}
+
+
+def max_seq_bisect(H, D, L, K, dev, limit_tokens=1 << 27):
+    """Longest T (multiple of 2^16) whose full fwd+bwd buffers fit and run."""
+    import torch
+
+    def fits(T):
+        try:
+            q = torch.empty(1, 1, T, H, D, dtype=torch.bfloat16, device=dev).normal_()
+            st = Step(q, q, q, q, torch.randn(1, L, K, D, device=dev), L, K)
+            st.run()
+            torch.cuda.synchronize()
+            del st, q
+            return True
+        except (torch.cuda.OutOfMemoryError, RuntimeError):
+            return False
+        finally:
+            torch.cuda.empty_cache()
+
+    lo, hi = 1 << 20, None
+    T = lo
+    while T <= limit_tokens and fits(T):
+        lo = T
+        T *= 2
+    hi = T
+    while hi - lo > (1 << 16):
+        mid = (lo + hi) // 2 // (1 << 16) * (1 << 16)
+        if fits(mid):
+            lo = mid
+        else:
+            hi = mid
+    return lo
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (requested --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "the RACE operator shards by head/batch streams with no communication, and multi-GPU runs are "
+              "not part of this build", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    B, T, H, D, L, K = 1, args.seq, args.heads, 64, 8, 4
+    print(f"bench: generating inputs B={B} T={T} H={H} D={D}", file=sys.stderr, flush=True)
+    q, k, v, do, planes = make_inputs(B, T, H, D, L, K, dev)
+    step = Step(q, k, v, do, planes, L, K)
+    for _ in range(args.warmup):
+        step.run()
+    torch.cuda.synchronize()
+    print("bench: warm-up done", file=sys.stderr, flush=True)
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(PHASES) + 1)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        ev[s][0].record()
+        for j, (_, which, ph) in enumerate(PHASES):
+            step.run(phases=ph, which=which)
+            ev[s][j + 1].record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / args.steps
+    per = {name: statistics.mean(ev[s][j].elapsed_time(ev[s][j + 1]) for s in range(args.steps))
+           for j, (name, _, _) in enumerate(PHASES)}
+    tokens = B * T
+    value = tokens / (ms / 1e3)
+
+    tok_heads = B * T * H
+    kernels = {}
+    for name, t_ms in per.items():
+        ab = algorithmic_bytes(name, tok_heads, D, 2)
+        kernels[name] = {"ms": round(t_ms, 4),
+                         "algorithmic_GBs": round(ab / (t_ms * 1e-3) / 1e9, 1) if ab else None}
+    dom = max(per, key=per.get)
+    ab = algorithmic_bytes(dom, tok_heads, D, 2)
+    achieved = ab / (per[dom] * 1e-3) / 1e9
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{dom}_c4.txt")
+    if os.path.exists(tfile) and T == 1 << 20:
+        for ln in open(tfile):
+            if ln.startswith("hbm_bytes_per_launch"):
+                traffic = float(ln.split("=")[1])
+    all_bytes = 11 * tok_heads * D * 2
+    res = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (unit-L2 N(0,1) Q/K/V, N(0,1) dO and hyperplanes, seeds 0/1234)",
+        "config": {"workload": f"C4 causal RACE layer core fwd+bwd: B={B} H={H} N={T} d={D} K={K} L={L} M=1 bf16",
+                   "B": B, "H": H, "seq_len": T, "d": D, "K": K, "L": L, "M": 1, "causal": True},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "layer_roofline": {"algorithmic_bytes_per_step": all_bytes,
+                           "hbm_bound_tokens_per_s": round(tokens / (all_bytes / (HBM_PEAK_GBS * 1e9)), 1),
+                           "frac": round(value / (tokens / (all_bytes / (HBM_PEAK_GBS * 1e9))), 4)},
+        "kernels": kernels,
+    }
+    if args.max_n:
+        del step, q, k, v, do
+        torch.cuda.empty_cache()
+        res["max_seq_len_fwd_bwd"] = max_seq_bisect(H, D, L, K, dev)
+    if not args.no_cpu_baseline:
+        print("bench: CPU baseline", file=sys.stderr, flush=True)
+        res["cpu_baseline"] = cpu_baseline(args.cpu_sample, H)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,119 @@
+/*
+ * race_attention.h -- C ABI of the MI355X (gfx950) RACE attention operator.
+ *
+ * Plain C: pointers, sizes, int status codes, no C++ or torch types.  Every
+ * entry point returns RACE_OK (0) or a negative RACE_E_* code and leaves a
+ * thread-local message readable through race_last_error().  Calls are
+ * enqueued on the given HIP stream (a hipStream_t passed as void*; NULL is the
+ * default stream); they allocate nothing -- the caller passes the state and
+ * workspace buffers sized by the *_bytes queries.  Results are deterministic
+ * (no floating-point atomics).
+ *
+ * Semantics ("F1", per-bucket normalised RACE; misc/race.py:63-142 causal,
+ * misc/vit.py:918-978 non-causal, in the reference repository):
+ *   streams n = (m*B + b)*H + h over q/k/v [M,B,T,H,D];
+ *   th = tanh(<x, plane_{l,k}>), u = th * inv_temp,
+ *   P[t,l,r] = softmax_r(sum_k c[r,k] u_k) with c[r,k] = +1 iff bit (K-1-k) of r;
+ *   causal: A_s(t) = sum_{tau<=t} P_K, B_s(t) = sum_{tau<=t} P_K v;
+ *   non-causal: the same sums over all tau;
+ *   out_t = sum_{s < L*2^K} P_Q[t,s] B_s(t) / (A_s(t) + eps).
+ */
+#ifndef RACE_ATTENTION_H
+#define RACE_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RACE_OK 0
+#define RACE_E_INVALID (-1)     /* bad descriptor, shape, stride or pointer */
+#define RACE_E_UNSUPPORTED (-2) /* valid request outside what this build implements */
+#define RACE_E_WORKSPACE (-3)   /* workspace smaller than the *_bytes query */
+#define RACE_E_LAUNCH (-4)      /* HIP error when enqueuing a kernel */
+
+#define RACE_PHASE_REDUCE 1 /* k_fwd_reduce / k_bwd_reduce: per-segment sums */
+#define RACE_PHASE_SCAN 2   /* segment prefix (forward) / suffix (backward) scan */
+#define RACE_PHASE_OUT 4    /* k_fwd_out / k_bwd_out (+ temperature-gradient sum) */
+
+#define RACE_DTYPE_F32 0
+#define RACE_DTYPE_BF16 1
+
+/* Operator descriptor.  Strides are in elements, over the (M, B, T, H)
+ * dimensions of a [M,B,T,H,D] tensor whose D dimension is contiguous; a zero
+ * M stride expresses the reference's M-fold expand (misc/race.py:167-168). */
+typedef struct race_desc {
+    int64_t M, B, T, H, D;    /* estimators, batch, tokens, heads, head dim (D = 64) */
+    int32_t L, K;             /* hash tables, hash bits per table (R = 2^K buckets) */
+    int32_t causal;           /* 1: prefix (causal) aggregation, 0: full sequence */
+    int32_t dtype;            /* RACE_DTYPE_F32 or RACE_DTYPE_BF16 for q/k/v/out/grads */
+    float eps;                /* added to every bucket denominator (1e-6 in the reference) */
+    float inv_temp;           /* 1/tau: causal reference 1/sqrt(D), non-causal 1/exp(logit_temp) */
+    int64_t planes_m_stride;  /* fp32 elements between per-estimator [L][K][D] plane blocks; 0 = shared */
+    int64_t q_stride[4], k_stride[4], v_stride[4];
+    int64_t o_stride[4];      /* forward output */
+    int64_t do_stride[4];     /* upstream gradient */
+    int64_t g_stride[4];      /* dq, dk, dv */
+    int32_t seg_tiles;        /* 32-token tiles per scan segment; 0 = automatic */
+    int32_t phases;           /* 0 = run every kernel of the call; otherwise a bitmask of
+                                 RACE_PHASE_* to run a subset (per-kernel timing); subsets of
+                                 one call must be enqueued in phase order on one stream */
+} race_desc;
+
+/* Bytes of the forward->backward state buffer (per-segment prefix carries,
+ * fp64).  race_fwd writes it; race_bwd reads it. */
+size_t race_state_bytes(const race_desc *d);
+
+/* Scratch bytes needed by race_fwd / race_bwd. */
+size_t race_fwd_workspace_bytes(const race_desc *d);
+size_t race_bwd_workspace_bytes(const race_desc *d);
+
+/* Forward.  Replaces the body of BatchedACE.forward (misc/race.py:63-142;
+ * misc/vit.py:918-978) and the unbound fused CUDA forward
+ * race_fused_fwd (kernels/gpu/forward_kernel.cu:64-96), computing the
+ * projection and soft hash in-kernel instead of taking probabilities.
+ * planes: fp32 [L][K][D] (or [M][L][K][D] with planes_m_stride = L*K*D). */
+int race_fwd(const race_desc *d, const void *q, const void *k, const void *v,
+             const float *planes, void *out, void *state, void *ws,
+             size_t ws_bytes, void *stream);
+
+/* Backward.  Replaces the autograd backward of BatchedACE.forward and the CUDA
+ * backward pair race_bwd_kq_noscan / race_bwd_v_noscan
+ * (kernels/gpu/backward_kernels.cu:145-176, :232-256) and the CPU kernel's
+ * race_prefix_mean_flat_bw (kernels/cpu/race_pref.cpp:104-220), recomputing
+ * the bucket probabilities from q/k.  grad_inv_temp (nullable, device fp32
+ * scalar) receives dL/d(inv_temp). */
+int race_bwd(const race_desc *d, const void *q, const void *k, const void *v,
+             const float *planes, const void *dout, const void *state,
+             void *dq, void *dk, void *dv, float *grad_inv_temp, void *ws,
+             size_t ws_bytes, void *stream);
+
+/* Causal prefix mean over flat streams, the reference CPU kernel's operator
+ * (race_prefix_mean_flat, kernels/cpu/race_pref.cpp:36-101):
+ * w [NS][T], v [NS][T][D], E [NS][T][D], all fp32 contiguous;
+ * E[n,t,:] = (sum_{tau<=t} w v) / (sum_{tau<=t} w + eps). */
+size_t race_prefix_mean_workspace_bytes(int64_t NS, int64_t T, int64_t D);
+int race_prefix_mean_fwd(const float *w, const float *v, float *E, int64_t NS,
+                         int64_t T, int64_t D, double eps, void *ws,
+                         size_t ws_bytes, void *stream);
+
+/* Its backward (race_prefix_mean_flat_bw, kernels/cpu/race_pref.cpp:104-220):
+ * gW [NS][T], gV [NS][T][D] from gE [NS][T][D]. */
+int race_prefix_mean_bwd(const float *w, const float *v, const float *gE,
+                         float *gW, float *gV, int64_t NS, int64_t T,
+                         int64_t D, double eps, void *ws, size_t ws_bytes,
+                         void *stream);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *race_last_error(void);
+
+/* ABI version (increments on incompatible changes). */
+int race_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RACE_ATTENTION_H */

@@ -74,10 +74,12 @@ static void soft_hash(const double *x, const double *pl, int64_t D, int L, int K
 
 /* Backward of soft_hash given dP: softmax backward, corner matmul backward,
  * tanh backward, projection backward.  Adds into dx[D]; adds
- * sum(du * th) into *g_inv_temp (du/d inv_temp = th). */
+ * sum(du * th) into *g_inv_temp (du/d inv_temp = th) and sum |du * th| into
+ * *g_abs (the magnitude of the summands, the scale of that reduction). */
 static void soft_hash_bwd(const double *P, const double *th, const double *dP,
                           const double *pl, int64_t D, int L, int K,
-                          double inv_temp, double *dx, double *g_inv_temp)
+                          double inv_temp, double *dx, double *g_inv_temp,
+                          double *g_abs)
 {
     const int R = 1 << K;
     for (int l = 0; l < L; ++l) {
@@ -90,6 +92,7 @@ static void soft_hash_bwd(const double *P, const double *th, const double *dP,
                 du += P[l * R + r] * (dP[l * R + r] - dot) * corner_sign(r, k, K);
             const double t = th[l * K + k];
             *g_inv_temp += du * t;
+            *g_abs += fabs(du * t);
             const double dproj = du * inv_temp * (1.0 - t * t);
             const double *w = pl + ((int64_t)l * K + k) * D;
             for (int64_t d = 0; d < D; ++d)
@@ -157,7 +160,7 @@ static void stream_backward(const double *q, const double *k, const double *v,
                             const double *g, const double *pl, int64_t T,
                             int64_t D, int L, int K, int causal, double eps,
                             double inv_temp, double *dq, double *dk, double *dv,
-                            double *g_it)
+                            double *g_it, double *g_abs)
 {
     const int R = 1 << K;
     const int64_t S = (int64_t)L * R;
@@ -207,7 +210,7 @@ static void stream_backward(const double *q, const double *k, const double *v,
             W[t * S + s] = PQ[s] * inv;
             dA[t * S + s] = -PQ[s] * inv * G * inv;
         }
-        soft_hash_bwd(PQ, th, dP, pl, D, L, K, inv_temp, dq + t * D, g_it);
+        soft_hash_bwd(PQ, th, dP, pl, D, L, K, inv_temp, dq + t * D, g_it, g_abs);
     }
     if (!causal) {
         for (int64_t t = 0; t < T; ++t) {
@@ -240,7 +243,7 @@ static void stream_backward(const double *q, const double *k, const double *v,
             }
             dP[s] = alpha[s] + vu;
         }
-        soft_hash_bwd(PK, th, dP, pl, D, L, K, inv_temp, dk + t * D, g_it);
+        soft_hash_bwd(PK, th, dP, pl, D, L, K, inv_temp, dk + t * D, g_it, g_abs);
     }
     free(A); free(B); free(dA); free(W); free(th); free(PK); free(PQ);
     free(dP); free(alpha); free(U);
@@ -269,24 +272,30 @@ int oracle_race_backward(const double *q, const double *k, const double *v,
                          const int64_t *plane_of, int64_t N, int64_t T,
                          int64_t D, int L, int K, int causal, double eps,
                          double inv_temp, double *dq, double *dk, double *dv,
-                         double *grad_inv_temp)
+                         double *grad_inv_temp, double *grad_inv_temp_l1)
 {
     if (K < 1 || K > ORACLE_MAX_K || L < 1 || N < 0 || T < 0 || D < 1)
         return -1;
     double *part = calloc((size_t)(N > 0 ? N : 1), sizeof(double));
+    double *pabs = calloc((size_t)(N > 0 ? N : 1), sizeof(double));
 #pragma omp parallel for schedule(dynamic, 1)
     for (int64_t n = 0; n < N; ++n) {
         const double *pl = planes + plane_of[n] * (int64_t)L * K * D;
         const int64_t o = n * T * D;
         stream_backward(q + o, k + o, v + o, dout + o, pl, T, D, L, K, causal,
-                        eps, inv_temp, dq + o, dk + o, dv + o, &part[n]);
+                        eps, inv_temp, dq + o, dk + o, dv + o, &part[n], &pabs[n]);
     }
-    double tot = 0.0;
-    for (int64_t n = 0; n < N; ++n)
+    double tot = 0.0, tabs = 0.0;
+    for (int64_t n = 0; n < N; ++n) {
         tot += part[n];
+        tabs += pabs[n];
+    }
     if (grad_inv_temp)
         *grad_inv_temp = tot;
+    if (grad_inv_temp_l1)
+        *grad_inv_temp_l1 = tabs;
     free(part);
+    free(pabs);
     return 0;
 }
 

@@ -52,7 +52,7 @@ def _lib():
         lib.oracle_race_forward.argtypes = [dp, dp, dp, dp, ip, i64, i64, i64, ci, ci, ci, cd, cd, dp]
         lib.oracle_race_forward.restype = ci
         lib.oracle_race_backward.argtypes = [dp, dp, dp, dp, dp, ip, i64, i64, i64, ci, ci, ci, cd, cd,
-                                             dp, dp, dp, dp]
+                                             dp, dp, dp, dp, dp]
         lib.oracle_race_backward.restype = ci
         lib.oracle_prefix_mean_flat.argtypes = [fp, fp, i64, i64, i64, cd, fp]
         lib.oracle_prefix_mean_flat.restype = None
@@ -110,24 +110,27 @@ def race_forward(q, k, v, planes, *, causal: bool, eps: float = 1e-6, inv_temp: 
     return from_streams(out, M, B, H)
 
 
-def race_backward(q, k, v, dout, planes, *, causal: bool, eps: float = 1e-6, inv_temp: float):
+def race_backward(q, k, v, dout, planes, *, causal: bool, eps: float = 1e-6, inv_temp: float,
+                  with_l1: bool = False):
     """fp64 backward. Returns (dq, dk, dv, grad_inv_temp); grads are [M,B,T,H,D]
-    and grad_inv_temp = dL/d(1/tau) summed over all streams."""
+    and grad_inv_temp = dL/d(1/tau) summed over all streams.  with_l1 appends
+    sum |du * th|, the l1 mass of the terms of that sum."""
     M, B, T, H, D = q.shape
     planes = np.ascontiguousarray(np.asarray(planes, dtype=np.float64))
     NP, L, K, _ = planes.shape
     qs, ks, vs, gs = to_streams(q), to_streams(k), to_streams(v), to_streams(dout)
     pm = _plane_map(M, B, H, NP)
     dq, dk, dv = np.zeros_like(qs), np.zeros_like(qs), np.zeros_like(qs)
-    git = np.zeros(1, dtype=np.float64)
+    git = np.zeros(2, dtype=np.float64)
     rc = _lib().oracle_race_backward(_dptr(qs), _dptr(ks), _dptr(vs), _dptr(gs), _dptr(planes),
                                      pm.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
                                      qs.shape[0], T, D, L, K, int(causal), float(eps),
-                                     float(inv_temp), _dptr(dq), _dptr(dk), _dptr(dv), _dptr(git))
+                                     float(inv_temp), _dptr(dq), _dptr(dk), _dptr(dv), _dptr(git),
+                                     _dptr(git[1:]))
     if rc != 0:
         raise ValueError("oracle_race_backward rejected its arguments")
-    return (from_streams(dq, M, B, H), from_streams(dk, M, B, H), from_streams(dv, M, B, H),
-            float(git[0]))
+    res = (from_streams(dq, M, B, H), from_streams(dk, M, B, H), from_streams(dv, M, B, H), float(git[0]))
+    return res + (float(git[1]),) if with_l1 else res
 
 
 def prefix_mean_flat(w, v, eps: float = 1e-6):

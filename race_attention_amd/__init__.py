@@ -1,0 +1,13 @@
+"""race_attention_amd -- MI355X (gfx950) RACE attention operator.
+
+Hand-written HIP kernels behind a C ABI (include/race_attention.h), with
+PyTorch modules mirroring the reference API:
+  race_attention_amd.race  causal BatchedACE / RACEAttention / RACEBlock /
+                           RACEPrefixMeanFlatFn   (misc/race.py)
+  race_attention_amd.vit   non-causal BatchedACE / RACEAttention / RACEBlock
+                           (misc/vit.py)
+  race_attention_amd.functional  race_attention(), RACEFunction, raw calls
+"""
+from .functional import RACEFunction, RACEPrefixMeanFlatFn, race_attention  # noqa: F401
+
+__all__ = ["RACEFunction", "RACEPrefixMeanFlatFn", "race_attention"]

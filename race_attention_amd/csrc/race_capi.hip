@@ -1,0 +1,369 @@
+// race_capi.hip -- the extern "C" boundary declared in include/race_attention.h.
+//
+// Validates descriptors and pointers on the host (shape, alignment and stride
+// checks happen before any launch, so a kernel never sees a shape it does not
+// assume), plans the segment decomposition, carves the caller's workspace and
+// enqueues the kernels on the caller's stream.  No allocation, no
+// synchronisation, no global mutable state besides the thread-local error.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/race_attention.h"
+#include "prefix_mean.hip"
+#include "race_kernels.hip"
+
+namespace race {
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    return RACE_OK;
+}
+
+constexpr int64_t kTargetBlocks = 2048;  // workgroups per scan phase (256 CUs x 8)
+
+struct Plan {
+    int SP = 0, S = 0, R = 0;
+    int64_t N = 0, ntiles = 0;
+    int nseg = 0, tps = 0;
+    size_t esize = 0;
+    size_t state_bytes = 0, fws = 0, bws = 0;
+};
+
+// (dtype, SP) pairs compiled into this build: bf16 up to 128 padded buckets,
+// fp32 up to 32 (LDS capacity of the backward tile kernels).
+bool supported(int dtype, int SP) {
+    if (dtype == RACE_DTYPE_BF16) return SP == 32 || SP == 64 || SP == 128;
+    return SP == 32;
+}
+
+int make_plan(const race_desc *d, Plan &p) {
+    if (!d) return fail(RACE_E_INVALID, "descriptor is NULL");
+    if (d->dtype != RACE_DTYPE_F32 && d->dtype != RACE_DTYPE_BF16)
+        return fail(RACE_E_INVALID, "dtype %d is not RACE_DTYPE_F32 or RACE_DTYPE_BF16", d->dtype);
+    if (d->M < 1 || d->B < 1 || d->T < 1 || d->H < 1)
+        return fail(RACE_E_INVALID, "M, B, T, H must be >= 1 (got %lld, %lld, %lld, %lld)", (long long)d->M,
+                    (long long)d->B, (long long)d->T, (long long)d->H);
+    if (d->D != D) return fail(RACE_E_UNSUPPORTED, "head dim D=%lld unsupported (this build: D=64)", (long long)d->D);
+    if (d->L < 1 || d->K < 1) return fail(RACE_E_INVALID, "L and K must be >= 1 (got L=%d K=%d)", d->L, d->K);
+    if (d->K > 8) return fail(RACE_E_UNSUPPORTED, "K=%d hash bits unsupported (K <= 8)", d->K);
+    if (d->L * d->K > NCOL)
+        return fail(RACE_E_UNSUPPORTED, "L*K=%d projection columns unsupported (L*K <= %d)", d->L * d->K, NCOL);
+    if (!(d->eps >= 0.f) || d->eps > 1e30f) return fail(RACE_E_INVALID, "eps must be finite and >= 0");
+    if (!(d->inv_temp == d->inv_temp) || d->inv_temp > 1e30f || d->inv_temp < -1e30f)
+        return fail(RACE_E_INVALID, "inv_temp must be finite");
+    if (d->planes_m_stride < 0) return fail(RACE_E_INVALID, "planes_m_stride must be >= 0");
+    if (d->phases < 0 || d->phases > 7) return fail(RACE_E_INVALID, "phases must be a RACE_PHASE_* bitmask");
+    p.R = 1 << d->K;
+    p.S = d->L * p.R;
+    p.SP = (p.S + 31) / 32 * 32;
+    if (!supported(d->dtype, p.SP))
+        return fail(RACE_E_UNSUPPORTED, "L*2^K=%d buckets unsupported for %s (supported padded sizes: %s)", p.S,
+                    d->dtype == RACE_DTYPE_BF16 ? "bf16" : "fp32",
+                    d->dtype == RACE_DTYPE_BF16 ? "32, 64, 128" : "32");
+    p.N = d->M * d->B * d->H;
+    if (p.N > 65535) return fail(RACE_E_UNSUPPORTED, "M*B*H=%lld streams exceed 65535", (long long)p.N);
+    p.ntiles = (d->T + TT - 1) / TT;
+    int64_t tps;
+    if (d->seg_tiles > 0) {
+        tps = d->seg_tiles;
+    } else {
+        int64_t nseg = (kTargetBlocks + p.N - 1) / p.N;
+        if (nseg > p.ntiles) nseg = p.ntiles;
+        tps = (p.ntiles + nseg - 1) / nseg;
+    }
+    p.tps = (int)(tps < p.ntiles ? tps : p.ntiles);
+    const int64_t nseg = (p.ntiles + p.tps - 1) / p.tps;
+    if (nseg > (1 << 30)) return fail(RACE_E_UNSUPPORTED, "too many segments");
+    p.nseg = (int)nseg;
+    p.esize = d->dtype == RACE_DTYPE_BF16 ? 2 : 4;
+    const size_t blk = (size_t)p.SP * SROW;
+    p.state_bytes = (size_t)p.N * (p.nseg + 1) * blk * sizeof(double);
+    p.fws = (size_t)p.N * p.nseg * blk * sizeof(double);
+    p.bws = 2 * (size_t)p.N * p.nseg * blk * sizeof(float) + align16(2 * (size_t)p.N * p.nseg * sizeof(float));
+    return RACE_OK;
+}
+
+int check_tensor(const char *name, const void *ptr, const int64_t *st, size_t esize, int64_t T) {
+    if (!ptr) return fail(RACE_E_INVALID, "%s is NULL", name);
+    if ((uintptr_t)ptr % 16) return fail(RACE_E_INVALID, "%s is not 16-byte aligned", name);
+    for (int j = 0; j < 4; ++j) {
+        if (st[j] < 0) return fail(RACE_E_INVALID, "%s stride %d is negative", name, j);
+        if ((st[j] * (int64_t)esize) % 16)
+            return fail(RACE_E_INVALID, "%s stride %d (%lld elements) is not a multiple of 16 bytes", name, j,
+                        (long long)st[j]);
+    }
+    if (T > 1 && st[2] < D)
+        return fail(RACE_E_INVALID, "%s token stride %lld overlaps rows", name, (long long)st[2]);
+    return RACE_OK;
+}
+
+Strides strides_of(const int64_t *s) { return Strides{s[0], s[1], s[2], s[3]}; }
+
+Args base_args(const race_desc *d, const Plan &p, const float *planes) {
+    Args a{};
+    a.sq = strides_of(d->q_stride);
+    a.sk = strides_of(d->k_stride);
+    a.sv = strides_of(d->v_stride);
+    a.so = strides_of(d->o_stride);
+    a.sdo = strides_of(d->do_stride);
+    a.sg = strides_of(d->g_stride);
+    a.planes = planes;
+    a.planes_m_stride = d->planes_m_stride;
+    a.M = (int)d->M;
+    a.B = (int)d->B;
+    a.H = (int)d->H;
+    a.L = d->L;
+    a.K = d->K;
+    a.R = p.R;
+    a.S = p.S;
+    a.T = d->T;
+    a.eps = d->eps;
+    a.inv_temp = d->inv_temp;
+    a.nseg = p.nseg;
+    a.tps = p.tps;
+    return a;
+}
+
+int launched(const char *what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(RACE_E_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+bool run_phase(const race_desc *d, int ph) { return d->phases == 0 || (d->phases & ph); }
+
+template <typename T, int SP> int fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
+    const dim3 grid(p.nseg, (unsigned)p.N);
+    if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP><<<grid, NT, 0, s>>>(a);
+    const int elems = SP * SROW;
+    if (run_phase(d, RACE_PHASE_SCAN))
+        k_fwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
+    if (run_phase(d, RACE_PHASE_OUT)) {
+        if (d->causal)
+            k_fwd_out<T, SP, true><<<grid, NT, 0, s>>>(a);
+        else
+            k_fwd_out<T, SP, false><<<grid, NT, 0, s>>>(a);
+    }
+    return launched("race_fwd");
+}
+
+template <typename T, int SP>
+int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hipStream_t s) {
+    const dim3 grid(p.nseg, (unsigned)p.N);
+    if (run_phase(d, RACE_PHASE_REDUCE)) {
+        if (d->causal)
+            k_bwd_reduce<T, SP, true><<<grid, NT, 0, s>>>(a);
+        else
+            k_bwd_reduce<T, SP, false><<<grid, NT, 0, s>>>(a);
+    }
+    const int elems = SP * SROW;
+    if (run_phase(d, RACE_PHASE_SCAN))
+        k_bwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.rstate, a.rdelta, p.nseg, elems,
+                                                                            d->causal);
+    if (run_phase(d, RACE_PHASE_OUT)) {
+        if (d->causal)
+            k_bwd_out<T, SP, true><<<grid, NT, 0, s>>>(a);
+        else
+            k_bwd_out<T, SP, false><<<grid, NT, 0, s>>>(a);
+        if (grad_inv_temp) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, 2 * p.N * p.nseg, grad_inv_temp);
+    }
+    return launched("race_bwd");
+}
+
+template <typename T> int fwd_dispatch(const race_desc *d, const Plan &p, const Args &a, hipStream_t s) {
+    switch (p.SP) {
+    case 32: return fwd_impl<T, 32>(d, p, a, s);
+    case 64: if constexpr (sizeof(T) == 2) return fwd_impl<T, 64>(d, p, a, s); break;
+    case 128: if constexpr (sizeof(T) == 2) return fwd_impl<T, 128>(d, p, a, s); break;
+    }
+    return fail(RACE_E_UNSUPPORTED, "bucket count not compiled");
+}
+
+template <typename T>
+int bwd_dispatch(const race_desc *d, const Plan &p, const Args &a, float *git, hipStream_t s) {
+    switch (p.SP) {
+    case 32: return bwd_impl<T, 32>(d, p, a, git, s);
+    case 64: if constexpr (sizeof(T) == 2) return bwd_impl<T, 64>(d, p, a, git, s); break;
+    case 128: if constexpr (sizeof(T) == 2) return bwd_impl<T, 128>(d, p, a, git, s); break;
+    }
+    return fail(RACE_E_UNSUPPORTED, "bucket count not compiled");
+}
+
+// prefix mean: segment length so that NS * nseg ~ 4096 waves
+int64_t pm_tseg(int64_t NS, int64_t T) {
+    int64_t nseg = (4096 + NS - 1) / NS;
+    if (nseg > T) nseg = T;
+    if (nseg < 1) nseg = 1;
+    return (T + nseg - 1) / nseg;
+}
+
+int pm_check(const void *a, const char *na, int64_t NS, int64_t T, int64_t D) {
+    if (!a) return fail(RACE_E_INVALID, "%s is NULL", na);
+    if (NS < 1 || T < 1 || D < 1) return fail(RACE_E_INVALID, "NS, T, D must be >= 1");
+    if (D > 64 * PM_MAXC) return fail(RACE_E_UNSUPPORTED, "D=%lld unsupported (D <= %d)", (long long)D, 64 * PM_MAXC);
+    if (NS > 65535) return fail(RACE_E_UNSUPPORTED, "NS=%lld exceeds 65535", (long long)NS);
+    return RACE_OK;
+}
+
+} // namespace
+} // namespace race
+
+using namespace race;
+
+extern "C" {
+
+size_t race_state_bytes(const race_desc *d) {
+    Plan p;
+    if (make_plan(d, p) != RACE_OK) return 0;
+    ok();
+    return p.state_bytes;
+}
+
+size_t race_fwd_workspace_bytes(const race_desc *d) {
+    Plan p;
+    if (make_plan(d, p) != RACE_OK) return 0;
+    ok();
+    return p.fws;
+}
+
+size_t race_bwd_workspace_bytes(const race_desc *d) {
+    Plan p;
+    if (make_plan(d, p) != RACE_OK) return 0;
+    ok();
+    return p.bws;
+}
+
+int race_fwd(const race_desc *d, const void *q, const void *k, const void *v, const float *planes, void *out,
+             void *state, void *ws, size_t ws_bytes, void *stream) {
+    Plan p;
+    int rc = make_plan(d, p);
+    if (rc) return rc;
+    if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
+        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) || (rc = check_tensor("out", out, d->o_stride, p.esize, d->T)))
+        return rc;
+    if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
+    if (!state) return fail(RACE_E_INVALID, "state is NULL");
+    if (!ws || ws_bytes < p.fws)
+        return fail(RACE_E_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, p.fws);
+    Args a = base_args(d, p, planes);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    a.fstate = (double *)state;
+    a.fdelta = (double *)ws;
+    hipStream_t s = (hipStream_t)stream;
+    if (d->dtype == RACE_DTYPE_BF16) return fwd_dispatch<bf16>(d, p, a, s);
+    return fwd_dispatch<float>(d, p, a, s);
+}
+
+int race_bwd(const race_desc *d, const void *q, const void *k, const void *v, const float *planes,
+             const void *dout, const void *state, void *dq, void *dk, void *dv, float *grad_inv_temp, void *ws,
+             size_t ws_bytes, void *stream) {
+    Plan p;
+    int rc = make_plan(d, p);
+    if (rc) return rc;
+    if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
+        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) ||
+        (rc = check_tensor("dout", dout, d->do_stride, p.esize, d->T)) ||
+        (rc = check_tensor("dq", dq, d->g_stride, p.esize, d->T)) || (rc = check_tensor("dk", dk, d->g_stride, p.esize, d->T)) ||
+        (rc = check_tensor("dv", dv, d->g_stride, p.esize, d->T)))
+        return rc;
+    if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
+    if (!state) return fail(RACE_E_INVALID, "state is NULL");
+    if (!ws || ws_bytes < p.bws)
+        return fail(RACE_E_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, p.bws);
+    Args a = base_args(d, p, planes);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.dout = dout;
+    a.dq = dq;
+    a.dk = dk;
+    a.dv = dv;
+    a.fstate = (double *)state;
+    const size_t blk = (size_t)p.N * p.nseg * p.SP * SROW;
+    a.rdelta = (float *)ws;
+    a.rstate = a.rdelta + blk;
+    a.tpart = a.rstate + blk;
+    hipStream_t s = (hipStream_t)stream;
+    if (d->dtype == RACE_DTYPE_BF16) return bwd_dispatch<bf16>(d, p, a, grad_inv_temp, s);
+    return bwd_dispatch<float>(d, p, a, grad_inv_temp, s);
+}
+
+size_t race_prefix_mean_workspace_bytes(int64_t NS, int64_t T, int64_t D) {
+    if (NS < 1 || T < 1 || D < 1) return 0;
+    const int64_t tseg = pm_tseg(NS, T), nseg = (T + tseg - 1) / tseg;
+    const size_t row = (size_t)(D + 1) * sizeof(double);
+    // forward: delta + state; backward adds invA, alpha, rdelta, rstate
+    return (size_t)NS * nseg * row + (size_t)NS * (nseg + 1) * row + 2 * (size_t)NS * T * sizeof(double) +
+           2 * (size_t)NS * nseg * row;
+}
+
+int race_prefix_mean_fwd(const float *w, const float *v, float *E, int64_t NS, int64_t T, int64_t D, double eps,
+                         void *ws, size_t ws_bytes, void *stream) {
+    int rc;
+    if ((rc = pm_check(w, "w", NS, T, D)) || (rc = pm_check(v, "v", NS, T, D)) || (rc = pm_check(E, "E", NS, T, D)))
+        return rc;
+    const size_t need = race_prefix_mean_workspace_bytes(NS, T, D);
+    if (!ws || ws_bytes < need) return fail(RACE_E_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, need);
+    const int64_t tseg = pm_tseg(NS, T);
+    const int nseg = (int)((T + tseg - 1) / tseg);
+    double *delta = (double *)ws;
+    double *state = delta + NS * nseg * (D + 1);
+    hipStream_t s = (hipStream_t)stream;
+    const int elems = (int)(D + 1);
+    k_pm_reduce<<<dim3(nseg, (unsigned)NS), 64, 0, s>>>(w, v, delta, T, (int)D, tseg, nseg);
+    k_pm_scan<<<dim3((elems + 255) / 256, (unsigned)NS), 256, 0, s>>>(state, delta, nseg, elems);
+    k_pm_out<<<dim3(nseg, (unsigned)NS), 64, 0, s>>>(w, v, E, state, T, (int)D, tseg, nseg, eps);
+    return launched("race_prefix_mean_fwd");
+}
+
+int race_prefix_mean_bwd(const float *w, const float *v, const float *gE, float *gW, float *gV, int64_t NS,
+                         int64_t T, int64_t D, double eps, void *ws, size_t ws_bytes, void *stream) {
+    int rc;
+    if ((rc = pm_check(w, "w", NS, T, D)) || (rc = pm_check(v, "v", NS, T, D)) ||
+        (rc = pm_check(gE, "gE", NS, T, D)) || (rc = pm_check(gW, "gW", NS, T, D)) ||
+        (rc = pm_check(gV, "gV", NS, T, D)))
+        return rc;
+    const size_t need = race_prefix_mean_workspace_bytes(NS, T, D);
+    if (!ws || ws_bytes < need) return fail(RACE_E_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, need);
+    const int64_t tseg = pm_tseg(NS, T);
+    const int nseg = (int)((T + tseg - 1) / tseg);
+    double *delta = (double *)ws;
+    double *state = delta + NS * nseg * (D + 1);
+    double *invA = state + NS * (nseg + 1) * (D + 1);
+    double *alpha = invA + NS * T;
+    double *rdelta = alpha + NS * T;
+    double *rstate = rdelta + NS * nseg * (D + 1);
+    hipStream_t s = (hipStream_t)stream;
+    const int elems = (int)(D + 1);
+    const dim3 grid(nseg, (unsigned)NS);
+    k_pm_reduce<<<grid, 64, 0, s>>>(w, v, delta, T, (int)D, tseg, nseg);
+    k_pm_scan<<<dim3((elems + 255) / 256, (unsigned)NS), 256, 0, s>>>(state, delta, nseg, elems);
+    k_pm_bw_fwd<<<grid, 64, 0, s>>>(w, v, gE, state, invA, alpha, rdelta, T, (int)D, tseg, nseg, eps);
+    k_pm_rscan<<<dim3((elems + 255) / 256, (unsigned)NS), 256, 0, s>>>(rstate, rdelta, nseg, elems);
+    k_pm_bw_rev<<<grid, 64, 0, s>>>(w, v, gE, invA, alpha, rstate, gW, gV, T, (int)D, tseg, nseg);
+    return launched("race_prefix_mean_bwd");
+}
+
+const char *race_last_error(void) { return g_err.c_str(); }
+
+int race_abi_version(void) { return 1; }
+
+} // extern "C"

@@ -1,0 +1,134 @@
+// race_device.h -- device building blocks for the gfx950 RACE kernels.
+//
+// Matrix products use the CDNA4 16x16 MFMA tiles with 64-wide waves:
+//   bf16: v_mfma_f32_16x16x32_bf16 (one instruction per 32-deep k step)
+//   fp32: v_mfma_f32_16x16x4_f32   (eight instructions per 32-deep k step)
+// Operand fragments: lane l = 16*g + i (g = l/16, i = l%16) holds row i of
+// the 16-row A tile (or column i of the B tile) and the 8 consecutive k values
+// 8g..8g+7 of the current 32-deep k step.  A and B use the same k mapping, so
+// the contraction covers all 32 k values whatever order the instruction uses
+// inside a step.  The fp32 accumulator of a 16x16 tile: lane l holds
+// D[4g + e][i] in element e (e = 0..3).
+//
+// Operands are staged in LDS with k contiguous ("A as [m][k], B as [n][k]"),
+// rows padded by 16 bytes so the 16 rows of a fragment fall in distinct banks.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace race {
+
+typedef __bf16 bf16;
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int D = 64;       // head dimension handled by this build
+constexpr int TT = 32;      // tokens per tile
+constexpr int NCOL = 32;    // projection columns (L*K <= 32)
+constexpr int NW = 4;       // waves per workgroup
+constexpr int NT = NW * 64; // threads per workgroup
+
+// padded leading dimension (elements) of an LDS array with n logical columns
+template <typename T> __host__ __device__ constexpr int ld_of(int n) { return n + 16 / (int)sizeof(T); }
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// ------------------------------------------------------------ conversions
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+
+// ------------------------------------------------------------ fragments
+template <typename T> struct Frag;
+template <> struct Frag<bf16> { bf16x8 v; };
+template <> struct Frag<float> { f32x4 lo, hi; };
+
+__device__ __forceinline__ Frag<bf16> ld_frag(const bf16 *p) {
+    Frag<bf16> f;
+    f.v = *reinterpret_cast<const bf16x8 *>(p);
+    return f;
+}
+__device__ __forceinline__ Frag<float> ld_frag(const float *p) {
+    Frag<float> f;
+    f.lo = *reinterpret_cast<const f32x4 *>(p);
+    f.hi = *reinterpret_cast<const f32x4 *>(p + 4);
+    return f;
+}
+// 8 k values spaced by `stride` elements (operand read across rows)
+__device__ __forceinline__ Frag<bf16> ld_frag_strided(const bf16 *p, int stride) {
+    Frag<bf16> f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f.v[e] = p[e * stride];
+    return f;
+}
+__device__ __forceinline__ Frag<float> ld_frag_strided(const float *p, int stride) {
+    Frag<float> f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f.lo[e] = p[e * stride];
+        f.hi[e] = p[(e + 4) * stride];
+    }
+    return f;
+}
+
+__device__ __forceinline__ void mma(f32x4 &c, const Frag<bf16> &a, const Frag<bf16> &b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, c, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f32x4 &c, const Frag<float> &a, const Frag<float> &b) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[e], b.lo[e], c, 0, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[e], b.hi[e], c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// acc += A[0:16, 0:32*ks] * B[0:16, 0:32*ks]^T, A/B pointers at the tile
+// origin, stored k-contiguous with leading dimensions lda/ldb.
+template <typename T>
+__device__ __forceinline__ void tile_mma(f32x4 &acc, const T *A, int lda, const T *B, int ldb, int ksteps) {
+    const int i = lane_id() & 15, g = lane_id() >> 4;
+    const T *pa = A + i * lda + 8 * g;
+    const T *pb = B + i * ldb + 8 * g;
+    for (int ks = 0; ks < ksteps; ++ks) mma(acc, ld_frag(pa + 32 * ks), ld_frag(pb + 32 * ks));
+}
+
+// Same, with B read from a [k][n] (n contiguous) array: lane reads 8 k rows.
+template <typename T>
+__device__ __forceinline__ void tile_mma_bT(f32x4 &acc, const T *A, int lda, const T *Bkn, int ldb, int ksteps) {
+    const int i = lane_id() & 15, g = lane_id() >> 4;
+    const T *pa = A + i * lda + 8 * g;
+    const T *pb = Bkn + (8 * g) * ldb + i;
+    for (int ks = 0; ks < ksteps; ++ks)
+        mma(acc, ld_frag(pa + 32 * ks), ld_frag_strided(pb + 32 * ks * ldb, ldb));
+}
+
+// store accumulator tile (origin row r0, col c0) to a [row][col] array
+template <typename T>
+__device__ __forceinline__ void st_tile(T *dst, int ld, const f32x4 &acc) {
+    const int i = lane_id() & 15, g = lane_id() >> 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[(4 * g + e) * ld + i] = from_f32<T>(acc[e]);
+}
+// store accumulator tile transposed: dst[col][row]
+template <typename T>
+__device__ __forceinline__ void st_tile_T(T *dst, int ld, const f32x4 &acc) {
+    const int i = lane_id() & 15, g = lane_id() >> 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[i * ld + 4 * g + e] = from_f32<T>(acc[e]);
+}
+
+// ------------------------------------------------------------ sigmoids
+// stable pair (sigmoid(x), sigmoid(-x))
+__device__ __forceinline__ void sigmoid_pair(float x, float &sp, float &sm) {
+    const float e = __expf(-fabsf(x));
+    const float p = 1.0f / (1.0f + e);
+    const float q = e * p;
+    sp = x >= 0.f ? p : q;
+    sm = x >= 0.f ? q : p;
+}
+
+} // namespace race

@@ -1,0 +1,223 @@
+"""Torch-facing calls into the HIP library and the autograd Functions.
+
+``race_attention(Qhf, Khf, Vhf, planes, ...)`` is the operator behind the
+reference's BatchedACE.forward (misc/race.py:63-142 causal,
+misc/vit.py:918-978 non-causal): inputs [M,B,T,H,D] (D = 64, bf16 or fp32,
+any strides with a contiguous last dimension, an M stride of 0 for the
+reference's M-fold expand), hyperplanes [L,K,D] shared or [M,L,K,D]
+per-estimator, output [M,B,T,H,D].  Forward and backward run as HIP kernels on
+the current stream; bucket probabilities are recomputed in the backward.
+
+``RACEPrefixMeanFlatFn`` is the autograd Function of misc/race.py:9-24 with the
+flat prefix mean computed by the HIP kernels instead of the CPU extension.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: _lib.RACE_DTYPE_BF16, torch.float32: _lib.RACE_DTYPE_F32}
+
+
+def _require_gpu(*tensors):
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError("race_attention_amd runs on ROCm GPUs only; got a tensor on "
+                               f"{t.device}")
+
+
+def _strides4(x: torch.Tensor):
+    if x.dim() != 5:
+        raise ValueError(f"expected a [M,B,T,H,D] tensor, got shape {tuple(x.shape)}")
+    if x.stride(4) != 1:
+        raise ValueError("the last (head) dimension must be contiguous")
+    return (ctypes.c_int64 * 4)(*[x.stride(j) if x.size(j) > 1 else 0 for j in range(4)])
+
+
+def _aligned(x: torch.Tensor) -> torch.Tensor:
+    """Make x usable by the kernels: contiguous D, 16-byte aligned rows."""
+    es = x.element_size()
+    ok = (x.stride(4) == 1 and x.data_ptr() % 16 == 0 and
+          all((x.stride(j) * es) % 16 == 0 or x.size(j) == 1 for j in range(4)) and
+          (x.size(2) == 1 or x.stride(2) >= x.size(4)))
+    return x if ok else x.contiguous()
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def make_desc(q, k, v, planes, *, L, K, causal, eps, inv_temp, seg_tiles=0):
+    M, B, T, H, D = q.shape
+    d = _lib.RaceDesc()
+    d.M, d.B, d.T, d.H, d.D = M, B, T, H, D
+    d.L, d.K = int(L), int(K)
+    d.causal = 1 if causal else 0
+    if q.dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {q.dtype} (bf16 or fp32)")
+    d.dtype = _DTYPES[q.dtype]
+    d.eps = float(eps)
+    d.inv_temp = float(inv_temp)
+    if planes.dim() == 3:
+        d.planes_m_stride = 0
+    elif planes.dim() == 4 and planes.size(0) == 1:
+        d.planes_m_stride = 0
+    elif planes.dim() == 4 and planes.size(0) == M:
+        d.planes_m_stride = L * K * D
+    else:
+        raise ValueError(f"planes must be [L,K,D], [1,L,K,D] or [M,L,K,D]; got {tuple(planes.shape)}")
+    d.q_stride, d.k_stride, d.v_stride = _strides4(q), _strides4(k), _strides4(v)
+    d.seg_tiles = int(seg_tiles)
+    return d
+
+
+def _check_inputs(q, k, v, planes, L, K):
+    if not (q.shape == k.shape == v.shape):
+        raise ValueError(f"Q, K, V shapes differ: {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("Q, K, V dtypes differ")
+    if planes.shape[-3:] != (L, K, q.shape[-1]):
+        raise ValueError(f"planes trailing shape {tuple(planes.shape[-3:])} != (L, K, D) = ({L}, {K}, {q.shape[-1]})")
+
+
+def race_fwd_raw(q, k, v, planes, *, L, K, causal, eps=1e-6, inv_temp, seg_tiles=0):
+    """Forward only: returns (out [M,B,T,H,D] contiguous, state for race_bwd_raw)."""
+    _require_gpu(q, k, v, planes)
+    _check_inputs(q, k, v, planes, L, K)
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    planes = planes.to(device=q.device, dtype=torch.float32).contiguous()
+    lib = _lib.load()
+    d = make_desc(q, k, v, planes, L=L, K=K, causal=causal, eps=eps, inv_temp=inv_temp, seg_tiles=seg_tiles)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    d.o_stride = _strides4(out)
+    sb = lib.race_state_bytes(ctypes.byref(d))
+    if sb == 0:
+        _lib.check(-1, "race_state_bytes")
+    wb = lib.race_fwd_workspace_bytes(ctypes.byref(d))
+    state = torch.empty(sb, dtype=torch.uint8, device=q.device)
+    ws = torch.empty(max(wb, 16), dtype=torch.uint8, device=q.device)
+    rc = lib.race_fwd(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(planes), _ptr(out), _ptr(state),
+                      _ptr(ws), ctypes.c_size_t(ws.numel()), _stream())
+    _lib.check(rc, "race_fwd")
+    return out, state
+
+
+def race_bwd_raw(q, k, v, planes, dout, state, *, L, K, causal, eps=1e-6, inv_temp, seg_tiles=0,
+                 want_temp_grad=True):
+    """Backward: returns (dq, dk, dv, grad_inv_temp (0-dim fp32 tensor or None))."""
+    _require_gpu(q, k, v, planes, dout, state)
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    dout = _aligned(dout.to(q.dtype))
+    planes = planes.to(device=q.device, dtype=torch.float32).contiguous()
+    lib = _lib.load()
+    d = make_desc(q, k, v, planes, L=L, K=K, causal=causal, eps=eps, inv_temp=inv_temp, seg_tiles=seg_tiles)
+    d.do_stride = _strides4(dout)
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty_like(dq)
+    dv = torch.empty_like(dq)
+    d.g_stride = _strides4(dq)
+    if state.numel() != lib.race_state_bytes(ctypes.byref(d)):
+        raise ValueError("state buffer does not match this descriptor")
+    wb = lib.race_bwd_workspace_bytes(ctypes.byref(d))
+    ws = torch.empty(max(wb, 16), dtype=torch.uint8, device=q.device)
+    git = torch.empty((), dtype=torch.float32, device=q.device) if want_temp_grad else None
+    rc = lib.race_bwd(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(planes), _ptr(dout), _ptr(state),
+                      _ptr(dq), _ptr(dk), _ptr(dv), _ptr(git) if git is not None else None,
+                      _ptr(ws), ctypes.c_size_t(ws.numel()), _stream())
+    _lib.check(rc, "race_bwd")
+    return dq, dk, dv, git
+
+
+class RACEFunction(torch.autograd.Function):
+    """Autograd Function of the RACE operator (F1 semantics).
+
+    forward(Qhf, Khf, Vhf, planes, inv_temp, L, K, causal, eps) -> [M,B,T,H,D].
+    inv_temp is a python float or a 0-dim tensor (then it receives a
+    gradient).  planes are buffers (no gradient), as in the reference
+    (misc/race.py:42-51)."""
+
+    @staticmethod
+    def forward(ctx, Qhf, Khf, Vhf, planes, inv_temp, L, K, causal, eps):
+        it = float(inv_temp) if torch.is_tensor(inv_temp) else float(inv_temp)
+        out, state = race_fwd_raw(Qhf, Khf, Vhf, planes, L=L, K=K, causal=causal, eps=eps, inv_temp=it)
+        ctx.save_for_backward(Qhf, Khf, Vhf, planes, state)
+        ctx.cfg = (L, K, causal, eps, it)
+        ctx.temp_is_tensor = torch.is_tensor(inv_temp)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        Qhf, Khf, Vhf, planes, state = ctx.saved_tensors
+        L, K, causal, eps, it = ctx.cfg
+        want = ctx.temp_is_tensor and ctx.needs_input_grad[4]
+        dq, dk, dv, git = race_bwd_raw(Qhf, Khf, Vhf, planes, dout, state, L=L, K=K, causal=causal, eps=eps,
+                                       inv_temp=it, want_temp_grad=want)
+        return (dq if ctx.needs_input_grad[0] else None,
+                dk if ctx.needs_input_grad[1] else None,
+                dv if ctx.needs_input_grad[2] else None,
+                None, git if want else None, None, None, None, None)
+
+
+def race_attention(Qhf, Khf, Vhf, planes, *, L, K, causal, inv_temp, eps=1e-6):
+    """Differentiable RACE operator on [M,B,T,H,D] tensors (see module doc)."""
+    return RACEFunction.apply(Qhf, Khf, Vhf, planes, inv_temp, L, K, causal, eps)
+
+
+# ------------------------------------------------------------- prefix mean
+def prefix_mean_fwd(w: torch.Tensor, v: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """race_prefix_mean_flat on the GPU: w [NS,T], v [NS,T,D] fp32 -> E [NS,T,D]."""
+    _require_gpu(w, v)
+    if w.dtype != torch.float32 or v.dtype != torch.float32:
+        raise TypeError("probsK_flat and V_flat must be float32")      # race_pref.cpp:9
+    if w.dim() != 2 or v.dim() != 3 or w.shape != v.shape[:2]:
+        raise ValueError("shapes must be [NS,T] and [NS,T,D] with matching NS and T")
+    w, v = w.contiguous(), v.contiguous()
+    NS, T, D = v.shape
+    lib = _lib.load()
+    E = torch.empty_like(v)
+    wb = lib.race_prefix_mean_workspace_bytes(NS, T, D)
+    ws = torch.empty(max(wb, 16), dtype=torch.uint8, device=v.device)
+    rc = lib.race_prefix_mean_fwd(_ptr(w), _ptr(v), _ptr(E), NS, T, D, float(eps), _ptr(ws),
+                                  ctypes.c_size_t(ws.numel()), _stream())
+    _lib.check(rc, "race_prefix_mean_fwd")
+    return E
+
+
+def prefix_mean_bwd(w, v, gE, eps: float = 1e-6):
+    """race_prefix_mean_flat_bw on the GPU -> (gW [NS,T], gV [NS,T,D])."""
+    _require_gpu(w, v, gE)
+    w, v, gE = w.contiguous(), v.contiguous(), gE.contiguous().to(torch.float32)
+    NS, T, D = v.shape
+    lib = _lib.load()
+    gW = torch.empty_like(w)
+    gV = torch.empty_like(v)
+    wb = lib.race_prefix_mean_workspace_bytes(NS, T, D)
+    ws = torch.empty(max(wb, 16), dtype=torch.uint8, device=v.device)
+    rc = lib.race_prefix_mean_bwd(_ptr(w), _ptr(v), _ptr(gE), _ptr(gW), _ptr(gV), NS, T, D, float(eps),
+                                  _ptr(ws), ctypes.c_size_t(ws.numel()), _stream())
+    _lib.check(rc, "race_prefix_mean_bwd")
+    return gW, gV
+
+
+class RACEPrefixMeanFlatFn(torch.autograd.Function):
+    """misc/race.py:9-24 with the HIP prefix-mean kernels."""
+
+    @staticmethod
+    def forward(ctx, probsK_flat, V_flat, eps):
+        E_flat = prefix_mean_fwd(probsK_flat, V_flat, float(eps))
+        ctx.save_for_backward(probsK_flat, V_flat)
+        ctx.eps = float(eps)
+        return E_flat
+
+    @staticmethod
+    def backward(ctx, gradE_flat):
+        probsK_flat, V_flat = ctx.saved_tensors
+        gW, gV = prefix_mean_bwd(probsK_flat, V_flat, gradE_flat.contiguous(), ctx.eps)
+        return gW, gV, None

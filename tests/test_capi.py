@@ -1,0 +1,115 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the
+header declares, and rejects invalid requests before launching anything.
+No compute call is made here (no GPU in this environment)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from race_attention_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "race_attention.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return set(re.findall(r"\b(race_[a-z_]+)\s*\(", src))
+
+
+def test_header_matches_binding_list():
+    assert _declared() == set(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.race_abi_version() == 1
+
+
+def test_desc_layout_matches_header():
+    # int64 x5, int32 x4, float x2, int64, 6 x int64[4], int32 x2
+    assert ctypes.sizeof(_lib.RaceDesc) == 5 * 8 + 4 * 4 + 2 * 4 + 8 + 6 * 32 + 2 * 4  # seg_tiles, phases
+    assert _lib.RaceDesc.planes_m_stride.offset == 64
+
+
+def _desc(**kw):
+    d = _lib.RaceDesc()
+    d.M, d.B, d.T, d.H, d.D = 1, 1, 1 << 20, 8, 64
+    d.L, d.K, d.causal, d.dtype = 8, 4, 1, _lib.RACE_DTYPE_BF16
+    d.eps, d.inv_temp = 1e-6, 0.125
+    for j in range(4):
+        d.q_stride[j] = d.k_stride[j] = d.v_stride[j] = d.o_stride[j] = d.do_stride[j] = d.g_stride[j] = 0
+    d.q_stride[2] = d.k_stride[2] = d.v_stride[2] = d.o_stride[2] = d.do_stride[2] = d.g_stride[2] = 512
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+def test_plan_sizes_c4():
+    lib = _lib.load()
+    d = _desc()
+    sb = lib.race_state_bytes(ctypes.byref(d))
+    # N=8 streams, 256 segments (+1 total), 128 buckets x 65 fp64
+    assert sb == 8 * 257 * 128 * 65 * 8
+    assert lib.race_fwd_workspace_bytes(ctypes.byref(d)) == 8 * 256 * 128 * 65 * 8
+    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) >= 2 * 8 * 256 * 128 * 65 * 4
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("D", 32, -2, "head dim"),
+    ("K", 9, -2, "hash bits"),
+    ("L", 9, -2, "projection columns"),
+    ("L", 0, -1, "L and K"),
+    ("T", 0, -1, "must be >= 1"),
+    ("dtype", 7, -1, "dtype"),
+])
+def test_invalid_descriptors_rejected(field, value, code, msg):
+    lib = _lib.load()
+    d = _desc(**{field: value})
+    assert lib.race_state_bytes(ctypes.byref(d)) == 0
+    assert msg in _lib.last_error()
+    rc = lib.race_fwd(ctypes.byref(d), None, None, None, None, None, None, None, 0, None)
+    assert rc == code
+    assert msg in _lib.last_error()
+
+
+def test_fp32_large_bucket_count_unsupported():
+    lib = _lib.load()
+    d = _desc(dtype=_lib.RACE_DTYPE_F32)
+    assert lib.race_state_bytes(ctypes.byref(d)) == 0
+    assert "fp32" in _lib.last_error()
+
+
+def test_null_and_misaligned_pointers_rejected():
+    lib = _lib.load()
+    d = _desc(T=64)
+    rc = lib.race_fwd(ctypes.byref(d), None, None, None, None, None, None, None, 0, None)
+    assert rc == -1 and "q is NULL" in _lib.last_error()
+    rc = lib.race_fwd(ctypes.byref(d), ctypes.c_void_p(8), None, None, None, None, None, None, 0, None)
+    assert rc == -1 and "aligned" in _lib.last_error()
+    d.q_stride[2] = 100   # 200 bytes: not a multiple of 16
+    rc = lib.race_fwd(ctypes.byref(d), ctypes.c_void_p(16), None, None, None, None, None, None, 0, None)
+    assert rc == -1 and "stride" in _lib.last_error()
+
+
+def test_workspace_too_small_rejected():
+    lib = _lib.load()
+    d = _desc(T=64)
+    p = ctypes.c_void_p(256)
+    rc = lib.race_fwd(ctypes.byref(d), p, p, p, p, p, p, p, 16, None)
+    assert rc == -3 and "workspace" in _lib.last_error()
+
+
+def test_prefix_mean_argument_checks():
+    lib = _lib.load()
+    assert lib.race_prefix_mean_workspace_bytes(4, 100, 64) > 0
+    assert lib.race_prefix_mean_workspace_bytes(0, 100, 64) == 0
+    rc = lib.race_prefix_mean_fwd(None, None, None, 4, 100, 64, 1e-6, None, 0, None)
+    assert rc == -1
+    p = ctypes.c_void_p(256)
+    rc = lib.race_prefix_mean_fwd(p, p, p, 4, 100, 1024, 1e-6, p, 1 << 30, None)
+    assert rc == -2 and "D=1024" in _lib.last_error()
