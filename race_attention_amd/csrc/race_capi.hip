@@ -60,7 +60,7 @@ int make_plan(const race_desc *d, Plan &p) {
                     (long long)d->B, (long long)d->T, (long long)d->H);
     if (d->D != D) return fail(RACE_E_UNSUPPORTED, "head dim D=%lld unsupported (this build: D=64)", (long long)d->D);
     if (d->L < 1 || d->K < 1) return fail(RACE_E_INVALID, "L and K must be >= 1 (got L=%d K=%d)", d->L, d->K);
-    if (d->K > 8) return fail(RACE_E_UNSUPPORTED, "K=%d hash bits unsupported (K <= 8)", d->K);
+    if (d->K > 4) return fail(RACE_E_UNSUPPORTED, "K=%d hash bits unsupported (K <= 4)", d->K);
     if (d->L * d->K > NCOL)
         return fail(RACE_E_UNSUPPORTED, "L*K=%d projection columns unsupported (L*K <= %d)", d->L * d->K, NCOL);
     if (!(d->eps >= 0.f) || d->eps > 1e30f) return fail(RACE_E_INVALID, "eps must be finite and >= 0");
@@ -149,15 +149,15 @@ bool run_phase(const race_desc *d, int ph) { return d->phases == 0 || (d->phases
 
 template <typename T, int SP> int fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
     const dim3 grid(p.nseg, (unsigned)p.N);
-    if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP><<<grid, NT, 0, s>>>(a);
+    if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP><<<grid, 2 * SP, 0, s>>>(a);
     const int elems = SP * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
         k_fwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
     if (run_phase(d, RACE_PHASE_OUT)) {
         if (d->causal)
-            k_fwd_out<T, SP, true><<<grid, NT, 0, s>>>(a);
+            k_fwd_out<T, SP, true><<<grid, 2 * SP, 0, s>>>(a);
         else
-            k_fwd_out<T, SP, false><<<grid, NT, 0, s>>>(a);
+            k_fwd_out<T, SP, false><<<grid, 2 * SP, 0, s>>>(a);
     }
     return launched("race_fwd");
 }
@@ -167,9 +167,9 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
     const dim3 grid(p.nseg, (unsigned)p.N);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
         if (d->causal)
-            k_bwd_reduce<T, SP, true><<<grid, NT, 0, s>>>(a);
+            k_bwd_reduce<T, SP, true><<<grid, 2 * SP, 0, s>>>(a);
         else
-            k_bwd_reduce<T, SP, false><<<grid, NT, 0, s>>>(a);
+            k_bwd_reduce<T, SP, false><<<grid, 2 * SP, 0, s>>>(a);
     }
     const int elems = SP * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
@@ -177,9 +177,9 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
                                                                             d->causal);
     if (run_phase(d, RACE_PHASE_OUT)) {
         if (d->causal)
-            k_bwd_out<T, SP, true><<<grid, NT, 0, s>>>(a);
+            k_bwd_out<T, SP, true><<<grid, 2 * SP, 0, s>>>(a);
         else
-            k_bwd_out<T, SP, false><<<grid, NT, 0, s>>>(a);
+            k_bwd_out<T, SP, false><<<grid, 2 * SP, 0, s>>>(a);
         if (grad_inv_temp) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, 2 * p.N * p.nseg, grad_inv_temp);
     }
     return launched("race_bwd");

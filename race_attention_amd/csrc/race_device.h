@@ -25,8 +25,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int D = 64;       // head dimension handled by this build
 constexpr int TT = 32;      // tokens per tile
 constexpr int NCOL = 32;    // projection columns (L*K <= 32)
-constexpr int NW = 4;       // waves per workgroup
-constexpr int NT = NW * 64; // threads per workgroup
 
 // padded leading dimension (elements) of an LDS array with n logical columns
 template <typename T> __host__ __device__ constexpr int ld_of(int n) { return n + 16 / (int)sizeof(T); }
@@ -119,6 +117,82 @@ __device__ __forceinline__ void st_tile_T(T *dst, int ld, const f32x4 &acc) {
     const int i = lane_id() & 15, g = lane_id() >> 4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) dst[i * ld + 4 * g + e] = from_f32<T>(acc[e]);
+}
+
+// Operand fragment from a pair of accumulator tiles X0 (rows 0..15) and X1
+// (rows 16..31) of a 32-row matrix: element j of lane (g, i) is row
+// pi(g, j) = (j < 4 ? 4g + j : 16 + 4g + j - 4), column i.  Used as a B
+// operand (k = row, n = i) or an A operand (m = i, k = row); the partner
+// operand must be read with ld_frag_pi, which uses the same k order.
+__device__ __forceinline__ Frag<bf16> frag_acc_bf16(const f32x4 &x0, const f32x4 &x1) {
+    Frag<bf16> f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f.v[j] = (bf16)x0[j];
+        f.v[j + 4] = (bf16)x1[j];
+    }
+    return f;
+}
+template <typename T> __device__ __forceinline__ Frag<T> frag_acc(const f32x4 &x0, const f32x4 &x1);
+template <> __device__ __forceinline__ Frag<bf16> frag_acc<bf16>(const f32x4 &x0, const f32x4 &x1) {
+    return frag_acc_bf16(x0, x1);
+}
+template <> __device__ __forceinline__ Frag<float> frag_acc<float>(const f32x4 &x0, const f32x4 &x1) {
+    Frag<float> f;
+    f.lo = x0;
+    f.hi = x1;
+    return f;
+}
+// 8 k values of one row in the pi order: p[4g..4g+3] then p[16+4g..16+4g+3]
+__device__ __forceinline__ Frag<bf16> ld_frag_pi(const bf16 *p) {
+    const int g = lane_id() >> 4;
+    typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    const bf16x4 a = *reinterpret_cast<const bf16x4 *>(p + 4 * g);
+    const bf16x4 b = *reinterpret_cast<const bf16x4 *>(p + 16 + 4 * g);
+    Frag<bf16> f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f.v[j] = a[j];
+        f.v[j + 4] = b[j];
+    }
+    return f;
+}
+__device__ __forceinline__ Frag<float> ld_frag_pi(const float *p) {
+    const int g = lane_id() >> 4;
+    Frag<float> f;
+    f.lo = *reinterpret_cast<const f32x4 *>(p + 4 * g);
+    f.hi = *reinterpret_cast<const f32x4 *>(p + 16 + 4 * g);
+    return f;
+}
+
+// ------------------------------------------------------------ row (16-lane) ops
+// DPP moves inside each 16-lane row; lanes whose source is outside the row read 0.
+template <int CTRL> __device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+// inclusive prefix over the lanes of a row (row_shr 1,2,4,8)
+__device__ __forceinline__ float row_prefix(float x) {
+    x += dpp_f<0x111>(x);
+    x += dpp_f<0x112>(x);
+    x += dpp_f<0x114>(x);
+    x += dpp_f<0x118>(x);
+    return x;
+}
+// inclusive suffix over the lanes of a row (row_shl 1,2,4,8)
+__device__ __forceinline__ float row_suffix(float x) {
+    x += dpp_f<0x101>(x);
+    x += dpp_f<0x102>(x);
+    x += dpp_f<0x104>(x);
+    x += dpp_f<0x108>(x);
+    return x;
+}
+// total of a row in every lane of it (quad swaps, half-row mirror, row mirror)
+__device__ __forceinline__ float row_sum(float x) {
+    x += dpp_f<0xB1>(x);  // quad_perm [1,0,3,2]
+    x += dpp_f<0x4E>(x);  // quad_perm [2,3,0,1]
+    x += dpp_f<0x141>(x); // row_half_mirror
+    x += dpp_f<0x140>(x); // row_mirror
+    return x;
 }
 
 // ------------------------------------------------------------ sigmoids

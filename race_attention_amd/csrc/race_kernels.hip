@@ -1,29 +1,34 @@
 // race_kernels.hip -- gfx950 kernels of the RACE attention operator.
 //
-// Work decomposition.  A stream n = (m, b, h) is a sequence of T tokens.  It
-// is cut into 32-token tiles; consecutive tiles form segments, and one
-// 256-thread workgroup walks one (segment, stream) pair.  Per bucket s the
-// causal state is the prefix pair (A_s, B_s) = (sum P_K, sum P_K v); inside a
-// tile the prefix is rebuilt from the state at the tile start plus a masked
-// 32x32 triangle (W = P_Q/(A+eps); O = W B_start + tril(W P_K^T) V).  Across
-// tiles the state is carried in MFMA accumulators, across segments by a
+// Work decomposition.  A stream n = (m, b, h) is a sequence of T tokens cut
+// into 32-token tiles; consecutive tiles form segments and one workgroup walks
+// one (segment, stream) pair.  Across tiles the per-bucket state (A_s, B_s) =
+// (sum P_K, sum P_K v) is carried in MFMA accumulators; across segments by a
 // three-phase scan:
-//   forward   k_fwd_reduce  per-segment sums of (A,B)        reads K,V
+//   forward   k_fwd_reduce  per-segment sums of (A, B)       reads K, V
 //             k_fwd_scan    exclusive segment prefixes (fp64, kept as state)
-//             k_fwd_out     outputs                          reads Q,K,V writes O
-//   backward  k_bwd_reduce  forward walk: dQ, per-segment sums of
-//                           (alpha, U) = (sum dA, sum W^T g)  reads Q,K,V,dO
+//             k_fwd_out     outputs                         reads Q, K, V, writes O
+//   backward  k_bwd_reduce  forward walk: dQ and per-segment sums of
+//                           alpha = sum dA, U = sum W^T g    reads Q, K, V, dO
 //             k_bwd_scan    exclusive segment suffixes
-//             k_bwd_out     reverse walk: dK, dV             reads Q,K,V,dO
-// The reverse walk of k_bwd_out needs the forward state at every tile start;
-// it subtracts each tile's (A,B) sum, recomputed exactly as k_fwd_reduce
-// computed it, from the segment's end state in fp64.
-// The non-causal operator uses the same kernels with the prefix replaced by
-// the full-sequence sums and no triangle terms.
+//             k_bwd_out     reverse walk: dK, dV            reads Q, K, V, dO
+// The reverse walk needs the forward state at every tile start: it subtracts
+// each tile's (A, B) sums -- recomputed with exactly the code of k_fwd_reduce,
+// so bit-identical -- from the segment's end state in fp64.  The non-causal
+// operator runs the same kernels with full-sequence sums and no triangles.
 //
-// Bucket probabilities are recomputed from Q/K in every kernel (projection on
-// MFMA, tanh, then P[t,l,r] = prod_k sigmoid(+-2u_k), which equals the
-// reference's softmax over the 2^K corner logits).
+// Inside a workgroup wave w owns buckets [32w, 32w+32): the workgroup has
+// SP/32 waves.  Per-bucket quantities live in the "bucket-row" accumulator
+// layout (lane (g,i) holds rows s = 16ms + 4g + e, column t = 16nt + i of a
+// [bucket x token] matrix), where prefix/suffix sums over tokens are 16-lane
+// DPP row scans and the 32 buckets of the wave form one 32-deep MFMA k step,
+// so accumulator tiles feed the next MFMA directly (frag_acc / ld_frag_pi).
+// Token contractions read the transposed operand from LDS.  The triangle of a
+// tile is a masked 32x32 product: O = W B_start + tril(W P_K^T) V.
+//
+// Bucket probabilities are recomputed in every kernel: projection on MFMA,
+// tanh, then P[t, l, r] = prod_k sigmoid(+-2 u_k), which equals the
+// reference's softmax over the 2^K corner logits.
 #include "race_device.h"
 
 namespace race {
@@ -49,7 +54,7 @@ struct Args {
     float *tpart;    // [2][N][nseg] partial sums of dU*th
 };
 
-constexpr int SROW = D + 1; // state row: D values of B (or U) then A (or alpha)
+constexpr int SROW = D + 1;  // state row: D values of B (or U) then A (or alpha)
 
 __device__ __forceinline__ int64_t stream_off(const Strides &s, int n, int B, int H) {
     const int h = n % H, b = (n / H) % B, m = n / (H * B);
@@ -59,15 +64,37 @@ __device__ __forceinline__ int64_t stream_off(const Strides &s, int n, int B, in
 __host__ __device__ constexpr size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
 __host__ __device__ constexpr size_t cmax(size_t a, size_t b) { return a > b ? a : b; }
 
+template <typename T> constexpr bool is_bf16() { return sizeof(T) == 2; }
+
+__device__ __forceinline__ int lg() { return (threadIdx.x & 63) >> 4; }
+__device__ __forceinline__ int li() { return threadIdx.x & 15; }
+
+// value as the MFMA will see it (bf16 rounding for the bf16 path)
+template <typename T> __device__ __forceinline__ float as_operand(float x) { return to_f32(from_f32<T>(x)); }
+
+__device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// 4 consecutive elements (one lane's accumulator column) to global memory
+template <typename T> __device__ __forceinline__ void store4(T *p, const f32x4 &v);
+template <> __device__ __forceinline__ void store4<float>(float *p, const f32x4 &v) {
+    *reinterpret_cast<f32x4 *>(p) = v;
+}
+template <> __device__ __forceinline__ void store4<bf16>(bf16 *p, const f32x4 &v) {
+    typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    bf16x4 o;
+    for (int e = 0; e < 4; ++e) o[e] = (bf16)v[e];
+    *reinterpret_cast<bf16x4 *>(p) = o;
+}
+
 // --------------------------------------------------------------- tile I/O
 // Load a [TT][D] token tile (rows t0.. of a stream, row stride st elements);
 // rows at or beyond T read as zero.  nat: [TT][ld_of<T>(D)], trn: [D][ld_of<T>(TT)].
-template <typename T>
+template <typename T, int NTH>
 __device__ void load_tile(const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn, T *nat, T *trn) {
     constexpr int EPC = 16 / sizeof(T);
     constexpr int CPR = D / EPC;
     constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT);
-    for (int idx = threadIdx.x; idx < TT * CPR; idx += NT) {
+    for (int idx = threadIdx.x; idx < TT * CPR; idx += NTH) {
         const int t = idx / CPR, c = idx % CPR;
         uint4 val = make_uint4(0, 0, 0, 0);
         if (t0 + t < Tn) val = *reinterpret_cast<const uint4 *>(src + (t0 + t) * st + c * EPC);
@@ -80,28 +107,12 @@ __device__ void load_tile(const T *__restrict__ src, int64_t st, int64_t t0, int
     }
 }
 
-// Store a staged [TT][ld_of<T>(D)] tile to rows t0.. (< T) of a stream.
-template <typename T>
-__device__ void store_tile(T *__restrict__ dst, int64_t st, int64_t t0, int64_t Tn, const T *stage) {
-    constexpr int EPC = 16 / sizeof(T);
-    constexpr int CPR = D / EPC;
-    constexpr int LDN = ld_of<T>(D);
-    for (int idx = threadIdx.x; idx < TT * CPR; idx += NT) {
-        const int t = idx / CPR, c = idx % CPR;
-        if (t0 + t < Tn)
-            *reinterpret_cast<uint4 *>(dst + (t0 + t) * st + c * EPC) =
-                *reinterpret_cast<const uint4 *>(stage + t * LDN + c * EPC);
-    }
-}
-
-template <typename T> constexpr bool is_bf16() { return sizeof(T) == 2; }
-
 // Planes [L*K][D] fp32 -> LDS.  pl/pllo: [NCOL][ld_of<T>(D)] (bf16 keeps a
 // hi/lo split so the projection is close to fp32), plt: [D][ld_of<T>(NCOL)].
-template <typename T>
+template <typename T, int NTH>
 __device__ void load_planes(const float *__restrict__ planes, int LK, T *pl, T *pllo, T *plt) {
     constexpr int LDN = ld_of<T>(D), LDC = ld_of<T>(NCOL);
-    for (int idx = threadIdx.x; idx < NCOL * D; idx += NT) {
+    for (int idx = threadIdx.x; idx < NCOL * D; idx += NTH) {
         const int c = idx / D, d = idx % D;
         const float w = c < LK ? planes[c * D + d] : 0.f;
         const T hi = from_f32<T>(w);
@@ -111,107 +122,256 @@ __device__ void load_planes(const float *__restrict__ planes, int LK, T *pl, T *
     }
 }
 
-// One 16x16 projection tile (rows 16*mt.., columns 16*nc..) of X . planes^T,
-// then th = tanh, the sigmoid pair of 2*th*inv_temp into sp/sm [TT][ld_of<float>(NCOL)]
-// and (optionally) th into sth.
+// One 16x16 tile (rows c = 16mc.., columns t = 16nt..) of planes . X^T, then
+// th = tanh and the sigmoid pair of 2*th*inv_temp, stored as sp/sm/sth
+// [TT][ld_of<float>(NCOL)] (lane writes its 4 consecutive c of token t).
 template <typename T>
-__device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mt, int nc, float inv_temp,
-                             float *sp, float *sm, float *sth) {
+__device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mc, int nt, float inv_temp, float *sp,
+                             float *sm, float *sth) {
     constexpr int LDN = ld_of<T>(D), LDC = ld_of<float>(NCOL);
     f32x4 acc = zero4();
-    tile_mma(acc, sx + 16 * mt * LDN, LDN, pl + 16 * nc * LDN, LDN, D / 32);
-    if constexpr (is_bf16<T>()) tile_mma(acc, sx + 16 * mt * LDN, LDN, pllo + 16 * nc * LDN, LDN, D / 32);
-    const int i = lane_id() & 15, g = lane_id() >> 4;
+    tile_mma(acc, pl + 16 * mc * LDN, LDN, sx + 16 * nt * LDN, LDN, D / 32);
+    if constexpr (is_bf16<T>()) tile_mma(acc, pllo + 16 * mc * LDN, LDN, sx + 16 * nt * LDN, LDN, D / 32);
+    const int t = 16 * nt + li(), c0 = 16 * mc + 4 * lg();
+    f32x4 a, b, th;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const int t = 16 * mt + 4 * g + e, c = 16 * nc + i;
-        const float th = tanhf(acc[e]);
-        float a, b;
-        sigmoid_pair(2.f * th * inv_temp, a, b);
-        sp[t * LDC + c] = a;
-        sm[t * LDC + c] = b;
-        if (sth) sth[t * LDC + c] = th;
+        th[e] = tanhf(acc[e]);
+        float x, y;
+        sigmoid_pair(2.f * th[e] * inv_temp, x, y);
+        a[e] = x;
+        b[e] = y;
     }
+    *reinterpret_cast<f32x4 *>(sp + t * LDC + c0) = a;
+    *reinterpret_cast<f32x4 *>(sm + t * LDC + c0) = b;
+    if (sth) *reinterpret_cast<f32x4 *>(sth + t * LDC + c0) = th;
 }
 
-// Bucket probability P[t, s] from the sigmoid tables; s = l*R + r.
-__device__ __forceinline__ float prob_at(const float *sp, const float *sm, int t, int s, int K) {
+// Bucket probabilities of the wave's 32 buckets in bucket-row layout:
+// P[ms][nt][e] = P[t = 16nt + i][s = sw + 16ms + 4g + e]; zero for s >= S or
+// t0 + t >= T.
+template <int KB>
+__device__ __forceinline__ void probs_kb(const float *sp, const float *sm, int sw, int S, int64_t t0, int64_t Tn,
+                                         f32x4 (&P)[2][2]) {
     constexpr int LDC = ld_of<float>(NCOL);
-    const int l = s >> K, r = s & ((1 << K) - 1);
-    const float *p = sp + t * LDC + l * K;
-    const float *q = sm + t * LDC + l * K;
-    float v = 1.f;
-    for (int k = 0; k < K; ++k) v *= ((r >> (K - 1 - k)) & 1) ? p[k] : q[k];
-    return v;
-}
-
-// P_K of a tile into pk [TT][ld_of<T>(SP)] and/or pkt [SP][ld_of<T>(TT)];
-// zero for padded buckets (s >= S) and tokens at or beyond T.
-template <typename T, int SP>
-__device__ void softhash_tile(const float *sp, const float *sm, int K, int S, int64_t t0, int64_t Tn, T *pk,
-                              T *pkt) {
-    constexpr int LDP = ld_of<T>(SP), LDT = ld_of<T>(TT);
-    for (int idx = threadIdx.x; idx < TT * SP; idx += NT) {
-        const int s = idx % SP, t = idx / SP;
-        float p = 0.f;
-        if (s < S && t0 + t < Tn) p = prob_at(sp, sm, t, s, K);
-        const T pv = from_f32<T>(p);
-        if (pk) pk[t * LDP + s] = pv;
-        if (pkt) pkt[s * LDT + t] = pv;
-    }
-}
-
-// Softmax/corner/tanh backward of one tile: dP [TT][ld_of<float>(SP)] ->
-// dproj [TT][ld_of<T>(NCOL)] (columns < L*K); returns this thread's sum of du*th.
-template <typename T, int SP>
-__device__ float softhash_bwd_tile(const float *sp, const float *sm, const float *sth, const float *dP, int L,
-                                   int K, int64_t t0, int64_t Tn, float inv_temp, T *dproj) {
-    constexpr int LDC = ld_of<float>(NCOL), LDA = ld_of<float>(SP), LDDP = ld_of<T>(NCOL);
-    const int R = 1 << K;
-    float tsum = 0.f;
-    for (int idx = threadIdx.x; idx < TT * L; idx += NT) {
-        const int t = idx / L, l = idx % L;
-        float du[8];
+    constexpr int R = 1 << KB;
+    const int g = lg(), i = li();
 #pragma unroll
-        for (int k = 0; k < 8; ++k) du[k] = 0.f;
-        if (t0 + t < Tn) {
-            float dot = 0.f;
-            for (int r = 0; r < R; ++r) dot += prob_at(sp, sm, t, l * R + r, K) * dP[t * LDA + l * R + r];
-            for (int r = 0; r < R; ++r) {
-                const float w = prob_at(sp, sm, t, l * R + r, K) * (dP[t * LDA + l * R + r] - dot);
+    for (int nt = 0; nt < 2; ++nt) {
+        const int t = 16 * nt + i;
+        const bool tv = t0 + t < Tn;
 #pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    if (k < K) du[k] += ((r >> (K - 1 - k)) & 1) ? w : -w;
+        for (int ms = 0; ms < 2; ++ms) {
+            const int s0 = sw + 16 * ms + 4 * g;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int s = s0 + e, l = s < S ? s >> KB : 0, r = s & (R - 1);
+                const float *p = sp + t * LDC + l * KB;
+                const float *q = sm + t * LDC + l * KB;
+                float v = 1.f;
+#pragma unroll
+                for (int k = 0; k < KB; ++k) v *= ((r >> (KB - 1 - k)) & 1) ? p[k] : q[k];
+                P[ms][nt][e] = (s < S && tv) ? v : 0.f;
             }
         }
+    }
+}
+
+__device__ __forceinline__ void probs_st(int K, const float *sp, const float *sm, int sw, int S, int64_t t0,
+                                         int64_t Tn, f32x4 (&P)[2][2]) {
+    switch (K) {
+    case 1: probs_kb<1>(sp, sm, sw, S, t0, Tn, P); break;
+    case 2: probs_kb<2>(sp, sm, sw, S, t0, Tn, P); break;
+    case 3: probs_kb<3>(sp, sm, sw, S, t0, Tn, P); break;
+    default: probs_kb<4>(sp, sm, sw, S, t0, Tn, P); break;
+    }
+}
+
+// sum over the buckets of one table that share this lane's token: in-lane
+// over e (pairs for KB = 1) and across rows g for KB >= 3
+template <int KB> __device__ __forceinline__ float table_reduce(float x) {
+    if constexpr (KB >= 3) x += __shfl_xor(x, 16, 64);
+    if constexpr (KB >= 4) x += __shfl_xor(x, 32, 64);
+    return x;
+}
+
+// Softmax / corner / tanh backward in bucket-row layout for the wave's
+// buckets: dP (and P, fp32) -> dproj [TT][ld_of<T>(NCOL)] columns l*K + k of
+// the wave's tables; returns this lane's share of sum du * th.
+template <int KB, typename T>
+__device__ float softhash_bwd_kb(const f32x4 (&P)[2][2], const f32x4 (&dP)[2][2], const float *sth, int sw, int L,
+                                 float inv_temp, T *dproj) {
+    constexpr int LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
+    constexpr int R = 1 << KB;
+    constexpr int RPT = R >= 4 ? R / 4 : 1;  // rows g per table
+    const int g = lg(), i = li();
+    float tsum = 0.f;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if (k < K) {
-                const float th = sth[t * LDC + l * K + k];
-                tsum += du[k] * th;
-                dproj[t * LDDP + l * K + k] = from_f32<T>(du[k] * inv_temp * (1.f - th * th));
+    for (int nt = 0; nt < 2; ++nt) {
+        const int t = 16 * nt + i;
+#pragma unroll
+        for (int ms = 0; ms < 2; ++ms) {
+            const int s0 = sw + 16 * ms + 4 * g;
+            f32x4 pd, dl;
+            for (int e = 0; e < 4; ++e) pd[e] = P[ms][nt][e] * dP[ms][nt][e];
+            if constexpr (KB == 1) {
+                const float d01 = pd[0] + pd[1], d23 = pd[2] + pd[3];
+                for (int e = 0; e < 4; ++e) dl[e] = P[ms][nt][e] * (dP[ms][nt][e] - (e < 2 ? d01 : d23));
+                // tables (s0 >> 1) and (s0 >> 1) + 1, one hash bit each
+                for (int h = 0; h < 2; ++h) {
+                    const int l = (s0 >> 1) + h;
+                    const float du = dl[2 * h + 1] - dl[2 * h];  // r = 1 is corner +1
+                    if (l < L) {
+                        const float th = sth[t * LDC + l];
+                        tsum += du * th;
+                        dproj[t * LDDP + l] = from_f32<T>(du * inv_temp * (1.f - th * th));
+                    }
+                }
+            } else {
+                const float dot = table_reduce<KB>(pd[0] + pd[1] + pd[2] + pd[3]);
+                for (int e = 0; e < 4; ++e) dl[e] = P[ms][nt][e] * (dP[ms][nt][e] - dot);
+                const int l = s0 >> KB;
+#pragma unroll
+                for (int k = 0; k < KB; ++k) {
+                    float part = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = (s0 + e) & (R - 1);
+                        part += ((r >> (KB - 1 - k)) & 1) ? dl[e] : -dl[e];
+                    }
+                    const float du = table_reduce<KB>(part);
+                    if (l < L && (k % RPT) == (g % RPT)) {
+                        const float th = sth[t * LDC + l * KB + k];
+                        tsum += du * th;
+                        dproj[t * LDDP + l * KB + k] = from_f32<T>(du * inv_temp * (1.f - th * th));
+                    }
+                }
             }
         }
     }
     return tsum;
 }
 
-// dX tile = dproj . planes  (rows 16*mt, cols 16*nd), into a staging tile.
 template <typename T>
-__device__ void dx_tile(const T *dproj, const T *plt, int mt, int nd, T *stage) {
-    constexpr int LDDP = ld_of<T>(NCOL), LDN = ld_of<T>(D);
-    f32x4 acc = zero4();
-    tile_mma(acc, dproj + 16 * mt * LDDP, LDDP, plt + 16 * nd * LDDP, LDDP, NCOL / 32);
-    st_tile(stage + 16 * mt * LDN + 16 * nd, LDN, acc);
+__device__ __forceinline__ float softhash_bwd_st(int K, const f32x4 (&P)[2][2], const f32x4 (&dP)[2][2],
+                                                 const float *sth, int sw, int L, float inv_temp, T *dproj) {
+    switch (K) {
+    case 1: return softhash_bwd_kb<1, T>(P, dP, sth, sw, L, inv_temp, dproj);
+    case 2: return softhash_bwd_kb<2, T>(P, dP, sth, sw, L, inv_temp, dproj);
+    case 3: return softhash_bwd_kb<3, T>(P, dP, sth, sw, L, inv_temp, dproj);
+    default: return softhash_bwd_kb<4, T>(P, dP, sth, sw, L, inv_temp, dproj);
+    }
 }
 
-// Sum of a wave-ordered per-thread value over the workgroup (fixed order).
-__device__ float block_sum(float v, float *scratch) {
+// Per-bucket token sums of a tile: tot[ms][e] = sum over the tile's 32 tokens
+// (identical code in every kernel, so the values are bit-identical).
+__device__ __forceinline__ void tile_totals(const f32x4 (&X)[2][2], float (&tot)[2][4]) {
+#pragma unroll
+    for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tot[ms][e] = row_sum(X[ms][0][e]) + row_sum(X[ms][1][e]);
+}
+// inclusive prefix over the tile's tokens, plus base
+__device__ __forceinline__ void tile_prefix(const f32x4 (&X)[2][2], f32x4 (&Y)[2][2]) {
+#pragma unroll
+    for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float tot0 = row_sum(X[ms][0][e]);
+            Y[ms][0][e] = row_prefix(X[ms][0][e]);
+            Y[ms][1][e] = row_prefix(X[ms][1][e]) + tot0;
+        }
+}
+// inclusive suffix over the tile's tokens
+__device__ __forceinline__ void tile_suffix(const f32x4 (&X)[2][2], f32x4 (&Y)[2][2]) {
+#pragma unroll
+    for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float tot1 = row_sum(X[ms][1][e]);
+            Y[ms][1][e] = row_suffix(X[ms][1][e]);
+            Y[ms][0][e] = row_suffix(X[ms][0][e]) + tot1;
+        }
+}
+
+// bucket-row values -> per-wave transposed LDS [32 s][ld_of<T>(TT)] (rows s, columns t)
+template <typename T> __device__ __forceinline__ void store_rows_T(T *dst, const f32x4 (&X)[2][2]) {
+    constexpr int LDT = ld_of<T>(TT);
+    const int g = lg(), i = li();
+#pragma unroll
+    for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dst[(16 * ms + 4 * g + e) * LDT + 16 * nt + i] = from_f32<T>(X[ms][nt][e]);
+}
+
+// d-row tile sums dB^T = V^T P_K for the wave's buckets (fp32 MFMA from zero):
+// out[md][ns] lane holds dB^T[d = 16md + 4g + e][s = sw + 16ns + i]
+template <typename T>
+__device__ __forceinline__ void tile_dBT(const T *vt, const T *pkt, f32x4 (&out)[4][2]) {
+    constexpr int LDT = ld_of<T>(TT);
+    const int g = lg(), i = li();
+#pragma unroll
+    for (int ns = 0; ns < 2; ++ns) {
+        const Frag<T> b = ld_frag(pkt + (16 * ns + i) * LDT + 8 * g);
+#pragma unroll
+        for (int md = 0; md < 4; ++md) {
+            out[md][ns] = zero4();
+            mma(out[md][ns], ld_frag(vt + (16 * md + i) * LDT + 8 * g), b);
+        }
+    }
+}
+
+// dX for the tile: dX^T = planes^T dproj^T, 8 tiles over the workgroup's waves,
+// stored straight to rows t0.. (< T) of dst.
+template <typename T, int NW_>
+__device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64_t t0, int64_t Tn) {
+    constexpr int LDDP = ld_of<T>(NCOL);
+    const int g = lg(), i = li(), w = wave_id();
+    for (int q = w; q < 8; q += NW_) {
+        const int md = q >> 1, nt = q & 1;
+        f32x4 acc = zero4();
+        tile_mma(acc, plt + 16 * md * LDDP, LDDP, dproj + 16 * nt * LDDP, LDDP, NCOL / 32);
+        const int t = 16 * nt + i;
+        if (t0 + t < Tn) store4<T>(dst + (t0 + t) * st + 16 * md + 4 * g, acc);
+    }
+}
+
+// Output tiles out[md][nt] (lane holds X^T[d = 16md + 4g + e][t = 16nt + i],
+// this wave's partial over its buckets): sum over the waves and store rows t.
+template <typename T, int NW_>
+__device__ void reduce_store(const f32x4 (&part)[4][2], float *red, T *dst, int64_t st, int64_t t0, int64_t Tn) {
+    constexpr int LDR = ld_of<float>(D);
+    const int g = lg(), i = li(), w = wave_id();
+    if constexpr (NW_ == 1) {
+        for (int md = 0; md < 4; ++md)
+            for (int nt = 0; nt < 2; ++nt) {
+                const int t = 16 * nt + i;
+                if (t0 + t < Tn) store4<T>(dst + (t0 + t) * st + 16 * md + 4 * g, part[md][nt]);
+            }
+    } else {
+        float *mine = red + w * TT * LDR;
+        for (int md = 0; md < 4; ++md)
+            for (int nt = 0; nt < 2; ++nt)
+                *reinterpret_cast<f32x4 *>(mine + (16 * nt + i) * LDR + 16 * md + 4 * g) = part[md][nt];
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < TT * D / 4; idx += 64 * NW_) {
+            const int t = idx / (D / 4), d0 = 4 * (idx % (D / 4));
+            f32x4 s = *reinterpret_cast<const f32x4 *>(red + t * LDR + d0);
+            for (int ww = 1; ww < NW_; ++ww) s += *reinterpret_cast<const f32x4 *>(red + ww * TT * LDR + t * LDR + d0);
+            if (t0 + t < Tn) store4<T>(dst + (t0 + t) * st + d0, s);
+        }
+    }
+}
+
+// Sum of a per-thread value over the workgroup in a fixed order.
+template <int NTH> __device__ float block_sum(float v, float *scratch) {
     scratch[threadIdx.x] = v;
     __syncthreads();
     if (threadIdx.x == 0) {
         float s = 0.f;
-        for (int j = 0; j < NT; ++j) s += scratch[j];
+        for (int j = 0; j < NTH; ++j) s += scratch[j];
         scratch[0] = s;
     }
     __syncthreads();
@@ -220,56 +380,34 @@ __device__ float block_sum(float v, float *scratch) {
     return r;
 }
 
-// The carry tiles of a wave: q = wave + NW*j, (ms, nd) = (q / 4, q % 4) over
-// the [SP][D] state.  Lane holds state[16ms + 4g + e][16nd + i].
-template <int SP> struct Carry {
-    static constexpr int NTL = SP / 16 * 4 / NW;
-    __device__ static int ms(int j) { return (wave_id() + NW * j) >> 2; }
-    __device__ static int nd(int j) { return (wave_id() + NW * j) & 3; }
-};
-
-// One tile's (A,B) sums: dB = P_K^T V for this wave's carry tiles (fp32 MFMA
-// from zero) -- shared by k_fwd_reduce and k_bwd_out so that both get
-// bit-identical values.
-template <typename T, int SP>
-__device__ __forceinline__ f32x4 tile_dB(const T *pkt, const T *vt, int j) {
-    constexpr int LDT = ld_of<T>(TT);
-    f32x4 c = zero4();
-    tile_mma(c, pkt + 16 * Carry<SP>::ms(j) * LDT, LDT, vt + 16 * Carry<SP>::nd(j) * LDT, LDT, 1);
-    return c;
-}
-// ... and the per-bucket A sum, summed in token order by thread s.
-template <typename T>
-__device__ __forceinline__ float tile_dA(const T *pkt, int s) {
-    constexpr int LDT = ld_of<T>(TT);
-    float run = 0.f;
-    for (int t = 0; t < TT; ++t) run += to_f32(pkt[s * LDT + t]);
-    return run;
-}
+// state row index of (bucket s, column d)
+__device__ __forceinline__ int64_t sidx(int s, int d) { return (int64_t)s * SROW + d; }
 
 // =====================================================================
 // k_fwd_reduce: per-segment (A, B) sums (fp64 over fp32 tile sums).
 // =====================================================================
 template <typename T, int SP> struct FwdReduceL {
+    static constexpr int NW_ = SP / 32;
     static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL);
     static constexpr size_t oK = 0;
     static constexpr size_t oVt = align16(oK + sizeof(T) * TT * LDN);
     static constexpr size_t oPkt = align16(oVt + sizeof(T) * D * LDT);
     static constexpr size_t oPl = align16(oPkt + sizeof(T) * SP * LDT);
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oSp = align16(oPlLo + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oSm = align16(oSp + sizeof(float) * TT * LDC);
-    static constexpr size_t bytes = align16(oSm + sizeof(float) * TT * LDC);
+    static constexpr size_t oSig = align16(oPlLo + sizeof(T) * NCOL * LDN);
+    static constexpr size_t bytes = align16(oSig + sizeof(float) * 2 * TT * LDC);
 };
 
 template <typename T, int SP>
-__global__ __launch_bounds__(NT) void k_fwd_reduce(Args a) {
+__global__ __launch_bounds__(SP * 2) void k_fwd_reduce(Args a) {
     using Ly = FwdReduceL<T, SP>;
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
-    T *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt), *sPkt = (T *)(smem + Ly::oPkt);
+    T *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
-    float *sSp = (float *)(smem + Ly::oSp), *sSm = (float *)(smem + Ly::oSm);
-    constexpr int NTL = Carry<SP>::NTL;
+    float *sSp = (float *)(smem + Ly::oSig), *sSm = sSp + TT * LDC;
+    const int w = wave_id(), g = lg(), i = li(), sw = 32 * w;
+    T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -278,34 +416,46 @@ __global__ __launch_bounds__(NT) void k_fwd_reduce(Args a) {
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
 
-    load_planes<T>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
-    double accB[NTL][4];
-    for (int j = 0; j < NTL; ++j)
-        for (int e = 0; e < 4; ++e) accB[j][e] = 0.0;
-    double accA = 0.0;
+    load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
+    double accB[4][2][4], accA[2][4];
+    for (int md = 0; md < 4; ++md)
+        for (int ns = 0; ns < 2; ++ns)
+            for (int e = 0; e < 4; ++e) accB[md][ns][e] = 0.0;
+    for (int ms = 0; ms < 2; ++ms)
+        for (int e = 0; e < 4; ++e) accA[ms][e] = 0.0;
 
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
         __syncthreads();
-        load_tile<T>(kp, a.sk.t, t0, a.T, sK, nullptr);
-        load_tile<T>(vp, a.sv.t, t0, a.T, nullptr, sVt);
+        load_tile<T, NTH>(kp, a.sk.t, t0, a.T, sK, nullptr);
+        load_tile<T, NTH>(vp, a.sv.t, t0, a.T, nullptr, sVt);
         __syncthreads();
-        project_tile<T>(sK, sPl, sPlLo, wave_id() >> 1, wave_id() & 1, a.inv_temp, sSp, sSm, nullptr);
+        for (int q = w; q < 4; q += NW_) project_tile<T>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, nullptr);
         __syncthreads();
-        softhash_tile<T, SP>(sSp, sSm, a.K, a.S, t0, a.T, nullptr, sPkt);
+        f32x4 PK[2][2];
+        probs_st(a.K, sSp, sSm, sw, a.S, t0, a.T, PK);
+        for (int ms = 0; ms < 2; ++ms)
+            for (int nt = 0; nt < 2; ++nt)
+                for (int e = 0; e < 4; ++e) PK[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
+        store_rows_T<T>(sPkt, PK);
+        float tot[2][4];
+        tile_totals(PK, tot);
+        for (int ms = 0; ms < 2; ++ms)
+            for (int e = 0; e < 4; ++e) accA[ms][e] += (double)tot[ms][e];
         __syncthreads();
-        if (threadIdx.x < SP) accA += (double)tile_dA<T>(sPkt, threadIdx.x);
-        for (int j = 0; j < NTL; ++j) {
-            const f32x4 c = tile_dB<T, SP>(sPkt, sVt, j);
-            for (int e = 0; e < 4; ++e) accB[j][e] += (double)c[e];
-        }
+        f32x4 dB[4][2];
+        tile_dBT<T>(sVt, sPkt, dB);
+        for (int md = 0; md < 4; ++md)
+            for (int ns = 0; ns < 2; ++ns)
+                for (int e = 0; e < 4; ++e) accB[md][ns][e] += (double)dB[md][ns][e];
     }
     double *out = a.fdelta + ((int64_t)n * a.nseg + seg) * SP * SROW;
-    const int i = lane_id() & 15, g = lane_id() >> 4;
-    for (int j = 0; j < NTL; ++j)
-        for (int e = 0; e < 4; ++e)
-            out[(16 * Carry<SP>::ms(j) + 4 * g + e) * SROW + 16 * Carry<SP>::nd(j) + i] = accB[j][e];
-    if (threadIdx.x < SP) out[threadIdx.x * SROW + D] = accA;
+    for (int md = 0; md < 4; ++md)
+        for (int ns = 0; ns < 2; ++ns)
+            for (int e = 0; e < 4; ++e) out[sidx(sw + 16 * ns + i, 16 * md + 4 * g + e)] = accB[md][ns][e];
+    if (i == 0)
+        for (int ms = 0; ms < 2; ++ms)
+            for (int e = 0; e < 4; ++e) out[sidx(sw + 16 * ms + 4 * g + e, D)] = accA[ms][e];
 }
 
 // exclusive prefix over segments; [nseg] receives the total
@@ -321,39 +471,34 @@ __global__ void k_fwd_scan(double *fstate, const double *fdelta, int nseg, int e
 }
 
 // =====================================================================
-// k_fwd_out: outputs.
+// k_fwd_out: outputs O^T = B^T W^T + V^T tril(W P_K^T)^T per wave, summed
+// over the waves.
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct FwdOutL {
-    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDP = ld_of<T>(SP), LDC = ld_of<float>(NCOL);
-    static constexpr size_t oQ = 0;  // Q tile, then output staging
+    static constexpr int NW_ = SP / 32;
+    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDR = ld_of<float>(D);
+    static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
     static constexpr size_t oVt = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
-    static constexpr size_t oPk = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oPkt = align16(oPk + (CAUSAL ? sizeof(T) * TT * LDP : 0));
-    static constexpr size_t oW = align16(oPkt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
-    static constexpr size_t oBct = align16(oW + sizeof(T) * TT * LDP);
-    static constexpr size_t oSc = align16(oBct + sizeof(T) * D * LDP);
-    static constexpr size_t oPl = align16(oSc + (CAUSAL ? sizeof(T) * TT * LDT : 0));
+    static constexpr size_t oPkt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
+    static constexpr size_t oPl = align16(oPkt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oSig = align16(oPlLo + sizeof(T) * NCOL * LDN);  // [2 tensors][2][TT][LDC]
-    static constexpr size_t oAc = align16(oSig + sizeof(float) * 4 * TT * LDC);
-    static constexpr size_t bytes = align16(oAc + sizeof(double) * SP);
+    static constexpr size_t oSig = align16(oPlLo + sizeof(T) * NCOL * LDN);  // Q sp, Q sm, K sp, K sm
+    static constexpr size_t oRed = align16(oSig + sizeof(float) * 4 * TT * LDC);
+    static constexpr size_t bytes = align16(oRed + (NW_ > 1 ? sizeof(float) * NW_ * TT * LDR : 0));
 };
 
 template <typename T, int SP, bool CAUSAL>
-__global__ __launch_bounds__(NT) void k_fwd_out(Args a) {
+__global__ __launch_bounds__(SP * 2) void k_fwd_out(Args a) {
     using Ly = FwdOutL<T, SP, CAUSAL>;
-    constexpr int LDN = Ly::LDN, LDT = Ly::LDT, LDP = Ly::LDP, LDC = Ly::LDC;
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
-    T *sPk = (T *)(smem + Ly::oPk), *sPkt = (T *)(smem + Ly::oPkt), *sW = (T *)(smem + Ly::oW);
-    T *sBct = (T *)(smem + Ly::oBct), *sSc = (T *)(smem + Ly::oSc);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
-    float *sSig = (float *)(smem + Ly::oSig);
+    float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sSpK = sSig + 2 * TT * LDC, *sSmK = sSig + 3 * TT * LDC;
-    double *sAc = (double *)(smem + Ly::oAc);
-    T *sO = sQ;
-    constexpr int NTL = Carry<SP>::NTL;
+    const int w = wave_id(), g = lg(), i = li(), sw = 32 * w;
+    T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -363,80 +508,94 @@ __global__ __launch_bounds__(NT) void k_fwd_out(Args a) {
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
     T *op = (T *)a.out + stream_off(a.so, n, a.B, a.H);
-    const int i = lane_id() & 15, g = lane_id() >> 4, w = wave_id();
 
-    load_planes<T>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
-    // carried state: causal = prefix at the segment start, non-causal = totals
+    load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
+    // carried state: causal = prefix at the segment start, non-causal = totals.
+    // B in bucket-row layout: lane holds B[s = sw + 16ms + 4g + e][d = 16md + i]
     const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * SP * SROW;
-    f32x4 accB[NTL];
-    for (int j = 0; j < NTL; ++j) {
-        for (int e = 0; e < 4; ++e)
-            accB[j][e] = (float)st[(16 * Carry<SP>::ms(j) + 4 * g + e) * SROW + 16 * Carry<SP>::nd(j) + i];
-        st_tile_T(sBct + 16 * Carry<SP>::nd(j) * LDP + 16 * Carry<SP>::ms(j), LDP, accB[j]);
+    f32x4 Bc[2][4];
+    double a0[2][4];
+    for (int ms = 0; ms < 2; ++ms) {
+        for (int md = 0; md < 4; ++md)
+            for (int e = 0; e < 4; ++e) Bc[ms][md][e] = (float)st[sidx(sw + 16 * ms + 4 * g + e, 16 * md + i)];
+        for (int e = 0; e < 4; ++e) a0[ms][e] = st[sidx(sw + 16 * ms + 4 * g + e, D)];
     }
-    if (threadIdx.x < SP) sAc[threadIdx.x] = st[threadIdx.x * SROW + D];
 
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
         __syncthreads();
-        load_tile<T>(qp, a.sq.t, t0, a.T, sQ, nullptr);
+        load_tile<T, NTH>(qp, a.sq.t, t0, a.T, sQ, nullptr);
         if constexpr (CAUSAL) {
-            load_tile<T>(kp, a.sk.t, t0, a.T, sK, nullptr);
-            load_tile<T>(vp, a.sv.t, t0, a.T, nullptr, sVt);
+            load_tile<T, NTH>(kp, a.sk.t, t0, a.T, sK, nullptr);
+            load_tile<T, NTH>(vp, a.sv.t, t0, a.T, nullptr, sVt);
         }
         __syncthreads();
-        project_tile<T>(sQ, sPl, sPlLo, w >> 1, w & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
-        if constexpr (CAUSAL) project_tile<T>(sK, sPl, sPlLo, w >> 1, w & 1, a.inv_temp, sSpK, sSmK, nullptr);
+        for (int q = w; q < (CAUSAL ? 8 : 4); q += NW_) {
+            if (q < 4)
+                project_tile<T>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+            else
+                project_tile<T>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
+        }
         __syncthreads();
+        f32x4 PQ[2][2], PK[2][2], Acum[2][2];
+        probs_st(a.K, sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
         if constexpr (CAUSAL) {
-            softhash_tile<T, SP>(sSpK, sSmK, a.K, a.S, t0, a.T, sPk, sPkt);
-            __syncthreads();
+            probs_st(a.K, sSpK, sSmK, sw, a.S, t0, a.T, PK);
+            for (int ms = 0; ms < 2; ++ms)
+                for (int nt = 0; nt < 2; ++nt)
+                    for (int e = 0; e < 4; ++e) PK[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
+            store_rows_T<T>(sPkt, PK);
+            tile_prefix(PK, Acum);
         }
-        if (threadIdx.x < SP) {  // W = P_Q / (A(t) + eps)
-            const int s = threadIdx.x;
-            const float a0 = (float)sAc[s];
-            float run = 0.f;
-            for (int t = 0; t < TT; ++t) {
-                if constexpr (CAUSAL) run += to_f32(sPkt[s * LDT + t]);
-                const float pq = (s < a.S && t0 + t < a.T) ? prob_at(sSpQ, sSmQ, t, s, a.K) : 0.f;
-                sW[t * LDP + s] = from_f32<T>(pq / (a0 + run + a.eps));
+        // W = P_Q / (A(t) + eps)
+        f32x4 W[2][2];
+        for (int ms = 0; ms < 2; ++ms)
+            for (int nt = 0; nt < 2; ++nt)
+                for (int e = 0; e < 4; ++e) {
+                    const float A = (float)a0[ms][e] + (CAUSAL ? Acum[ms][nt][e] : 0.f);
+                    W[ms][nt][e] = PQ[ms][nt][e] * rcp(A + a.eps);
+                }
+        Frag<T> Wf[2];
+        for (int nt = 0; nt < 2; ++nt) Wf[nt] = frag_acc<T>(W[0][nt], W[1][nt]);
+        // O1^T[d][t] = sum_s B[s][d] W[t][s]
+        f32x4 O[4][2];
+        for (int md = 0; md < 4; ++md) {
+            const Frag<T> bf = frag_acc<T>(Bc[0][md], Bc[1][md]);
+            for (int nt = 0; nt < 2; ++nt) {
+                O[md][nt] = zero4();
+                mma(O[md][nt], bf, Wf[nt]);
             }
-            if constexpr (CAUSAL) sAc[s] += (double)run;
         }
-        __syncthreads();
-        if constexpr (CAUSAL) {  // Sc = tril(W P_K^T): waves 0-2 the lower tiles, wave 3 zeroes tile (0,1)
-            const int mt = w == 0 ? 0 : 1, nt = w == 2 ? 1 : 0;
-            if (w < 3) {
-                f32x4 c = zero4();
-                tile_mma(c, sW + 16 * mt * LDP, LDP, sPk + 16 * nt * LDP, LDP, SP / 32);
-                for (int e = 0; e < 4; ++e)
-                    if (16 * nt + i > 16 * mt + 4 * g + e) c[e] = 0.f;
-                st_tile(sSc + 16 * mt * LDT + 16 * nt, LDT, c);
-            } else {
-                st_tile(sSc + 16, LDT, zero4());
+        if constexpr (CAUSAL) {
+            // Sc^T[t'][t] = sum_s P_K[t'][s] W[t][s], kept for t' <= t
+            f32x4 Sc[2][2];
+            Frag<T> PKf[2];
+            for (int nt = 0; nt < 2; ++nt) PKf[nt] = frag_acc<T>(PK[0][nt], PK[1][nt]);
+            for (int mt = 0; mt < 2; ++mt)
+                for (int nt = 0; nt < 2; ++nt) {
+                    Sc[mt][nt] = zero4();
+                    if (mt <= nt) mma(Sc[mt][nt], PKf[mt], Wf[nt]);
+                    for (int e = 0; e < 4; ++e)
+                        if (16 * mt + 4 * g + e > 16 * nt + i) Sc[mt][nt][e] = 0.f;
+                }
+            for (int ms = 0; ms < 2; ++ms) {
+                float tot[4];
+                for (int e = 0; e < 4; ++e) tot[e] = row_sum(PK[ms][0][e]) + row_sum(PK[ms][1][e]);
+                for (int e = 0; e < 4; ++e) a0[ms][e] += (double)tot[e];
             }
-            __syncthreads();
+            __syncthreads();  // sPkt of this wave complete
+            // O2^T[d][t] = sum_t' V[t'][d] Sc^T[t'][t]
+            for (int nt = 0; nt < 2; ++nt) {
+                const Frag<T> sf = frag_acc<T>(Sc[0][nt], Sc[1][nt]);
+                for (int md = 0; md < 4; ++md) mma(O[md][nt], ld_frag_pi(sVt + (16 * md + i) * LDT), sf);
+            }
+            // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
+            for (int ms = 0; ms < 2; ++ms) {
+                const Frag<T> pa = ld_frag(sPkt + (16 * ms + i) * LDT + 8 * g);
+                for (int md = 0; md < 4; ++md) mma(Bc[ms][md], pa, ld_frag(sVt + (16 * md + i) * LDT + 8 * g));
+            }
         }
-        f32x4 oacc[2];
-        for (int j = 0; j < 2; ++j) {
-            const int q = w + NW * j, mt = q >> 2, nd = q & 3;
-            oacc[j] = zero4();
-            tile_mma(oacc[j], sW + 16 * mt * LDP, LDP, sBct + 16 * nd * LDP, LDP, SP / 32);
-            if constexpr (CAUSAL) tile_mma(oacc[j], sSc + 16 * mt * LDT, LDT, sVt + 16 * nd * LDT, LDT, 1);
-        }
-        if constexpr (CAUSAL)
-            for (int j = 0; j < NTL; ++j)
-                tile_mma(accB[j], sPkt + 16 * Carry<SP>::ms(j) * LDT, LDT, sVt + 16 * Carry<SP>::nd(j) * LDT, LDT, 1);
-        __syncthreads();
-        for (int j = 0; j < 2; ++j) {
-            const int q = w + NW * j, mt = q >> 2, nd = q & 3;
-            st_tile(sO + 16 * mt * LDN + 16 * nd, LDN, oacc[j]);
-        }
-        if constexpr (CAUSAL)
-            for (int j = 0; j < NTL; ++j)
-                st_tile_T(sBct + 16 * Carry<SP>::nd(j) * LDP + 16 * Carry<SP>::ms(j), LDP, accB[j]);
-        __syncthreads();
-        store_tile<T>(op, a.so.t, t0, a.T, sO);
+        reduce_store<T, NW_>(O, sRed, op, a.so.t, t0, a.T);
     }
 }
 
@@ -445,9 +604,9 @@ __global__ __launch_bounds__(NT) void k_fwd_out(Args a) {
 // alpha = sum_t dA and U = sum_t W^T g.
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct BwdReduceL {
-    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDA = ld_of<float>(SP),
-                         LDDP = ld_of<T>(NCOL);
-    static constexpr size_t oQ = 0;  // Q tile, then dQ staging
+    static constexpr int NW_ = SP / 32;
+    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
+    static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
     static constexpr size_t oV = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oG = align16(oV + (CAUSAL ? sizeof(T) * TT * LDN : 0));
@@ -455,37 +614,29 @@ template <typename T, int SP, bool CAUSAL> struct BwdReduceL {
     static constexpr size_t oGt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
     static constexpr size_t oPkt = align16(oGt + sizeof(T) * D * LDT);
     static constexpr size_t oWt = align16(oPkt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
-    static constexpr size_t oBc = align16(oWt + sizeof(T) * SP * LDT);
-    static constexpr size_t oHm = align16(oBc + sizeof(T) * SP * LDN);
-    static constexpr size_t oDA = align16(oHm + (CAUSAL ? sizeof(T) * TT * LDT : 0));
-    static constexpr size_t oDproj = align16(oDA + sizeof(float) * TT * LDA);
+    static constexpr size_t oDproj = align16(oWt + sizeof(T) * SP * LDT);
     static constexpr size_t oPl = align16(oDproj + sizeof(T) * TT * LDDP);
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t oPlT = align16(oPlLo + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oSig = align16(oPlT + sizeof(T) * D * LDDP);  // [Q sp, Q sm, Q th, K sp, K sm]
-    static constexpr size_t oAc = align16(oSig + sizeof(float) * 5 * TT * LDC);
-    static constexpr size_t oAl = align16(oAc + sizeof(double) * SP);
-    static constexpr size_t oRed = align16(oAl + sizeof(double) * SP);
-    static constexpr size_t bytes = align16(oRed + sizeof(float) * NT);
+    static constexpr size_t oSig = align16(oPlT + sizeof(T) * D * LDDP);  // Q sp, Q sm, Q th, K sp, K sm
+    static constexpr size_t oRed = align16(oSig + sizeof(float) * 5 * TT * LDC);
+    static constexpr size_t bytes = align16(oRed + sizeof(float) * 64 * NW_);
 };
 
 template <typename T, int SP, bool CAUSAL>
-__global__ __launch_bounds__(NT) void k_bwd_reduce(Args a) {
+__global__ __launch_bounds__(SP * 2) void k_bwd_reduce(Args a) {
     using Ly = BwdReduceL<T, SP, CAUSAL>;
-    constexpr int LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDA = Ly::LDA, LDDP = Ly::LDDP;
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sV = (T *)(smem + Ly::oV);
     T *sG = (T *)(smem + Ly::oG), *sVt = (T *)(smem + Ly::oVt), *sGt = (T *)(smem + Ly::oGt);
-    T *sPkt = (T *)(smem + Ly::oPkt), *sWt = (T *)(smem + Ly::oWt), *sBc = (T *)(smem + Ly::oBc);
-    T *sHm = (T *)(smem + Ly::oHm), *sDproj = (T *)(smem + Ly::oDproj);
+    T *sDproj = (T *)(smem + Ly::oDproj);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo), *sPlT = (T *)(smem + Ly::oPlT);
-    float *sDA = (float *)(smem + Ly::oDA), *sSig = (float *)(smem + Ly::oSig);
+    float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sThQ = sSig + 2 * TT * LDC;
     float *sSpK = sSig + 3 * TT * LDC, *sSmK = sSig + 4 * TT * LDC;
-    double *sAc = (double *)(smem + Ly::oAc), *sAl = (double *)(smem + Ly::oAl);
-    float *sRed = (float *)(smem + Ly::oRed);
-    T *sStage = sQ;
-    constexpr int NTL = Carry<SP>::NTL;
+    const int w = wave_id(), g = lg(), i = li(), sw = 32 * w;
+    T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT, *sWt = (T *)(smem + Ly::oWt) + sw * LDT;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -496,114 +647,124 @@ __global__ __launch_bounds__(NT) void k_bwd_reduce(Args a) {
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
     const T *gp = (const T *)a.dout + stream_off(a.sdo, n, a.B, a.H);
     T *dqp = (T *)a.dq + stream_off(a.sg, n, a.B, a.H);
-    const int i = lane_id() & 15, g = lane_id() >> 4, w = wave_id();
 
-    load_planes<T>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
-    for (int idx = threadIdx.x; idx < TT * LDDP; idx += NT) sDproj[idx] = from_f32<T>(0.f);
+    load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
+    for (int idx = threadIdx.x; idx < TT * LDDP; idx += NTH) sDproj[idx] = from_f32<T>(0.f);
+    // forward state in d-row layout: lane holds B^T[d = 16md + 4g + e][s = sw + 16ns + i]
     const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * SP * SROW;
-    f32x4 accB[NTL], accU[NTL];
-    for (int j = 0; j < NTL; ++j) {
-        accU[j] = zero4();
-        for (int e = 0; e < 4; ++e)
-            accB[j][e] = (float)st[(16 * Carry<SP>::ms(j) + 4 * g + e) * SROW + 16 * Carry<SP>::nd(j) + i];
-        st_tile(sBc + 16 * Carry<SP>::ms(j) * LDN + 16 * Carry<SP>::nd(j), LDN, accB[j]);
-    }
-    if (threadIdx.x < SP) {
-        sAc[threadIdx.x] = st[threadIdx.x * SROW + D];
-        sAl[threadIdx.x] = 0.0;
-    }
+    f32x4 Bt[4][2], Ut[4][2];
+    double a0[2][4], al[2][4];
+    for (int md = 0; md < 4; ++md)
+        for (int ns = 0; ns < 2; ++ns) {
+            Ut[md][ns] = zero4();
+            for (int e = 0; e < 4; ++e) Bt[md][ns][e] = (float)st[sidx(sw + 16 * ns + i, 16 * md + 4 * g + e)];
+        }
+    for (int ms = 0; ms < 2; ++ms)
+        for (int e = 0; e < 4; ++e) {
+            a0[ms][e] = st[sidx(sw + 16 * ms + 4 * g + e, D)];
+            al[ms][e] = 0.0;
+        }
     float tsum = 0.f;
 
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
         __syncthreads();
-        load_tile<T>(qp, a.sq.t, t0, a.T, sQ, nullptr);
-        load_tile<T>(gp, a.sdo.t, t0, a.T, sG, sGt);
+        load_tile<T, NTH>(qp, a.sq.t, t0, a.T, sQ, nullptr);
+        load_tile<T, NTH>(gp, a.sdo.t, t0, a.T, sG, sGt);
         if constexpr (CAUSAL) {
-            load_tile<T>(kp, a.sk.t, t0, a.T, sK, nullptr);
-            load_tile<T>(vp, a.sv.t, t0, a.T, sV, sVt);
+            load_tile<T, NTH>(kp, a.sk.t, t0, a.T, sK, nullptr);
+            load_tile<T, NTH>(vp, a.sv.t, t0, a.T, sV, sVt);
         }
         __syncthreads();
-        project_tile<T>(sQ, sPl, sPlLo, w >> 1, w & 1, a.inv_temp, sSpQ, sSmQ, sThQ);
-        if constexpr (CAUSAL) project_tile<T>(sK, sPl, sPlLo, w >> 1, w & 1, a.inv_temp, sSpK, sSmK, nullptr);
+        for (int q = w; q < (CAUSAL ? 8 : 4); q += NW_) {
+            if (q < 4)
+                project_tile<T>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, sThQ);
+            else
+                project_tile<T>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
+        }
         __syncthreads();
+        f32x4 PQ[2][2], PK[2][2], Acum[2][2], W[2][2], inv[2][2];
+        probs_st(a.K, sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
         if constexpr (CAUSAL) {
-            softhash_tile<T, SP>(sSpK, sSmK, a.K, a.S, t0, a.T, nullptr, sPkt);
-            __syncthreads();
+            probs_st(a.K, sSpK, sSmK, sw, a.S, t0, a.T, PK);
+            for (int ms = 0; ms < 2; ++ms)
+                for (int nt = 0; nt < 2; ++nt)
+                    for (int e = 0; e < 4; ++e) PK[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
+            store_rows_T<T>(sPkt, PK);
+            tile_prefix(PK, Acum);
         }
-        if (threadIdx.x < SP) {  // W^T into sWt
-            const int s = threadIdx.x;
-            const float a0 = (float)sAc[s];
-            float run = 0.f;
-            for (int t = 0; t < TT; ++t) {
-                if constexpr (CAUSAL) run += to_f32(sPkt[s * LDT + t]);
-                const float pq = (s < a.S && t0 + t < a.T) ? prob_at(sSpQ, sSmQ, t, s, a.K) : 0.f;
-                sWt[s * LDT + t] = from_f32<T>(pq / (a0 + run + a.eps));
+        for (int ms = 0; ms < 2; ++ms)
+            for (int nt = 0; nt < 2; ++nt)
+                for (int e = 0; e < 4; ++e) {
+                    const float A = (float)a0[ms][e] + (CAUSAL ? Acum[ms][nt][e] : 0.f);
+                    inv[ms][nt][e] = rcp(A + a.eps);
+                    W[ms][nt][e] = PQ[ms][nt][e] * inv[ms][nt][e];
+                }
+        store_rows_T<T>(sWt, W);
+        // Hm^T[tau][t] = v_tau . g_t for tau <= t (B operand over tau, pi order)
+        f32x4 HmT[2][2];
+        if constexpr (CAUSAL) {
+            for (int mt = 0; mt < 2; ++mt)
+                for (int nt = 0; nt < 2; ++nt) {
+                    HmT[mt][nt] = zero4();
+                    if (mt <= nt) tile_mma(HmT[mt][nt], sV + 16 * mt * LDN, LDN, sG + 16 * nt * LDN, LDN, D / 32);
+                    for (int e = 0; e < 4; ++e)
+                        if (16 * mt + 4 * g + e > 16 * nt + i) HmT[mt][nt][e] = 0.f;
+                }
+        }
+        __syncthreads();  // sPkt, sWt of this wave complete
+        // G[s][t] = g_t . B_s(t) = sum_d B[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] Hm[t][tau]
+        f32x4 G[2][2];
+        for (int ms = 0; ms < 2; ++ms)
+            for (int nt = 0; nt < 2; ++nt) {
+                G[ms][nt] = zero4();
+                for (int kk = 0; kk < 2; ++kk)
+                    mma(G[ms][nt], frag_acc<T>(Bt[2 * kk][ms], Bt[2 * kk + 1][ms]),
+                        ld_frag_pi(sG + (16 * nt + i) * LDN + 32 * kk));
+                if constexpr (CAUSAL)
+                    mma(G[ms][nt], ld_frag_pi(sPkt + (16 * ms + i) * LDT), frag_acc<T>(HmT[0][nt], HmT[1][nt]));
+            }
+        // dP_Q = G/(A+eps); dA = -W G/(A+eps)
+        f32x4 dPQ[2][2], dA[2][2];
+        for (int ms = 0; ms < 2; ++ms)
+            for (int nt = 0; nt < 2; ++nt)
+                for (int e = 0; e < 4; ++e) {
+                    dPQ[ms][nt][e] = G[ms][nt][e] * inv[ms][nt][e];
+                    dA[ms][nt][e] = -W[ms][nt][e] * dPQ[ms][nt][e];
+                }
+        {
+            float tot[2][4];
+            tile_totals(dA, tot);
+            for (int ms = 0; ms < 2; ++ms)
+                for (int e = 0; e < 4; ++e) al[ms][e] += (double)tot[ms][e];
+        }
+        // U^T[d][s] += sum_t g[t][d] W[t][s]; carry B^T[d][s] += sum_t V[t][d] P_K[t][s]
+        for (int ns = 0; ns < 2; ++ns) {
+            const Frag<T> wb = ld_frag(sWt + (16 * ns + i) * LDT + 8 * g);
+            for (int md = 0; md < 4; ++md) mma(Ut[md][ns], ld_frag(sGt + (16 * md + i) * LDT + 8 * g), wb);
+            if constexpr (CAUSAL) {
+                const Frag<T> pb = ld_frag(sPkt + (16 * ns + i) * LDT + 8 * g);
+                for (int md = 0; md < 4; ++md) mma(Bt[md][ns], ld_frag(sVt + (16 * md + i) * LDT + 8 * g), pb);
             }
         }
-        if constexpr (CAUSAL) {  // Hm = tril(g V^T) (tau <= t)
-            const int mt = w == 0 ? 0 : 1, nt = w == 2 ? 1 : 0;
-            if (w < 3) {
-                f32x4 c = zero4();
-                tile_mma(c, sG + 16 * mt * LDN, LDN, sV + 16 * nt * LDN, LDN, D / 32);
-                for (int e = 0; e < 4; ++e)
-                    if (16 * nt + i > 16 * mt + 4 * g + e) c[e] = 0.f;
-                st_tile(sHm + 16 * mt * LDT + 16 * nt, LDT, c);
-            } else {
-                st_tile(sHm + 16, LDT, zero4());
-            }
+        if constexpr (CAUSAL) {
+            float tot[2][4];
+            tile_totals(PK, tot);
+            for (int ms = 0; ms < 2; ++ms)
+                for (int e = 0; e < 4; ++e) a0[ms][e] += (double)tot[ms][e];
         }
+        tsum += softhash_bwd_st<T>(a.K, PQ, dPQ, sThQ, sw, a.L, a.inv_temp, sDproj);
         __syncthreads();
-        // G[t,s] = g_t . B_s(t) = g B_start^T + tril(g V^T) P_K
-        for (int q = w; q < 2 * SP / 16; q += NW) {
-            const int mt = q & 1, ns = q >> 1;
-            f32x4 c = zero4();
-            tile_mma(c, sG + 16 * mt * LDN, LDN, sBc + 16 * ns * LDN, LDN, D / 32);
-            if constexpr (CAUSAL) tile_mma(c, sHm + 16 * mt * LDT, LDT, sPkt + 16 * ns * LDT, LDT, 1);
-            st_tile(sDA + 16 * mt * LDA + 16 * ns, LDA, c);
-        }
-        for (int j = 0; j < NTL; ++j) {
-            tile_mma(accU[j], sWt + 16 * Carry<SP>::ms(j) * LDT, LDT, sGt + 16 * Carry<SP>::nd(j) * LDT, LDT, 1);
-            if constexpr (CAUSAL)
-                tile_mma(accB[j], sPkt + 16 * Carry<SP>::ms(j) * LDT, LDT, sVt + 16 * Carry<SP>::nd(j) * LDT, LDT,
-                         1);
-        }
-        __syncthreads();
-        if (threadIdx.x < SP) {  // dP_Q = G/(A+eps) in place; alpha += sum_t -W G/(A+eps)
-            const int s = threadIdx.x;
-            const float a0 = (float)sAc[s];
-            float run = 0.f, sda = 0.f;
-            for (int t = 0; t < TT; ++t) {
-                if constexpr (CAUSAL) run += to_f32(sPkt[s * LDT + t]);
-                const float inv = 1.f / (a0 + run + a.eps);
-                const float pq = (s < a.S && t0 + t < a.T) ? prob_at(sSpQ, sSmQ, t, s, a.K) : 0.f;
-                const float G = sDA[t * LDA + s];
-                sDA[t * LDA + s] = G * inv;
-                sda -= pq * inv * G * inv;
-            }
-            sAl[s] += (double)sda;
-            if constexpr (CAUSAL) sAc[s] += (double)run;
-        }
-        if constexpr (CAUSAL)
-            for (int j = 0; j < NTL; ++j)
-                st_tile(sBc + 16 * Carry<SP>::ms(j) * LDN + 16 * Carry<SP>::nd(j), LDN, accB[j]);
-        __syncthreads();
-        tsum += softhash_bwd_tile<T, SP>(sSpQ, sSmQ, sThQ, sDA, a.L, a.K, t0, a.T, a.inv_temp, sDproj);
-        __syncthreads();
-        for (int j = 0; j < 2; ++j) {
-            const int q = w + NW * j;
-            dx_tile<T>(sDproj, sPlT, q >> 2, q & 3, sStage);
-        }
-        __syncthreads();
-        store_tile<T>(dqp, a.sg.t, t0, a.T, sStage);
+        dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0, a.T);
     }
     float *out = a.rdelta + ((int64_t)n * a.nseg + seg) * SP * SROW;
-    for (int j = 0; j < NTL; ++j)
-        for (int e = 0; e < 4; ++e)
-            out[(16 * Carry<SP>::ms(j) + 4 * g + e) * SROW + 16 * Carry<SP>::nd(j) + i] = accU[j][e];
-    __syncthreads();
-    if (threadIdx.x < SP) out[threadIdx.x * SROW + D] = (float)sAl[threadIdx.x];
-    const float ts = block_sum(tsum, sRed);
+    for (int md = 0; md < 4; ++md)
+        for (int ns = 0; ns < 2; ++ns)
+            for (int e = 0; e < 4; ++e) out[sidx(sw + 16 * ns + i, 16 * md + 4 * g + e)] = Ut[md][ns][e];
+    if (i == 0)
+        for (int ms = 0; ms < 2; ++ms)
+            for (int e = 0; e < 4; ++e) out[sidx(sw + 16 * ms + 4 * g + e, D)] = (float)al[ms][e];
+    const float ts = block_sum<NTH>(tsum, sRed);
     if (threadIdx.x == 0) a.tpart[(int64_t)n * a.nseg + seg] = ts;
 }
 
@@ -627,52 +788,40 @@ __global__ void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int ele
 // k_bwd_out: reverse walk.  dK, dV.
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct BwdOutL {
-    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDP = ld_of<T>(SP), LDC = ld_of<float>(NCOL),
-                         LDA = ld_of<float>(SP), LDDP = ld_of<T>(NCOL);
-    // region X: {Q, K} during projection; {Hm, HmT, Sc2} in the middle; {stage, dproj} at the end
-    static constexpr size_t xsz = cmax(cmax(sizeof(T) * 2 * TT * LDN, sizeof(T) * 3 * TT * LDT),
-                                       align16(sizeof(T) * TT * LDN) + sizeof(T) * TT * LDDP);
-    static constexpr size_t oX = 0;
-    static constexpr size_t oV = align16(oX + xsz);
+    static constexpr int NW_ = SP / 32;
+    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL),
+                         LDR = ld_of<float>(D);
+    static constexpr size_t oQ = 0;
+    static constexpr size_t oK = align16(oQ + (CAUSAL ? sizeof(T) * TT * LDN : 0));
+    static constexpr size_t oV = align16(oK + sizeof(T) * TT * LDN);
     static constexpr size_t oG = align16(oV + sizeof(T) * TT * LDN);
     static constexpr size_t oVt = align16(oG + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oGt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oPk = align16(oGt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oPkt = align16(oPk + sizeof(T) * TT * LDP);
-    static constexpr size_t oW = align16(oPkt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
-    static constexpr size_t oWt = align16(oW + (CAUSAL ? sizeof(T) * TT * LDP : 0));
-    static constexpr size_t oBs = align16(oWt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
-    static constexpr size_t oUt = align16(oBs + (CAUSAL ? sizeof(T) * SP * LDN : 0));
-    static constexpr size_t oDA = align16(oUt + sizeof(T) * D * LDP);
-    static constexpr size_t oPl = align16(oDA + sizeof(float) * TT * LDA);
+    static constexpr size_t oPkt = align16(oGt + (CAUSAL ? sizeof(T) * D * LDT : 0));
+    static constexpr size_t oWt = align16(oPkt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
+    static constexpr size_t oDproj = align16(oWt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
+    static constexpr size_t oPl = align16(oDproj + sizeof(T) * TT * LDDP);
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oPlT = align16(oPlLo + (is_bf16<T>() ? sizeof(T) * NCOL * LDN : 0));
-    static constexpr size_t oSig = align16(oPlT + sizeof(T) * D * LDDP);  // [K sp, K sm, K th, Q sp, Q sm]
-    static constexpr size_t oAe = align16(oSig + sizeof(float) * (CAUSAL ? 5 : 3) * TT * LDC);
-    static constexpr size_t oAl = align16(oAe + sizeof(double) * SP);
-    static constexpr size_t oRed = align16(oAl + sizeof(float) * SP);
-    static constexpr size_t bytes = align16(oRed + sizeof(float) * NT);
+    static constexpr size_t oPlT = align16(oPlLo + sizeof(T) * NCOL * LDN);
+    static constexpr size_t oSig = align16(oPlT + sizeof(T) * D * LDDP);  // K sp, K sm, K th, Q sp, Q sm
+    static constexpr size_t oRed = align16(oSig + sizeof(float) * (CAUSAL ? 5 : 3) * TT * LDC);
+    static constexpr size_t bytes = align16(oRed + sizeof(float) * cmax(64 * NW_, NW_ > 1 ? NW_ * TT * LDR : 0));
 };
 
 template <typename T, int SP, bool CAUSAL>
-__global__ __launch_bounds__(NT) void k_bwd_out(Args a) {
+__global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
     using Ly = BwdOutL<T, SP, CAUSAL>;
-    constexpr int LDN = Ly::LDN, LDT = Ly::LDT, LDP = Ly::LDP, LDC = Ly::LDC, LDA = Ly::LDA, LDDP = Ly::LDDP;
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
-    T *sQ = (T *)(smem + Ly::oX), *sK = sQ + TT * LDN;
-    T *sHm = (T *)(smem + Ly::oX), *sHmT = sHm + TT * LDT, *sSc2 = sHm + 2 * TT * LDT;
-    T *sStage = (T *)(smem + Ly::oX), *sDproj = (T *)(smem + Ly::oX + align16(sizeof(T) * TT * LDN));
-    T *sV = (T *)(smem + Ly::oV), *sG = (T *)(smem + Ly::oG), *sVt = (T *)(smem + Ly::oVt);
-    T *sGt = (T *)(smem + Ly::oGt), *sPk = (T *)(smem + Ly::oPk), *sPkt = (T *)(smem + Ly::oPkt);
-    T *sW = (T *)(smem + Ly::oW), *sWt = (T *)(smem + Ly::oWt), *sBs = (T *)(smem + Ly::oBs);
-    T *sUt = (T *)(smem + Ly::oUt);
+    T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sV = (T *)(smem + Ly::oV);
+    T *sG = (T *)(smem + Ly::oG), *sVt = (T *)(smem + Ly::oVt), *sGt = (T *)(smem + Ly::oGt);
+    T *sDproj = (T *)(smem + Ly::oDproj);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo), *sPlT = (T *)(smem + Ly::oPlT);
-    float *sDA = (float *)(smem + Ly::oDA), *sSig = (float *)(smem + Ly::oSig);
+    float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
     float *sSpK = sSig, *sSmK = sSig + TT * LDC, *sThK = sSig + 2 * TT * LDC;
     float *sSpQ = sSig + 3 * TT * LDC, *sSmQ = sSig + 4 * TT * LDC;
-    double *sAe = (double *)(smem + Ly::oAe);
-    float *sAl = (float *)(smem + Ly::oAl), *sRed = (float *)(smem + Ly::oRed);
-    constexpr int NTL = Carry<SP>::NTL;
+    const int w = wave_id(), g = lg(), i = li(), sw = 32 * w;
+    T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT, *sWt = (T *)(smem + Ly::oWt) + sw * LDT;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -684,170 +833,187 @@ __global__ __launch_bounds__(NT) void k_bwd_out(Args a) {
     const T *gp = (const T *)a.dout + stream_off(a.sdo, n, a.B, a.H);
     T *dkp = (T *)a.dk + stream_off(a.sg, n, a.B, a.H);
     T *dvp = (T *)a.dv + stream_off(a.sg, n, a.B, a.H);
-    const int i = lane_id() & 15, g = lane_id() >> 4, w = wave_id();
 
-    load_planes<T>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
-    // reverse carries (U, alpha) at the segment end; forward state at the segment end
+    load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
+    for (int idx = threadIdx.x; idx < TT * LDDP; idx += NTH) sDproj[idx] = from_f32<T>(0.f);
+    // reverse carries (U, alpha) after the segment; forward state at the segment end
     const float *rs = a.rstate + ((int64_t)n * a.nseg + seg) * SP * SROW;
     const double *fs = a.fstate + ((int64_t)n * (a.nseg + 1) + seg + 1) * SP * SROW;
-    f32x4 accU[NTL];
-    double accB[NTL][4];
-    for (int j = 0; j < NTL; ++j) {
+    f32x4 Ut[4][2], Us[2][4];  // U^T[d][s] (d-row) and U[s][d] (bucket-row)
+    double Be[4][2][4], Ae[2][4];
+    float al[2][4];
+    for (int md = 0; md < 4; ++md)
+        for (int ns = 0; ns < 2; ++ns)
+            for (int e = 0; e < 4; ++e) {
+                const int64_t r = sidx(sw + 16 * ns + i, 16 * md + 4 * g + e);
+                Ut[md][ns][e] = rs[r];
+                Be[md][ns][e] = CAUSAL ? fs[r] : 0.0;
+            }
+    for (int ms = 0; ms < 2; ++ms) {
+        for (int md = 0; md < 4; ++md)
+            for (int e = 0; e < 4; ++e) Us[ms][md][e] = rs[sidx(sw + 16 * ms + 4 * g + e, 16 * md + i)];
         for (int e = 0; e < 4; ++e) {
-            const int r = (16 * Carry<SP>::ms(j) + 4 * g + e) * SROW + 16 * Carry<SP>::nd(j) + i;
-            accU[j][e] = rs[r];
-            accB[j][e] = CAUSAL ? fs[r] : 0.0;
+            al[ms][e] = rs[sidx(sw + 16 * ms + 4 * g + e, D)];
+            Ae[ms][e] = CAUSAL ? fs[sidx(sw + 16 * ms + 4 * g + e, D)] : 0.0;
         }
-        st_tile_T(sUt + 16 * Carry<SP>::nd(j) * LDP + 16 * Carry<SP>::ms(j), LDP, accU[j]);
-    }
-    if (threadIdx.x < SP) {
-        sAl[threadIdx.x] = rs[threadIdx.x * SROW + D];
-        if (CAUSAL) sAe[threadIdx.x] = fs[threadIdx.x * SROW + D];
     }
     float tsum = 0.f;
 
     for (int64_t jr = j1 - 1; jr >= j0; --jr) {
         const int64_t t0 = jr * TT;
         __syncthreads();
-        load_tile<T>(kp, a.sk.t, t0, a.T, sK, nullptr);
-        load_tile<T>(vp, a.sv.t, t0, a.T, sV, CAUSAL ? sVt : nullptr);
+        load_tile<T, NTH>(kp, a.sk.t, t0, a.T, sK, nullptr);
+        load_tile<T, NTH>(vp, a.sv.t, t0, a.T, sV, CAUSAL ? sVt : nullptr);
         if constexpr (CAUSAL) {
-            load_tile<T>(qp, a.sq.t, t0, a.T, sQ, nullptr);
-            load_tile<T>(gp, a.sdo.t, t0, a.T, sG, sGt);
+            load_tile<T, NTH>(qp, a.sq.t, t0, a.T, sQ, nullptr);
+            load_tile<T, NTH>(gp, a.sdo.t, t0, a.T, sG, sGt);
         }
         __syncthreads();
-        project_tile<T>(sK, sPl, sPlLo, w >> 1, w & 1, a.inv_temp, sSpK, sSmK, sThK);
-        if constexpr (CAUSAL) project_tile<T>(sQ, sPl, sPlLo, w >> 1, w & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+        for (int q = w; q < (CAUSAL ? 8 : 4); q += NW_) {
+            if (q < 4)
+                project_tile<T>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpK, sSmK, sThK);
+            else
+                project_tile<T>(sQ, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+        }
         __syncthreads();
-        softhash_tile<T, SP>(sSpK, sSmK, a.K, a.S, t0, a.T, sPk, CAUSAL ? sPkt : nullptr);
-        __syncthreads();
+        f32x4 PK[2][2], PKr[2][2];  // fp32 and operand-rounded
+        probs_st(a.K, sSpK, sSmK, sw, a.S, t0, a.T, PK);
+        for (int ms = 0; ms < 2; ++ms)
+            for (int nt = 0; nt < 2; ++nt)
+                for (int e = 0; e < 4; ++e) PKr[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
+        Frag<T> PKf[2];
+        for (int nt = 0; nt < 2; ++nt) PKf[nt] = frag_acc<T>(PKr[0][nt], PKr[1][nt]);
+        f32x4 dPK[2][2];
+        f32x4 VT[4][2];  // dV^T partial: lane holds dV^T[d = 16md + 4g + e][tau = 16nt + i]
         if constexpr (CAUSAL) {
-            // forward state at the tile start: end state minus this tile's sums (fp64)
-            for (int j = 0; j < NTL; ++j) {
-                const f32x4 c = tile_dB<T, SP>(sPkt, sVt, j);
-                for (int e = 0; e < 4; ++e) accB[j][e] -= (double)c[e];
-                f32x4 b;
-                for (int e = 0; e < 4; ++e) b[e] = (float)accB[j][e];
-                st_tile(sBs + 16 * Carry<SP>::ms(j) * LDN + 16 * Carry<SP>::nd(j), LDN, b);
+            f32x4 PQ[2][2], Acum[2][2], W[2][2], inv[2][2];
+            probs_st(a.K, sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
+            store_rows_T<T>(sPkt, PKr);
+            // forward state at the tile start: end state minus this tile's sums
+            {
+                float tot[2][4];
+                tile_totals(PKr, tot);
+                for (int ms = 0; ms < 2; ++ms)
+                    for (int e = 0; e < 4; ++e) Ae[ms][e] -= (double)tot[ms][e];
             }
-            if (threadIdx.x < SP) {
-                const int s = threadIdx.x;
-                const double as = sAe[s] - (double)tile_dA<T>(sPkt, s);
-                sAe[s] = as;
-                const float a0 = (float)as;
-                float run = 0.f;
-                for (int t = 0; t < TT; ++t) {
-                    run += to_f32(sPkt[s * LDT + t]);
-                    const float pq = (s < a.S && t0 + t < a.T) ? prob_at(sSpQ, sSmQ, t, s, a.K) : 0.f;
-                    const T wv = from_f32<T>(pq / (a0 + run + a.eps));
-                    sW[t * LDP + s] = wv;
-                    sWt[s * LDT + t] = wv;
-                }
-            }
-            __syncthreads();
-            // region X now holds Hm [t][tau] (tau <= t), HmT [tau][t], Sc2 [tau][t] (t >= tau)
-            for (int q = w; q < 8; q += NW) {
-                const int kind = q >> 2, sub = q & 3;  // sub: 0 (0,0), 1 (1,0), 2 (1,1), 3 zero tile
-                const int mt = sub == 0 ? 0 : 1, nt = sub == 2 ? 1 : 0;
-                if (kind == 0) {
-                    if (sub < 3) {
-                        f32x4 c = zero4();
-                        tile_mma(c, sG + 16 * mt * LDN, LDN, sV + 16 * nt * LDN, LDN, D / 32);
-                        for (int e = 0; e < 4; ++e)
-                            if (16 * nt + i > 16 * mt + 4 * g + e) c[e] = 0.f;
-                        st_tile(sHm + 16 * mt * LDT + 16 * nt, LDT, c);
-                        st_tile_T(sHmT + 16 * nt * LDT + 16 * mt, LDT, c);
-                    } else {
-                        st_tile(sHm + 16, LDT, zero4());
-                        st_tile(sHmT + 16 * LDT, LDT, zero4());
+            tile_prefix(PKr, Acum);
+            for (int ms = 0; ms < 2; ++ms)
+                for (int nt = 0; nt < 2; ++nt)
+                    for (int e = 0; e < 4; ++e) {
+                        inv[ms][nt][e] = rcp((float)Ae[ms][e] + Acum[ms][nt][e] + a.eps);
+                        W[ms][nt][e] = PQ[ms][nt][e] * inv[ms][nt][e];
                     }
-                } else {
-                    // Sc2[tau][t] = sum_s P_K[tau,s] W[t,s] for t >= tau: tiles (tau-tile, t-tile)
-                    const int mtau = sub == 2 ? 1 : 0, ntt = sub == 0 ? 0 : 1;
-                    if (sub < 3) {
-                        f32x4 c = zero4();
-                        tile_mma(c, sPk + 16 * mtau * LDP, LDP, sW + 16 * ntt * LDP, LDP, SP / 32);
-                        for (int e = 0; e < 4; ++e)
-                            if (16 * ntt + i < 16 * mtau + 4 * g + e) c[e] = 0.f;
-                        st_tile(sSc2 + 16 * mtau * LDT + 16 * ntt, LDT, c);
-                    } else {
-                        st_tile(sSc2 + 16 * LDT, LDT, zero4());
+            store_rows_T<T>(sWt, W);
+            f32x4 HmT[2][2], Hm[2][2];
+            for (int mt = 0; mt < 2; ++mt)
+                for (int nt = 0; nt < 2; ++nt) {
+                    // Hm^T[tau][t] (tau <= t) for G; Hm[t][tau] (tau <= t) for dP_K
+                    HmT[mt][nt] = zero4();
+                    Hm[mt][nt] = zero4();
+                    if (mt <= nt) tile_mma(HmT[mt][nt], sV + 16 * mt * LDN, LDN, sG + 16 * nt * LDN, LDN, D / 32);
+                    if (mt >= nt) tile_mma(Hm[mt][nt], sG + 16 * mt * LDN, LDN, sV + 16 * nt * LDN, LDN, D / 32);
+                    for (int e = 0; e < 4; ++e) {
+                        if (16 * mt + 4 * g + e > 16 * nt + i) HmT[mt][nt][e] = 0.f;
+                        if (16 * nt + i > 16 * mt + 4 * g + e) Hm[mt][nt][e] = 0.f;
                     }
                 }
-            }
-            __syncthreads();
-            // G = g B_start^T + tril(g V^T) P_K
-            for (int q = w; q < 2 * SP / 16; q += NW) {
-                const int mt = q & 1, ns = q >> 1;
-                f32x4 c = zero4();
-                tile_mma(c, sG + 16 * mt * LDN, LDN, sBs + 16 * ns * LDN, LDN, D / 32);
-                tile_mma(c, sHm + 16 * mt * LDT, LDT, sPkt + 16 * ns * LDT, LDT, 1);
-                st_tile(sDA + 16 * mt * LDA + 16 * ns, LDA, c);
-            }
-            __syncthreads();
-            if (threadIdx.x < SP) {  // dA = -W G/(A+eps), then alpha(tau) = alpha_end + suffix sum
-                const int s = threadIdx.x;
-                const float a0 = (float)sAe[s];
-                float run = 0.f;
-                for (int t = 0; t < TT; ++t) {
-                    run += to_f32(sPkt[s * LDT + t]);
-                    const float inv = 1.f / (a0 + run + a.eps);
-                    const float pq = (s < a.S && t0 + t < a.T) ? prob_at(sSpQ, sSmQ, t, s, a.K) : 0.f;
-                    sDA[t * LDA + s] = -pq * inv * sDA[t * LDA + s] * inv;
+            __syncthreads();  // sPkt, sWt of this wave complete
+            f32x4 dB[4][2];
+            tile_dBT<T>(sVt, sPkt, dB);
+            f32x4 Bs[4][2];
+            for (int md = 0; md < 4; ++md)
+                for (int ns = 0; ns < 2; ++ns)
+                    for (int e = 0; e < 4; ++e) {
+                        Be[md][ns][e] -= (double)dB[md][ns][e];
+                        Bs[md][ns][e] = (float)Be[md][ns][e];
+                    }
+            // G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] Hm[t][tau]; dA = -W G/(A+eps)
+            f32x4 dA[2][2];
+            for (int ms = 0; ms < 2; ++ms)
+                for (int nt = 0; nt < 2; ++nt) {
+                    f32x4 G = zero4();
+                    for (int kk = 0; kk < 2; ++kk)
+                        mma(G, frag_acc<T>(Bs[2 * kk][ms], Bs[2 * kk + 1][ms]),
+                            ld_frag_pi(sG + (16 * nt + i) * LDN + 32 * kk));
+                    mma(G, ld_frag_pi(sPkt + (16 * ms + i) * LDT), frag_acc<T>(HmT[0][nt], HmT[1][nt]));
+                    for (int e = 0; e < 4; ++e) dA[ms][nt][e] = -W[ms][nt][e] * G[e] * inv[ms][nt][e];
                 }
-                float al = sAl[s];
-                for (int t = TT - 1; t >= 0; --t) {
-                    al += sDA[t * LDA + s];
-                    sDA[t * LDA + s] = al;
+            // alpha(tau) = alpha_end + sum_{t >= tau} dA
+            f32x4 alpha[2][2];
+            tile_suffix(dA, alpha);
+            {
+                float tot[2][4];
+                tile_totals(dA, tot);
+                for (int ms = 0; ms < 2; ++ms)
+                    for (int nt = 0; nt < 2; ++nt)
+                        for (int e = 0; e < 4; ++e) alpha[ms][nt][e] += al[ms][e];
+                for (int ms = 0; ms < 2; ++ms)
+                    for (int e = 0; e < 4; ++e) al[ms][e] += tot[ms][e];
+            }
+            // dP_K[tau][s] = alpha + sum_d U[s][d] v_tau[d] + sum_{t >= tau} W[t][s] Hm[t][tau]
+            for (int ms = 0; ms < 2; ++ms)
+                for (int nt = 0; nt < 2; ++nt) {
+                    f32x4 c = zero4();
+                    for (int kk = 0; kk < 2; ++kk)
+                        mma(c, frag_acc<T>(Ut[2 * kk][ms], Ut[2 * kk + 1][ms]),
+                            ld_frag_pi(sV + (16 * nt + i) * LDN + 32 * kk));
+                    mma(c, ld_frag_pi(sWt + (16 * ms + i) * LDT), frag_acc<T>(Hm[0][nt], Hm[1][nt]));
+                    for (int e = 0; e < 4; ++e) dPK[ms][nt][e] = c[e] + alpha[ms][nt][e];
                 }
-                sAl[s] = al;
+            // Sc2^T[t][tau] = sum_s W[t][s] P_K[tau][s] for t >= tau
+            f32x4 Sc2[2][2];
+            Frag<T> Wf[2];
+            for (int nt = 0; nt < 2; ++nt) Wf[nt] = frag_acc<T>(W[0][nt], W[1][nt]);
+            for (int mt = 0; mt < 2; ++mt)
+                for (int nt = 0; nt < 2; ++nt) {
+                    Sc2[mt][nt] = zero4();
+                    if (mt >= nt) mma(Sc2[mt][nt], Wf[mt], PKf[nt]);
+                    for (int e = 0; e < 4; ++e)
+                        if (16 * mt + 4 * g + e < 16 * nt + i) Sc2[mt][nt][e] = 0.f;
+                }
+            // dV^T[d][tau] = sum_s U[s][d] P_K[tau][s] + sum_{t >= tau} g[t][d] Sc2^T[t][tau]
+            for (int md = 0; md < 4; ++md) {
+                const Frag<T> uf = frag_acc<T>(Us[0][md], Us[1][md]);
+                const Frag<T> gf = ld_frag_pi(sGt + (16 * md + i) * LDT);
+                for (int nt = 0; nt < 2; ++nt) {
+                    VT[md][nt] = zero4();
+                    mma(VT[md][nt], uf, PKf[nt]);
+                    mma(VT[md][nt], gf, frag_acc<T>(Sc2[0][nt], Sc2[1][nt]));
+                }
             }
-            __syncthreads();
-        }
-        // dP_K[tau,s] = alpha(tau) + v_tau . U_s(tau)
-        for (int q = w; q < 2 * SP / 16; q += NW) {
-            const int mt = q & 1, ns = q >> 1;
-            f32x4 c = zero4();
-            tile_mma_bT(c, sV + 16 * mt * LDN, LDN, sUt + 16 * ns, LDP, D / 32);
-            if constexpr (CAUSAL) tile_mma(c, sHmT + 16 * mt * LDT, LDT, sWt + 16 * ns * LDT, LDT, 1);
-            for (int e = 0; e < 4; ++e) {
-                const int t = 16 * mt + 4 * g + e, s = 16 * ns + i;
-                const float al = CAUSAL ? sDA[t * LDA + s] : sAl[s];
-                sDA[t * LDA + s] = c[e] + al;
+            // U += this tile: U[s][d] += sum_t W[t][s] g[t][d] (both layouts)
+            for (int ms = 0; ms < 2; ++ms) {
+                const Frag<T> wa = ld_frag(sWt + (16 * ms + i) * LDT + 8 * g);
+                for (int md = 0; md < 4; ++md) {
+                    const Frag<T> gb = ld_frag(sGt + (16 * md + i) * LDT + 8 * g);
+                    mma(Us[ms][md], wa, gb);
+                    mma(Ut[md][ms], gb, wa);
+                }
+            }
+        } else {
+            // non-causal: dP_K = alpha + v . U (totals); dV^T = U^T P_K^T
+            for (int ms = 0; ms < 2; ++ms)
+                for (int nt = 0; nt < 2; ++nt) {
+                    f32x4 c = zero4();
+                    for (int kk = 0; kk < 2; ++kk)
+                        mma(c, frag_acc<T>(Ut[2 * kk][ms], Ut[2 * kk + 1][ms]),
+                            ld_frag_pi(sV + (16 * nt + i) * LDN + 32 * kk));
+                    for (int e = 0; e < 4; ++e) dPK[ms][nt][e] = c[e] + al[ms][e];
+                }
+            for (int md = 0; md < 4; ++md) {
+                const Frag<T> uf = frag_acc<T>(Us[0][md], Us[1][md]);
+                for (int nt = 0; nt < 2; ++nt) {
+                    VT[md][nt] = zero4();
+                    mma(VT[md][nt], uf, PKf[nt]);
+                }
             }
         }
-        // dV[tau] = sum_s P_K[tau,s] U_s(tau)
-        f32x4 vacc[2];
-        for (int j = 0; j < 2; ++j) {
-            const int q = w + NW * j, mt = q >> 2, nd = q & 3;
-            vacc[j] = zero4();
-            tile_mma(vacc[j], sPk + 16 * mt * LDP, LDP, sUt + 16 * nd * LDP, LDP, SP / 32);
-            if constexpr (CAUSAL) tile_mma(vacc[j], sSc2 + 16 * mt * LDT, LDT, sGt + 16 * nd * LDT, LDT, 1);
-        }
-        if constexpr (CAUSAL)
-            for (int j = 0; j < NTL; ++j)
-                tile_mma(accU[j], sWt + 16 * Carry<SP>::ms(j) * LDT, LDT, sGt + 16 * Carry<SP>::nd(j) * LDT, LDT, 1);
+        tsum += softhash_bwd_st<T>(a.K, PK, dPK, sThK, sw, a.L, a.inv_temp, sDproj);
+        reduce_store<T, NW_>(VT, sRed, dvp, a.sg.t, t0, a.T);
         __syncthreads();
-        for (int j = 0; j < 2; ++j) {
-            const int q = w + NW * j;
-            st_tile(sStage + 16 * (q >> 2) * LDN + 16 * (q & 3), LDN, vacc[j]);
-        }
-        if constexpr (CAUSAL)
-            for (int j = 0; j < NTL; ++j)
-                st_tile_T(sUt + 16 * Carry<SP>::nd(j) * LDP + 16 * Carry<SP>::ms(j), LDP, accU[j]);
-        for (int idx = threadIdx.x; idx < TT * LDDP; idx += NT) sDproj[idx] = from_f32<T>(0.f);
-        __syncthreads();
-        store_tile<T>(dvp, a.sg.t, t0, a.T, sStage);
-        tsum += softhash_bwd_tile<T, SP>(sSpK, sSmK, sThK, sDA, a.L, a.K, t0, a.T, a.inv_temp, sDproj);
-        __syncthreads();
-        for (int j = 0; j < 2; ++j) {
-            const int q = w + NW * j;
-            dx_tile<T>(sDproj, sPlT, q >> 2, q & 3, sStage);
-        }
-        __syncthreads();
-        store_tile<T>(dkp, a.sg.t, t0, a.T, sStage);
+        dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0, a.T);
     }
-    const float ts = block_sum(tsum, sRed);
+    const float ts = block_sum<NTH>(tsum, sRed);
     if (threadIdx.x == 0) a.tpart[(int64_t)(a.M * a.B * a.H + n) * a.nseg + seg] = ts;
 }
 

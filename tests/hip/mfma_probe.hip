@@ -38,3 +38,50 @@ extern "C" int probe_mfma(int bf16, const void *A, const void *B, float *C, floa
         k_probe<float><<<1, 64>>>((const float *)A, (const float *)B, C, Cbt, Ct);
     return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
 }
+
+// Row (16-lane) DPP scans: out[0..63] prefix, [64..127] suffix, [128..191] row sum.
+__global__ __launch_bounds__(64) void k_probe_rows(const float *x, float *out) {
+    const float v = x[threadIdx.x];
+    out[threadIdx.x] = row_prefix(v);
+    out[64 + threadIdx.x] = row_suffix(v);
+    out[128 + threadIdx.x] = row_sum(v);
+}
+
+// MFMA chain with pi-ordered k: X = A . Bm^T (32 x 16, two tiles) kept in
+// registers, then D = E . X (B operand from the accumulators) and
+// Dt = X^T . E^T (A operand from the accumulators), E read with ld_frag_pi.
+template <typename T>
+__global__ __launch_bounds__(64) void k_probe_chain(const T *A, const T *Bm, const T *E, float *Dout, float *Dtout) {
+    constexpr int LD = ld_of<T>(64), LDE = ld_of<T>(32);
+    __shared__ __align__(16) T sA[32 * LD], sB[16 * LD], sE[16 * LDE];
+    for (int idx = threadIdx.x; idx < 32 * 64; idx += 64) sA[(idx / 64) * LD + idx % 64] = A[idx];
+    for (int idx = threadIdx.x; idx < 16 * 64; idx += 64) sB[(idx / 64) * LD + idx % 64] = Bm[idx];
+    for (int idx = threadIdx.x; idx < 16 * 32; idx += 64) sE[(idx / 32) * LDE + idx % 32] = E[idx];
+    __syncthreads();
+    f32x4 x0 = zero4(), x1 = zero4();
+    tile_mma(x0, sA, LD, sB, LD, 2);
+    tile_mma(x1, sA + 16 * LD, LD, sB, LD, 2);
+    const Frag<T> xf = frag_acc<T>(x0, x1);
+    const int i = lane_id() & 15, g = lane_id() >> 4;
+    const Frag<T> ef = ld_frag_pi(sE + i * LDE);
+    f32x4 d = zero4(), dt = zero4();
+    mma(d, ef, xf);
+    mma(dt, xf, ef);
+    for (int e = 0; e < 4; ++e) {
+        Dout[(4 * g + e) * 16 + i] = d[e];
+        Dtout[(4 * g + e) * 16 + i] = dt[e];
+    }
+}
+
+extern "C" int probe_rows(const float *x, float *out) {
+    k_probe_rows<<<1, 64>>>(x, out);
+    return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int probe_chain(int bf16, const void *A, const void *Bm, const void *E, float *D, float *Dt) {
+    if (bf16)
+        k_probe_chain<race::bf16><<<1, 64>>>((const race::bf16 *)A, (const race::bf16 *)Bm, (const race::bf16 *)E, D, Dt);
+    else
+        k_probe_chain<float><<<1, 64>>>((const float *)A, (const float *)Bm, (const float *)E, D, Dt);
+    return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}

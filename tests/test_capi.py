@@ -61,7 +61,7 @@ def test_plan_sizes_c4():
 
 @pytest.mark.parametrize("field,value,code,msg", [
     ("D", 32, -2, "head dim"),
-    ("K", 9, -2, "hash bits"),
+    ("K", 5, -2, "hash bits"),
     ("L", 9, -2, "projection columns"),
     ("L", 0, -1, "L and K"),
     ("T", 0, -1, "must be >= 1"),

@@ -27,7 +27,45 @@ def dev():
 def _probe_lib():
     lib = ctypes.CDLL(os.path.join(HERE, "hip", "libmfma_probe.so"))
     lib.probe_mfma.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5
+    lib.probe_rows.argtypes = [ctypes.c_void_p] * 2
+    lib.probe_chain.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5
     return lib
+
+
+def test_dpp_row_scans(dev):
+    """16-lane row prefix/suffix/total helpers (in-bounds, one wave)."""
+    lib = _probe_lib()
+    x = torch.randn(64, generator=torch.Generator().manual_seed(2)).to(dev)
+    out = torch.zeros(192, device=dev)
+    assert lib.probe_rows(x.data_ptr(), out.data_ptr()) == 0
+    rows = x.cpu().double().view(4, 16)
+    pre = torch.cumsum(rows, 1).reshape(-1)
+    suf = torch.flip(torch.cumsum(torch.flip(rows, [1]), 1), [1]).reshape(-1)
+    tot = rows.sum(1, keepdim=True).expand(4, 16).reshape(-1)
+    o = out.cpu().double()
+    assert torch.allclose(o[:64], pre, atol=1e-5)
+    assert torch.allclose(o[64:128], suf, atol=1e-5)
+    assert torch.allclose(o[128:], tot, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_mfma_chain_pi_order(dev, dtype):
+    """Accumulator tiles reused as the next MFMA's operand (pi-ordered k)."""
+    lib = _probe_lib()
+    g = torch.Generator().manual_seed(3)
+    A = torch.randn(32, 64, generator=g).to(dtype)
+    Bm = torch.randn(16, 64, generator=g).to(dtype)
+    E = torch.randn(16, 32, generator=g).to(dtype)
+    D, Dt = torch.zeros(16, 16, device=dev), torch.zeros(16, 16, device=dev)
+    assert lib.probe_chain(int(dtype == torch.bfloat16), A.to(dev).data_ptr(), Bm.to(dev).data_ptr(),
+                           E.to(dev).data_ptr(), D.data_ptr(), Dt.data_ptr()) == 0
+    X = A.double() @ Bm.double().T
+    if dtype == torch.bfloat16:
+        X = X.to(torch.bfloat16).double()      # the chained operand is rounded to bf16
+    ref = E.double() @ X
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert relerr(D.cpu(), ref) < tol
+    assert relerr(Dt.cpu(), ref.T) < tol
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
