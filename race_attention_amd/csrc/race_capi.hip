@@ -9,6 +9,7 @@
 #include <stdio.h>
 
 #include <string>
+#include <type_traits>
 
 #include "../../include/race_attention.h"
 #include "prefix_mean.hip"
@@ -147,29 +148,29 @@ int launched(const char *what) {
 
 bool run_phase(const race_desc *d, int ph) { return d->phases == 0 || (d->phases & ph); }
 
-template <typename T, int SP> int fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
+template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
     const dim3 grid(p.nseg, (unsigned)p.N);
-    if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP><<<grid, 2 * SP, 0, s>>>(a);
+    if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP, KB><<<grid, 2 * SP, 0, s>>>(a);
     const int elems = SP * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
         k_fwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
     if (run_phase(d, RACE_PHASE_OUT)) {
         if (d->causal)
-            k_fwd_out<T, SP, true><<<grid, 2 * SP, 0, s>>>(a);
+            k_fwd_out<T, SP, true, KB><<<grid, 2 * SP, 0, s>>>(a);
         else
-            k_fwd_out<T, SP, false><<<grid, 2 * SP, 0, s>>>(a);
+            k_fwd_out<T, SP, false, KB><<<grid, 2 * SP, 0, s>>>(a);
     }
     return launched("race_fwd");
 }
 
-template <typename T, int SP>
+template <typename T, int SP, int KB>
 int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hipStream_t s) {
     const dim3 grid(p.nseg, (unsigned)p.N);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
         if (d->causal)
-            k_bwd_reduce<T, SP, true><<<grid, 2 * SP, 0, s>>>(a);
+            k_bwd_reduce<T, SP, true, KB><<<grid, 2 * SP, 0, s>>>(a);
         else
-            k_bwd_reduce<T, SP, false><<<grid, 2 * SP, 0, s>>>(a);
+            k_bwd_reduce<T, SP, false, KB><<<grid, 2 * SP, 0, s>>>(a);
     }
     const int elems = SP * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
@@ -177,31 +178,35 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
                                                                             d->causal);
     if (run_phase(d, RACE_PHASE_OUT)) {
         if (d->causal)
-            k_bwd_out<T, SP, true><<<grid, 2 * SP, 0, s>>>(a);
+            k_bwd_out<T, SP, true, KB><<<grid, 2 * SP, 0, s>>>(a);
         else
-            k_bwd_out<T, SP, false><<<grid, 2 * SP, 0, s>>>(a);
+            k_bwd_out<T, SP, false, KB><<<grid, 2 * SP, 0, s>>>(a);
         if (grad_inv_temp) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, 2 * p.N * p.nseg, grad_inv_temp);
     }
     return launched("race_bwd");
 }
 
+// Compiled (dtype, padded buckets, hash bits) combinations: every K in 1..4
+// with the padded bucket counts its L*2^K <= 128 and L*K <= 32 allow.
+#define RACE_FOR_COMBOS(X)                                                                                          \
+    X(bf16, 32, 1) X(bf16, 64, 1) X(bf16, 32, 2) X(bf16, 64, 2) X(bf16, 32, 3) X(bf16, 64, 3) X(bf16, 128, 3)       \
+    X(bf16, 32, 4) X(bf16, 64, 4) X(bf16, 128, 4) X(float, 32, 1) X(float, 32, 2) X(float, 32, 3) X(float, 32, 4)
+
 template <typename T> int fwd_dispatch(const race_desc *d, const Plan &p, const Args &a, hipStream_t s) {
-    switch (p.SP) {
-    case 32: return fwd_impl<T, 32>(d, p, a, s);
-    case 64: if constexpr (sizeof(T) == 2) return fwd_impl<T, 64>(d, p, a, s); break;
-    case 128: if constexpr (sizeof(T) == 2) return fwd_impl<T, 128>(d, p, a, s); break;
-    }
-    return fail(RACE_E_UNSUPPORTED, "bucket count not compiled");
+#define X(TT_, SP_, KB_)                                                                                             \
+    if (std::is_same<T, TT_>::value && p.SP == SP_ && d->K == KB_) return fwd_impl<TT_, SP_, KB_>(d, p, a, s);
+    RACE_FOR_COMBOS(X)
+#undef X
+    return fail(RACE_E_UNSUPPORTED, "bucket count / hash bits combination not compiled");
 }
 
 template <typename T>
 int bwd_dispatch(const race_desc *d, const Plan &p, const Args &a, float *git, hipStream_t s) {
-    switch (p.SP) {
-    case 32: return bwd_impl<T, 32>(d, p, a, git, s);
-    case 64: if constexpr (sizeof(T) == 2) return bwd_impl<T, 64>(d, p, a, git, s); break;
-    case 128: if constexpr (sizeof(T) == 2) return bwd_impl<T, 128>(d, p, a, git, s); break;
-    }
-    return fail(RACE_E_UNSUPPORTED, "bucket count not compiled");
+#define X(TT_, SP_, KB_)                                                                                             \
+    if (std::is_same<T, TT_>::value && p.SP == SP_ && d->K == KB_) return bwd_impl<TT_, SP_, KB_>(d, p, a, git, s);
+    RACE_FOR_COMBOS(X)
+#undef X
+    return fail(RACE_E_UNSUPPORTED, "bucket count / hash bits combination not compiled");
 }
 
 // prefix mean: segment length so that NS * nseg ~ 4096 waves

@@ -107,6 +107,37 @@ __device__ void load_tile(const T *__restrict__ src, int64_t st, int64_t t0, int
     }
 }
 
+// Register-staged tile load: issue() starts the global loads of one tile
+// into registers, commit() writes them to LDS (natural and/or transposed), so
+// the next tile's loads overlap the current tile's compute.
+template <typename T, int NTH> struct Prefetch {
+    static constexpr int EPC = 16 / sizeof(T), CPR = D / EPC, CHUNKS = TT * CPR;
+    static constexpr int PER = (CHUNKS + NTH - 1) / NTH;
+    uint4 v[PER];
+    __device__ __forceinline__ void issue(const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int idx = threadIdx.x + j * NTH, t = idx / CPR, c = idx % CPR;
+            v[j] = make_uint4(0, 0, 0, 0);
+            if (idx < CHUNKS && t0 + t < Tn) v[j] = *reinterpret_cast<const uint4 *>(src + (t0 + t) * st + c * EPC);
+        }
+    }
+    __device__ __forceinline__ void commit(T *nat, T *trn) const {
+        constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int idx = threadIdx.x + j * NTH, t = idx / CPR, c = idx % CPR;
+            if (idx >= CHUNKS) continue;
+            if (nat) *reinterpret_cast<uint4 *>(nat + t * LDN + c * EPC) = v[j];
+            if (trn) {
+                const T *e = reinterpret_cast<const T *>(&v[j]);
+#pragma unroll
+                for (int q = 0; q < EPC; ++q) trn[(c * EPC + q) * LDT + t] = e[q];
+            }
+        }
+    }
+};
+
 // Planes [L*K][D] fp32 -> LDS.  pl/pllo: [NCOL][ld_of<T>(D)] (bf16 keeps a
 // hi/lo split so the projection is close to fp32), plt: [D][ld_of<T>(NCOL)].
 template <typename T, int NTH>
@@ -149,9 +180,10 @@ __device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mc, in
 
 // Bucket probabilities of the wave's 32 buckets in bucket-row layout:
 // P[ms][nt][e] = P[t = 16nt + i][s = sw + 16ms + 4g + e]; zero for s >= S or
-// t0 + t >= T.
+// t0 + t >= T.  For K >= 2 the 4 buckets of a lane share one table and differ
+// in the two lowest corner bits: P = hi * (bit1 ? s+ : s-) * (bit0 ? s+ : s-).
 template <int KB>
-__device__ __forceinline__ void probs_kb(const float *sp, const float *sm, int sw, int S, int64_t t0, int64_t Tn,
+__device__ __forceinline__ void probs_st(const float *sp, const float *sm, int sw, int S, int64_t t0, int64_t Tn,
                                          f32x4 (&P)[2][2]) {
     constexpr int LDC = ld_of<float>(NCOL);
     constexpr int R = 1 << KB;
@@ -163,27 +195,35 @@ __device__ __forceinline__ void probs_kb(const float *sp, const float *sm, int s
 #pragma unroll
         for (int ms = 0; ms < 2; ++ms) {
             const int s0 = sw + 16 * ms + 4 * g;
+            if constexpr (KB == 1) {
+                // tables s0/2 and s0/2 + 1; corner r = 1 is sigmoid(+2u)
+                const bool v01 = tv && s0 < S, v23 = tv && s0 + 2 < S;
+                const int l0 = v01 ? s0 >> 1 : 0, l1 = v23 ? (s0 >> 1) + 1 : 0;
+                P[ms][nt][0] = v01 ? sm[t * LDC + l0] : 0.f;
+                P[ms][nt][1] = v01 ? sp[t * LDC + l0] : 0.f;
+                P[ms][nt][2] = v23 ? sm[t * LDC + l1] : 0.f;
+                P[ms][nt][3] = v23 ? sp[t * LDC + l1] : 0.f;
+            } else {
+                const bool v = tv && s0 < S;
+                const int l = s0 < S ? s0 >> KB : 0;
+                const int r0 = s0 & (R - 1);
+                const float *pp = sp + t * LDC + l * KB, *pm = sm + t * LDC + l * KB;
+                float fp[KB], fm[KB];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int s = s0 + e, l = s < S ? s >> KB : 0, r = s & (R - 1);
-                const float *p = sp + t * LDC + l * KB;
-                const float *q = sm + t * LDC + l * KB;
-                float v = 1.f;
+                for (int k = 0; k < KB; ++k) {
+                    fp[k] = pp[k];
+                    fm[k] = pm[k];
+                }
+                float hi = v ? 1.f : 0.f;
 #pragma unroll
-                for (int k = 0; k < KB; ++k) v *= ((r >> (KB - 1 - k)) & 1) ? p[k] : q[k];
-                P[ms][nt][e] = (s < S && tv) ? v : 0.f;
+                for (int k = 0; k < KB - 2; ++k) hi *= ((r0 >> (KB - 1 - k)) & 1) ? fp[k] : fm[k];
+                const float h0 = hi * fm[KB - 2], h1 = hi * fp[KB - 2];
+                P[ms][nt][0] = h0 * fm[KB - 1];
+                P[ms][nt][1] = h0 * fp[KB - 1];
+                P[ms][nt][2] = h1 * fm[KB - 1];
+                P[ms][nt][3] = h1 * fp[KB - 1];
             }
         }
-    }
-}
-
-__device__ __forceinline__ void probs_st(int K, const float *sp, const float *sm, int sw, int S, int64_t t0,
-                                         int64_t Tn, f32x4 (&P)[2][2]) {
-    switch (K) {
-    case 1: probs_kb<1>(sp, sm, sw, S, t0, Tn, P); break;
-    case 2: probs_kb<2>(sp, sm, sw, S, t0, Tn, P); break;
-    case 3: probs_kb<3>(sp, sm, sw, S, t0, Tn, P); break;
-    default: probs_kb<4>(sp, sm, sw, S, t0, Tn, P); break;
     }
 }
 
@@ -198,8 +238,10 @@ template <int KB> __device__ __forceinline__ float table_reduce(float x) {
 // Softmax / corner / tanh backward in bucket-row layout for the wave's
 // buckets: dP (and P, fp32) -> dproj [TT][ld_of<T>(NCOL)] columns l*K + k of
 // the wave's tables; returns this lane's share of sum du * th.
+// du_k = sum_r dl_r c_rk over the table; the two lowest corner bits vary with
+// e inside the lane, the higher ones are fixed per lane (from its rows g).
 template <int KB, typename T>
-__device__ float softhash_bwd_kb(const f32x4 (&P)[2][2], const f32x4 (&dP)[2][2], const float *sth, int sw, int L,
+__device__ float softhash_bwd_st(const f32x4 (&P)[2][2], const f32x4 (&dP)[2][2], const float *sth, int sw, int L,
                                  float inv_temp, T *dproj) {
     constexpr int LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
     constexpr int R = 1 << KB;
@@ -213,14 +255,16 @@ __device__ float softhash_bwd_kb(const f32x4 (&P)[2][2], const f32x4 (&dP)[2][2]
         for (int ms = 0; ms < 2; ++ms) {
             const int s0 = sw + 16 * ms + 4 * g;
             f32x4 pd, dl;
+#pragma unroll
             for (int e = 0; e < 4; ++e) pd[e] = P[ms][nt][e] * dP[ms][nt][e];
             if constexpr (KB == 1) {
                 const float d01 = pd[0] + pd[1], d23 = pd[2] + pd[3];
+#pragma unroll
                 for (int e = 0; e < 4; ++e) dl[e] = P[ms][nt][e] * (dP[ms][nt][e] - (e < 2 ? d01 : d23));
-                // tables (s0 >> 1) and (s0 >> 1) + 1, one hash bit each
+#pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int l = (s0 >> 1) + h;
-                    const float du = dl[2 * h + 1] - dl[2 * h];  // r = 1 is corner +1
+                    const float du = dl[2 * h + 1] - dl[2 * h];  // corner r = 1 is +1
                     if (l < L) {
                         const float th = sth[t * LDC + l];
                         tsum += du * th;
@@ -229,38 +273,31 @@ __device__ float softhash_bwd_kb(const f32x4 (&P)[2][2], const f32x4 (&dP)[2][2]
                 }
             } else {
                 const float dot = table_reduce<KB>(pd[0] + pd[1] + pd[2] + pd[3]);
+#pragma unroll
                 for (int e = 0; e < 4; ++e) dl[e] = P[ms][nt][e] * (dP[ms][nt][e] - dot);
-                const int l = s0 >> KB;
+                const float sum = dl[0] + dl[1] + dl[2] + dl[3];
+                const int l = s0 >> KB, r0 = s0 & (R - 1);
+                float du[KB];
 #pragma unroll
-                for (int k = 0; k < KB; ++k) {
-                    float part = 0.f;
+                for (int k = 0; k < KB - 2; ++k) du[k] = ((r0 >> (KB - 1 - k)) & 1) ? sum : -sum;
+                du[KB - 2] = (dl[2] + dl[3]) - (dl[0] + dl[1]);
+                du[KB - 1] = (dl[1] + dl[3]) - (dl[0] + dl[2]);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int r = (s0 + e) & (R - 1);
-                        part += ((r >> (KB - 1 - k)) & 1) ? dl[e] : -dl[e];
-                    }
-                    const float du = table_reduce<KB>(part);
-                    if (l < L && (k % RPT) == (g % RPT)) {
-                        const float th = sth[t * LDC + l * KB + k];
-                        tsum += du * th;
-                        dproj[t * LDDP + l * KB + k] = from_f32<T>(du * inv_temp * (1.f - th * th));
+                for (int k = 0; k < KB; ++k) du[k] = table_reduce<KB>(du[k]);
+                if (l < L) {
+#pragma unroll
+                    for (int k = 0; k < KB; ++k) {
+                        if ((k % RPT) == (g % RPT)) {
+                            const float th = sth[t * LDC + l * KB + k];
+                            tsum += du[k] * th;
+                            dproj[t * LDDP + l * KB + k] = from_f32<T>(du[k] * inv_temp * (1.f - th * th));
+                        }
                     }
                 }
             }
         }
     }
     return tsum;
-}
-
-template <typename T>
-__device__ __forceinline__ float softhash_bwd_st(int K, const f32x4 (&P)[2][2], const f32x4 (&dP)[2][2],
-                                                 const float *sth, int sw, int L, float inv_temp, T *dproj) {
-    switch (K) {
-    case 1: return softhash_bwd_kb<1, T>(P, dP, sth, sw, L, inv_temp, dproj);
-    case 2: return softhash_bwd_kb<2, T>(P, dP, sth, sw, L, inv_temp, dproj);
-    case 3: return softhash_bwd_kb<3, T>(P, dP, sth, sw, L, inv_temp, dproj);
-    default: return softhash_bwd_kb<4, T>(P, dP, sth, sw, L, inv_temp, dproj);
-    }
 }
 
 // Per-bucket token sums of a tile: tot[ms][e] = sum over the tile's 32 tokens
@@ -338,11 +375,15 @@ __device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64
     }
 }
 
-// Output tiles out[md][nt] (lane holds X^T[d = 16md + 4g + e][t = 16nt + i],
+// Output tiles part[md][nt] (lane holds X^T[d = 16md + 4g + e][t = 16nt + i],
 // this wave's partial over its buckets): sum over the waves and store rows t.
+// With several waves the partials go through red ([NW][TT][ld_of<float>(32)]
+// fp32, RED_BYTES), one half of d at a time; red must be free on entry.
+template <int NW_> constexpr size_t red_bytes() { return NW_ > 1 ? sizeof(float) * NW_ * TT * ld_of<float>(32) : 0; }
+
 template <typename T, int NW_>
 __device__ void reduce_store(const f32x4 (&part)[4][2], float *red, T *dst, int64_t st, int64_t t0, int64_t Tn) {
-    constexpr int LDR = ld_of<float>(D);
+    constexpr int LDR = ld_of<float>(32);
     const int g = lg(), i = li(), w = wave_id();
     if constexpr (NW_ == 1) {
         for (int md = 0; md < 4; ++md)
@@ -352,15 +393,19 @@ __device__ void reduce_store(const f32x4 (&part)[4][2], float *red, T *dst, int6
             }
     } else {
         float *mine = red + w * TT * LDR;
-        for (int md = 0; md < 4; ++md)
-            for (int nt = 0; nt < 2; ++nt)
-                *reinterpret_cast<f32x4 *>(mine + (16 * nt + i) * LDR + 16 * md + 4 * g) = part[md][nt];
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < TT * D / 4; idx += 64 * NW_) {
-            const int t = idx / (D / 4), d0 = 4 * (idx % (D / 4));
-            f32x4 s = *reinterpret_cast<const f32x4 *>(red + t * LDR + d0);
-            for (int ww = 1; ww < NW_; ++ww) s += *reinterpret_cast<const f32x4 *>(red + ww * TT * LDR + t * LDR + d0);
-            if (t0 + t < Tn) store4<T>(dst + (t0 + t) * st + d0, s);
+        for (int h = 0; h < 2; ++h) {
+            for (int mh = 0; mh < 2; ++mh)
+                for (int nt = 0; nt < 2; ++nt)
+                    *reinterpret_cast<f32x4 *>(mine + (16 * nt + i) * LDR + 16 * mh + 4 * g) = part[2 * h + mh][nt];
+            __syncthreads();
+            for (int idx = threadIdx.x; idx < TT * 8; idx += 64 * NW_) {
+                const int t = idx >> 3, d0 = 4 * (idx & 7);
+                f32x4 sum = *reinterpret_cast<const f32x4 *>(red + t * LDR + d0);
+                for (int ww = 1; ww < NW_; ++ww)
+                    sum += *reinterpret_cast<const f32x4 *>(red + ww * TT * LDR + t * LDR + d0);
+                if (t0 + t < Tn) store4<T>(dst + (t0 + t) * st + 32 * h + d0, sum);
+            }
+            __syncthreads();
         }
     }
 }
@@ -398,7 +443,7 @@ template <typename T, int SP> struct FwdReduceL {
     static constexpr size_t bytes = align16(oSig + sizeof(float) * 2 * TT * LDC);
 };
 
-template <typename T, int SP>
+template <typename T, int SP, int KB>
 __global__ __launch_bounds__(SP * 2) void k_fwd_reduce(Args a) {
     using Ly = FwdReduceL<T, SP>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC;
@@ -424,16 +469,25 @@ __global__ __launch_bounds__(SP * 2) void k_fwd_reduce(Args a) {
     for (int ms = 0; ms < 2; ++ms)
         for (int e = 0; e < 4; ++e) accA[ms][e] = 0.0;
 
+    Prefetch<T, NTH> pk_, pv_;
+    if (j0 < j1) {
+        pk_.issue(kp, a.sk.t, j0 * TT, a.T);
+        pv_.issue(vp, a.sv.t, j0 * TT, a.T);
+    }
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
         __syncthreads();
-        load_tile<T, NTH>(kp, a.sk.t, t0, a.T, sK, nullptr);
-        load_tile<T, NTH>(vp, a.sv.t, t0, a.T, nullptr, sVt);
+        pk_.commit(sK, nullptr);
+        pv_.commit(nullptr, sVt);
+        if (jt + 1 < j1) {
+            pk_.issue(kp, a.sk.t, t0 + TT, a.T);
+            pv_.issue(vp, a.sv.t, t0 + TT, a.T);
+        }
         __syncthreads();
         for (int q = w; q < 4; q += NW_) project_tile<T>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, nullptr);
         __syncthreads();
         f32x4 PK[2][2];
-        probs_st(a.K, sSp, sSm, sw, a.S, t0, a.T, PK);
+        probs_st<KB>(sSp, sSm, sw, a.S, t0, a.T, PK);
         for (int ms = 0; ms < 2; ++ms)
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PK[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
@@ -476,26 +530,27 @@ __global__ void k_fwd_scan(double *fstate, const double *fdelta, int nseg, int e
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct FwdOutL {
     static constexpr int NW_ = SP / 32;
-    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDR = ld_of<float>(D);
+    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL);
+    // region R0 = {Q, K, sigma tables}; the output reduction reuses it once they are dead
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
-    static constexpr size_t oVt = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
+    static constexpr size_t oSig = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));  // Q sp, Q sm, K sp, K sm
+    static constexpr size_t r0 = align16(cmax(oSig + sizeof(float) * 4 * TT * LDC, red_bytes<NW_>()));
+    static constexpr size_t oVt = r0;
     static constexpr size_t oPkt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
     static constexpr size_t oPl = align16(oPkt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oSig = align16(oPlLo + sizeof(T) * NCOL * LDN);  // Q sp, Q sm, K sp, K sm
-    static constexpr size_t oRed = align16(oSig + sizeof(float) * 4 * TT * LDC);
-    static constexpr size_t bytes = align16(oRed + (NW_ > 1 ? sizeof(float) * NW_ * TT * LDR : 0));
+    static constexpr size_t bytes = align16(oPlLo + sizeof(T) * NCOL * LDN);
 };
 
-template <typename T, int SP, bool CAUSAL>
+template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(SP * 2) void k_fwd_out(Args a) {
     using Ly = FwdOutL<T, SP, CAUSAL>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
-    float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
+    float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oQ);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sSpK = sSig + 2 * TT * LDC, *sSmK = sSig + 3 * TT * LDC;
     const int w = wave_id(), g = lg(), i = li(), sw = 32 * w;
     T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT;
@@ -521,13 +576,28 @@ __global__ __launch_bounds__(SP * 2) void k_fwd_out(Args a) {
         for (int e = 0; e < 4; ++e) a0[ms][e] = st[sidx(sw + 16 * ms + 4 * g + e, D)];
     }
 
+    Prefetch<T, NTH> pq_, pk_, pv_;
+    if (j0 < j1) {
+        pq_.issue(qp, a.sq.t, j0 * TT, a.T);
+        if constexpr (CAUSAL) {
+            pk_.issue(kp, a.sk.t, j0 * TT, a.T);
+            pv_.issue(vp, a.sv.t, j0 * TT, a.T);
+        }
+    }
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
         __syncthreads();
-        load_tile<T, NTH>(qp, a.sq.t, t0, a.T, sQ, nullptr);
+        pq_.commit(sQ, nullptr);
         if constexpr (CAUSAL) {
-            load_tile<T, NTH>(kp, a.sk.t, t0, a.T, sK, nullptr);
-            load_tile<T, NTH>(vp, a.sv.t, t0, a.T, nullptr, sVt);
+            pk_.commit(sK, nullptr);
+            pv_.commit(nullptr, sVt);
+        }
+        if (jt + 1 < j1) {
+            pq_.issue(qp, a.sq.t, t0 + TT, a.T);
+            if constexpr (CAUSAL) {
+                pk_.issue(kp, a.sk.t, t0 + TT, a.T);
+                pv_.issue(vp, a.sv.t, t0 + TT, a.T);
+            }
         }
         __syncthreads();
         for (int q = w; q < (CAUSAL ? 8 : 4); q += NW_) {
@@ -538,9 +608,9 @@ __global__ __launch_bounds__(SP * 2) void k_fwd_out(Args a) {
         }
         __syncthreads();
         f32x4 PQ[2][2], PK[2][2], Acum[2][2];
-        probs_st(a.K, sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
+        probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
         if constexpr (CAUSAL) {
-            probs_st(a.K, sSpK, sSmK, sw, a.S, t0, a.T, PK);
+            probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
             for (int ms = 0; ms < 2; ++ms)
                 for (int nt = 0; nt < 2; ++nt)
                     for (int e = 0; e < 4; ++e) PK[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
@@ -595,6 +665,7 @@ __global__ __launch_bounds__(SP * 2) void k_fwd_out(Args a) {
                 for (int md = 0; md < 4; ++md) mma(Bc[ms][md], pa, ld_frag(sVt + (16 * md + i) * LDT + 8 * g));
             }
         }
+        if constexpr (!CAUSAL) __syncthreads();  // sigma tables and Q tile dead before R0 is reused
         reduce_store<T, NW_>(O, sRed, op, a.so.t, t0, a.T);
     }
 }
@@ -623,7 +694,7 @@ template <typename T, int SP, bool CAUSAL> struct BwdReduceL {
     static constexpr size_t bytes = align16(oRed + sizeof(float) * 64 * NW_);
 };
 
-template <typename T, int SP, bool CAUSAL>
+template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(SP * 2) void k_bwd_reduce(Args a) {
     using Ly = BwdReduceL<T, SP, CAUSAL>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
@@ -666,14 +737,31 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_reduce(Args a) {
         }
     float tsum = 0.f;
 
+    Prefetch<T, NTH> pq_, pg_, pk_, pv_;
+    if (j0 < j1) {
+        pq_.issue(qp, a.sq.t, j0 * TT, a.T);
+        pg_.issue(gp, a.sdo.t, j0 * TT, a.T);
+        if constexpr (CAUSAL) {
+            pk_.issue(kp, a.sk.t, j0 * TT, a.T);
+            pv_.issue(vp, a.sv.t, j0 * TT, a.T);
+        }
+    }
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
         __syncthreads();
-        load_tile<T, NTH>(qp, a.sq.t, t0, a.T, sQ, nullptr);
-        load_tile<T, NTH>(gp, a.sdo.t, t0, a.T, sG, sGt);
+        pq_.commit(sQ, nullptr);
+        pg_.commit(sG, sGt);
         if constexpr (CAUSAL) {
-            load_tile<T, NTH>(kp, a.sk.t, t0, a.T, sK, nullptr);
-            load_tile<T, NTH>(vp, a.sv.t, t0, a.T, sV, sVt);
+            pk_.commit(sK, nullptr);
+            pv_.commit(sV, sVt);
+        }
+        if (jt + 1 < j1) {
+            pq_.issue(qp, a.sq.t, t0 + TT, a.T);
+            pg_.issue(gp, a.sdo.t, t0 + TT, a.T);
+            if constexpr (CAUSAL) {
+                pk_.issue(kp, a.sk.t, t0 + TT, a.T);
+                pv_.issue(vp, a.sv.t, t0 + TT, a.T);
+            }
         }
         __syncthreads();
         for (int q = w; q < (CAUSAL ? 8 : 4); q += NW_) {
@@ -684,9 +772,9 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_reduce(Args a) {
         }
         __syncthreads();
         f32x4 PQ[2][2], PK[2][2], Acum[2][2], W[2][2], inv[2][2];
-        probs_st(a.K, sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
+        probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
         if constexpr (CAUSAL) {
-            probs_st(a.K, sSpK, sSmK, sw, a.S, t0, a.T, PK);
+            probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
             for (int ms = 0; ms < 2; ++ms)
                 for (int nt = 0; nt < 2; ++nt)
                     for (int e = 0; e < 4; ++e) PK[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
@@ -753,7 +841,7 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_reduce(Args a) {
             for (int ms = 0; ms < 2; ++ms)
                 for (int e = 0; e < 4; ++e) a0[ms][e] += (double)tot[ms][e];
         }
-        tsum += softhash_bwd_st<T>(a.K, PQ, dPQ, sThQ, sw, a.L, a.inv_temp, sDproj);
+        tsum += softhash_bwd_st<KB, T>(PQ, dPQ, sThQ, sw, a.L, a.inv_temp, sDproj);
         __syncthreads();
         dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0, a.T);
     }
@@ -790,38 +878,44 @@ __global__ void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int ele
 template <typename T, int SP, bool CAUSAL> struct BwdOutL {
     static constexpr int NW_ = SP / 32;
     static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL),
-                         LDR = ld_of<float>(D);
+                         LDU = ld_of<T>(32);
+    // region R0 = {Q, K, sigma tables}; the dV reduction reuses it once they are dead
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + (CAUSAL ? sizeof(T) * TT * LDN : 0));
-    static constexpr size_t oV = align16(oK + sizeof(T) * TT * LDN);
+    static constexpr size_t oSig = align16(oK + sizeof(T) * TT * LDN);  // K sp, K sm, Q sp, Q sm
+    static constexpr size_t r0 = align16(cmax(oSig + sizeof(float) * (CAUSAL ? 4 : 2) * TT * LDC, red_bytes<NW_>()));
+    static constexpr size_t oTh = r0;
+    static constexpr size_t oV = align16(oTh + sizeof(float) * TT * LDC);
     static constexpr size_t oG = align16(oV + sizeof(T) * TT * LDN);
     static constexpr size_t oVt = align16(oG + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oGt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
     static constexpr size_t oPkt = align16(oGt + (CAUSAL ? sizeof(T) * D * LDT : 0));
     static constexpr size_t oWt = align16(oPkt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
-    static constexpr size_t oDproj = align16(oWt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
+    static constexpr size_t oUs = align16(oWt + (CAUSAL ? sizeof(T) * SP * LDT : 0));  // per wave [D][LDU]
+    static constexpr size_t oDproj = align16(oUs + sizeof(T) * NW_ * D * LDU);
     static constexpr size_t oPl = align16(oDproj + sizeof(T) * TT * LDDP);
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t oPlT = align16(oPlLo + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oSig = align16(oPlT + sizeof(T) * D * LDDP);  // K sp, K sm, K th, Q sp, Q sm
-    static constexpr size_t oRed = align16(oSig + sizeof(float) * (CAUSAL ? 5 : 3) * TT * LDC);
-    static constexpr size_t bytes = align16(oRed + sizeof(float) * cmax(64 * NW_, NW_ > 1 ? NW_ * TT * LDR : 0));
+    static constexpr size_t oRed = align16(oPlT + sizeof(T) * D * LDDP);
+    static constexpr size_t bytes = align16(oRed + sizeof(float) * 64 * NW_);
 };
 
-template <typename T, int SP, bool CAUSAL>
+template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
     using Ly = BwdOutL<T, SP, CAUSAL>;
-    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
+                  LDU = Ly::LDU;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sV = (T *)(smem + Ly::oV);
     T *sG = (T *)(smem + Ly::oG), *sVt = (T *)(smem + Ly::oVt), *sGt = (T *)(smem + Ly::oGt);
     T *sDproj = (T *)(smem + Ly::oDproj);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo), *sPlT = (T *)(smem + Ly::oPlT);
-    float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
-    float *sSpK = sSig, *sSmK = sSig + TT * LDC, *sThK = sSig + 2 * TT * LDC;
-    float *sSpQ = sSig + 3 * TT * LDC, *sSmQ = sSig + 4 * TT * LDC;
+    float *sSig = (float *)(smem + Ly::oSig), *sThK = (float *)(smem + Ly::oTh);
+    float *sRedV = (float *)(smem + Ly::oQ), *sRed = (float *)(smem + Ly::oRed);
+    float *sSpK = sSig, *sSmK = sSig + TT * LDC, *sSpQ = sSig + 2 * TT * LDC, *sSmQ = sSig + 3 * TT * LDC;
     const int w = wave_id(), g = lg(), i = li(), sw = 32 * w;
     T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT, *sWt = (T *)(smem + Ly::oWt) + sw * LDT;
+    T *sUs = (T *)(smem + Ly::oUs) + w * D * LDU;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -839,7 +933,7 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
     // reverse carries (U, alpha) after the segment; forward state at the segment end
     const float *rs = a.rstate + ((int64_t)n * a.nseg + seg) * SP * SROW;
     const double *fs = a.fstate + ((int64_t)n * (a.nseg + 1) + seg + 1) * SP * SROW;
-    f32x4 Ut[4][2], Us[2][4];  // U^T[d][s] (d-row) and U[s][d] (bucket-row)
+    f32x4 Ut[4][2];  // U^T[d = 16md + 4g + e][s = sw + 16ns + i]
     double Be[4][2][4], Ae[2][4];
     float al[2][4];
     for (int md = 0; md < 4; ++md)
@@ -849,25 +943,44 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
                 Ut[md][ns][e] = rs[r];
                 Be[md][ns][e] = CAUSAL ? fs[r] : 0.0;
             }
-    for (int ms = 0; ms < 2; ++ms) {
-        for (int md = 0; md < 4; ++md)
-            for (int e = 0; e < 4; ++e) Us[ms][md][e] = rs[sidx(sw + 16 * ms + 4 * g + e, 16 * md + i)];
+    for (int ms = 0; ms < 2; ++ms)
         for (int e = 0; e < 4; ++e) {
             al[ms][e] = rs[sidx(sw + 16 * ms + 4 * g + e, D)];
             Ae[ms][e] = CAUSAL ? fs[sidx(sw + 16 * ms + 4 * g + e, D)] : 0.0;
         }
-    }
     float tsum = 0.f;
 
+    Prefetch<T, NTH> pq_, pg_, pk_, pv_;
+    if (j0 < j1) {
+        const int64_t tl = (j1 - 1) * TT;
+        pk_.issue(kp, a.sk.t, tl, a.T);
+        pv_.issue(vp, a.sv.t, tl, a.T);
+        if constexpr (CAUSAL) {
+            pq_.issue(qp, a.sq.t, tl, a.T);
+            pg_.issue(gp, a.sdo.t, tl, a.T);
+        }
+    }
     for (int64_t jr = j1 - 1; jr >= j0; --jr) {
         const int64_t t0 = jr * TT;
         __syncthreads();
-        load_tile<T, NTH>(kp, a.sk.t, t0, a.T, sK, nullptr);
-        load_tile<T, NTH>(vp, a.sv.t, t0, a.T, sV, CAUSAL ? sVt : nullptr);
+        pk_.commit(sK, nullptr);
+        pv_.commit(sV, CAUSAL ? sVt : nullptr);
         if constexpr (CAUSAL) {
-            load_tile<T, NTH>(qp, a.sq.t, t0, a.T, sQ, nullptr);
-            load_tile<T, NTH>(gp, a.sdo.t, t0, a.T, sG, sGt);
+            pq_.commit(sQ, nullptr);
+            pg_.commit(sG, sGt);
         }
+        if (jr > j0) {
+            pk_.issue(kp, a.sk.t, t0 - TT, a.T);
+            pv_.issue(vp, a.sv.t, t0 - TT, a.T);
+            if constexpr (CAUSAL) {
+                pq_.issue(qp, a.sq.t, t0 - TT, a.T);
+                pg_.issue(gp, a.sdo.t, t0 - TT, a.T);
+            }
+        }
+        // U (after this tile) in [d][s] layout for the dV contraction over s
+        for (int md = 0; md < 4; ++md)
+            for (int ns = 0; ns < 2; ++ns)
+                for (int e = 0; e < 4; ++e) sUs[(16 * md + 4 * g + e) * LDU + 16 * ns + i] = from_f32<T>(Ut[md][ns][e]);
         __syncthreads();
         for (int q = w; q < (CAUSAL ? 8 : 4); q += NW_) {
             if (q < 4)
@@ -877,139 +990,154 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
         }
         __syncthreads();
         f32x4 PK[2][2], PKr[2][2];  // fp32 and operand-rounded
-        probs_st(a.K, sSpK, sSmK, sw, a.S, t0, a.T, PK);
+        probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
         for (int ms = 0; ms < 2; ++ms)
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PKr[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
         Frag<T> PKf[2];
         for (int nt = 0; nt < 2; ++nt) PKf[nt] = frag_acc<T>(PKr[0][nt], PKr[1][nt]);
         f32x4 dPK[2][2];
-        f32x4 VT[4][2];  // dV^T partial: lane holds dV^T[d = 16md + 4g + e][tau = 16nt + i]
         if constexpr (CAUSAL) {
-            f32x4 PQ[2][2], Acum[2][2], W[2][2], inv[2][2];
-            probs_st(a.K, sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
-            store_rows_T<T>(sPkt, PKr);
-            // forward state at the tile start: end state minus this tile's sums
+            f32x4 W[2][2], inv[2][2];
             {
+                f32x4 PQ[2][2], Acum[2][2];
+                probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
+                store_rows_T<T>(sPkt, PKr);
+                // forward state at the tile start: end state minus this tile's sums
                 float tot[2][4];
                 tile_totals(PKr, tot);
                 for (int ms = 0; ms < 2; ++ms)
                     for (int e = 0; e < 4; ++e) Ae[ms][e] -= (double)tot[ms][e];
-            }
-            tile_prefix(PKr, Acum);
-            for (int ms = 0; ms < 2; ++ms)
-                for (int nt = 0; nt < 2; ++nt)
-                    for (int e = 0; e < 4; ++e) {
-                        inv[ms][nt][e] = rcp((float)Ae[ms][e] + Acum[ms][nt][e] + a.eps);
-                        W[ms][nt][e] = PQ[ms][nt][e] * inv[ms][nt][e];
-                    }
-            store_rows_T<T>(sWt, W);
-            f32x4 HmT[2][2], Hm[2][2];
-            for (int mt = 0; mt < 2; ++mt)
-                for (int nt = 0; nt < 2; ++nt) {
-                    // Hm^T[tau][t] (tau <= t) for G; Hm[t][tau] (tau <= t) for dP_K
-                    HmT[mt][nt] = zero4();
-                    Hm[mt][nt] = zero4();
-                    if (mt <= nt) tile_mma(HmT[mt][nt], sV + 16 * mt * LDN, LDN, sG + 16 * nt * LDN, LDN, D / 32);
-                    if (mt >= nt) tile_mma(Hm[mt][nt], sG + 16 * mt * LDN, LDN, sV + 16 * nt * LDN, LDN, D / 32);
-                    for (int e = 0; e < 4; ++e) {
-                        if (16 * mt + 4 * g + e > 16 * nt + i) HmT[mt][nt][e] = 0.f;
-                        if (16 * nt + i > 16 * mt + 4 * g + e) Hm[mt][nt][e] = 0.f;
-                    }
-                }
-            __syncthreads();  // sPkt, sWt of this wave complete
-            f32x4 dB[4][2];
-            tile_dBT<T>(sVt, sPkt, dB);
-            f32x4 Bs[4][2];
-            for (int md = 0; md < 4; ++md)
-                for (int ns = 0; ns < 2; ++ns)
-                    for (int e = 0; e < 4; ++e) {
-                        Be[md][ns][e] -= (double)dB[md][ns][e];
-                        Bs[md][ns][e] = (float)Be[md][ns][e];
-                    }
-            // G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] Hm[t][tau]; dA = -W G/(A+eps)
-            f32x4 dA[2][2];
-            for (int ms = 0; ms < 2; ++ms)
-                for (int nt = 0; nt < 2; ++nt) {
-                    f32x4 G = zero4();
-                    for (int kk = 0; kk < 2; ++kk)
-                        mma(G, frag_acc<T>(Bs[2 * kk][ms], Bs[2 * kk + 1][ms]),
-                            ld_frag_pi(sG + (16 * nt + i) * LDN + 32 * kk));
-                    mma(G, ld_frag_pi(sPkt + (16 * ms + i) * LDT), frag_acc<T>(HmT[0][nt], HmT[1][nt]));
-                    for (int e = 0; e < 4; ++e) dA[ms][nt][e] = -W[ms][nt][e] * G[e] * inv[ms][nt][e];
-                }
-            // alpha(tau) = alpha_end + sum_{t >= tau} dA
-            f32x4 alpha[2][2];
-            tile_suffix(dA, alpha);
-            {
-                float tot[2][4];
-                tile_totals(dA, tot);
+                tile_prefix(PKr, Acum);
                 for (int ms = 0; ms < 2; ++ms)
                     for (int nt = 0; nt < 2; ++nt)
-                        for (int e = 0; e < 4; ++e) alpha[ms][nt][e] += al[ms][e];
+                        for (int e = 0; e < 4; ++e) {
+                            inv[ms][nt][e] = rcp((float)Ae[ms][e] + Acum[ms][nt][e] + a.eps);
+                            W[ms][nt][e] = PQ[ms][nt][e] * inv[ms][nt][e];
+                        }
+                store_rows_T<T>(sWt, W);
+            }
+            Frag<T> Wf[2];
+            for (int nt = 0; nt < 2; ++nt) Wf[nt] = frag_acc<T>(W[0][nt], W[1][nt]);
+            __syncthreads();  // sPkt, sWt, sUs complete; sigma tables and Q/K tiles dead
+            // ---- dV^T[d][tau] = sum_s U[s][d] P_K[tau][s] + sum_{t >= tau} g[t][d] Sc2^T[t][tau]
+            {
+                f32x4 Sc2[2][2];
+                for (int mt = 0; mt < 2; ++mt)
+                    for (int nt = 0; nt < 2; ++nt) {
+                        Sc2[mt][nt] = zero4();
+                        if (mt >= nt) mma(Sc2[mt][nt], Wf[mt], PKf[nt]);
+                        for (int e = 0; e < 4; ++e)
+                            if (16 * mt + 4 * g + e < 16 * nt + i) Sc2[mt][nt][e] = 0.f;
+                    }
+                f32x4 VT[4][2];
+                for (int md = 0; md < 4; ++md) {
+                    const Frag<T> uf = ld_frag_pi(sUs + (16 * md + i) * LDU);
+                    const Frag<T> gf = ld_frag_pi(sGt + (16 * md + i) * LDT);
+                    for (int nt = 0; nt < 2; ++nt) {
+                        VT[md][nt] = zero4();
+                        mma(VT[md][nt], uf, PKf[nt]);
+                        mma(VT[md][nt], gf, frag_acc<T>(Sc2[0][nt], Sc2[1][nt]));
+                    }
+                }
+                reduce_store<T, NW_>(VT, sRedV, dvp, a.sg.t, t0, a.T);
+            }
+            // ---- dA = -W G/(A+eps), G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] Hm[t][tau]
+            f32x4 dA[2][2];
+            {
+                f32x4 dB[4][2];
+                tile_dBT<T>(sVt, sPkt, dB);
+                Frag<T> Bf[2][2];  // [ns][kk]
+                for (int md = 0; md < 4; ++md)
+                    for (int ns = 0; ns < 2; ++ns)
+                        for (int e = 0; e < 4; ++e) Be[md][ns][e] -= (double)dB[md][ns][e];
+                for (int ns = 0; ns < 2; ++ns)
+                    for (int kk = 0; kk < 2; ++kk) {
+                        f32x4 b0, b1;
+                        for (int e = 0; e < 4; ++e) {
+                            b0[e] = (float)Be[2 * kk][ns][e];
+                            b1[e] = (float)Be[2 * kk + 1][ns][e];
+                        }
+                        Bf[ns][kk] = frag_acc<T>(b0, b1);
+                    }
+                f32x4 HmT[2][2];
+                for (int mt = 0; mt < 2; ++mt)
+                    for (int nt = 0; nt < 2; ++nt) {
+                        HmT[mt][nt] = zero4();
+                        if (mt <= nt) tile_mma(HmT[mt][nt], sV + 16 * mt * LDN, LDN, sG + 16 * nt * LDN, LDN, D / 32);
+                        for (int e = 0; e < 4; ++e)
+                            if (16 * mt + 4 * g + e > 16 * nt + i) HmT[mt][nt][e] = 0.f;
+                    }
+                for (int nt = 0; nt < 2; ++nt) {
+                    const Frag<T> hf = frag_acc<T>(HmT[0][nt], HmT[1][nt]);
+                    const Frag<T> g0 = ld_frag_pi(sG + (16 * nt + i) * LDN), g1 = ld_frag_pi(sG + (16 * nt + i) * LDN + 32);
+                    for (int ms = 0; ms < 2; ++ms) {
+                        f32x4 G = zero4();
+                        mma(G, Bf[ms][0], g0);
+                        mma(G, Bf[ms][1], g1);
+                        mma(G, ld_frag_pi(sPkt + (16 * ms + i) * LDT), hf);
+                        for (int e = 0; e < 4; ++e) dA[ms][nt][e] = -W[ms][nt][e] * G[e] * inv[ms][nt][e];
+                    }
+                }
+            }
+            // ---- dP_K[tau][s] = alpha(tau) + sum_d U[s][d] v_tau[d] + sum_{t >= tau} W[t][s] Hm[t][tau]
+            {
+                f32x4 alpha[2][2];
+                tile_suffix(dA, alpha);
+                float tot[2][4];
+                tile_totals(dA, tot);
+                f32x4 Hm[2][2];
+                for (int mt = 0; mt < 2; ++mt)
+                    for (int nt = 0; nt < 2; ++nt) {
+                        Hm[mt][nt] = zero4();
+                        if (mt >= nt) tile_mma(Hm[mt][nt], sG + 16 * mt * LDN, LDN, sV + 16 * nt * LDN, LDN, D / 32);
+                        for (int e = 0; e < 4; ++e)
+                            if (16 * nt + i > 16 * mt + 4 * g + e) Hm[mt][nt][e] = 0.f;
+                    }
+                for (int nt = 0; nt < 2; ++nt) {
+                    const Frag<T> hf = frag_acc<T>(Hm[0][nt], Hm[1][nt]);
+                    const Frag<T> v0 = ld_frag_pi(sV + (16 * nt + i) * LDN), v1 = ld_frag_pi(sV + (16 * nt + i) * LDN + 32);
+                    for (int ms = 0; ms < 2; ++ms) {
+                        f32x4 c = zero4();
+                        mma(c, frag_acc<T>(Ut[0][ms], Ut[1][ms]), v0);
+                        mma(c, frag_acc<T>(Ut[2][ms], Ut[3][ms]), v1);
+                        mma(c, ld_frag_pi(sWt + (16 * ms + i) * LDT), hf);
+                        for (int e = 0; e < 4; ++e) dPK[ms][nt][e] = c[e] + alpha[ms][nt][e] + al[ms][e];
+                    }
+                }
                 for (int ms = 0; ms < 2; ++ms)
                     for (int e = 0; e < 4; ++e) al[ms][e] += tot[ms][e];
             }
-            // dP_K[tau][s] = alpha + sum_d U[s][d] v_tau[d] + sum_{t >= tau} W[t][s] Hm[t][tau]
-            for (int ms = 0; ms < 2; ++ms)
-                for (int nt = 0; nt < 2; ++nt) {
-                    f32x4 c = zero4();
-                    for (int kk = 0; kk < 2; ++kk)
-                        mma(c, frag_acc<T>(Ut[2 * kk][ms], Ut[2 * kk + 1][ms]),
-                            ld_frag_pi(sV + (16 * nt + i) * LDN + 32 * kk));
-                    mma(c, ld_frag_pi(sWt + (16 * ms + i) * LDT), frag_acc<T>(Hm[0][nt], Hm[1][nt]));
-                    for (int e = 0; e < 4; ++e) dPK[ms][nt][e] = c[e] + alpha[ms][nt][e];
-                }
-            // Sc2^T[t][tau] = sum_s W[t][s] P_K[tau][s] for t >= tau
-            f32x4 Sc2[2][2];
-            Frag<T> Wf[2];
-            for (int nt = 0; nt < 2; ++nt) Wf[nt] = frag_acc<T>(W[0][nt], W[1][nt]);
-            for (int mt = 0; mt < 2; ++mt)
-                for (int nt = 0; nt < 2; ++nt) {
-                    Sc2[mt][nt] = zero4();
-                    if (mt >= nt) mma(Sc2[mt][nt], Wf[mt], PKf[nt]);
-                    for (int e = 0; e < 4; ++e)
-                        if (16 * mt + 4 * g + e < 16 * nt + i) Sc2[mt][nt][e] = 0.f;
-                }
-            // dV^T[d][tau] = sum_s U[s][d] P_K[tau][s] + sum_{t >= tau} g[t][d] Sc2^T[t][tau]
-            for (int md = 0; md < 4; ++md) {
-                const Frag<T> uf = frag_acc<T>(Us[0][md], Us[1][md]);
-                const Frag<T> gf = ld_frag_pi(sGt + (16 * md + i) * LDT);
-                for (int nt = 0; nt < 2; ++nt) {
-                    VT[md][nt] = zero4();
-                    mma(VT[md][nt], uf, PKf[nt]);
-                    mma(VT[md][nt], gf, frag_acc<T>(Sc2[0][nt], Sc2[1][nt]));
-                }
-            }
-            // U += this tile: U[s][d] += sum_t W[t][s] g[t][d] (both layouts)
-            for (int ms = 0; ms < 2; ++ms) {
-                const Frag<T> wa = ld_frag(sWt + (16 * ms + i) * LDT + 8 * g);
-                for (int md = 0; md < 4; ++md) {
-                    const Frag<T> gb = ld_frag(sGt + (16 * md + i) * LDT + 8 * g);
-                    mma(Us[ms][md], wa, gb);
-                    mma(Ut[md][ms], gb, wa);
-                }
+            // ---- U^T[d][s] += sum_t g[t][d] W[t][s]
+            for (int ns = 0; ns < 2; ++ns) {
+                const Frag<T> wb = ld_frag(sWt + (16 * ns + i) * LDT + 8 * g);
+                for (int md = 0; md < 4; ++md) mma(Ut[md][ns], ld_frag(sGt + (16 * md + i) * LDT + 8 * g), wb);
             }
         } else {
-            // non-causal: dP_K = alpha + v . U (totals); dV^T = U^T P_K^T
-            for (int ms = 0; ms < 2; ++ms)
-                for (int nt = 0; nt < 2; ++nt) {
-                    f32x4 c = zero4();
-                    for (int kk = 0; kk < 2; ++kk)
-                        mma(c, frag_acc<T>(Ut[2 * kk][ms], Ut[2 * kk + 1][ms]),
-                            ld_frag_pi(sV + (16 * nt + i) * LDN + 32 * kk));
-                    for (int e = 0; e < 4; ++e) dPK[ms][nt][e] = c[e] + al[ms][e];
+            __syncthreads();  // sUs complete; sigma tables and K tile dead
+            // non-causal: dV^T = U^T P_K^T; dP_K = alpha + v . U (totals)
+            {
+                f32x4 VT[4][2];
+                for (int md = 0; md < 4; ++md) {
+                    const Frag<T> uf = ld_frag_pi(sUs + (16 * md + i) * LDU);
+                    for (int nt = 0; nt < 2; ++nt) {
+                        VT[md][nt] = zero4();
+                        mma(VT[md][nt], uf, PKf[nt]);
+                    }
                 }
-            for (int md = 0; md < 4; ++md) {
-                const Frag<T> uf = frag_acc<T>(Us[0][md], Us[1][md]);
-                for (int nt = 0; nt < 2; ++nt) {
-                    VT[md][nt] = zero4();
-                    mma(VT[md][nt], uf, PKf[nt]);
+                reduce_store<T, NW_>(VT, sRedV, dvp, a.sg.t, t0, a.T);
+            }
+            for (int nt = 0; nt < 2; ++nt) {
+                const Frag<T> v0 = ld_frag_pi(sV + (16 * nt + i) * LDN), v1 = ld_frag_pi(sV + (16 * nt + i) * LDN + 32);
+                for (int ms = 0; ms < 2; ++ms) {
+                    f32x4 c = zero4();
+                    mma(c, frag_acc<T>(Ut[0][ms], Ut[1][ms]), v0);
+                    mma(c, frag_acc<T>(Ut[2][ms], Ut[3][ms]), v1);
+                    for (int e = 0; e < 4; ++e) dPK[ms][nt][e] = c[e] + al[ms][e];
                 }
             }
         }
-        tsum += softhash_bwd_st<T>(a.K, PK, dPK, sThK, sw, a.L, a.inv_temp, sDproj);
-        reduce_store<T, NW_>(VT, sRed, dvp, a.sg.t, t0, a.T);
+        tsum += softhash_bwd_st<KB, T>(PK, dPK, sThK, sw, a.L, a.inv_temp, sDproj);
         __syncthreads();
         dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0, a.T);
     }
