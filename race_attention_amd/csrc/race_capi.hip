@@ -150,15 +150,15 @@ bool run_phase(const race_desc *d, int ph) { return d->phases == 0 || (d->phases
 
 template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
     const dim3 grid(p.nseg, (unsigned)p.N);
-    if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP, KB><<<grid, 2 * SP, 0, s>>>(a);
+    if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
     const int elems = SP * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
         k_fwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
     if (run_phase(d, RACE_PHASE_OUT)) {
         if (d->causal)
-            k_fwd_out<T, SP, true, KB><<<grid, 2 * SP, 0, s>>>(a);
+            k_fwd_out<T, SP, true, KB><<<grid, threads_of(SP), 0, s>>>(a);
         else
-            k_fwd_out<T, SP, false, KB><<<grid, 2 * SP, 0, s>>>(a);
+            k_fwd_out<T, SP, false, KB><<<grid, threads_of(SP), 0, s>>>(a);
     }
     return launched("race_fwd");
 }
@@ -168,9 +168,9 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
     const dim3 grid(p.nseg, (unsigned)p.N);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
         if (d->causal)
-            k_bwd_reduce<T, SP, true, KB><<<grid, 2 * SP, 0, s>>>(a);
+            k_bwd_reduce<T, SP, true, KB><<<grid, threads_of(SP), 0, s>>>(a);
         else
-            k_bwd_reduce<T, SP, false, KB><<<grid, 2 * SP, 0, s>>>(a);
+            k_bwd_reduce<T, SP, false, KB><<<grid, threads_of(SP), 0, s>>>(a);
     }
     const int elems = SP * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
@@ -178,9 +178,9 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
                                                                             d->causal);
     if (run_phase(d, RACE_PHASE_OUT)) {
         if (d->causal)
-            k_bwd_out<T, SP, true, KB><<<grid, 2 * SP, 0, s>>>(a);
+            k_bwd_out<T, SP, true, KB><<<grid, threads_of(SP), 0, s>>>(a);
         else
-            k_bwd_out<T, SP, false, KB><<<grid, 2 * SP, 0, s>>>(a);
+            k_bwd_out<T, SP, false, KB><<<grid, threads_of(SP), 0, s>>>(a);
         if (grad_inv_temp) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, 2 * p.N * p.nseg, grad_inv_temp);
     }
     return launched("race_bwd");

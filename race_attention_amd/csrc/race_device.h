@@ -165,6 +165,52 @@ __device__ __forceinline__ Frag<float> ld_frag_pi(const float *p) {
     return f;
 }
 
+// 16-deep k step: lane (g, i) holds k = 4g..4g+3 of row/column i
+// (v_mfma_f32_16x16x16_bf16; fp32: four 16x16x4 steps).  One accumulator tile
+// (lane holds X[4g + e][i]) is directly such an operand over its 16 rows.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+template <typename T> struct Frag4;
+template <> struct Frag4<bf16> { s16x4 v; };
+template <> struct Frag4<float> { f32x4 v; };
+
+template <typename T> __device__ __forceinline__ Frag4<T> frag16_acc(const f32x4 &x);
+template <> __device__ __forceinline__ Frag4<bf16> frag16_acc<bf16>(const f32x4 &x) {
+    typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    bf16x4 b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = (bf16)x[j];
+    Frag4<bf16> f;
+    f.v = __builtin_bit_cast(s16x4, b);
+    return f;
+}
+template <> __device__ __forceinline__ Frag4<float> frag16_acc<float>(const f32x4 &x) {
+    Frag4<float> f;
+    f.v = x;
+    return f;
+}
+// p[4g..4g+3]
+__device__ __forceinline__ Frag4<bf16> ld_frag16(const bf16 *p) {
+    Frag4<bf16> f;
+    f.v = *reinterpret_cast<const s16x4 *>(p + 4 * (lane_id() >> 4));
+    return f;
+}
+__device__ __forceinline__ Frag4<float> ld_frag16(const float *p) {
+    Frag4<float> f;
+    f.v = *reinterpret_cast<const f32x4 *>(p + 4 * (lane_id() >> 4));
+    return f;
+}
+// The accumulator of a 16x16x16 bf16 product is never passed as SrcC of a
+// 16x16x32 product (or the reverse): the compiler may issue such a pair back
+// to back without wait states, and on gfx950 the second product then reads a
+// stale accumulator.  Mixed-depth sums use separate accumulators added on VALU.
+__device__ __forceinline__ void mma16(f32x4 &c, const Frag4<bf16> &a, const Frag4<bf16> &b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.v, b.v, c, 0, 0, 0);
+}
+__device__ __forceinline__ void mma16(f32x4 &c, const Frag4<float> &a, const Frag4<float> &b) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[e], b.v[e], c, 0, 0, 0);
+}
+
 // ------------------------------------------------------------ row (16-lane) ops
 // DPP moves inside each 16-lane row; lanes whose source is outside the row read 0.
 template <int CTRL> __device__ __forceinline__ float dpp_f(float x) {

@@ -17,12 +17,14 @@
 // so bit-identical -- from the segment's end state in fp64.  The non-causal
 // operator runs the same kernels with full-sequence sums and no triangles.
 //
-// Inside a workgroup wave w owns buckets [32w, 32w+32): the workgroup has
-// SP/32 waves.  Per-bucket quantities live in the "bucket-row" accumulator
-// layout (lane (g,i) holds rows s = 16ms + 4g + e, column t = 16nt + i of a
+// Inside a workgroup wave w owns buckets [16w, 16w+16): the workgroup has
+// SP/16 waves.  Per-bucket quantities live in the "bucket-row" accumulator
+// layout (lane (g,i) holds row s = 16w + 4g + e, column t = 16nt + i of a
 // [bucket x token] matrix), where prefix/suffix sums over tokens are 16-lane
-// DPP row scans and the 32 buckets of the wave form one 32-deep MFMA k step,
-// so accumulator tiles feed the next MFMA directly (frag_acc / ld_frag_pi).
+// DPP row scans and the 16 buckets of the wave form one 16-deep MFMA k step,
+// so accumulator tiles feed the next MFMA directly (frag16_acc); token
+// contractions pair two accumulator tiles into a 32-deep step (frag_acc /
+// ld_frag_pi).
 // Token contractions read the transposed operand from LDS.  The triangle of a
 // tile is a masked 32x32 product: O = W B_start + tril(W P_K^T) V.
 //
@@ -55,6 +57,8 @@ struct Args {
 };
 
 constexpr int SROW = D + 1;  // state row: D values of B (or U) then A (or alpha)
+constexpr int WB = 16;       // buckets per wave
+__host__ __device__ constexpr int threads_of(int SP) { return 64 * (SP / WB); }
 
 __device__ __forceinline__ int64_t stream_off(const Strides &s, int n, int B, int H) {
     const int h = n % H, b = (n / H) % B, m = n / (H * B);
@@ -87,26 +91,6 @@ template <> __device__ __forceinline__ void store4<bf16>(bf16 *p, const f32x4 &v
 }
 
 // --------------------------------------------------------------- tile I/O
-// Load a [TT][D] token tile (rows t0.. of a stream, row stride st elements);
-// rows at or beyond T read as zero.  nat: [TT][ld_of<T>(D)], trn: [D][ld_of<T>(TT)].
-template <typename T, int NTH>
-__device__ void load_tile(const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn, T *nat, T *trn) {
-    constexpr int EPC = 16 / sizeof(T);
-    constexpr int CPR = D / EPC;
-    constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT);
-    for (int idx = threadIdx.x; idx < TT * CPR; idx += NTH) {
-        const int t = idx / CPR, c = idx % CPR;
-        uint4 val = make_uint4(0, 0, 0, 0);
-        if (t0 + t < Tn) val = *reinterpret_cast<const uint4 *>(src + (t0 + t) * st + c * EPC);
-        if (nat) *reinterpret_cast<uint4 *>(nat + t * LDN + c * EPC) = val;
-        if (trn) {
-            const T *e = reinterpret_cast<const T *>(&val);
-#pragma unroll
-            for (int j = 0; j < EPC; ++j) trn[(c * EPC + j) * LDT + t] = e[j];
-        }
-    }
-}
-
 // Register-staged tile load: issue() starts the global loads of one tile
 // into registers, commit() writes them to LDS (natural and/or transposed), so
 // the next tile's loads overlap the current tile's compute.
@@ -178,51 +162,48 @@ __device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mc, in
     if (sth) *reinterpret_cast<f32x4 *>(sth + t * LDC + c0) = th;
 }
 
-// Bucket probabilities of the wave's 32 buckets in bucket-row layout:
-// P[ms][nt][e] = P[t = 16nt + i][s = sw + 16ms + 4g + e]; zero for s >= S or
-// t0 + t >= T.  For K >= 2 the 4 buckets of a lane share one table and differ
-// in the two lowest corner bits: P = hi * (bit1 ? s+ : s-) * (bit0 ? s+ : s-).
+// Bucket probabilities of the wave's 16 buckets in bucket-row layout:
+// P[nt][e] = P[t = 16nt + i][s = sw + 4g + e]; zero for s >= S or t0 + t >= T.
+// For K >= 2 the 4 buckets of a lane share one table and differ in the two
+// lowest corner bits: P = hi * (bit1 ? s+ : s-) * (bit0 ? s+ : s-).
 template <int KB>
 __device__ __forceinline__ void probs_st(const float *sp, const float *sm, int sw, int S, int64_t t0, int64_t Tn,
-                                         f32x4 (&P)[2][2]) {
+                                         f32x4 (&P)[2]) {
     constexpr int LDC = ld_of<float>(NCOL);
     constexpr int R = 1 << KB;
     const int g = lg(), i = li();
+    const int s0 = sw + 4 * g;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int t = 16 * nt + i;
         const bool tv = t0 + t < Tn;
+        if constexpr (KB == 1) {
+            // tables s0/2 and s0/2 + 1; corner r = 1 is sigmoid(+2u)
+            const bool v01 = tv && s0 < S, v23 = tv && s0 + 2 < S;
+            const int l0 = v01 ? s0 >> 1 : 0, l1 = v23 ? (s0 >> 1) + 1 : 0;
+            P[nt][0] = v01 ? sm[t * LDC + l0] : 0.f;
+            P[nt][1] = v01 ? sp[t * LDC + l0] : 0.f;
+            P[nt][2] = v23 ? sm[t * LDC + l1] : 0.f;
+            P[nt][3] = v23 ? sp[t * LDC + l1] : 0.f;
+        } else {
+            const bool v = tv && s0 < S;
+            const int l = s0 < S ? s0 >> KB : 0;
+            const int r0 = s0 & (R - 1);
+            const float *pp = sp + t * LDC + l * KB, *pm = sm + t * LDC + l * KB;
+            float fp[KB], fm[KB];
 #pragma unroll
-        for (int ms = 0; ms < 2; ++ms) {
-            const int s0 = sw + 16 * ms + 4 * g;
-            if constexpr (KB == 1) {
-                // tables s0/2 and s0/2 + 1; corner r = 1 is sigmoid(+2u)
-                const bool v01 = tv && s0 < S, v23 = tv && s0 + 2 < S;
-                const int l0 = v01 ? s0 >> 1 : 0, l1 = v23 ? (s0 >> 1) + 1 : 0;
-                P[ms][nt][0] = v01 ? sm[t * LDC + l0] : 0.f;
-                P[ms][nt][1] = v01 ? sp[t * LDC + l0] : 0.f;
-                P[ms][nt][2] = v23 ? sm[t * LDC + l1] : 0.f;
-                P[ms][nt][3] = v23 ? sp[t * LDC + l1] : 0.f;
-            } else {
-                const bool v = tv && s0 < S;
-                const int l = s0 < S ? s0 >> KB : 0;
-                const int r0 = s0 & (R - 1);
-                const float *pp = sp + t * LDC + l * KB, *pm = sm + t * LDC + l * KB;
-                float fp[KB], fm[KB];
-#pragma unroll
-                for (int k = 0; k < KB; ++k) {
-                    fp[k] = pp[k];
-                    fm[k] = pm[k];
-                }
-                float hi = v ? 1.f : 0.f;
-#pragma unroll
-                for (int k = 0; k < KB - 2; ++k) hi *= ((r0 >> (KB - 1 - k)) & 1) ? fp[k] : fm[k];
-                const float h0 = hi * fm[KB - 2], h1 = hi * fp[KB - 2];
-                P[ms][nt][0] = h0 * fm[KB - 1];
-                P[ms][nt][1] = h0 * fp[KB - 1];
-                P[ms][nt][2] = h1 * fm[KB - 1];
-                P[ms][nt][3] = h1 * fp[KB - 1];
+            for (int k = 0; k < KB; ++k) {
+                fp[k] = pp[k];
+                fm[k] = pm[k];
             }
+            float hi = v ? 1.f : 0.f;
+#pragma unroll
+            for (int k = 0; k < KB - 2; ++k) hi *= ((r0 >> (KB - 1 - k)) & 1) ? fp[k] : fm[k];
+            const float h0 = hi * fm[KB - 2], h1 = hi * fp[KB - 2];
+            P[nt][0] = h0 * fm[KB - 1];
+            P[nt][1] = h0 * fp[KB - 1];
+            P[nt][2] = h1 * fm[KB - 1];
+            P[nt][3] = h1 * fp[KB - 1];
         }
     }
 }
@@ -239,59 +220,56 @@ template <int KB> __device__ __forceinline__ float table_reduce(float x) {
 // buckets: dP (and P, fp32) -> dproj [TT][ld_of<T>(NCOL)] columns l*K + k of
 // the wave's tables; returns this lane's share of sum du * th.
 // du_k = sum_r dl_r c_rk over the table; the two lowest corner bits vary with
-// e inside the lane, the higher ones are fixed per lane (from its rows g).
+// e inside the lane, the higher ones are fixed per lane (from its row g).
 template <int KB, typename T>
-__device__ float softhash_bwd_st(const f32x4 (&P)[2][2], const f32x4 (&dP)[2][2], const float *sth, int sw, int L,
+__device__ float softhash_bwd_st(const f32x4 (&P)[2], const f32x4 (&dP)[2], const float *sth, int sw, int L,
                                  float inv_temp, T *dproj) {
     constexpr int LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
     constexpr int R = 1 << KB;
     constexpr int RPT = R >= 4 ? R / 4 : 1;  // rows g per table
     const int g = lg(), i = li();
+    const int s0 = sw + 4 * g;
     float tsum = 0.f;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int t = 16 * nt + i;
+        f32x4 pd, dl;
 #pragma unroll
-        for (int ms = 0; ms < 2; ++ms) {
-            const int s0 = sw + 16 * ms + 4 * g;
-            f32x4 pd, dl;
+        for (int e = 0; e < 4; ++e) pd[e] = P[nt][e] * dP[nt][e];
+        if constexpr (KB == 1) {
+            const float d01 = pd[0] + pd[1], d23 = pd[2] + pd[3];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) pd[e] = P[ms][nt][e] * dP[ms][nt][e];
-            if constexpr (KB == 1) {
-                const float d01 = pd[0] + pd[1], d23 = pd[2] + pd[3];
+            for (int e = 0; e < 4; ++e) dl[e] = P[nt][e] * (dP[nt][e] - (e < 2 ? d01 : d23));
 #pragma unroll
-                for (int e = 0; e < 4; ++e) dl[e] = P[ms][nt][e] * (dP[ms][nt][e] - (e < 2 ? d01 : d23));
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int l = (s0 >> 1) + h;
-                    const float du = dl[2 * h + 1] - dl[2 * h];  // corner r = 1 is +1
-                    if (l < L) {
-                        const float th = sth[t * LDC + l];
-                        tsum += du * th;
-                        dproj[t * LDDP + l] = from_f32<T>(du * inv_temp * (1.f - th * th));
-                    }
-                }
-            } else {
-                const float dot = table_reduce<KB>(pd[0] + pd[1] + pd[2] + pd[3]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) dl[e] = P[ms][nt][e] * (dP[ms][nt][e] - dot);
-                const float sum = dl[0] + dl[1] + dl[2] + dl[3];
-                const int l = s0 >> KB, r0 = s0 & (R - 1);
-                float du[KB];
-#pragma unroll
-                for (int k = 0; k < KB - 2; ++k) du[k] = ((r0 >> (KB - 1 - k)) & 1) ? sum : -sum;
-                du[KB - 2] = (dl[2] + dl[3]) - (dl[0] + dl[1]);
-                du[KB - 1] = (dl[1] + dl[3]) - (dl[0] + dl[2]);
-#pragma unroll
-                for (int k = 0; k < KB; ++k) du[k] = table_reduce<KB>(du[k]);
+            for (int h = 0; h < 2; ++h) {
+                const int l = (s0 >> 1) + h;
+                const float du = dl[2 * h + 1] - dl[2 * h];  // corner r = 1 is +1
                 if (l < L) {
+                    const float th = sth[t * LDC + l];
+                    tsum += du * th;
+                    dproj[t * LDDP + l] = from_f32<T>(du * inv_temp * (1.f - th * th));
+                }
+            }
+        } else {
+            const float dot = table_reduce<KB>(pd[0] + pd[1] + pd[2] + pd[3]);
 #pragma unroll
-                    for (int k = 0; k < KB; ++k) {
-                        if ((k % RPT) == (g % RPT)) {
-                            const float th = sth[t * LDC + l * KB + k];
-                            tsum += du[k] * th;
-                            dproj[t * LDDP + l * KB + k] = from_f32<T>(du[k] * inv_temp * (1.f - th * th));
-                        }
+            for (int e = 0; e < 4; ++e) dl[e] = P[nt][e] * (dP[nt][e] - dot);
+            const float sum = dl[0] + dl[1] + dl[2] + dl[3];
+            const int l = s0 >> KB, r0 = s0 & (R - 1);
+            float du[KB];
+#pragma unroll
+            for (int k = 0; k < KB - 2; ++k) du[k] = ((r0 >> (KB - 1 - k)) & 1) ? sum : -sum;
+            du[KB - 2] = (dl[2] + dl[3]) - (dl[0] + dl[1]);
+            du[KB - 1] = (dl[1] + dl[3]) - (dl[0] + dl[2]);
+#pragma unroll
+            for (int k = 0; k < KB; ++k) du[k] = table_reduce<KB>(du[k]);
+            if (l < L) {
+#pragma unroll
+                for (int k = 0; k < KB; ++k) {
+                    if ((k % RPT) == (g % RPT)) {
+                        const float th = sth[t * LDC + l * KB + k];
+                        tsum += du[k] * th;
+                        dproj[t * LDDP + l * KB + k] = from_f32<T>(du[k] * inv_temp * (1.f - th * th));
                     }
                 }
             }
@@ -300,63 +278,52 @@ __device__ float softhash_bwd_st(const f32x4 (&P)[2][2], const f32x4 (&dP)[2][2]
     return tsum;
 }
 
-// Per-bucket token sums of a tile: tot[ms][e] = sum over the tile's 32 tokens
+// Per-bucket token sums of a tile: tot[e] = sum over the tile's 32 tokens
 // (identical code in every kernel, so the values are bit-identical).
-__device__ __forceinline__ void tile_totals(const f32x4 (&X)[2][2], float (&tot)[2][4]) {
+__device__ __forceinline__ void tile_totals(const f32x4 (&X)[2], float (&tot)[4]) {
 #pragma unroll
-    for (int ms = 0; ms < 2; ++ms)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) tot[ms][e] = row_sum(X[ms][0][e]) + row_sum(X[ms][1][e]);
+    for (int e = 0; e < 4; ++e) tot[e] = row_sum(X[0][e]) + row_sum(X[1][e]);
 }
-// inclusive prefix over the tile's tokens, plus base
-__device__ __forceinline__ void tile_prefix(const f32x4 (&X)[2][2], f32x4 (&Y)[2][2]) {
+// inclusive prefix over the tile's tokens
+__device__ __forceinline__ void tile_prefix(const f32x4 (&X)[2], f32x4 (&Y)[2]) {
 #pragma unroll
-    for (int ms = 0; ms < 2; ++ms)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float tot0 = row_sum(X[ms][0][e]);
-            Y[ms][0][e] = row_prefix(X[ms][0][e]);
-            Y[ms][1][e] = row_prefix(X[ms][1][e]) + tot0;
-        }
+    for (int e = 0; e < 4; ++e) {
+        const float tot0 = row_sum(X[0][e]);
+        Y[0][e] = row_prefix(X[0][e]);
+        Y[1][e] = row_prefix(X[1][e]) + tot0;
+    }
 }
 // inclusive suffix over the tile's tokens
-__device__ __forceinline__ void tile_suffix(const f32x4 (&X)[2][2], f32x4 (&Y)[2][2]) {
+__device__ __forceinline__ void tile_suffix(const f32x4 (&X)[2], f32x4 (&Y)[2]) {
 #pragma unroll
-    for (int ms = 0; ms < 2; ++ms)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float tot1 = row_sum(X[ms][1][e]);
-            Y[ms][1][e] = row_suffix(X[ms][1][e]);
-            Y[ms][0][e] = row_suffix(X[ms][0][e]) + tot1;
-        }
+    for (int e = 0; e < 4; ++e) {
+        const float tot1 = row_sum(X[1][e]);
+        Y[1][e] = row_suffix(X[1][e]);
+        Y[0][e] = row_suffix(X[0][e]) + tot1;
+    }
 }
 
-// bucket-row values -> per-wave transposed LDS [32 s][ld_of<T>(TT)] (rows s, columns t)
-template <typename T> __device__ __forceinline__ void store_rows_T(T *dst, const f32x4 (&X)[2][2]) {
+// bucket-row values -> per-wave transposed LDS [16 s][ld_of<T>(TT)] (rows s, columns t)
+template <typename T> __device__ __forceinline__ void store_rows_T(T *dst, const f32x4 (&X)[2]) {
     constexpr int LDT = ld_of<T>(TT);
     const int g = lg(), i = li();
 #pragma unroll
-    for (int ms = 0; ms < 2; ++ms)
+    for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dst[(16 * ms + 4 * g + e) * LDT + 16 * nt + i] = from_f32<T>(X[ms][nt][e]);
+        for (int e = 0; e < 4; ++e) dst[(4 * g + e) * LDT + 16 * nt + i] = from_f32<T>(X[nt][e]);
 }
 
 // d-row tile sums dB^T = V^T P_K for the wave's buckets (fp32 MFMA from zero):
-// out[md][ns] lane holds dB^T[d = 16md + 4g + e][s = sw + 16ns + i]
+// out[md] lane holds dB^T[d = 16md + 4g + e][s = sw + i]
 template <typename T>
-__device__ __forceinline__ void tile_dBT(const T *vt, const T *pkt, f32x4 (&out)[4][2]) {
+__device__ __forceinline__ void tile_dBT(const T *vt, const T *pkt, f32x4 (&out)[4]) {
     constexpr int LDT = ld_of<T>(TT);
     const int g = lg(), i = li();
+    const Frag<T> b = ld_frag(pkt + i * LDT + 8 * g);
 #pragma unroll
-    for (int ns = 0; ns < 2; ++ns) {
-        const Frag<T> b = ld_frag(pkt + (16 * ns + i) * LDT + 8 * g);
-#pragma unroll
-        for (int md = 0; md < 4; ++md) {
-            out[md][ns] = zero4();
-            mma(out[md][ns], ld_frag(vt + (16 * md + i) * LDT + 8 * g), b);
-        }
+    for (int md = 0; md < 4; ++md) {
+        out[md] = zero4();
+        mma(out[md], ld_frag(vt + (16 * md + i) * LDT + 8 * g), b);
     }
 }
 
@@ -432,7 +399,7 @@ __device__ __forceinline__ int64_t sidx(int s, int d) { return (int64_t)s * SROW
 // k_fwd_reduce: per-segment (A, B) sums (fp64 over fp32 tile sums).
 // =====================================================================
 template <typename T, int SP> struct FwdReduceL {
-    static constexpr int NW_ = SP / 32;
+    static constexpr int NW_ = SP / WB;
     static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL);
     static constexpr size_t oK = 0;
     static constexpr size_t oVt = align16(oK + sizeof(T) * TT * LDN);
@@ -444,14 +411,14 @@ template <typename T, int SP> struct FwdReduceL {
 };
 
 template <typename T, int SP, int KB>
-__global__ __launch_bounds__(SP * 2) void k_fwd_reduce(Args a) {
+__global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     using Ly = FwdReduceL<T, SP>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
     float *sSp = (float *)(smem + Ly::oSig), *sSm = sSp + TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = 32 * w;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
     T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT;
 
     const int n = blockIdx.y, seg = blockIdx.x;
@@ -462,12 +429,11 @@ __global__ __launch_bounds__(SP * 2) void k_fwd_reduce(Args a) {
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
 
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
-    double accB[4][2][4], accA[2][4];
-    for (int md = 0; md < 4; ++md)
-        for (int ns = 0; ns < 2; ++ns)
-            for (int e = 0; e < 4; ++e) accB[md][ns][e] = 0.0;
-    for (int ms = 0; ms < 2; ++ms)
-        for (int e = 0; e < 4; ++e) accA[ms][e] = 0.0;
+    double accB[4][4], accA[4];
+    for (int e = 0; e < 4; ++e) {
+        accA[e] = 0.0;
+        for (int md = 0; md < 4; ++md) accB[md][e] = 0.0;
+    }
 
     Prefetch<T, NTH> pk_, pv_;
     if (j0 < j1) {
@@ -486,30 +452,25 @@ __global__ __launch_bounds__(SP * 2) void k_fwd_reduce(Args a) {
         __syncthreads();
         for (int q = w; q < 4; q += NW_) project_tile<T>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, nullptr);
         __syncthreads();
-        f32x4 PK[2][2];
+        f32x4 PK[2];
         probs_st<KB>(sSp, sSm, sw, a.S, t0, a.T, PK);
-        for (int ms = 0; ms < 2; ++ms)
-            for (int nt = 0; nt < 2; ++nt)
-                for (int e = 0; e < 4; ++e) PK[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
+        for (int nt = 0; nt < 2; ++nt)
+            for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
         store_rows_T<T>(sPkt, PK);
-        float tot[2][4];
+        float tot[4];
         tile_totals(PK, tot);
-        for (int ms = 0; ms < 2; ++ms)
-            for (int e = 0; e < 4; ++e) accA[ms][e] += (double)tot[ms][e];
+        for (int e = 0; e < 4; ++e) accA[e] += (double)tot[e];
         __syncthreads();
-        f32x4 dB[4][2];
+        f32x4 dB[4];
         tile_dBT<T>(sVt, sPkt, dB);
         for (int md = 0; md < 4; ++md)
-            for (int ns = 0; ns < 2; ++ns)
-                for (int e = 0; e < 4; ++e) accB[md][ns][e] += (double)dB[md][ns][e];
+            for (int e = 0; e < 4; ++e) accB[md][e] += (double)dB[md][e];
     }
     double *out = a.fdelta + ((int64_t)n * a.nseg + seg) * SP * SROW;
     for (int md = 0; md < 4; ++md)
-        for (int ns = 0; ns < 2; ++ns)
-            for (int e = 0; e < 4; ++e) out[sidx(sw + 16 * ns + i, 16 * md + 4 * g + e)] = accB[md][ns][e];
+        for (int e = 0; e < 4; ++e) out[sidx(sw + i, 16 * md + 4 * g + e)] = accB[md][e];
     if (i == 0)
-        for (int ms = 0; ms < 2; ++ms)
-            for (int e = 0; e < 4; ++e) out[sidx(sw + 16 * ms + 4 * g + e, D)] = accA[ms][e];
+        for (int e = 0; e < 4; ++e) out[sidx(sw + 4 * g + e, D)] = accA[e];
 }
 
 // exclusive prefix over segments; [nseg] receives the total
@@ -529,7 +490,7 @@ __global__ void k_fwd_scan(double *fstate, const double *fdelta, int nseg, int e
 // over the waves.
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct FwdOutL {
-    static constexpr int NW_ = SP / 32;
+    static constexpr int NW_ = SP / WB;
     static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL);
     // region R0 = {Q, K, sigma tables}; the output reduction reuses it once they are dead
     static constexpr size_t oQ = 0;
@@ -544,7 +505,7 @@ template <typename T, int SP, bool CAUSAL> struct FwdOutL {
 };
 
 template <typename T, int SP, bool CAUSAL, int KB>
-__global__ __launch_bounds__(SP * 2) void k_fwd_out(Args a) {
+__global__ __launch_bounds__(threads_of(SP)) void k_fwd_out(Args a) {
     using Ly = FwdOutL<T, SP, CAUSAL>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
@@ -552,7 +513,7 @@ __global__ __launch_bounds__(SP * 2) void k_fwd_out(Args a) {
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
     float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oQ);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sSpK = sSig + 2 * TT * LDC, *sSmK = sSig + 3 * TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = 32 * w;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
     T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT;
 
     const int n = blockIdx.y, seg = blockIdx.x;
@@ -566,14 +527,13 @@ __global__ __launch_bounds__(SP * 2) void k_fwd_out(Args a) {
 
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
     // carried state: causal = prefix at the segment start, non-causal = totals.
-    // B in bucket-row layout: lane holds B[s = sw + 16ms + 4g + e][d = 16md + i]
+    // B in bucket-row layout: lane holds B[s = sw + 4g + e][d = 16md + i]
     const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * SP * SROW;
-    f32x4 Bc[2][4];
-    double a0[2][4];
-    for (int ms = 0; ms < 2; ++ms) {
-        for (int md = 0; md < 4; ++md)
-            for (int e = 0; e < 4; ++e) Bc[ms][md][e] = (float)st[sidx(sw + 16 * ms + 4 * g + e, 16 * md + i)];
-        for (int e = 0; e < 4; ++e) a0[ms][e] = st[sidx(sw + 16 * ms + 4 * g + e, D)];
+    f32x4 Bc[4];
+    double a0[4];
+    for (int e = 0; e < 4; ++e) {
+        for (int md = 0; md < 4; ++md) Bc[md][e] = (float)st[sidx(sw + 4 * g + e, 16 * md + i)];
+        a0[e] = st[sidx(sw + 4 * g + e, D)];
     }
 
     Prefetch<T, NTH> pq_, pk_, pv_;
@@ -607,65 +567,65 @@ __global__ __launch_bounds__(SP * 2) void k_fwd_out(Args a) {
                 project_tile<T>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
         }
         __syncthreads();
-        f32x4 PQ[2][2], PK[2][2], Acum[2][2];
+        f32x4 PQ[2], PK[2], Acum[2];
         probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
         if constexpr (CAUSAL) {
             probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
-            for (int ms = 0; ms < 2; ++ms)
-                for (int nt = 0; nt < 2; ++nt)
-                    for (int e = 0; e < 4; ++e) PK[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
+            for (int nt = 0; nt < 2; ++nt)
+                for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
             store_rows_T<T>(sPkt, PK);
             tile_prefix(PK, Acum);
         }
         // W = P_Q / (A(t) + eps)
-        f32x4 W[2][2];
-        for (int ms = 0; ms < 2; ++ms)
-            for (int nt = 0; nt < 2; ++nt)
-                for (int e = 0; e < 4; ++e) {
-                    const float A = (float)a0[ms][e] + (CAUSAL ? Acum[ms][nt][e] : 0.f);
-                    W[ms][nt][e] = PQ[ms][nt][e] * rcp(A + a.eps);
-                }
-        Frag<T> Wf[2];
-        for (int nt = 0; nt < 2; ++nt) Wf[nt] = frag_acc<T>(W[0][nt], W[1][nt]);
+        Frag4<T> Wf[2];
+        for (int nt = 0; nt < 2; ++nt) {
+            f32x4 W;
+            for (int e = 0; e < 4; ++e) {
+                const float A = (float)a0[e] + (CAUSAL ? Acum[nt][e] : 0.f);
+                W[e] = PQ[nt][e] * rcp(A + a.eps);
+            }
+            Wf[nt] = frag16_acc<T>(W);
+        }
         // O1^T[d][t] = sum_s B[s][d] W[t][s]
         f32x4 O[4][2];
         for (int md = 0; md < 4; ++md) {
-            const Frag<T> bf = frag_acc<T>(Bc[0][md], Bc[1][md]);
+            const Frag4<T> bf = frag16_acc<T>(Bc[md]);
             for (int nt = 0; nt < 2; ++nt) {
                 O[md][nt] = zero4();
-                mma(O[md][nt], bf, Wf[nt]);
+                mma16(O[md][nt], bf, Wf[nt]);
             }
         }
         if constexpr (CAUSAL) {
             // Sc^T[t'][t] = sum_s P_K[t'][s] W[t][s], kept for t' <= t
             f32x4 Sc[2][2];
-            Frag<T> PKf[2];
-            for (int nt = 0; nt < 2; ++nt) PKf[nt] = frag_acc<T>(PK[0][nt], PK[1][nt]);
-            for (int mt = 0; mt < 2; ++mt)
+            for (int mt = 0; mt < 2; ++mt) {
+                const Frag4<T> pf = frag16_acc<T>(PK[mt]);
                 for (int nt = 0; nt < 2; ++nt) {
                     Sc[mt][nt] = zero4();
-                    if (mt <= nt) mma(Sc[mt][nt], PKf[mt], Wf[nt]);
+                    if (mt <= nt) mma16(Sc[mt][nt], pf, Wf[nt]);
                     for (int e = 0; e < 4; ++e)
                         if (16 * mt + 4 * g + e > 16 * nt + i) Sc[mt][nt][e] = 0.f;
                 }
-            for (int ms = 0; ms < 2; ++ms) {
-                float tot[4];
-                for (int e = 0; e < 4; ++e) tot[e] = row_sum(PK[ms][0][e]) + row_sum(PK[ms][1][e]);
-                for (int e = 0; e < 4; ++e) a0[ms][e] += (double)tot[e];
             }
-            __syncthreads();  // sPkt of this wave complete
-            // O2^T[d][t] = sum_t' V[t'][d] Sc^T[t'][t]
+            float tot[4];
+            tile_totals(PK, tot);
+            for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
+            __syncthreads();  // sPkt complete; sigma tables and Q/K tiles dead before R0 is reused
+            // O2^T[d][t] = sum_t' V[t'][d] Sc^T[t'][t] (own accumulator: see mma16)
             for (int nt = 0; nt < 2; ++nt) {
                 const Frag<T> sf = frag_acc<T>(Sc[0][nt], Sc[1][nt]);
-                for (int md = 0; md < 4; ++md) mma(O[md][nt], ld_frag_pi(sVt + (16 * md + i) * LDT), sf);
+                for (int md = 0; md < 4; ++md) {
+                    f32x4 o2 = zero4();
+                    mma(o2, ld_frag_pi(sVt + (16 * md + i) * LDT), sf);
+                    O[md][nt] += o2;
+                }
             }
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
-            for (int ms = 0; ms < 2; ++ms) {
-                const Frag<T> pa = ld_frag(sPkt + (16 * ms + i) * LDT + 8 * g);
-                for (int md = 0; md < 4; ++md) mma(Bc[ms][md], pa, ld_frag(sVt + (16 * md + i) * LDT + 8 * g));
-            }
+            const Frag<T> pa = ld_frag(sPkt + i * LDT + 8 * g);
+            for (int md = 0; md < 4; ++md) mma(Bc[md], pa, ld_frag(sVt + (16 * md + i) * LDT + 8 * g));
+        } else {
+            __syncthreads();  // sigma tables and Q tile dead before R0 is reused
         }
-        if constexpr (!CAUSAL) __syncthreads();  // sigma tables and Q tile dead before R0 is reused
         reduce_store<T, NW_>(O, sRed, op, a.so.t, t0, a.T);
     }
 }
@@ -675,7 +635,7 @@ __global__ __launch_bounds__(SP * 2) void k_fwd_out(Args a) {
 // alpha = sum_t dA and U = sum_t W^T g.
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct BwdReduceL {
-    static constexpr int NW_ = SP / 32;
+    static constexpr int NW_ = SP / WB;
     static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
@@ -695,7 +655,7 @@ template <typename T, int SP, bool CAUSAL> struct BwdReduceL {
 };
 
 template <typename T, int SP, bool CAUSAL, int KB>
-__global__ __launch_bounds__(SP * 2) void k_bwd_reduce(Args a) {
+__global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     using Ly = BwdReduceL<T, SP, CAUSAL>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
@@ -706,7 +666,7 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_reduce(Args a) {
     float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sThQ = sSig + 2 * TT * LDC;
     float *sSpK = sSig + 3 * TT * LDC, *sSmK = sSig + 4 * TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = 32 * w;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
     T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT, *sWt = (T *)(smem + Ly::oWt) + sw * LDT;
 
     const int n = blockIdx.y, seg = blockIdx.x;
@@ -721,20 +681,18 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_reduce(Args a) {
 
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
     for (int idx = threadIdx.x; idx < TT * LDDP; idx += NTH) sDproj[idx] = from_f32<T>(0.f);
-    // forward state in d-row layout: lane holds B^T[d = 16md + 4g + e][s = sw + 16ns + i]
+    // forward state in d-row layout: lane holds B^T[d = 16md + 4g + e][s = sw + i]
     const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * SP * SROW;
-    f32x4 Bt[4][2], Ut[4][2];
-    double a0[2][4], al[2][4];
-    for (int md = 0; md < 4; ++md)
-        for (int ns = 0; ns < 2; ++ns) {
-            Ut[md][ns] = zero4();
-            for (int e = 0; e < 4; ++e) Bt[md][ns][e] = (float)st[sidx(sw + 16 * ns + i, 16 * md + 4 * g + e)];
-        }
-    for (int ms = 0; ms < 2; ++ms)
-        for (int e = 0; e < 4; ++e) {
-            a0[ms][e] = st[sidx(sw + 16 * ms + 4 * g + e, D)];
-            al[ms][e] = 0.0;
-        }
+    f32x4 Bt[4], Ut[4];
+    double a0[4], al[4];
+    for (int md = 0; md < 4; ++md) {
+        Ut[md] = zero4();
+        for (int e = 0; e < 4; ++e) Bt[md][e] = (float)st[sidx(sw + i, 16 * md + 4 * g + e)];
+    }
+    for (int e = 0; e < 4; ++e) {
+        a0[e] = st[sidx(sw + 4 * g + e, D)];
+        al[e] = 0.0;
+    }
     float tsum = 0.f;
 
     Prefetch<T, NTH> pq_, pg_, pk_, pv_;
@@ -771,23 +729,21 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_reduce(Args a) {
                 project_tile<T>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
         }
         __syncthreads();
-        f32x4 PQ[2][2], PK[2][2], Acum[2][2], W[2][2], inv[2][2];
+        f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2];
         probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
         if constexpr (CAUSAL) {
             probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
-            for (int ms = 0; ms < 2; ++ms)
-                for (int nt = 0; nt < 2; ++nt)
-                    for (int e = 0; e < 4; ++e) PK[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
+            for (int nt = 0; nt < 2; ++nt)
+                for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
             store_rows_T<T>(sPkt, PK);
             tile_prefix(PK, Acum);
         }
-        for (int ms = 0; ms < 2; ++ms)
-            for (int nt = 0; nt < 2; ++nt)
-                for (int e = 0; e < 4; ++e) {
-                    const float A = (float)a0[ms][e] + (CAUSAL ? Acum[ms][nt][e] : 0.f);
-                    inv[ms][nt][e] = rcp(A + a.eps);
-                    W[ms][nt][e] = PQ[ms][nt][e] * inv[ms][nt][e];
-                }
+        for (int nt = 0; nt < 2; ++nt)
+            for (int e = 0; e < 4; ++e) {
+                const float A = (float)a0[e] + (CAUSAL ? Acum[nt][e] : 0.f);
+                inv[nt][e] = rcp(A + a.eps);
+                W[nt][e] = PQ[nt][e] * inv[nt][e];
+            }
         store_rows_T<T>(sWt, W);
         // Hm^T[tau][t] = v_tau . g_t for tau <= t (B operand over tau, pi order)
         f32x4 HmT[2][2];
@@ -802,44 +758,36 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_reduce(Args a) {
         }
         __syncthreads();  // sPkt, sWt of this wave complete
         // G[s][t] = g_t . B_s(t) = sum_d B[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] Hm[t][tau]
-        f32x4 G[2][2];
-        for (int ms = 0; ms < 2; ++ms)
-            for (int nt = 0; nt < 2; ++nt) {
-                G[ms][nt] = zero4();
-                for (int kk = 0; kk < 2; ++kk)
-                    mma(G[ms][nt], frag_acc<T>(Bt[2 * kk][ms], Bt[2 * kk + 1][ms]),
-                        ld_frag_pi(sG + (16 * nt + i) * LDN + 32 * kk));
-                if constexpr (CAUSAL)
-                    mma(G[ms][nt], ld_frag_pi(sPkt + (16 * ms + i) * LDT), frag_acc<T>(HmT[0][nt], HmT[1][nt]));
+        f32x4 dPQ[2], dA[2];
+        for (int nt = 0; nt < 2; ++nt) {
+            f32x4 G = zero4();
+            for (int kk = 0; kk < 2; ++kk)
+                mma(G, frag_acc<T>(Bt[2 * kk], Bt[2 * kk + 1]), ld_frag_pi(sG + (16 * nt + i) * LDN + 32 * kk));
+            if constexpr (CAUSAL) mma(G, ld_frag_pi(sPkt + i * LDT), frag_acc<T>(HmT[0][nt], HmT[1][nt]));
+            // dP_Q = G/(A+eps); dA = -W G/(A+eps)
+            for (int e = 0; e < 4; ++e) {
+                dPQ[nt][e] = G[e] * inv[nt][e];
+                dA[nt][e] = -W[nt][e] * dPQ[nt][e];
             }
-        // dP_Q = G/(A+eps); dA = -W G/(A+eps)
-        f32x4 dPQ[2][2], dA[2][2];
-        for (int ms = 0; ms < 2; ++ms)
-            for (int nt = 0; nt < 2; ++nt)
-                for (int e = 0; e < 4; ++e) {
-                    dPQ[ms][nt][e] = G[ms][nt][e] * inv[ms][nt][e];
-                    dA[ms][nt][e] = -W[ms][nt][e] * dPQ[ms][nt][e];
-                }
+        }
         {
-            float tot[2][4];
+            float tot[4];
             tile_totals(dA, tot);
-            for (int ms = 0; ms < 2; ++ms)
-                for (int e = 0; e < 4; ++e) al[ms][e] += (double)tot[ms][e];
+            for (int e = 0; e < 4; ++e) al[e] += (double)tot[e];
         }
         // U^T[d][s] += sum_t g[t][d] W[t][s]; carry B^T[d][s] += sum_t V[t][d] P_K[t][s]
-        for (int ns = 0; ns < 2; ++ns) {
-            const Frag<T> wb = ld_frag(sWt + (16 * ns + i) * LDT + 8 * g);
-            for (int md = 0; md < 4; ++md) mma(Ut[md][ns], ld_frag(sGt + (16 * md + i) * LDT + 8 * g), wb);
+        {
+            const Frag<T> wb = ld_frag(sWt + i * LDT + 8 * g);
+            for (int md = 0; md < 4; ++md) mma(Ut[md], ld_frag(sGt + (16 * md + i) * LDT + 8 * g), wb);
             if constexpr (CAUSAL) {
-                const Frag<T> pb = ld_frag(sPkt + (16 * ns + i) * LDT + 8 * g);
-                for (int md = 0; md < 4; ++md) mma(Bt[md][ns], ld_frag(sVt + (16 * md + i) * LDT + 8 * g), pb);
+                const Frag<T> pb = ld_frag(sPkt + i * LDT + 8 * g);
+                for (int md = 0; md < 4; ++md) mma(Bt[md], ld_frag(sVt + (16 * md + i) * LDT + 8 * g), pb);
             }
         }
         if constexpr (CAUSAL) {
-            float tot[2][4];
+            float tot[4];
             tile_totals(PK, tot);
-            for (int ms = 0; ms < 2; ++ms)
-                for (int e = 0; e < 4; ++e) a0[ms][e] += (double)tot[ms][e];
+            for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
         }
         tsum += softhash_bwd_st<KB, T>(PQ, dPQ, sThQ, sw, a.L, a.inv_temp, sDproj);
         __syncthreads();
@@ -847,11 +795,9 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_reduce(Args a) {
     }
     float *out = a.rdelta + ((int64_t)n * a.nseg + seg) * SP * SROW;
     for (int md = 0; md < 4; ++md)
-        for (int ns = 0; ns < 2; ++ns)
-            for (int e = 0; e < 4; ++e) out[sidx(sw + 16 * ns + i, 16 * md + 4 * g + e)] = Ut[md][ns][e];
+        for (int e = 0; e < 4; ++e) out[sidx(sw + i, 16 * md + 4 * g + e)] = Ut[md][e];
     if (i == 0)
-        for (int ms = 0; ms < 2; ++ms)
-            for (int e = 0; e < 4; ++e) out[sidx(sw + 16 * ms + 4 * g + e, D)] = (float)al[ms][e];
+        for (int e = 0; e < 4; ++e) out[sidx(sw + 4 * g + e, D)] = (float)al[e];
     const float ts = block_sum<NTH>(tsum, sRed);
     if (threadIdx.x == 0) a.tpart[(int64_t)n * a.nseg + seg] = ts;
 }
@@ -876,9 +822,8 @@ __global__ void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int ele
 // k_bwd_out: reverse walk.  dK, dV.
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct BwdOutL {
-    static constexpr int NW_ = SP / 32;
-    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL),
-                         LDU = ld_of<T>(32);
+    static constexpr int NW_ = SP / WB;
+    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
     // region R0 = {Q, K, sigma tables}; the dV reduction reuses it once they are dead
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + (CAUSAL ? sizeof(T) * TT * LDN : 0));
@@ -891,8 +836,7 @@ template <typename T, int SP, bool CAUSAL> struct BwdOutL {
     static constexpr size_t oGt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
     static constexpr size_t oPkt = align16(oGt + (CAUSAL ? sizeof(T) * D * LDT : 0));
     static constexpr size_t oWt = align16(oPkt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
-    static constexpr size_t oUs = align16(oWt + (CAUSAL ? sizeof(T) * SP * LDT : 0));  // per wave [D][LDU]
-    static constexpr size_t oDproj = align16(oUs + sizeof(T) * NW_ * D * LDU);
+    static constexpr size_t oDproj = align16(oWt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
     static constexpr size_t oPl = align16(oDproj + sizeof(T) * TT * LDDP);
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t oPlT = align16(oPlLo + sizeof(T) * NCOL * LDN);
@@ -901,10 +845,9 @@ template <typename T, int SP, bool CAUSAL> struct BwdOutL {
 };
 
 template <typename T, int SP, bool CAUSAL, int KB>
-__global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
+__global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     using Ly = BwdOutL<T, SP, CAUSAL>;
-    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
-                  LDU = Ly::LDU;
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sV = (T *)(smem + Ly::oV);
     T *sG = (T *)(smem + Ly::oG), *sVt = (T *)(smem + Ly::oVt), *sGt = (T *)(smem + Ly::oGt);
@@ -913,9 +856,8 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
     float *sSig = (float *)(smem + Ly::oSig), *sThK = (float *)(smem + Ly::oTh);
     float *sRedV = (float *)(smem + Ly::oQ), *sRed = (float *)(smem + Ly::oRed);
     float *sSpK = sSig, *sSmK = sSig + TT * LDC, *sSpQ = sSig + 2 * TT * LDC, *sSmQ = sSig + 3 * TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = 32 * w;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
     T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT, *sWt = (T *)(smem + Ly::oWt) + sw * LDT;
-    T *sUs = (T *)(smem + Ly::oUs) + w * D * LDU;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -930,24 +872,24 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
 
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
     for (int idx = threadIdx.x; idx < TT * LDDP; idx += NTH) sDproj[idx] = from_f32<T>(0.f);
-    // reverse carries (U, alpha) after the segment; forward state at the segment end
+    // reverse carries (U, alpha) after the segment; forward state at the segment end.
+    // U is kept in both layouts: Ut (d-row) feeds dP_K, Us (bucket-row) feeds dV.
     const float *rs = a.rstate + ((int64_t)n * a.nseg + seg) * SP * SROW;
     const double *fs = a.fstate + ((int64_t)n * (a.nseg + 1) + seg + 1) * SP * SROW;
-    f32x4 Ut[4][2];  // U^T[d = 16md + 4g + e][s = sw + 16ns + i]
-    double Be[4][2][4], Ae[2][4];
-    float al[2][4];
+    f32x4 Ut[4], Us[4];  // Ut: U^T[d = 16md + 4g + e][s = sw + i]; Us: U[s = sw + 4g + e][d = 16md + i]
+    double Be[4][4], Ae[4];
+    float al[4];
     for (int md = 0; md < 4; ++md)
-        for (int ns = 0; ns < 2; ++ns)
-            for (int e = 0; e < 4; ++e) {
-                const int64_t r = sidx(sw + 16 * ns + i, 16 * md + 4 * g + e);
-                Ut[md][ns][e] = rs[r];
-                Be[md][ns][e] = CAUSAL ? fs[r] : 0.0;
-            }
-    for (int ms = 0; ms < 2; ++ms)
         for (int e = 0; e < 4; ++e) {
-            al[ms][e] = rs[sidx(sw + 16 * ms + 4 * g + e, D)];
-            Ae[ms][e] = CAUSAL ? fs[sidx(sw + 16 * ms + 4 * g + e, D)] : 0.0;
+            const int64_t r = sidx(sw + i, 16 * md + 4 * g + e);
+            Ut[md][e] = rs[r];
+            Be[md][e] = CAUSAL ? fs[r] : 0.0;
+            Us[md][e] = rs[sidx(sw + 4 * g + e, 16 * md + i)];
         }
+    for (int e = 0; e < 4; ++e) {
+        al[e] = rs[sidx(sw + 4 * g + e, D)];
+        Ae[e] = CAUSAL ? fs[sidx(sw + 4 * g + e, D)] : 0.0;
+    }
     float tsum = 0.f;
 
     Prefetch<T, NTH> pq_, pg_, pk_, pv_;
@@ -977,10 +919,6 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
                 pg_.issue(gp, a.sdo.t, t0 - TT, a.T);
             }
         }
-        // U (after this tile) in [d][s] layout for the dV contraction over s
-        for (int md = 0; md < 4; ++md)
-            for (int ns = 0; ns < 2; ++ns)
-                for (int e = 0; e < 4; ++e) sUs[(16 * md + 4 * g + e) * LDU + 16 * ns + i] = from_f32<T>(Ut[md][ns][e]);
         __syncthreads();
         for (int q = w; q < (CAUSAL ? 8 : 4); q += NW_) {
             if (q < 4)
@@ -989,77 +927,74 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
                 project_tile<T>(sQ, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
         }
         __syncthreads();
-        f32x4 PK[2][2], PKr[2][2];  // fp32 and operand-rounded
+        f32x4 PK[2], PKr[2];  // fp32 and operand-rounded
         probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
-        for (int ms = 0; ms < 2; ++ms)
-            for (int nt = 0; nt < 2; ++nt)
-                for (int e = 0; e < 4; ++e) PKr[ms][nt][e] = as_operand<T>(PK[ms][nt][e]);
-        Frag<T> PKf[2];
-        for (int nt = 0; nt < 2; ++nt) PKf[nt] = frag_acc<T>(PKr[0][nt], PKr[1][nt]);
-        f32x4 dPK[2][2];
+        for (int nt = 0; nt < 2; ++nt)
+            for (int e = 0; e < 4; ++e) PKr[nt][e] = as_operand<T>(PK[nt][e]);
+        Frag4<T> PKf[2];
+        for (int nt = 0; nt < 2; ++nt) PKf[nt] = frag16_acc<T>(PKr[nt]);
+        f32x4 dPK[2];
         if constexpr (CAUSAL) {
-            f32x4 W[2][2], inv[2][2];
+            f32x4 W[2], inv[2];
             {
-                f32x4 PQ[2][2], Acum[2][2];
+                f32x4 PQ[2], Acum[2];
                 probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
                 store_rows_T<T>(sPkt, PKr);
                 // forward state at the tile start: end state minus this tile's sums
-                float tot[2][4];
+                float tot[4];
                 tile_totals(PKr, tot);
-                for (int ms = 0; ms < 2; ++ms)
-                    for (int e = 0; e < 4; ++e) Ae[ms][e] -= (double)tot[ms][e];
+                for (int e = 0; e < 4; ++e) Ae[e] -= (double)tot[e];
                 tile_prefix(PKr, Acum);
-                for (int ms = 0; ms < 2; ++ms)
-                    for (int nt = 0; nt < 2; ++nt)
-                        for (int e = 0; e < 4; ++e) {
-                            inv[ms][nt][e] = rcp((float)Ae[ms][e] + Acum[ms][nt][e] + a.eps);
-                            W[ms][nt][e] = PQ[ms][nt][e] * inv[ms][nt][e];
-                        }
+                for (int nt = 0; nt < 2; ++nt)
+                    for (int e = 0; e < 4; ++e) {
+                        inv[nt][e] = rcp((float)Ae[e] + Acum[nt][e] + a.eps);
+                        W[nt][e] = PQ[nt][e] * inv[nt][e];
+                    }
                 store_rows_T<T>(sWt, W);
             }
-            Frag<T> Wf[2];
-            for (int nt = 0; nt < 2; ++nt) Wf[nt] = frag_acc<T>(W[0][nt], W[1][nt]);
-            __syncthreads();  // sPkt, sWt, sUs complete; sigma tables and Q/K tiles dead
+            Frag4<T> Wf[2];
+            for (int nt = 0; nt < 2; ++nt) Wf[nt] = frag16_acc<T>(W[nt]);
+            __syncthreads();  // sPkt, sWt complete; sigma tables and Q/K tiles dead
             // ---- dV^T[d][tau] = sum_s U[s][d] P_K[tau][s] + sum_{t >= tau} g[t][d] Sc2^T[t][tau]
             {
                 f32x4 Sc2[2][2];
                 for (int mt = 0; mt < 2; ++mt)
                     for (int nt = 0; nt < 2; ++nt) {
                         Sc2[mt][nt] = zero4();
-                        if (mt >= nt) mma(Sc2[mt][nt], Wf[mt], PKf[nt]);
+                        if (mt >= nt) mma16(Sc2[mt][nt], Wf[mt], PKf[nt]);
                         for (int e = 0; e < 4; ++e)
                             if (16 * mt + 4 * g + e < 16 * nt + i) Sc2[mt][nt][e] = 0.f;
                     }
                 f32x4 VT[4][2];
                 for (int md = 0; md < 4; ++md) {
-                    const Frag<T> uf = ld_frag_pi(sUs + (16 * md + i) * LDU);
+                    const Frag4<T> uf = frag16_acc<T>(Us[md]);
                     const Frag<T> gf = ld_frag_pi(sGt + (16 * md + i) * LDT);
                     for (int nt = 0; nt < 2; ++nt) {
+                        f32x4 v2 = zero4();
                         VT[md][nt] = zero4();
-                        mma(VT[md][nt], uf, PKf[nt]);
-                        mma(VT[md][nt], gf, frag_acc<T>(Sc2[0][nt], Sc2[1][nt]));
+                        mma16(VT[md][nt], uf, PKf[nt]);
+                        mma(v2, gf, frag_acc<T>(Sc2[0][nt], Sc2[1][nt]));
+                        VT[md][nt] += v2;
                     }
                 }
                 reduce_store<T, NW_>(VT, sRedV, dvp, a.sg.t, t0, a.T);
             }
             // ---- dA = -W G/(A+eps), G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] Hm[t][tau]
-            f32x4 dA[2][2];
+            f32x4 dA[2];
             {
-                f32x4 dB[4][2];
+                f32x4 dB[4];
                 tile_dBT<T>(sVt, sPkt, dB);
-                Frag<T> Bf[2][2];  // [ns][kk]
                 for (int md = 0; md < 4; ++md)
-                    for (int ns = 0; ns < 2; ++ns)
-                        for (int e = 0; e < 4; ++e) Be[md][ns][e] -= (double)dB[md][ns][e];
-                for (int ns = 0; ns < 2; ++ns)
-                    for (int kk = 0; kk < 2; ++kk) {
-                        f32x4 b0, b1;
-                        for (int e = 0; e < 4; ++e) {
-                            b0[e] = (float)Be[2 * kk][ns][e];
-                            b1[e] = (float)Be[2 * kk + 1][ns][e];
-                        }
-                        Bf[ns][kk] = frag_acc<T>(b0, b1);
+                    for (int e = 0; e < 4; ++e) Be[md][e] -= (double)dB[md][e];
+                Frag<T> Bf[2];
+                for (int kk = 0; kk < 2; ++kk) {
+                    f32x4 b0, b1;
+                    for (int e = 0; e < 4; ++e) {
+                        b0[e] = (float)Be[2 * kk][e];
+                        b1[e] = (float)Be[2 * kk + 1][e];
                     }
+                    Bf[kk] = frag_acc<T>(b0, b1);
+                }
                 f32x4 HmT[2][2];
                 for (int mt = 0; mt < 2; ++mt)
                     for (int nt = 0; nt < 2; ++nt) {
@@ -1068,23 +1003,20 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
                         for (int e = 0; e < 4; ++e)
                             if (16 * mt + 4 * g + e > 16 * nt + i) HmT[mt][nt][e] = 0.f;
                     }
+                const Frag<T> pkp = ld_frag_pi(sPkt + i * LDT);
                 for (int nt = 0; nt < 2; ++nt) {
-                    const Frag<T> hf = frag_acc<T>(HmT[0][nt], HmT[1][nt]);
-                    const Frag<T> g0 = ld_frag_pi(sG + (16 * nt + i) * LDN), g1 = ld_frag_pi(sG + (16 * nt + i) * LDN + 32);
-                    for (int ms = 0; ms < 2; ++ms) {
-                        f32x4 G = zero4();
-                        mma(G, Bf[ms][0], g0);
-                        mma(G, Bf[ms][1], g1);
-                        mma(G, ld_frag_pi(sPkt + (16 * ms + i) * LDT), hf);
-                        for (int e = 0; e < 4; ++e) dA[ms][nt][e] = -W[ms][nt][e] * G[e] * inv[ms][nt][e];
-                    }
+                    f32x4 G = zero4();
+                    mma(G, Bf[0], ld_frag_pi(sG + (16 * nt + i) * LDN));
+                    mma(G, Bf[1], ld_frag_pi(sG + (16 * nt + i) * LDN + 32));
+                    mma(G, pkp, frag_acc<T>(HmT[0][nt], HmT[1][nt]));
+                    for (int e = 0; e < 4; ++e) dA[nt][e] = -W[nt][e] * G[e] * inv[nt][e];
                 }
             }
             // ---- dP_K[tau][s] = alpha(tau) + sum_d U[s][d] v_tau[d] + sum_{t >= tau} W[t][s] Hm[t][tau]
             {
-                f32x4 alpha[2][2];
+                f32x4 alpha[2];
                 tile_suffix(dA, alpha);
-                float tot[2][4];
+                float tot[4];
                 tile_totals(dA, tot);
                 f32x4 Hm[2][2];
                 for (int mt = 0; mt < 2; ++mt)
@@ -1094,47 +1026,46 @@ __global__ __launch_bounds__(SP * 2) void k_bwd_out(Args a) {
                         for (int e = 0; e < 4; ++e)
                             if (16 * nt + i > 16 * mt + 4 * g + e) Hm[mt][nt][e] = 0.f;
                     }
+                const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
+                const Frag<T> wp = ld_frag_pi(sWt + i * LDT);
                 for (int nt = 0; nt < 2; ++nt) {
-                    const Frag<T> hf = frag_acc<T>(Hm[0][nt], Hm[1][nt]);
-                    const Frag<T> v0 = ld_frag_pi(sV + (16 * nt + i) * LDN), v1 = ld_frag_pi(sV + (16 * nt + i) * LDN + 32);
-                    for (int ms = 0; ms < 2; ++ms) {
-                        f32x4 c = zero4();
-                        mma(c, frag_acc<T>(Ut[0][ms], Ut[1][ms]), v0);
-                        mma(c, frag_acc<T>(Ut[2][ms], Ut[3][ms]), v1);
-                        mma(c, ld_frag_pi(sWt + (16 * ms + i) * LDT), hf);
-                        for (int e = 0; e < 4; ++e) dPK[ms][nt][e] = c[e] + alpha[ms][nt][e] + al[ms][e];
-                    }
+                    f32x4 c = zero4();
+                    mma(c, u0, ld_frag_pi(sV + (16 * nt + i) * LDN));
+                    mma(c, u1, ld_frag_pi(sV + (16 * nt + i) * LDN + 32));
+                    mma(c, wp, frag_acc<T>(Hm[0][nt], Hm[1][nt]));
+                    for (int e = 0; e < 4; ++e) dPK[nt][e] = c[e] + alpha[nt][e] + al[e];
                 }
-                for (int ms = 0; ms < 2; ++ms)
-                    for (int e = 0; e < 4; ++e) al[ms][e] += tot[ms][e];
+                for (int e = 0; e < 4; ++e) al[e] += tot[e];
             }
-            // ---- U^T[d][s] += sum_t g[t][d] W[t][s]
-            for (int ns = 0; ns < 2; ++ns) {
-                const Frag<T> wb = ld_frag(sWt + (16 * ns + i) * LDT + 8 * g);
-                for (int md = 0; md < 4; ++md) mma(Ut[md][ns], ld_frag(sGt + (16 * md + i) * LDT + 8 * g), wb);
+            // ---- U[s][d] += sum_t W[t][s] g[t][d], in both layouts
+            {
+                const Frag<T> wb = ld_frag(sWt + i * LDT + 8 * g);
+                for (int md = 0; md < 4; ++md) {
+                    const Frag<T> gb = ld_frag(sGt + (16 * md + i) * LDT + 8 * g);
+                    mma(Ut[md], gb, wb);
+                    mma(Us[md], wb, gb);
+                }
             }
         } else {
-            __syncthreads();  // sUs complete; sigma tables and K tile dead
+            __syncthreads();  // sigma tables and K tile dead before R0 is reused
             // non-causal: dV^T = U^T P_K^T; dP_K = alpha + v . U (totals)
             {
                 f32x4 VT[4][2];
                 for (int md = 0; md < 4; ++md) {
-                    const Frag<T> uf = ld_frag_pi(sUs + (16 * md + i) * LDU);
+                    const Frag4<T> uf = frag16_acc<T>(Us[md]);
                     for (int nt = 0; nt < 2; ++nt) {
                         VT[md][nt] = zero4();
-                        mma(VT[md][nt], uf, PKf[nt]);
+                        mma16(VT[md][nt], uf, PKf[nt]);
                     }
                 }
                 reduce_store<T, NW_>(VT, sRedV, dvp, a.sg.t, t0, a.T);
             }
+            const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
             for (int nt = 0; nt < 2; ++nt) {
-                const Frag<T> v0 = ld_frag_pi(sV + (16 * nt + i) * LDN), v1 = ld_frag_pi(sV + (16 * nt + i) * LDN + 32);
-                for (int ms = 0; ms < 2; ++ms) {
-                    f32x4 c = zero4();
-                    mma(c, frag_acc<T>(Ut[0][ms], Ut[1][ms]), v0);
-                    mma(c, frag_acc<T>(Ut[2][ms], Ut[3][ms]), v1);
-                    for (int e = 0; e < 4; ++e) dPK[ms][nt][e] = c[e] + al[ms][e];
-                }
+                f32x4 c = zero4();
+                mma(c, u0, ld_frag_pi(sV + (16 * nt + i) * LDN));
+                mma(c, u1, ld_frag_pi(sV + (16 * nt + i) * LDN + 32));
+                for (int e = 0; e < 4; ++e) dPK[nt][e] = c[e] + al[e];
             }
         }
         tsum += softhash_bwd_st<KB, T>(PK, dPK, sThK, sw, a.L, a.inv_temp, sDproj);

@@ -85,3 +85,37 @@ extern "C" int probe_chain(int bf16, const void *A, const void *Bm, const void *
         k_probe_chain<float><<<1, 64>>>((const float *)A, (const float *)Bm, (const float *)E, D, Dt);
     return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
 }
+
+// 16-deep chained product: X = A . Bm^T (16 x 16, one tile) kept in registers,
+// D = E . X with X as the B operand (k = row of X) and E read with ld_frag16.
+template <typename T>
+__global__ __launch_bounds__(64) void k_probe_chain16(const T *A, const T *Bm, const T *E, float *Dout, float *Dtout) {
+    constexpr int LD = ld_of<T>(64), LDE = ld_of<T>(16);
+    __shared__ __align__(16) T sA[16 * LD], sB[16 * LD], sE[16 * LDE];
+    for (int idx = threadIdx.x; idx < 16 * 64; idx += 64) {
+        sA[(idx / 64) * LD + idx % 64] = A[idx];
+        sB[(idx / 64) * LD + idx % 64] = Bm[idx];
+    }
+    for (int idx = threadIdx.x; idx < 16 * 16; idx += 64) sE[(idx / 16) * LDE + idx % 16] = E[idx];
+    __syncthreads();
+    f32x4 x = zero4();
+    tile_mma(x, sA, LD, sB, LD, 2);
+    const Frag4<T> xf = frag16_acc<T>(x);
+    const int i = lane_id() & 15, g = lane_id() >> 4;
+    const Frag4<T> ef = ld_frag16(sE + i * LDE);
+    f32x4 d = zero4(), dt = zero4();
+    mma16(d, ef, xf);
+    mma16(dt, xf, ef);
+    for (int e = 0; e < 4; ++e) {
+        Dout[(4 * g + e) * 16 + i] = d[e];
+        Dtout[(4 * g + e) * 16 + i] = dt[e];
+    }
+}
+
+extern "C" int probe_chain16(int bf16, const void *A, const void *Bm, const void *E, float *D, float *Dt) {
+    if (bf16)
+        k_probe_chain16<race::bf16><<<1, 64>>>((const race::bf16 *)A, (const race::bf16 *)Bm, (const race::bf16 *)E, D, Dt);
+    else
+        k_probe_chain16<float><<<1, 64>>>((const float *)A, (const float *)Bm, (const float *)E, D, Dt);
+    return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}

@@ -29,7 +29,28 @@ def _probe_lib():
     lib.probe_mfma.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5
     lib.probe_rows.argtypes = [ctypes.c_void_p] * 2
     lib.probe_chain.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5
+    lib.probe_chain16.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5
     return lib
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_mfma_chain16(dev, dtype):
+    """One accumulator tile reused as a 16-deep operand (16x16x16 MFMA)."""
+    lib = _probe_lib()
+    g = torch.Generator().manual_seed(4)
+    A = torch.randn(16, 64, generator=g).to(dtype)
+    Bm = torch.randn(16, 64, generator=g).to(dtype)
+    E = torch.randn(16, 16, generator=g).to(dtype)
+    D, Dt = torch.zeros(16, 16, device=dev), torch.zeros(16, 16, device=dev)
+    assert lib.probe_chain16(int(dtype == torch.bfloat16), A.to(dev).data_ptr(), Bm.to(dev).data_ptr(),
+                             E.to(dev).data_ptr(), D.data_ptr(), Dt.data_ptr()) == 0
+    X = A.double() @ Bm.double().T
+    if dtype == torch.bfloat16:
+        X = X.to(torch.bfloat16).double()
+    ref = E.double() @ X
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert relerr(D.cpu(), ref) < tol
+    assert relerr(Dt.cpu(), ref.T) < tol
 
 
 def test_dpp_row_scans(dev):
