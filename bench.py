@@ -17,6 +17,11 @@ path (aten + kernels/cpu/race_pref.cpp compiled from source) on a bounded
 sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--seq N] [--no-cpu-baseline] [--max-n]
+                    [--copy-calib MIB]
+
+--copy-calib MIB ends the run with one device-to-device copy of MIB MiB, the
+known-size kernel against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters
+are scaled when the HBM traffic of the operator's kernels is measured.
 """
 from __future__ import annotations
 
@@ -48,8 +53,10 @@ def parse():
     ap.add_argument("--seq", type=int, default=1 << 20, help="tokens per sequence (default 2^20)")
     ap.add_argument("--heads", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=65536, help="tokens of one head timed on the CPU")
+    ap.add_argument("--cpu-sample", type=int, default=65536, help="tokens of one head per timed CPU run")
     ap.add_argument("--max-n", action="store_true", help="also bisect the longest sequence that fits in HBM")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="finish with a device-to-device copy of MIB MiB (PMC calibration)")
     return ap.parse_args()
 
 
@@ -122,67 +129,78 @@ def algorithmic_bytes(name, tok_heads, D, esize):
     return {"fwd_reduce": 2, "fwd_out": 4, "bwd_reduce": 5, "bwd_out": 6}.get(name, 0) * unit
 
 
-def cpu_baseline(sample_T, H_full, D=64, L=8, K=4, reps=3):
+def cpu_baseline(sample_T, H_full, D=64, L=8, K=4, reps=16):
     """Reference CPU path (aten + race_pref.cpp from source) on one head of
-    sample_T tokens of the same workload; reported as tokens/s of the full
-    H-head layer.  Falls back to the fp64 C restatement if oracle/_ref is absent."""
+    sample_T tokens of the same workload, run reps times (default 16 x 65536
+    tokens = 2^20 token-heads, about 12 s on 16 host threads; the reference's
+    flat layout copies V once per bucket, about 128 KB of host memory per
+    token, which bounds one run's length); the median run is reported as
+    tokens/s of the full H-head layer.  Falls back to the fp64 C restatement
+    if oracle/_ref is absent."""
     import torch
     from oracle import race_oracle
-    q, k, v, do, planes = make_inputs(1, sample_T, 1, D, L, K, "cpu", seed=7)
     threads = torch.get_num_threads()
     ext = race_oracle.ref_race_pref()
     times = []
     if ext is not None:
         from oracle import ref_cpu_path
-        planes_T = planes[0].reshape(L * K, D).T.contiguous().float()
-        Kf, Vf, Qf = [x.float().requires_grad_(True) for x in (k, v, q)]
-        for r in range(reps + 1):
-            for x in (Kf, Vf, Qf):
-                x.grad = None
+
+        def run(T, seed):
+            q, k, v, do, planes = make_inputs(1, T, 1, D, L, K, "cpu", seed=seed)
+            planes_T = planes[0].reshape(L * K, D).T.contiguous().float()
+            Kf, Vf, Qf = [x.float().requires_grad_(True) for x in (k, v, q)]
+            dof = do.float()
             t0 = time.perf_counter()
             out = ref_cpu_path.causal_forward(Kf, Vf, Qf, planes_T, K, L, ext=ext)
-            out.backward(do.float())
-            if r > 0:
-                times.append(time.perf_counter() - t0)
+            out.backward(dof)
+            return time.perf_counter() - t0
+
+        run(8192, 6)  # warm-up: thread pool, allocator
+        times = [run(sample_T, 7 + r) for r in range(reps)]
         kind = "reference"
         what = "misc/race.py CPU path: aten projection/softmax/readout + kernels/cpu/race_pref.cpp (built from source)"
     else:
         from oracle import race_oracle as ro
-        import numpy as np
+        q, k, v, do, planes = make_inputs(1, sample_T, 1, D, L, K, "cpu", seed=7)
         arrs = [x.double().numpy() for x in (q, k, v, do)]
         pl = planes.double().numpy()
-        for r in range(reps + 1):
+        for _ in range(reps):
             t0 = time.perf_counter()
             ro.race_forward(arrs[0], arrs[1], arrs[2], pl, causal=True, inv_temp=1 / math.sqrt(D))
             ro.race_backward(*arrs, pl, causal=True, inv_temp=1 / math.sqrt(D))
-            if r > 0:
-                times.append(time.perf_counter() - t0)
+            times.append(time.perf_counter() - t0)
         kind = "port"
         what = "fp64 C restatement (oracle/race_oracle.c), one thread per stream"
         threads = 1
     t = statistics.median(times)
     return {"value": sample_T / t / H_full, "unit": "tokens/s", "cores": threads, "kind": kind,
             "sample": f"1 of {H_full} heads x {sample_T} tokens of the same causal K=4 L=8 d=64 workload, "
-                      f"fwd+bwd, median of {reps} after 1 warm-up ({what}); {t:.2f} s per sample; "
+                      f"fwd+bwd, median of {reps} runs after a warm-up ({what}); {t:.2f} s per run; "
                       f"value scaled to tokens of the {H_full}-head layer",
-            "host_cpus": os.cpu_count()}
+            "host_cpus": os.cpu_count(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
 
 def max_seq_bisect(H, D, L, K, dev, limit_tokens=1 << 27):
-    """Longest T (multiple of 2^16) whose full fwd+bwd buffers fit and run."""
+    """Longest T (multiple of 2^16) for which one layer's fwd+bwd fits in HBM:
+    separate Q, K, V, dO inputs, O, dQ, dK, dV outputs, the forward state and
+    the workspace, all allocated and the step run once."""
     import torch
 
     def fits(T):
+        bufs = None
         try:
-            q = torch.empty(1, 1, T, H, D, dtype=torch.bfloat16, device=dev).normal_()
-            st = Step(q, q, q, q, torch.randn(1, L, K, D, device=dev), L, K)
+            bufs = [torch.empty(1, 1, T, H, D, dtype=torch.bfloat16, device=dev) for _ in range(4)]
+            for b in bufs:
+                b.normal_()
+            st = Step(*bufs, torch.randn(1, L, K, D, device=dev), L, K)
             st.run()
             torch.cuda.synchronize()
-            del st, q
+            del st
             return True
         except (torch.cuda.OutOfMemoryError, RuntimeError):
             return False
         finally:
+            del bufs
             torch.cuda.empty_cache()
 
     lo, hi = 1 << 20, None
@@ -265,6 +283,14 @@ def main():
                            "frac": round(value / (tokens / (all_bytes / (HBM_PEAK_GBS * 1e9))), 4)},
         "kernels": kernels,
     }
+    if args.copy_calib:
+        n = args.copy_calib << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        res["copy_calib_bytes"] = n
+        del src, dst
     if args.max_n:
         del step, q, k, v, do
         torch.cuda.empty_cache()

@@ -25,3 +25,11 @@ def oracle():
     from oracle import race_oracle
     race_oracle._lib()
     return race_oracle
+
+
+@pytest.fixture(scope="session")
+def dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm device")
+    return torch.device("cuda:0")

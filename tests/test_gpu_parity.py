@@ -17,13 +17,6 @@ pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
-@pytest.fixture(scope="module")
-def dev():
-    if not torch.cuda.is_available():
-        pytest.fail("GPU tests need a ROCm device")
-    return torch.device("cuda:0")
-
-
 def _probe_lib():
     lib = ctypes.CDLL(os.path.join(HERE, "hip", "libmfma_probe.so"))
     lib.probe_mfma.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5
