@@ -14,6 +14,12 @@ from helpers import TOL, relerr
 pytestmark = pytest.mark.gpu
 
 
+def _planes4(planes):
+    """[L,K,D] (shared) or [M,L,K,D] -> the oracle's [NP,L,K,D] fp64."""
+    p = planes.detach().double()
+    return (p.unsqueeze(0) if p.dim() == 3 else p).numpy()
+
+
 class OracleRACE(torch.autograd.Function):
     """race_attention's contract on CPU fp64, computed by the oracle."""
 
@@ -22,7 +28,7 @@ class OracleRACE(torch.autograd.Function):
         from oracle import race_oracle as ro
         it = float(inv_temp)
         arr = [x.detach().double().contiguous().numpy() for x in (Q, K, V)]
-        pl = planes.detach().double().numpy()
+        pl = _planes4(planes)
         out = ro.race_forward(*arr, pl, causal=causal, eps=eps, inv_temp=it)
         ctx.save_for_backward(Q, K, V, planes)
         ctx.cfg = (causal, eps, it, torch.is_tensor(inv_temp))
@@ -34,8 +40,7 @@ class OracleRACE(torch.autograd.Function):
         Q, K, V, planes = ctx.saved_tensors
         causal, eps, it, temp_tensor = ctx.cfg
         arr = [x.detach().double().contiguous().numpy() for x in (Q, K, V, g)]
-        dq, dk, dv, git = ro.race_backward(*arr, planes.detach().double().numpy(), causal=causal, eps=eps,
-                                           inv_temp=it)
+        dq, dk, dv, git = ro.race_backward(*arr, _planes4(planes), causal=causal, eps=eps, inv_temp=it)
         gt = torch.tensor(git, dtype=torch.float64) if temp_tensor else None
         return (torch.from_numpy(dq), torch.from_numpy(dk), torch.from_numpy(dv), None, gt,
                 None, None, None, None)
