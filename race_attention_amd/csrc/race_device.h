@@ -165,22 +165,23 @@ __device__ __forceinline__ Frag<float> ld_frag_pi(const float *p) {
     return f;
 }
 
-// 16-deep k step: lane (g, i) holds k = 4g..4g+3 of row/column i
-// (v_mfma_f32_16x16x16_bf16; fp32: four 16x16x4 steps).  One accumulator tile
-// (lane holds X[4g + e][i]) is directly such an operand over its 16 rows.
-typedef short s16x4 __attribute__((ext_vector_type(4)));
+// 16-deep k step: lane (g, i) holds k = 4g..4g+3 of row/column i, so one
+// accumulator tile (lane holds X[4g + e][i]) is directly such an operand over
+// its 16 rows.  bf16 runs it as a 16x16x32 product whose k slots 4..7 of each
+// lane are zero (the same instruction as every other bf16 product, so partial
+// sums of both depths chain in one accumulator); fp32 runs four 16x16x4 steps.
 template <typename T> struct Frag4;
-template <> struct Frag4<bf16> { s16x4 v; };
+template <> struct Frag4<bf16> { bf16x8 v; };
 template <> struct Frag4<float> { f32x4 v; };
 
 template <typename T> __device__ __forceinline__ Frag4<T> frag16_acc(const f32x4 &x);
 template <> __device__ __forceinline__ Frag4<bf16> frag16_acc<bf16>(const f32x4 &x) {
-    typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
-    bf16x4 b;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = (bf16)x[j];
     Frag4<bf16> f;
-    f.v = __builtin_bit_cast(s16x4, b);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f.v[j] = (bf16)x[j];
+        f.v[j + 4] = (bf16)0.f;
+    }
     return f;
 }
 template <> __device__ __forceinline__ Frag4<float> frag16_acc<float>(const f32x4 &x) {
@@ -190,8 +191,14 @@ template <> __device__ __forceinline__ Frag4<float> frag16_acc<float>(const f32x
 }
 // p[4g..4g+3]
 __device__ __forceinline__ Frag4<bf16> ld_frag16(const bf16 *p) {
+    typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    const bf16x4 a = *reinterpret_cast<const bf16x4 *>(p + 4 * (lane_id() >> 4));
     Frag4<bf16> f;
-    f.v = *reinterpret_cast<const s16x4 *>(p + 4 * (lane_id() >> 4));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f.v[j] = a[j];
+        f.v[j + 4] = (bf16)0.f;
+    }
     return f;
 }
 __device__ __forceinline__ Frag4<float> ld_frag16(const float *p) {
@@ -199,16 +206,36 @@ __device__ __forceinline__ Frag4<float> ld_frag16(const float *p) {
     f.v = *reinterpret_cast<const f32x4 *>(p + 4 * (lane_id() >> 4));
     return f;
 }
-// The accumulator of a 16x16x16 bf16 product is never passed as SrcC of a
-// 16x16x32 product (or the reverse): the compiler may issue such a pair back
-// to back without wait states, and on gfx950 the second product then reads a
-// stale accumulator.  Mixed-depth sums use separate accumulators added on VALU.
+// v_mfma_f32_16x16x16_bf16 is not used: the compiler may issue it and a
+// following 16x16x32 product that reads its accumulator as SrcC back to back
+// with no wait states, and on gfx950 the second product then reads a stale
+// accumulator.
 __device__ __forceinline__ void mma16(f32x4 &c, const Frag4<bf16> &a, const Frag4<bf16> &b) {
-    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.v, b.v, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, c, 0, 0, 0);
 }
 __device__ __forceinline__ void mma16(f32x4 &c, const Frag4<float> &a, const Frag4<float> &b) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[e], b.v[e], c, 0, 0, 0);
+}
+
+// fp64 -> fp32 as its own rounding step (kept from being fused with a
+// following fp32 -> bf16 conversion into a double -> bf16 one, which the
+// compiler expands into a multi-instruction round-to-odd sequence)
+__device__ __forceinline__ float narrow(double x) {
+    float f = (float)x;
+    asm volatile("" : "+v"(f));
+    return f;
+}
+
+// ------------------------------------------------------------ cross-row sums
+// x + x[lane ^ 16] and x + x[lane ^ 32] with the gfx950 row/half swaps
+__device__ __forceinline__ float xor16_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // ------------------------------------------------------------ row (16-lane) ops
@@ -242,13 +269,19 @@ __device__ __forceinline__ float row_sum(float x) {
 }
 
 // ------------------------------------------------------------ sigmoids
-// stable pair (sigmoid(x), sigmoid(-x))
+__device__ __forceinline__ float rcp_f(float x) { return __builtin_amdgcn_rcpf(x); }
+// stable pair (sigmoid(x), sigmoid(-x)) from one exp and one reciprocal
 __device__ __forceinline__ void sigmoid_pair(float x, float &sp, float &sm) {
     const float e = __expf(-fabsf(x));
-    const float p = 1.0f / (1.0f + e);
+    const float p = rcp_f(1.0f + e);
     const float q = e * p;
     sp = x >= 0.f ? p : q;
     sm = x >= 0.f ? q : p;
+}
+// tanh(x) = sign(x) (1 - e) / (1 + e), e = exp(-2|x|); absolute error ~1e-7
+__device__ __forceinline__ float tanh_fast(float x) {
+    const float e = __expf(-2.f * fabsf(x));
+    return copysignf((1.f - e) * rcp_f(1.f + e), x);
 }
 
 } // namespace race

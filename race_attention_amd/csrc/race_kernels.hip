@@ -151,7 +151,7 @@ __device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mc, in
     f32x4 a, b, th;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        th[e] = tanhf(acc[e]);
+        th[e] = tanh_fast(acc[e]);
         float x, y;
         sigmoid_pair(2.f * th[e] * inv_temp, x, y);
         a[e] = x;
@@ -211,8 +211,8 @@ __device__ __forceinline__ void probs_st(const float *sp, const float *sm, int s
 // sum over the buckets of one table that share this lane's token: in-lane
 // over e (pairs for KB = 1) and across rows g for KB >= 3
 template <int KB> __device__ __forceinline__ float table_reduce(float x) {
-    if constexpr (KB >= 3) x += __shfl_xor(x, 16, 64);
-    if constexpr (KB >= 4) x += __shfl_xor(x, 32, 64);
+    if constexpr (KB >= 3) x = xor16_sum(x);
+    if constexpr (KB >= 4) x = xor32_sum(x);
     return x;
 }
 
@@ -611,14 +611,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_out(Args a) {
             tile_totals(PK, tot);
             for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
             __syncthreads();  // sPkt complete; sigma tables and Q/K tiles dead before R0 is reused
-            // O2^T[d][t] = sum_t' V[t'][d] Sc^T[t'][t] (own accumulator: see mma16)
+            // O2^T[d][t] = sum_t' V[t'][d] Sc^T[t'][t]
             for (int nt = 0; nt < 2; ++nt) {
                 const Frag<T> sf = frag_acc<T>(Sc[0][nt], Sc[1][nt]);
-                for (int md = 0; md < 4; ++md) {
-                    f32x4 o2 = zero4();
-                    mma(o2, ld_frag_pi(sVt + (16 * md + i) * LDT), sf);
-                    O[md][nt] += o2;
-                }
+                for (int md = 0; md < 4; ++md) mma(O[md][nt], ld_frag_pi(sVt + (16 * md + i) * LDT), sf);
             }
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
             const Frag<T> pa = ld_frag(sPkt + i * LDT + 8 * g);
@@ -970,11 +966,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                     const Frag4<T> uf = frag16_acc<T>(Us[md]);
                     const Frag<T> gf = ld_frag_pi(sGt + (16 * md + i) * LDT);
                     for (int nt = 0; nt < 2; ++nt) {
-                        f32x4 v2 = zero4();
                         VT[md][nt] = zero4();
                         mma16(VT[md][nt], uf, PKf[nt]);
-                        mma(v2, gf, frag_acc<T>(Sc2[0][nt], Sc2[1][nt]));
-                        VT[md][nt] += v2;
+                        mma(VT[md][nt], gf, frag_acc<T>(Sc2[0][nt], Sc2[1][nt]));
                     }
                 }
                 reduce_store<T, NW_>(VT, sRedV, dvp, a.sg.t, t0, a.T);
@@ -990,8 +984,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 for (int kk = 0; kk < 2; ++kk) {
                     f32x4 b0, b1;
                     for (int e = 0; e < 4; ++e) {
-                        b0[e] = (float)Be[2 * kk][e];
-                        b1[e] = (float)Be[2 * kk + 1][e];
+                        b0[e] = narrow(Be[2 * kk][e]);
+                        b1[e] = narrow(Be[2 * kk + 1][e]);
                     }
                     Bf[kk] = frag_acc<T>(b0, b1);
                 }

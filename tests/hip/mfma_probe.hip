@@ -119,3 +119,16 @@ extern "C" int probe_chain16(int bf16, const void *A, const void *Bm, const void
         k_probe_chain16<float><<<1, 64>>>((const float *)A, (const float *)Bm, (const float *)E, D, Dt);
     return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
 }
+
+// cross-row sums with the gfx950 permlane swaps: out[0:64] = x + x[l^16],
+// out[64:128] = x + x[l^32]
+__global__ __launch_bounds__(64) void k_probe_xor(const float *x, float *out) {
+    const float v = x[threadIdx.x];
+    out[threadIdx.x] = xor16_sum(v);
+    out[64 + threadIdx.x] = xor32_sum(v);
+}
+
+extern "C" int probe_xor(const float *x, float *out) {
+    k_probe_xor<<<1, 64>>>(x, out);
+    return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}

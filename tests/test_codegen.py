@@ -4,9 +4,9 @@ The compiler issues a 16x16x16 bf16 MFMA and a following 16x16x32 bf16 MFMA
 that reads the first one's accumulator as SrcC back to back, with no wait
 states; on gfx950 the second product then reads a stale accumulator (measured
 on MI355X: 0.74 relative error back to back, exact with s_nop padding between
-the two).  The kernels keep mixed-depth sums in separate accumulators; this
-test fails if any kernel in the built assembly chains the two forms through
-SrcC.
+the two).  The kernels therefore run 16-deep bf16 products as zero-padded
+16x16x32 products; this test fails if any kernel in the built assembly
+contains the 16x16x16 form or chains two different depths through SrcC.
 """
 import os
 import re
@@ -66,6 +66,7 @@ def test_no_mixed_depth_srcc_chain(tmp_path):
                            os.path.join(ROOT, "race_attention_amd", "csrc", "race_capi.hip"), "-o", str(out)],
                           stderr=subprocess.DEVNULL)
     asm = out.read_text()
-    assert "v_mfma_f32_16x16x16_bf16" in asm
+    assert "v_mfma_f32_16x16x32_bf16" in asm
+    assert "v_mfma_f32_16x16x16_bf16" not in asm
     bad = mixed_srcc_chains(asm)
     assert not bad, bad[:5]

@@ -23,7 +23,20 @@ def _probe_lib():
     lib.probe_rows.argtypes = [ctypes.c_void_p] * 2
     lib.probe_chain.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5
     lib.probe_chain16.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5
+    lib.probe_xor.argtypes = [ctypes.c_void_p] * 2
     return lib
+
+
+def test_permlane_xor_sums(dev):
+    """xor16_sum / xor32_sum (v_permlane16/32_swap) equal x + x[lane^16|32]."""
+    lib = _probe_lib()
+    x = torch.randn(64, generator=torch.Generator().manual_seed(9)).to(dev)
+    out = torch.zeros(128, device=dev)
+    assert lib.probe_xor(x.data_ptr(), out.data_ptr()) == 0
+    xc = x.cpu()
+    idx = torch.arange(64)
+    assert torch.allclose(out[:64].cpu(), xc + xc[idx ^ 16], atol=1e-6)
+    assert torch.allclose(out[64:].cpu(), xc + xc[idx ^ 32], atol=1e-6)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
