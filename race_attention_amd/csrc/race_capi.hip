@@ -110,6 +110,8 @@ int check_tensor(const char *name, const void *ptr, const int64_t *st, size_t es
     }
     if (T > 1 && st[2] < D)
         return fail(RACE_E_INVALID, "%s token stride %lld overlaps rows", name, (long long)st[2]);
+    if (st[2] >= (int64_t(1) << 26))  // lane offsets within a 32-token tile are 32-bit
+        return fail(RACE_E_UNSUPPORTED, "%s token stride %lld exceeds 2^26 elements", name, (long long)st[2]);
     return RACE_OK;
 }
 

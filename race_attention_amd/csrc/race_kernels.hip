@@ -18,15 +18,19 @@
 // operator runs the same kernels with full-sequence sums and no triangles.
 //
 // Inside a workgroup wave w owns buckets [16w, 16w+16): the workgroup has
-// SP/16 waves.  Per-bucket quantities live in the "bucket-row" accumulator
-// layout (lane (g,i) holds row s = 16w + 4g + e, column t = 16nt + i of a
-// [bucket x token] matrix), where prefix/suffix sums over tokens are 16-lane
-// DPP row scans and the 16 buckets of the wave form one 16-deep MFMA k step,
-// so accumulator tiles feed the next MFMA directly (frag16_acc); token
-// contractions pair two accumulator tiles into a 32-deep step (frag_acc /
-// ld_frag_pi).
-// Token contractions read the transposed operand from LDS.  The triangle of a
-// tile is a masked 32x32 product: O = W B_start + tril(W P_K^T) V.
+// SP/16 waves.  Per-bucket elementwise work (probabilities, W = P_Q/(A+eps),
+// dA, the softmax backward) runs in the "bucket-row" accumulator layout: lane
+// (g,i) holds bucket s = 16w + 4g + e and token t = 16nt + i.  Contractions
+// over the wave's 16 buckets take such tiles directly as 16-deep MFMA
+// operands.  Contractions over tokens need the token index in k: each tile is
+// transposed on the matrix core (identity product) and a tile pair forms a
+// 32-deep operand (frag_acc, pi order); token prefix sums and totals are the
+// same operand against constant triangular / all-ones operands.  Sums over
+// ALL buckets (the outputs O and dV) are computed as output tiles, one per
+// wave, from [.][s] LDS arrays to which every wave writes its buckets' W,
+// P_K and carry rows; the v.g triangle of the tile is built once per
+// workgroup.  Within a tile the causal triangle is a masked 32x32 product:
+// O = W B_start + tril(W P_K^T) V.
 //
 // Bucket probabilities are recomputed in every kernel: projection on MFMA,
 // tanh, then P[t, l, r] = prod_k sigmoid(+-2 u_k), which equals the
@@ -98,12 +102,16 @@ template <typename T, int NTH> struct Prefetch {
     static constexpr int EPC = 16 / sizeof(T), CPR = D / EPC, CHUNKS = TT * CPR;
     static constexpr int PER = (CHUNKS + NTH - 1) / NTH;
     uint4 v[PER];
+    // tile base src + t0 * st is uniform; the lane offset t * st + c * EPC is
+    // 32-bit (the host bounds 32 * token stride below 2^31)
     __device__ __forceinline__ void issue(const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn) {
+        const T *base = src + t0 * st;
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int idx = threadIdx.x + j * NTH, t = idx / CPR, c = idx % CPR;
             v[j] = make_uint4(0, 0, 0, 0);
-            if (idx < CHUNKS && t0 + t < Tn) v[j] = *reinterpret_cast<const uint4 *>(src + (t0 + t) * st + c * EPC);
+            const uint32_t off = (uint32_t)t * (uint32_t)st + (uint32_t)(c * EPC);
+            if (idx < CHUNKS && t0 + t < Tn) v[j] = *reinterpret_cast<const uint4 *>(base + off);
         }
     }
     __device__ __forceinline__ void commit(T *nat, T *trn) const {
@@ -303,28 +311,116 @@ __device__ __forceinline__ void tile_suffix(const f32x4 (&X)[2], f32x4 (&Y)[2]) 
     }
 }
 
-// bucket-row values -> per-wave transposed LDS [16 s][ld_of<T>(TT)] (rows s, columns t)
-template <typename T> __device__ __forceinline__ void store_rows_T(T *dst, const f32x4 (&X)[2]) {
-    constexpr int LDT = ld_of<T>(TT);
-    const int g = lg(), i = li();
+// ------------------------------------------------------------ constant operands
+// Operand slots in the pi order of frag_acc: slot j < 4 is row 4g + j, slot
+// 4 + j is row 16 + 4g + j of a 32-row operand.
+template <typename T> __device__ __forceinline__ Frag<T> frag_pi_from(const float (&v)[8]);
+template <> __device__ __forceinline__ Frag<bf16> frag_pi_from<bf16>(const float (&v)[8]) {
+    Frag<bf16> f;
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int j = 0; j < 8; ++j) f.v[j] = (bf16)v[j];
+    return f;
+}
+template <> __device__ __forceinline__ Frag<float> frag_pi_from<float>(const float (&v)[8]) {
+    Frag<float> f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) dst[(4 * g + e) * LDT + 16 * nt + i] = from_f32<T>(X[nt][e]);
+    for (int j = 0; j < 4; ++j) {
+        f.lo[j] = v[j];
+        f.hi[j] = v[4 + j];
+    }
+    return f;
 }
 
-// d-row tile sums dB^T = V^T P_K for the wave's buckets (fp32 MFMA from zero):
-// out[md] lane holds dB^T[d = 16md + 4g + e][s = sw + i]
+// B operands that turn token contractions into prefix sums, totals and
+// transposes on the matrix cores, read from small LDS tables:
+//   tri[t][tau] = (tau <= t): column t = 16nt + i of the prefix (row 31 is
+//                 all ones: token totals, replicated over the columns)
+//   id[s][s']   = (s == s'): 16-deep identity for transposes
+template <typename T> struct Consts {
+    static constexpr int LDT = ld_of<T>(TT), LDI = ld_of<T>(16);
+    static constexpr size_t bytes = sizeof(T) * (TT * LDT + 16 * LDI);
+    const T *tri, *id;
+    __device__ __forceinline__ void init(T *buf, int nth) {
+        T *t = buf, *d = buf + TT * LDT;
+        for (int idx = threadIdx.x; idx < TT * LDT; idx += nth)
+            t[idx] = from_f32<T>(idx % LDT <= idx / LDT ? 1.f : 0.f);
+        for (int idx = threadIdx.x; idx < 16 * LDI; idx += nth)
+            d[idx] = from_f32<T>(idx % LDI == idx / LDI ? 1.f : 0.f);
+        tri = t;
+        id = d;
+    }
+    __device__ __forceinline__ Frag<T> tri_op(int nt) const { return ld_frag_pi(tri + (16 * nt + li()) * LDT); }
+    __device__ __forceinline__ Frag<T> ones() const { return ld_frag_pi(tri + (TT - 1) * LDT); }
+    __device__ __forceinline__ Frag4<T> ident() const { return ld_frag16(id + li() * LDI); }
+};
+
+// Token-direction operand of the wave's bucket-row tiles X[2] (lane holds
+// X[s = 4g + e][t = 16nt + i]): each tile is transposed on the matrix core
+// (identity product; exact for operand-rounded values) into token-row
+// layout, and the pair forms the operand with row s and k = t (pi order).
+template <typename T> __device__ __forceinline__ Frag<T> token_operand(const f32x4 (&X)[2], const Consts<T> &cst) {
+    const Frag4<T> ident = cst.ident();
+    f32x4 r0 = zero4(), r1 = zero4();
+    mma16(r0, frag16_acc<T>(X[0]), ident);
+    mma16(r1, frag16_acc<T>(X[1]), ident);
+    return frag_acc<T>(r0, r1);
+}
+
+// bucket-row tiles -> [t][s] LDS array (s contiguous, leading dimension ld):
+// each lane writes its 4 consecutive buckets of one token
+template <typename T> __device__ __forceinline__ void store_ts(T *dst, int ld, int sw, const f32x4 (&X)[2]) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) store4<T>(dst + (16 * nt + li()) * ld + sw + 4 * lg(), X[nt]);
+}
+// bucket-row [s][d] carry (lane holds [s = sw + 4g + e][d = 16md + i]) ->
+// [d][s] LDS array (s contiguous)
+template <typename T> __device__ __forceinline__ void store_ds(T *dst, int ld, int sw, const f32x4 (&X)[4]) {
+#pragma unroll
+    for (int md = 0; md < 4; ++md) store4<T>(dst + (16 * md + li()) * ld + sw + 4 * lg(), X[md]);
+}
+
+// d-row U^T (lane holds U^T[d = 16md + 4g + e][s = sw + i]) -> [d][s] LDS
+// array, each 16x16 block transposed on the matrix core into bucket-row
+// layout (lane: [s = sw + 4g + e][d = 16md + i]) for 4-bucket stores
 template <typename T>
-__device__ __forceinline__ void tile_dBT(const T *vt, const T *pkt, f32x4 (&out)[4]) {
-    constexpr int LDT = ld_of<T>(TT);
-    const int g = lg(), i = li();
-    const Frag<T> b = ld_frag(pkt + i * LDT + 8 * g);
+__device__ __forceinline__ void store_ut(T *dst, int ld, int sw, const f32x4 (&Ut)[4], const Consts<T> &cst) {
+    const Frag4<T> ident = cst.ident();
+    f32x4 Us[4];
 #pragma unroll
     for (int md = 0; md < 4; ++md) {
-        out[md] = zero4();
-        mma(out[md], ld_frag(vt + (16 * md + i) * LDT + 8 * g), b);
+        Us[md] = zero4();
+        mma16(Us[md], frag16_acc<T>(Ut[md]), ident);
     }
+    store_ds<T>(dst, ld, sw, Us);
+}
+
+// M[tau][t] = v_tau . g_t for tau <= t, 0 above the diagonal, for the tile's
+// causal triangle.  Task q < 3 writes tile q of X[t][tau] (rows t, the G
+// term's operand), q >= 3 tile q - 3 of Y[tau][t] (rows tau, the dP_K term's);
+// tiles (mt, nt) = (0,0), (0,1), (1,1); the all-zero tile (1,0) is cleared
+// once at kernel start.
+template <typename T> __device__ void m_tile(int q, const T *sV, const T *sG, T *X, T *Y) {
+    constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT);
+    const int g = lg(), i = li();
+    const int r = q % 3, mt = r == 2 ? 1 : 0, nt = r == 0 ? 0 : 1;
+    f32x4 acc = zero4();
+    if (q < 3) {
+        tile_mma(acc, sV + 16 * mt * LDN, LDN, sG + 16 * nt * LDN, LDN, D / 32);  // [tau = 16mt+4g+e][t = 16nt+i]
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (16 * mt + 4 * g + e > 16 * nt + i) acc[e] = 0.f;
+        store4<T>(X + (16 * nt + i) * LDT + 16 * mt + 4 * g, acc);
+    } else {
+        tile_mma(acc, sG + 16 * nt * LDN, LDN, sV + 16 * mt * LDN, LDN, D / 32);  // [t = 16nt+4g+e][tau = 16mt+i]
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (16 * mt + i > 16 * nt + 4 * g + e) acc[e] = 0.f;
+        store4<T>(Y + (16 * mt + i) * LDT + 16 * nt + 4 * g, acc);
+    }
+}
+
+template <typename T> __device__ void zero_lds(T *p, int n, int nth) {
+    for (int idx = threadIdx.x; idx < n; idx += nth) p[idx] = from_f32<T>(0.f);
 }
 
 // dX for the tile: dX^T = planes^T dproj^T, 8 tiles over the workgroup's waves,
@@ -338,42 +434,7 @@ __device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64
         f32x4 acc = zero4();
         tile_mma(acc, plt + 16 * md * LDDP, LDDP, dproj + 16 * nt * LDDP, LDDP, NCOL / 32);
         const int t = 16 * nt + i;
-        if (t0 + t < Tn) store4<T>(dst + (t0 + t) * st + 16 * md + 4 * g, acc);
-    }
-}
-
-// Output tiles part[md][nt] (lane holds X^T[d = 16md + 4g + e][t = 16nt + i],
-// this wave's partial over its buckets): sum over the waves and store rows t.
-// With several waves the partials go through red ([NW][TT][ld_of<float>(32)]
-// fp32, RED_BYTES), one half of d at a time; red must be free on entry.
-template <int NW_> constexpr size_t red_bytes() { return NW_ > 1 ? sizeof(float) * NW_ * TT * ld_of<float>(32) : 0; }
-
-template <typename T, int NW_>
-__device__ void reduce_store(const f32x4 (&part)[4][2], float *red, T *dst, int64_t st, int64_t t0, int64_t Tn) {
-    constexpr int LDR = ld_of<float>(32);
-    const int g = lg(), i = li(), w = wave_id();
-    if constexpr (NW_ == 1) {
-        for (int md = 0; md < 4; ++md)
-            for (int nt = 0; nt < 2; ++nt) {
-                const int t = 16 * nt + i;
-                if (t0 + t < Tn) store4<T>(dst + (t0 + t) * st + 16 * md + 4 * g, part[md][nt]);
-            }
-    } else {
-        float *mine = red + w * TT * LDR;
-        for (int h = 0; h < 2; ++h) {
-            for (int mh = 0; mh < 2; ++mh)
-                for (int nt = 0; nt < 2; ++nt)
-                    *reinterpret_cast<f32x4 *>(mine + (16 * nt + i) * LDR + 16 * mh + 4 * g) = part[2 * h + mh][nt];
-            __syncthreads();
-            for (int idx = threadIdx.x; idx < TT * 8; idx += 64 * NW_) {
-                const int t = idx >> 3, d0 = 4 * (idx & 7);
-                f32x4 sum = *reinterpret_cast<const f32x4 *>(red + t * LDR + d0);
-                for (int ww = 1; ww < NW_; ++ww)
-                    sum += *reinterpret_cast<const f32x4 *>(red + ww * TT * LDR + t * LDR + d0);
-                if (t0 + t < Tn) store4<T>(dst + (t0 + t) * st + 32 * h + d0, sum);
-            }
-            __syncthreads();
-        }
+        if (t0 + t < Tn) store4<T>(dst + t0 * st + ((uint32_t)t * (uint32_t)st + (uint32_t)(16 * md + 4 * g)), acc);
     }
 }
 
@@ -403,23 +464,38 @@ template <typename T, int SP> struct FwdReduceL {
     static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL);
     static constexpr size_t oK = 0;
     static constexpr size_t oVt = align16(oK + sizeof(T) * TT * LDN);
-    static constexpr size_t oPkt = align16(oVt + sizeof(T) * D * LDT);
-    static constexpr size_t oPl = align16(oPkt + sizeof(T) * SP * LDT);
+    static constexpr size_t oPl = align16(oVt + sizeof(T) * D * LDT);
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t oSig = align16(oPlLo + sizeof(T) * NCOL * LDN);
-    static constexpr size_t bytes = align16(oSig + sizeof(float) * 2 * TT * LDC);
+    static constexpr size_t oCst = align16(oSig + sizeof(float) * 2 * TT * LDC);
+    static constexpr size_t bytes = align16(oCst + Consts<T>::bytes);
 };
+
+// The tile's (A, B) sums -- tot (lane: bucket 4g + e) and dB^T (d-row) --
+// from the wave's token operand Pf.  k_bwd_out subtracts exactly these values
+// (same operands, same instructions) to walk the forward state backwards.
+template <typename T>
+__device__ __forceinline__ void tile_sums(const Frag<T> &Pf, const Consts<T> &cst, const T *sVt, f32x4 &tot,
+                                          f32x4 (&dB)[4]) {
+    constexpr int LDT = ld_of<T>(TT);
+    tot = zero4();
+    mma(tot, Pf, cst.ones());
+#pragma unroll
+    for (int md = 0; md < 4; ++md) {
+        dB[md] = zero4();
+        mma(dB[md], ld_frag_pi(sVt + (16 * md + li()) * LDT), Pf);
+    }
+}
 
 template <typename T, int SP, int KB>
 __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     using Ly = FwdReduceL<T, SP>;
-    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC;
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDC = Ly::LDC;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
     float *sSp = (float *)(smem + Ly::oSig), *sSm = sSp + TT * LDC;
     const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
-    T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -428,6 +504,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
 
+    Consts<T> cst;
+    cst.init((T *)(smem + Ly::oCst), NTH);
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
     double accB[4][4], accA[4];
     for (int e = 0; e < 4; ++e) {
@@ -454,17 +532,13 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
         __syncthreads();
         f32x4 PK[2];
         probs_st<KB>(sSp, sSm, sw, a.S, t0, a.T, PK);
-        for (int nt = 0; nt < 2; ++nt)
-            for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
-        store_rows_T<T>(sPkt, PK);
-        float tot[4];
-        tile_totals(PK, tot);
-        for (int e = 0; e < 4; ++e) accA[e] += (double)tot[e];
-        __syncthreads();
-        f32x4 dB[4];
-        tile_dBT<T>(sVt, sPkt, dB);
-        for (int md = 0; md < 4; ++md)
-            for (int e = 0; e < 4; ++e) accB[md][e] += (double)dB[md][e];
+        const Frag<T> Pf = token_operand<T>(PK, cst);
+        f32x4 tot, dB[4];
+        tile_sums<T>(Pf, cst, sVt, tot, dB);
+        for (int e = 0; e < 4; ++e) {
+            accA[e] += (double)tot[e];
+            for (int md = 0; md < 4; ++md) accB[md][e] += (double)dB[md][e];
+        }
     }
     double *out = a.fdelta + ((int64_t)n * a.nseg + seg) * SP * SROW;
     for (int md = 0; md < 4; ++md)
@@ -486,35 +560,67 @@ __global__ void k_fwd_scan(double *fstate, const double *fdelta, int nseg, int e
 }
 
 // =====================================================================
-// k_fwd_out: outputs O^T = B^T W^T + V^T tril(W P_K^T)^T per wave, summed
-// over the waves.
+// k_fwd_out: O^T[d][t] = sum_s B[s][d] W[t][s] + sum_{t' <= t} V[t'][d] Sc[t'][t],
+// Sc[t'][t] = sum_s P_K[t'][s] W[t][s].  Each wave writes its buckets' W,
+// P_K and B (tile start) to LDS as [.][s] arrays, then computes output tiles
+// over all buckets; the B carry of its buckets stays in registers.
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct FwdOutL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL);
-    // region R0 = {Q, K, sigma tables}; the output reduction reuses it once they are dead
+    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDS_ = ld_of<T>(SP);
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
-    static constexpr size_t oSig = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));  // Q sp, Q sm, K sp, K sm
-    static constexpr size_t r0 = align16(cmax(oSig + sizeof(float) * 4 * TT * LDC, red_bytes<NW_>()));
-    static constexpr size_t oVt = r0;
-    static constexpr size_t oPkt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oPl = align16(oPkt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
+    static constexpr size_t oVt = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
+    static constexpr size_t oSig = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));  // Q sp, Q sm, K sp, K sm
+    static constexpr size_t oPts = align16(oSig + sizeof(float) * (CAUSAL ? 4 : 2) * TT * LDC);
+    static constexpr size_t oWts = align16(oPts + (CAUSAL ? sizeof(T) * TT * LDS_ : 0));
+    static constexpr size_t oBT = align16(oWts + sizeof(T) * TT * LDS_);
+    static constexpr size_t oPl = align16(oBT + sizeof(T) * D * LDS_);
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
-    static constexpr size_t bytes = align16(oPlLo + sizeof(T) * NCOL * LDN);
+    static constexpr size_t oCst = align16(oPlLo + sizeof(T) * NCOL * LDN);
+    static constexpr size_t bytes = align16(oCst + Consts<T>::bytes);
 };
+
+template <typename T, int SP, bool CAUSAL>
+__device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T *Wts, const T *sVt, T *op,
+                             int64_t st, int64_t t0, int64_t Tn) {
+    constexpr int LDS_ = ld_of<T>(SP), LDT = ld_of<T>(TT);
+    const int g = lg(), i = li();
+    const T *pb = sBT + (16 * md + i) * LDS_ + 8 * g, *pw = Wts + (16 * nt + i) * LDS_ + 8 * g;
+    f32x4 O = zero4();
+#pragma unroll
+    for (int ks = 0; ks < SP / 32; ++ks) mma(O, ld_frag(pb + 32 * ks), ld_frag(pw + 32 * ks));
+    if constexpr (CAUSAL) {
+        f32x4 Sc[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            Sc[mt] = zero4();
+            if (mt <= nt) {
+                const T *pp = Pts + (16 * mt + i) * LDS_ + 8 * g;
+#pragma unroll
+                for (int ks = 0; ks < SP / 32; ++ks) mma(Sc[mt], ld_frag(pp + 32 * ks), ld_frag(pw + 32 * ks));
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (16 * mt + 4 * g + e > 16 * nt + i) Sc[mt][e] = 0.f;  // keep t' <= t
+            }
+        }
+        mma(O, ld_frag_pi(sVt + (16 * md + i) * LDT), frag_acc<T>(Sc[0], Sc[1]));
+    }
+    const int t = 16 * nt + i;
+    if (t0 + t < Tn) store4<T>(op + t0 * st + ((uint32_t)t * (uint32_t)st + (uint32_t)(16 * md + 4 * g)), O);
+}
 
 template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(threads_of(SP)) void k_fwd_out(Args a) {
     using Ly = FwdOutL<T, SP, CAUSAL>;
-    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC;
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC, LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
+    T *sPts = (T *)(smem + Ly::oPts), *sWts = (T *)(smem + Ly::oWts), *sBT = (T *)(smem + Ly::oBT);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
-    float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oQ);
+    float *sSig = (float *)(smem + Ly::oSig);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sSpK = sSig + 2 * TT * LDC, *sSmK = sSig + 3 * TT * LDC;
     const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
-    T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -525,6 +631,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_out(Args a) {
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
     T *op = (T *)a.out + stream_off(a.so, n, a.B, a.H);
 
+    Consts<T> cst;
+    cst.init((T *)(smem + Ly::oCst), NTH);
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
     // carried state: causal = prefix at the segment start, non-causal = totals.
     // B in bucket-row layout: lane holds B[s = sw + 4g + e][d = 16md + i]
@@ -535,6 +643,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_out(Args a) {
         for (int md = 0; md < 4; ++md) Bc[md][e] = (float)st[sidx(sw + 4 * g + e, 16 * md + i)];
         a0[e] = st[sidx(sw + 4 * g + e, D)];
     }
+    if constexpr (!CAUSAL) store_ds<T>(sBT, LDS_, sw, Bc);  // constant totals
 
     Prefetch<T, NTH> pq_, pk_, pv_;
     if (j0 < j1) {
@@ -546,7 +655,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_out(Args a) {
     }
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
-        __syncthreads();
+        __syncthreads();  // previous tile's readers of sVt / sPts / sWts / sBT are done
         pq_.commit(sQ, nullptr);
         if constexpr (CAUSAL) {
             pk_.commit(sK, nullptr);
@@ -567,62 +676,40 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_out(Args a) {
                 project_tile<T>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
         }
         __syncthreads();
-        f32x4 PQ[2], PK[2], Acum[2];
+        f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
+        Frag<T> Pf;
         probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
         if constexpr (CAUSAL) {
             probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
-            store_rows_T<T>(sPkt, PK);
-            tile_prefix(PK, Acum);
+            Pf = token_operand<T>(PK, cst);
+            for (int nt = 0; nt < 2; ++nt) {
+                Acum[nt] = zero4();
+                mma(Acum[nt], Pf, cst.tri_op(nt));
+            }
+            tot = zero4();
+            mma(tot, Pf, cst.ones());
         }
         // W = P_Q / (A(t) + eps)
-        Frag4<T> Wf[2];
-        for (int nt = 0; nt < 2; ++nt) {
-            f32x4 W;
+        for (int nt = 0; nt < 2; ++nt)
             for (int e = 0; e < 4; ++e) {
                 const float A = (float)a0[e] + (CAUSAL ? Acum[nt][e] : 0.f);
-                W[e] = PQ[nt][e] * rcp(A + a.eps);
+                W[nt][e] = PQ[nt][e] * rcp(A + a.eps);
             }
-            Wf[nt] = frag16_acc<T>(W);
-        }
-        // O1^T[d][t] = sum_s B[s][d] W[t][s]
-        f32x4 O[4][2];
-        for (int md = 0; md < 4; ++md) {
-            const Frag4<T> bf = frag16_acc<T>(Bc[md]);
-            for (int nt = 0; nt < 2; ++nt) {
-                O[md][nt] = zero4();
-                mma16(O[md][nt], bf, Wf[nt]);
-            }
-        }
+        store_ts<T>(sWts, LDS_, sw, W);
         if constexpr (CAUSAL) {
-            // Sc^T[t'][t] = sum_s P_K[t'][s] W[t][s], kept for t' <= t
-            f32x4 Sc[2][2];
-            for (int mt = 0; mt < 2; ++mt) {
-                const Frag4<T> pf = frag16_acc<T>(PK[mt]);
-                for (int nt = 0; nt < 2; ++nt) {
-                    Sc[mt][nt] = zero4();
-                    if (mt <= nt) mma16(Sc[mt][nt], pf, Wf[nt]);
-                    for (int e = 0; e < 4; ++e)
-                        if (16 * mt + 4 * g + e > 16 * nt + i) Sc[mt][nt][e] = 0.f;
-                }
-            }
-            float tot[4];
-            tile_totals(PK, tot);
-            for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
-            __syncthreads();  // sPkt complete; sigma tables and Q/K tiles dead before R0 is reused
-            // O2^T[d][t] = sum_t' V[t'][d] Sc^T[t'][t]
-            for (int nt = 0; nt < 2; ++nt) {
-                const Frag<T> sf = frag_acc<T>(Sc[0][nt], Sc[1][nt]);
-                for (int md = 0; md < 4; ++md) mma(O[md][nt], ld_frag_pi(sVt + (16 * md + i) * LDT), sf);
-            }
-            // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
-            const Frag<T> pa = ld_frag(sPkt + i * LDT + 8 * g);
-            for (int md = 0; md < 4; ++md) mma(Bc[md], pa, ld_frag(sVt + (16 * md + i) * LDT + 8 * g));
-        } else {
-            __syncthreads();  // sigma tables and Q tile dead before R0 is reused
+            store_ts<T>(sPts, LDS_, sw, PK);
+            store_ds<T>(sBT, LDS_, sw, Bc);
         }
-        reduce_store<T, NW_>(O, sRed, op, a.so.t, t0, a.T);
+        __syncthreads();
+        for (int q = w; q < 8; q += NW_)
+            fwd_out_tile<T, SP, CAUSAL>(q >> 1, q & 1, sBT, sPts, sWts, sVt, op, a.so.t, t0, a.T);
+        if constexpr (CAUSAL) {
+            // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
+            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, ld_frag_pi(sVt + (16 * md + i) * LDT));
+            for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
+        }
     }
 }
 
@@ -639,31 +726,31 @@ template <typename T, int SP, bool CAUSAL> struct BwdReduceL {
     static constexpr size_t oG = align16(oV + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oVt = align16(oG + sizeof(T) * TT * LDN);
     static constexpr size_t oGt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oPkt = align16(oGt + sizeof(T) * D * LDT);
-    static constexpr size_t oWt = align16(oPkt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
-    static constexpr size_t oDproj = align16(oWt + sizeof(T) * SP * LDT);
+    static constexpr size_t oX = align16(oGt + sizeof(T) * D * LDT);
+    static constexpr size_t oDproj = align16(oX + (CAUSAL ? sizeof(T) * TT * LDT : 0));
     static constexpr size_t oPl = align16(oDproj + sizeof(T) * TT * LDDP);
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t oPlT = align16(oPlLo + sizeof(T) * NCOL * LDN);
     static constexpr size_t oSig = align16(oPlT + sizeof(T) * D * LDDP);  // Q sp, Q sm, Q th, K sp, K sm
     static constexpr size_t oRed = align16(oSig + sizeof(float) * 5 * TT * LDC);
-    static constexpr size_t bytes = align16(oRed + sizeof(float) * 64 * NW_);
+    static constexpr size_t oCst = align16(oRed + sizeof(float) * 64 * NW_);
+    static constexpr size_t bytes = align16(oCst + Consts<T>::bytes);
 };
 
 template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     using Ly = BwdReduceL<T, SP, CAUSAL>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
+    constexpr int NTASK = CAUSAL ? 11 : 4;  // Q projection (4), K projection (4), X tiles (3)
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sV = (T *)(smem + Ly::oV);
     T *sG = (T *)(smem + Ly::oG), *sVt = (T *)(smem + Ly::oVt), *sGt = (T *)(smem + Ly::oGt);
-    T *sDproj = (T *)(smem + Ly::oDproj);
+    T *sX = (T *)(smem + Ly::oX), *sDproj = (T *)(smem + Ly::oDproj);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo), *sPlT = (T *)(smem + Ly::oPlT);
     float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sThQ = sSig + 2 * TT * LDC;
     float *sSpK = sSig + 3 * TT * LDC, *sSmK = sSig + 4 * TT * LDC;
     const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
-    T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT, *sWt = (T *)(smem + Ly::oWt) + sw * LDT;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -675,8 +762,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     const T *gp = (const T *)a.dout + stream_off(a.sdo, n, a.B, a.H);
     T *dqp = (T *)a.dq + stream_off(a.sg, n, a.B, a.H);
 
+    Consts<T> cst;
+    cst.init((T *)(smem + Ly::oCst), NTH);
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
-    for (int idx = threadIdx.x; idx < TT * LDDP; idx += NTH) sDproj[idx] = from_f32<T>(0.f);
+    zero_lds<T>(sDproj, TT * LDDP, NTH);
+    if constexpr (CAUSAL) zero_lds<T>(sX, TT * LDT, NTH);
     // forward state in d-row layout: lane holds B^T[d = 16md + 4g + e][s = sw + i]
     const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * SP * SROW;
     f32x4 Bt[4], Ut[4];
@@ -702,7 +792,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     }
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
-        __syncthreads();
+        // no barrier before the commit: since the previous tile's last barrier
+        // only dx_store ran, which reads neither the token tiles nor X
         pq_.commit(sQ, nullptr);
         pg_.commit(sG, sGt);
         if constexpr (CAUSAL) {
@@ -718,21 +809,29 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             }
         }
         __syncthreads();
-        for (int q = w; q < (CAUSAL ? 8 : 4); q += NW_) {
+        for (int q = w; q < NTASK; q += NW_) {
             if (q < 4)
                 project_tile<T>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, sThQ);
-            else
+            else if (q < 8)
                 project_tile<T>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
+            else
+                m_tile<T>(q - 8, sV, sG, sX, nullptr);
         }
         __syncthreads();
-        f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2];
+        f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2], tot;
+        Frag<T> Pf;
         probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
         if constexpr (CAUSAL) {
             probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
-            store_rows_T<T>(sPkt, PK);
-            tile_prefix(PK, Acum);
+            Pf = token_operand<T>(PK, cst);
+            for (int nt = 0; nt < 2; ++nt) {
+                Acum[nt] = zero4();
+                mma(Acum[nt], Pf, cst.tri_op(nt));
+            }
+            tot = zero4();
+            mma(tot, Pf, cst.ones());
         }
         for (int nt = 0; nt < 2; ++nt)
             for (int e = 0; e < 4; ++e) {
@@ -740,51 +839,35 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
                 inv[nt][e] = rcp(A + a.eps);
                 W[nt][e] = PQ[nt][e] * inv[nt][e];
             }
-        store_rows_T<T>(sWt, W);
-        // Hm^T[tau][t] = v_tau . g_t for tau <= t (B operand over tau, pi order)
-        f32x4 HmT[2][2];
-        if constexpr (CAUSAL) {
-            for (int mt = 0; mt < 2; ++mt)
-                for (int nt = 0; nt < 2; ++nt) {
-                    HmT[mt][nt] = zero4();
-                    if (mt <= nt) tile_mma(HmT[mt][nt], sV + 16 * mt * LDN, LDN, sG + 16 * nt * LDN, LDN, D / 32);
-                    for (int e = 0; e < 4; ++e)
-                        if (16 * mt + 4 * g + e > 16 * nt + i) HmT[mt][nt][e] = 0.f;
-                }
-        }
-        __syncthreads();  // sPkt, sWt of this wave complete
-        // G[s][t] = g_t . B_s(t) = sum_d B[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] Hm[t][tau]
+        const Frag<T> Wf = token_operand<T>(W, cst);
+        // G[s][t] = g_t . B_s(t) = sum_d B[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
         f32x4 dPQ[2], dA[2];
-        for (int nt = 0; nt < 2; ++nt) {
-            f32x4 G = zero4();
-            for (int kk = 0; kk < 2; ++kk)
-                mma(G, frag_acc<T>(Bt[2 * kk], Bt[2 * kk + 1]), ld_frag_pi(sG + (16 * nt + i) * LDN + 32 * kk));
-            if constexpr (CAUSAL) mma(G, ld_frag_pi(sPkt + i * LDT), frag_acc<T>(HmT[0][nt], HmT[1][nt]));
-            // dP_Q = G/(A+eps); dA = -W G/(A+eps)
-            for (int e = 0; e < 4; ++e) {
-                dPQ[nt][e] = G[e] * inv[nt][e];
-                dA[nt][e] = -W[nt][e] * dPQ[nt][e];
+        {
+            const Frag<T> b0 = frag_acc<T>(Bt[0], Bt[1]), b1 = frag_acc<T>(Bt[2], Bt[3]);
+            for (int nt = 0; nt < 2; ++nt) {
+                f32x4 G = zero4();
+                mma(G, b0, ld_frag_pi(sG + (16 * nt + i) * LDN));
+                mma(G, b1, ld_frag_pi(sG + (16 * nt + i) * LDN + 32));
+                if constexpr (CAUSAL) mma(G, Pf, ld_frag_pi(sX + (16 * nt + i) * LDT));
+                // dP_Q = G/(A+eps); dA = -W G/(A+eps)
+                for (int e = 0; e < 4; ++e) {
+                    dPQ[nt][e] = G[e] * inv[nt][e];
+                    dA[nt][e] = -W[nt][e] * dPQ[nt][e];
+                }
             }
         }
         {
-            float tot[4];
-            tile_totals(dA, tot);
-            for (int e = 0; e < 4; ++e) al[e] += (double)tot[e];
+            float tdA[4];
+            tile_totals(dA, tdA);
+            for (int e = 0; e < 4; ++e) al[e] += (double)tdA[e];
         }
         // U^T[d][s] += sum_t g[t][d] W[t][s]; carry B^T[d][s] += sum_t V[t][d] P_K[t][s]
-        {
-            const Frag<T> wb = ld_frag(sWt + i * LDT + 8 * g);
-            for (int md = 0; md < 4; ++md) mma(Ut[md], ld_frag(sGt + (16 * md + i) * LDT + 8 * g), wb);
-            if constexpr (CAUSAL) {
-                const Frag<T> pb = ld_frag(sPkt + i * LDT + 8 * g);
-                for (int md = 0; md < 4; ++md) mma(Bt[md], ld_frag(sVt + (16 * md + i) * LDT + 8 * g), pb);
-            }
+        for (int md = 0; md < 4; ++md) {
+            mma(Ut[md], ld_frag_pi(sGt + (16 * md + i) * LDT), Wf);
+            if constexpr (CAUSAL) mma(Bt[md], ld_frag_pi(sVt + (16 * md + i) * LDT), Pf);
         }
-        if constexpr (CAUSAL) {
-            float tot[4];
-            tile_totals(PK, tot);
+        if constexpr (CAUSAL)
             for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
-        }
         tsum += softhash_bwd_st<KB, T>(PQ, dPQ, sThQ, sw, a.L, a.inv_temp, sDproj);
         __syncthreads();
         dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0, a.T);
@@ -816,44 +899,81 @@ __global__ void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int ele
 
 // =====================================================================
 // k_bwd_out: reverse walk.  dK, dV.
+// dV^T[d][tau] = sum_s U[s][d] P_K[tau][s] + sum_{t >= tau} g[t][d] Sc2[t][tau],
+// Sc2[t][tau] = sum_s W[t][s] P_K[tau][s], computed as output tiles over all
+// buckets from the waves' [.][s] LDS arrays; dK through each wave's buckets.
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct BwdOutL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
-    // region R0 = {Q, K, sigma tables}; the dV reduction reuses it once they are dead
-    static constexpr size_t oQ = 0;
-    static constexpr size_t oK = align16(oQ + (CAUSAL ? sizeof(T) * TT * LDN : 0));
-    static constexpr size_t oSig = align16(oK + sizeof(T) * TT * LDN);  // K sp, K sm, Q sp, Q sm
-    static constexpr size_t r0 = align16(cmax(oSig + sizeof(float) * (CAUSAL ? 4 : 2) * TT * LDC, red_bytes<NW_>()));
-    static constexpr size_t oTh = r0;
-    static constexpr size_t oV = align16(oTh + sizeof(float) * TT * LDC);
+    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL),
+                         LDS_ = ld_of<T>(SP);
+    static constexpr size_t oK = 0;
+    static constexpr size_t oQ = align16(oK + sizeof(T) * TT * LDN);
+    static constexpr size_t oV = align16(oQ + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oG = align16(oV + sizeof(T) * TT * LDN);
     static constexpr size_t oVt = align16(oG + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oGt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oPkt = align16(oGt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oWt = align16(oPkt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
-    static constexpr size_t oDproj = align16(oWt + (CAUSAL ? sizeof(T) * SP * LDT : 0));
+    static constexpr size_t oX = align16(oGt + (CAUSAL ? sizeof(T) * D * LDT : 0));
+    static constexpr size_t oY = align16(oX + (CAUSAL ? sizeof(T) * TT * LDT : 0));
+    static constexpr size_t oPts = align16(oY + (CAUSAL ? sizeof(T) * TT * LDT : 0));
+    static constexpr size_t oWts = align16(oPts + sizeof(T) * TT * LDS_);
+    static constexpr size_t oUT = align16(oWts + (CAUSAL ? sizeof(T) * TT * LDS_ : 0));
+    static constexpr size_t oDproj = align16(oUT + sizeof(T) * D * LDS_);
     static constexpr size_t oPl = align16(oDproj + sizeof(T) * TT * LDDP);
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t oPlT = align16(oPlLo + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oRed = align16(oPlT + sizeof(T) * D * LDDP);
-    static constexpr size_t bytes = align16(oRed + sizeof(float) * 64 * NW_);
+    static constexpr size_t oSig = align16(oPlT + sizeof(T) * D * LDDP);  // K sp, K sm, K th, Q sp, Q sm
+    static constexpr size_t oRed = align16(oSig + sizeof(float) * (CAUSAL ? 5 : 3) * TT * LDC);
+    static constexpr size_t oCst = align16(oRed + sizeof(float) * 64 * NW_);
+    static constexpr size_t bytes = align16(oCst + Consts<T>::bytes);
 };
+
+template <typename T, int SP, bool CAUSAL>
+__device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts, const T *sGt, T *dvp, int64_t st,
+                        int64_t t0, int64_t Tn) {
+    constexpr int LDS_ = ld_of<T>(SP), LDT = ld_of<T>(TT);
+    const int g = lg(), i = li();
+    const T *pu = sUT + (16 * md + i) * LDS_ + 8 * g, *pp = Pts + (16 * nt + i) * LDS_ + 8 * g;
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int ks = 0; ks < SP / 32; ++ks) mma(acc, ld_frag(pu + 32 * ks), ld_frag(pp + 32 * ks));
+    if constexpr (CAUSAL) {
+        f32x4 Sc2[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            Sc2[mt] = zero4();
+            if (mt >= nt) {
+                const T *pw = Wts + (16 * mt + i) * LDS_ + 8 * g;
+#pragma unroll
+                for (int ks = 0; ks < SP / 32; ++ks) mma(Sc2[mt], ld_frag(pw + 32 * ks), ld_frag(pp + 32 * ks));
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (16 * mt + 4 * g + e < 16 * nt + i) Sc2[mt][e] = 0.f;  // keep t >= tau
+            }
+        }
+        mma(acc, ld_frag_pi(sGt + (16 * md + i) * LDT), frag_acc<T>(Sc2[0], Sc2[1]));
+    }
+    const int t = 16 * nt + i;
+    if (t0 + t < Tn) store4<T>(dvp + t0 * st + ((uint32_t)t * (uint32_t)st + (uint32_t)(16 * md + 4 * g)), acc);
+}
 
 template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     using Ly = BwdOutL<T, SP, CAUSAL>;
-    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
+                  LDS_ = Ly::LDS_;
+    constexpr int NTASK = CAUSAL ? 14 : 4;  // K projection (4), Q projection (4), X and Y tiles (6)
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sV = (T *)(smem + Ly::oV);
     T *sG = (T *)(smem + Ly::oG), *sVt = (T *)(smem + Ly::oVt), *sGt = (T *)(smem + Ly::oGt);
+    T *sX = (T *)(smem + Ly::oX), *sY = (T *)(smem + Ly::oY);
+    T *sPts = (T *)(smem + Ly::oPts), *sWts = (T *)(smem + Ly::oWts), *sUT = (T *)(smem + Ly::oUT);
     T *sDproj = (T *)(smem + Ly::oDproj);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo), *sPlT = (T *)(smem + Ly::oPlT);
-    float *sSig = (float *)(smem + Ly::oSig), *sThK = (float *)(smem + Ly::oTh);
-    float *sRedV = (float *)(smem + Ly::oQ), *sRed = (float *)(smem + Ly::oRed);
-    float *sSpK = sSig, *sSmK = sSig + TT * LDC, *sSpQ = sSig + 2 * TT * LDC, *sSmQ = sSig + 3 * TT * LDC;
+    float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
+    float *sSpK = sSig, *sSmK = sSig + TT * LDC, *sThK = sSig + 2 * TT * LDC;
+    float *sSpQ = sSig + 3 * TT * LDC, *sSmQ = sSig + 4 * TT * LDC;
     const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
-    T *sPkt = (T *)(smem + Ly::oPkt) + sw * LDT, *sWt = (T *)(smem + Ly::oWt) + sw * LDT;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -866,13 +986,18 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     T *dkp = (T *)a.dk + stream_off(a.sg, n, a.B, a.H);
     T *dvp = (T *)a.dv + stream_off(a.sg, n, a.B, a.H);
 
+    Consts<T> cst;
+    cst.init((T *)(smem + Ly::oCst), NTH);
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
-    for (int idx = threadIdx.x; idx < TT * LDDP; idx += NTH) sDproj[idx] = from_f32<T>(0.f);
-    // reverse carries (U, alpha) after the segment; forward state at the segment end.
-    // U is kept in both layouts: Ut (d-row) feeds dP_K, Us (bucket-row) feeds dV.
+    zero_lds<T>(sDproj, TT * LDDP, NTH);
+    if constexpr (CAUSAL) {
+        zero_lds<T>(sX, TT * LDT, NTH);
+        zero_lds<T>(sY, TT * LDT, NTH);
+    }
+    // reverse carries (U, alpha) after the segment; forward state at the segment end
     const float *rs = a.rstate + ((int64_t)n * a.nseg + seg) * SP * SROW;
     const double *fs = a.fstate + ((int64_t)n * (a.nseg + 1) + seg + 1) * SP * SROW;
-    f32x4 Ut[4], Us[4];  // Ut: U^T[d = 16md + 4g + e][s = sw + i]; Us: U[s = sw + 4g + e][d = 16md + i]
+    f32x4 Ut[4];  // U^T[d = 16md + 4g + e][s = sw + i]
     double Be[4][4], Ae[4];
     float al[4];
     for (int md = 0; md < 4; ++md)
@@ -880,12 +1005,12 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             const int64_t r = sidx(sw + i, 16 * md + 4 * g + e);
             Ut[md][e] = rs[r];
             Be[md][e] = CAUSAL ? fs[r] : 0.0;
-            Us[md][e] = rs[sidx(sw + 4 * g + e, 16 * md + i)];
         }
     for (int e = 0; e < 4; ++e) {
         al[e] = rs[sidx(sw + 4 * g + e, D)];
         Ae[e] = CAUSAL ? fs[sidx(sw + 4 * g + e, D)] : 0.0;
     }
+    if constexpr (!CAUSAL) store_ut<T>(sUT, LDS_, sw, Ut, cst);  // constant totals
     float tsum = 0.f;
 
     Prefetch<T, NTH> pq_, pg_, pk_, pv_;
@@ -900,7 +1025,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     }
     for (int64_t jr = j1 - 1; jr >= j0; --jr) {
         const int64_t t0 = jr * TT;
-        __syncthreads();
+        // no barrier before the commit: since the previous tile's last barrier
+        // only dx_store ran, which reads neither the token tiles nor X / Y
         pk_.commit(sK, nullptr);
         pv_.commit(sV, CAUSAL ? sVt : nullptr);
         if constexpr (CAUSAL) {
@@ -916,70 +1042,54 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             }
         }
         __syncthreads();
-        for (int q = w; q < (CAUSAL ? 8 : 4); q += NW_) {
+        for (int q = w; q < NTASK; q += NW_) {
             if (q < 4)
                 project_tile<T>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpK, sSmK, sThK);
-            else
+            else if (q < 8)
                 project_tile<T>(sQ, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+            else
+                m_tile<T>(q - 8, sV, sG, sX, sY);
         }
         __syncthreads();
         f32x4 PK[2], PKr[2];  // fp32 and operand-rounded
         probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
         for (int nt = 0; nt < 2; ++nt)
             for (int e = 0; e < 4; ++e) PKr[nt][e] = as_operand<T>(PK[nt][e]);
-        Frag4<T> PKf[2];
-        for (int nt = 0; nt < 2; ++nt) PKf[nt] = frag16_acc<T>(PKr[nt]);
+        const Frag<T> Pf = token_operand<T>(PKr, cst);
+        store_ts<T>(sPts, LDS_, sw, PKr);
         f32x4 dPK[2];
         if constexpr (CAUSAL) {
-            f32x4 W[2], inv[2];
+            f32x4 Wi[2];  // W / (A + eps), the factor of dA
+            Frag<T> Wf;
             {
-                f32x4 PQ[2], Acum[2];
+                f32x4 PQ[2], Acum[2], W[2], tot, dB[4];
                 probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
-                store_rows_T<T>(sPkt, PKr);
                 // forward state at the tile start: end state minus this tile's sums
-                float tot[4];
-                tile_totals(PKr, tot);
-                for (int e = 0; e < 4; ++e) Ae[e] -= (double)tot[e];
-                tile_prefix(PKr, Acum);
+                tile_sums<T>(Pf, cst, sVt, tot, dB);
+                for (int e = 0; e < 4; ++e) {
+                    Ae[e] -= (double)tot[e];
+                    for (int md = 0; md < 4; ++md) Be[md][e] -= (double)dB[md][e];
+                }
+                for (int nt = 0; nt < 2; ++nt) {
+                    Acum[nt] = zero4();
+                    mma(Acum[nt], Pf, cst.tri_op(nt));
+                }
                 for (int nt = 0; nt < 2; ++nt)
                     for (int e = 0; e < 4; ++e) {
-                        inv[nt][e] = rcp((float)Ae[e] + Acum[nt][e] + a.eps);
-                        W[nt][e] = PQ[nt][e] * inv[nt][e];
+                        const float inv = rcp((float)Ae[e] + Acum[nt][e] + a.eps);
+                        W[nt][e] = PQ[nt][e] * inv;
+                        Wi[nt][e] = W[nt][e] * inv;
                     }
-                store_rows_T<T>(sWt, W);
+                store_ts<T>(sWts, LDS_, sw, W);
+                Wf = token_operand<T>(W, cst);
             }
-            Frag4<T> Wf[2];
-            for (int nt = 0; nt < 2; ++nt) Wf[nt] = frag16_acc<T>(W[nt]);
-            __syncthreads();  // sPkt, sWt complete; sigma tables and Q/K tiles dead
-            // ---- dV^T[d][tau] = sum_s U[s][d] P_K[tau][s] + sum_{t >= tau} g[t][d] Sc2^T[t][tau]
-            {
-                f32x4 Sc2[2][2];
-                for (int mt = 0; mt < 2; ++mt)
-                    for (int nt = 0; nt < 2; ++nt) {
-                        Sc2[mt][nt] = zero4();
-                        if (mt >= nt) mma16(Sc2[mt][nt], Wf[mt], PKf[nt]);
-                        for (int e = 0; e < 4; ++e)
-                            if (16 * mt + 4 * g + e < 16 * nt + i) Sc2[mt][nt][e] = 0.f;
-                    }
-                f32x4 VT[4][2];
-                for (int md = 0; md < 4; ++md) {
-                    const Frag4<T> uf = frag16_acc<T>(Us[md]);
-                    const Frag<T> gf = ld_frag_pi(sGt + (16 * md + i) * LDT);
-                    for (int nt = 0; nt < 2; ++nt) {
-                        VT[md][nt] = zero4();
-                        mma16(VT[md][nt], uf, PKf[nt]);
-                        mma(VT[md][nt], gf, frag_acc<T>(Sc2[0][nt], Sc2[1][nt]));
-                    }
-                }
-                reduce_store<T, NW_>(VT, sRedV, dvp, a.sg.t, t0, a.T);
-            }
-            // ---- dA = -W G/(A+eps), G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] Hm[t][tau]
+            store_ut<T>(sUT, LDS_, sw, Ut, cst);
+            __syncthreads();  // all waves' P_K, W, U rows in LDS
+            for (int q = w; q < 8; q += NW_)
+                dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T);
+            // ---- dA = -W G/(A+eps), G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
             f32x4 dA[2];
             {
-                f32x4 dB[4];
-                tile_dBT<T>(sVt, sPkt, dB);
-                for (int md = 0; md < 4; ++md)
-                    for (int e = 0; e < 4; ++e) Be[md][e] -= (double)dB[md][e];
                 Frag<T> Bf[2];
                 for (int kk = 0; kk < 2; ++kk) {
                     f32x4 b0, b1;
@@ -989,71 +1099,37 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                     }
                     Bf[kk] = frag_acc<T>(b0, b1);
                 }
-                f32x4 HmT[2][2];
-                for (int mt = 0; mt < 2; ++mt)
-                    for (int nt = 0; nt < 2; ++nt) {
-                        HmT[mt][nt] = zero4();
-                        if (mt <= nt) tile_mma(HmT[mt][nt], sV + 16 * mt * LDN, LDN, sG + 16 * nt * LDN, LDN, D / 32);
-                        for (int e = 0; e < 4; ++e)
-                            if (16 * mt + 4 * g + e > 16 * nt + i) HmT[mt][nt][e] = 0.f;
-                    }
-                const Frag<T> pkp = ld_frag_pi(sPkt + i * LDT);
                 for (int nt = 0; nt < 2; ++nt) {
                     f32x4 G = zero4();
                     mma(G, Bf[0], ld_frag_pi(sG + (16 * nt + i) * LDN));
                     mma(G, Bf[1], ld_frag_pi(sG + (16 * nt + i) * LDN + 32));
-                    mma(G, pkp, frag_acc<T>(HmT[0][nt], HmT[1][nt]));
-                    for (int e = 0; e < 4; ++e) dA[nt][e] = -W[nt][e] * G[e] * inv[nt][e];
+                    mma(G, Pf, ld_frag_pi(sX + (16 * nt + i) * LDT));
+                    for (int e = 0; e < 4; ++e) dA[nt][e] = -Wi[nt][e] * G[e];
                 }
             }
-            // ---- dP_K[tau][s] = alpha(tau) + sum_d U[s][d] v_tau[d] + sum_{t >= tau} W[t][s] Hm[t][tau]
+            // ---- dP_K[tau][s] = alpha(tau) + sum_d U[s][d] v_tau[d] + sum_{t >= tau} W[t][s] M[tau][t]
             {
                 f32x4 alpha[2];
                 tile_suffix(dA, alpha);
-                float tot[4];
-                tile_totals(dA, tot);
-                f32x4 Hm[2][2];
-                for (int mt = 0; mt < 2; ++mt)
-                    for (int nt = 0; nt < 2; ++nt) {
-                        Hm[mt][nt] = zero4();
-                        if (mt >= nt) tile_mma(Hm[mt][nt], sG + 16 * mt * LDN, LDN, sV + 16 * nt * LDN, LDN, D / 32);
-                        for (int e = 0; e < 4; ++e)
-                            if (16 * nt + i > 16 * mt + 4 * g + e) Hm[mt][nt][e] = 0.f;
-                    }
+                float tdA[4];
+                tile_totals(dA, tdA);
                 const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
-                const Frag<T> wp = ld_frag_pi(sWt + i * LDT);
                 for (int nt = 0; nt < 2; ++nt) {
                     f32x4 c = zero4();
                     mma(c, u0, ld_frag_pi(sV + (16 * nt + i) * LDN));
                     mma(c, u1, ld_frag_pi(sV + (16 * nt + i) * LDN + 32));
-                    mma(c, wp, frag_acc<T>(Hm[0][nt], Hm[1][nt]));
+                    mma(c, Wf, ld_frag_pi(sY + (16 * nt + i) * LDT));
                     for (int e = 0; e < 4; ++e) dPK[nt][e] = c[e] + alpha[nt][e] + al[e];
                 }
-                for (int e = 0; e < 4; ++e) al[e] += tot[e];
+                for (int e = 0; e < 4; ++e) al[e] += tdA[e];
             }
-            // ---- U[s][d] += sum_t W[t][s] g[t][d], in both layouts
-            {
-                const Frag<T> wb = ld_frag(sWt + i * LDT + 8 * g);
-                for (int md = 0; md < 4; ++md) {
-                    const Frag<T> gb = ld_frag(sGt + (16 * md + i) * LDT + 8 * g);
-                    mma(Ut[md], gb, wb);
-                    mma(Us[md], wb, gb);
-                }
-            }
+            // ---- U^T[d][s] += sum_t g[t][d] W[t][s]
+            for (int md = 0; md < 4; ++md) mma(Ut[md], ld_frag_pi(sGt + (16 * md + i) * LDT), Wf);
         } else {
-            __syncthreads();  // sigma tables and K tile dead before R0 is reused
+            __syncthreads();  // all waves' P_K rows in LDS
             // non-causal: dV^T = U^T P_K^T; dP_K = alpha + v . U (totals)
-            {
-                f32x4 VT[4][2];
-                for (int md = 0; md < 4; ++md) {
-                    const Frag4<T> uf = frag16_acc<T>(Us[md]);
-                    for (int nt = 0; nt < 2; ++nt) {
-                        VT[md][nt] = zero4();
-                        mma16(VT[md][nt], uf, PKf[nt]);
-                    }
-                }
-                reduce_store<T, NW_>(VT, sRedV, dvp, a.sg.t, t0, a.T);
-            }
+            for (int q = w; q < 8; q += NW_)
+                dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, nullptr, nullptr, dvp, a.sg.t, t0, a.T);
             const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
             for (int nt = 0; nt < 2; ++nt) {
                 f32x4 c = zero4();
