@@ -94,14 +94,65 @@ template <> __device__ __forceinline__ void store4<bf16>(bf16 *p, const f32x4 &v
     *reinterpret_cast<bf16x4 *>(p) = o;
 }
 
+// Wait for every load issued so far.  Placed after a kernel's state loads
+// and before its first prefetch: otherwise the compiler keeps waits for the
+// state registers inside the tile loop, where they would also wait for the
+// prefetch of the next tile.
+__device__ __forceinline__ void wait_state_loads() { __builtin_amdgcn_s_waitcnt(0); }
+
 // --------------------------------------------------------------- tile I/O
 // Register-staged tile load: issue() starts the global loads of one tile
 // into registers, commit() writes them to LDS (natural and/or transposed), so
 // the next tile's loads overlap the current tile's compute.
+// Token-tile global access: a uniform tile base and a 32-bit per-lane byte
+// offset (the host bounds the token stride below 2^26 elements).
+template <typename V, typename T> __device__ __forceinline__ V ld_at(const T *base, uint32_t off_bytes) {
+    return *reinterpret_cast<const V *>(reinterpret_cast<const char *>(base) + off_bytes);
+}
+template <typename T> __device__ __forceinline__ T *at_bytes(T *base, uint32_t off_bytes) {
+    return reinterpret_cast<T *>(reinterpret_cast<char *>(base) + off_bytes);
+}
+// The output tiles of k_fwd_out are written with buffer stores (measured
+// faster there): a resource over the valid bytes from the tile's first row
+// (word 3 = 0x00020000, the gfx9 raw-buffer format); every store is still
+// guarded by t0 + t < T, the record count is only a second bound.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const T *base, int64_t st, int64_t rows) {
+    int64_t bytes = rows > 0 ? ((rows - 1) * st + D) * (int64_t)sizeof(T) : 0;
+    if (bytes > 0x7FFFFFFFll) bytes = 0x7FFFFFFFll;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T *>(base), 0, (int)bytes, 0x00020000);
+}
+// 4 consecutive elements (one accumulator column) at byte offset off
+template <typename T> __device__ __forceinline__ void buf_st4(__amdgpu_buffer_rsrc_t r, uint32_t off, const f32x4 &v);
+template <> __device__ __forceinline__ void buf_st4<float>(__amdgpu_buffer_rsrc_t r, uint32_t off, const f32x4 &v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)off, 0, 0);
+}
+template <> __device__ __forceinline__ void buf_st4<bf16>(__amdgpu_buffer_rsrc_t r, uint32_t off, const f32x4 &v) {
+    typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    bf16x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = (bf16)v[e];
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o), r, (int)off, 0, 0);
+}
+// byte offset of element (t, d) of a token tile
+__device__ __forceinline__ uint32_t tile_off(int t, int64_t st, int d, int esize) {
+    return ((uint32_t)t * (uint32_t)st + (uint32_t)d) * (uint32_t)esize;
+}
+
+template <int B> struct ChunkOf;
+template <> struct ChunkOf<16> { typedef uint4 type; };
+template <> struct ChunkOf<8> { typedef uint2 type; };
+
+// Chunks of 16 bytes, or of 8 bytes when 16-byte chunks would leave some of
+// the workgroup's threads without one (every wave shares the staging work).
 template <typename T, int NTH> struct Prefetch {
-    static constexpr int EPC = 16 / sizeof(T), CPR = D / EPC, CHUNKS = TT * CPR;
+    static constexpr int CB = (TT * D * (int)sizeof(T) / 16 >= NTH) ? 16 : 8;
+    typedef typename ChunkOf<CB>::type chunk_t;
+    static constexpr int EPC = CB / sizeof(T), CPR = D / EPC, CHUNKS = TT * CPR;
     static constexpr int PER = (CHUNKS + NTH - 1) / NTH;
-    uint4 v[PER];
+    chunk_t v[PER];
     // tile base src + t0 * st is uniform; the lane offset t * st + c * EPC is
     // 32-bit (the host bounds 32 * token stride below 2^31)
     __device__ __forceinline__ void issue(const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn) {
@@ -109,9 +160,8 @@ template <typename T, int NTH> struct Prefetch {
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int idx = threadIdx.x + j * NTH, t = idx / CPR, c = idx % CPR;
-            v[j] = make_uint4(0, 0, 0, 0);
-            const uint32_t off = (uint32_t)t * (uint32_t)st + (uint32_t)(c * EPC);
-            if (idx < CHUNKS && t0 + t < Tn) v[j] = *reinterpret_cast<const uint4 *>(base + off);
+            v[j] = chunk_t{};
+            if (idx < CHUNKS && t0 + t < Tn) v[j] = ld_at<chunk_t>(base, tile_off(t, st, c * EPC, sizeof(T)));
         }
     }
     __device__ __forceinline__ void commit(T *nat, T *trn) const {
@@ -120,11 +170,68 @@ template <typename T, int NTH> struct Prefetch {
         for (int j = 0; j < PER; ++j) {
             const int idx = threadIdx.x + j * NTH, t = idx / CPR, c = idx % CPR;
             if (idx >= CHUNKS) continue;
-            if (nat) *reinterpret_cast<uint4 *>(nat + t * LDN + c * EPC) = v[j];
+            if (nat) *reinterpret_cast<chunk_t *>(nat + t * LDN + c * EPC) = v[j];
             if (trn) {
                 const T *e = reinterpret_cast<const T *>(&v[j]);
 #pragma unroll
                 for (int q = 0; q < EPC; ++q) trn[(c * EPC + q) * LDT + t] = e[q];
+            }
+        }
+    }
+};
+
+// Staging of a tile that is also needed transposed ([D][TT], t contiguous):
+// each task is a pair of tokens (2tp, 2tp+1) times one 8-byte chunk of d.
+// Lanes of a wave cover 16 token pairs x 4 chunks, so the transposed rows are
+// written as packed token pairs to consecutive LDS words (few bank conflicts)
+// while each token row is still read in 32-byte runs.  NPART tensors share
+// the workgroup: this one uses threads [part*NTH/NPART, (part+1)*NTH/NPART).
+template <typename T, int NTH, int NPART> struct PrefetchT {
+    static constexpr int NT = NTH / NPART;
+    static constexpr int EPC = 8 / sizeof(T), CPR = D / EPC, TASKS = (TT / 2) * CPR;
+    static constexpr int PER = (TASKS + NT - 1) / NT;
+    uint2 v[PER][2];
+    __device__ __forceinline__ static bool task_of(int part, int j, int &tp, int &c) {
+        const int local = (int)threadIdx.x - part * NT, task = local + j * NT;
+        tp = (task >> 2) & 15;
+        c = (task & 3) + 4 * (task >> 6);
+        return local >= 0 && local < NT && task < TASKS;
+    }
+    __device__ __forceinline__ void issue(int part, const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn) {
+        const T *base = src + t0 * st;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            int tp, c;
+            const bool ok = task_of(part, j, tp, c);
+            const uint32_t off = tile_off(2 * tp, st, c * EPC, sizeof(T));
+            v[j][0] = uint2{0, 0};
+            v[j][1] = uint2{0, 0};
+            if (ok && t0 + 2 * tp < Tn) v[j][0] = ld_at<uint2>(base, off);
+            if (ok && t0 + 2 * tp + 1 < Tn) v[j][1] = ld_at<uint2>(base, off + (uint32_t)st * (uint32_t)sizeof(T));
+        }
+    }
+    __device__ __forceinline__ void commit(int part, T *nat, T *trn) const {
+        constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            int tp, c;
+            if (!task_of(part, j, tp, c)) continue;
+            if (nat) {
+                *reinterpret_cast<uint2 *>(nat + (2 * tp) * LDN + c * EPC) = v[j][0];
+                *reinterpret_cast<uint2 *>(nat + (2 * tp + 1) * LDN + c * EPC) = v[j][1];
+            }
+            // element q of a chunk: bf16 -> 16-bit half q of the 64-bit chunk; fp32 -> word q
+            const uint2 a = v[j][0], b = v[j][1];
+            uint32_t *row = reinterpret_cast<uint32_t *>(trn + (c * EPC) * LDT + 2 * tp);
+            constexpr int RW = LDT * (int)sizeof(T) / 4;  // words per transposed row
+            if constexpr (sizeof(T) == 2) {
+                row[0 * RW] = (a.x & 0xFFFFu) | (b.x << 16);
+                row[1 * RW] = (a.x >> 16) | (b.x & 0xFFFF0000u);
+                row[2 * RW] = (a.y & 0xFFFFu) | (b.y << 16);
+                row[3 * RW] = (a.y >> 16) | (b.y & 0xFFFF0000u);
+            } else {
+                *reinterpret_cast<uint2 *>(row) = uint2{a.x, b.x};
+                *reinterpret_cast<uint2 *>(row + RW) = uint2{a.y, b.y};
             }
         }
     }
@@ -216,101 +323,6 @@ __device__ __forceinline__ void probs_st(const float *sp, const float *sm, int s
     }
 }
 
-// sum over the buckets of one table that share this lane's token: in-lane
-// over e (pairs for KB = 1) and across rows g for KB >= 3
-template <int KB> __device__ __forceinline__ float table_reduce(float x) {
-    if constexpr (KB >= 3) x = xor16_sum(x);
-    if constexpr (KB >= 4) x = xor32_sum(x);
-    return x;
-}
-
-// Softmax / corner / tanh backward in bucket-row layout for the wave's
-// buckets: dP (and P, fp32) -> dproj [TT][ld_of<T>(NCOL)] columns l*K + k of
-// the wave's tables; returns this lane's share of sum du * th.
-// du_k = sum_r dl_r c_rk over the table; the two lowest corner bits vary with
-// e inside the lane, the higher ones are fixed per lane (from its row g).
-template <int KB, typename T>
-__device__ float softhash_bwd_st(const f32x4 (&P)[2], const f32x4 (&dP)[2], const float *sth, int sw, int L,
-                                 float inv_temp, T *dproj) {
-    constexpr int LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
-    constexpr int R = 1 << KB;
-    constexpr int RPT = R >= 4 ? R / 4 : 1;  // rows g per table
-    const int g = lg(), i = li();
-    const int s0 = sw + 4 * g;
-    float tsum = 0.f;
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int t = 16 * nt + i;
-        f32x4 pd, dl;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) pd[e] = P[nt][e] * dP[nt][e];
-        if constexpr (KB == 1) {
-            const float d01 = pd[0] + pd[1], d23 = pd[2] + pd[3];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dl[e] = P[nt][e] * (dP[nt][e] - (e < 2 ? d01 : d23));
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int l = (s0 >> 1) + h;
-                const float du = dl[2 * h + 1] - dl[2 * h];  // corner r = 1 is +1
-                if (l < L) {
-                    const float th = sth[t * LDC + l];
-                    tsum += du * th;
-                    dproj[t * LDDP + l] = from_f32<T>(du * inv_temp * (1.f - th * th));
-                }
-            }
-        } else {
-            const float dot = table_reduce<KB>(pd[0] + pd[1] + pd[2] + pd[3]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dl[e] = P[nt][e] * (dP[nt][e] - dot);
-            const float sum = dl[0] + dl[1] + dl[2] + dl[3];
-            const int l = s0 >> KB, r0 = s0 & (R - 1);
-            float du[KB];
-#pragma unroll
-            for (int k = 0; k < KB - 2; ++k) du[k] = ((r0 >> (KB - 1 - k)) & 1) ? sum : -sum;
-            du[KB - 2] = (dl[2] + dl[3]) - (dl[0] + dl[1]);
-            du[KB - 1] = (dl[1] + dl[3]) - (dl[0] + dl[2]);
-#pragma unroll
-            for (int k = 0; k < KB; ++k) du[k] = table_reduce<KB>(du[k]);
-            if (l < L) {
-#pragma unroll
-                for (int k = 0; k < KB; ++k) {
-                    if ((k % RPT) == (g % RPT)) {
-                        const float th = sth[t * LDC + l * KB + k];
-                        tsum += du[k] * th;
-                        dproj[t * LDDP + l * KB + k] = from_f32<T>(du[k] * inv_temp * (1.f - th * th));
-                    }
-                }
-            }
-        }
-    }
-    return tsum;
-}
-
-// Per-bucket token sums of a tile: tot[e] = sum over the tile's 32 tokens
-// (identical code in every kernel, so the values are bit-identical).
-__device__ __forceinline__ void tile_totals(const f32x4 (&X)[2], float (&tot)[4]) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) tot[e] = row_sum(X[0][e]) + row_sum(X[1][e]);
-}
-// inclusive prefix over the tile's tokens
-__device__ __forceinline__ void tile_prefix(const f32x4 (&X)[2], f32x4 (&Y)[2]) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float tot0 = row_sum(X[0][e]);
-        Y[0][e] = row_prefix(X[0][e]);
-        Y[1][e] = row_prefix(X[1][e]) + tot0;
-    }
-}
-// inclusive suffix over the tile's tokens
-__device__ __forceinline__ void tile_suffix(const f32x4 (&X)[2], f32x4 (&Y)[2]) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float tot1 = row_sum(X[1][e]);
-        Y[1][e] = row_suffix(X[1][e]);
-        Y[0][e] = row_suffix(X[0][e]) + tot1;
-    }
-}
-
 // ------------------------------------------------------------ constant operands
 // Operand slots in the pi order of frag_acc: slot j < 4 is row 4g + j, slot
 // 4 + j is row 16 + 4g + j of a 32-row operand.
@@ -353,6 +365,45 @@ template <typename T> struct Consts {
     __device__ __forceinline__ Frag<T> ones() const { return ld_frag_pi(tri + (TT - 1) * LDT); }
     __device__ __forceinline__ Frag4<T> ident() const { return ld_frag16(id + li() * LDI); }
 };
+// suf[t][tau] = (tau >= t): column t = 16nt + i of a token suffix
+template <typename T> struct SufOps {
+    static constexpr int LDT = ld_of<T>(TT);
+    static constexpr size_t bytes = sizeof(T) * TT * LDT;
+    const T *suf;
+    __device__ __forceinline__ void init(T *buf, int nth) {
+        for (int idx = threadIdx.x; idx < TT * LDT; idx += nth)
+            buf[idx] = from_f32<T>(idx % LDT >= idx / LDT ? 1.f : 0.f);
+        suf = buf;
+    }
+    __device__ __forceinline__ Frag<T> op(int nt) const { return ld_frag_pi(suf + (16 * nt + li()) * LDT); }
+};
+
+// Softmax / corner backward over the wave's 16 buckets (tables of 2^KB
+// buckets, R-aligned), as 16-deep A operands (row, k = local bucket s):
+//   dot[s'][s] = 1 if s and s' share a table (per-table sums, per bucket)
+//   cs[r][s]   = c_{s,k} = +-1 if s is in table tl, r = tl*KB + k (corner sums)
+template <typename T, int KB> struct HashOps {
+    static constexpr int LDI = ld_of<T>(16), NROWS = (16 >> KB) * KB;
+    static constexpr size_t bytes = sizeof(T) * 2 * 16 * LDI;
+    const T *dot, *cs;
+    __device__ __forceinline__ void init(T *buf, int nth) {
+        T *d = buf, *c = buf + 16 * LDI;
+        for (int idx = threadIdx.x; idx < 16 * LDI; idx += nth) {
+            const int r = idx / LDI, sb = idx % LDI;
+            float vd = 0.f, vc = 0.f;
+            if (sb < 16) {
+                vd = (r >> KB) == (sb >> KB) ? 1.f : 0.f;
+                if (r < NROWS && (sb >> KB) == r / KB) vc = ((sb >> (KB - 1 - r % KB)) & 1) ? 1.f : -1.f;
+            }
+            d[idx] = from_f32<T>(vd);
+            c[idx] = from_f32<T>(vc);
+        }
+        dot = d;
+        cs = c;
+    }
+    __device__ __forceinline__ Frag4<T> dot_op() const { return ld_frag16(dot + li() * LDI); }
+    __device__ __forceinline__ Frag4<T> cs_op() const { return ld_frag16(cs + li() * LDI); }
+};
 
 // Token-direction operand of the wave's bucket-row tiles X[2] (lane holds
 // X[s = 4g + e][t = 16nt + i]): each tile is transposed on the matrix core
@@ -364,6 +415,108 @@ template <typename T> __device__ __forceinline__ Frag<T> token_operand(const f32
     mma16(r0, frag16_acc<T>(X[0]), ident);
     mma16(r1, frag16_acc<T>(X[1]), ident);
     return frag_acc<T>(r0, r1);
+}
+
+// c += A . X^T over the wave's 16 buckets, X a bucket-row tile taken as the B
+// operand (column t, k = s); bf16 splits X into two bf16 parts so that the
+// product keeps fp32 accuracy
+template <typename T> __device__ __forceinline__ void mma16_x(f32x4 &c, const Frag4<T> &A, const f32x4 &x) {
+    if constexpr (is_bf16<T>()) {
+        f32x4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            hi[e] = as_operand<T>(x[e]);
+            lo[e] = x[e] - hi[e];
+        }
+        mma16(c, A, frag16_acc<T>(hi));
+        mma16(c, A, frag16_acc<T>(lo));
+    } else {
+        mma16(c, A, frag16_acc<T>(x));
+    }
+}
+
+// Inclusive token suffix Y and token totals of a bucket-row tile pair on the
+// matrix cores; bf16 splits X into two bf16 parts (fp32-accurate sums).
+template <typename T>
+__device__ void suffix_totals(const f32x4 (&X)[2], const Consts<T> &cst, const SufOps<T> &suf, f32x4 (&Y)[2],
+                              f32x4 &tot) {
+    Y[0] = zero4();
+    Y[1] = zero4();
+    tot = zero4();
+    auto add = [&](const f32x4 (&Z)[2]) {
+        const Frag<T> F = token_operand<T>(Z, cst);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) mma(Y[nt], F, suf.op(nt));
+        mma(tot, F, cst.ones());
+    };
+    if constexpr (is_bf16<T>()) {
+        f32x4 hi[2], lo[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hi[nt][e] = as_operand<T>(X[nt][e]);
+                lo[nt][e] = X[nt][e] - hi[nt][e];
+            }
+        add(hi);
+        add(lo);
+    } else {
+        add(X);
+    }
+}
+// token totals only (lane: bucket 4g + e)
+template <typename T> __device__ void totals_of(const f32x4 (&X)[2], const Consts<T> &cst, f32x4 &tot) {
+    tot = zero4();
+    if constexpr (is_bf16<T>()) {
+        f32x4 hi[2], lo[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hi[nt][e] = as_operand<T>(X[nt][e]);
+                lo[nt][e] = X[nt][e] - hi[nt][e];
+            }
+        mma(tot, token_operand<T>(hi, cst), cst.ones());
+        mma(tot, token_operand<T>(lo, cst), cst.ones());
+    } else {
+        mma(tot, token_operand<T>(X, cst), cst.ones());
+    }
+}
+
+// Softmax / corner / tanh backward for the wave's buckets on the matrix
+// cores: dP (and P, fp32, bucket-row) -> dproj [TT][ld_of<T>(NCOL)] columns
+// l*K + k of the wave's tables; returns this lane's share of sum du * th.
+//   dl = P (dP - sum_table P dP),  du_k = sum_table dl c_k,
+//   dproj = du * inv_temp * (1 - th^2)
+// The du tile holds row r = tl*KB + k (lane rows 4g..4g+3), column t.
+template <int KB, typename T>
+__device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const float *sth, int sw, int L,
+                              float inv_temp, T *dproj, const HashOps<T, KB> &ho) {
+    constexpr int LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL), NROWS = HashOps<T, KB>::NROWS;
+    const int g = lg(), i = li(), c0 = (sw >> KB) * KB;
+    const Frag4<T> Ad = ho.dot_op(), Ac = ho.cs_op();
+    float tsum = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        f32x4 pd, dl, dot = zero4(), du = zero4();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pd[e] = P[nt][e] * dP[nt][e];
+        mma16_x<T>(dot, Ad, pd);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dl[e] = P[nt][e] * (dP[nt][e] - dot[e]);
+        mma16_x<T>(du, Ac, dl);
+        const int t = 16 * nt + i;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = 4 * g + e, col = c0 + row;
+            if (row < NROWS && col < L * KB) {
+                const float th = sth[t * LDC + col];
+                tsum += du[e] * th;
+                dproj[t * LDDP + col] = from_f32<T>(du[e] * inv_temp * (1.f - th * th));
+            }
+        }
+    }
+    return tsum;
 }
 
 // bucket-row tiles -> [t][s] LDS array (s contiguous, leading dimension ld):
@@ -429,12 +582,13 @@ template <typename T, int NW_>
 __device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64_t t0, int64_t Tn) {
     constexpr int LDDP = ld_of<T>(NCOL);
     const int g = lg(), i = li(), w = wave_id();
+    T *base = dst + t0 * st;
     for (int q = w; q < 8; q += NW_) {
         const int md = q >> 1, nt = q & 1;
         f32x4 acc = zero4();
         tile_mma(acc, plt + 16 * md * LDDP, LDDP, dproj + 16 * nt * LDDP, LDDP, NCOL / 32);
         const int t = 16 * nt + i;
-        if (t0 + t < Tn) store4<T>(dst + t0 * st + ((uint32_t)t * (uint32_t)st + (uint32_t)(16 * md + 4 * g)), acc);
+        if (t0 + t < Tn) store4<T>(at_bytes(base, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
     }
 }
 
@@ -513,19 +667,21 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
         for (int md = 0; md < 4; ++md) accB[md][e] = 0.0;
     }
 
-    Prefetch<T, NTH> pk_, pv_;
+    wait_state_loads();
+    Prefetch<T, NTH> pk_;
+    PrefetchT<T, NTH, 1> pv_;
     if (j0 < j1) {
         pk_.issue(kp, a.sk.t, j0 * TT, a.T);
-        pv_.issue(vp, a.sv.t, j0 * TT, a.T);
+        pv_.issue(0, vp, a.sv.t, j0 * TT, a.T);
     }
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
         __syncthreads();
         pk_.commit(sK, nullptr);
-        pv_.commit(nullptr, sVt);
+        pv_.commit(0, nullptr, sVt);
         if (jt + 1 < j1) {
             pk_.issue(kp, a.sk.t, t0 + TT, a.T);
-            pv_.issue(vp, a.sv.t, t0 + TT, a.T);
+            pv_.issue(0, vp, a.sv.t, t0 + TT, a.T);
         }
         __syncthreads();
         for (int q = w; q < 4; q += NW_) project_tile<T>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, nullptr);
@@ -607,11 +763,11 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
         mma(O, ld_frag_pi(sVt + (16 * md + i) * LDT), frag_acc<T>(Sc[0], Sc[1]));
     }
     const int t = 16 * nt + i;
-    if (t0 + t < Tn) store4<T>(op + t0 * st + ((uint32_t)t * (uint32_t)st + (uint32_t)(16 * md + 4 * g)), O);
+    if (t0 + t < Tn) buf_st4<T>(tile_rsrc(op + t0 * st, st, Tn - t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T)), O);
 }
 
 template <typename T, int SP, bool CAUSAL, int KB>
-__global__ __launch_bounds__(threads_of(SP)) void k_fwd_out(Args a) {
+__global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(Args a) {
     using Ly = FwdOutL<T, SP, CAUSAL>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC, LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
@@ -645,12 +801,14 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_out(Args a) {
     }
     if constexpr (!CAUSAL) store_ds<T>(sBT, LDS_, sw, Bc);  // constant totals
 
-    Prefetch<T, NTH> pq_, pk_, pv_;
+    wait_state_loads();
+    Prefetch<T, NTH> pq_, pk_;
+    PrefetchT<T, NTH, 1> pv_;
     if (j0 < j1) {
         pq_.issue(qp, a.sq.t, j0 * TT, a.T);
         if constexpr (CAUSAL) {
             pk_.issue(kp, a.sk.t, j0 * TT, a.T);
-            pv_.issue(vp, a.sv.t, j0 * TT, a.T);
+            pv_.issue(0, vp, a.sv.t, j0 * TT, a.T);
         }
     }
     for (int64_t jt = j0; jt < j1; ++jt) {
@@ -659,13 +817,13 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_out(Args a) {
         pq_.commit(sQ, nullptr);
         if constexpr (CAUSAL) {
             pk_.commit(sK, nullptr);
-            pv_.commit(nullptr, sVt);
+            pv_.commit(0, nullptr, sVt);
         }
         if (jt + 1 < j1) {
             pq_.issue(qp, a.sq.t, t0 + TT, a.T);
             if constexpr (CAUSAL) {
                 pk_.issue(kp, a.sk.t, t0 + TT, a.T);
-                pv_.issue(vp, a.sv.t, t0 + TT, a.T);
+                pv_.issue(0, vp, a.sv.t, t0 + TT, a.T);
             }
         }
         __syncthreads();
@@ -734,7 +892,8 @@ template <typename T, int SP, bool CAUSAL> struct BwdReduceL {
     static constexpr size_t oSig = align16(oPlT + sizeof(T) * D * LDDP);  // Q sp, Q sm, Q th, K sp, K sm
     static constexpr size_t oRed = align16(oSig + sizeof(float) * 5 * TT * LDC);
     static constexpr size_t oCst = align16(oRed + sizeof(float) * 64 * NW_);
-    static constexpr size_t bytes = align16(oCst + Consts<T>::bytes);
+    static constexpr size_t oHash = align16(oCst + Consts<T>::bytes);
+    static constexpr size_t bytes = align16(oHash + HashOps<T, 4>::bytes);
 };
 
 template <typename T, int SP, bool CAUSAL, int KB>
@@ -764,6 +923,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
+    HashOps<T, KB> ho;
+    ho.init((T *)(smem + Ly::oHash), NTH);
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
     zero_lds<T>(sDproj, TT * LDDP, NTH);
     if constexpr (CAUSAL) zero_lds<T>(sX, TT * LDT, NTH);
@@ -781,13 +942,16 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     }
     float tsum = 0.f;
 
-    Prefetch<T, NTH> pq_, pg_, pk_, pv_;
+    wait_state_loads();
+    constexpr int NP = CAUSAL ? 2 : 1;  // transposed tiles: dO (and V)
+    Prefetch<T, NTH> pq_, pk_;
+    PrefetchT<T, NTH, NP> pg_, pv_;
     if (j0 < j1) {
         pq_.issue(qp, a.sq.t, j0 * TT, a.T);
-        pg_.issue(gp, a.sdo.t, j0 * TT, a.T);
+        pg_.issue(0, gp, a.sdo.t, j0 * TT, a.T);
         if constexpr (CAUSAL) {
             pk_.issue(kp, a.sk.t, j0 * TT, a.T);
-            pv_.issue(vp, a.sv.t, j0 * TT, a.T);
+            pv_.issue(1, vp, a.sv.t, j0 * TT, a.T);
         }
     }
     for (int64_t jt = j0; jt < j1; ++jt) {
@@ -795,17 +959,17 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         // no barrier before the commit: since the previous tile's last barrier
         // only dx_store ran, which reads neither the token tiles nor X
         pq_.commit(sQ, nullptr);
-        pg_.commit(sG, sGt);
+        pg_.commit(0, sG, sGt);
         if constexpr (CAUSAL) {
             pk_.commit(sK, nullptr);
-            pv_.commit(sV, sVt);
+            pv_.commit(1, sV, sVt);
         }
         if (jt + 1 < j1) {
             pq_.issue(qp, a.sq.t, t0 + TT, a.T);
-            pg_.issue(gp, a.sdo.t, t0 + TT, a.T);
+            pg_.issue(0, gp, a.sdo.t, t0 + TT, a.T);
             if constexpr (CAUSAL) {
                 pk_.issue(kp, a.sk.t, t0 + TT, a.T);
-                pv_.issue(vp, a.sv.t, t0 + TT, a.T);
+                pv_.issue(1, vp, a.sv.t, t0 + TT, a.T);
             }
         }
         __syncthreads();
@@ -857,8 +1021,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             }
         }
         {
-            float tdA[4];
-            tile_totals(dA, tdA);
+            f32x4 tdA;
+            totals_of<T>(dA, cst, tdA);
             for (int e = 0; e < 4; ++e) al[e] += (double)tdA[e];
         }
         // U^T[d][s] += sum_t g[t][d] W[t][s]; carry B^T[d][s] += sum_t V[t][d] P_K[t][s]
@@ -868,7 +1032,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         }
         if constexpr (CAUSAL)
             for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
-        tsum += softhash_bwd_st<KB, T>(PQ, dPQ, sThQ, sw, a.L, a.inv_temp, sDproj);
+        tsum += softhash_bwd<KB, T>(PQ, dPQ, sThQ, sw, a.L, a.inv_temp, sDproj, ho);
         __syncthreads();
         dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0, a.T);
     }
@@ -925,7 +1089,9 @@ template <typename T, int SP, bool CAUSAL> struct BwdOutL {
     static constexpr size_t oSig = align16(oPlT + sizeof(T) * D * LDDP);  // K sp, K sm, K th, Q sp, Q sm
     static constexpr size_t oRed = align16(oSig + sizeof(float) * (CAUSAL ? 5 : 3) * TT * LDC);
     static constexpr size_t oCst = align16(oRed + sizeof(float) * 64 * NW_);
-    static constexpr size_t bytes = align16(oCst + Consts<T>::bytes);
+    static constexpr size_t oHash = align16(oCst + Consts<T>::bytes);
+    static constexpr size_t oSuf = align16(oHash + HashOps<T, 4>::bytes);
+    static constexpr size_t bytes = align16(oSuf + (CAUSAL ? SufOps<T>::bytes : 0));
 };
 
 template <typename T, int SP, bool CAUSAL>
@@ -954,7 +1120,7 @@ __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts
         mma(acc, ld_frag_pi(sGt + (16 * md + i) * LDT), frag_acc<T>(Sc2[0], Sc2[1]));
     }
     const int t = 16 * nt + i;
-    if (t0 + t < Tn) store4<T>(dvp + t0 * st + ((uint32_t)t * (uint32_t)st + (uint32_t)(16 * md + 4 * g)), acc);
+    if (t0 + t < Tn) store4<T>(at_bytes(dvp + t0 * st, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
 }
 
 template <typename T, int SP, bool CAUSAL, int KB>
@@ -988,6 +1154,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
+    HashOps<T, KB> ho;
+    ho.init((T *)(smem + Ly::oHash), NTH);
+    SufOps<T> sufo;
+    if constexpr (CAUSAL) sufo.init((T *)(smem + Ly::oSuf), NTH);
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
     zero_lds<T>(sDproj, TT * LDDP, NTH);
     if constexpr (CAUSAL) {
@@ -1013,14 +1183,18 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     if constexpr (!CAUSAL) store_ut<T>(sUT, LDS_, sw, Ut, cst);  // constant totals
     float tsum = 0.f;
 
-    Prefetch<T, NTH> pq_, pg_, pk_, pv_;
+    wait_state_loads();
+    Prefetch<T, NTH> pq_, pk_, pvn_;  // pvn_: non-causal V (natural only)
+    PrefetchT<T, NTH, 2> pg_, pv_;   // causal dO and V (natural and transposed)
     if (j0 < j1) {
         const int64_t tl = (j1 - 1) * TT;
         pk_.issue(kp, a.sk.t, tl, a.T);
-        pv_.issue(vp, a.sv.t, tl, a.T);
         if constexpr (CAUSAL) {
+            pv_.issue(1, vp, a.sv.t, tl, a.T);
             pq_.issue(qp, a.sq.t, tl, a.T);
-            pg_.issue(gp, a.sdo.t, tl, a.T);
+            pg_.issue(0, gp, a.sdo.t, tl, a.T);
+        } else {
+            pvn_.issue(vp, a.sv.t, tl, a.T);
         }
     }
     for (int64_t jr = j1 - 1; jr >= j0; --jr) {
@@ -1028,17 +1202,21 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         // no barrier before the commit: since the previous tile's last barrier
         // only dx_store ran, which reads neither the token tiles nor X / Y
         pk_.commit(sK, nullptr);
-        pv_.commit(sV, CAUSAL ? sVt : nullptr);
         if constexpr (CAUSAL) {
+            pv_.commit(1, sV, sVt);
             pq_.commit(sQ, nullptr);
-            pg_.commit(sG, sGt);
+            pg_.commit(0, sG, sGt);
+        } else {
+            pvn_.commit(sV, nullptr);
         }
         if (jr > j0) {
             pk_.issue(kp, a.sk.t, t0 - TT, a.T);
-            pv_.issue(vp, a.sv.t, t0 - TT, a.T);
             if constexpr (CAUSAL) {
+                pv_.issue(1, vp, a.sv.t, t0 - TT, a.T);
                 pq_.issue(qp, a.sq.t, t0 - TT, a.T);
-                pg_.issue(gp, a.sdo.t, t0 - TT, a.T);
+                pg_.issue(0, gp, a.sdo.t, t0 - TT, a.T);
+            } else {
+                pvn_.issue(vp, a.sv.t, t0 - TT, a.T);
             }
         }
         __syncthreads();
@@ -1051,10 +1229,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 m_tile<T>(q - 8, sV, sG, sX, sY);
         }
         __syncthreads();
-        f32x4 PK[2], PKr[2];  // fp32 and operand-rounded
-        probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
+        f32x4 PKr[2];  // operand-rounded P_K (fp32 P_K is rebuilt for the softmax backward)
+        probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PKr);
         for (int nt = 0; nt < 2; ++nt)
-            for (int e = 0; e < 4; ++e) PKr[nt][e] = as_operand<T>(PK[nt][e]);
+            for (int e = 0; e < 4; ++e) PKr[nt][e] = as_operand<T>(PKr[nt][e]);
         const Frag<T> Pf = token_operand<T>(PKr, cst);
         store_ts<T>(sPts, LDS_, sw, PKr);
         f32x4 dPK[2];
@@ -1085,8 +1263,6 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             }
             store_ut<T>(sUT, LDS_, sw, Ut, cst);
             __syncthreads();  // all waves' P_K, W, U rows in LDS
-            for (int q = w; q < 8; q += NW_)
-                dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T);
             // ---- dA = -W G/(A+eps), G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
             f32x4 dA[2];
             {
@@ -1109,10 +1285,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             }
             // ---- dP_K[tau][s] = alpha(tau) + sum_d U[s][d] v_tau[d] + sum_{t >= tau} W[t][s] M[tau][t]
             {
-                f32x4 alpha[2];
-                tile_suffix(dA, alpha);
-                float tdA[4];
-                tile_totals(dA, tdA);
+                f32x4 alpha[2], tdA;
+                suffix_totals<T>(dA, cst, sufo, alpha, tdA);
                 const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
                 for (int nt = 0; nt < 2; ++nt) {
                     f32x4 c = zero4();
@@ -1123,8 +1297,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 }
                 for (int e = 0; e < 4; ++e) al[e] += tdA[e];
             }
-            // ---- U^T[d][s] += sum_t g[t][d] W[t][s]
+            // ---- U^T[d][s] += sum_t g[t][d] W[t][s]  (the dV tiles read the LDS copy of U)
             for (int md = 0; md < 4; ++md) mma(Ut[md], ld_frag_pi(sGt + (16 * md + i) * LDT), Wf);
+            for (int q = w; q < 8; q += NW_)
+                dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T);
         } else {
             __syncthreads();  // all waves' P_K rows in LDS
             // non-causal: dV^T = U^T P_K^T; dP_K = alpha + v . U (totals)
@@ -1138,7 +1314,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 for (int e = 0; e < 4; ++e) dPK[nt][e] = c[e] + al[e];
             }
         }
-        tsum += softhash_bwd_st<KB, T>(PK, dPK, sThK, sw, a.L, a.inv_temp, sDproj);
+        {
+            f32x4 PK[2];
+            probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
+            tsum += softhash_bwd<KB, T>(PK, dPK, sThK, sw, a.L, a.inv_temp, sDproj, ho);
+        }
         __syncthreads();
         dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0, a.T);
     }
