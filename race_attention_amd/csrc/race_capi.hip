@@ -38,18 +38,28 @@ int ok() {
 constexpr int64_t kTargetBlocks = 2048;  // workgroups per scan phase (256 CUs x 8)
 
 struct Plan {
-    int SP = 0, S = 0, R = 0;
+    int SP = 0, S = 0, R = 0, nslice = 1, Spad = 0;
+    bool parts = false;  // fp32 partial outputs + slice sum (sliced<T, KB>() instantiations)
     int64_t N = 0, ntiles = 0;
     int nseg = 0, tps = 0;
     size_t esize = 0;
     size_t state_bytes = 0, fws = 0, bws = 0;
+    size_t fws_core = 0, bws_core = 0, part_bytes = 0;  // partial-output buffers follow the core
 };
 
-// (dtype, SP) pairs compiled into this build: bf16 up to 128 padded buckets,
-// fp32 up to 32 (LDS capacity of the backward tile kernels).
-bool supported(int dtype, int SP) {
-    if (dtype == RACE_DTYPE_BF16) return SP == 32 || SP == 64 || SP == 128;
-    return SP == 32;
+// Bucket slices: a workgroup handles SP buckets (bf16: 32, 64 or 128; fp32:
+// 32, the LDS capacity of the backward tile kernels).  bf16 with K <= 4 and
+// L*2^K <= 128 runs one slice of the padded bucket count; everything else
+// runs ceil(S / SP) slices whose partial outputs are summed.
+void slice_plan(int dtype, int K, int S, int &SP, int &nslice) {
+    if (dtype == RACE_DTYPE_BF16 && K <= 4 && S <= 128) {
+        SP = (S + 31) / 32 * 32;
+        if (SP == 96) SP = 128;
+        nslice = 1;
+        return;
+    }
+    SP = dtype == RACE_DTYPE_BF16 ? 128 : 32;
+    nslice = (S + SP - 1) / SP;
 }
 
 int make_plan(const race_desc *d, Plan &p) {
@@ -61,7 +71,7 @@ int make_plan(const race_desc *d, Plan &p) {
                     (long long)d->B, (long long)d->T, (long long)d->H);
     if (d->D != D) return fail(RACE_E_UNSUPPORTED, "head dim D=%lld unsupported (this build: D=64)", (long long)d->D);
     if (d->L < 1 || d->K < 1) return fail(RACE_E_INVALID, "L and K must be >= 1 (got L=%d K=%d)", d->L, d->K);
-    if (d->K > 4) return fail(RACE_E_UNSUPPORTED, "K=%d hash bits unsupported (K <= 4)", d->K);
+    if (d->K > 8) return fail(RACE_E_UNSUPPORTED, "K=%d hash bits unsupported (K <= 8)", d->K);
     if (d->L * d->K > NCOL)
         return fail(RACE_E_UNSUPPORTED, "L*K=%d projection columns unsupported (L*K <= %d)", d->L * d->K, NCOL);
     if (!(d->eps >= 0.f) || d->eps > 1e30f) return fail(RACE_E_INVALID, "eps must be finite and >= 0");
@@ -71,11 +81,9 @@ int make_plan(const race_desc *d, Plan &p) {
     if (d->phases < 0 || d->phases > 7) return fail(RACE_E_INVALID, "phases must be a RACE_PHASE_* bitmask");
     p.R = 1 << d->K;
     p.S = d->L * p.R;
-    p.SP = (p.S + 31) / 32 * 32;
-    if (!supported(d->dtype, p.SP))
-        return fail(RACE_E_UNSUPPORTED, "L*2^K=%d buckets unsupported for %s (supported padded sizes: %s)", p.S,
-                    d->dtype == RACE_DTYPE_BF16 ? "bf16" : "fp32",
-                    d->dtype == RACE_DTYPE_BF16 ? "32, 64, 128" : "32");
+    slice_plan(d->dtype, d->K, p.S, p.SP, p.nslice);
+    p.Spad = p.nslice * p.SP;
+    p.parts = d->dtype != RACE_DTYPE_BF16 || d->K > 4;
     p.N = d->M * d->B * d->H;
     if (p.N > 65535) return fail(RACE_E_UNSUPPORTED, "M*B*H=%lld streams exceed 65535", (long long)p.N);
     p.ntiles = (d->T + TT - 1) / TT;
@@ -92,10 +100,14 @@ int make_plan(const race_desc *d, Plan &p) {
     if (nseg > (1 << 30)) return fail(RACE_E_UNSUPPORTED, "too many segments");
     p.nseg = (int)nseg;
     p.esize = d->dtype == RACE_DTYPE_BF16 ? 2 : 4;
-    const size_t blk = (size_t)p.SP * SROW;
+    const size_t blk = (size_t)p.Spad * SROW;
     p.state_bytes = (size_t)p.N * (p.nseg + 1) * blk * sizeof(double);
-    p.fws = (size_t)p.N * p.nseg * blk * sizeof(double);
-    p.bws = 2 * (size_t)p.N * p.nseg * blk * sizeof(float) + align16(2 * (size_t)p.N * p.nseg * sizeof(float));
+    p.fws_core = align16((size_t)p.N * p.nseg * blk * sizeof(double));
+    p.bws_core = 2 * (size_t)p.N * p.nseg * blk * sizeof(float) +
+                 align16(2 * (size_t)p.N * p.nseg * p.nslice * sizeof(float));
+    p.part_bytes = p.parts ? (size_t)p.nslice * p.N * d->T * D * sizeof(float) : 0;
+    p.fws = p.fws_core + p.part_bytes;        // partial O
+    p.bws = p.bws_core + 3 * p.part_bytes;    // partial dQ, dK, dV
     return RACE_OK;
 }
 
@@ -139,6 +151,8 @@ Args base_args(const race_desc *d, const Plan &p, const float *planes) {
     a.inv_temp = d->inv_temp;
     a.nseg = p.nseg;
     a.tps = p.tps;
+    a.nslice = p.nslice;
+    a.Spad = p.Spad;
     return a;
 }
 
@@ -150,10 +164,17 @@ int launched(const char *what) {
 
 bool run_phase(const race_desc *d, int ph) { return d->phases == 0 || (d->phases & ph); }
 
+template <typename T>
+void slice_sum(const Plan &p, const race_desc *d, const float *part, const int64_t *st, void *out, hipStream_t s) {
+    const int64_t n4 = p.N * d->T * (D / 4);
+    k_slice_sum<T><<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(part, p.nslice, p.N, d->T, (int)d->B, (int)d->H,
+                                                                Strides{st[0], st[1], st[2], st[3]}, (T *)out);
+}
+
 template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
-    const dim3 grid(p.nseg, (unsigned)p.N);
+    const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
     if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
-    const int elems = SP * SROW;
+    const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
         k_fwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
     if (run_phase(d, RACE_PHASE_OUT)) {
@@ -161,20 +182,22 @@ template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Pla
             k_fwd_out<T, SP, true, KB><<<grid, threads_of(SP), 0, s>>>(a);
         else
             k_fwd_out<T, SP, false, KB><<<grid, threads_of(SP), 0, s>>>(a);
+        if (sliced<T, KB>()) slice_sum<T>(p, d, a.opart, d->o_stride, a.out, s);
     }
     return launched("race_fwd");
 }
 
 template <typename T, int SP, int KB>
 int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hipStream_t s) {
-    const dim3 grid(p.nseg, (unsigned)p.N);
+    const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
         if (d->causal)
             k_bwd_reduce<T, SP, true, KB><<<grid, threads_of(SP), 0, s>>>(a);
         else
             k_bwd_reduce<T, SP, false, KB><<<grid, threads_of(SP), 0, s>>>(a);
+        if (sliced<T, KB>()) slice_sum<T>(p, d, a.dqpart, d->g_stride, a.dq, s);
     }
-    const int elems = SP * SROW;
+    const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
         k_bwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.rstate, a.rdelta, p.nseg, elems,
                                                                             d->causal);
@@ -183,16 +206,22 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
             k_bwd_out<T, SP, true, KB><<<grid, threads_of(SP), 0, s>>>(a);
         else
             k_bwd_out<T, SP, false, KB><<<grid, threads_of(SP), 0, s>>>(a);
-        if (grad_inv_temp) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, 2 * p.N * p.nseg, grad_inv_temp);
+        if (sliced<T, KB>()) {
+            slice_sum<T>(p, d, a.dkpart, d->g_stride, a.dk, s);
+            slice_sum<T>(p, d, a.dvpart, d->g_stride, a.dv, s);
+        }
+        if (grad_inv_temp) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, 2 * p.N * p.nseg * p.nslice, grad_inv_temp);
     }
     return launched("race_bwd");
 }
 
-// Compiled (dtype, padded buckets, hash bits) combinations: every K in 1..4
-// with the padded bucket counts its L*2^K <= 128 and L*K <= 32 allow.
+// Compiled (dtype, slice buckets, hash bits) combinations: every K in 1..8
+// with the slice sizes slice_plan() picks (L*K <= 32).
 #define RACE_FOR_COMBOS(X)                                                                                          \
     X(bf16, 32, 1) X(bf16, 64, 1) X(bf16, 32, 2) X(bf16, 64, 2) X(bf16, 32, 3) X(bf16, 64, 3) X(bf16, 128, 3)       \
-    X(bf16, 32, 4) X(bf16, 64, 4) X(bf16, 128, 4) X(float, 32, 1) X(float, 32, 2) X(float, 32, 3) X(float, 32, 4)
+    X(bf16, 32, 4) X(bf16, 64, 4) X(bf16, 128, 4) X(bf16, 128, 5) X(bf16, 128, 6) X(bf16, 128, 7) X(bf16, 128, 8)   \
+    X(float, 32, 1) X(float, 32, 2) X(float, 32, 3) X(float, 32, 4) X(float, 32, 5) X(float, 32, 6) X(float, 32, 7)  \
+    X(float, 32, 8)
 
 template <typename T> int fwd_dispatch(const race_desc *d, const Plan &p, const Args &a, hipStream_t s) {
 #define X(TT_, SP_, KB_)                                                                                             \
@@ -274,6 +303,7 @@ int race_fwd(const race_desc *d, const void *q, const void *k, const void *v, co
     a.out = out;
     a.fstate = (double *)state;
     a.fdelta = (double *)ws;
+    a.opart = p.parts ? (float *)((char *)ws + p.fws_core) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     if (d->dtype == RACE_DTYPE_BF16) return fwd_dispatch<bf16>(d, p, a, s);
     return fwd_dispatch<float>(d, p, a, s);
@@ -304,10 +334,17 @@ int race_bwd(const race_desc *d, const void *q, const void *k, const void *v, co
     a.dk = dk;
     a.dv = dv;
     a.fstate = (double *)state;
-    const size_t blk = (size_t)p.N * p.nseg * p.SP * SROW;
+    const size_t blk = (size_t)p.N * p.nseg * p.Spad * SROW;
     a.rdelta = (float *)ws;
     a.rstate = a.rdelta + blk;
     a.tpart = a.rstate + blk;
+    if (p.parts) {
+        float *part = (float *)((char *)ws + p.bws_core);
+        const size_t pe = p.part_bytes / sizeof(float);
+        a.dqpart = part;
+        a.dkpart = part + pe;
+        a.dvpart = part + 2 * pe;
+    }
     hipStream_t s = (hipStream_t)stream;
     if (d->dtype == RACE_DTYPE_BF16) return bwd_dispatch<bf16>(d, p, a, grad_inv_temp, s);
     return bwd_dispatch<float>(d, p, a, grad_inv_temp, s);

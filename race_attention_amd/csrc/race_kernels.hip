@@ -35,6 +35,8 @@
 // Bucket probabilities are recomputed in every kernel: projection on MFMA,
 // tanh, then P[t, l, r] = prod_k sigmoid(+-2 u_k), which equals the
 // reference's softmax over the 2^K corner logits.
+#include <type_traits>
+
 #include "race_device.h"
 
 namespace race {
@@ -53,16 +55,26 @@ struct Args {
     int64_t T;
     float eps, inv_temp;
     int nseg, tps;   // segments per stream, tiles per segment
-    double *fstate;  // [N][nseg+1][SP][D+1] exclusive segment prefixes; [nseg] = totals
-    double *fdelta;  // [N][nseg][SP][D+1]
-    float *rdelta;   // [N][nseg][SP][D+1]  per-segment (U, alpha) sums
-    float *rstate;   // [N][nseg][SP][D+1]  exclusive suffixes (non-causal: totals)
-    float *tpart;    // [2][N][nseg] partial sums of dU*th
+    int nslice, Spad;  // bucket slices (grid z) of SP buckets each; Spad = nslice * SP
+    double *fstate;  // [N][nseg+1][Spad][D+1] exclusive segment prefixes; [nseg] = totals
+    double *fdelta;  // [N][nseg][Spad][D+1]
+    float *rdelta;   // [N][nseg][Spad][D+1]  per-segment (U, alpha) sums
+    float *rstate;   // [N][nseg][Spad][D+1]  exclusive suffixes (non-causal: totals)
+    float *tpart;    // [2][N][nseg][nslice] partial sums of dU*th
+    // sliced() instantiations: per-slice fp32 partial outputs [nslice][N][T][D], summed by k_slice_sum
+    float *opart, *dqpart, *dkpart, *dvpart;
 };
 
 constexpr int SROW = D + 1;  // state row: D values of B (or U) then A (or alpha)
 constexpr int WB = 16;       // buckets per wave
 __host__ __device__ constexpr int threads_of(int SP) { return 64 * (SP / WB); }
+
+// Instantiations that may run several bucket slices (fp32, and bf16 with more
+// than 4 hash bits) write fp32 partial outputs; the others write the outputs
+// directly and never read blockIdx.z.
+template <typename T, int KB> __host__ __device__ constexpr bool sliced() {
+    return !std::is_same<T, bf16>::value || KB > 4;
+}
 
 __device__ __forceinline__ int64_t stream_off(const Strides &s, int n, int B, int H) {
     const int h = n % H, b = (n / H) % B, m = n / (H * B);
@@ -435,6 +447,78 @@ template <typename T> __device__ __forceinline__ void mma16_x(f32x4 &c, const Fr
     }
 }
 
+// Tables of 2^KB >= 32 buckets span several waves (and, when 2^KB > SP,
+// several bucket slices).  The corner backward is linear in the buckets:
+//   du_k = sum_r P_r dP_r c_rk - (sum_r P_r dP_r) tanh(u_k),
+// since sum_r P_r c_rk = sigmoid(2u_k) - sigmoid(-2u_k) = tanh(u_k) over a
+// whole table.  Each wave writes its buckets' sums (sum P dP c_k, sum P dP)
+// per token (softhash_share); the waves of a table are then summed in a fixed
+// order (softhash_combine), and slices of a table add up through the partial
+// dQ / dK outputs.
+template <typename T, int KB> struct WideHash {
+    static constexpr size_t bytes(int nw) { return sizeof(float) * nw * TT * (KB + 1); }
+    Frag4<T> cs, ones;  // A operands over the wave's 16 buckets: rows k < KB: c_{s,k}; all ones
+    __device__ __forceinline__ void init(int sg) {
+        const int g = lg(), i = li();
+        f32x4 c, o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = (sg + 4 * g + j) & ((1 << KB) - 1);
+            c[j] = i < KB ? (((r >> (KB - 1 - i)) & 1) ? 1.f : -1.f) : 0.f;
+            o[j] = 1.f;
+        }
+        cs = frag16_acc<T>(c);
+        ones = frag16_acc<T>(o);
+    }
+};
+
+template <int KB, typename T>
+__device__ void softhash_share(const f32x4 (&P)[2], const f32x4 (&dP)[2], const WideHash<T, KB> &wh, float *share) {
+    const int g = lg(), i = li();
+    float *mine = share + wave_id() * TT * (KB + 1);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        f32x4 pd, X = zero4(), Sd = zero4();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pd[e] = P[nt][e] * dP[nt][e];
+        mma16_x<T>(X, wh.cs, pd);    // rows k: sum_s c_{s,k} P dP
+        mma16_x<T>(Sd, wh.ones, pd); // every row: sum_s P dP
+        const int t = 16 * nt + i;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (4 * g + e < KB) mine[t * (KB + 1) + 4 * g + e] = X[e];
+        if (g == 0) mine[t * (KB + 1) + KB] = Sd[0];
+    }
+}
+
+// after the shares are visible: du -> dproj for the slice's tables; returns
+// this thread's part of sum du * th
+template <int KB, typename T, int SP, int NTH>
+__device__ float softhash_combine(const float *share, const float *sp, const float *sm, const float *sth, int z, int L,
+                                  float inv_temp, T *dproj) {
+    constexpr int LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL), R = 1 << KB, NW_ = SP / WB;
+    constexpr int NTAB = SP >= R ? SP / R : 1;          // tables (or one table part) in the slice
+    constexpr int WPT = (R / WB) < NW_ ? R / WB : NW_;  // waves per table in the slice
+    const int l0 = (z * SP) >> KB;
+    float tsum = 0.f;
+    for (int idx = threadIdx.x; idx < TT * NTAB * KB; idx += NTH) {
+        const int t = idx / (NTAB * KB), r = idx % (NTAB * KB), tl = r / KB, k = r % KB;
+        const int l = l0 + tl;
+        if (l >= L) continue;
+        float sx = 0.f, sd = 0.f;
+        for (int ww = tl * WPT; ww < (tl + 1) * WPT; ++ww) {
+            sx += share[(ww * TT + t) * (KB + 1) + k];
+            sd += share[(ww * TT + t) * (KB + 1) + KB];
+        }
+        const int col = l * KB + k;
+        const float th = sth[t * LDC + col];
+        const float du = sx - sd * (sp[t * LDC + col] - sm[t * LDC + col]);
+        tsum += du * th;
+        dproj[t * LDDP + col] = from_f32<T>(du * inv_temp * (1.f - th * th));
+    }
+    return tsum;
+}
+
 // Inclusive token suffix Y and token totals of a bucket-row tile pair on the
 // matrix cores; bf16 splits X into two bf16 parts (fp32-accurate sums).
 template <typename T>
@@ -578,8 +662,9 @@ template <typename T> __device__ void zero_lds(T *p, int n, int nth) {
 
 // dX for the tile: dX^T = planes^T dproj^T, 8 tiles over the workgroup's waves,
 // stored straight to rows t0.. (< T) of dst.
+// part != nullptr: fp32 partial of this bucket slice, rows t0.. of a [T][D] block.
 template <typename T, int NW_>
-__device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64_t t0, int64_t Tn) {
+__device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64_t t0, int64_t Tn, float *part) {
     constexpr int LDDP = ld_of<T>(NCOL);
     const int g = lg(), i = li(), w = wave_id();
     T *base = dst + t0 * st;
@@ -588,7 +673,12 @@ __device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64
         f32x4 acc = zero4();
         tile_mma(acc, plt + 16 * md * LDDP, LDDP, dproj + 16 * nt * LDDP, LDDP, NCOL / 32);
         const int t = 16 * nt + i;
-        if (t0 + t < Tn) store4<T>(at_bytes(base, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
+        if (t0 + t < Tn) {
+            if (part)
+                store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, acc);
+            else
+                store4<T>(at_bytes(base, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
+        }
     }
 }
 
@@ -649,7 +739,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     T *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
     float *sSp = (float *)(smem + Ly::oSig), *sSm = sSp + TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
+              sg = z * SP + sw;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -687,7 +778,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
         for (int q = w; q < 4; q += NW_) project_tile<T>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, nullptr);
         __syncthreads();
         f32x4 PK[2];
-        probs_st<KB>(sSp, sSm, sw, a.S, t0, a.T, PK);
+        probs_st<KB>(sSp, sSm, sg, a.S, t0, a.T, PK);
         const Frag<T> Pf = token_operand<T>(PK, cst);
         f32x4 tot, dB[4];
         tile_sums<T>(Pf, cst, sVt, tot, dB);
@@ -696,11 +787,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
             for (int md = 0; md < 4; ++md) accB[md][e] += (double)dB[md][e];
         }
     }
-    double *out = a.fdelta + ((int64_t)n * a.nseg + seg) * SP * SROW;
+    double *out = a.fdelta + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     for (int md = 0; md < 4; ++md)
-        for (int e = 0; e < 4; ++e) out[sidx(sw + i, 16 * md + 4 * g + e)] = accB[md][e];
+        for (int e = 0; e < 4; ++e) out[sidx(sg + i, 16 * md + 4 * g + e)] = accB[md][e];
     if (i == 0)
-        for (int e = 0; e < 4; ++e) out[sidx(sw + 4 * g + e, D)] = accA[e];
+        for (int e = 0; e < 4; ++e) out[sidx(sg + 4 * g + e, D)] = accA[e];
 }
 
 // exclusive prefix over segments; [nseg] receives the total
@@ -739,7 +830,7 @@ template <typename T, int SP, bool CAUSAL> struct FwdOutL {
 
 template <typename T, int SP, bool CAUSAL>
 __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T *Wts, const T *sVt, T *op,
-                             int64_t st, int64_t t0, int64_t Tn) {
+                             int64_t st, int64_t t0, int64_t Tn, float *part) {
     constexpr int LDS_ = ld_of<T>(SP), LDT = ld_of<T>(TT);
     const int g = lg(), i = li();
     const T *pb = sBT + (16 * md + i) * LDS_ + 8 * g, *pw = Wts + (16 * nt + i) * LDS_ + 8 * g;
@@ -763,7 +854,12 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
         mma(O, ld_frag_pi(sVt + (16 * md + i) * LDT), frag_acc<T>(Sc[0], Sc[1]));
     }
     const int t = 16 * nt + i;
-    if (t0 + t < Tn) buf_st4<T>(tile_rsrc(op + t0 * st, st, Tn - t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T)), O);
+    if (t0 + t < Tn) {
+        if (part)
+            store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, O);
+        else
+            buf_st4<T>(tile_rsrc(op + t0 * st, st, Tn - t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T)), O);
+    }
 }
 
 template <typename T, int SP, bool CAUSAL, int KB>
@@ -776,7 +872,8 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
     float *sSig = (float *)(smem + Ly::oSig);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sSpK = sSig + 2 * TT * LDC, *sSmK = sSig + 3 * TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
+              sg = z * SP + sw;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -786,18 +883,19 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
     T *op = (T *)a.out + stream_off(a.so, n, a.B, a.H);
+    float *opart = sliced<T, KB>() ? a.opart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
     // carried state: causal = prefix at the segment start, non-causal = totals.
     // B in bucket-row layout: lane holds B[s = sw + 4g + e][d = 16md + i]
-    const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * SP * SROW;
+    const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * a.Spad * SROW;
     f32x4 Bc[4];
     double a0[4];
     for (int e = 0; e < 4; ++e) {
-        for (int md = 0; md < 4; ++md) Bc[md][e] = (float)st[sidx(sw + 4 * g + e, 16 * md + i)];
-        a0[e] = st[sidx(sw + 4 * g + e, D)];
+        for (int md = 0; md < 4; ++md) Bc[md][e] = (float)st[sidx(sg + 4 * g + e, 16 * md + i)];
+        a0[e] = st[sidx(sg + 4 * g + e, D)];
     }
     if constexpr (!CAUSAL) store_ds<T>(sBT, LDS_, sw, Bc);  // constant totals
 
@@ -836,9 +934,9 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
         Frag<T> Pf;
-        probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
+        probs_st<KB>(sSpQ, sSmQ, sg, a.S, t0, a.T, PQ);
         if constexpr (CAUSAL) {
-            probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
+            probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PK);
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
             Pf = token_operand<T>(PK, cst);
@@ -862,7 +960,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         }
         __syncthreads();
         for (int q = w; q < 8; q += NW_)
-            fwd_out_tile<T, SP, CAUSAL>(q >> 1, q & 1, sBT, sPts, sWts, sVt, op, a.so.t, t0, a.T);
+            fwd_out_tile<T, SP, CAUSAL>(q >> 1, q & 1, sBT, sPts, sWts, sVt, op, a.so.t, t0, a.T, opart);
         if constexpr (CAUSAL) {
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
             for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, ld_frag_pi(sVt + (16 * md + i) * LDT));
@@ -875,7 +973,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 // k_bwd_reduce: forward walk.  dQ, and per-segment sums of
 // alpha = sum_t dA and U = sum_t W^T g.
 // =====================================================================
-template <typename T, int SP, bool CAUSAL> struct BwdReduceL {
+template <typename T, int SP, bool CAUSAL, int KB> struct BwdReduceL {
     static constexpr int NW_ = SP / WB;
     static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
     static constexpr size_t oQ = 0;
@@ -893,12 +991,13 @@ template <typename T, int SP, bool CAUSAL> struct BwdReduceL {
     static constexpr size_t oRed = align16(oSig + sizeof(float) * 5 * TT * LDC);
     static constexpr size_t oCst = align16(oRed + sizeof(float) * 64 * NW_);
     static constexpr size_t oHash = align16(oCst + Consts<T>::bytes);
-    static constexpr size_t bytes = align16(oHash + HashOps<T, 4>::bytes);
+    static constexpr size_t oShare = align16(oHash + HashOps<T, 4>::bytes);
+    static constexpr size_t bytes = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
 };
 
 template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
-    using Ly = BwdReduceL<T, SP, CAUSAL>;
+    using Ly = BwdReduceL<T, SP, CAUSAL, KB>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     constexpr int NTASK = CAUSAL ? 11 : 4;  // Q projection (4), K projection (4), X tiles (3)
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
@@ -909,7 +1008,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sThQ = sSig + 2 * TT * LDC;
     float *sSpK = sSig + 3 * TT * LDC, *sSmK = sSig + 4 * TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
+              sg = z * SP + sw;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -920,24 +1020,30 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
     const T *gp = (const T *)a.dout + stream_off(a.sdo, n, a.B, a.H);
     T *dqp = (T *)a.dq + stream_off(a.sg, n, a.B, a.H);
+    float *xpart = sliced<T, KB>() ? a.dqpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
     HashOps<T, KB> ho;
-    ho.init((T *)(smem + Ly::oHash), NTH);
+    WideHash<T, KB> wh;
+    float *sShare = (float *)(smem + Ly::oShare);
+    if constexpr (KB <= 4)
+        ho.init((T *)(smem + Ly::oHash), NTH);
+    else
+        wh.init(sg);
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
     zero_lds<T>(sDproj, TT * LDDP, NTH);
     if constexpr (CAUSAL) zero_lds<T>(sX, TT * LDT, NTH);
     // forward state in d-row layout: lane holds B^T[d = 16md + 4g + e][s = sw + i]
-    const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * SP * SROW;
+    const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * a.Spad * SROW;
     f32x4 Bt[4], Ut[4];
     double a0[4], al[4];
     for (int md = 0; md < 4; ++md) {
         Ut[md] = zero4();
-        for (int e = 0; e < 4; ++e) Bt[md][e] = (float)st[sidx(sw + i, 16 * md + 4 * g + e)];
+        for (int e = 0; e < 4; ++e) Bt[md][e] = (float)st[sidx(sg + i, 16 * md + 4 * g + e)];
     }
     for (int e = 0; e < 4; ++e) {
-        a0[e] = st[sidx(sw + 4 * g + e, D)];
+        a0[e] = st[sidx(sg + 4 * g + e, D)];
         al[e] = 0.0;
     }
     float tsum = 0.f;
@@ -984,9 +1090,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2], tot;
         Frag<T> Pf;
-        probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
+        probs_st<KB>(sSpQ, sSmQ, sg, a.S, t0, a.T, PQ);
         if constexpr (CAUSAL) {
-            probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
+            probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PK);
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
             Pf = token_operand<T>(PK, cst);
@@ -1032,17 +1138,23 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         }
         if constexpr (CAUSAL)
             for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
-        tsum += softhash_bwd<KB, T>(PQ, dPQ, sThQ, sw, a.L, a.inv_temp, sDproj, ho);
+        if constexpr (KB <= 4) {
+            tsum += softhash_bwd<KB, T>(PQ, dPQ, sThQ, sg, a.L, a.inv_temp, sDproj, ho);
+        } else {
+            softhash_share<KB, T>(PQ, dPQ, wh, sShare);
+            __syncthreads();
+            tsum += softhash_combine<KB, T, SP, NTH>(sShare, sSpQ, sSmQ, sThQ, z, a.L, a.inv_temp, sDproj);
+        }
         __syncthreads();
-        dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0, a.T);
+        dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0, a.T, xpart);
     }
-    float *out = a.rdelta + ((int64_t)n * a.nseg + seg) * SP * SROW;
+    float *out = a.rdelta + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     for (int md = 0; md < 4; ++md)
-        for (int e = 0; e < 4; ++e) out[sidx(sw + i, 16 * md + 4 * g + e)] = Ut[md][e];
+        for (int e = 0; e < 4; ++e) out[sidx(sg + i, 16 * md + 4 * g + e)] = Ut[md][e];
     if (i == 0)
-        for (int e = 0; e < 4; ++e) out[sidx(sw + 4 * g + e, D)] = (float)al[e];
+        for (int e = 0; e < 4; ++e) out[sidx(sg + 4 * g + e, D)] = (float)al[e];
     const float ts = block_sum<NTH>(tsum, sRed);
-    if (threadIdx.x == 0) a.tpart[(int64_t)n * a.nseg + seg] = ts;
+    if (threadIdx.x == 0) a.tpart[((int64_t)n * a.nseg + seg) * a.nslice + z] = ts;
 }
 
 // exclusive suffix over segments (causal) or totals (non-causal)
@@ -1067,7 +1179,7 @@ __global__ void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int ele
 // Sc2[t][tau] = sum_s W[t][s] P_K[tau][s], computed as output tiles over all
 // buckets from the waves' [.][s] LDS arrays; dK through each wave's buckets.
 // =====================================================================
-template <typename T, int SP, bool CAUSAL> struct BwdOutL {
+template <typename T, int SP, bool CAUSAL, int KB> struct BwdOutL {
     static constexpr int NW_ = SP / WB;
     static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL),
                          LDS_ = ld_of<T>(SP);
@@ -1091,12 +1203,13 @@ template <typename T, int SP, bool CAUSAL> struct BwdOutL {
     static constexpr size_t oCst = align16(oRed + sizeof(float) * 64 * NW_);
     static constexpr size_t oHash = align16(oCst + Consts<T>::bytes);
     static constexpr size_t oSuf = align16(oHash + HashOps<T, 4>::bytes);
-    static constexpr size_t bytes = align16(oSuf + (CAUSAL ? SufOps<T>::bytes : 0));
+    static constexpr size_t oShare = align16(oSuf + (CAUSAL ? SufOps<T>::bytes : 0));
+    static constexpr size_t bytes = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
 };
 
 template <typename T, int SP, bool CAUSAL>
 __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts, const T *sGt, T *dvp, int64_t st,
-                        int64_t t0, int64_t Tn) {
+                        int64_t t0, int64_t Tn, float *part) {
     constexpr int LDS_ = ld_of<T>(SP), LDT = ld_of<T>(TT);
     const int g = lg(), i = li();
     const T *pu = sUT + (16 * md + i) * LDS_ + 8 * g, *pp = Pts + (16 * nt + i) * LDS_ + 8 * g;
@@ -1120,12 +1233,17 @@ __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts
         mma(acc, ld_frag_pi(sGt + (16 * md + i) * LDT), frag_acc<T>(Sc2[0], Sc2[1]));
     }
     const int t = 16 * nt + i;
-    if (t0 + t < Tn) store4<T>(at_bytes(dvp + t0 * st, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
+    if (t0 + t < Tn) {
+        if (part)
+            store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, acc);
+        else
+            store4<T>(at_bytes(dvp + t0 * st, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
+    }
 }
 
 template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
-    using Ly = BwdOutL<T, SP, CAUSAL>;
+    using Ly = BwdOutL<T, SP, CAUSAL, KB>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
                   LDS_ = Ly::LDS_;
     constexpr int NTASK = CAUSAL ? 14 : 4;  // K projection (4), Q projection (4), X and Y tiles (6)
@@ -1139,7 +1257,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
     float *sSpK = sSig, *sSmK = sSig + TT * LDC, *sThK = sSig + 2 * TT * LDC;
     float *sSpQ = sSig + 3 * TT * LDC, *sSmQ = sSig + 4 * TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = WB * w;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
+              sg = z * SP + sw;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -1151,11 +1270,18 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     const T *gp = (const T *)a.dout + stream_off(a.sdo, n, a.B, a.H);
     T *dkp = (T *)a.dk + stream_off(a.sg, n, a.B, a.H);
     T *dvp = (T *)a.dv + stream_off(a.sg, n, a.B, a.H);
+    float *xpart = sliced<T, KB>() ? a.dkpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
+    float *vpart = sliced<T, KB>() ? a.dvpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
     HashOps<T, KB> ho;
-    ho.init((T *)(smem + Ly::oHash), NTH);
+    WideHash<T, KB> wh;
+    float *sShare = (float *)(smem + Ly::oShare);
+    if constexpr (KB <= 4)
+        ho.init((T *)(smem + Ly::oHash), NTH);
+    else
+        wh.init(sg);
     SufOps<T> sufo;
     if constexpr (CAUSAL) sufo.init((T *)(smem + Ly::oSuf), NTH);
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
@@ -1165,20 +1291,20 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         zero_lds<T>(sY, TT * LDT, NTH);
     }
     // reverse carries (U, alpha) after the segment; forward state at the segment end
-    const float *rs = a.rstate + ((int64_t)n * a.nseg + seg) * SP * SROW;
-    const double *fs = a.fstate + ((int64_t)n * (a.nseg + 1) + seg + 1) * SP * SROW;
+    const float *rs = a.rstate + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
+    const double *fs = a.fstate + ((int64_t)n * (a.nseg + 1) + seg + 1) * a.Spad * SROW;
     f32x4 Ut[4];  // U^T[d = 16md + 4g + e][s = sw + i]
     double Be[4][4], Ae[4];
     float al[4];
     for (int md = 0; md < 4; ++md)
         for (int e = 0; e < 4; ++e) {
-            const int64_t r = sidx(sw + i, 16 * md + 4 * g + e);
+            const int64_t r = sidx(sg + i, 16 * md + 4 * g + e);
             Ut[md][e] = rs[r];
             Be[md][e] = CAUSAL ? fs[r] : 0.0;
         }
     for (int e = 0; e < 4; ++e) {
-        al[e] = rs[sidx(sw + 4 * g + e, D)];
-        Ae[e] = CAUSAL ? fs[sidx(sw + 4 * g + e, D)] : 0.0;
+        al[e] = rs[sidx(sg + 4 * g + e, D)];
+        Ae[e] = CAUSAL ? fs[sidx(sg + 4 * g + e, D)] : 0.0;
     }
     if constexpr (!CAUSAL) store_ut<T>(sUT, LDS_, sw, Ut, cst);  // constant totals
     float tsum = 0.f;
@@ -1230,7 +1356,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         }
         __syncthreads();
         f32x4 PKr[2];  // operand-rounded P_K (fp32 P_K is rebuilt for the softmax backward)
-        probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PKr);
+        probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PKr);
         for (int nt = 0; nt < 2; ++nt)
             for (int e = 0; e < 4; ++e) PKr[nt][e] = as_operand<T>(PKr[nt][e]);
         const Frag<T> Pf = token_operand<T>(PKr, cst);
@@ -1241,7 +1367,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             Frag<T> Wf;
             {
                 f32x4 PQ[2], Acum[2], W[2], tot, dB[4];
-                probs_st<KB>(sSpQ, sSmQ, sw, a.S, t0, a.T, PQ);
+                probs_st<KB>(sSpQ, sSmQ, sg, a.S, t0, a.T, PQ);
                 // forward state at the tile start: end state minus this tile's sums
                 tile_sums<T>(Pf, cst, sVt, tot, dB);
                 for (int e = 0; e < 4; ++e) {
@@ -1300,12 +1426,12 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             // ---- U^T[d][s] += sum_t g[t][d] W[t][s]  (the dV tiles read the LDS copy of U)
             for (int md = 0; md < 4; ++md) mma(Ut[md], ld_frag_pi(sGt + (16 * md + i) * LDT), Wf);
             for (int q = w; q < 8; q += NW_)
-                dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T);
+                dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T, vpart);
         } else {
             __syncthreads();  // all waves' P_K rows in LDS
             // non-causal: dV^T = U^T P_K^T; dP_K = alpha + v . U (totals)
             for (int q = w; q < 8; q += NW_)
-                dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, nullptr, nullptr, dvp, a.sg.t, t0, a.T);
+                dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, nullptr, nullptr, dvp, a.sg.t, t0, a.T, vpart);
             const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
             for (int nt = 0; nt < 2; ++nt) {
                 f32x4 c = zero4();
@@ -1316,14 +1442,35 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         }
         {
             f32x4 PK[2];
-            probs_st<KB>(sSpK, sSmK, sw, a.S, t0, a.T, PK);
-            tsum += softhash_bwd<KB, T>(PK, dPK, sThK, sw, a.L, a.inv_temp, sDproj, ho);
+            probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PK);
+            if constexpr (KB <= 4) {
+                tsum += softhash_bwd<KB, T>(PK, dPK, sThK, sg, a.L, a.inv_temp, sDproj, ho);
+            } else {
+                softhash_share<KB, T>(PK, dPK, wh, sShare);
+                __syncthreads();
+                tsum += softhash_combine<KB, T, SP, NTH>(sShare, sSpK, sSmK, sThK, z, a.L, a.inv_temp, sDproj);
+            }
         }
         __syncthreads();
-        dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0, a.T);
+        dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0, a.T, xpart);
     }
     const float ts = block_sum<NTH>(tsum, sRed);
-    if (threadIdx.x == 0) a.tpart[(int64_t)(a.M * a.B * a.H + n) * a.nseg + seg] = ts;
+    if (threadIdx.x == 0) a.tpart[((int64_t)(a.M * a.B * a.H + n) * a.nseg + seg) * a.nslice + z] = ts;
+}
+
+// Sum of the per-slice fp32 partials [nslice][N][T][D] in slice order,
+// written to the strided output (4 consecutive d per thread).
+template <typename T>
+__global__ void k_slice_sum(const float *part, int nslice, int64_t N, int64_t Tn, int B, int H, Strides so, T *out) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over N * T * D/4
+    const int64_t per = Tn * (D / 4);
+    if (idx >= N * per) return;
+    const int64_t n = idx / per, r = idx % per, t = r / (D / 4);
+    const int d0 = 4 * (int)(r % (D / 4));
+    const int64_t row = (n * Tn + t) * D + d0, zs = N * Tn * D;
+    f32x4 acc = *reinterpret_cast<const f32x4 *>(part + row);
+    for (int z = 1; z < nslice; ++z) acc += *reinterpret_cast<const f32x4 *>(part + z * zs + row);
+    store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc);
 }
 
 // grad_inv_temp = sum of all partials, in a fixed order

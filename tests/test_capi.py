@@ -61,7 +61,7 @@ def test_plan_sizes_c4():
 
 @pytest.mark.parametrize("field,value,code,msg", [
     ("D", 32, -2, "head dim"),
-    ("K", 5, -2, "hash bits"),
+    ("K", 9, -2, "hash bits"),
     ("L", 9, -2, "projection columns"),
     ("L", 0, -1, "L and K"),
     ("T", 0, -1, "must be >= 1"),
@@ -77,11 +77,33 @@ def test_invalid_descriptors_rejected(field, value, code, msg):
     assert msg in _lib.last_error()
 
 
-def test_fp32_large_bucket_count_unsupported():
+def _plan(**kw):
     lib = _lib.load()
-    d = _desc(dtype=_lib.RACE_DTYPE_F32)
-    assert lib.race_state_bytes(ctypes.byref(d)) == 0
-    assert "fp32" in _lib.last_error()
+    d = _desc(**kw)
+    return (lib.race_state_bytes(ctypes.byref(d)), lib.race_fwd_workspace_bytes(ctypes.byref(d)),
+            lib.race_bwd_workspace_bytes(ctypes.byref(d)))
+
+
+@pytest.mark.parametrize("dtype,K,L,M,B,H,T,spad", [
+    # fp32: slices of 32 buckets, L*2^K = 128 -> 4 slices
+    (_lib.RACE_DTYPE_F32, 4, 8, 1, 1, 8, 4096, 128),
+    # bf16, 2^K > 16: slices of 128 buckets; the decoder config's K=8, L=4
+    # (1024 buckets, 8 slices), M=2 estimators, 8 x 12 heads
+    (_lib.RACE_DTYPE_BF16, 8, 4, 2, 8, 12, 8192, 1024),
+    (_lib.RACE_DTYPE_BF16, 5, 6, 1, 1, 2, 1000, 256),
+])
+def test_sliced_plans(dtype, K, L, M, B, H, T, spad):
+    """Bucket counts beyond one workgroup run as slices: the state holds every
+    (padded) bucket, and the workspaces add fp32 per-slice partial outputs
+    (O forward; dQ, dK, dV backward)."""
+    sb, fw, bw = _plan(dtype=dtype, K=K, L=L, M=M, B=B, H=H, T=T)
+    N = M * B * H
+    row = spad * 65
+    assert sb > 0 and sb % (N * row * 8) == 0
+    nseg = sb // (N * row * 8) - 1
+    part = (spad // (32 if dtype == _lib.RACE_DTYPE_F32 else 128)) * N * T * 64 * 4
+    assert fw >= N * nseg * row * 8 + part
+    assert bw >= 2 * N * nseg * row * 4 + 3 * part
 
 
 def test_null_and_misaligned_pointers_rejected():

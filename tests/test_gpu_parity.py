@@ -175,6 +175,20 @@ CASES = [
     ("causal_bf16_T32", dict(T=32, H=1, L=8, K=4), True, None, 0),
     ("causal_bf16_T33", dict(T=33, H=1, L=8, K=4), True, None, 0),
     ("causal_fp32_T31", dict(T=31, H=1, L=5, K=2, dtype=torch.float32, unit=False), True, 1.0, 0),
+    # Bucket slices (grid z): bf16 with 2^K > 16 runs slices of 128 buckets,
+    # fp32 slices of 32; partial outputs are summed per slice.  A table can
+    # span several waves (K=5, 6), fill a slice (K=7) or span several slices
+    # (K=8), and the last slice can be partly padding.
+    ("causal_bf16_K5L6_2slices", dict(T=150, H=2, L=6, K=5), True, None, 0),
+    ("noncausal_bf16_K6L3_pad", dict(T=120, H=1, L=3, K=6), False, 1.0, 0),
+    ("causal_bf16_K7L1_1slice", dict(T=64, H=1, L=1, K=7), True, None, 0),
+    ("causal_bf16_K8L4_M2", dict(M=2, T=100, H=2, L=4, K=8, share_planes=False), True, None, 0),
+    ("causal_bf16_K8L4_seg", dict(T=300, H=1, L=4, K=8), True, None, 2),
+    ("noncausal_bf16_K8L2", dict(T=90, H=2, L=2, K=8), False, None, 0),
+    ("causal_fp32_K4L8_4slices", dict(T=140, H=2, L=8, K=4, dtype=torch.float32, unit=False), True, 1.0, 0),
+    ("causal_fp32_K3L5_pad", dict(T=90, H=1, L=5, K=3, dtype=torch.float32, unit=False), True, 0.5, 0),
+    ("noncausal_fp32_K5L3", dict(T=100, H=1, L=3, K=5, dtype=torch.float32, unit=False), False, 1.0, 2),
+    ("causal_fp32_K8L2_16slices", dict(T=70, H=1, L=2, K=8, dtype=torch.float32, unit=False), True, 0.5, 0),
 ]
 
 
@@ -247,3 +261,21 @@ def test_config_c2(dev):
     gpu = _run_gpu(q, k, v, do, planes, L=8, K=4, causal=True, inv_temp=it, dev=dev)
     ref = _run_oracle(q, k, v, do, planes, causal=True, inv_temp=it)
     _compare("C2", gpu, ref, 2e-2)
+
+
+def test_config_c5_attention(dev):
+    """C5's attention layer at full shape: causal bf16, K=8 (256 buckets),
+    L=4, M=2 independent sketches, B=8, 12 heads, N=8192, d=64 -- 8 bucket
+    slices per stream.  Streams are independent, so two heads of the first
+    batch row of each estimator are checked against the oracle."""
+    M, B, T, H, L, K = 2, 8, 8192, 12, 4, 8
+    q, k, v, do, planes = make_case(M=M, B=B, T=T, H=H, L=L, K=K, seed=21, share_planes=False)
+    it = 1.0 / 8.0
+    out, dq, dk, dv, _ = _run_gpu(q, k, v, do, planes, L=L, K=K, causal=True, inv_temp=it, dev=dev)
+    sub = lambda x: x[:, :1, :, :2]  # noqa: E731
+    ref = _run_oracle(sub(q), sub(k), sub(v), sub(do), planes, causal=True, inv_temp=it)
+    errs = {nm: relerr(to64(sub(a)), b) for nm, a, b in zip(("out", "dq", "dk", "dv"), (out, dq, dk, dv), ref[:4])}
+    print("[C5 attention] " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
+    for x in (out, dq, dk, dv):
+        assert torch.isfinite(x).all()
+    assert max(errs.values()) <= TOL[torch.bfloat16]
