@@ -17,7 +17,13 @@ path (aten + kernels/cpu/race_pref.cpp compiled from source) on a bounded
 sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--seq N] [--no-cpu-baseline] [--max-n]
-                    [--copy-calib MIB]
+                    [--copy-calib MIB] [--workload c4|c5]
+
+--workload c5 times the attention core of BASELINE configs[4] instead (the
+GPT-style decoder's layer: causal, K=8 so 256 buckets per table, L=4, M=2
+estimators with independent hyperplanes over Q/K/V expanded with stride 0,
+B=8, 12 heads, N=8192, d=64, bf16): 1024 buckets run as 8 bucket slices.
+The default (c4) line is the headline metric.
 
 --copy-calib MIB ends the run with one device-to-device copy of MIB MiB, the
 known-size kernel against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters
@@ -57,10 +63,13 @@ def parse():
     ap.add_argument("--max-n", action="store_true", help="also bisect the longest sequence that fits in HBM")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="finish with a device-to-device copy of MIB MiB (PMC calibration)")
+    ap.add_argument("--workload", choices=("c4", "c5"), default="c4")
     return ap.parse_args()
 
 
-def make_inputs(B, T, H, D, L, K, dev, seed=0):
+def make_inputs(B, T, H, D, L, K, dev, seed=0, M=1):
+    """Q, K, V [M,B,T,H,D] (one [B,T,H,D] tensor expanded over M with stride
+    0, as the modules pass them), dO [M,B,T,H,D], planes [M,L,K,D] fp32."""
     import torch
     g = torch.Generator(device="cpu").manual_seed(seed)
     out = []
@@ -71,14 +80,15 @@ def make_inputs(B, T, H, D, L, K, dev, seed=0):
             t1 = min(T, t0 + step)
             c = torch.randn(B, t1 - t0, H, D, generator=g)
             x[:, t0:t1] = torch.nn.functional.normalize(c, dim=-1).to(torch.bfloat16).to(dev)
-        out.append(x.unsqueeze(0))
-    do = torch.empty(1, B, T, H, D, dtype=torch.bfloat16, device=dev)
+        out.append(x.unsqueeze(0).expand(M, -1, -1, -1, -1))
+    do = torch.empty(M, B, T, H, D, dtype=torch.bfloat16, device=dev)
     step = 1 << 18
-    for t0 in range(0, T, step):
-        t1 = min(T, t0 + step)
-        do[0, :, t0:t1] = torch.randn(B, t1 - t0, H, D, generator=g).to(torch.bfloat16).to(dev)
+    for m in range(M):
+        for t0 in range(0, T, step):
+            t1 = min(T, t0 + step)
+            do[m, :, t0:t1] = torch.randn(B, t1 - t0, H, D, generator=g).to(torch.bfloat16).to(dev)
     gp = torch.Generator(device="cpu").manual_seed(1234)
-    planes = torch.randn(1, L, K, D, generator=gp).to(dev)
+    planes = torch.randn(M, L, K, D, generator=gp).to(dev)
     return out[0], out[1], out[2], do, planes
 
 
@@ -92,8 +102,9 @@ class Step:
         self.lib = _lib.load()
         self.q, self.k, self.v, self.do, self.planes = q, k, v, do, planes.float().contiguous()
         self.d = make_desc(q, k, v, self.planes, L=L, K=K, causal=True, eps=1e-6, inv_temp=1.0 / math.sqrt(q.shape[-1]))
-        self.out = torch.empty_like(q)
-        self.dq, self.dk, self.dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+        new = lambda: torch.empty(q.shape, dtype=q.dtype, device=q.device)  # noqa: E731  (q may be an M-expand)
+        self.out = new()
+        self.dq, self.dk, self.dv = new(), new(), new()
         self.d.o_stride = _strides4(self.out)
         self.d.do_stride = _strides4(do)
         self.d.g_stride = _strides4(self.dq)
@@ -155,7 +166,7 @@ def cpu_baseline(sample_T, H_full, D=64, L=8, K=4, reps=16):
             out.backward(dof)
             return time.perf_counter() - t0
 
-        run(8192, 6)  # warm-up: thread pool, allocator
+        run(min(8192, sample_T), 6)  # warm-up: thread pool, allocator
         times = [run(sample_T, 7 + r) for r in range(reps)]
         kind = "reference"
         what = "misc/race.py CPU path: aten projection/softmax/readout + kernels/cpu/race_pref.cpp (built from source)"
@@ -174,9 +185,9 @@ def cpu_baseline(sample_T, H_full, D=64, L=8, K=4, reps=16):
         threads = 1
     t = statistics.median(times)
     return {"value": sample_T / t / H_full, "unit": "tokens/s", "cores": threads, "kind": kind,
-            "sample": f"1 of {H_full} heads x {sample_T} tokens of the same causal K=4 L=8 d=64 workload, "
+            "sample": f"1 of {H_full} streams x {sample_T} tokens of the same causal K={K} L={L} d={D} workload, "
                       f"fwd+bwd, median of {reps} runs after a warm-up ({what}); {t:.2f} s per run; "
-                      f"value scaled to tokens of the {H_full}-head layer",
+                      f"value scaled to tokens of the {H_full}-stream layer",
             "host_cpus": os.cpu_count(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
 
@@ -228,9 +239,14 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
-    B, T, H, D, L, K = 1, args.seq, args.heads, 64, 8, 4
-    print(f"bench: generating inputs B={B} T={T} H={H} D={D}", file=sys.stderr, flush=True)
-    q, k, v, do, planes = make_inputs(B, T, H, D, L, K, dev)
+    if args.workload == "c5":
+        M, B, T, H, D, L, K = 2, 8, 8192, 12, 64, 4, 8
+        wl = "C5 decoder attention core fwd+bwd"
+    else:
+        M, B, T, H, D, L, K = 1, 1, args.seq, args.heads, 64, 8, 4
+        wl = "C4 causal RACE layer core fwd+bwd"
+    print(f"bench: generating inputs M={M} B={B} T={T} H={H} D={D} L={L} K={K}", file=sys.stderr, flush=True)
+    q, k, v, do, planes = make_inputs(B, T, H, D, L, K, dev, M=M)
     step = Step(q, k, v, do, planes, L, K)
     for _ in range(args.warmup):
         step.run()
@@ -253,7 +269,7 @@ def main():
     tokens = B * T
     value = tokens / (ms / 1e3)
 
-    tok_heads = B * T * H
+    tok_heads = M * B * T * H  # token-streams: each (m, b, h) stream reads its own Q, K, V rows
     kernels = {}
     for name, t_ms in per.items():
         ab = algorithmic_bytes(name, tok_heads, D, 2)
@@ -263,8 +279,8 @@ def main():
     ab = algorithmic_bytes(dom, tok_heads, D, 2)
     achieved = ab / (per[dom] * 1e-3) / 1e9
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"traffic_{dom}_c4.txt")
-    if os.path.exists(tfile) and T == 1 << 20:
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{dom}_{args.workload}.txt")
+    if os.path.exists(tfile) and (args.workload != "c4" or T == 1 << 20):
         for ln in open(tfile):
             if ln.startswith("hbm_bytes_per_launch"):
                 traffic = float(ln.split("=")[1])
@@ -274,8 +290,8 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (unit-L2 N(0,1) Q/K/V, N(0,1) dO and hyperplanes, seeds 0/1234)",
-        "config": {"workload": f"C4 causal RACE layer core fwd+bwd: B={B} H={H} N={T} d={D} K={K} L={L} M=1 bf16",
-                   "B": B, "H": H, "seq_len": T, "d": D, "K": K, "L": L, "M": 1, "causal": True},
+        "config": {"workload": f"{wl}: B={B} H={H} N={T} d={D} K={K} L={L} M={M} bf16",
+                   "B": B, "H": H, "seq_len": T, "d": D, "K": K, "L": L, "M": M, "causal": True},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "layer_roofline": {"algorithmic_bytes_per_step": all_bytes,
@@ -297,7 +313,10 @@ def main():
         res["max_seq_len_fwd_bwd"] = max_seq_bisect(H, D, L, K, dev)
     if not args.no_cpu_baseline:
         print("bench: CPU baseline", file=sys.stderr, flush=True)
-        res["cpu_baseline"] = cpu_baseline(args.cpu_sample, H)
+        if args.workload == "c4":
+            res["cpu_baseline"] = cpu_baseline(args.cpu_sample, H * M, D=D, L=L, K=K)
+        else:  # 1024 buckets: the reference's flat layout holds 256 KB per token
+            res["cpu_baseline"] = cpu_baseline(min(args.cpu_sample, 2048), H * M, D=D, L=L, K=K, reps=8)
     print(json.dumps(res), flush=True)
 
 

@@ -28,6 +28,12 @@ constexpr int NCOL = 32;    // projection columns (L*K <= 32)
 
 // padded leading dimension (elements) of an LDS array with n logical columns
 template <typename T> __host__ __device__ constexpr int ld_of(int n) { return n + 16 / (int)sizeof(T); }
+// Leading dimension of rows that are read only as pi-order operand pairs
+// (8 bytes at k = 4g and at k = 16 + 4g for bf16, ds_read2_b64) and written in
+// 4- or 8-byte pieces.  ds_read_b64 serves 16 consecutive lanes per pass over
+// 32 four-byte banks, so the 16 rows of one read are conflict-free when the
+// row pitch is 8 (mod 16) bytes: a 4-element pad, 72-byte bf16 rows of 32.
+template <typename T> __host__ __device__ constexpr int ldp_of(int n) { return n + 4; }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }

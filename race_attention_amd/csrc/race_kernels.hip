@@ -159,6 +159,12 @@ template <> struct ChunkOf<8> { typedef uint2 type; };
 
 // Chunks of 16 bytes, or of 8 bytes when 16-byte chunks would leave some of
 // the workgroup's threads without one (every wave shares the staging work).
+// rows of the tile at t0 that exist (0 .. TT), as a wave-uniform 32-bit count
+__device__ __forceinline__ int tile_rows(int64_t t0, int64_t Tn) {
+    const int64_t r = Tn - t0;
+    return r < 0 ? 0 : (r > TT ? TT : (int)r);
+}
+
 template <typename T, int NTH> struct Prefetch {
     static constexpr int CB = (TT * D * (int)sizeof(T) / 16 >= NTH) ? 16 : 8;
     typedef typename ChunkOf<CB>::type chunk_t;
@@ -169,15 +175,16 @@ template <typename T, int NTH> struct Prefetch {
     // 32-bit (the host bounds 32 * token stride below 2^31)
     __device__ __forceinline__ void issue(const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn) {
         const T *base = src + t0 * st;
+        const int rem = tile_rows(t0, Tn);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int idx = threadIdx.x + j * NTH, t = idx / CPR, c = idx % CPR;
             v[j] = chunk_t{};
-            if (idx < CHUNKS && t0 + t < Tn) v[j] = ld_at<chunk_t>(base, tile_off(t, st, c * EPC, sizeof(T)));
+            if (idx < CHUNKS && t < rem) v[j] = ld_at<chunk_t>(base, tile_off(t, st, c * EPC, sizeof(T)));
         }
     }
     __device__ __forceinline__ void commit(T *nat, T *trn) const {
-        constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT);
+        constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int idx = threadIdx.x + j * NTH, t = idx / CPR, c = idx % CPR;
@@ -211,6 +218,7 @@ template <typename T, int NTH, int NPART> struct PrefetchT {
     }
     __device__ __forceinline__ void issue(int part, const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn) {
         const T *base = src + t0 * st;
+        const int rem = tile_rows(t0, Tn);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             int tp, c;
@@ -218,12 +226,12 @@ template <typename T, int NTH, int NPART> struct PrefetchT {
             const uint32_t off = tile_off(2 * tp, st, c * EPC, sizeof(T));
             v[j][0] = uint2{0, 0};
             v[j][1] = uint2{0, 0};
-            if (ok && t0 + 2 * tp < Tn) v[j][0] = ld_at<uint2>(base, off);
-            if (ok && t0 + 2 * tp + 1 < Tn) v[j][1] = ld_at<uint2>(base, off + (uint32_t)st * (uint32_t)sizeof(T));
+            if (ok && 2 * tp < rem) v[j][0] = ld_at<uint2>(base, off);
+            if (ok && 2 * tp + 1 < rem) v[j][1] = ld_at<uint2>(base, off + (uint32_t)st * (uint32_t)sizeof(T));
         }
     }
     __device__ __forceinline__ void commit(int part, T *nat, T *trn) const {
-        constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT);
+        constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             int tp, c;
@@ -361,7 +369,7 @@ template <> __device__ __forceinline__ Frag<float> frag_pi_from<float>(const flo
 //                 all ones: token totals, replicated over the columns)
 //   id[s][s']   = (s == s'): 16-deep identity for transposes
 template <typename T> struct Consts {
-    static constexpr int LDT = ld_of<T>(TT), LDI = ld_of<T>(16);
+    static constexpr int LDT = ldp_of<T>(TT), LDI = ldp_of<T>(16);
     static constexpr size_t bytes = sizeof(T) * (TT * LDT + 16 * LDI);
     const T *tri, *id;
     __device__ __forceinline__ void init(T *buf, int nth) {
@@ -379,7 +387,7 @@ template <typename T> struct Consts {
 };
 // suf[t][tau] = (tau >= t): column t = 16nt + i of a token suffix
 template <typename T> struct SufOps {
-    static constexpr int LDT = ld_of<T>(TT);
+    static constexpr int LDT = ldp_of<T>(TT);
     static constexpr size_t bytes = sizeof(T) * TT * LDT;
     const T *suf;
     __device__ __forceinline__ void init(T *buf, int nth) {
@@ -389,21 +397,46 @@ template <typename T> struct SufOps {
     }
     __device__ __forceinline__ Frag<T> op(int nt) const { return ld_frag_pi(suf + (16 * nt + li()) * LDT); }
 };
+// bf16 pairwise transposes: id[n][k] = (k == n), 32 x 32.  With the pair
+// operand A = frag_acc(X0, X1) of two bucket-row tiles, A . lo() = X0^T and
+// A . hi() = X1^T: every k slot holds data, none is zero padding.
+template <typename T> struct PairOps {
+    static constexpr int LDT = ldp_of<T>(TT);
+    static constexpr size_t bytes = is_bf16<T>() ? sizeof(T) * TT * LDT : 0;
+    const T *id = nullptr;
+    __device__ __forceinline__ void init(T *buf, int nth) {
+        if constexpr (is_bf16<T>()) {
+            for (int idx = threadIdx.x; idx < TT * LDT; idx += nth)
+                buf[idx] = from_f32<T>(idx % LDT == idx / LDT ? 1.f : 0.f);
+            id = buf;
+        }
+    }
+    __device__ __forceinline__ Frag<T> lo() const { return ld_frag_pi(id + li() * LDT); }
+    __device__ __forceinline__ Frag<T> hi() const { return ld_frag_pi(id + (16 + li()) * LDT); }
+};
+
+// 16-deep constant A operand of mma16_x: bf16 holds the row's 16 k values
+// twice (slots j and 4 + j) so that one 16x16x32 product takes B = (hi, lo);
+// fp32 holds them once.
+template <typename T> struct OpX;
+template <> struct OpX<bf16> { Frag<bf16> f; };
+template <> struct OpX<float> { Frag4<float> f; };
 
 // Softmax / corner backward over the wave's 16 buckets (tables of 2^KB
 // buckets, R-aligned), as 16-deep A operands (row, k = local bucket s):
 //   dot[s'][s] = 1 if s and s' share a table (per-table sums, per bucket)
 //   cs[r][s]   = c_{s,k} = +-1 if s is in table tl, r = tl*KB + k (corner sums)
 template <typename T, int KB> struct HashOps {
-    static constexpr int LDI = ld_of<T>(16), NROWS = (16 >> KB) * KB;
+    static constexpr int W_ = is_bf16<T>() ? TT : 16;  // bf16: 16 k values, then the same 16 again
+    static constexpr int LDI = ldp_of<T>(W_), NROWS = (16 >> KB) * KB;
     static constexpr size_t bytes = sizeof(T) * 2 * 16 * LDI;
     const T *dot, *cs;
     __device__ __forceinline__ void init(T *buf, int nth) {
         T *d = buf, *c = buf + 16 * LDI;
         for (int idx = threadIdx.x; idx < 16 * LDI; idx += nth) {
-            const int r = idx / LDI, sb = idx % LDI;
+            const int r = idx / LDI, kk = idx % LDI, sb = kk & 15;
             float vd = 0.f, vc = 0.f;
-            if (sb < 16) {
+            if (kk < W_) {
                 vd = (r >> KB) == (sb >> KB) ? 1.f : 0.f;
                 if (r < NROWS && (sb >> KB) == r / KB) vc = ((sb >> (KB - 1 - r % KB)) & 1) ? 1.f : -1.f;
             }
@@ -413,8 +446,16 @@ template <typename T, int KB> struct HashOps {
         dot = d;
         cs = c;
     }
-    __device__ __forceinline__ Frag4<T> dot_op() const { return ld_frag16(dot + li() * LDI); }
-    __device__ __forceinline__ Frag4<T> cs_op() const { return ld_frag16(cs + li() * LDI); }
+    __device__ __forceinline__ static OpX<T> op_of(const T *p) {
+        OpX<T> o;
+        if constexpr (is_bf16<T>())
+            o.f = ld_frag_pi(p + li() * LDI);
+        else
+            o.f = ld_frag16(p + li() * LDI);
+        return o;
+    }
+    __device__ __forceinline__ OpX<T> dot_op() const { return op_of(dot); }
+    __device__ __forceinline__ OpX<T> cs_op() const { return op_of(cs); }
 };
 
 // Token-direction operand of the wave's bucket-row tiles X[2] (lane holds
@@ -429,21 +470,47 @@ template <typename T> __device__ __forceinline__ Frag<T> token_operand(const f32
     return frag_acc<T>(r0, r1);
 }
 
-// c += A . X^T over the wave's 16 buckets, X a bucket-row tile taken as the B
-// operand (column t, k = s); bf16 splits X into two bf16 parts so that the
-// product keeps fp32 accuracy
-template <typename T> __device__ __forceinline__ void mma16_x(f32x4 &c, const Frag4<T> &A, const f32x4 &x) {
-    if constexpr (is_bf16<T>()) {
-        f32x4 hi, lo;
+// bf16: the exact transposes of a pair operand A = (X0, X1), as the operand
+// with row s and k = t (pi order) -- two products, no padded k slots
+__device__ __forceinline__ Frag<bf16> transpose_pair(const Frag<bf16> &A, const PairOps<bf16> &po) {
+    f32x4 r0 = zero4(), r1 = zero4();
+    mma(r0, A, po.lo());
+    mma(r1, A, po.hi());
+    return frag_acc<bf16>(r0, r1);
+}
+template <typename T>
+__device__ __forceinline__ Frag<T> token_operand(const f32x4 (&X)[2], const Consts<T> &cst, const PairOps<T> &po) {
+    if constexpr (is_bf16<T>())
+        return transpose_pair(frag_acc<T>(X[0], X[1]), po);
+    else
+        return token_operand<T>(X, cst);
+}
+// bf16 parts of a tile pair: hi = bf16(X), lo = bf16(X - hi); hi + lo holds
+// X to ~2^-16 relative, so products of both keep fp32 accuracy
+__device__ __forceinline__ void split_pair(const f32x4 &x0, const f32x4 &x1, Frag<bf16> &hi, Frag<bf16> &lo) {
+    hi = frag_acc<bf16>(x0, x1);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            hi[e] = as_operand<T>(x[e]);
-            lo[e] = x[e] - hi[e];
+    for (int j = 0; j < 4; ++j) {
+        lo.v[j] = (bf16)(x0[j] - (float)hi.v[j]);
+        lo.v[j + 4] = (bf16)(x1[j] - (float)hi.v[j + 4]);
+    }
+}
+
+// c += A . X^T over the wave's 16 buckets, X a bucket-row tile taken as the B
+// operand (column t, k = s); bf16 runs A . hi + A . lo as one 32-deep product
+// (A duplicated in OpX, X split into its two bf16 parts), fp32 accuracy.
+template <typename T> __device__ __forceinline__ void mma16_x(f32x4 &c, const OpX<T> &A, const f32x4 &x) {
+    if constexpr (is_bf16<T>()) {
+        Frag<bf16> hl;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bf16 h = (bf16)x[j];
+            hl.v[j] = h;
+            hl.v[j + 4] = (bf16)(x[j] - (float)h);
         }
-        mma16(c, A, frag16_acc<T>(hi));
-        mma16(c, A, frag16_acc<T>(lo));
+        mma(c, A.f, hl);
     } else {
-        mma16(c, A, frag16_acc<T>(x));
+        mma16(c, A.f, frag16_acc<T>(x));
     }
 }
 
@@ -457,7 +524,7 @@ template <typename T> __device__ __forceinline__ void mma16_x(f32x4 &c, const Fr
 // dQ / dK outputs.
 template <typename T, int KB> struct WideHash {
     static constexpr size_t bytes(int nw) { return sizeof(float) * nw * TT * (KB + 1); }
-    Frag4<T> cs, ones;  // A operands over the wave's 16 buckets: rows k < KB: c_{s,k}; all ones
+    OpX<T> cs, ones;  // A operands over the wave's 16 buckets: rows k < KB: c_{s,k}; all ones
     __device__ __forceinline__ void init(int sg) {
         const int g = lg(), i = li();
         f32x4 c, o;
@@ -467,8 +534,16 @@ template <typename T, int KB> struct WideHash {
             c[j] = i < KB ? (((r >> (KB - 1 - i)) & 1) ? 1.f : -1.f) : 0.f;
             o[j] = 1.f;
         }
-        cs = frag16_acc<T>(c);
-        ones = frag16_acc<T>(o);
+        if constexpr (is_bf16<T>()) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                cs.f.v[j] = cs.f.v[j + 4] = (bf16)c[j];
+                ones.f.v[j] = ones.f.v[j + 4] = (bf16)o[j];
+            }
+        } else {
+            cs.f = frag16_acc<T>(c);
+            ones.f = frag16_acc<T>(o);
+        }
     }
 };
 
@@ -522,49 +597,30 @@ __device__ float softhash_combine(const float *share, const float *sp, const flo
 // Inclusive token suffix Y and token totals of a bucket-row tile pair on the
 // matrix cores; bf16 splits X into two bf16 parts (fp32-accurate sums).
 template <typename T>
-__device__ void suffix_totals(const f32x4 (&X)[2], const Consts<T> &cst, const SufOps<T> &suf, f32x4 (&Y)[2],
-                              f32x4 &tot) {
+__device__ void suffix_totals(const f32x4 (&X)[2], const Consts<T> &cst, const SufOps<T> &suf, const PairOps<T> &po,
+                              f32x4 (&Y)[2], f32x4 &tot) {
     Y[0] = zero4();
     Y[1] = zero4();
     tot = zero4();
-    auto add = [&](const f32x4 (&Z)[2]) {
-        const Frag<T> F = token_operand<T>(Z, cst);
+    auto add = [&](const Frag<T> &F) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) mma(Y[nt], F, suf.op(nt));
         mma(tot, F, cst.ones());
     };
     if constexpr (is_bf16<T>()) {
-        f32x4 hi[2], lo[2];
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hi[nt][e] = as_operand<T>(X[nt][e]);
-                lo[nt][e] = X[nt][e] - hi[nt][e];
-            }
-        add(hi);
-        add(lo);
+        Frag<bf16> hi, lo;
+        split_pair(X[0], X[1], hi, lo);
+        add(transpose_pair(hi, po));
+        add(transpose_pair(lo, po));
     } else {
-        add(X);
+        add(token_operand<T>(X, cst));
     }
 }
-// token totals only (lane: bucket 4g + e)
-template <typename T> __device__ void totals_of(const f32x4 (&X)[2], const Consts<T> &cst, f32x4 &tot) {
-    tot = zero4();
-    if constexpr (is_bf16<T>()) {
-        f32x4 hi[2], lo[2];
+// token totals only (lane: bucket 4g + e), fp32 row sums over the 16 lanes
+// of each row
+__device__ __forceinline__ void totals_of(const f32x4 (&X)[2], f32x4 &tot) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hi[nt][e] = as_operand<T>(X[nt][e]);
-                lo[nt][e] = X[nt][e] - hi[nt][e];
-            }
-        mma(tot, token_operand<T>(hi, cst), cst.ones());
-        mma(tot, token_operand<T>(lo, cst), cst.ones());
-    } else {
-        mma(tot, token_operand<T>(X, cst), cst.ones());
-    }
+    for (int e = 0; e < 4; ++e) tot[e] = row_sum(X[0][e] + X[1][e]);
 }
 
 // Softmax / corner / tanh backward for the wave's buckets on the matrix
@@ -578,7 +634,7 @@ __device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const f
                               float inv_temp, T *dproj, const HashOps<T, KB> &ho) {
     constexpr int LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL), NROWS = HashOps<T, KB>::NROWS;
     const int g = lg(), i = li(), c0 = (sw >> KB) * KB;
-    const Frag4<T> Ad = ho.dot_op(), Ac = ho.cs_op();
+    const OpX<T> Ad = ho.dot_op(), Ac = ho.cs_op();
     float tsum = 0.f;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -620,13 +676,25 @@ template <typename T> __device__ __forceinline__ void store_ds(T *dst, int ld, i
 // array, each 16x16 block transposed on the matrix core into bucket-row
 // layout (lane: [s = sw + 4g + e][d = 16md + i]) for 4-bucket stores
 template <typename T>
-__device__ __forceinline__ void store_ut(T *dst, int ld, int sw, const f32x4 (&Ut)[4], const Consts<T> &cst) {
-    const Frag4<T> ident = cst.ident();
+__device__ __forceinline__ void store_ut(T *dst, int ld, int sw, const f32x4 (&Ut)[4], const Consts<T> &cst,
+                                         const PairOps<T> &po) {
     f32x4 Us[4];
+    if constexpr (is_bf16<T>()) {
 #pragma unroll
-    for (int md = 0; md < 4; ++md) {
-        Us[md] = zero4();
-        mma16(Us[md], frag16_acc<T>(Ut[md]), ident);
+        for (int p = 0; p < 2; ++p) {
+            const Frag<bf16> A = frag_acc<bf16>(Ut[2 * p], Ut[2 * p + 1]);
+            Us[2 * p] = zero4();
+            Us[2 * p + 1] = zero4();
+            mma(Us[2 * p], A, po.lo());
+            mma(Us[2 * p + 1], A, po.hi());
+        }
+    } else {
+        const Frag4<T> ident = cst.ident();
+#pragma unroll
+        for (int md = 0; md < 4; ++md) {
+            Us[md] = zero4();
+            mma16(Us[md], frag16_acc<T>(Ut[md]), ident);
+        }
     }
     store_ds<T>(dst, ld, sw, Us);
 }
@@ -637,7 +705,7 @@ __device__ __forceinline__ void store_ut(T *dst, int ld, int sw, const f32x4 (&U
 // tiles (mt, nt) = (0,0), (0,1), (1,1); the all-zero tile (1,0) is cleared
 // once at kernel start.
 template <typename T> __device__ void m_tile(int q, const T *sV, const T *sG, T *X, T *Y) {
-    constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT);
+    constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
     const int r = q % 3, mt = r == 2 ? 1 : 0, nt = r == 0 ? 0 : 1;
     f32x4 acc = zero4();
@@ -705,7 +773,7 @@ __device__ __forceinline__ int64_t sidx(int s, int d) { return (int64_t)s * SROW
 // =====================================================================
 template <typename T, int SP> struct FwdReduceL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL);
+    static constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL);
     static constexpr size_t oK = 0;
     static constexpr size_t oVt = align16(oK + sizeof(T) * TT * LDN);
     static constexpr size_t oPl = align16(oVt + sizeof(T) * D * LDT);
@@ -721,7 +789,7 @@ template <typename T, int SP> struct FwdReduceL {
 template <typename T>
 __device__ __forceinline__ void tile_sums(const Frag<T> &Pf, const Consts<T> &cst, const T *sVt, f32x4 &tot,
                                           f32x4 (&dB)[4]) {
-    constexpr int LDT = ld_of<T>(TT);
+    constexpr int LDT = ldp_of<T>(TT);
     tot = zero4();
     mma(tot, Pf, cst.ones());
 #pragma unroll
@@ -814,7 +882,7 @@ __global__ void k_fwd_scan(double *fstate, const double *fdelta, int nseg, int e
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct FwdOutL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDS_ = ld_of<T>(SP);
+    static constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDS_ = ld_of<T>(SP);
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
     static constexpr size_t oVt = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
@@ -831,7 +899,7 @@ template <typename T, int SP, bool CAUSAL> struct FwdOutL {
 template <typename T, int SP, bool CAUSAL>
 __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T *Wts, const T *sVt, T *op,
                              int64_t st, int64_t t0, int64_t Tn, float *part) {
-    constexpr int LDS_ = ld_of<T>(SP), LDT = ld_of<T>(TT);
+    constexpr int LDS_ = ld_of<T>(SP), LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
     const T *pb = sBT + (16 * md + i) * LDS_ + 8 * g, *pw = Wts + (16 * nt + i) * LDS_ + 8 * g;
     f32x4 O = zero4();
@@ -975,7 +1043,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 // =====================================================================
 template <typename T, int SP, bool CAUSAL, int KB> struct BwdReduceL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
+    static constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
     static constexpr size_t oV = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
@@ -991,7 +1059,8 @@ template <typename T, int SP, bool CAUSAL, int KB> struct BwdReduceL {
     static constexpr size_t oRed = align16(oSig + sizeof(float) * 5 * TT * LDC);
     static constexpr size_t oCst = align16(oRed + sizeof(float) * 64 * NW_);
     static constexpr size_t oHash = align16(oCst + Consts<T>::bytes);
-    static constexpr size_t oShare = align16(oHash + HashOps<T, 4>::bytes);
+    static constexpr size_t oPair = align16(oHash + HashOps<T, 4>::bytes);
+    static constexpr size_t oShare = align16(oPair + PairOps<T>::bytes);
     static constexpr size_t bytes = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
 };
 
@@ -1031,6 +1100,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         ho.init((T *)(smem + Ly::oHash), NTH);
     else
         wh.init(sg);
+    PairOps<T> po;
+    po.init((T *)(smem + Ly::oPair), NTH);
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
     zero_lds<T>(sDproj, TT * LDDP, NTH);
     if constexpr (CAUSAL) zero_lds<T>(sX, TT * LDT, NTH);
@@ -1095,7 +1166,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PK);
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
-            Pf = token_operand<T>(PK, cst);
+            Pf = token_operand<T>(PK, cst, po);
             for (int nt = 0; nt < 2; ++nt) {
                 Acum[nt] = zero4();
                 mma(Acum[nt], Pf, cst.tri_op(nt));
@@ -1109,7 +1180,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
                 inv[nt][e] = rcp(A + a.eps);
                 W[nt][e] = PQ[nt][e] * inv[nt][e];
             }
-        const Frag<T> Wf = token_operand<T>(W, cst);
+        const Frag<T> Wf = token_operand<T>(W, cst, po);
         // G[s][t] = g_t . B_s(t) = sum_d B[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
         f32x4 dPQ[2], dA[2];
         {
@@ -1128,7 +1199,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         }
         {
             f32x4 tdA;
-            totals_of<T>(dA, cst, tdA);
+            totals_of(dA, tdA);
             for (int e = 0; e < 4; ++e) al[e] += (double)tdA[e];
         }
         // U^T[d][s] += sum_t g[t][d] W[t][s]; carry B^T[d][s] += sum_t V[t][d] P_K[t][s]
@@ -1181,7 +1252,7 @@ __global__ void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int ele
 // =====================================================================
 template <typename T, int SP, bool CAUSAL, int KB> struct BwdOutL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = ld_of<T>(D), LDT = ld_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL),
+    static constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL),
                          LDS_ = ld_of<T>(SP);
     static constexpr size_t oK = 0;
     static constexpr size_t oQ = align16(oK + sizeof(T) * TT * LDN);
@@ -1203,14 +1274,15 @@ template <typename T, int SP, bool CAUSAL, int KB> struct BwdOutL {
     static constexpr size_t oCst = align16(oRed + sizeof(float) * 64 * NW_);
     static constexpr size_t oHash = align16(oCst + Consts<T>::bytes);
     static constexpr size_t oSuf = align16(oHash + HashOps<T, 4>::bytes);
-    static constexpr size_t oShare = align16(oSuf + (CAUSAL ? SufOps<T>::bytes : 0));
+    static constexpr size_t oPair = align16(oSuf + (CAUSAL ? SufOps<T>::bytes : 0));
+    static constexpr size_t oShare = align16(oPair + PairOps<T>::bytes);
     static constexpr size_t bytes = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
 };
 
 template <typename T, int SP, bool CAUSAL>
 __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts, const T *sGt, T *dvp, int64_t st,
                         int64_t t0, int64_t Tn, float *part) {
-    constexpr int LDS_ = ld_of<T>(SP), LDT = ld_of<T>(TT);
+    constexpr int LDS_ = ld_of<T>(SP), LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
     const T *pu = sUT + (16 * md + i) * LDS_ + 8 * g, *pp = Pts + (16 * nt + i) * LDS_ + 8 * g;
     f32x4 acc = zero4();
@@ -1282,6 +1354,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         ho.init((T *)(smem + Ly::oHash), NTH);
     else
         wh.init(sg);
+    PairOps<T> po;
+    po.init((T *)(smem + Ly::oPair), NTH);
     SufOps<T> sufo;
     if constexpr (CAUSAL) sufo.init((T *)(smem + Ly::oSuf), NTH);
     load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
@@ -1306,7 +1380,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         al[e] = rs[sidx(sg + 4 * g + e, D)];
         Ae[e] = CAUSAL ? fs[sidx(sg + 4 * g + e, D)] : 0.0;
     }
-    if constexpr (!CAUSAL) store_ut<T>(sUT, LDS_, sw, Ut, cst);  // constant totals
+    if constexpr (!CAUSAL) store_ut<T>(sUT, LDS_, sw, Ut, cst, po);  // constant totals
     float tsum = 0.f;
 
     wait_state_loads();
@@ -1359,7 +1433,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PKr);
         for (int nt = 0; nt < 2; ++nt)
             for (int e = 0; e < 4; ++e) PKr[nt][e] = as_operand<T>(PKr[nt][e]);
-        const Frag<T> Pf = token_operand<T>(PKr, cst);
+        const Frag<T> Pf = token_operand<T>(PKr, cst, po);
         store_ts<T>(sPts, LDS_, sw, PKr);
         f32x4 dPK[2];
         if constexpr (CAUSAL) {
@@ -1385,9 +1459,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                         Wi[nt][e] = W[nt][e] * inv;
                     }
                 store_ts<T>(sWts, LDS_, sw, W);
-                Wf = token_operand<T>(W, cst);
+                Wf = token_operand<T>(W, cst, po);
             }
-            store_ut<T>(sUT, LDS_, sw, Ut, cst);
+            store_ut<T>(sUT, LDS_, sw, Ut, cst, po);
             __syncthreads();  // all waves' P_K, W, U rows in LDS
             // ---- dA = -W G/(A+eps), G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
             f32x4 dA[2];
@@ -1412,7 +1486,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             // ---- dP_K[tau][s] = alpha(tau) + sum_d U[s][d] v_tau[d] + sum_{t >= tau} W[t][s] M[tau][t]
             {
                 f32x4 alpha[2], tdA;
-                suffix_totals<T>(dA, cst, sufo, alpha, tdA);
+                suffix_totals<T>(dA, cst, sufo, po, alpha, tdA);
                 const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
                 for (int nt = 0; nt < 2; ++nt) {
                     f32x4 c = zero4();
