@@ -159,6 +159,34 @@ template <> struct ChunkOf<8> { typedef uint2 type; };
 
 // Chunks of 16 bytes, or of 8 bytes when 16-byte chunks would leave some of
 // the workgroup's threads without one (every wave shares the staging work).
+// ---- swizzled LDS rows (bf16).  Arrays read as 16-byte operand pieces of
+// 16 rows (ds_read_b128) and written in 8-byte pieces pad each row by 32
+// bytes and XOR the 16-byte granule index by (row >> 2) & 3.  ds_read_b128
+// serves 16 lanes per pass -- lanes {0-3, 12-15, 20-27}, {4-11, 16-19, 28-31}
+// and the same +32 -- over 64 four-byte banks; with this layout every such
+// read is conflict-free and an 8-byte store of 16 rows (16-lane passes over
+// 32 banks) is at most 2-way.  The swizzle stays inside each 64-byte chunk
+// (32 elements), so a lane's k slots hold the same logical k in every row:
+// products of two such operands pair equal k.  fp32 keeps padded rows.
+__device__ __forceinline__ int gswz(int r) { return (r >> 2) & 3; }
+// element offset of logical element e of row r of a [rows][N] array
+template <typename T, int N> __device__ __forceinline__ int sw_off(int r, int e);
+// row pitch (elements) of such an array
+template <typename T, int N> __host__ __device__ constexpr int sw_ld() { return is_bf16<T>() ? N + 16 : ld_of<T>(N); }
+template <typename T, int N> __device__ __forceinline__ int sw_off(int r, int e) {
+    if constexpr (is_bf16<T>())
+        return r * sw_ld<T, N>() + (((e >> 3) ^ gswz(r)) << 3) + (e & 7);
+    else
+        return r * sw_ld<T, N>() + e;
+}
+// gswz depends on r & 15 only, so rows 16 apart share it: a lane keeps one
+// pointer for rows r, r + 16, ... (steps of 16 * sw_ld).
+// Operand pointer of lane (g, i) into row r for 16-byte reads of logical
+// elements 32 kp + 8g .. + 7 at ld_frag(p + 32 * kp).
+template <typename T, int N> __device__ __forceinline__ const T *sw_frag_ptr(const T *base, int r) {
+    return base + sw_off<T, N>(r, 8 * lg());
+}
+
 // rows of the tile at t0 that exist (0 .. TT), as a wave-uniform 32-bit count
 __device__ __forceinline__ int tile_rows(int64_t t0, int64_t Tn) {
     const int64_t r = Tn - t0;
@@ -661,22 +689,24 @@ __device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const f
 
 // bucket-row tiles -> [t][s] LDS array (s contiguous, leading dimension ld):
 // each lane writes its 4 consecutive buckets of one token
-template <typename T> __device__ __forceinline__ void store_ts(T *dst, int ld, int sw, const f32x4 (&X)[2]) {
+template <typename T, int N> __device__ __forceinline__ void store_ts(T *dst, int sw, const f32x4 (&X)[2]) {
+    T *p = dst + sw_off<T, N>(li(), sw + 4 * lg());
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) store4<T>(dst + (16 * nt + li()) * ld + sw + 4 * lg(), X[nt]);
+    for (int nt = 0; nt < 2; ++nt) store4<T>(p + 16 * sw_ld<T, N>() * nt, X[nt]);
 }
 // bucket-row [s][d] carry (lane holds [s = sw + 4g + e][d = 16md + i]) ->
 // [d][s] LDS array (s contiguous)
-template <typename T> __device__ __forceinline__ void store_ds(T *dst, int ld, int sw, const f32x4 (&X)[4]) {
+template <typename T, int N> __device__ __forceinline__ void store_ds(T *dst, int sw, const f32x4 (&X)[4]) {
+    T *p = dst + sw_off<T, N>(li(), sw + 4 * lg());
 #pragma unroll
-    for (int md = 0; md < 4; ++md) store4<T>(dst + (16 * md + li()) * ld + sw + 4 * lg(), X[md]);
+    for (int md = 0; md < 4; ++md) store4<T>(p + 16 * sw_ld<T, N>() * md, X[md]);
 }
 
 // d-row U^T (lane holds U^T[d = 16md + 4g + e][s = sw + i]) -> [d][s] LDS
 // array, each 16x16 block transposed on the matrix core into bucket-row
 // layout (lane: [s = sw + 4g + e][d = 16md + i]) for 4-bucket stores
-template <typename T>
-__device__ __forceinline__ void store_ut(T *dst, int ld, int sw, const f32x4 (&Ut)[4], const Consts<T> &cst,
+template <typename T, int N>
+__device__ __forceinline__ void store_ut(T *dst, int sw, const f32x4 (&Ut)[4], const Consts<T> &cst,
                                          const PairOps<T> &po) {
     f32x4 Us[4];
     if constexpr (is_bf16<T>()) {
@@ -696,7 +726,7 @@ __device__ __forceinline__ void store_ut(T *dst, int ld, int sw, const f32x4 (&U
             mma16(Us[md], frag16_acc<T>(Ut[md]), ident);
         }
     }
-    store_ds<T>(dst, ld, sw, Us);
+    store_ds<T, N>(dst, sw, Us);
 }
 
 // M[tau][t] = v_tau . g_t for tau <= t, 0 above the diagonal, for the tile's
@@ -882,7 +912,7 @@ __global__ void k_fwd_scan(double *fstate, const double *fdelta, int nseg, int e
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct FwdOutL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDS_ = ld_of<T>(SP);
+    static constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDS_ = sw_ld<T, SP>();
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
     static constexpr size_t oVt = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
@@ -899,21 +929,21 @@ template <typename T, int SP, bool CAUSAL> struct FwdOutL {
 template <typename T, int SP, bool CAUSAL>
 __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T *Wts, const T *sVt, T *op,
                              int64_t st, int64_t t0, int64_t Tn, float *part) {
-    constexpr int LDS_ = ld_of<T>(SP), LDT = ldp_of<T>(TT);
+    constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
-    const T *pb = sBT + (16 * md + i) * LDS_ + 8 * g, *pw = Wts + (16 * nt + i) * LDS_ + 8 * g;
+    const T *pb = sw_frag_ptr<T, SP>(sBT, 16 * md + i), *pw = sw_frag_ptr<T, SP>(Wts, 16 * nt + i);
     f32x4 O = zero4();
 #pragma unroll
-    for (int ks = 0; ks < SP / 32; ++ks) mma(O, ld_frag(pb + 32 * ks), ld_frag(pw + 32 * ks));
+    for (int kp = 0; kp < SP / 32; ++kp) mma(O, ld_frag(pb + 32 * kp), ld_frag(pw + 32 * kp));
     if constexpr (CAUSAL) {
         f32x4 Sc[2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             Sc[mt] = zero4();
             if (mt <= nt) {
-                const T *pp = Pts + (16 * mt + i) * LDS_ + 8 * g;
+                const T *pp = sw_frag_ptr<T, SP>(Pts, 16 * mt + i);
 #pragma unroll
-                for (int ks = 0; ks < SP / 32; ++ks) mma(Sc[mt], ld_frag(pp + 32 * ks), ld_frag(pw + 32 * ks));
+                for (int kp = 0; kp < SP / 32; ++kp) mma(Sc[mt], ld_frag(pp + 32 * kp), ld_frag(pw + 32 * kp));
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     if (16 * mt + 4 * g + e > 16 * nt + i) Sc[mt][e] = 0.f;  // keep t' <= t
@@ -965,7 +995,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         for (int md = 0; md < 4; ++md) Bc[md][e] = (float)st[sidx(sg + 4 * g + e, 16 * md + i)];
         a0[e] = st[sidx(sg + 4 * g + e, D)];
     }
-    if constexpr (!CAUSAL) store_ds<T>(sBT, LDS_, sw, Bc);  // constant totals
+    if constexpr (!CAUSAL) store_ds<T, SP>(sBT, sw, Bc);  // constant totals
 
     wait_state_loads();
     Prefetch<T, NTH> pq_, pk_;
@@ -1021,10 +1051,10 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
                 const float A = (float)a0[e] + (CAUSAL ? Acum[nt][e] : 0.f);
                 W[nt][e] = PQ[nt][e] * rcp(A + a.eps);
             }
-        store_ts<T>(sWts, LDS_, sw, W);
+        store_ts<T, SP>(sWts, sw, W);
         if constexpr (CAUSAL) {
-            store_ts<T>(sPts, LDS_, sw, PK);
-            store_ds<T>(sBT, LDS_, sw, Bc);
+            store_ts<T, SP>(sPts, sw, PK);
+            store_ds<T, SP>(sBT, sw, Bc);
         }
         __syncthreads();
         for (int q = w; q < 8; q += NW_)
@@ -1253,7 +1283,7 @@ __global__ void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int ele
 template <typename T, int SP, bool CAUSAL, int KB> struct BwdOutL {
     static constexpr int NW_ = SP / WB;
     static constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL),
-                         LDS_ = ld_of<T>(SP);
+                         LDS_ = sw_ld<T, SP>();
     static constexpr size_t oK = 0;
     static constexpr size_t oQ = align16(oK + sizeof(T) * TT * LDN);
     static constexpr size_t oV = align16(oQ + (CAUSAL ? sizeof(T) * TT * LDN : 0));
@@ -1282,21 +1312,21 @@ template <typename T, int SP, bool CAUSAL, int KB> struct BwdOutL {
 template <typename T, int SP, bool CAUSAL>
 __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts, const T *sGt, T *dvp, int64_t st,
                         int64_t t0, int64_t Tn, float *part) {
-    constexpr int LDS_ = ld_of<T>(SP), LDT = ldp_of<T>(TT);
+    constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
-    const T *pu = sUT + (16 * md + i) * LDS_ + 8 * g, *pp = Pts + (16 * nt + i) * LDS_ + 8 * g;
+    const T *pu = sw_frag_ptr<T, SP>(sUT, 16 * md + i), *pp = sw_frag_ptr<T, SP>(Pts, 16 * nt + i);
     f32x4 acc = zero4();
 #pragma unroll
-    for (int ks = 0; ks < SP / 32; ++ks) mma(acc, ld_frag(pu + 32 * ks), ld_frag(pp + 32 * ks));
+    for (int kp = 0; kp < SP / 32; ++kp) mma(acc, ld_frag(pu + 32 * kp), ld_frag(pp + 32 * kp));
     if constexpr (CAUSAL) {
         f32x4 Sc2[2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             Sc2[mt] = zero4();
             if (mt >= nt) {
-                const T *pw = Wts + (16 * mt + i) * LDS_ + 8 * g;
+                const T *pw = sw_frag_ptr<T, SP>(Wts, 16 * mt + i);
 #pragma unroll
-                for (int ks = 0; ks < SP / 32; ++ks) mma(Sc2[mt], ld_frag(pw + 32 * ks), ld_frag(pp + 32 * ks));
+                for (int kp = 0; kp < SP / 32; ++kp) mma(Sc2[mt], ld_frag(pw + 32 * kp), ld_frag(pp + 32 * kp));
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     if (16 * mt + 4 * g + e < 16 * nt + i) Sc2[mt][e] = 0.f;  // keep t >= tau
@@ -1380,7 +1410,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         al[e] = rs[sidx(sg + 4 * g + e, D)];
         Ae[e] = CAUSAL ? fs[sidx(sg + 4 * g + e, D)] : 0.0;
     }
-    if constexpr (!CAUSAL) store_ut<T>(sUT, LDS_, sw, Ut, cst, po);  // constant totals
+    if constexpr (!CAUSAL) store_ut<T, SP>(sUT, sw, Ut, cst, po);  // constant totals
     float tsum = 0.f;
 
     wait_state_loads();
@@ -1434,7 +1464,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         for (int nt = 0; nt < 2; ++nt)
             for (int e = 0; e < 4; ++e) PKr[nt][e] = as_operand<T>(PKr[nt][e]);
         const Frag<T> Pf = token_operand<T>(PKr, cst, po);
-        store_ts<T>(sPts, LDS_, sw, PKr);
+        store_ts<T, SP>(sPts, sw, PKr);
         f32x4 dPK[2];
         if constexpr (CAUSAL) {
             f32x4 Wi[2];  // W / (A + eps), the factor of dA
@@ -1458,10 +1488,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                         W[nt][e] = PQ[nt][e] * inv;
                         Wi[nt][e] = W[nt][e] * inv;
                     }
-                store_ts<T>(sWts, LDS_, sw, W);
+                store_ts<T, SP>(sWts, sw, W);
                 Wf = token_operand<T>(W, cst, po);
             }
-            store_ut<T>(sUT, LDS_, sw, Ut, cst, po);
+            store_ut<T, SP>(sUT, sw, Ut, cst, po);
             __syncthreads();  // all waves' P_K, W, U rows in LDS
             // ---- dA = -W G/(A+eps), G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
             f32x4 dA[2];
