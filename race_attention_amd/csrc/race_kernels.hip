@@ -157,8 +157,6 @@ template <int B> struct ChunkOf;
 template <> struct ChunkOf<16> { typedef uint4 type; };
 template <> struct ChunkOf<8> { typedef uint2 type; };
 
-// Chunks of 16 bytes, or of 8 bytes when 16-byte chunks would leave some of
-// the workgroup's threads without one (every wave shares the staging work).
 // ---- swizzled LDS rows (bf16).  Arrays read as 16-byte operand pieces of
 // 16 rows (ds_read_b128) and written in 8-byte pieces pad each row by 32
 // bytes and XOR the 16-byte granule index by (row >> 2) & 3.  ds_read_b128
@@ -187,6 +185,50 @@ template <typename T, int N> __device__ __forceinline__ const T *sw_frag_ptr(con
     return base + sw_off<T, N>(r, 8 * lg());
 }
 
+// ---- natural token tiles and planes ([rows][D], k = d).  With SW (bf16), k
+// is stored in pi order inside each 32-element chunk (k = 16h + 4g + j at
+// 8g + 4h + j) in the swizzled rows above, so a pi-order operand (k = 4g..,
+// 16 + 4g..) is one contiguous 16-byte read like the operand of a [rows][k]
+// product, and every operand read of 16 rows is conflict-free.  Runs of 4
+// k aligned to 4 stay contiguous.  Without SW: padded natural rows.
+template <typename T, bool SW> struct NatL {
+    static constexpr bool P = SW && is_bf16<T>();
+    static constexpr int LD = P ? sw_ld<T, D>() : ld_of<T>(D);
+    __device__ __forceinline__ static int pos(int k) {
+        return (k & ~31) | (((k & 15) >> 2) << 3) | (((k >> 4) & 1) << 2) | (k & 3);
+    }
+    // element offset of logical (r, k)
+    __device__ __forceinline__ static int off(int r, int k) {
+        if constexpr (P)
+            return sw_off<T, D>(r, pos(k));
+        else
+            return r * LD + k;
+    }
+    // operand of a [rows][k] product: row r, k chunk kp (both operands of
+    // such a product read with this, so their k slots agree)
+    __device__ __forceinline__ static Frag<T> frag(const T *base, int r, int kp) {
+        if constexpr (P)
+            return ld_frag(sw_frag_ptr<T, D>(base, r) + 32 * kp);
+        else
+            return ld_frag(base + r * LD + 8 * lg() + 32 * kp);
+    }
+    // pi-order operand of row r over k = 32h .. 32h + 31
+    __device__ __forceinline__ static Frag<T> frag_pi(const T *base, int r, int h) {
+        if constexpr (P)
+            return ld_frag(sw_frag_ptr<T, D>(base, r) + 32 * h);
+        else
+            return ld_frag_pi(base + r * LD + 32 * h);
+    }
+};
+// acc += A[rA .. rA+15][:] * B[rB .. rB+15][:]^T over all D of two natural arrays
+template <class NL, typename T>
+__device__ __forceinline__ void nat_mma(f32x4 &acc, const T *A, int rA, const T *B, int rB) {
+#pragma unroll
+    for (int kp = 0; kp < D / 32; ++kp) mma(acc, NL::frag(A, rA + li(), kp), NL::frag(B, rB + li(), kp));
+}
+
+// Chunks of 16 bytes, or of 8 bytes when 16-byte chunks would leave some of
+// the workgroup's threads without one (every wave shares the staging work).
 // rows of the tile at t0 that exist (0 .. TT), as a wave-uniform 32-bit count
 __device__ __forceinline__ int tile_rows(int64_t t0, int64_t Tn) {
     const int64_t r = Tn - t0;
@@ -211,13 +253,20 @@ template <typename T, int NTH> struct Prefetch {
             if (idx < CHUNKS && t < rem) v[j] = ld_at<chunk_t>(base, tile_off(t, st, c * EPC, sizeof(T)));
         }
     }
-    __device__ __forceinline__ void commit(T *nat, T *trn) const {
-        constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT);
+    template <class NL = NatL<T, false>> __device__ __forceinline__ void commit(T *nat, T *trn) const {
+        constexpr int LDT = ldp_of<T>(TT);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int idx = threadIdx.x + j * NTH, t = idx / CPR, c = idx % CPR;
             if (idx >= CHUNKS) continue;
-            if (nat) *reinterpret_cast<chunk_t *>(nat + t * LDN + c * EPC) = v[j];
+            if (nat) {
+                if constexpr (NL::P && CB == 16) {  // two runs of 4 elements
+                    *reinterpret_cast<uint2 *>(nat + NL::off(t, c * EPC)) = uint2{v[j].x, v[j].y};
+                    *reinterpret_cast<uint2 *>(nat + NL::off(t, c * EPC + 4)) = uint2{v[j].z, v[j].w};
+                } else {
+                    *reinterpret_cast<chunk_t *>(nat + NL::off(t, c * EPC)) = v[j];
+                }
+            }
             if (trn) {
                 const T *e = reinterpret_cast<const T *>(&v[j]);
 #pragma unroll
@@ -258,15 +307,15 @@ template <typename T, int NTH, int NPART> struct PrefetchT {
             if (ok && 2 * tp + 1 < rem) v[j][1] = ld_at<uint2>(base, off + (uint32_t)st * (uint32_t)sizeof(T));
         }
     }
-    __device__ __forceinline__ void commit(int part, T *nat, T *trn) const {
-        constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT);
+    template <class NL = NatL<T, false>> __device__ __forceinline__ void commit(int part, T *nat, T *trn) const {
+        constexpr int LDT = ldp_of<T>(TT);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             int tp, c;
             if (!task_of(part, j, tp, c)) continue;
             if (nat) {
-                *reinterpret_cast<uint2 *>(nat + (2 * tp) * LDN + c * EPC) = v[j][0];
-                *reinterpret_cast<uint2 *>(nat + (2 * tp + 1) * LDN + c * EPC) = v[j][1];
+                *reinterpret_cast<uint2 *>(nat + NL::off(2 * tp, c * EPC)) = v[j][0];
+                *reinterpret_cast<uint2 *>(nat + NL::off(2 * tp + 1, c * EPC)) = v[j][1];
             }
             // element q of a chunk: bf16 -> 16-bit half q of the 64-bit chunk; fp32 -> word q
             const uint2 a = v[j][0], b = v[j][1];
@@ -287,15 +336,15 @@ template <typename T, int NTH, int NPART> struct PrefetchT {
 
 // Planes [L*K][D] fp32 -> LDS.  pl/pllo: [NCOL][ld_of<T>(D)] (bf16 keeps a
 // hi/lo split so the projection is close to fp32), plt: [D][ld_of<T>(NCOL)].
-template <typename T, int NTH>
+template <typename T, int NTH, class NL = NatL<T, false>>
 __device__ void load_planes(const float *__restrict__ planes, int LK, T *pl, T *pllo, T *plt) {
-    constexpr int LDN = ld_of<T>(D), LDC = ld_of<T>(NCOL);
+    constexpr int LDC = ld_of<T>(NCOL);
     for (int idx = threadIdx.x; idx < NCOL * D; idx += NTH) {
         const int c = idx / D, d = idx % D;
         const float w = c < LK ? planes[c * D + d] : 0.f;
         const T hi = from_f32<T>(w);
-        if (pl) pl[c * LDN + d] = hi;
-        if (pllo) pllo[c * LDN + d] = from_f32<T>(w - to_f32(hi));
+        if (pl) pl[NL::off(c, d)] = hi;
+        if (pllo) pllo[NL::off(c, d)] = from_f32<T>(w - to_f32(hi));
         if (plt) plt[d * LDC + c] = hi;
     }
 }
@@ -303,13 +352,17 @@ __device__ void load_planes(const float *__restrict__ planes, int LK, T *pl, T *
 // One 16x16 tile (rows c = 16mc.., columns t = 16nt..) of planes . X^T, then
 // th = tanh and the sigmoid pair of 2*th*inv_temp, stored as sp/sm/sth
 // [TT][ld_of<float>(NCOL)] (lane writes its 4 consecutive c of token t).
-template <typename T>
+template <typename T, class NL = NatL<T, false>>
 __device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mc, int nt, float inv_temp, float *sp,
                              float *sm, float *sth) {
-    constexpr int LDN = ld_of<T>(D), LDC = ld_of<float>(NCOL);
+    constexpr int LDC = ld_of<float>(NCOL);
     f32x4 acc = zero4();
-    tile_mma(acc, pl + 16 * mc * LDN, LDN, sx + 16 * nt * LDN, LDN, D / 32);
-    if constexpr (is_bf16<T>()) tile_mma(acc, pllo + 16 * mc * LDN, LDN, sx + 16 * nt * LDN, LDN, D / 32);
+#pragma unroll
+    for (int kp = 0; kp < D / 32; ++kp) {
+        const Frag<T> x = NL::frag(sx, 16 * nt + li(), kp);
+        mma(acc, NL::frag(pl, 16 * mc + li(), kp), x);
+        if constexpr (is_bf16<T>()) mma(acc, NL::frag(pllo, 16 * mc + li(), kp), x);
+    }
     const int t = 16 * nt + li(), c0 = 16 * mc + 4 * lg();
     f32x4 a, b, th;
 #pragma unroll
@@ -734,19 +787,19 @@ __device__ __forceinline__ void store_ut(T *dst, int sw, const f32x4 (&Ut)[4], c
 // term's operand), q >= 3 tile q - 3 of Y[tau][t] (rows tau, the dP_K term's);
 // tiles (mt, nt) = (0,0), (0,1), (1,1); the all-zero tile (1,0) is cleared
 // once at kernel start.
-template <typename T> __device__ void m_tile(int q, const T *sV, const T *sG, T *X, T *Y) {
-    constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT);
+template <typename T, class NL = NatL<T, false>> __device__ void m_tile(int q, const T *sV, const T *sG, T *X, T *Y) {
+    constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
     const int r = q % 3, mt = r == 2 ? 1 : 0, nt = r == 0 ? 0 : 1;
     f32x4 acc = zero4();
     if (q < 3) {
-        tile_mma(acc, sV + 16 * mt * LDN, LDN, sG + 16 * nt * LDN, LDN, D / 32);  // [tau = 16mt+4g+e][t = 16nt+i]
+        nat_mma<NL>(acc, sV, 16 * mt, sG, 16 * nt);  // [tau = 16mt+4g+e][t = 16nt+i]
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             if (16 * mt + 4 * g + e > 16 * nt + i) acc[e] = 0.f;
         store4<T>(X + (16 * nt + i) * LDT + 16 * mt + 4 * g, acc);
     } else {
-        tile_mma(acc, sG + 16 * nt * LDN, LDN, sV + 16 * mt * LDN, LDN, D / 32);  // [t = 16nt+4g+e][tau = 16mt+i]
+        nat_mma<NL>(acc, sG, 16 * nt, sV, 16 * mt);  // [t = 16nt+4g+e][tau = 16mt+i]
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             if (16 * mt + i > 16 * nt + 4 * g + e) acc[e] = 0.f;
@@ -803,7 +856,7 @@ __device__ __forceinline__ int64_t sidx(int s, int d) { return (int64_t)s * SROW
 // =====================================================================
 template <typename T, int SP> struct FwdReduceL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL);
+    static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL);
     static constexpr size_t oK = 0;
     static constexpr size_t oVt = align16(oK + sizeof(T) * TT * LDN);
     static constexpr size_t oPl = align16(oVt + sizeof(T) * D * LDT);
@@ -832,6 +885,7 @@ __device__ __forceinline__ void tile_sums(const Frag<T> &Pf, const Consts<T> &cs
 template <typename T, int SP, int KB>
 __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     using Ly = FwdReduceL<T, SP>;
+    using NL = NatL<T, true>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDC = Ly::LDC;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
@@ -849,7 +903,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
-    load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
+    load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
     double accB[4][4], accA[4];
     for (int e = 0; e < 4; ++e) {
         accA[e] = 0.0;
@@ -866,14 +920,14 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
         __syncthreads();
-        pk_.commit(sK, nullptr);
-        pv_.commit(0, nullptr, sVt);
+        pk_.template commit<NL>(sK, nullptr);
+        pv_.template commit<NL>(0, nullptr, sVt);
         if (jt + 1 < j1) {
             pk_.issue(kp, a.sk.t, t0 + TT, a.T);
             pv_.issue(0, vp, a.sv.t, t0 + TT, a.T);
         }
         __syncthreads();
-        for (int q = w; q < 4; q += NW_) project_tile<T>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, nullptr);
+        for (int q = w; q < 4; q += NW_) project_tile<T, NL>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, nullptr);
         __syncthreads();
         f32x4 PK[2];
         probs_st<KB>(sSp, sSm, sg, a.S, t0, a.T, PK);
@@ -912,7 +966,7 @@ __global__ void k_fwd_scan(double *fstate, const double *fdelta, int nseg, int e
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct FwdOutL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDS_ = sw_ld<T, SP>();
+    static constexpr int LDN = NatL<T, false>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDS_ = sw_ld<T, SP>();
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
     static constexpr size_t oVt = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
@@ -963,6 +1017,7 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
 template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(Args a) {
     using Ly = FwdOutL<T, SP, CAUSAL>;
+    using NL = NatL<T, false>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC, LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
@@ -1073,7 +1128,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 // =====================================================================
 template <typename T, int SP, bool CAUSAL, int KB> struct BwdReduceL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
+    static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
     static constexpr size_t oV = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
@@ -1097,6 +1152,7 @@ template <typename T, int SP, bool CAUSAL, int KB> struct BwdReduceL {
 template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     using Ly = BwdReduceL<T, SP, CAUSAL, KB>;
+    using NL = NatL<T, true>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     constexpr int NTASK = CAUSAL ? 11 : 4;  // Q projection (4), K projection (4), X tiles (3)
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
@@ -1132,7 +1188,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         wh.init(sg);
     PairOps<T> po;
     po.init((T *)(smem + Ly::oPair), NTH);
-    load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
+    load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
     zero_lds<T>(sDproj, TT * LDDP, NTH);
     if constexpr (CAUSAL) zero_lds<T>(sX, TT * LDT, NTH);
     // forward state in d-row layout: lane holds B^T[d = 16md + 4g + e][s = sw + i]
@@ -1165,11 +1221,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         const int64_t t0 = jt * TT;
         // no barrier before the commit: since the previous tile's last barrier
         // only dx_store ran, which reads neither the token tiles nor X
-        pq_.commit(sQ, nullptr);
-        pg_.commit(0, sG, sGt);
+        pq_.template commit<NL>(sQ, nullptr);
+        pg_.template commit<NL>(0, sG, sGt);
         if constexpr (CAUSAL) {
-            pk_.commit(sK, nullptr);
-            pv_.commit(1, sV, sVt);
+            pk_.template commit<NL>(sK, nullptr);
+            pv_.template commit<NL>(1, sV, sVt);
         }
         if (jt + 1 < j1) {
             pq_.issue(qp, a.sq.t, t0 + TT, a.T);
@@ -1182,11 +1238,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         __syncthreads();
         for (int q = w; q < NTASK; q += NW_) {
             if (q < 4)
-                project_tile<T>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, sThQ);
+                project_tile<T, NL>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, sThQ);
             else if (q < 8)
-                project_tile<T>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
+                project_tile<T, NL>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
             else
-                m_tile<T>(q - 8, sV, sG, sX, nullptr);
+                m_tile<T, NL>(q - 8, sV, sG, sX, nullptr);
         }
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2], tot;
@@ -1217,8 +1273,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             const Frag<T> b0 = frag_acc<T>(Bt[0], Bt[1]), b1 = frag_acc<T>(Bt[2], Bt[3]);
             for (int nt = 0; nt < 2; ++nt) {
                 f32x4 G = zero4();
-                mma(G, b0, ld_frag_pi(sG + (16 * nt + i) * LDN));
-                mma(G, b1, ld_frag_pi(sG + (16 * nt + i) * LDN + 32));
+                mma(G, b0, NL::frag_pi(sG, 16 * nt + i, 0));
+                mma(G, b1, NL::frag_pi(sG, 16 * nt + i, 1));
                 if constexpr (CAUSAL) mma(G, Pf, ld_frag_pi(sX + (16 * nt + i) * LDT));
                 // dP_Q = G/(A+eps); dA = -W G/(A+eps)
                 for (int e = 0; e < 4; ++e) {
@@ -1282,7 +1338,7 @@ __global__ void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int ele
 // =====================================================================
 template <typename T, int SP, bool CAUSAL, int KB> struct BwdOutL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = ld_of<T>(D), LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL),
+    static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL),
                          LDS_ = sw_ld<T, SP>();
     static constexpr size_t oK = 0;
     static constexpr size_t oQ = align16(oK + sizeof(T) * TT * LDN);
@@ -1346,6 +1402,7 @@ __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts
 template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     using Ly = BwdOutL<T, SP, CAUSAL, KB>;
+    using NL = NatL<T, true>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
                   LDS_ = Ly::LDS_;
     constexpr int NTASK = CAUSAL ? 14 : 4;  // K projection (4), Q projection (4), X and Y tiles (6)
@@ -1388,7 +1445,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     po.init((T *)(smem + Ly::oPair), NTH);
     SufOps<T> sufo;
     if constexpr (CAUSAL) sufo.init((T *)(smem + Ly::oSuf), NTH);
-    load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
+    load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
     zero_lds<T>(sDproj, TT * LDDP, NTH);
     if constexpr (CAUSAL) {
         zero_lds<T>(sX, TT * LDT, NTH);
@@ -1431,13 +1488,13 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         const int64_t t0 = jr * TT;
         // no barrier before the commit: since the previous tile's last barrier
         // only dx_store ran, which reads neither the token tiles nor X / Y
-        pk_.commit(sK, nullptr);
+        pk_.template commit<NL>(sK, nullptr);
         if constexpr (CAUSAL) {
-            pv_.commit(1, sV, sVt);
-            pq_.commit(sQ, nullptr);
-            pg_.commit(0, sG, sGt);
+            pv_.template commit<NL>(1, sV, sVt);
+            pq_.template commit<NL>(sQ, nullptr);
+            pg_.template commit<NL>(0, sG, sGt);
         } else {
-            pvn_.commit(sV, nullptr);
+            pvn_.template commit<NL>(sV, nullptr);
         }
         if (jr > j0) {
             pk_.issue(kp, a.sk.t, t0 - TT, a.T);
@@ -1452,11 +1509,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         __syncthreads();
         for (int q = w; q < NTASK; q += NW_) {
             if (q < 4)
-                project_tile<T>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpK, sSmK, sThK);
+                project_tile<T, NL>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpK, sSmK, sThK);
             else if (q < 8)
-                project_tile<T>(sQ, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+                project_tile<T, NL>(sQ, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
             else
-                m_tile<T>(q - 8, sV, sG, sX, sY);
+                m_tile<T, NL>(q - 8, sV, sG, sX, sY);
         }
         __syncthreads();
         f32x4 PKr[2];  // operand-rounded P_K (fp32 P_K is rebuilt for the softmax backward)
@@ -1507,8 +1564,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 }
                 for (int nt = 0; nt < 2; ++nt) {
                     f32x4 G = zero4();
-                    mma(G, Bf[0], ld_frag_pi(sG + (16 * nt + i) * LDN));
-                    mma(G, Bf[1], ld_frag_pi(sG + (16 * nt + i) * LDN + 32));
+                    mma(G, Bf[0], NL::frag_pi(sG, 16 * nt + i, 0));
+                    mma(G, Bf[1], NL::frag_pi(sG, 16 * nt + i, 1));
                     mma(G, Pf, ld_frag_pi(sX + (16 * nt + i) * LDT));
                     for (int e = 0; e < 4; ++e) dA[nt][e] = -Wi[nt][e] * G[e];
                 }
@@ -1520,8 +1577,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
                 for (int nt = 0; nt < 2; ++nt) {
                     f32x4 c = zero4();
-                    mma(c, u0, ld_frag_pi(sV + (16 * nt + i) * LDN));
-                    mma(c, u1, ld_frag_pi(sV + (16 * nt + i) * LDN + 32));
+                    mma(c, u0, NL::frag_pi(sV, 16 * nt + i, 0));
+                    mma(c, u1, NL::frag_pi(sV, 16 * nt + i, 1));
                     mma(c, Wf, ld_frag_pi(sY + (16 * nt + i) * LDT));
                     for (int e = 0; e < 4; ++e) dPK[nt][e] = c[e] + alpha[nt][e] + al[e];
                 }
@@ -1539,8 +1596,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
             for (int nt = 0; nt < 2; ++nt) {
                 f32x4 c = zero4();
-                mma(c, u0, ld_frag_pi(sV + (16 * nt + i) * LDN));
-                mma(c, u1, ld_frag_pi(sV + (16 * nt + i) * LDN + 32));
+                mma(c, u0, NL::frag_pi(sV, 16 * nt + i, 0));
+                mma(c, u1, NL::frag_pi(sV, 16 * nt + i, 1));
                 for (int e = 0; e < 4; ++e) dPK[nt][e] = c[e] + al[e];
             }
         }
