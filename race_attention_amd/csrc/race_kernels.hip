@@ -966,15 +966,24 @@ __global__ void k_fwd_scan(double *fstate, const double *fdelta, int nseg, int e
 // =====================================================================
 template <typename T, int SP, bool CAUSAL> struct FwdOutL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = NatL<T, false>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDS_ = sw_ld<T, SP>();
-    static constexpr size_t oQ = 0;
-    static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
-    static constexpr size_t oVt = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
+    // The Q and K tiles live inside the P_K / W region when they fit: they
+    // are dead from the projection until the next tile's commit, P_K and W
+    // are written after the projection and read before that commit (barriers
+    // separate all four steps).  Then they also take the swizzled layout.
+    static constexpr bool ALIAS = sw_ld<T, SP>() >= NatL<T, true>::LD;
+    using NL = NatL<T, ALIAS>;
+    static constexpr int LDN = NL::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDS_ = sw_ld<T, SP>();
+    static constexpr size_t oVt = 0;
     static constexpr size_t oSig = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));  // Q sp, Q sm, K sp, K sm
     static constexpr size_t oPts = align16(oSig + sizeof(float) * (CAUSAL ? 4 : 2) * TT * LDC);
     static constexpr size_t oWts = align16(oPts + (CAUSAL ? sizeof(T) * TT * LDS_ : 0));
     static constexpr size_t oBT = align16(oWts + sizeof(T) * TT * LDS_);
-    static constexpr size_t oPl = align16(oBT + sizeof(T) * D * LDS_);
+    static constexpr size_t oEnd = align16(oBT + sizeof(T) * D * LDS_);
+    static constexpr size_t oQ = ALIAS ? oPts : oEnd;
+    static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
+    static constexpr size_t oKEnd = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
+    static_assert(!ALIAS || oKEnd <= oBT, "Q/K tiles must fit in the P_K / W region");
+    static constexpr size_t oPl = ALIAS ? oEnd : oKEnd;
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t oCst = align16(oPlLo + sizeof(T) * NCOL * LDN);
     static constexpr size_t bytes = align16(oCst + Consts<T>::bytes);
@@ -1017,7 +1026,7 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
 template <typename T, int SP, bool CAUSAL, int KB>
 __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(Args a) {
     using Ly = FwdOutL<T, SP, CAUSAL>;
-    using NL = NatL<T, false>;
+    using NL = typename Ly::NL;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC, LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
@@ -1040,7 +1049,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
-    load_planes<T, NTH>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
+    load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
     // carried state: causal = prefix at the segment start, non-causal = totals.
     // B in bucket-row layout: lane holds B[s = sw + 4g + e][d = 16md + i]
     const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * a.Spad * SROW;
@@ -1065,10 +1074,10 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
         __syncthreads();  // previous tile's readers of sVt / sPts / sWts / sBT are done
-        pq_.commit(sQ, nullptr);
+        pq_.template commit<NL>(sQ, nullptr);
         if constexpr (CAUSAL) {
-            pk_.commit(sK, nullptr);
-            pv_.commit(0, nullptr, sVt);
+            pk_.template commit<NL>(sK, nullptr);
+            pv_.template commit<NL>(0, nullptr, sVt);
         }
         if (jt + 1 < j1) {
             pq_.issue(qp, a.sq.t, t0 + TT, a.T);
@@ -1080,9 +1089,9 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         __syncthreads();
         for (int q = w; q < (CAUSAL ? 8 : 4); q += NW_) {
             if (q < 4)
-                project_tile<T>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+                project_tile<T, NL>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
             else
-                project_tile<T>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
+                project_tile<T, NL>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
         }
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
