@@ -338,14 +338,13 @@ template <typename T, int NTH, int NPART> struct PrefetchT {
 // hi/lo split so the projection is close to fp32), plt: [D][ld_of<T>(NCOL)].
 template <typename T, int NTH, class NL = NatL<T, false>>
 __device__ void load_planes(const float *__restrict__ planes, int LK, T *pl, T *pllo, T *plt) {
-    constexpr int LDC = ld_of<T>(NCOL);
     for (int idx = threadIdx.x; idx < NCOL * D; idx += NTH) {
         const int c = idx / D, d = idx % D;
         const float w = c < LK ? planes[c * D + d] : 0.f;
         const T hi = from_f32<T>(w);
         if (pl) pl[NL::off(c, d)] = hi;
         if (pllo) pllo[NL::off(c, d)] = from_f32<T>(w - to_f32(hi));
-        if (plt) plt[d * LDC + c] = hi;
+        if (plt) plt[sw_off<T, NCOL>(d, c)] = hi;
     }
 }
 
@@ -652,7 +651,7 @@ __device__ void softhash_share(const f32x4 (&P)[2], const f32x4 (&dP)[2], const 
 template <int KB, typename T, int SP, int NTH>
 __device__ float softhash_combine(const float *share, const float *sp, const float *sm, const float *sth, int z, int L,
                                   float inv_temp, T *dproj) {
-    constexpr int LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL), R = 1 << KB, NW_ = SP / WB;
+    constexpr int LDC = ld_of<float>(NCOL), R = 1 << KB, NW_ = SP / WB;
     constexpr int NTAB = SP >= R ? SP / R : 1;          // tables (or one table part) in the slice
     constexpr int WPT = (R / WB) < NW_ ? R / WB : NW_;  // waves per table in the slice
     const int l0 = (z * SP) >> KB;
@@ -670,7 +669,7 @@ __device__ float softhash_combine(const float *share, const float *sp, const flo
         const float th = sth[t * LDC + col];
         const float du = sx - sd * (sp[t * LDC + col] - sm[t * LDC + col]);
         tsum += du * th;
-        dproj[t * LDDP + col] = from_f32<T>(du * inv_temp * (1.f - th * th));
+        dproj[sw_off<T, NCOL>(t, col)] = from_f32<T>(du * inv_temp * (1.f - th * th));
     }
     return tsum;
 }
@@ -713,7 +712,7 @@ __device__ __forceinline__ void totals_of(const f32x4 (&X)[2], f32x4 &tot) {
 template <int KB, typename T>
 __device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const float *sth, int sw, int L,
                               float inv_temp, T *dproj, const HashOps<T, KB> &ho) {
-    constexpr int LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL), NROWS = HashOps<T, KB>::NROWS;
+    constexpr int LDC = ld_of<float>(NCOL), NROWS = HashOps<T, KB>::NROWS;
     const int g = lg(), i = li(), c0 = (sw >> KB) * KB;
     const OpX<T> Ad = ho.dot_op(), Ac = ho.cs_op();
     float tsum = 0.f;
@@ -733,7 +732,7 @@ __device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const f
             if (row < NROWS && col < L * KB) {
                 const float th = sth[t * LDC + col];
                 tsum += du[e] * th;
-                dproj[t * LDDP + col] = from_f32<T>(du[e] * inv_temp * (1.f - th * th));
+                dproj[sw_off<T, NCOL>(t, col)] = from_f32<T>(du[e] * inv_temp * (1.f - th * th));
             }
         }
     }
@@ -816,13 +815,12 @@ template <typename T> __device__ void zero_lds(T *p, int n, int nth) {
 // part != nullptr: fp32 partial of this bucket slice, rows t0.. of a [T][D] block.
 template <typename T, int NW_>
 __device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64_t t0, int64_t Tn, float *part) {
-    constexpr int LDDP = ld_of<T>(NCOL);
     const int g = lg(), i = li(), w = wave_id();
     T *base = dst + t0 * st;
     for (int q = w; q < 8; q += NW_) {
         const int md = q >> 1, nt = q & 1;
         f32x4 acc = zero4();
-        tile_mma(acc, plt + 16 * md * LDDP, LDDP, dproj + 16 * nt * LDDP, LDDP, NCOL / 32);
+        mma(acc, ld_frag(sw_frag_ptr<T, NCOL>(plt, 16 * md + i)), ld_frag(sw_frag_ptr<T, NCOL>(dproj, 16 * nt + i)));
         const int t = 16 * nt + i;
         if (t0 + t < Tn) {
             if (part)
@@ -1137,7 +1135,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 // =====================================================================
 template <typename T, int SP, bool CAUSAL, int KB> struct BwdReduceL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL);
+    static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>();
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
     static constexpr size_t oV = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
@@ -1347,7 +1345,7 @@ __global__ void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int ele
 // =====================================================================
 template <typename T, int SP, bool CAUSAL, int KB> struct BwdOutL {
     static constexpr int NW_ = SP / WB;
-    static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = ld_of<T>(NCOL),
+    static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>(),
                          LDS_ = sw_ld<T, SP>();
     static constexpr size_t oK = 0;
     static constexpr size_t oQ = align16(oK + sizeof(T) * TT * LDN);
