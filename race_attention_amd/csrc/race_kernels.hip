@@ -38,6 +38,7 @@
 #include <type_traits>
 
 #include "race_device.h"
+#include "race_layout.h"
 
 namespace race {
 
@@ -157,23 +158,19 @@ template <int B> struct ChunkOf;
 template <> struct ChunkOf<16> { typedef uint4 type; };
 template <> struct ChunkOf<8> { typedef uint2 type; };
 
-// ---- swizzled LDS rows (bf16).  Arrays read as 16-byte operand pieces of
-// 16 rows (ds_read_b128) and written in 8-byte pieces pad each row by 32
-// bytes and XOR the 16-byte granule index by (row >> 2) & 3.  ds_read_b128
-// serves 16 lanes per pass -- lanes {0-3, 12-15, 20-27}, {4-11, 16-19, 28-31}
-// and the same +32 -- over 64 four-byte banks; with this layout every such
-// read is conflict-free and an 8-byte store of 16 rows (16-lane passes over
-// 32 banks) is at most 2-way.  The swizzle stays inside each 64-byte chunk
-// (32 elements), so a lane's k slots hold the same logical k in every row:
-// products of two such operands pair equal k.  fp32 keeps padded rows.
-__device__ __forceinline__ int gswz(int r) { return (r >> 2) & 3; }
-// element offset of logical element e of row r of a [rows][N] array
-template <typename T, int N> __device__ __forceinline__ int sw_off(int r, int e);
+// ---- swizzled LDS rows (bf16; race_layout.h): arrays read as 16-byte
+// operand pieces of 16 rows and written in 8-byte pieces.  fp32 keeps padded
+// rows.  The swizzle stays inside each 32-element chunk, so a lane's k slots
+// hold the same logical k in every row: products of two such operands pair
+// equal k.
 // row pitch (elements) of such an array
-template <typename T, int N> __host__ __device__ constexpr int sw_ld() { return is_bf16<T>() ? N + 16 : ld_of<T>(N); }
+template <typename T, int N> __host__ __device__ constexpr int sw_ld() {
+    return is_bf16<T>() ? layout::sw_pitch(N) : ld_of<T>(N);
+}
+// element offset of logical element e of row r of a [rows][N] array
 template <typename T, int N> __device__ __forceinline__ int sw_off(int r, int e) {
     if constexpr (is_bf16<T>())
-        return r * sw_ld<T, N>() + (((e >> 3) ^ gswz(r)) << 3) + (e & 7);
+        return layout::sw_elem(N, r, e);
     else
         return r * sw_ld<T, N>() + e;
 }
@@ -194,9 +191,7 @@ template <typename T, int N> __device__ __forceinline__ const T *sw_frag_ptr(con
 template <typename T, bool SW> struct NatL {
     static constexpr bool P = SW && is_bf16<T>();
     static constexpr int LD = P ? sw_ld<T, D>() : ld_of<T>(D);
-    __device__ __forceinline__ static int pos(int k) {
-        return (k & ~31) | (((k & 15) >> 2) << 3) | (((k >> 4) & 1) << 2) | (k & 3);
-    }
+    __device__ __forceinline__ static int pos(int k) { return layout::pi_pos(k); }
     // element offset of logical (r, k)
     __device__ __forceinline__ static int off(int r, int k) {
         if constexpr (P)
