@@ -112,6 +112,12 @@ template <> __device__ __forceinline__ void store4<bf16>(bf16 *p, const f32x4 &v
 // state registers inside the tile loop, where they would also wait for the
 // prefetch of the next tile.
 __device__ __forceinline__ void wait_state_loads() { __builtin_amdgcn_s_waitcnt(0); }
+// Wait for vector memory operations only (s_waitcnt vmcnt(0); expcnt and
+// lgkmcnt at their maxima).  Placed unconditionally ahead of a commit whose
+// LDS stores sit under lane conditions, it retires the prefetch loads on every
+// path, so no wait is needed before the registers are reused for the next
+// tile's loads -- a wait there would also wait for the stores just issued.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // --------------------------------------------------------------- tile I/O
 // Register-staged tile load: issue() starts the global loads of one tile
@@ -1211,6 +1217,18 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     constexpr int NP = CAUSAL ? 2 : 1;  // transposed tiles: dO (and V)
     Prefetch<T, NTH> pq_, pk_;
     PrefetchT<T, NTH, NP> pg_, pv_;
+    // The next tile's rows are committed to LDS right after a tile's last
+    // barrier and before its dQ stores: that commit waits (vmcnt) on loads
+    // issued a tile earlier, never on the stores just issued.
+    auto commit = [&]() {
+        wait_vmem();
+        pq_.template commit<NL>(sQ, nullptr);
+        pg_.template commit<NL>(0, sG, sGt);
+        if constexpr (CAUSAL) {
+            pk_.template commit<NL>(sK, nullptr);
+            pv_.template commit<NL>(1, sV, sVt);
+        }
+    };
     if (j0 < j1) {
         pq_.issue(qp, a.sq.t, j0 * TT, a.T);
         pg_.issue(0, gp, a.sdo.t, j0 * TT, a.T);
@@ -1218,24 +1236,20 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             pk_.issue(kp, a.sk.t, j0 * TT, a.T);
             pv_.issue(1, vp, a.sv.t, j0 * TT, a.T);
         }
+        commit();
     }
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
-        // no barrier before the commit: since the previous tile's last barrier
-        // only dx_store ran, which reads neither the token tiles nor X
-        pq_.template commit<NL>(sQ, nullptr);
-        pg_.template commit<NL>(0, sG, sGt);
+        // next tile's rows; the last tile reloads itself (loads stay in range).
+        // Issue and commit run every iteration: a commit under a condition
+        // leaves the prefetch registers possibly pending at the loop head, and
+        // the wait placed there also waits for the previous tile's stores.
+        const int64_t tn = (jt + 1 < j1 ? jt + 1 : jt) * TT;
+        pq_.issue(qp, a.sq.t, tn, a.T);
+        pg_.issue(0, gp, a.sdo.t, tn, a.T);
         if constexpr (CAUSAL) {
-            pk_.template commit<NL>(sK, nullptr);
-            pv_.template commit<NL>(1, sV, sVt);
-        }
-        if (jt + 1 < j1) {
-            pq_.issue(qp, a.sq.t, t0 + TT, a.T);
-            pg_.issue(0, gp, a.sdo.t, t0 + TT, a.T);
-            if constexpr (CAUSAL) {
-                pk_.issue(kp, a.sk.t, t0 + TT, a.T);
-                pv_.issue(1, vp, a.sv.t, t0 + TT, a.T);
-            }
+            pk_.issue(kp, a.sk.t, tn, a.T);
+            pv_.issue(1, vp, a.sv.t, tn, a.T);
         }
         __syncthreads();
         for (int q = w; q < NTASK; q += NW_) {
@@ -1305,6 +1319,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             tsum += softhash_combine<KB, T, SP, NTH>(sShare, sSpQ, sSmQ, sThQ, z, a.L, a.inv_temp, sDproj);
         }
         __syncthreads();
+        // after the last barrier only dx_store runs, which reads neither the
+        // token tiles nor X: the next tile's rows can go to LDS now
+        commit();
         dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0, a.T, xpart);
     }
     float *out = a.rdelta + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
@@ -1475,6 +1492,20 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     wait_state_loads();
     Prefetch<T, NTH> pq_, pk_, pvn_;  // pvn_: non-causal V (natural only)
     PrefetchT<T, NTH, 2> pg_, pv_;   // causal dO and V (natural and transposed)
+    // The next tile's rows are committed to LDS right after a tile's last
+    // barrier and before its dK stores: that commit waits (vmcnt) on loads
+    // issued a tile earlier, never on the stores just issued.
+    auto commit = [&]() {
+        wait_vmem();
+        pk_.template commit<NL>(sK, nullptr);
+        if constexpr (CAUSAL) {
+            pv_.template commit<NL>(1, sV, sVt);
+            pq_.template commit<NL>(sQ, nullptr);
+            pg_.template commit<NL>(0, sG, sGt);
+        } else {
+            pvn_.template commit<NL>(sV, nullptr);
+        }
+    };
     if (j0 < j1) {
         const int64_t tl = (j1 - 1) * TT;
         pk_.issue(kp, a.sk.t, tl, a.T);
@@ -1485,28 +1516,23 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         } else {
             pvn_.issue(vp, a.sv.t, tl, a.T);
         }
+        commit();
     }
     for (int64_t jr = j1 - 1; jr >= j0; --jr) {
         const int64_t t0 = jr * TT;
-        // no barrier before the commit: since the previous tile's last barrier
-        // only dx_store ran, which reads neither the token tiles nor X / Y
-        pk_.template commit<NL>(sK, nullptr);
+        // next tile's rows (walking down); the last tile reloads itself (loads
+        // stay in range).  Issue and commit run every iteration: a commit under
+        // a condition leaves the prefetch registers possibly pending at the
+        // loop head, and the wait placed there also waits for the previous
+        // tile's stores.
+        const int64_t tn = (jr > j0 ? jr - 1 : jr) * TT;
+        pk_.issue(kp, a.sk.t, tn, a.T);
         if constexpr (CAUSAL) {
-            pv_.template commit<NL>(1, sV, sVt);
-            pq_.template commit<NL>(sQ, nullptr);
-            pg_.template commit<NL>(0, sG, sGt);
+            pv_.issue(1, vp, a.sv.t, tn, a.T);
+            pq_.issue(qp, a.sq.t, tn, a.T);
+            pg_.issue(0, gp, a.sdo.t, tn, a.T);
         } else {
-            pvn_.template commit<NL>(sV, nullptr);
-        }
-        if (jr > j0) {
-            pk_.issue(kp, a.sk.t, t0 - TT, a.T);
-            if constexpr (CAUSAL) {
-                pv_.issue(1, vp, a.sv.t, t0 - TT, a.T);
-                pq_.issue(qp, a.sq.t, t0 - TT, a.T);
-                pg_.issue(0, gp, a.sdo.t, t0 - TT, a.T);
-            } else {
-                pvn_.issue(vp, a.sv.t, t0 - TT, a.T);
-            }
+            pvn_.issue(vp, a.sv.t, tn, a.T);
         }
         __syncthreads();
         for (int q = w; q < NTASK; q += NW_) {
@@ -1615,6 +1641,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             }
         }
         __syncthreads();
+        // after the last barrier only dx_store runs, which reads neither the
+        // token tiles nor X / Y: the next tile's rows can go to LDS now
+        commit();
         dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0, a.T, xpart);
     }
     const float ts = block_sum<NTH>(tsum, sRed);
