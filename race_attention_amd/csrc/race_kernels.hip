@@ -504,39 +504,63 @@ template <> struct OpX<bf16> { Frag<bf16> f; };
 template <> struct OpX<float> { Frag4<float> f; };
 
 // Softmax / corner backward over the wave's 16 buckets (tables of 2^KB
-// buckets, R-aligned), as 16-deep A operands (row, k = local bucket s):
-//   dot[s'][s] = 1 if s and s' share a table (per-table sums, per bucket)
-//   cs[r][s]   = c_{s,k} = +-1 if s is in table tl, r = tl*KB + k (corner sums)
+// buckets, R-aligned): one 16-deep A operand (row r, k = local bucket s) whose
+// product with pd = P dP gives, per local table tl, the corner sums
+// sum_s pd c_{s,k} (c = +-1, corner bit) and the table sum sum_s pd, with
+// each corner row and its table's sum row in the same lane group (rows
+// 4g..4g+3), so no value crosses lanes:
+//   KB=4: g0 = c0 c1 c2 sum, g1 = c3 sum;  KB=3: g = table g: c0 c1 c2 sum;
+//   KB=2: g = table g: c0 c1 sum;          KB=1: g = tables 2g, 2g+1: (c0 sum) x 2.
 template <typename T, int KB> struct HashOps {
     static constexpr int W_ = is_bf16<T>() ? TT : 16;  // bf16: 16 k values, then the same 16 again
-    static constexpr int LDI = ldp_of<T>(W_), NROWS = (16 >> KB) * KB;
-    static constexpr size_t bytes = sizeof(T) * 2 * 16 * LDI;
-    const T *dot, *cs;
+    static constexpr int LDI = ldp_of<T>(W_);
+    static constexpr size_t bytes = sizeof(T) * 16 * LDI;
+    const T *a;
+    // row r: 1 = corner k of local table tl, 2 = sum of tl, 0 = unused;
+    // de = slot of tl's sum row in the row's lane group
+    __host__ __device__ static constexpr int kind_of(int r, int &k, int &tl, int &de) {
+        const int g = r >> 2, e = r & 3;
+        k = 0;
+        if constexpr (KB == 4) {
+            tl = 0;
+            de = g == 0 ? 3 : 1;
+            if (g == 0) return e < 3 ? (k = e, 1) : 2;
+            if (g == 1) return e == 0 ? (k = 3, 1) : (e == 1 ? 2 : 0);
+            return 0;
+        } else if constexpr (KB == 3) {
+            tl = g;
+            de = 3;
+            if (g >= 2) return 0;
+            return e < 3 ? (k = e, 1) : 2;
+        } else if constexpr (KB == 2) {
+            tl = g;
+            de = 2;
+            return e < 2 ? (k = e, 1) : (e == 2 ? 2 : 0);
+        } else {
+            tl = 2 * g + (e >> 1);
+            de = (e & 2) | 1;
+            return (e & 1) ? 2 : 1;
+        }
+    }
     __device__ __forceinline__ void init(T *buf, int nth) {
-        T *d = buf, *c = buf + 16 * LDI;
         for (int idx = threadIdx.x; idx < 16 * LDI; idx += nth) {
             const int r = idx / LDI, kk = idx % LDI, sb = kk & 15;
-            float vd = 0.f, vc = 0.f;
-            if (kk < W_) {
-                vd = (r >> KB) == (sb >> KB) ? 1.f : 0.f;
-                if (r < NROWS && (sb >> KB) == r / KB) vc = ((sb >> (KB - 1 - r % KB)) & 1) ? 1.f : -1.f;
-            }
-            d[idx] = from_f32<T>(vd);
-            c[idx] = from_f32<T>(vc);
+            int k = 0, tl = 0, de = 0;
+            const int kind = kind_of(r, k, tl, de);
+            float v = 0.f;
+            if (kk < W_ && (sb >> KB) == tl) v = kind == 2 ? 1.f : (kind == 1 ? (((sb >> (KB - 1 - k)) & 1) ? 1.f : -1.f) : 0.f);
+            buf[idx] = from_f32<T>(v);
         }
-        dot = d;
-        cs = c;
+        a = buf;
     }
-    __device__ __forceinline__ static OpX<T> op_of(const T *p) {
+    __device__ __forceinline__ OpX<T> op() const {
         OpX<T> o;
         if constexpr (is_bf16<T>())
-            o.f = ld_frag_pi(p + li() * LDI);
+            o.f = ld_frag_pi(a + li() * LDI);
         else
-            o.f = ld_frag16(p + li() * LDI);
+            o.f = ld_frag16(a + li() * LDI);
         return o;
     }
-    __device__ __forceinline__ OpX<T> dot_op() const { return op_of(dot); }
-    __device__ __forceinline__ OpX<T> cs_op() const { return op_of(cs); }
 };
 
 // Token-direction operand of the wave's bucket-row tiles X[2] (lane holds
@@ -705,35 +729,46 @@ __device__ __forceinline__ void totals_of(const f32x4 (&X)[2], f32x4 &tot) {
 }
 
 // Softmax / corner / tanh backward for the wave's buckets on the matrix
-// cores: dP (and P, fp32, bucket-row) -> dproj [TT][ld_of<T>(NCOL)] columns
-// l*K + k of the wave's tables; returns this lane's share of sum du * th.
-//   dl = P (dP - sum_table P dP),  du_k = sum_table dl c_k,
-//   dproj = du * inv_temp * (1 - th^2)
-// The du tile holds row r = tl*KB + k (lane rows 4g..4g+3), column t.
+// cores: dP (and P, fp32, bucket-row) -> dproj [TT][NCOL] columns l*K + k of
+// the wave's tables; returns this lane's share of sum du * th.
+//   du_k = sum_table P (dP - sum_table P dP) c_k
+//        = sum_table pd c_k - (sum_table pd) tanh(u_k),  pd = P dP,
+// since sum_table P c_k = sigmoid(2u_k) - sigmoid(-2u_k) = tanh(u_k) (= sp - sm);
+//   dproj = du * inv_temp * (1 - th^2).
 template <int KB, typename T>
-__device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const float *sth, int sw, int L,
-                              float inv_temp, T *dproj, const HashOps<T, KB> &ho) {
-    constexpr int LDC = ld_of<float>(NCOL), NROWS = HashOps<T, KB>::NROWS;
-    const int g = lg(), i = li(), c0 = (sw >> KB) * KB;
-    const OpX<T> Ad = ho.dot_op(), Ac = ho.cs_op();
+__device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const float *sp, const float *sm,
+                              const float *sth, int sw, int L, float inv_temp, T *dproj, const HashOps<T, KB> &ho) {
+    constexpr int LDC = ld_of<float>(NCOL);
+    const int g = lg(), i = li(), l0 = sw >> KB;
+    const OpX<T> A = ho.op();
     float tsum = 0.f;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        f32x4 pd, dl, dot = zero4(), du = zero4();
+        f32x4 pd, X = zero4();
 #pragma unroll
         for (int e = 0; e < 4; ++e) pd[e] = P[nt][e] * dP[nt][e];
-        mma16_x<T>(dot, Ad, pd);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dl[e] = P[nt][e] * (dP[nt][e] - dot[e]);
-        mma16_x<T>(du, Ac, dl);
+        mma16_x<T>(X, A, pd);
         const int t = 16 * nt + i;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int row = 4 * g + e, col = c0 + row;
-            if (row < NROWS && col < L * KB) {
+            int k = 0, tl = 0, de = 0;
+            const int kind = HashOps<T, KB>::kind_of(4 * g + e, k, tl, de);
+            const int l = l0 + tl, col = l * KB + k;
+            if (kind == 1 && l < L) {
+                float sum;
+                if constexpr (KB == 4)
+                    sum = g == 0 ? X[3] : X[1];
+                else if constexpr (KB == 3)
+                    sum = X[3];
+                else if constexpr (KB == 2)
+                    sum = X[2];
+                else
+                    sum = X[(e & 2) | 1];
+                const float tu = sp[t * LDC + col] - sm[t * LDC + col];
+                const float du = X[e] - sum * tu;
                 const float th = sth[t * LDC + col];
-                tsum += du[e] * th;
-                dproj[sw_off<T, NCOL>(t, col)] = from_f32<T>(du[e] * inv_temp * (1.f - th * th));
+                tsum += du * th;
+                dproj[sw_off<T, NCOL>(t, col)] = from_f32<T>(du * inv_temp * (1.f - th * th));
             }
         }
     }
@@ -1312,7 +1347,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         if constexpr (CAUSAL)
             for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
         if constexpr (KB <= 4) {
-            tsum += softhash_bwd<KB, T>(PQ, dPQ, sThQ, sg, a.L, a.inv_temp, sDproj, ho);
+            tsum += softhash_bwd<KB, T>(PQ, dPQ, sSpQ, sSmQ, sThQ, sg, a.L, a.inv_temp, sDproj, ho);
         } else {
             softhash_share<KB, T>(PQ, dPQ, wh, sShare);
             __syncthreads();
@@ -1633,7 +1668,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             f32x4 PK[2];
             probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PK);
             if constexpr (KB <= 4) {
-                tsum += softhash_bwd<KB, T>(PK, dPK, sThK, sg, a.L, a.inv_temp, sDproj, ho);
+                tsum += softhash_bwd<KB, T>(PK, dPK, sSpK, sSmK, sThK, sg, a.L, a.inv_temp, sDproj, ho);
             } else {
                 softhash_share<KB, T>(PK, dPK, wh, sShare);
                 __syncthreads();
