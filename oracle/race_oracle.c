@@ -1,6 +1,7 @@
 /*
  * race_oracle.c -- CPU fp64 restatement of the RACE attention operator ("F1",
- * per-bucket normalised) and of the reference CPU prefix-mean kernel.
+ * per-bucket normalised; "F2", one normaliser per token) and of the reference
+ * CPU prefix-mean kernel.
  *
  * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP path of
  * race_attention_amd is compared against.  Only tests/, __graft_entry__.smoke()
@@ -16,6 +17,8 @@
  *   misc/race.py:135-138     out_t = sum over all S=L*R buckets of P_Q * E
  *   kernels/cpu/race_pref.cpp:36-101   prefix mean forward (fp64 accumulators)
  *   kernels/cpu/race_pref.cpp:104-220  prefix mean backward (two passes)
+ *   misc/elsaa_causal_complete.py:438-586, misc/race_kernel.py:8-124
+ *                            F2 causal readout num/max(den, 1e-6)
  *
  * Layout used here: streams are independent; every per-stream tensor is
  * [T][D] row-major double.  planes are [NP][L][K][D]; stream n uses planes
@@ -369,4 +372,187 @@ void oracle_prefix_mean_flat_bw(const float *w, const float *v, const float *gE,
         }
         free(invA); free(al); free(B); free(beta);
     }
+}
+
+/* ------------------------------------------------- global normalisation (F2)
+ *
+ * Causal RACE with one normaliser per token instead of one per bucket
+ * (CausalRACEAttention, misc/elsaa_causal_complete.py:438-586; the Triton
+ * readout misc/race_kernel.py:8-124; its autograd
+ * misc/elsaa_causal_complete.py:384-436):
+ *   P = softmax_r(beta * sum_k c[r,k] tanh(<x, w_lk>))        (:483-490)
+ *   num_t = sum_s P_Q[t,s] B_s(t),  den_t = sum_s P_Q[t,s] A_s(t)
+ *           (sums over all L tables, race_kernel.py:108-123)
+ *   out_t = num_t / max(den_t, floor)                           (:537)
+ * with A, B the inclusive prefixes of P_K and P_K v.  beta enters exactly as
+ * inv_temp does in F1, so soft_hash / soft_hash_bwd serve both. */
+static void stream_forward_global(const double *q, const double *k, const double *v,
+                                  const double *pl, int64_t T, int64_t D, int L, int K,
+                                  double floor_, double beta, double *o, double *den)
+{
+    const int R = 1 << K;
+    const int64_t S = (int64_t)L * R;
+    double *A = calloc((size_t)S, sizeof(double));
+    double *B = calloc((size_t)(S * D), sizeof(double));
+    double *th = malloc(sizeof(double) * (size_t)(L * K));
+    double *PK = malloc(sizeof(double) * (size_t)S);
+    double *PQ = malloc(sizeof(double) * (size_t)S);
+    for (int64_t t = 0; t < T; ++t) {
+        soft_hash(k + t * D, pl, D, L, K, beta, th, PK);
+        for (int64_t s = 0; s < S; ++s) {
+            A[s] += PK[s];
+            for (int64_t d = 0; d < D; ++d)
+                B[s * D + d] += PK[s] * v[t * D + d];
+        }
+        soft_hash(q + t * D, pl, D, L, K, beta, th, PQ);
+        double *ot = o + t * D, dn = 0.0;
+        for (int64_t d = 0; d < D; ++d)
+            ot[d] = 0.0;
+        for (int64_t s = 0; s < S; ++s) {
+            dn += PQ[s] * A[s];
+            for (int64_t d = 0; d < D; ++d)
+                ot[d] += PQ[s] * B[s * D + d];
+        }
+        den[t] = dn;
+        const double dc = dn > floor_ ? dn : floor_;
+        for (int64_t d = 0; d < D; ++d)
+            ot[d] /= dc;
+    }
+    free(A); free(B); free(th); free(PK); free(PQ);
+}
+
+/* Backward of stream_forward_global for upstream gradients g (of out) and h
+ * (of den, may be NULL).  With dc = max(den, floor):
+ *   gd_t      = h_t - [den_t >= floor] (g_t . out_t) / dc_t
+ *   dP_Q[t,s] = (g_t . B_s(t)) / dc_t + gd_t A_s(t)
+ *   W[t,s]    = P_Q[t,s] / dc_t,     dA[t,s] = gd_t P_Q[t,s]
+ * and then, as in F1, alpha_s(tau) = sum_{t>=tau} dA[t,s],
+ * U_s(tau) = sum_{t>=tau} W[t,s] g_t, dP_K[tau,s] = alpha_s(tau) + v_tau . U_s(tau),
+ * dv_tau = sum_s P_K[tau,s] U_s(tau). */
+static void stream_backward_global(const double *q, const double *k, const double *v,
+                                   const double *g, const double *h, const double *pl,
+                                   int64_t T, int64_t D, int L, int K, double floor_,
+                                   double beta, double *dq, double *dk, double *dv,
+                                   double *g_beta, double *g_abs)
+{
+    const int R = 1 << K;
+    const int64_t S = (int64_t)L * R;
+    double *A = calloc((size_t)S, sizeof(double));
+    double *B = calloc((size_t)(S * D), sizeof(double));
+    double *dA = malloc(sizeof(double) * (size_t)(T * S));
+    double *W = malloc(sizeof(double) * (size_t)(T * S));
+    double *th = malloc(sizeof(double) * (size_t)(L * K));
+    double *PK = malloc(sizeof(double) * (size_t)S);
+    double *PQ = malloc(sizeof(double) * (size_t)S);
+    double *dP = malloc(sizeof(double) * (size_t)S);
+    double *alpha = calloc((size_t)S, sizeof(double));
+    double *U = calloc((size_t)(S * D), sizeof(double));
+    double *num = malloc(sizeof(double) * (size_t)D);
+
+    memset(dq, 0, sizeof(double) * (size_t)(T * D));
+    memset(dk, 0, sizeof(double) * (size_t)(T * D));
+    memset(dv, 0, sizeof(double) * (size_t)(T * D));
+    for (int64_t t = 0; t < T; ++t) {
+        soft_hash(k + t * D, pl, D, L, K, beta, th, PK);
+        for (int64_t s = 0; s < S; ++s) {
+            A[s] += PK[s];
+            for (int64_t d = 0; d < D; ++d)
+                B[s * D + d] += PK[s] * v[t * D + d];
+        }
+        soft_hash(q + t * D, pl, D, L, K, beta, th, PQ);
+        const double *gt = g + t * D;
+        double dn = 0.0;
+        for (int64_t d = 0; d < D; ++d)
+            num[d] = 0.0;
+        for (int64_t s = 0; s < S; ++s) {
+            dn += PQ[s] * A[s];
+            for (int64_t d = 0; d < D; ++d)
+                num[d] += PQ[s] * B[s * D + d];
+        }
+        const double dc = dn > floor_ ? dn : floor_;
+        double go = 0.0;
+        for (int64_t d = 0; d < D; ++d)
+            go += gt[d] * num[d] / dc;
+        const double gd = (h ? h[t] : 0.0) - (dn >= floor_ ? go / dc : 0.0);
+        for (int64_t s = 0; s < S; ++s) {
+            double G = 0.0;
+            for (int64_t d = 0; d < D; ++d)
+                G += gt[d] * B[s * D + d];
+            dP[s] = G / dc + gd * A[s];
+            W[t * S + s] = PQ[s] / dc;
+            dA[t * S + s] = gd * PQ[s];
+        }
+        soft_hash_bwd(PQ, th, dP, pl, D, L, K, beta, dq + t * D, g_beta, g_abs);
+    }
+    for (int64_t t = T - 1; t >= 0; --t) {
+        const double *gt = g + t * D;
+        const double *vt = v + t * D;
+        for (int64_t s = 0; s < S; ++s) {
+            alpha[s] += dA[t * S + s];
+            for (int64_t d = 0; d < D; ++d)
+                U[s * D + d] += W[t * S + s] * gt[d];
+        }
+        soft_hash(k + t * D, pl, D, L, K, beta, th, PK);
+        double *dvt = dv + t * D;
+        for (int64_t s = 0; s < S; ++s) {
+            double vu = 0.0;
+            for (int64_t d = 0; d < D; ++d) {
+                vu += vt[d] * U[s * D + d];
+                dvt[d] += PK[s] * U[s * D + d];
+            }
+            dP[s] = alpha[s] + vu;
+        }
+        soft_hash_bwd(PK, th, dP, pl, D, L, K, beta, dk + t * D, g_beta, g_abs);
+    }
+    free(A); free(B); free(dA); free(W); free(th); free(PK); free(PQ);
+    free(dP); free(alpha); free(U); free(num);
+}
+
+int oracle_race_global_forward(const double *q, const double *k, const double *v,
+                               const double *planes, const int64_t *plane_of,
+                               int64_t N, int64_t T, int64_t D, int L, int K,
+                               double floor_, double beta, double *out, double *den)
+{
+    if (K < 1 || K > ORACLE_MAX_K || L < 1 || N < 0 || T < 0 || D < 1)
+        return -1;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t n = 0; n < N; ++n) {
+        const double *pl = planes + plane_of[n] * (int64_t)L * K * D;
+        stream_forward_global(q + n * T * D, k + n * T * D, v + n * T * D, pl, T, D,
+                              L, K, floor_, beta, out + n * T * D, den + n * T);
+    }
+    return 0;
+}
+
+int oracle_race_global_backward(const double *q, const double *k, const double *v,
+                                const double *dout, const double *dden,
+                                const double *planes, const int64_t *plane_of,
+                                int64_t N, int64_t T, int64_t D, int L, int K,
+                                double floor_, double beta, double *dq, double *dk,
+                                double *dv, double *grad_beta, double *grad_beta_l1)
+{
+    if (K < 1 || K > ORACLE_MAX_K || L < 1 || N < 0 || T < 0 || D < 1)
+        return -1;
+    double *part = calloc((size_t)(N > 0 ? N : 1), sizeof(double));
+    double *pabs = calloc((size_t)(N > 0 ? N : 1), sizeof(double));
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t n = 0; n < N; ++n) {
+        const double *pl = planes + plane_of[n] * (int64_t)L * K * D;
+        const int64_t o = n * T * D;
+        stream_backward_global(q + o, k + o, v + o, dout + o, dden ? dden + n * T : NULL, pl,
+                               T, D, L, K, floor_, beta, dq + o, dk + o, dv + o,
+                               &part[n], &pabs[n]);
+    }
+    double tot = 0.0, tabs = 0.0;
+    for (int64_t n = 0; n < N; ++n) {
+        tot += part[n];
+        tabs += pabs[n];
+    }
+    if (grad_beta)
+        *grad_beta = tot;
+    if (grad_beta_l1)
+        *grad_beta_l1 = tabs;
+    free(part);
+    free(pabs);
+    return 0;
 }

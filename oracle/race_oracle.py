@@ -1,4 +1,4 @@
-"""CPU checker for the RACE attention operator (F1 semantics).
+"""CPU checker for the RACE attention operator (F1 and F2 semantics).
 
 TEST INFRASTRUCTURE ONLY.  tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg may use this module, and only as the checker; the product
@@ -10,6 +10,9 @@ Two layers:
     kernels/cpu/race_pref.cpp:36-220).  Inputs are [M,B,T,H,D] arrays like the
     reference's BatchedACE; planes are [NP,L,K,D] (NP = 1 when shared,
     misc/race.py:39-51).
+  * ``race_global_forward`` / ``race_global_backward``: the same C file's
+    restatement of the globally normalised causal mode ("F2",
+    misc/elsaa_causal_complete.py:438-586, misc/race_kernel.py:8-124).
   * ``prefix_mean_flat`` / ``prefix_mean_flat_bw``: restatement of the
     reference CPU kernel's flat prefix mean (race_pref.cpp:36-101, :104-220).
   * ``ref_race_pref()``: the reference's own race_pref.cpp compiled from its
@@ -54,6 +57,11 @@ def _lib():
         lib.oracle_race_backward.argtypes = [dp, dp, dp, dp, dp, ip, i64, i64, i64, ci, ci, ci, cd, cd,
                                              dp, dp, dp, dp, dp]
         lib.oracle_race_backward.restype = ci
+        lib.oracle_race_global_forward.argtypes = [dp, dp, dp, dp, ip, i64, i64, i64, ci, ci, cd, cd, dp, dp]
+        lib.oracle_race_global_forward.restype = ci
+        lib.oracle_race_global_backward.argtypes = [dp, dp, dp, dp, dp, dp, ip, i64, i64, i64, ci, ci, cd, cd,
+                                                    dp, dp, dp, dp, dp]
+        lib.oracle_race_global_backward.restype = ci
         lib.oracle_prefix_mean_flat.argtypes = [fp, fp, i64, i64, i64, cd, fp]
         lib.oracle_prefix_mean_flat.restype = None
         lib.oracle_prefix_mean_flat_bw.argtypes = [fp, fp, fp, i64, i64, i64, cd, fp, fp]
@@ -131,6 +139,56 @@ def race_backward(q, k, v, dout, planes, *, causal: bool, eps: float = 1e-6, inv
         raise ValueError("oracle_race_backward rejected its arguments")
     res = (from_streams(dq, M, B, H), from_streams(dk, M, B, H), from_streams(dv, M, B, H), float(git[0]))
     return res + (float(git[1]),) if with_l1 else res
+
+
+def den_to_streams(h, M, B, H):
+    """[M,B,H,T] (or [N,T]) per-token array -> [N,T] float64, stream-major."""
+    return np.ascontiguousarray(np.asarray(h, dtype=np.float64).reshape(M * B * H, -1))
+
+
+def race_global_forward(q, k, v, planes, *, floor: float = 1e-6, beta: float):
+    """fp64 F2 forward (causal).  q,k,v [M,B,T,H,D]; planes [NP,L,K,D].
+    Returns (out [M,B,T,H,D], den [M,B,H,T]) with out = num / max(den, floor)
+    and den the sum over all L*2^K buckets of P_Q A(t) (unclamped)."""
+    M, B, T, H, D = q.shape
+    planes = np.ascontiguousarray(np.asarray(planes, dtype=np.float64))
+    NP, L, K, Dp = planes.shape
+    assert Dp == D
+    qs, ks, vs = to_streams(q), to_streams(k), to_streams(v)
+    pm = _plane_map(M, B, H, NP)
+    out = np.zeros_like(qs)
+    den = np.zeros((qs.shape[0], T), dtype=np.float64)
+    rc = _lib().oracle_race_global_forward(_dptr(qs), _dptr(ks), _dptr(vs), _dptr(planes),
+                                           pm.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                           qs.shape[0], T, D, L, K, float(floor), float(beta),
+                                           _dptr(out), _dptr(den))
+    if rc != 0:
+        raise ValueError("oracle_race_global_forward rejected its arguments")
+    return from_streams(out, M, B, H), den.reshape(M, B, H, T)
+
+
+def race_global_backward(q, k, v, dout, planes, *, dden=None, floor: float = 1e-6, beta: float,
+                         with_l1: bool = False):
+    """fp64 F2 backward for upstream gradients dout [M,B,T,H,D] and dden
+    [M,B,H,T] (None = 0).  Returns (dq, dk, dv, grad_beta[, l1 mass of the
+    grad_beta summands])."""
+    M, B, T, H, D = q.shape
+    planes = np.ascontiguousarray(np.asarray(planes, dtype=np.float64))
+    NP, L, K, _ = planes.shape
+    qs, ks, vs, gs = to_streams(q), to_streams(k), to_streams(v), to_streams(dout)
+    hs = den_to_streams(dden, M, B, H) if dden is not None else None
+    pm = _plane_map(M, B, H, NP)
+    dq, dk, dv = np.zeros_like(qs), np.zeros_like(qs), np.zeros_like(qs)
+    gb = np.zeros(2, dtype=np.float64)
+    rc = _lib().oracle_race_global_backward(_dptr(qs), _dptr(ks), _dptr(vs), _dptr(gs),
+                                            _dptr(hs) if hs is not None else None, _dptr(planes),
+                                            pm.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                            qs.shape[0], T, D, L, K, float(floor), float(beta),
+                                            _dptr(dq), _dptr(dk), _dptr(dv), _dptr(gb), _dptr(gb[1:]))
+    if rc != 0:
+        raise ValueError("oracle_race_global_backward rejected its arguments")
+    res = (from_streams(dq, M, B, H), from_streams(dk, M, B, H), from_streams(dv, M, B, H), float(gb[0]))
+    return res + (float(gb[1]),) if with_l1 else res
 
 
 def prefix_mean_flat(w, v, eps: float = 1e-6):
