@@ -90,6 +90,42 @@ int race_bwd(const race_desc *d, const void *q, const void *k, const void *v,
              void *dq, void *dk, void *dv, float *grad_inv_temp, void *ws,
              size_t ws_bytes, void *stream);
 
+/* ---------------------------------------------------------------------
+ * Global normalisation ("F2", causal only): one normaliser per token
+ * instead of one per bucket, the readout of CausalRACEAttention
+ * (misc/elsaa_causal_complete.py:438-586) and of its Triton kernel
+ * (misc/race_kernel.py:8-124):
+ *   P as above with inv_temp = beta (logits = beta * sum_k c[r,k] th_k,
+ *   misc/elsaa_causal_complete.py:483-490);
+ *   num_t = sum_s P_Q[t,s] B_s(t),  den_t = sum_s P_Q[t,s] A_s(t)
+ *           (sums over all L tables and 2^K corners);
+ *   out_t = num_t / max(den_t, eps)   (eps = the floor, 1e-6 in the reference).
+ * den is fp32 [M*B*H][T], stream-major (stream n = (m*B + b)*H + h),
+ * contiguous.  The state buffer is race_state_bytes() as for race_fwd.
+ * --------------------------------------------------------------------- */
+size_t race_fwd_global_workspace_bytes(const race_desc *d);
+size_t race_bwd_global_workspace_bytes(const race_desc *d);
+
+/* Forward.  Replaces race_chunkwise_triton_forward (misc/race_kernel.py:126-163)
+ * together with the phi / chunk-state / division steps of
+ * CausalRACEAttention.forward (misc/elsaa_causal_complete.py:492-544):
+ * writes out and den (unclamped; the module's d_token is den's mean over
+ * heads divided by L, clamped at 1e-6). */
+int race_fwd_global(const race_desc *d, const void *q, const void *k,
+                    const void *v, const float *planes, void *out, float *den,
+                    void *state, void *ws, size_t ws_bytes, void *stream);
+
+/* Backward.  Replaces _RaceChunkwiseTritonFn.backward
+ * (misc/elsaa_causal_complete.py:392-436) and the autograd of the module's
+ * phi and division: out and den are the forward's outputs, dout the
+ * gradient of out, dden (nullable = zero) the gradient of den, fp32 like den.
+ * grad_beta (nullable, device fp32 scalar) receives dL/d(beta). */
+int race_bwd_global(const race_desc *d, const void *q, const void *k,
+                    const void *v, const float *planes, const void *out,
+                    const float *den, const void *dout, const float *dden,
+                    const void *state, void *dq, void *dk, void *dv,
+                    float *grad_beta, void *ws, size_t ws_bytes, void *stream);
+
 /* Causal prefix mean over flat streams, the reference CPU kernel's operator
  * (race_prefix_mean_flat, kernels/cpu/race_pref.cpp:36-101):
  * w [NS][T], v [NS][T][D], E [NS][T][D], all fp32 contiguous;

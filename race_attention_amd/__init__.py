@@ -6,8 +6,12 @@ PyTorch modules mirroring the reference API:
                            RACEPrefixMeanFlatFn   (misc/race.py)
   race_attention_amd.vit   non-causal BatchedACE / RACEAttention / RACEBlock
                            (misc/vit.py)
-  race_attention_amd.functional  race_attention(), RACEFunction, raw calls
+  race_attention_amd.causal  globally normalised CausalRACEAttention
+                           (misc/elsaa_causal_complete.py)
+  race_attention_amd.functional  race_attention(), race_attention_global(),
+                           RACEFunction, RACEGlobalFunction, raw calls
 """
-from .functional import RACEFunction, RACEPrefixMeanFlatFn, race_attention  # noqa: F401
+from .functional import (RACEFunction, RACEGlobalFunction, RACEPrefixMeanFlatFn, race_attention,  # noqa: F401
+                         race_attention_global)
 
-__all__ = ["RACEFunction", "RACEPrefixMeanFlatFn", "race_attention"]
+__all__ = ["RACEFunction", "RACEGlobalFunction", "RACEPrefixMeanFlatFn", "race_attention", "race_attention_global"]

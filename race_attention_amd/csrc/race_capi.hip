@@ -45,6 +45,9 @@ struct Plan {
     size_t esize = 0;
     size_t state_bytes = 0, fws = 0, bws = 0;
     size_t fws_core = 0, bws_core = 0, part_bytes = 0;  // partial-output buffers follow the core
+    // global normalisation: den partials after the forward workspace; rden
+    // and gden [N][T] after the backward workspace
+    size_t gfws = 0, gbws = 0, tok_bytes = 0;
 };
 
 // Bucket slices: a workgroup handles SP buckets (bf16: 32, 64 or 128; fp32:
@@ -108,6 +111,9 @@ int make_plan(const race_desc *d, Plan &p) {
     p.part_bytes = p.parts ? (size_t)p.nslice * p.N * d->T * D * sizeof(float) : 0;
     p.fws = p.fws_core + p.part_bytes;        // partial O
     p.bws = p.bws_core + 3 * p.part_bytes;    // partial dQ, dK, dV
+    p.tok_bytes = align16((size_t)p.N * d->T * sizeof(float));
+    p.gfws = p.fws + (p.parts ? p.nslice * p.tok_bytes : 0);
+    p.gbws = p.bws + 2 * p.tok_bytes;
     return RACE_OK;
 }
 
@@ -179,9 +185,9 @@ template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Pla
         k_fwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
     if (run_phase(d, RACE_PHASE_OUT)) {
         if (d->causal)
-            k_fwd_out<T, SP, true, KB><<<grid, threads_of(SP), 0, s>>>(a);
+            k_fwd_out<T, SP, true, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         else
-            k_fwd_out<T, SP, false, KB><<<grid, threads_of(SP), 0, s>>>(a);
+            k_fwd_out<T, SP, false, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) slice_sum<T>(p, d, a.opart, d->o_stride, a.out, s);
     }
     return launched("race_fwd");
@@ -192,9 +198,9 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
     const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
         if (d->causal)
-            k_bwd_reduce<T, SP, true, KB><<<grid, threads_of(SP), 0, s>>>(a);
+            k_bwd_reduce<T, SP, true, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         else
-            k_bwd_reduce<T, SP, false, KB><<<grid, threads_of(SP), 0, s>>>(a);
+            k_bwd_reduce<T, SP, false, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) slice_sum<T>(p, d, a.dqpart, d->g_stride, a.dq, s);
     }
     const int elems = p.Spad * SROW;
@@ -203,9 +209,9 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
                                                                             d->causal);
     if (run_phase(d, RACE_PHASE_OUT)) {
         if (d->causal)
-            k_bwd_out<T, SP, true, KB><<<grid, threads_of(SP), 0, s>>>(a);
+            k_bwd_out<T, SP, true, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         else
-            k_bwd_out<T, SP, false, KB><<<grid, threads_of(SP), 0, s>>>(a);
+            k_bwd_out<T, SP, false, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) {
             slice_sum<T>(p, d, a.dkpart, d->g_stride, a.dk, s);
             slice_sum<T>(p, d, a.dvpart, d->g_stride, a.dv, s);
@@ -213,6 +219,54 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
         if (grad_inv_temp) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, 2 * p.N * p.nseg * p.nslice, grad_inv_temp);
     }
     return launched("race_bwd");
+}
+
+// Global normalisation (causal): the F1 reduce and scan kernels, then the GN
+// readout; its den partials (sliced) are summed with the numerators.
+template <typename T, int SP, int KB> int gn_fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
+    const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
+    if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
+    const int elems = p.Spad * SROW;
+    if (run_phase(d, RACE_PHASE_SCAN))
+        k_fwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
+    if (run_phase(d, RACE_PHASE_OUT)) {
+        k_fwd_out<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
+        if (sliced<T, KB>()) {
+            const int64_t n4 = p.N * d->T * (D / 4);
+            k_slice_sum_gn<T><<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(
+                a.opart, a.denpart, p.nslice, p.N, d->T, (int)d->B, (int)d->H, strides_of(d->o_stride), (T *)a.out,
+                a.den, d->eps);
+        }
+    }
+    return launched("race_fwd_global");
+}
+
+// The prologue kernel turns (out, den, dout, dden) into per-token rden, gden;
+// the backward kernels then run in GN mode.
+template <typename T, int SP, int KB>
+int gn_bwd_impl(const race_desc *d, const Plan &p, Args a, const void *out, const float *den, const float *dden,
+                float *grad_beta, hipStream_t s) {
+    const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
+    if (run_phase(d, RACE_PHASE_REDUCE)) {
+        const int64_t nthr = p.N * d->T * 16;
+        k_gn_prep<T><<<(unsigned)((nthr + 255) / 256), 256, 0, s>>>(
+            (const T *)out, strides_of(d->o_stride), (const T *)a.dout, a.sdo, den, dden, p.N, d->T, (int)d->B,
+            (int)d->H, d->eps, const_cast<float *>(a.rden), const_cast<float *>(a.gden));
+        k_bwd_reduce<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
+        if (sliced<T, KB>()) slice_sum<T>(p, d, a.dqpart, d->g_stride, a.dq, s);
+    }
+    const int elems = p.Spad * SROW;
+    if (run_phase(d, RACE_PHASE_SCAN))
+        k_bwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.rstate, a.rdelta, p.nseg, elems, 1);
+    if (run_phase(d, RACE_PHASE_OUT)) {
+        k_bwd_out<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
+        if (sliced<T, KB>()) {
+            slice_sum<T>(p, d, a.dkpart, d->g_stride, a.dk, s);
+            slice_sum<T>(p, d, a.dvpart, d->g_stride, a.dv, s);
+        }
+        if (grad_beta) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, 2 * p.N * p.nseg * p.nslice, grad_beta);
+    }
+    return launched("race_bwd_global");
 }
 
 // Compiled (dtype, slice buckets, hash bits) combinations: every K in 1..8
@@ -238,6 +292,38 @@ int bwd_dispatch(const race_desc *d, const Plan &p, const Args &a, float *git, h
     RACE_FOR_COMBOS(X)
 #undef X
     return fail(RACE_E_UNSUPPORTED, "bucket count / hash bits combination not compiled");
+}
+
+template <typename T> int gn_fwd_dispatch(const race_desc *d, const Plan &p, const Args &a, hipStream_t s) {
+#define X(TT_, SP_, KB_)                                                                                             \
+    if (std::is_same<T, TT_>::value && p.SP == SP_ && d->K == KB_) return gn_fwd_impl<TT_, SP_, KB_>(d, p, a, s);
+    RACE_FOR_COMBOS(X)
+#undef X
+    return fail(RACE_E_UNSUPPORTED, "bucket count / hash bits combination not compiled");
+}
+
+template <typename T>
+int gn_bwd_dispatch(const race_desc *d, const Plan &p, const Args &a, const void *out, const float *den,
+                    const float *dden, float *gb, hipStream_t s) {
+#define X(TT_, SP_, KB_)                                                                                             \
+    if (std::is_same<T, TT_>::value && p.SP == SP_ && d->K == KB_)                                                   \
+        return gn_bwd_impl<TT_, SP_, KB_>(d, p, a, out, den, dden, gb, s);
+    RACE_FOR_COMBOS(X)
+#undef X
+    return fail(RACE_E_UNSUPPORTED, "bucket count / hash bits combination not compiled");
+}
+
+int check_gn(const race_desc *d) {
+    if (d->causal != 1)
+        return fail(RACE_E_UNSUPPORTED, "global normalisation is implemented for the causal operator only");
+    if (!(d->eps > 0.f)) return fail(RACE_E_INVALID, "eps (the floor of den) must be > 0 for global normalisation");
+    return RACE_OK;
+}
+
+int check_den(const char *name, const float *p) {
+    if (!p) return fail(RACE_E_INVALID, "%s is NULL", name);
+    if ((uintptr_t)p % 4) return fail(RACE_E_INVALID, "%s is not 4-byte aligned", name);
+    return RACE_OK;
 }
 
 // prefix mean: segment length so that NS * nseg ~ 4096 waves
@@ -350,6 +436,93 @@ int race_bwd(const race_desc *d, const void *q, const void *k, const void *v, co
     return bwd_dispatch<float>(d, p, a, grad_inv_temp, s);
 }
 
+size_t race_fwd_global_workspace_bytes(const race_desc *d) {
+    Plan p;
+    if (make_plan(d, p) != RACE_OK) return 0;
+    ok();
+    return p.gfws;
+}
+
+size_t race_bwd_global_workspace_bytes(const race_desc *d) {
+    Plan p;
+    if (make_plan(d, p) != RACE_OK) return 0;
+    ok();
+    return p.gbws;
+}
+
+int race_fwd_global(const race_desc *d, const void *q, const void *k, const void *v, const float *planes, void *out,
+                    float *den, void *state, void *ws, size_t ws_bytes, void *stream) {
+    Plan p;
+    int rc = make_plan(d, p);
+    if (rc || (rc = check_gn(d))) return rc;
+    if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
+        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) || (rc = check_tensor("out", out, d->o_stride, p.esize, d->T)) ||
+        (rc = check_den("den", den)))
+        return rc;
+    if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
+    if (!state) return fail(RACE_E_INVALID, "state is NULL");
+    if (!ws || ws_bytes < p.gfws)
+        return fail(RACE_E_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, p.gfws);
+    Args a = base_args(d, p, planes);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    a.den = den;
+    a.fstate = (double *)state;
+    a.fdelta = (double *)ws;
+    a.opart = p.parts ? (float *)((char *)ws + p.fws_core) : nullptr;
+    a.denpart = p.parts ? (float *)((char *)ws + p.fws) : nullptr;
+    hipStream_t s = (hipStream_t)stream;
+    if (d->dtype == RACE_DTYPE_BF16) return gn_fwd_dispatch<bf16>(d, p, a, s);
+    return gn_fwd_dispatch<float>(d, p, a, s);
+}
+
+int race_bwd_global(const race_desc *d, const void *q, const void *k, const void *v, const float *planes,
+                    const void *out, const float *den, const void *dout, const float *dden, const void *state,
+                    void *dq, void *dk, void *dv, float *grad_beta, void *ws, size_t ws_bytes, void *stream) {
+    Plan p;
+    int rc = make_plan(d, p);
+    if (rc || (rc = check_gn(d))) return rc;
+    if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
+        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) ||
+        (rc = check_tensor("out", out, d->o_stride, p.esize, d->T)) ||
+        (rc = check_tensor("dout", dout, d->do_stride, p.esize, d->T)) ||
+        (rc = check_tensor("dq", dq, d->g_stride, p.esize, d->T)) || (rc = check_tensor("dk", dk, d->g_stride, p.esize, d->T)) ||
+        (rc = check_tensor("dv", dv, d->g_stride, p.esize, d->T)) || (rc = check_den("den", den)) ||
+        (dden && (rc = check_den("dden", dden))))
+        return rc;
+    if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
+    if (!state) return fail(RACE_E_INVALID, "state is NULL");
+    if (!ws || ws_bytes < p.gbws)
+        return fail(RACE_E_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, p.gbws);
+    Args a = base_args(d, p, planes);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.dout = dout;
+    a.dq = dq;
+    a.dk = dk;
+    a.dv = dv;
+    a.fstate = (double *)state;
+    const size_t blk = (size_t)p.N * p.nseg * p.Spad * SROW;
+    a.rdelta = (float *)ws;
+    a.rstate = a.rdelta + blk;
+    a.tpart = a.rstate + blk;
+    if (p.parts) {
+        float *part = (float *)((char *)ws + p.bws_core);
+        const size_t pe = p.part_bytes / sizeof(float);
+        a.dqpart = part;
+        a.dkpart = part + pe;
+        a.dvpart = part + 2 * pe;
+    }
+    a.rden = (const float *)((char *)ws + p.bws);
+    a.gden = (const float *)((char *)ws + p.bws + p.tok_bytes);
+    hipStream_t s = (hipStream_t)stream;
+    if (d->dtype == RACE_DTYPE_BF16) return gn_bwd_dispatch<bf16>(d, p, a, out, den, dden, grad_beta, s);
+    return gn_bwd_dispatch<float>(d, p, a, out, den, dden, grad_beta, s);
+}
+
 size_t race_prefix_mean_workspace_bytes(int64_t NS, int64_t T, int64_t D) {
     if (NS < 1 || T < 1 || D < 1) return 0;
     const int64_t tseg = pm_tseg(NS, T), nseg = (T + tseg - 1) / tseg;
@@ -408,6 +581,6 @@ int race_prefix_mean_bwd(const float *w, const float *v, const float *gE, float 
 
 const char *race_last_error(void) { return g_err.c_str(); }
 
-int race_abi_version(void) { return 1; }
+int race_abi_version(void) { return 2; }
 
 } // extern "C"

@@ -64,6 +64,11 @@ struct Args {
     float *tpart;    // [2][N][nseg][nslice] partial sums of dU*th
     // sliced() instantiations: per-slice fp32 partial outputs [nslice][N][T][D], summed by k_slice_sum
     float *opart, *dqpart, *dkpart, *dvpart;
+    // global normalisation (GN instantiations; eps is the floor of den):
+    // den [N][T] output (sliced: per-slice partials denpart [nslice][N][T]);
+    // backward inputs rden = 1/max(den, eps) and gden = dL/d den, [N][T]
+    float *den, *denpart;
+    const float *rden, *gden;
 };
 
 constexpr int SROW = D + 1;  // state row: D values of B (or U) then A (or alpha)
@@ -97,6 +102,14 @@ __device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x);
 
 // 4 consecutive elements (one lane's accumulator column) to global memory
 template <typename T> __device__ __forceinline__ void store4(T *p, const f32x4 &v);
+// 4 consecutive elements (8- or 16-byte aligned) as fp32
+template <typename T> __device__ __forceinline__ f32x4 load4(const T *p);
+template <> __device__ __forceinline__ f32x4 load4<float>(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
+template <> __device__ __forceinline__ f32x4 load4<bf16>(const bf16 *p) {
+    const uint2 u = *reinterpret_cast<const uint2 *>(p);
+    return f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u), __uint_as_float(u.y << 16),
+                 __uint_as_float(u.y & 0xFFFF0000u)};
+}
 template <> __device__ __forceinline__ void store4<float>(float *p, const f32x4 &v) {
     *reinterpret_cast<f32x4 *>(p) = v;
 }
@@ -332,6 +345,24 @@ template <typename T, int NTH, int NPART> struct PrefetchT {
                 *reinterpret_cast<uint2 *>(row + RW) = uint2{a.y, b.y};
             }
         }
+    }
+};
+
+// Per-token fp32 pair (a[t], b[t]) of a 32-token tile (the GN backward's
+// 1/max(den, eps) and dL/d den), loaded by wave 0 with the token tiles and
+// committed to LDS as [2][TT] with them; zero past the sequence end.
+struct TokPre {
+    float v;
+    __device__ __forceinline__ void issue(const float *__restrict__ a, const float *__restrict__ b, int64_t t0,
+                                          int64_t Tn) {
+        v = 0.f;
+        if (threadIdx.x < 64) {
+            const int t = threadIdx.x & 31;
+            if (t < tile_rows(t0, Tn)) v = (threadIdx.x < 32 ? a : b)[t0 + t];
+        }
+    }
+    __device__ __forceinline__ void commit(float *dst) const {
+        if (threadIdx.x < 64) dst[threadIdx.x] = v;
     }
 };
 
@@ -998,7 +1029,7 @@ __global__ void k_fwd_scan(double *fstate, const double *fdelta, int nseg, int e
 // P_K and B (tile start) to LDS as [.][s] arrays, then computes output tiles
 // over all buckets; the B carry of its buckets stays in registers.
 // =====================================================================
-template <typename T, int SP, bool CAUSAL> struct FwdOutL {
+template <typename T, int SP, bool CAUSAL, bool GN> struct FwdOutL {
     static constexpr int NW_ = SP / WB;
     // The Q and K tiles live inside the P_K / W region when they fit: they
     // are dead from the projection until the next tile's commit, P_K and W
@@ -1020,12 +1051,18 @@ template <typename T, int SP, bool CAUSAL> struct FwdOutL {
     static constexpr size_t oPl = ALIAS ? oEnd : oKEnd;
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t oCst = align16(oPlLo + sizeof(T) * NCOL * LDN);
-    static constexpr size_t bytes = align16(oCst + Consts<T>::bytes);
+    static constexpr size_t oDen = align16(oCst + Consts<T>::bytes);  // GN: [NW_][TT] per-wave den shares
+    static constexpr size_t bytes = align16(oDen + (GN ? sizeof(float) * NW_ * TT : 0));
 };
 
-template <typename T, int SP, bool CAUSAL>
+// Output tile (d = 16md.., t = 16nt..).  GN: the tile's numerator is divided
+// by max(den, eps), den summed from the waves' shares (sDen [NW_][TT]); the
+// md == 0 tiles also write den.  Sliced GN instantiations write the
+// numerator and this slice's den share as partials instead.
+template <typename T, int SP, bool CAUSAL, bool GN = false>
 __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T *Wts, const T *sVt, T *op,
-                             int64_t st, int64_t t0, int64_t Tn, float *part) {
+                             int64_t st, int64_t t0, int64_t Tn, float *part, const float *sDen = nullptr,
+                             float *den = nullptr, float eps = 0.f) {
     constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
     const T *pb = sw_frag_ptr<T, SP>(sBT, 16 * md + i), *pw = sw_frag_ptr<T, SP>(Wts, 16 * nt + i);
@@ -1049,6 +1086,18 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
         mma(O, ld_frag_pi(sVt + (16 * md + i) * LDT), frag_acc<T>(Sc[0], Sc[1]));
     }
     const int t = 16 * nt + i;
+    if constexpr (GN) {
+        constexpr int NW_ = SP / WB;
+        float dn = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW_; ++w) dn += sDen[w * TT + t];
+        if (!part) {
+            const float r = 1.0f / fmaxf(dn, eps);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) O[e] *= r;
+        }
+        if (md == 0 && g == 0 && t0 + t < Tn) den[t0 + t] = dn;
+    }
     if (t0 + t < Tn) {
         if (part)
             store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, O);
@@ -1057,9 +1106,12 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
     }
 }
 
-template <typename T, int SP, bool CAUSAL, int KB>
+// GN: global normalisation (causal only) -- W = P_Q, and the output is
+// divided by den(t) = sum over all buckets of P_Q A_s(t), clamped below at eps.
+template <typename T, int SP, bool CAUSAL, int KB, bool GN>
 __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(Args a) {
-    using Ly = FwdOutL<T, SP, CAUSAL>;
+    static_assert(CAUSAL || !GN, "global normalisation is causal only");
+    using Ly = FwdOutL<T, SP, CAUSAL, GN>;
     using NL = typename Ly::NL;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC, LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
@@ -1080,6 +1132,9 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
     T *op = (T *)a.out + stream_off(a.so, n, a.B, a.H);
     float *opart = sliced<T, KB>() ? a.opart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
+    float *sDen = (float *)(smem + Ly::oDen);
+    float *denp = !GN ? nullptr
+                      : sliced<T, KB>() ? a.denpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T : a.den + (int64_t)n * a.T;
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
@@ -1143,12 +1198,25 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             tot = zero4();
             mma(tot, Pf, cst.ones());
         }
-        // W = P_Q / (A(t) + eps)
-        for (int nt = 0; nt < 2; ++nt)
-            for (int e = 0; e < 4; ++e) {
-                const float A = (float)a0[e] + (CAUSAL ? Acum[nt][e] : 0.f);
-                W[nt][e] = PQ[nt][e] * rcp(A + a.eps);
+        if constexpr (GN) {
+            // W = P_Q; this wave's share of den(t) = sum_s P_Q A_s(t)
+            for (int nt = 0; nt < 2; ++nt) {
+                float dp = 0.f;
+                for (int e = 0; e < 4; ++e) {
+                    dp += PQ[nt][e] * ((float)a0[e] + Acum[nt][e]);
+                    W[nt][e] = PQ[nt][e];
+                }
+                dp = xor32_sum(xor16_sum(dp));
+                if (g == 0) sDen[w * TT + 16 * nt + i] = dp;
             }
+        } else {
+            // W = P_Q / (A(t) + eps)
+            for (int nt = 0; nt < 2; ++nt)
+                for (int e = 0; e < 4; ++e) {
+                    const float A = (float)a0[e] + (CAUSAL ? Acum[nt][e] : 0.f);
+                    W[nt][e] = PQ[nt][e] * rcp(A + a.eps);
+                }
+        }
         store_ts<T, SP>(sWts, sw, W);
         if constexpr (CAUSAL) {
             store_ts<T, SP>(sPts, sw, PK);
@@ -1156,7 +1224,8 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         }
         __syncthreads();
         for (int q = w; q < 8; q += NW_)
-            fwd_out_tile<T, SP, CAUSAL>(q >> 1, q & 1, sBT, sPts, sWts, sVt, op, a.so.t, t0, a.T, opart);
+            fwd_out_tile<T, SP, CAUSAL, GN>(q >> 1, q & 1, sBT, sPts, sWts, sVt, op, a.so.t, t0, a.T, opart, sDen,
+                                            denp, a.eps);
         if constexpr (CAUSAL) {
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
             for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, ld_frag_pi(sVt + (16 * md + i) * LDT));
@@ -1169,7 +1238,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 // k_bwd_reduce: forward walk.  dQ, and per-segment sums of
 // alpha = sum_t dA and U = sum_t W^T g.
 // =====================================================================
-template <typename T, int SP, bool CAUSAL, int KB> struct BwdReduceL {
+template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr int NW_ = SP / WB;
     static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>();
     static constexpr size_t oQ = 0;
@@ -1189,12 +1258,16 @@ template <typename T, int SP, bool CAUSAL, int KB> struct BwdReduceL {
     static constexpr size_t oHash = align16(oCst + Consts<T>::bytes);
     static constexpr size_t oPair = align16(oHash + HashOps<T, 4>::bytes);
     static constexpr size_t oShare = align16(oPair + PairOps<T>::bytes);
-    static constexpr size_t bytes = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
+    static constexpr size_t oTok = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
+    static constexpr size_t bytes = align16(oTok + (GN ? sizeof(float) * 2 * TT : 0));  // GN: rden, gden
 };
 
-template <typename T, int SP, bool CAUSAL, int KB>
+// GN (global normalisation, causal only): with rd = 1/max(den, eps) and
+// gd = dL/d den per token, W = P_Q rd, dP_Q = G rd + gd A_s(t), dA = gd P_Q.
+template <typename T, int SP, bool CAUSAL, int KB, bool GN>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
-    using Ly = BwdReduceL<T, SP, CAUSAL, KB>;
+    static_assert(CAUSAL || !GN, "global normalisation is causal only");
+    using Ly = BwdReduceL<T, SP, CAUSAL, KB, GN>;
     using NL = NatL<T, true>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     constexpr int NTASK = CAUSAL ? 11 : 4;  // Q projection (4), K projection (4), X tiles (3)
@@ -1219,6 +1292,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     const T *gp = (const T *)a.dout + stream_off(a.sdo, n, a.B, a.H);
     T *dqp = (T *)a.dq + stream_off(a.sg, n, a.B, a.H);
     float *xpart = sliced<T, KB>() ? a.dqpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
+    float *sTok = (float *)(smem + Ly::oTok);
+    const float *rdp = GN ? a.rden + (int64_t)n * a.T : nullptr, *gdp = GN ? a.gden + (int64_t)n * a.T : nullptr;
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
@@ -1252,6 +1327,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     constexpr int NP = CAUSAL ? 2 : 1;  // transposed tiles: dO (and V)
     Prefetch<T, NTH> pq_, pk_;
     PrefetchT<T, NTH, NP> pg_, pv_;
+    TokPre pt_;
     // The next tile's rows are committed to LDS right after a tile's last
     // barrier and before its dQ stores: that commit waits (vmcnt) on loads
     // issued a tile earlier, never on the stores just issued.
@@ -1263,6 +1339,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             pk_.template commit<NL>(sK, nullptr);
             pv_.template commit<NL>(1, sV, sVt);
         }
+        if constexpr (GN) pt_.commit(sTok);
     };
     if (j0 < j1) {
         pq_.issue(qp, a.sq.t, j0 * TT, a.T);
@@ -1271,6 +1348,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             pk_.issue(kp, a.sk.t, j0 * TT, a.T);
             pv_.issue(1, vp, a.sv.t, j0 * TT, a.T);
         }
+        if constexpr (GN) pt_.issue(rdp, gdp, j0 * TT, a.T);
         commit();
     }
     for (int64_t jt = j0; jt < j1; ++jt) {
@@ -1286,6 +1364,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             pk_.issue(kp, a.sk.t, tn, a.T);
             pv_.issue(1, vp, a.sv.t, tn, a.T);
         }
+        if constexpr (GN) pt_.issue(rdp, gdp, tn, a.T);
         __syncthreads();
         for (int q = w; q < NTASK; q += NW_) {
             if (q < 4)
@@ -1311,12 +1390,24 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             tot = zero4();
             mma(tot, Pf, cst.ones());
         }
-        for (int nt = 0; nt < 2; ++nt)
+        f32x4 Ag[2];  // GN: A_s(t)
+        float rd[2], gd[2];
+        for (int nt = 0; nt < 2; ++nt) {
+            if constexpr (GN) {
+                rd[nt] = sTok[16 * nt + i];
+                gd[nt] = sTok[TT + 16 * nt + i];
+            }
             for (int e = 0; e < 4; ++e) {
                 const float A = (float)a0[e] + (CAUSAL ? Acum[nt][e] : 0.f);
-                inv[nt][e] = rcp(A + a.eps);
+                if constexpr (GN) {
+                    Ag[nt][e] = A;
+                    inv[nt][e] = rd[nt];
+                } else {
+                    inv[nt][e] = rcp(A + a.eps);
+                }
                 W[nt][e] = PQ[nt][e] * inv[nt][e];
             }
+        }
         const Frag<T> Wf = token_operand<T>(W, cst, po);
         // G[s][t] = g_t . B_s(t) = sum_d B[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
         f32x4 dPQ[2], dA[2];
@@ -1327,10 +1418,15 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
                 mma(G, b0, NL::frag_pi(sG, 16 * nt + i, 0));
                 mma(G, b1, NL::frag_pi(sG, 16 * nt + i, 1));
                 if constexpr (CAUSAL) mma(G, Pf, ld_frag_pi(sX + (16 * nt + i) * LDT));
-                // dP_Q = G/(A+eps); dA = -W G/(A+eps)
+                // dP_Q = G/(A+eps); dA = -W G/(A+eps).  GN: dP_Q = G rd + gd A; dA = gd P_Q
                 for (int e = 0; e < 4; ++e) {
-                    dPQ[nt][e] = G[e] * inv[nt][e];
-                    dA[nt][e] = -W[nt][e] * dPQ[nt][e];
+                    if constexpr (GN) {
+                        dPQ[nt][e] = G[e] * inv[nt][e] + gd[nt] * Ag[nt][e];
+                        dA[nt][e] = gd[nt] * PQ[nt][e];
+                    } else {
+                        dPQ[nt][e] = G[e] * inv[nt][e];
+                        dA[nt][e] = -W[nt][e] * dPQ[nt][e];
+                    }
                 }
             }
         }
@@ -1390,7 +1486,7 @@ __global__ void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int ele
 // Sc2[t][tau] = sum_s W[t][s] P_K[tau][s], computed as output tiles over all
 // buckets from the waves' [.][s] LDS arrays; dK through each wave's buckets.
 // =====================================================================
-template <typename T, int SP, bool CAUSAL, int KB> struct BwdOutL {
+template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     static constexpr int NW_ = SP / WB;
     static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>(),
                          LDS_ = sw_ld<T, SP>();
@@ -1416,7 +1512,8 @@ template <typename T, int SP, bool CAUSAL, int KB> struct BwdOutL {
     static constexpr size_t oSuf = align16(oHash + HashOps<T, 4>::bytes);
     static constexpr size_t oPair = align16(oSuf + (CAUSAL ? SufOps<T>::bytes : 0));
     static constexpr size_t oShare = align16(oPair + PairOps<T>::bytes);
-    static constexpr size_t bytes = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
+    static constexpr size_t oTok = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
+    static constexpr size_t bytes = align16(oTok + (GN ? sizeof(float) * 2 * TT : 0));  // GN: rden, gden
 };
 
 template <typename T, int SP, bool CAUSAL>
@@ -1453,9 +1550,13 @@ __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts
     }
 }
 
-template <typename T, int SP, bool CAUSAL, int KB>
+// GN (global normalisation, causal only): W = P_Q rd and dA = gd P_Q per
+// token (rd = 1/max(den, eps), gd = dL/d den), so the reverse walk needs
+// neither the forward state nor G.
+template <typename T, int SP, bool CAUSAL, int KB, bool GN>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
-    using Ly = BwdOutL<T, SP, CAUSAL, KB>;
+    static_assert(CAUSAL || !GN, "global normalisation is causal only");
+    using Ly = BwdOutL<T, SP, CAUSAL, KB, GN>;
     using NL = NatL<T, true>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
                   LDS_ = Ly::LDS_;
@@ -1485,6 +1586,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     T *dvp = (T *)a.dv + stream_off(a.sg, n, a.B, a.H);
     float *xpart = sliced<T, KB>() ? a.dkpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
     float *vpart = sliced<T, KB>() ? a.dvpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
+    float *sTok = (float *)(smem + Ly::oTok);
+    const float *rdp = GN ? a.rden + (int64_t)n * a.T : nullptr, *gdp = GN ? a.gden + (int64_t)n * a.T : nullptr;
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
@@ -1511,15 +1614,16 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     f32x4 Ut[4];  // U^T[d = 16md + 4g + e][s = sw + i]
     double Be[4][4], Ae[4];
     float al[4];
+    constexpr bool FSTATE = CAUSAL && !GN;
     for (int md = 0; md < 4; ++md)
         for (int e = 0; e < 4; ++e) {
             const int64_t r = sidx(sg + i, 16 * md + 4 * g + e);
             Ut[md][e] = rs[r];
-            Be[md][e] = CAUSAL ? fs[r] : 0.0;
+            Be[md][e] = FSTATE ? fs[r] : 0.0;
         }
     for (int e = 0; e < 4; ++e) {
         al[e] = rs[sidx(sg + 4 * g + e, D)];
-        Ae[e] = CAUSAL ? fs[sidx(sg + 4 * g + e, D)] : 0.0;
+        Ae[e] = FSTATE ? fs[sidx(sg + 4 * g + e, D)] : 0.0;
     }
     if constexpr (!CAUSAL) store_ut<T, SP>(sUT, sw, Ut, cst, po);  // constant totals
     float tsum = 0.f;
@@ -1527,6 +1631,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     wait_state_loads();
     Prefetch<T, NTH> pq_, pk_, pvn_;  // pvn_: non-causal V (natural only)
     PrefetchT<T, NTH, 2> pg_, pv_;   // causal dO and V (natural and transposed)
+    TokPre pt_;
     // The next tile's rows are committed to LDS right after a tile's last
     // barrier and before its dK stores: that commit waits (vmcnt) on loads
     // issued a tile earlier, never on the stores just issued.
@@ -1540,6 +1645,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         } else {
             pvn_.template commit<NL>(sV, nullptr);
         }
+        if constexpr (GN) pt_.commit(sTok);
     };
     if (j0 < j1) {
         const int64_t tl = (j1 - 1) * TT;
@@ -1551,6 +1657,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         } else {
             pvn_.issue(vp, a.sv.t, tl, a.T);
         }
+        if constexpr (GN) pt_.issue(rdp, gdp, tl, a.T);
         commit();
     }
     for (int64_t jr = j1 - 1; jr >= j0; --jr) {
@@ -1569,6 +1676,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         } else {
             pvn_.issue(vp, a.sv.t, tn, a.T);
         }
+        if constexpr (GN) pt_.issue(rdp, gdp, tn, a.T);
         __syncthreads();
         for (int q = w; q < NTASK; q += NW_) {
             if (q < 4)
@@ -1588,8 +1696,21 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         f32x4 dPK[2];
         if constexpr (CAUSAL) {
             f32x4 Wi[2];  // W / (A + eps), the factor of dA
+            f32x4 dA[2];
             Frag<T> Wf;
-            {
+            if constexpr (GN) {
+                f32x4 PQ[2], W[2];
+                probs_st<KB>(sSpQ, sSmQ, sg, a.S, t0, a.T, PQ);
+                for (int nt = 0; nt < 2; ++nt) {
+                    const float rd = sTok[16 * nt + i], gd = sTok[TT + 16 * nt + i];
+                    for (int e = 0; e < 4; ++e) {
+                        W[nt][e] = PQ[nt][e] * rd;
+                        dA[nt][e] = gd * PQ[nt][e];
+                    }
+                }
+                store_ts<T, SP>(sWts, sw, W);
+                Wf = token_operand<T>(W, cst, po);
+            } else {
                 f32x4 PQ[2], Acum[2], W[2], tot, dB[4];
                 probs_st<KB>(sSpQ, sSmQ, sg, a.S, t0, a.T, PQ);
                 // forward state at the tile start: end state minus this tile's sums
@@ -1614,8 +1735,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             store_ut<T, SP>(sUT, sw, Ut, cst, po);
             __syncthreads();  // all waves' P_K, W, U rows in LDS
             // ---- dA = -W G/(A+eps), G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
-            f32x4 dA[2];
-            {
+            if constexpr (!GN) {
                 Frag<T> Bf[2];
                 for (int kk = 0; kk < 2; ++kk) {
                     f32x4 b0, b1;
@@ -1698,6 +1818,55 @@ __global__ void k_slice_sum(const float *part, int nslice, int64_t N, int64_t Tn
     f32x4 acc = *reinterpret_cast<const f32x4 *>(part + row);
     for (int z = 1; z < nslice; ++z) acc += *reinterpret_cast<const f32x4 *>(part + z * zs + row);
     store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc);
+}
+
+// Global normalisation, sliced instantiations: out = (sum of the slices'
+// numerator partials) / max(den, eps), den = sum of the slices' den partials
+// [nslice][N][T] (slice order), also written to den [N][T].
+template <typename T>
+__global__ void k_slice_sum_gn(const float *part, const float *denpart, int nslice, int64_t N, int64_t Tn, int B,
+                               int H, Strides so, T *out, float *den, float eps) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over N * T * D/4
+    const int64_t per = Tn * (D / 4);
+    if (idx >= N * per) return;
+    const int64_t n = idx / per, r = idx % per, t = r / (D / 4);
+    const int d0 = 4 * (int)(r % (D / 4));
+    const int64_t row = (n * Tn + t) * D + d0, zs = N * Tn * D, nt = n * Tn + t;
+    f32x4 acc = *reinterpret_cast<const f32x4 *>(part + row);
+    float dn = denpart[nt];
+    for (int z = 1; z < nslice; ++z) {
+        acc += *reinterpret_cast<const f32x4 *>(part + z * zs + row);
+        dn += denpart[z * N * Tn + nt];
+    }
+    const float rc = 1.0f / fmaxf(dn, eps);
+    store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc * rc);
+    if (d0 == 0) den[nt] = dn;
+}
+
+// Global normalisation, backward prologue: per token of every stream,
+// rden = 1/max(den, eps) and gden = dL/d den = dden - [den >= eps] (dO . O) rden
+// (out = num / max(den, eps)).  16 threads per token, 4 d each.
+template <typename T>
+__global__ void k_gn_prep(const T *out, Strides so, const T *dout, Strides sdo, const float *den, const float *dden,
+                          int64_t N, int64_t Tn, int B, int H, float eps, float *rden, float *gden) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over N * T * 16
+    const int64_t nt = idx >> 4;
+    const int d0 = 4 * (int)(idx & 15);
+    const bool ok = nt < N * Tn;
+    float dot = 0.f;
+    if (ok) {
+        const int n = (int)(nt / Tn);
+        const int64_t t = nt % Tn;
+        const f32x4 o = load4<T>(out + stream_off(so, n, B, H) + t * so.t + d0);
+        const f32x4 gr = load4<T>(dout + stream_off(sdo, n, B, H) + t * sdo.t + d0);
+        dot = o[0] * gr[0] + o[1] * gr[1] + o[2] * gr[2] + o[3] * gr[3];
+    }
+    dot = row_sum(dot);  // the token's 16 lanes are one DPP row
+    if (ok && d0 == 0) {
+        const float dn = den[nt], r = 1.0f / fmaxf(dn, eps);
+        rden[nt] = r;
+        gden[nt] = (dden ? dden[nt] : 0.f) - (dn >= eps ? dot * r : 0.f);
+    }
 }
 
 // grad_inv_temp = sum of all partials, in a fixed order

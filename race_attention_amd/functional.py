@@ -8,6 +8,12 @@ reference's M-fold expand), hyperplanes [L,K,D] shared or [M,L,K,D]
 per-estimator, output [M,B,T,H,D].  Forward and backward run as HIP kernels on
 the current stream; bucket probabilities are recomputed in the backward.
 
+``race_attention_global(Q, K, V, planes, beta, ...)`` is the globally
+normalised causal operator ("F2") behind CausalRACEAttention
+(misc/elsaa_causal_complete.py:438-586): it returns out = num / max(den, 1e-6)
+and den [M,B,H,T] (fp32), both differentiable (the module's d_token is built
+from den).
+
 ``RACEPrefixMeanFlatFn`` is the autograd Function of misc/race.py:9-24 with the
 flat prefix mean computed by the HIP kernels instead of the CPU extension.
 """
@@ -168,6 +174,111 @@ class RACEFunction(torch.autograd.Function):
 def race_attention(Qhf, Khf, Vhf, planes, *, L, K, causal, inv_temp, eps=1e-6):
     """Differentiable RACE operator on [M,B,T,H,D] tensors (see module doc)."""
     return RACEFunction.apply(Qhf, Khf, Vhf, planes, inv_temp, L, K, causal, eps)
+
+
+# ------------------------------------------------- global normalisation (F2)
+def _den_check(den, M, B, H, T, name):
+    if den.shape != (M, B, H, T) or den.dtype != torch.float32:
+        raise ValueError(f"{name} must be float32 [M,B,H,T] = {(M, B, H, T)}; got {den.dtype} {tuple(den.shape)}")
+    return den.contiguous()
+
+
+def race_global_fwd_raw(q, k, v, planes, *, L, K, beta, floor=1e-6, seg_tiles=0):
+    """F2 forward: returns (out [M,B,T,H,D], den [M,B,H,T] fp32, state)."""
+    _require_gpu(q, k, v, planes)
+    _check_inputs(q, k, v, planes, L, K)
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    planes = planes.to(device=q.device, dtype=torch.float32).contiguous()
+    lib = _lib.load()
+    d = make_desc(q, k, v, planes, L=L, K=K, causal=True, eps=floor, inv_temp=beta, seg_tiles=seg_tiles)
+    M, B, T, H, _ = q.shape
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    den = torch.empty((M, B, H, T), dtype=torch.float32, device=q.device)
+    d.o_stride = _strides4(out)
+    sb = lib.race_state_bytes(ctypes.byref(d))
+    if sb == 0:
+        _lib.check(-1, "race_state_bytes")
+    wb = lib.race_fwd_global_workspace_bytes(ctypes.byref(d))
+    state = torch.empty(sb, dtype=torch.uint8, device=q.device)
+    ws = torch.empty(max(wb, 16), dtype=torch.uint8, device=q.device)
+    rc = lib.race_fwd_global(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(planes), _ptr(out), _ptr(den),
+                             _ptr(state), _ptr(ws), ctypes.c_size_t(ws.numel()), _stream())
+    _lib.check(rc, "race_fwd_global")
+    return out, den, state
+
+
+def race_global_bwd_raw(q, k, v, planes, out, den, dout, dden, state, *, L, K, beta, floor=1e-6, seg_tiles=0,
+                        want_beta_grad=True):
+    """F2 backward: returns (dq, dk, dv, grad_beta (0-dim fp32 tensor or None)).
+    dden (gradient of den, [M,B,H,T]) may be None."""
+    _require_gpu(q, k, v, planes, out, den, dout, state)
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    out = _aligned(out)
+    dout = _aligned(dout.to(q.dtype))
+    planes = planes.to(device=q.device, dtype=torch.float32).contiguous()
+    M, B, T, H, _ = q.shape
+    den = _den_check(den, M, B, H, T, "den")
+    if dden is not None:
+        dden = _den_check(dden.to(torch.float32), M, B, H, T, "dden")
+    lib = _lib.load()
+    d = make_desc(q, k, v, planes, L=L, K=K, causal=True, eps=floor, inv_temp=beta, seg_tiles=seg_tiles)
+    d.o_stride = _strides4(out)
+    d.do_stride = _strides4(dout)
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty_like(dq)
+    dv = torch.empty_like(dq)
+    d.g_stride = _strides4(dq)
+    if state.numel() != lib.race_state_bytes(ctypes.byref(d)):
+        raise ValueError("state buffer does not match this descriptor")
+    wb = lib.race_bwd_global_workspace_bytes(ctypes.byref(d))
+    ws = torch.empty(max(wb, 16), dtype=torch.uint8, device=q.device)
+    gb = torch.empty((), dtype=torch.float32, device=q.device) if want_beta_grad else None
+    rc = lib.race_bwd_global(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(planes), _ptr(out), _ptr(den),
+                             _ptr(dout), _ptr(dden) if dden is not None else None, _ptr(state),
+                             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(gb) if gb is not None else None,
+                             _ptr(ws), ctypes.c_size_t(ws.numel()), _stream())
+    _lib.check(rc, "race_bwd_global")
+    return dq, dk, dv, gb
+
+
+class RACEGlobalFunction(torch.autograd.Function):
+    """Autograd Function of the globally normalised causal operator (F2).
+
+    forward(Q, K, V, planes, beta, L, K, floor) -> (out [M,B,T,H,D], den
+    [M,B,H,T] fp32).  beta is a python float or a 0-dim tensor (then it
+    receives a gradient); planes are buffers (no gradient), as in the
+    reference (misc/elsaa_causal_complete.py:473-474).  Replaces
+    _RaceChunkwiseTritonFn (misc/elsaa_causal_complete.py:384-436) together
+    with the probabilities, chunk states and division around it."""
+
+    @staticmethod
+    def forward(ctx, Q, Kx, V, planes, beta, L, K, floor):
+        b = float(beta)
+        out, den, state = race_global_fwd_raw(Q, Kx, V, planes, L=L, K=K, beta=b, floor=floor)
+        ctx.save_for_backward(Q, Kx, V, planes, out, den, state)
+        ctx.cfg = (L, K, floor, b)
+        ctx.beta_is_tensor = torch.is_tensor(beta)
+        ctx.set_materialize_grads(False)  # an unused den arrives as None, not zeros
+        return out, den
+
+    @staticmethod
+    def backward(ctx, dout, dden):
+        Q, Kx, V, planes, out, den, state = ctx.saved_tensors
+        L, K, floor, b = ctx.cfg
+        want = ctx.beta_is_tensor and ctx.needs_input_grad[4]
+        if dout is None:
+            dout = torch.zeros_like(out)
+        dq, dk, dv, gb = race_global_bwd_raw(Q, Kx, V, planes, out, den, dout, dden, state, L=L, K=K, beta=b,
+                                             floor=floor, want_beta_grad=want)
+        return (dq if ctx.needs_input_grad[0] else None,
+                dk if ctx.needs_input_grad[1] else None,
+                dv if ctx.needs_input_grad[2] else None,
+                None, gb if want else None, None, None, None)
+
+
+def race_attention_global(Qhf, Khf, Vhf, planes, *, L, K, beta, floor=1e-6):
+    """Differentiable F2 operator on [M,B,T,H,D] tensors -> (out, den [M,B,H,T])."""
+    return RACEGlobalFunction.apply(Qhf, Khf, Vhf, planes, beta, L, K, floor)
 
 
 # ------------------------------------------------------------- prefix mean

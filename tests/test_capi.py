@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.race_abi_version() == 1
+    assert lib.race_abi_version() == 2
 
 
 def test_desc_layout_matches_header():
@@ -135,3 +135,51 @@ def test_prefix_mean_argument_checks():
     p = ctypes.c_void_p(256)
     rc = lib.race_prefix_mean_fwd(p, p, p, 4, 100, 1024, 1e-6, p, 1 << 30, None)
     assert rc == -2 and "D=1024" in _lib.last_error()
+
+
+# ------------------------------------------------- global normalisation (F2)
+def test_global_workspace_sizes():
+    """F2 adds per-token fp32 buffers: den partials per slice (sliced
+    instantiations, forward) and rden/gden (backward)."""
+    lib = _lib.load()
+    d = _desc()
+    N, T = 8, 1 << 20
+    tok = N * T * 4
+    assert lib.race_fwd_global_workspace_bytes(ctypes.byref(d)) == lib.race_fwd_workspace_bytes(ctypes.byref(d))
+    assert lib.race_bwd_global_workspace_bytes(ctypes.byref(d)) == lib.race_bwd_workspace_bytes(ctypes.byref(d)) + 2 * tok
+    d = _desc(dtype=_lib.RACE_DTYPE_F32, T=4096)      # 4 slices of 32 buckets
+    f1 = lib.race_fwd_workspace_bytes(ctypes.byref(d))
+    assert lib.race_fwd_global_workspace_bytes(ctypes.byref(d)) == f1 + 4 * N * 4096 * 4
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("causal", 0, -2, "causal operator only"),
+    ("eps", 0.0, -1, "must be > 0"),
+    ("K", 9, -2, "hash bits"),
+])
+def test_global_invalid_descriptors_rejected(field, value, code, msg):
+    lib = _lib.load()
+    d = _desc(**{field: value})
+    rc = lib.race_fwd_global(ctypes.byref(d), None, None, None, None, None, None, None, None, 0, None)
+    assert rc == code and msg in _lib.last_error()
+    rc = lib.race_bwd_global(ctypes.byref(d), *([None] * 14), 0, None)
+    assert rc == code and msg in _lib.last_error()
+
+
+def test_global_null_den_and_workspace_rejected():
+    lib = _lib.load()
+    d = _desc(T=64)
+    p = ctypes.c_void_p(256)
+    rc = lib.race_fwd_global(ctypes.byref(d), p, p, p, p, p, None, p, p, 1 << 30, None)
+    assert rc == -1 and "den is NULL" in _lib.last_error()
+    rc = lib.race_fwd_global(ctypes.byref(d), p, p, p, p, p, ctypes.c_void_p(258), p, p, 1 << 30, None)
+    assert rc == -1 and "den is not 4-byte aligned" in _lib.last_error()
+    rc = lib.race_fwd_global(ctypes.byref(d), p, p, p, p, p, p, p, p, 16, None)
+    assert rc == -3 and "workspace" in _lib.last_error()
+    # dden is optional, but when given it is checked like den
+    rc = lib.race_bwd_global(ctypes.byref(d), p, p, p, p, p, p, p, ctypes.c_void_p(6), p, p, p, p, None, p,
+                             1 << 30, None)
+    assert rc == -1 and "dden is not 4-byte aligned" in _lib.last_error()
+    need = lib.race_bwd_global_workspace_bytes(ctypes.byref(d))
+    rc = lib.race_bwd_global(ctypes.byref(d), p, p, p, p, p, p, p, None, p, p, p, p, None, p, need - 1, None)
+    assert rc == -3 and "workspace" in _lib.last_error()

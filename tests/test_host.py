@@ -75,3 +75,21 @@ def test_desc_from_expanded_inputs():
     with pytest.raises(ValueError):
         make_desc(q, q, q, torch.randn(3, 8, 4, 64), L=8, K=4, causal=False, eps=1e-6, inv_temp=1.0)
     assert np.isclose(d.inv_temp, 0.125)
+
+
+def test_global_module_matches_reference_construction():
+    """CausalRACEAttention (misc/elsaa_causal_complete.py:438-481): buffer
+    names and shapes, non-persistent buffers, log_beta parameter, clamp."""
+    from race_attention_amd.causal import CausalRACEAttention
+    m = CausalRACEAttention(256, 4, 0.1, num_bits=3, num_tables=5, beta_init=2.0)
+    assert (m.h, m.dk, m.num_bits, m.num_tables, m.R, m.C, m.chunk_group_size) == (4, 64, 3, 5, 8, 256, 64)
+    assert m.planes.shape == (5, 3, 64)
+    assert torch.equal(m.corners, torch.tensor(list(itertools.product([-1.0, 1.0], repeat=3))))
+    assert "planes" not in m.state_dict() and "corners" not in m.state_dict()
+    assert abs(float(m.log_beta) - np.log(2.0)) < 1e-7
+    with torch.no_grad():
+        m.log_beta.fill_(10.0)
+    assert float(m.beta()) == 20.0
+    assert m.last_den is None
+    with pytest.raises(RuntimeError, match="ROCm GPUs only"):
+        m(torch.randn(1, 8, 256))
