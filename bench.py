@@ -17,13 +17,19 @@ path (aten + kernels/cpu/race_pref.cpp compiled from source) on a bounded
 sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--seq N] [--no-cpu-baseline] [--max-n]
-                    [--copy-calib MIB] [--workload c4|c5]
+                    [--copy-calib MIB] [--workload c4|c5] [--mode f1|global]
 
 --workload c5 times the attention core of BASELINE configs[4] instead (the
 GPT-style decoder's layer: causal, K=8 so 256 buckets per table, L=4, M=2
 estimators with independent hyperplanes over Q/K/V expanded with stride 0,
 B=8, 12 heads, N=8192, d=64, bf16): 1024 buckets run as 8 bucket slices.
 The default (c4) line is the headline metric.
+
+--mode global times the globally normalised causal mode (CausalRACEAttention,
+misc/elsaa_causal_complete.py:438-586) on the same workload with beta = 1:
+race_fwd_global + race_bwd_global (the backward's first phase also runs the
+per-token prologue kernel).  Its CPU baseline is the fp64 C restatement under
+oracle/ (the reference's F2 CPU path is aten einsums), on a bounded sample.
 
 --copy-calib MIB ends the run with one device-to-device copy of MIB MiB, the
 known-size kernel against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters
@@ -64,6 +70,8 @@ def parse():
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="finish with a device-to-device copy of MIB MiB (PMC calibration)")
     ap.add_argument("--workload", choices=("c4", "c5"), default="c4")
+    ap.add_argument("--mode", choices=("f1", "global"), default="f1",
+                    help="f1: per-bucket normalisation (headline); global: one normaliser per token")
     return ap.parse_args()
 
 
@@ -134,10 +142,64 @@ class Step:
         self.d.phases = 0
 
 
-def algorithmic_bytes(name, tok_heads, D, esize):
-    """Compulsory HBM bytes of each kernel: token tensors it must read/write."""
+class GlobalStep(Step):
+    """One race_fwd_global + race_bwd_global (beta = 1, no upstream den gradient)."""
+
+    def __init__(self, q, k, v, do, planes, L, K):
+        import torch
+        super().__init__(q, k, v, do, planes, L, K)
+        self.d.inv_temp = 1.0
+        M, B, T, H, _ = q.shape
+        self.den = torch.empty((M, B, H, T), dtype=torch.float32, device=q.device)
+        ref = ctypes.byref(self.d)
+        fw, bw = self.lib.race_fwd_global_workspace_bytes(ref), self.lib.race_bwd_global_workspace_bytes(ref)
+        self.ws = torch.empty(max(fw, bw), dtype=torch.uint8, device=q.device)
+        P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        self.fargs = (P(q), P(k), P(v), P(self.planes), P(self.out), P(self.den), P(self.state), P(self.ws),
+                      ctypes.c_size_t(self.ws.numel()))
+        self.bargs = (P(q), P(k), P(v), P(self.planes), P(self.out), P(self.den), P(do), None, P(self.state),
+                      P(self.dq), P(self.dk), P(self.dv), P(self.git), P(self.ws), ctypes.c_size_t(self.ws.numel()))
+
+    def run(self, phases=0, which="both"):
+        import torch
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        self.d.phases = phases
+        if which in ("both", "fwd"):
+            self.check(self.lib.race_fwd_global(ctypes.byref(self.d), *self.fargs, st), "race_fwd_global")
+        if which in ("both", "bwd"):
+            self.check(self.lib.race_bwd_global(ctypes.byref(self.d), *self.bargs, st), "race_bwd_global")
+        self.d.phases = 0
+
+
+def cpu_baseline_global(sample_T, H, D=64, L=8, K=4, reps=3):
+    """The fp64 C restatement (oracle/race_oracle.c) of the globally normalised
+    mode, fwd+bwd, on one batch row of H heads x sample_T tokens (OpenMP over
+    the H streams); median of reps runs, as tokens/s."""
+    import numpy as np
+    from oracle import race_oracle as ro
+    rng = np.random.default_rng(0)
+    x = [rng.standard_normal((1, 1, sample_T, H, D)) for _ in range(4)]
+    x[:3] = [a / np.linalg.norm(a, axis=-1, keepdims=True) for a in x[:3]]
+    pl = rng.standard_normal((1, L, K, D))
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        ro.race_global_forward(x[0], x[1], x[2], pl, beta=1.0)
+        ro.race_global_backward(x[0], x[1], x[2], x[3], pl, beta=1.0)
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    return {"value": round(sample_T / t, 1), "unit": "tokens/s", "cores": min(H, os.cpu_count() or 1), "kind": "port",
+            "sample": f"1 batch row x {H} heads x {sample_T} tokens of the same workload, fwd+bwd in the fp64 C "
+                      f"restatement (oracle/race_oracle.c, OpenMP over the {H} head streams), median of {reps} runs; "
+                      f"{t:.2f} s per run"}
+
+
+def algorithmic_bytes(name, tok_heads, D, esize, mode="f1"):
+    """Compulsory HBM bytes of each kernel: token tensors it must read/write
+    (global mode: the backward's first phase also reads O for dL/d den)."""
     unit = tok_heads * D * esize
-    return {"fwd_reduce": 2, "fwd_out": 4, "bwd_reduce": 5, "bwd_out": 6}.get(name, 0) * unit
+    units = {"fwd_reduce": 2, "fwd_out": 4, "bwd_reduce": 5 if mode == "f1" else 6, "bwd_out": 6}
+    return units.get(name, 0) * unit
 
 
 def cpu_baseline(sample_T, H_full, D=64, L=8, K=4, reps=16):
@@ -245,9 +307,11 @@ def main():
     else:
         M, B, T, H, D, L, K = 1, 1, args.seq, args.heads, 64, 8, 4
         wl = "C4 causal RACE layer core fwd+bwd"
+    if args.mode == "global":
+        wl += ", global normalisation (F2, beta=1)"
     print(f"bench: generating inputs M={M} B={B} T={T} H={H} D={D} L={L} K={K}", file=sys.stderr, flush=True)
     q, k, v, do, planes = make_inputs(B, T, H, D, L, K, dev, M=M)
-    step = Step(q, k, v, do, planes, L, K)
+    step = (GlobalStep if args.mode == "global" else Step)(q, k, v, do, planes, L, K)
     for _ in range(args.warmup):
         step.run()
     torch.cuda.synchronize()
@@ -272,15 +336,15 @@ def main():
     tok_heads = M * B * T * H  # token-streams: each (m, b, h) stream reads its own Q, K, V rows
     kernels = {}
     for name, t_ms in per.items():
-        ab = algorithmic_bytes(name, tok_heads, D, 2)
+        ab = algorithmic_bytes(name, tok_heads, D, 2, args.mode)
         kernels[name] = {"ms": round(t_ms, 4),
                          "algorithmic_GBs": round(ab / (t_ms * 1e-3) / 1e9, 1) if ab else None}
     dom = max(per, key=per.get)
-    ab = algorithmic_bytes(dom, tok_heads, D, 2)
+    ab = algorithmic_bytes(dom, tok_heads, D, 2, args.mode)
     achieved = ab / (per[dom] * 1e-3) / 1e9
     traffic = None
     tfile = os.path.join(ROOT, "profiles", f"traffic_{dom}_{args.workload}.txt")
-    if os.path.exists(tfile) and (args.workload != "c4" or T == 1 << 20):
+    if os.path.exists(tfile) and args.mode == "f1" and (args.workload != "c4" or T == 1 << 20):
         for ln in open(tfile):
             if ln.startswith("hbm_bytes_per_launch"):
                 traffic = float(ln.split("=")[1])
@@ -291,7 +355,8 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (unit-L2 N(0,1) Q/K/V, N(0,1) dO and hyperplanes, seeds 0/1234)",
         "config": {"workload": f"{wl}: B={B} H={H} N={T} d={D} K={K} L={L} M={M} bf16",
-                   "B": B, "H": H, "seq_len": T, "d": D, "K": K, "L": L, "M": M, "causal": True},
+                   "B": B, "H": H, "seq_len": T, "d": D, "K": K, "L": L, "M": M, "causal": True,
+                   "normalisation": "per-bucket (F1)" if args.mode == "f1" else "global (F2)"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "layer_roofline": {"algorithmic_bytes_per_step": all_bytes,
@@ -313,7 +378,9 @@ def main():
         res["max_seq_len_fwd_bwd"] = max_seq_bisect(H, D, L, K, dev)
     if not args.no_cpu_baseline:
         print("bench: CPU baseline", file=sys.stderr, flush=True)
-        if args.workload == "c4":
+        if args.mode == "global":
+            res["cpu_baseline"] = cpu_baseline_global(min(T, 8192), H * M, D=D, L=L, K=K)
+        elif args.workload == "c4":
             res["cpu_baseline"] = cpu_baseline(args.cpu_sample, H * M, D=D, L=L, K=K)
         else:  # 1024 buckets: the reference's flat layout holds 256 KB per token
             res["cpu_baseline"] = cpu_baseline(min(args.cpu_sample, 2048), H * M, D=D, L=L, K=K, reps=8)

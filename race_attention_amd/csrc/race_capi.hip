@@ -241,17 +241,12 @@ template <typename T, int SP, int KB> int gn_fwd_impl(const race_desc *d, const 
     return launched("race_fwd_global");
 }
 
-// The prologue kernel turns (out, den, dout, dden) into per-token rden, gden;
-// the backward kernels then run in GN mode.
+// The GN backward: k_bwd_reduce also forms the per-token terms
+// (1/max(den, eps) and dL/d den, from out, dout, den, dden) that k_bwd_out reads.
 template <typename T, int SP, int KB>
-int gn_bwd_impl(const race_desc *d, const Plan &p, Args a, const void *out, const float *den, const float *dden,
-                float *grad_beta, hipStream_t s) {
+int gn_bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_beta, hipStream_t s) {
     const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
-        const int64_t nthr = p.N * d->T * 16;
-        k_gn_prep<T><<<(unsigned)((nthr + 255) / 256), 256, 0, s>>>(
-            (const T *)out, strides_of(d->o_stride), (const T *)a.dout, a.sdo, den, dden, p.N, d->T, (int)d->B,
-            (int)d->H, d->eps, const_cast<float *>(a.rden), const_cast<float *>(a.gden));
         k_bwd_reduce<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) slice_sum<T>(p, d, a.dqpart, d->g_stride, a.dq, s);
     }
@@ -302,12 +297,9 @@ template <typename T> int gn_fwd_dispatch(const race_desc *d, const Plan &p, con
     return fail(RACE_E_UNSUPPORTED, "bucket count / hash bits combination not compiled");
 }
 
-template <typename T>
-int gn_bwd_dispatch(const race_desc *d, const Plan &p, const Args &a, const void *out, const float *den,
-                    const float *dden, float *gb, hipStream_t s) {
+template <typename T> int gn_bwd_dispatch(const race_desc *d, const Plan &p, const Args &a, float *gb, hipStream_t s) {
 #define X(TT_, SP_, KB_)                                                                                             \
-    if (std::is_same<T, TT_>::value && p.SP == SP_ && d->K == KB_)                                                   \
-        return gn_bwd_impl<TT_, SP_, KB_>(d, p, a, out, den, dden, gb, s);
+    if (std::is_same<T, TT_>::value && p.SP == SP_ && d->K == KB_) return gn_bwd_impl<TT_, SP_, KB_>(d, p, a, gb, s);
     RACE_FOR_COMBOS(X)
 #undef X
     return fail(RACE_E_UNSUPPORTED, "bucket count / hash bits combination not compiled");
@@ -516,11 +508,14 @@ int race_bwd_global(const race_desc *d, const void *q, const void *k, const void
         a.dkpart = part + pe;
         a.dvpart = part + 2 * pe;
     }
-    a.rden = (const float *)((char *)ws + p.bws);
-    a.gden = (const float *)((char *)ws + p.bws + p.tok_bytes);
+    a.out = const_cast<void *>(out);  // read only (the GN per-token terms)
+    a.den = const_cast<float *>(den);
+    a.dden = dden;
+    a.rden = (float *)((char *)ws + p.bws);
+    a.gden = (float *)((char *)ws + p.bws + p.tok_bytes);
     hipStream_t s = (hipStream_t)stream;
-    if (d->dtype == RACE_DTYPE_BF16) return gn_bwd_dispatch<bf16>(d, p, a, out, den, dden, grad_beta, s);
-    return gn_bwd_dispatch<float>(d, p, a, out, den, dden, grad_beta, s);
+    if (d->dtype == RACE_DTYPE_BF16) return gn_bwd_dispatch<bf16>(d, p, a, grad_beta, s);
+    return gn_bwd_dispatch<float>(d, p, a, grad_beta, s);
 }
 
 size_t race_prefix_mean_workspace_bytes(int64_t NS, int64_t T, int64_t D) {

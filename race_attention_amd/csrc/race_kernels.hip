@@ -66,9 +66,12 @@ struct Args {
     float *opart, *dqpart, *dkpart, *dvpart;
     // global normalisation (GN instantiations; eps is the floor of den):
     // den [N][T] output (sliced: per-slice partials denpart [nslice][N][T]);
-    // backward inputs rden = 1/max(den, eps) and gden = dL/d den, [N][T]
+    // backward: den and dden (dL/d den, nullable) in, and per-token
+    // rden = 1/max(den, eps), gden = dL/d den + d(out)/d den terms [N][T],
+    // written by k_bwd_reduce and read by k_bwd_out
     float *den, *denpart;
-    const float *rden, *gden;
+    const float *dden;
+    float *rden, *gden;
 };
 
 constexpr int SROW = D + 1;  // state row: D values of B (or U) then A (or alpha)
@@ -349,8 +352,9 @@ template <typename T, int NTH, int NPART> struct PrefetchT {
 };
 
 // Per-token fp32 pair (a[t], b[t]) of a 32-token tile (the GN backward's
-// 1/max(den, eps) and dL/d den), loaded by wave 0 with the token tiles and
-// committed to LDS as [2][TT] with them; zero past the sequence end.
+// den and dden, or rden and gden), loaded by wave 0 with the token tiles and
+// committed to LDS as [2][TT] with them; zero past the sequence end and for
+// a null b.
 struct TokPre {
     float v;
     __device__ __forceinline__ void issue(const float *__restrict__ a, const float *__restrict__ b, int64_t t0,
@@ -358,7 +362,8 @@ struct TokPre {
         v = 0.f;
         if (threadIdx.x < 64) {
             const int t = threadIdx.x & 31;
-            if (t < tile_rows(t0, Tn)) v = (threadIdx.x < 32 ? a : b)[t0 + t];
+            const float *src = threadIdx.x < 32 ? a : b;  // b may be null: zeros
+            if (src && t < tile_rows(t0, Tn)) v = src[t0 + t];
         }
     }
     __device__ __forceinline__ void commit(float *dst) const {
@@ -1238,6 +1243,35 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 // k_bwd_reduce: forward walk.  dQ, and per-segment sums of
 // alpha = sum_t dA and U = sum_t W^T g.
 // =====================================================================
+// GN backward, per token of the tile: with dc = max(den, eps) and the
+// forward's out = num / dc,
+//   rd = 1 / dc,  gd = dL/d den = dden - [den >= eps] (dO . O) rd.
+// dO and O are natural tiles of one layout (the dot product reads both at the
+// same physical offsets); den, dden come from sIn [2][TT].  Results go to
+// sOut [2][TT] and, when rdw is set, to rdw / gdw [t] for k_bwd_out.  A wave
+// takes 4 tokens per pass, 16 lanes x 4 d each.
+template <typename T, class NL, int NW_>
+__device__ void gn_token_terms(const T *sG, const T *sO, const float *sIn, float *sOut, float eps, float *rdw,
+                               float *gdw, int64_t t0, int64_t Tn) {
+    const int w = wave_id(), r = lane_id() >> 4, c = lane_id() & 15;
+    for (int tb = 4 * w; tb < TT; tb += 4 * NW_) {
+        const int t = tb + r;
+        const int o = NL::P ? sw_off<T, D>(t, 4 * c) : t * NL::LD + 4 * c;
+        const f32x4 g = load4<T>(sG + o), y = load4<T>(sO + o);
+        const float dot = row_sum(g[0] * y[0] + g[1] * y[1] + g[2] * y[2] + g[3] * y[3]);
+        const float dn = sIn[t], rd = 1.0f / fmaxf(dn, eps);
+        const float gd = sIn[TT + t] - (dn >= eps ? dot * rd : 0.f);
+        if (c == 0) {
+            sOut[t] = rd;
+            sOut[TT + t] = gd;
+            if (rdw && t0 + t < Tn) {
+                rdw[t0 + t] = rd;
+                gdw[t0 + t] = gd;
+            }
+        }
+    }
+}
+
 template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr int NW_ = SP / WB;
     static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>();
@@ -1259,11 +1293,15 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr size_t oPair = align16(oHash + HashOps<T, 4>::bytes);
     static constexpr size_t oShare = align16(oPair + PairOps<T>::bytes);
     static constexpr size_t oTok = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
-    static constexpr size_t bytes = align16(oTok + (GN ? sizeof(float) * 2 * TT : 0));  // GN: rden, gden
+    // GN: staged (den, dden) [2][TT], computed (rd, gd) [2][TT], the O tile
+    static constexpr size_t oTokIn = align16(oTok + (GN ? sizeof(float) * 2 * TT : 0));
+    static constexpr size_t oO = align16(oTokIn + (GN ? sizeof(float) * 2 * TT : 0));
+    static constexpr size_t bytes = align16(oO + (GN ? sizeof(T) * TT * LDN : 0));
 };
 
 // GN (global normalisation, causal only): with rd = 1/max(den, eps) and
-// gd = dL/d den per token, W = P_Q rd, dP_Q = G rd + gd A_s(t), dA = gd P_Q.
+// gd = dL/d den per token (gn_token_terms, from the O and dO tiles),
+// W = P_Q rd, dP_Q = G rd + gd A_s(t), dA = gd P_Q.
 template <typename T, int SP, bool CAUSAL, int KB, bool GN>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
@@ -1292,8 +1330,14 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     const T *gp = (const T *)a.dout + stream_off(a.sdo, n, a.B, a.H);
     T *dqp = (T *)a.dq + stream_off(a.sg, n, a.B, a.H);
     float *xpart = sliced<T, KB>() ? a.dqpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
-    float *sTok = (float *)(smem + Ly::oTok);
-    const float *rdp = GN ? a.rden + (int64_t)n * a.T : nullptr, *gdp = GN ? a.gden + (int64_t)n * a.T : nullptr;
+    float *sTok = (float *)(smem + Ly::oTok), *sTokIn = (float *)(smem + Ly::oTokIn);
+    T *sO = (T *)(smem + Ly::oO);
+    const T *op = GN ? (const T *)a.out + stream_off(a.so, n, a.B, a.H) : nullptr;
+    const float *denp = GN ? a.den + (int64_t)n * a.T : nullptr;
+    const float *ddp = GN && a.dden ? a.dden + (int64_t)n * a.T : nullptr;
+    // one bucket slice writes the per-token terms for k_bwd_out
+    float *rdw = GN && z == 0 ? a.rden + (int64_t)n * a.T : nullptr;
+    float *gdw = GN && z == 0 ? a.gden + (int64_t)n * a.T : nullptr;
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
@@ -1325,7 +1369,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
 
     wait_state_loads();
     constexpr int NP = CAUSAL ? 2 : 1;  // transposed tiles: dO (and V)
-    Prefetch<T, NTH> pq_, pk_;
+    Prefetch<T, NTH> pq_, pk_, po_;  // po_: GN's O tile
     PrefetchT<T, NTH, NP> pg_, pv_;
     TokPre pt_;
     // The next tile's rows are committed to LDS right after a tile's last
@@ -1339,7 +1383,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             pk_.template commit<NL>(sK, nullptr);
             pv_.template commit<NL>(1, sV, sVt);
         }
-        if constexpr (GN) pt_.commit(sTok);
+        if constexpr (GN) {
+            po_.template commit<NL>(sO, nullptr);
+            pt_.commit(sTokIn);
+        }
     };
     if (j0 < j1) {
         pq_.issue(qp, a.sq.t, j0 * TT, a.T);
@@ -1348,7 +1395,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             pk_.issue(kp, a.sk.t, j0 * TT, a.T);
             pv_.issue(1, vp, a.sv.t, j0 * TT, a.T);
         }
-        if constexpr (GN) pt_.issue(rdp, gdp, j0 * TT, a.T);
+        if constexpr (GN) {
+            po_.issue(op, a.so.t, j0 * TT, a.T);
+            pt_.issue(denp, ddp, j0 * TT, a.T);
+        }
         commit();
     }
     for (int64_t jt = j0; jt < j1; ++jt) {
@@ -1364,8 +1414,12 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             pk_.issue(kp, a.sk.t, tn, a.T);
             pv_.issue(1, vp, a.sv.t, tn, a.T);
         }
-        if constexpr (GN) pt_.issue(rdp, gdp, tn, a.T);
+        if constexpr (GN) {
+            po_.issue(op, a.so.t, tn, a.T);
+            pt_.issue(denp, ddp, tn, a.T);
+        }
         __syncthreads();
+        if constexpr (GN) gn_token_terms<T, NL, NW_>(sG, sO, sTokIn, sTok, a.eps, rdw, gdw, t0, a.T);
         for (int q = w; q < NTASK; q += NW_) {
             if (q < 4)
                 project_tile<T, NL>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, sThQ);
@@ -1841,32 +1895,6 @@ __global__ void k_slice_sum_gn(const float *part, const float *denpart, int nsli
     const float rc = 1.0f / fmaxf(dn, eps);
     store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc * rc);
     if (d0 == 0) den[nt] = dn;
-}
-
-// Global normalisation, backward prologue: per token of every stream,
-// rden = 1/max(den, eps) and gden = dL/d den = dden - [den >= eps] (dO . O) rden
-// (out = num / max(den, eps)).  16 threads per token, 4 d each.
-template <typename T>
-__global__ void k_gn_prep(const T *out, Strides so, const T *dout, Strides sdo, const float *den, const float *dden,
-                          int64_t N, int64_t Tn, int B, int H, float eps, float *rden, float *gden) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over N * T * 16
-    const int64_t nt = idx >> 4;
-    const int d0 = 4 * (int)(idx & 15);
-    const bool ok = nt < N * Tn;
-    float dot = 0.f;
-    if (ok) {
-        const int n = (int)(nt / Tn);
-        const int64_t t = nt % Tn;
-        const f32x4 o = load4<T>(out + stream_off(so, n, B, H) + t * so.t + d0);
-        const f32x4 gr = load4<T>(dout + stream_off(sdo, n, B, H) + t * sdo.t + d0);
-        dot = o[0] * gr[0] + o[1] * gr[1] + o[2] * gr[2] + o[3] * gr[3];
-    }
-    dot = row_sum(dot);  // the token's 16 lanes are one DPP row
-    if (ok && d0 == 0) {
-        const float dn = den[nt], r = 1.0f / fmaxf(dn, eps);
-        rden[nt] = r;
-        gden[nt] = (dden ? dden[nt] : 0.f) - (dn >= eps ? dot * r : 0.f);
-    }
 }
 
 // grad_inv_temp = sum of all partials, in a fixed order
