@@ -91,6 +91,31 @@ int race_bwd(const race_desc *d, const void *q, const void *k, const void *v,
              size_t ws_bytes, void *stream);
 
 /* ---------------------------------------------------------------------
+ * Padded batches and the den output (non-causal F1): the forms of
+ * BatchedACE.forward(..., mask) (misc/classification.py:576-592) and of
+ * _ace_with_denom (misc/classification.py:641-659, misc/vit.py:1452-1510).
+ *   kmask: fp32 [B][T] per-token key weights, shared by heads and
+ *          estimators (nullable = 1): P_K'[t,s] = kmask[b][t] * P_K[t,s]
+ *          feeds A and B.  The reference's mask also multiplies V, P_Q and
+ *          the output; those are elementwise on the inputs and outputs and
+ *          stay with the caller.
+ *   den:   fp32 [M*B*H][T] (nullable), den_t = sum_s P_Q[t,s] A_s,
+ *          unclamped (the reference clamps it at eps).
+ *   dden:  its upstream gradient (nullable = 0).
+ * Non-causal only (d->causal = 1 with kmask, den or dden returns
+ * RACE_E_UNSUPPORTED); state and backward workspace as race_fwd/race_bwd.
+ * --------------------------------------------------------------------- */
+size_t race_fwd_ex_workspace_bytes(const race_desc *d);
+int race_fwd_ex(const race_desc *d, const void *q, const void *k, const void *v,
+                const float *planes, const float *kmask, void *out, float *den,
+                void *state, void *ws, size_t ws_bytes, void *stream);
+int race_bwd_ex(const race_desc *d, const void *q, const void *k, const void *v,
+                const float *planes, const float *kmask, const void *dout,
+                const float *dden, const void *state, void *dq, void *dk,
+                void *dv, float *grad_inv_temp, void *ws, size_t ws_bytes,
+                void *stream);
+
+/* ---------------------------------------------------------------------
  * Global normalisation ("F2", causal only): one normaliser per token
  * instead of one per bucket, the readout of CausalRACEAttention
  * (misc/elsaa_causal_complete.py:438-586) and of its Triton kernel

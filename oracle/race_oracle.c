@@ -19,6 +19,8 @@
  *   kernels/cpu/race_pref.cpp:104-220  prefix mean backward (two passes)
  *   misc/elsaa_causal_complete.py:438-586, misc/race_kernel.py:8-124
  *                            F2 causal readout num/max(den, 1e-6)
+ *   misc/classification.py:576-592, :641-659, misc/vit.py:1452-1510
+ *                            padding mask on P_K and the den output (F1)
  *
  * Layout used here: streams are independent; every per-stream tensor is
  * [T][D] row-major double.  planes are [NP][L][K][D]; stream n uses planes
@@ -552,6 +554,198 @@ int oracle_race_global_backward(const double *q, const double *k, const double *
         *grad_beta = tot;
     if (grad_beta_l1)
         *grad_beta_l1 = tabs;
+    free(part);
+    free(pabs);
+    return 0;
+}
+
+/* ------------------------------------------- key weights and den (F1 extras)
+ *
+ * The padded-batch forms of the non-causal operator
+ * (misc/classification.py:576-592, BatchedACE.forward with mask;
+ * :641-659 and misc/vit.py:1452-1510, _ace_with_denom):
+ *   P_K'[t,s] = w_t P_K[t,s]   (w: per-token key weight, the mask)
+ *   A, B from P_K' (V is masked by the caller), out as in F1,
+ *   den_t = sum_s P_Q[t,s] A_s(t)   (unclamped; the caller clamps).
+ * Causal and non-causal, like stream_forward.  w and den may be NULL. */
+static void stream_forward_ex(const double *q, const double *k, const double *v,
+                              const double *w, const double *pl, int64_t T, int64_t D,
+                              int L, int K, int causal, double eps, double inv_temp,
+                              double *o, double *den)
+{
+    const int R = 1 << K;
+    const int64_t S = (int64_t)L * R;
+    double *A = calloc((size_t)S, sizeof(double));
+    double *B = calloc((size_t)(S * D), sizeof(double));
+    double *th = malloc(sizeof(double) * (size_t)(L * K));
+    double *PK = malloc(sizeof(double) * (size_t)S);
+    double *PQ = malloc(sizeof(double) * (size_t)S);
+    for (int64_t pass = causal ? 1 : 0; pass < 2; ++pass) {
+        for (int64_t t = 0; t < T; ++t) {
+            if (pass == 0 || causal) {
+                soft_hash(k + t * D, pl, D, L, K, inv_temp, th, PK);
+                const double wt = w ? w[t] : 1.0;
+                for (int64_t s = 0; s < S; ++s) {
+                    A[s] += wt * PK[s];
+                    for (int64_t d = 0; d < D; ++d)
+                        B[s * D + d] += wt * PK[s] * v[t * D + d];
+                }
+            }
+            if (pass == 0)
+                continue;
+            soft_hash(q + t * D, pl, D, L, K, inv_temp, th, PQ);
+            double *ot = o + t * D, dn = 0.0;
+            for (int64_t d = 0; d < D; ++d)
+                ot[d] = 0.0;
+            for (int64_t s = 0; s < S; ++s) {
+                dn += PQ[s] * A[s];
+                const double ws = PQ[s] / (A[s] + eps);
+                for (int64_t d = 0; d < D; ++d)
+                    ot[d] += ws * B[s * D + d];
+            }
+            if (den)
+                den[t] = dn;
+        }
+    }
+    free(A); free(B); free(th); free(PK); free(PQ);
+}
+
+/* Backward of stream_forward_ex for upstream gradients g (out) and h (den,
+ * may be NULL): F1's formulas with P_K' = w P_K, plus
+ *   dP_Q[t,s] += h_t A_s(t),  dA[t,s] += h_t P_Q[t,s],
+ * and dP_K = w (alpha + v . U) through the weight. */
+static void stream_backward_ex(const double *q, const double *k, const double *v,
+                               const double *w, const double *g, const double *h,
+                               const double *pl, int64_t T, int64_t D, int L, int K,
+                               int causal, double eps, double inv_temp, double *dq,
+                               double *dk, double *dv, double *g_it, double *g_abs)
+{
+    const int R = 1 << K;
+    const int64_t S = (int64_t)L * R;
+    double *A = calloc((size_t)S, sizeof(double));
+    double *B = calloc((size_t)(S * D), sizeof(double));
+    double *dA = malloc(sizeof(double) * (size_t)(T * S));
+    double *W = malloc(sizeof(double) * (size_t)(T * S));
+    double *th = malloc(sizeof(double) * (size_t)(L * K));
+    double *PK = malloc(sizeof(double) * (size_t)S);
+    double *PQ = malloc(sizeof(double) * (size_t)S);
+    double *dP = malloc(sizeof(double) * (size_t)S);
+    double *alpha = calloc((size_t)S, sizeof(double));
+    double *U = calloc((size_t)(S * D), sizeof(double));
+
+    memset(dq, 0, sizeof(double) * (size_t)(T * D));
+    memset(dk, 0, sizeof(double) * (size_t)(T * D));
+    memset(dv, 0, sizeof(double) * (size_t)(T * D));
+    for (int64_t pass = causal ? 1 : 0; pass < 2; ++pass) {
+        for (int64_t t = 0; t < T; ++t) {
+            if (pass == 0 || causal) {
+                soft_hash(k + t * D, pl, D, L, K, inv_temp, th, PK);
+                const double wt = w ? w[t] : 1.0;
+                for (int64_t s = 0; s < S; ++s) {
+                    A[s] += wt * PK[s];
+                    for (int64_t d = 0; d < D; ++d)
+                        B[s * D + d] += wt * PK[s] * v[t * D + d];
+                }
+            }
+            if (pass == 0)
+                continue;
+            soft_hash(q + t * D, pl, D, L, K, inv_temp, th, PQ);
+            const double *gt = g + t * D;
+            const double ht = h ? h[t] : 0.0;
+            for (int64_t s = 0; s < S; ++s) {
+                const double inv = 1.0 / (A[s] + eps);
+                double G = 0.0;
+                for (int64_t d = 0; d < D; ++d)
+                    G += gt[d] * B[s * D + d];
+                dP[s] = G * inv + ht * A[s];
+                W[t * S + s] = PQ[s] * inv;
+                dA[t * S + s] = -PQ[s] * inv * G * inv + ht * PQ[s];
+            }
+            soft_hash_bwd(PQ, th, dP, pl, D, L, K, inv_temp, dq + t * D, g_it, g_abs);
+        }
+    }
+    if (!causal) {
+        for (int64_t t = 0; t < T; ++t) {
+            const double *gt = g + t * D;
+            for (int64_t s = 0; s < S; ++s) {
+                alpha[s] += dA[t * S + s];
+                for (int64_t d = 0; d < D; ++d)
+                    U[s * D + d] += W[t * S + s] * gt[d];
+            }
+        }
+    }
+    for (int64_t t = T - 1; t >= 0; --t) {
+        const double *gt = g + t * D;
+        const double *vt = v + t * D;
+        if (causal) {
+            for (int64_t s = 0; s < S; ++s) {
+                alpha[s] += dA[t * S + s];
+                for (int64_t d = 0; d < D; ++d)
+                    U[s * D + d] += W[t * S + s] * gt[d];
+            }
+        }
+        soft_hash(k + t * D, pl, D, L, K, inv_temp, th, PK);
+        const double wt = w ? w[t] : 1.0;
+        double *dvt = dv + t * D;
+        for (int64_t s = 0; s < S; ++s) {
+            double vu = 0.0;
+            for (int64_t d = 0; d < D; ++d) {
+                vu += vt[d] * U[s * D + d];
+                dvt[d] += wt * PK[s] * U[s * D + d];
+            }
+            dP[s] = wt * (alpha[s] + vu);
+        }
+        soft_hash_bwd(PK, th, dP, pl, D, L, K, inv_temp, dk + t * D, g_it, g_abs);
+    }
+    free(A); free(B); free(dA); free(W); free(th); free(PK); free(PQ);
+    free(dP); free(alpha); free(U);
+}
+
+int oracle_race_forward_ex(const double *q, const double *k, const double *v,
+                           const double *kw, const double *planes, const int64_t *plane_of,
+                           int64_t N, int64_t T, int64_t D, int L, int K, int causal,
+                           double eps, double inv_temp, double *out, double *den)
+{
+    if (K < 1 || K > ORACLE_MAX_K || L < 1 || N < 0 || T < 0 || D < 1)
+        return -1;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t n = 0; n < N; ++n) {
+        const double *pl = planes + plane_of[n] * (int64_t)L * K * D;
+        stream_forward_ex(q + n * T * D, k + n * T * D, v + n * T * D, kw ? kw + n * T : NULL,
+                          pl, T, D, L, K, causal, eps, inv_temp, out + n * T * D,
+                          den ? den + n * T : NULL);
+    }
+    return 0;
+}
+
+int oracle_race_backward_ex(const double *q, const double *k, const double *v,
+                            const double *kw, const double *dout, const double *dden,
+                            const double *planes, const int64_t *plane_of, int64_t N,
+                            int64_t T, int64_t D, int L, int K, int causal, double eps,
+                            double inv_temp, double *dq, double *dk, double *dv,
+                            double *grad_inv_temp, double *grad_inv_temp_l1)
+{
+    if (K < 1 || K > ORACLE_MAX_K || L < 1 || N < 0 || T < 0 || D < 1)
+        return -1;
+    double *part = calloc((size_t)(N > 0 ? N : 1), sizeof(double));
+    double *pabs = calloc((size_t)(N > 0 ? N : 1), sizeof(double));
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t n = 0; n < N; ++n) {
+        const double *pl = planes + plane_of[n] * (int64_t)L * K * D;
+        const int64_t o = n * T * D;
+        stream_backward_ex(q + o, k + o, v + o, kw ? kw + n * T : NULL, dout + o,
+                           dden ? dden + n * T : NULL, pl, T, D, L, K, causal, eps, inv_temp,
+                           dq + o, dk + o, dv + o, &part[n], &pabs[n]);
+    }
+    double tot = 0.0, tabs = 0.0;
+    for (int64_t n = 0; n < N; ++n) {
+        tot += part[n];
+        tabs += pabs[n];
+    }
+    if (grad_inv_temp)
+        *grad_inv_temp = tot;
+    if (grad_inv_temp_l1)
+        *grad_inv_temp_l1 = tabs;
     free(part);
     free(pabs);
     return 0;

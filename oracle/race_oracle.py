@@ -10,6 +10,9 @@ Two layers:
     kernels/cpu/race_pref.cpp:36-220).  Inputs are [M,B,T,H,D] arrays like the
     reference's BatchedACE; planes are [NP,L,K,D] (NP = 1 when shared,
     misc/race.py:39-51).
+  * ``race_forward_ex`` / ``race_backward_ex``: F1 with per-token key
+    weights (the padding mask, misc/classification.py:576-592) and the den
+    output of misc/classification.py:641-659 and misc/vit.py:1452-1510.
   * ``race_global_forward`` / ``race_global_backward``: the same C file's
     restatement of the globally normalised causal mode ("F2",
     misc/elsaa_causal_complete.py:438-586, misc/race_kernel.py:8-124).
@@ -62,6 +65,11 @@ def _lib():
         lib.oracle_race_global_backward.argtypes = [dp, dp, dp, dp, dp, dp, ip, i64, i64, i64, ci, ci, cd, cd,
                                                     dp, dp, dp, dp, dp]
         lib.oracle_race_global_backward.restype = ci
+        lib.oracle_race_forward_ex.argtypes = [dp, dp, dp, dp, dp, ip, i64, i64, i64, ci, ci, ci, cd, cd, dp, dp]
+        lib.oracle_race_forward_ex.restype = ci
+        lib.oracle_race_backward_ex.argtypes = [dp, dp, dp, dp, dp, dp, dp, ip, i64, i64, i64, ci, ci, ci, cd, cd,
+                                                dp, dp, dp, dp, dp]
+        lib.oracle_race_backward_ex.restype = ci
         lib.oracle_prefix_mean_flat.argtypes = [fp, fp, i64, i64, i64, cd, fp]
         lib.oracle_prefix_mean_flat.restype = None
         lib.oracle_prefix_mean_flat_bw.argtypes = [fp, fp, fp, i64, i64, i64, cd, fp, fp]
@@ -137,6 +145,57 @@ def race_backward(q, k, v, dout, planes, *, causal: bool, eps: float = 1e-6, inv
                                      _dptr(git[1:]))
     if rc != 0:
         raise ValueError("oracle_race_backward rejected its arguments")
+    res = (from_streams(dq, M, B, H), from_streams(dk, M, B, H), from_streams(dv, M, B, H), float(git[0]))
+    return res + (float(git[1]),) if with_l1 else res
+
+
+def mask_to_streams(mask, M, H):
+    """[B,T] per-token key weights -> [N,T] (stream n = (m*B + b)*H + h)."""
+    m = np.asarray(mask, dtype=np.float64)
+    B, T = m.shape
+    return np.ascontiguousarray(np.broadcast_to(m[None, :, None, :], (M, B, H, T)).reshape(M * B * H, T))
+
+
+def race_forward_ex(q, k, v, planes, *, kmask=None, causal: bool, eps: float = 1e-6, inv_temp: float):
+    """fp64 F1 forward with key weights kmask [B,T] (None = 1) on P_K.
+    Returns (out [M,B,T,H,D], den [M,B,H,T]), den = sum_s P_Q A_s(t) unclamped."""
+    M, B, T, H, D = q.shape
+    planes = np.ascontiguousarray(np.asarray(planes, dtype=np.float64))
+    NP, L, K, _ = planes.shape
+    qs, ks, vs = to_streams(q), to_streams(k), to_streams(v)
+    kw = mask_to_streams(kmask, M, H) if kmask is not None else None
+    pm = _plane_map(M, B, H, NP)
+    out = np.zeros_like(qs)
+    den = np.zeros((qs.shape[0], T), dtype=np.float64)
+    rc = _lib().oracle_race_forward_ex(_dptr(qs), _dptr(ks), _dptr(vs), _dptr(kw) if kw is not None else None,
+                                       _dptr(planes), pm.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                       qs.shape[0], T, D, L, K, int(causal), float(eps), float(inv_temp),
+                                       _dptr(out), _dptr(den))
+    if rc != 0:
+        raise ValueError("oracle_race_forward_ex rejected its arguments")
+    return from_streams(out, M, B, H), den.reshape(M, B, H, T)
+
+
+def race_backward_ex(q, k, v, dout, planes, *, kmask=None, dden=None, causal: bool, eps: float = 1e-6,
+                     inv_temp: float, with_l1: bool = False):
+    """fp64 backward of race_forward_ex for dout [M,B,T,H,D] and dden
+    [M,B,H,T] (None = 0).  Returns (dq, dk, dv, grad_inv_temp[, l1])."""
+    M, B, T, H, D = q.shape
+    planes = np.ascontiguousarray(np.asarray(planes, dtype=np.float64))
+    NP, L, K, _ = planes.shape
+    qs, ks, vs, gs = to_streams(q), to_streams(k), to_streams(v), to_streams(dout)
+    kw = mask_to_streams(kmask, M, H) if kmask is not None else None
+    hs = den_to_streams(dden, M, B, H) if dden is not None else None
+    pm = _plane_map(M, B, H, NP)
+    dq, dk, dv = np.zeros_like(qs), np.zeros_like(qs), np.zeros_like(qs)
+    git = np.zeros(2, dtype=np.float64)
+    rc = _lib().oracle_race_backward_ex(_dptr(qs), _dptr(ks), _dptr(vs), _dptr(kw) if kw is not None else None,
+                                        _dptr(gs), _dptr(hs) if hs is not None else None, _dptr(planes),
+                                        pm.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), qs.shape[0], T, D, L, K,
+                                        int(causal), float(eps), float(inv_temp), _dptr(dq), _dptr(dk), _dptr(dv),
+                                        _dptr(git), _dptr(git[1:]))
+    if rc != 0:
+        raise ValueError("oracle_race_backward_ex rejected its arguments")
     res = (from_streams(dq, M, B, H), from_streams(dk, M, B, H), from_streams(dv, M, B, H), float(git[0]))
     return res + (float(git[1]),) if with_l1 else res
 

@@ -188,7 +188,13 @@ template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Pla
             k_fwd_out<T, SP, true, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         else
             k_fwd_out<T, SP, false, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
-        if (sliced<T, KB>()) slice_sum<T>(p, d, a.opart, d->o_stride, a.out, s);
+        if (sliced<T, KB>()) {
+            slice_sum<T>(p, d, a.opart, d->o_stride, a.out, s);
+            if (a.den) {
+                const int64_t nt = p.N * d->T;
+                k_den_sum<<<(unsigned)((nt + 255) / 256), 256, 0, s>>>(a.denpart, p.nslice, nt, a.den);
+            }
+        }
     }
     return launched("race_fwd");
 }
@@ -318,6 +324,43 @@ int check_den(const char *name, const float *p) {
     return RACE_OK;
 }
 
+// Checks and Args of a backward call (race_bwd, race_bwd_ex)
+int bwd_args(const race_desc *d, const Plan &p, const void *q, const void *k, const void *v, const float *planes,
+             const void *dout, const void *state, void *dq, void *dk, void *dv, void *ws, size_t ws_bytes, Args &a) {
+    int rc;
+    if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
+        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) ||
+        (rc = check_tensor("dout", dout, d->do_stride, p.esize, d->T)) ||
+        (rc = check_tensor("dq", dq, d->g_stride, p.esize, d->T)) || (rc = check_tensor("dk", dk, d->g_stride, p.esize, d->T)) ||
+        (rc = check_tensor("dv", dv, d->g_stride, p.esize, d->T)))
+        return rc;
+    if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
+    if (!state) return fail(RACE_E_INVALID, "state is NULL");
+    if (!ws || ws_bytes < p.bws)
+        return fail(RACE_E_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, p.bws);
+    a = base_args(d, p, planes);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.dout = dout;
+    a.dq = dq;
+    a.dk = dk;
+    a.dv = dv;
+    a.fstate = (double *)state;
+    const size_t blk = (size_t)p.N * p.nseg * p.Spad * SROW;
+    a.rdelta = (float *)ws;
+    a.rstate = a.rdelta + blk;
+    a.tpart = a.rstate + blk;
+    if (p.parts) {
+        float *part = (float *)((char *)ws + p.bws_core);
+        const size_t pe = p.part_bytes / sizeof(float);
+        a.dqpart = part;
+        a.dkpart = part + pe;
+        a.dvpart = part + 2 * pe;
+    }
+    return RACE_OK;
+}
+
 // prefix mean: segment length so that NS * nseg ~ 4096 waves
 int64_t pm_tseg(int64_t NS, int64_t T) {
     int64_t nseg = (4096 + NS - 1) / NS;
@@ -393,36 +436,64 @@ int race_bwd(const race_desc *d, const void *q, const void *k, const void *v, co
     Plan p;
     int rc = make_plan(d, p);
     if (rc) return rc;
+    Args a;
+    if ((rc = bwd_args(d, p, q, k, v, planes, dout, state, dq, dk, dv, ws, ws_bytes, a))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    if (d->dtype == RACE_DTYPE_BF16) return bwd_dispatch<bf16>(d, p, a, grad_inv_temp, s);
+    return bwd_dispatch<float>(d, p, a, grad_inv_temp, s);
+}
+
+size_t race_fwd_ex_workspace_bytes(const race_desc *d) {
+    Plan p;
+    if (make_plan(d, p) != RACE_OK) return 0;
+    ok();
+    return p.gfws;  // den partials per slice, like the global mode
+}
+
+int race_fwd_ex(const race_desc *d, const void *q, const void *k, const void *v, const float *planes,
+                const float *kmask, void *out, float *den, void *state, void *ws, size_t ws_bytes, void *stream) {
+    Plan p;
+    int rc = make_plan(d, p);
+    if (rc) return rc;
+    if (d->causal && (kmask || den))
+        return fail(RACE_E_UNSUPPORTED, "key weights and den are implemented for the non-causal operator");
     if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
-        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) ||
-        (rc = check_tensor("dout", dout, d->do_stride, p.esize, d->T)) ||
-        (rc = check_tensor("dq", dq, d->g_stride, p.esize, d->T)) || (rc = check_tensor("dk", dk, d->g_stride, p.esize, d->T)) ||
-        (rc = check_tensor("dv", dv, d->g_stride, p.esize, d->T)))
+        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) || (rc = check_tensor("out", out, d->o_stride, p.esize, d->T)) ||
+        (kmask && (rc = check_den("kmask", kmask))) || (den && (rc = check_den("den", den))))
         return rc;
     if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
     if (!state) return fail(RACE_E_INVALID, "state is NULL");
-    if (!ws || ws_bytes < p.bws)
-        return fail(RACE_E_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, p.bws);
+    const size_t need = den ? p.gfws : p.fws;
+    if (!ws || ws_bytes < need) return fail(RACE_E_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, need);
     Args a = base_args(d, p, planes);
     a.q = q;
     a.k = k;
     a.v = v;
-    a.dout = dout;
-    a.dq = dq;
-    a.dk = dk;
-    a.dv = dv;
+    a.out = out;
+    a.kw = kmask;
+    a.den = den;
     a.fstate = (double *)state;
-    const size_t blk = (size_t)p.N * p.nseg * p.Spad * SROW;
-    a.rdelta = (float *)ws;
-    a.rstate = a.rdelta + blk;
-    a.tpart = a.rstate + blk;
-    if (p.parts) {
-        float *part = (float *)((char *)ws + p.bws_core);
-        const size_t pe = p.part_bytes / sizeof(float);
-        a.dqpart = part;
-        a.dkpart = part + pe;
-        a.dvpart = part + 2 * pe;
-    }
+    a.fdelta = (double *)ws;
+    a.opart = p.parts ? (float *)((char *)ws + p.fws_core) : nullptr;
+    a.denpart = p.parts && den ? (float *)((char *)ws + p.fws) : nullptr;
+    hipStream_t s = (hipStream_t)stream;
+    if (d->dtype == RACE_DTYPE_BF16) return fwd_dispatch<bf16>(d, p, a, s);
+    return fwd_dispatch<float>(d, p, a, s);
+}
+
+int race_bwd_ex(const race_desc *d, const void *q, const void *k, const void *v, const float *planes,
+                const float *kmask, const void *dout, const float *dden, const void *state, void *dq, void *dk,
+                void *dv, float *grad_inv_temp, void *ws, size_t ws_bytes, void *stream) {
+    Plan p;
+    int rc = make_plan(d, p);
+    if (rc) return rc;
+    if (d->causal && (kmask || dden))
+        return fail(RACE_E_UNSUPPORTED, "key weights and den are implemented for the non-causal operator");
+    if ((kmask && (rc = check_den("kmask", kmask))) || (dden && (rc = check_den("dden", dden)))) return rc;
+    Args a;
+    if ((rc = bwd_args(d, p, q, k, v, planes, dout, state, dq, dk, dv, ws, ws_bytes, a))) return rc;
+    a.kw = kmask;
+    a.dden = dden;
     hipStream_t s = (hipStream_t)stream;
     if (d->dtype == RACE_DTYPE_BF16) return bwd_dispatch<bf16>(d, p, a, grad_inv_temp, s);
     return bwd_dispatch<float>(d, p, a, grad_inv_temp, s);

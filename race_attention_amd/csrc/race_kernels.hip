@@ -72,6 +72,9 @@ struct Args {
     float *den, *denpart;
     const float *dden;
     float *rden, *gden;
+    // per-token key weights [B][T] on P_K (non-causal padding mask; nullable).
+    // Non-causal F1 also writes den [N][T] when den is set and reads dden.
+    const float *kw;
 };
 
 constexpr int SROW = D + 1;  // state row: D values of B (or U) then A (or alpha)
@@ -933,7 +936,8 @@ template <typename T, int SP> struct FwdReduceL {
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t oSig = align16(oPlLo + sizeof(T) * NCOL * LDN);
     static constexpr size_t oCst = align16(oSig + sizeof(float) * 2 * TT * LDC);
-    static constexpr size_t bytes = align16(oCst + Consts<T>::bytes);
+    static constexpr size_t oTok = align16(oCst + Consts<T>::bytes);  // key weights [TT] (+ unused [TT])
+    static constexpr size_t bytes = align16(oTok + sizeof(float) * 2 * TT);
 };
 
 // The tile's (A, B) sums -- tot (lane: bucket 4g + e) and dB^T (d-row) --
@@ -970,6 +974,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
+    float *sTok = (float *)(smem + Ly::oTok);
+    const float *kwp = a.kw ? a.kw + (int64_t)((n / a.H) % a.B) * a.T : nullptr;  // batch row's key weights
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
@@ -983,24 +989,33 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     wait_state_loads();
     Prefetch<T, NTH> pk_;
     PrefetchT<T, NTH, 1> pv_;
+    TokPre pt_;
     if (j0 < j1) {
         pk_.issue(kp, a.sk.t, j0 * TT, a.T);
         pv_.issue(0, vp, a.sv.t, j0 * TT, a.T);
+        if (kwp) pt_.issue(kwp, nullptr, j0 * TT, a.T);
     }
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
         __syncthreads();
         pk_.template commit<NL>(sK, nullptr);
         pv_.template commit<NL>(0, nullptr, sVt);
+        if (kwp) pt_.commit(sTok);
         if (jt + 1 < j1) {
             pk_.issue(kp, a.sk.t, t0 + TT, a.T);
             pv_.issue(0, vp, a.sv.t, t0 + TT, a.T);
+            if (kwp) pt_.issue(kwp, nullptr, t0 + TT, a.T);
         }
         __syncthreads();
         for (int q = w; q < 4; q += NW_) project_tile<T, NL>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, nullptr);
         __syncthreads();
         f32x4 PK[2];
         probs_st<KB>(sSp, sSm, sg, a.S, t0, a.T, PK);
+        if (kwp)  // P_K' = w_t P_K
+            for (int nt = 0; nt < 2; ++nt) {
+                const float wt = sTok[16 * nt + i];
+                for (int e = 0; e < 4; ++e) PK[nt][e] *= wt;
+            }
         const Frag<T> Pf = token_operand<T>(PK, cst);
         f32x4 tot, dB[4];
         tile_sums<T>(Pf, cst, sVt, tot, dB);
@@ -1056,14 +1071,15 @@ template <typename T, int SP, bool CAUSAL, bool GN> struct FwdOutL {
     static constexpr size_t oPl = ALIAS ? oEnd : oKEnd;
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t oCst = align16(oPlLo + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oDen = align16(oCst + Consts<T>::bytes);  // GN: [NW_][TT] per-wave den shares
-    static constexpr size_t bytes = align16(oDen + (GN ? sizeof(float) * NW_ * TT : 0));
+    // [NW_][TT] per-wave den shares (GN; non-causal F1 when den is requested)
+    static constexpr size_t oDen = align16(oCst + Consts<T>::bytes);
+    static constexpr size_t bytes = align16(oDen + (GN || !CAUSAL ? sizeof(float) * NW_ * TT : 0));
 };
 
-// Output tile (d = 16md.., t = 16nt..).  GN: the tile's numerator is divided
-// by max(den, eps), den summed from the waves' shares (sDen [NW_][TT]); the
-// md == 0 tiles also write den.  Sliced GN instantiations write the
-// numerator and this slice's den share as partials instead.
+// Output tile (d = 16md.., t = 16nt..).  With sDen set, den is summed from
+// the waves' shares (sDen [NW_][TT]) and the md == 0 tiles write it (sliced
+// instantiations: this slice's den share, a partial).  GN also divides the
+// tile's numerator by max(den, eps) (sliced: the numerator is the partial).
 template <typename T, int SP, bool CAUSAL, bool GN = false>
 __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T *Wts, const T *sVt, T *op,
                              int64_t st, int64_t t0, int64_t Tn, float *part, const float *sDen = nullptr,
@@ -1091,12 +1107,12 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
         mma(O, ld_frag_pi(sVt + (16 * md + i) * LDT), frag_acc<T>(Sc[0], Sc[1]));
     }
     const int t = 16 * nt + i;
-    if constexpr (GN) {
+    if (GN || !CAUSAL ? sDen != nullptr : false) {
         constexpr int NW_ = SP / WB;
         float dn = 0.f;
 #pragma unroll
         for (int w = 0; w < NW_; ++w) dn += sDen[w * TT + t];
-        if (!part) {
+        if (GN && !part) {
             const float r = 1.0f / fmaxf(dn, eps);
 #pragma unroll
             for (int e = 0; e < 4; ++e) O[e] *= r;
@@ -1137,9 +1153,11 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
     T *op = (T *)a.out + stream_off(a.so, n, a.B, a.H);
     float *opart = sliced<T, KB>() ? a.opart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
-    float *sDen = (float *)(smem + Ly::oDen);
-    float *denp = !GN ? nullptr
-                      : sliced<T, KB>() ? a.denpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T : a.den + (int64_t)n * a.T;
+    const bool want_den = GN || (!CAUSAL && a.den);
+    float *sDen = want_den ? (float *)(smem + Ly::oDen) : nullptr;
+    float *denp = !want_den       ? nullptr
+                  : sliced<T, KB>() ? a.denpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T
+                                    : a.den + (int64_t)n * a.T;
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
@@ -1221,6 +1239,15 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
                     const float A = (float)a0[e] + (CAUSAL ? Acum[nt][e] : 0.f);
                     W[nt][e] = PQ[nt][e] * rcp(A + a.eps);
                 }
+            if constexpr (!CAUSAL) {
+                if (want_den)  // this wave's share of den(t) = sum_s P_Q A_s
+                    for (int nt = 0; nt < 2; ++nt) {
+                        float dp = 0.f;
+                        for (int e = 0; e < 4; ++e) dp += PQ[nt][e] * (float)a0[e];
+                        dp = xor32_sum(xor16_sum(dp));
+                        if (g == 0) sDen[w * TT + 16 * nt + i] = dp;
+                    }
+            }
         }
         store_ts<T, SP>(sWts, sw, W);
         if constexpr (CAUSAL) {
@@ -1293,9 +1320,10 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr size_t oPair = align16(oHash + HashOps<T, 4>::bytes);
     static constexpr size_t oShare = align16(oPair + PairOps<T>::bytes);
     static constexpr size_t oTok = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
-    // GN: staged (den, dden) [2][TT], computed (rd, gd) [2][TT], the O tile
+    // GN: staged (den, dden) [2][TT], computed (rd, gd) [2][TT], the O tile;
+    // non-causal: staged dden [TT]
     static constexpr size_t oTokIn = align16(oTok + (GN ? sizeof(float) * 2 * TT : 0));
-    static constexpr size_t oO = align16(oTokIn + (GN ? sizeof(float) * 2 * TT : 0));
+    static constexpr size_t oO = align16(oTokIn + (GN || !CAUSAL ? sizeof(float) * 2 * TT : 0));
     static constexpr size_t bytes = align16(oO + (GN ? sizeof(T) * TT * LDN : 0));
 };
 
@@ -1334,7 +1362,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     T *sO = (T *)(smem + Ly::oO);
     const T *op = GN ? (const T *)a.out + stream_off(a.so, n, a.B, a.H) : nullptr;
     const float *denp = GN ? a.den + (int64_t)n * a.T : nullptr;
-    const float *ddp = GN && a.dden ? a.dden + (int64_t)n * a.T : nullptr;
+    const float *ddp = (GN || !CAUSAL) && a.dden ? a.dden + (int64_t)n * a.T : nullptr;
     // one bucket slice writes the per-token terms for k_bwd_out
     float *rdw = GN && z == 0 ? a.rden + (int64_t)n * a.T : nullptr;
     float *gdw = GN && z == 0 ? a.gden + (int64_t)n * a.T : nullptr;
@@ -1386,6 +1414,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         if constexpr (GN) {
             po_.template commit<NL>(sO, nullptr);
             pt_.commit(sTokIn);
+        } else if constexpr (!CAUSAL) {
+            if (ddp) pt_.commit(sTokIn);
         }
     };
     if (j0 < j1) {
@@ -1398,6 +1428,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         if constexpr (GN) {
             po_.issue(op, a.so.t, j0 * TT, a.T);
             pt_.issue(denp, ddp, j0 * TT, a.T);
+        } else if constexpr (!CAUSAL) {
+            if (ddp) pt_.issue(ddp, nullptr, j0 * TT, a.T);
         }
         commit();
     }
@@ -1417,6 +1449,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         if constexpr (GN) {
             po_.issue(op, a.so.t, tn, a.T);
             pt_.issue(denp, ddp, tn, a.T);
+        } else if constexpr (!CAUSAL) {
+            if (ddp) pt_.issue(ddp, nullptr, tn, a.T);
         }
         __syncthreads();
         if constexpr (GN) gn_token_terms<T, NL, NW_>(sG, sO, sTokIn, sTok, a.eps, rdw, gdw, t0, a.T);
@@ -1480,6 +1514,15 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
                     } else {
                         dPQ[nt][e] = G[e] * inv[nt][e];
                         dA[nt][e] = -W[nt][e] * dPQ[nt][e];
+                    }
+                }
+                if constexpr (!CAUSAL && !GN) {
+                    if (ddp) {  // den = sum_s P_Q A_s: dP_Q += h A, dA += h P_Q
+                        const float h = sTokIn[16 * nt + i];
+                        for (int e = 0; e < 4; ++e) {
+                            dA[nt][e] += h * PQ[nt][e];
+                            dPQ[nt][e] += h * (float)a0[e];
+                        }
                     }
                 }
             }
@@ -1567,7 +1610,8 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     static constexpr size_t oPair = align16(oSuf + (CAUSAL ? SufOps<T>::bytes : 0));
     static constexpr size_t oShare = align16(oPair + PairOps<T>::bytes);
     static constexpr size_t oTok = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
-    static constexpr size_t bytes = align16(oTok + (GN ? sizeof(float) * 2 * TT : 0));  // GN: rden, gden
+    // GN: rden, gden [2][TT]; non-causal: key weights [TT]
+    static constexpr size_t bytes = align16(oTok + (GN || !CAUSAL ? sizeof(float) * 2 * TT : 0));
 };
 
 template <typename T, int SP, bool CAUSAL>
@@ -1642,6 +1686,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     float *vpart = sliced<T, KB>() ? a.dvpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
     float *sTok = (float *)(smem + Ly::oTok);
     const float *rdp = GN ? a.rden + (int64_t)n * a.T : nullptr, *gdp = GN ? a.gden + (int64_t)n * a.T : nullptr;
+    const float *kwp = !CAUSAL && a.kw ? a.kw + (int64_t)((n / a.H) % a.B) * a.T : nullptr;
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
@@ -1698,6 +1743,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             pg_.template commit<NL>(0, sG, sGt);
         } else {
             pvn_.template commit<NL>(sV, nullptr);
+            if (kwp) pt_.commit(sTok);
         }
         if constexpr (GN) pt_.commit(sTok);
     };
@@ -1710,6 +1756,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             pg_.issue(0, gp, a.sdo.t, tl, a.T);
         } else {
             pvn_.issue(vp, a.sv.t, tl, a.T);
+            if (kwp) pt_.issue(kwp, nullptr, tl, a.T);
         }
         if constexpr (GN) pt_.issue(rdp, gdp, tl, a.T);
         commit();
@@ -1729,6 +1776,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             pg_.issue(0, gp, a.sdo.t, tn, a.T);
         } else {
             pvn_.issue(vp, a.sv.t, tn, a.T);
+            if (kwp) pt_.issue(kwp, nullptr, tn, a.T);
         }
         if constexpr (GN) pt_.issue(rdp, gdp, tn, a.T);
         __syncthreads();
@@ -1743,6 +1791,14 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         __syncthreads();
         f32x4 PKr[2];  // operand-rounded P_K (fp32 P_K is rebuilt for the softmax backward)
         probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PKr);
+        float kwt[2] = {1.f, 1.f};  // non-causal key weights: P_K' = w_t P_K
+        if constexpr (!CAUSAL) {
+            if (kwp)
+                for (int nt = 0; nt < 2; ++nt) {
+                    kwt[nt] = sTok[16 * nt + i];
+                    for (int e = 0; e < 4; ++e) PKr[nt][e] *= kwt[nt];
+                }
+        }
         for (int nt = 0; nt < 2; ++nt)
             for (int e = 0; e < 4; ++e) PKr[nt][e] = as_operand<T>(PKr[nt][e]);
         const Frag<T> Pf = token_operand<T>(PKr, cst, po);
@@ -1835,7 +1891,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 f32x4 c = zero4();
                 mma(c, u0, NL::frag_pi(sV, 16 * nt + i, 0));
                 mma(c, u1, NL::frag_pi(sV, 16 * nt + i, 1));
-                for (int e = 0; e < 4; ++e) dPK[nt][e] = c[e] + al[e];
+                for (int e = 0; e < 4; ++e) dPK[nt][e] = (c[e] + al[e]) * kwt[nt];  // through the key weight
             }
         }
         {
@@ -1872,6 +1928,15 @@ __global__ void k_slice_sum(const float *part, int nslice, int64_t N, int64_t Tn
     f32x4 acc = *reinterpret_cast<const f32x4 *>(part + row);
     for (int z = 1; z < nslice; ++z) acc += *reinterpret_cast<const f32x4 *>(part + z * zs + row);
     store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc);
+}
+
+// den [N][T] = sum of the per-slice partials [nslice][N][T], in slice order.
+__global__ void k_den_sum(const float *denpart, int nslice, int64_t NT, float *den) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= NT) return;
+    float dn = denpart[idx];
+    for (int z = 1; z < nslice; ++z) dn += denpart[z * NT + idx];
+    den[idx] = dn;
 }
 
 // Global normalisation, sliced instantiations: out = (sum of the slices'

@@ -8,6 +8,11 @@ reference's M-fold expand), hyperplanes [L,K,D] shared or [M,L,K,D]
 per-estimator, output [M,B,T,H,D].  Forward and backward run as HIP kernels on
 the current stream; bucket probabilities are recomputed in the backward.
 
+``race_attention_ex(..., kmask=, with_den=)`` is the non-causal operator of
+padded batches and of the denominator proxy: per-token key weights on P_K
+(misc/classification.py:576-592) and den = sum_s P_Q A_s
+(misc/classification.py:641-659, misc/vit.py:1452-1510).
+
 ``race_attention_global(Q, K, V, planes, beta, ...)`` is the globally
 normalised causal operator ("F2") behind CausalRACEAttention
 (misc/elsaa_causal_complete.py:438-586): it returns out = num / max(den, 1e-6)
@@ -174,6 +179,115 @@ class RACEFunction(torch.autograd.Function):
 def race_attention(Qhf, Khf, Vhf, planes, *, L, K, causal, inv_temp, eps=1e-6):
     """Differentiable RACE operator on [M,B,T,H,D] tensors (see module doc)."""
     return RACEFunction.apply(Qhf, Khf, Vhf, planes, inv_temp, L, K, causal, eps)
+
+
+# ------------------------------------------------- key weights and den (F1 extras)
+def _kmask_check(kmask, B, T, dev):
+    if kmask is None:
+        return None
+    if kmask.shape != (B, T):
+        raise ValueError(f"kmask must be [B,T] = {(B, T)}; got {tuple(kmask.shape)}")
+    return kmask.to(device=dev, dtype=torch.float32).contiguous()
+
+
+def race_fwd_ex_raw(q, k, v, planes, *, L, K, inv_temp, kmask=None, want_den=False, eps=1e-6, seg_tiles=0):
+    """Non-causal forward with key weights kmask [B,T] (None = 1) and the den
+    output: returns (out [M,B,T,H,D], den [M,B,H,T] fp32 or None, state)."""
+    _require_gpu(q, k, v, planes)
+    _check_inputs(q, k, v, planes, L, K)
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    planes = planes.to(device=q.device, dtype=torch.float32).contiguous()
+    M, B, T, H, _ = q.shape
+    kmask = _kmask_check(kmask, B, T, q.device)
+    lib = _lib.load()
+    d = make_desc(q, k, v, planes, L=L, K=K, causal=False, eps=eps, inv_temp=inv_temp, seg_tiles=seg_tiles)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    den = torch.empty((M, B, H, T), dtype=torch.float32, device=q.device) if want_den else None
+    d.o_stride = _strides4(out)
+    sb = lib.race_state_bytes(ctypes.byref(d))
+    if sb == 0:
+        _lib.check(-1, "race_state_bytes")
+    wb = lib.race_fwd_ex_workspace_bytes(ctypes.byref(d))
+    state = torch.empty(sb, dtype=torch.uint8, device=q.device)
+    ws = torch.empty(max(wb, 16), dtype=torch.uint8, device=q.device)
+    rc = lib.race_fwd_ex(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(planes),
+                         _ptr(kmask) if kmask is not None else None, _ptr(out),
+                         _ptr(den) if den is not None else None, _ptr(state), _ptr(ws),
+                         ctypes.c_size_t(ws.numel()), _stream())
+    _lib.check(rc, "race_fwd_ex")
+    return out, den, state
+
+
+def race_bwd_ex_raw(q, k, v, planes, dout, dden, state, *, L, K, inv_temp, kmask=None, eps=1e-6, seg_tiles=0,
+                    want_temp_grad=True):
+    """Backward of race_fwd_ex_raw: returns (dq, dk, dv, grad_inv_temp or None)."""
+    _require_gpu(q, k, v, planes, state)
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    M, B, T, H, _ = q.shape
+    dout = _aligned(dout.to(q.dtype)) if dout is not None else torch.zeros(q.shape, dtype=q.dtype, device=q.device)
+    planes = planes.to(device=q.device, dtype=torch.float32).contiguous()
+    kmask = _kmask_check(kmask, B, T, q.device)
+    if dden is not None:
+        dden = _den_check(dden.to(torch.float32), M, B, H, T, "dden")
+    lib = _lib.load()
+    d = make_desc(q, k, v, planes, L=L, K=K, causal=False, eps=eps, inv_temp=inv_temp, seg_tiles=seg_tiles)
+    d.do_stride = _strides4(dout)
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty_like(dq)
+    dv = torch.empty_like(dq)
+    d.g_stride = _strides4(dq)
+    if state.numel() != lib.race_state_bytes(ctypes.byref(d)):
+        raise ValueError("state buffer does not match this descriptor")
+    wb = lib.race_bwd_workspace_bytes(ctypes.byref(d))
+    ws = torch.empty(max(wb, 16), dtype=torch.uint8, device=q.device)
+    git = torch.empty((), dtype=torch.float32, device=q.device) if want_temp_grad else None
+    rc = lib.race_bwd_ex(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(planes),
+                         _ptr(kmask) if kmask is not None else None, _ptr(dout),
+                         _ptr(dden) if dden is not None else None, _ptr(state), _ptr(dq), _ptr(dk), _ptr(dv),
+                         _ptr(git) if git is not None else None, _ptr(ws), ctypes.c_size_t(ws.numel()), _stream())
+    _lib.check(rc, "race_bwd_ex")
+    return dq, dk, dv, git
+
+
+class RACEExFunction(torch.autograd.Function):
+    """Autograd Function of the non-causal operator with key weights and the
+    den output: forward(Q, K, V, planes, inv_temp, kmask, L, K, eps,
+    want_den) -> (out, den); den is an empty tensor unless want_den.  kmask
+    (key weights, [B,T]) receives no gradient."""
+
+    @staticmethod
+    def forward(ctx, Q, Kx, V, planes, inv_temp, kmask, L, K, eps, want_den):
+        it = float(inv_temp)
+        out, den, state = race_fwd_ex_raw(Q, Kx, V, planes, L=L, K=K, inv_temp=it, kmask=kmask,
+                                          want_den=want_den, eps=eps)
+        ctx.save_for_backward(Q, Kx, V, planes, kmask if kmask is not None else torch.empty(0), state)
+        ctx.cfg = (L, K, eps, it, kmask is not None)
+        ctx.temp_is_tensor = torch.is_tensor(inv_temp)
+        ctx.set_materialize_grads(False)
+        if den is None:
+            den = torch.empty(0, dtype=torch.float32, device=Q.device)
+        return out, den
+
+    @staticmethod
+    def backward(ctx, dout, dden):
+        Q, Kx, V, planes, kmask, state = ctx.saved_tensors
+        L, K, eps, it, has_mask = ctx.cfg
+        want = ctx.temp_is_tensor and ctx.needs_input_grad[4]
+        if dden is not None and dden.numel() == 0:
+            dden = None
+        dq, dk, dv, git = race_bwd_ex_raw(Q, Kx, V, planes, dout, dden, state, L=L, K=K, inv_temp=it,
+                                          kmask=kmask if has_mask else None, eps=eps, want_temp_grad=want)
+        return (dq if ctx.needs_input_grad[0] else None,
+                dk if ctx.needs_input_grad[1] else None,
+                dv if ctx.needs_input_grad[2] else None,
+                None, git if want else None, None, None, None, None, None)
+
+
+def race_attention_ex(Qhf, Khf, Vhf, planes, *, L, K, inv_temp, kmask=None, with_den=False, eps=1e-6):
+    """Non-causal RACE on [M,B,T,H,D] with per-token key weights kmask [B,T]
+    on P_K.  Returns out, or (out, den [M,B,H,T] unclamped) with with_den."""
+    out, den = RACEExFunction.apply(Qhf, Khf, Vhf, planes, inv_temp, kmask, L, K, eps, bool(with_den))
+    return (out, den) if with_den else out
 
 
 # ------------------------------------------------- global normalisation (F2)

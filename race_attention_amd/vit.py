@@ -1,7 +1,8 @@
 """Non-causal RACE modules with the reference API of misc/vit.py.
 
 Drop-in replacements for misc/vit.py's BatchedACE (:888-979), RACEAttention
-(:994-1039) and RACEBlock (:1040-1068): same arguments, buffer/parameter names
+(:994-1039), RACEAttentionWithDenom (:1441-1543) and RACEBlock (:1040-1068):
+same arguments, buffer/parameter names
 (planes_T, protos_T, logit_temp) and shapes; the attention core runs in the
 HIP library.  The learnable temperature is exp(logit_temp) clamped to
 [1e-2, temp_max] (temp_max 20 as misc/vit.py:923; the notebooks, misc/mlm.py
@@ -12,7 +13,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from .functional import race_attention
+from .functional import race_attention, race_attention_ex
 from .race import _corner_protos, merge_heads, planes_from_T
 
 
@@ -78,6 +79,32 @@ class RACEAttention(nn.Module):
         pack = lambda z: z.unsqueeze(0).expand(M, -1, -1, -1, -1)  # noqa: E731
         out_hm = self.ace(pack(K), pack(V), pack(Q))
         return self.drop(self.out(merge_heads(out_hm, self.reference_head_merge)))
+
+
+class RACEAttentionWithDenom(RACEAttention):
+    """RACEAttention that also returns the denominator proxy
+    (misc/vit.py:1441-1543): forward(x) -> (out [B,T,d_out], d_race_token
+    [B,T,1]), d_race(i) = mean over M and heads of sum_s P_Q(i,s) A(s),
+    each clamped at eps, then at 1e-6."""
+
+    def _ace_with_denom(self, Khf, Vhf, Qhf, eps: float = 1e-6):
+        """(out [M,B,T,H,d_k], den [M,B,T,H]) (misc/vit.py:1452-1510)."""
+        ace = self.ace
+        out, den = race_attention_ex(Qhf, Khf, Vhf, ace.planes(), L=ace.L, K=ace.K, inv_temp=1.0 / ace.scale(),
+                                     with_den=True, eps=eps)
+        return out, den.clamp_min(eps).permute(0, 1, 3, 2)
+
+    def forward(self, x):
+        B, T, _ = x.shape
+        H, d_k, M = self.H, self.d_k, self.M
+        Q = self.q_proj(x).view(B, T, H, d_k)
+        K = self.k_proj(x).view(B, T, H, d_k)
+        V = self.v_proj(x).view(B, T, H, d_k)
+        pack = lambda z: z.unsqueeze(0).expand(M, -1, -1, -1, -1)  # noqa: E731
+        out_m, den_m = self._ace_with_denom(pack(K), pack(V), pack(Q))
+        out = merge_heads(out_m, self.reference_head_merge)
+        d_race_token = den_m.mean(dim=0).mean(dim=-1, keepdim=True).clamp_min(1e-6)
+        return self.drop(self.out(out)), d_race_token
 
 
 class RACEBlock(nn.Module):

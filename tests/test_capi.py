@@ -183,3 +183,20 @@ def test_global_null_den_and_workspace_rejected():
     need = lib.race_bwd_global_workspace_bytes(ctypes.byref(d))
     rc = lib.race_bwd_global(ctypes.byref(d), p, p, p, p, p, p, p, None, p, p, p, p, None, p, need - 1, None)
     assert rc == -3 and "workspace" in _lib.last_error()
+
+
+# ------------------------------------------------- key weights and den (F1 extras)
+def test_ex_rejects_causal_extras_and_checks_pointers():
+    lib = _lib.load()
+    d = _desc(T=64)        # causal
+    p = ctypes.c_void_p(256)
+    rc = lib.race_fwd_ex(ctypes.byref(d), p, p, p, p, p, p, None, p, p, 1 << 30, None)
+    assert rc == -2 and "non-causal" in _lib.last_error()
+    rc = lib.race_bwd_ex(ctypes.byref(d), p, p, p, p, None, p, p, p, p, p, p, None, p, 1 << 30, None)
+    assert rc == -2 and "non-causal" in _lib.last_error()
+    d = _desc(T=64, causal=0)
+    rc = lib.race_fwd_ex(ctypes.byref(d), p, p, p, p, ctypes.c_void_p(258), p, None, p, p, 1 << 30, None)
+    assert rc == -1 and "kmask is not 4-byte aligned" in _lib.last_error()
+    assert lib.race_fwd_ex_workspace_bytes(ctypes.byref(d)) == lib.race_fwd_workspace_bytes(ctypes.byref(d))
+    rc = lib.race_fwd_ex(ctypes.byref(d), p, p, p, p, None, p, p, p, p, 16, None)
+    assert rc == -3 and "workspace" in _lib.last_error()
