@@ -116,6 +116,22 @@ int race_bwd_ex(const race_desc *d, const void *q, const void *k, const void *v,
                 void *stream);
 
 /* ---------------------------------------------------------------------
+ * Bucket probabilities as an output, for the hybrid consumers that read
+ * them (race_bucket_probs_from_qk, misc/arxiv_64K.py:1580-1644;
+ * race_avg_bucket_probs_from_x, misc/vit.py:3193-3262):
+ *   P[n][t][l*2^K + r] = softmax_r(sum_k c[r,k] tanh(<x_t, plane_{l,k}>) inv_temp),
+ * fp32 [M*B*H][T][L*2^K] contiguous (stream-major), from one input x read
+ * with d->q_stride (d->causal is not used).  race_probs_bwd turns dP into dx
+ * (d->g_stride) and grad_inv_temp (nullable, device fp32 scalar).
+ * --------------------------------------------------------------------- */
+size_t race_probs_bwd_workspace_bytes(const race_desc *d);
+int race_probs(const race_desc *d, const void *x, const float *planes, float *P,
+               void *stream);
+int race_probs_bwd(const race_desc *d, const void *x, const float *planes,
+                   const float *dP, void *dx, float *grad_inv_temp, void *ws,
+                   size_t ws_bytes, void *stream);
+
+/* ---------------------------------------------------------------------
  * Global normalisation ("F2", causal only): one normaliser per token
  * instead of one per bucket, the readout of CausalRACEAttention
  * (misc/elsaa_causal_complete.py:438-586) and of its Triton kernel

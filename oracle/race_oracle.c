@@ -750,3 +750,63 @@ int oracle_race_backward_ex(const double *q, const double *k, const double *v,
     free(pabs);
     return 0;
 }
+
+/* ------------------------------------------------ bucket probabilities
+ * P[n][t][s] of one input (misc/arxiv_64K.py:1580-1644,
+ * misc/vit.py:3193-3262: projection, tanh, /temperature, corner logits,
+ * softmax per table) and the backward dP -> dx, d inv_temp. */
+int oracle_race_probs(const double *x, const double *planes, const int64_t *plane_of,
+                      int64_t N, int64_t T, int64_t D, int L, int K, double inv_temp,
+                      double *P)
+{
+    if (K < 1 || K > ORACLE_MAX_K || L < 1 || N < 0 || T < 0 || D < 1)
+        return -1;
+    const int64_t S = (int64_t)L << K;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t n = 0; n < N; ++n) {
+        const double *pl = planes + plane_of[n] * (int64_t)L * K * D;
+        double *th = malloc(sizeof(double) * (size_t)(L * K));
+        for (int64_t t = 0; t < T; ++t)
+            soft_hash(x + (n * T + t) * D, pl, D, L, K, inv_temp, th, P + (n * T + t) * S);
+        free(th);
+    }
+    return 0;
+}
+
+int oracle_race_probs_bwd(const double *x, const double *dP, const double *planes,
+                          const int64_t *plane_of, int64_t N, int64_t T, int64_t D, int L,
+                          int K, double inv_temp, double *dx, double *grad_inv_temp,
+                          double *grad_inv_temp_l1)
+{
+    if (K < 1 || K > ORACLE_MAX_K || L < 1 || N < 0 || T < 0 || D < 1)
+        return -1;
+    const int64_t S = (int64_t)L << K;
+    double *part = calloc((size_t)(N > 0 ? N : 1), sizeof(double));
+    double *pabs = calloc((size_t)(N > 0 ? N : 1), sizeof(double));
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t n = 0; n < N; ++n) {
+        const double *pl = planes + plane_of[n] * (int64_t)L * K * D;
+        double *th = malloc(sizeof(double) * (size_t)(L * K));
+        double *P = malloc(sizeof(double) * (size_t)S);
+        for (int64_t t = 0; t < T; ++t) {
+            double *dxt = dx + (n * T + t) * D;
+            memset(dxt, 0, sizeof(double) * (size_t)D);
+            soft_hash(x + (n * T + t) * D, pl, D, L, K, inv_temp, th, P);
+            soft_hash_bwd(P, th, dP + (n * T + t) * S, pl, D, L, K, inv_temp, dxt, &part[n], &pabs[n]);
+        }
+        free(th);
+        free(P);
+    }
+    double tot = 0.0, tabs = 0.0;
+    for (int64_t n = 0; n < N; ++n) {
+        tot += part[n];
+        tabs += pabs[n];
+    }
+    if (grad_inv_temp)
+        *grad_inv_temp = tot;
+    if (grad_inv_temp_l1)
+        *grad_inv_temp_l1 = tabs;
+    free(part);
+    free(pabs);
+    return 0;
+}

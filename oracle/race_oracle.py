@@ -13,6 +13,8 @@ Two layers:
   * ``race_forward_ex`` / ``race_backward_ex``: F1 with per-token key
     weights (the padding mask, misc/classification.py:576-592) and the den
     output of misc/classification.py:641-659 and misc/vit.py:1452-1510.
+  * ``race_probs`` / ``race_probs_bwd``: the bucket probabilities of one
+    input and their backward (misc/arxiv_64K.py:1580-1644, misc/vit.py:3193-3262).
   * ``race_global_forward`` / ``race_global_backward``: the same C file's
     restatement of the globally normalised causal mode ("F2",
     misc/elsaa_causal_complete.py:438-586, misc/race_kernel.py:8-124).
@@ -70,6 +72,10 @@ def _lib():
         lib.oracle_race_backward_ex.argtypes = [dp, dp, dp, dp, dp, dp, dp, ip, i64, i64, i64, ci, ci, ci, cd, cd,
                                                 dp, dp, dp, dp, dp]
         lib.oracle_race_backward_ex.restype = ci
+        lib.oracle_race_probs.argtypes = [dp, dp, ip, i64, i64, i64, ci, ci, cd, dp]
+        lib.oracle_race_probs.restype = ci
+        lib.oracle_race_probs_bwd.argtypes = [dp, dp, dp, ip, i64, i64, i64, ci, ci, cd, dp, dp, dp]
+        lib.oracle_race_probs_bwd.restype = ci
         lib.oracle_prefix_mean_flat.argtypes = [fp, fp, i64, i64, i64, cd, fp]
         lib.oracle_prefix_mean_flat.restype = None
         lib.oracle_prefix_mean_flat_bw.argtypes = [fp, fp, fp, i64, i64, i64, cd, fp, fp]
@@ -197,6 +203,41 @@ def race_backward_ex(q, k, v, dout, planes, *, kmask=None, dden=None, causal: bo
     if rc != 0:
         raise ValueError("oracle_race_backward_ex rejected its arguments")
     res = (from_streams(dq, M, B, H), from_streams(dk, M, B, H), from_streams(dv, M, B, H), float(git[0]))
+    return res + (float(git[1]),) if with_l1 else res
+
+
+def race_probs(x, planes, *, inv_temp: float):
+    """fp64 bucket probabilities of x [M,B,T,H,D] -> [M,B,H,T,L*2^K]."""
+    M, B, T, H, D = x.shape
+    planes = np.ascontiguousarray(np.asarray(planes, dtype=np.float64))
+    NP, L, K, _ = planes.shape
+    xs = to_streams(x)
+    pm = _plane_map(M, B, H, NP)
+    P = np.zeros((xs.shape[0], T, L << K), dtype=np.float64)
+    rc = _lib().oracle_race_probs(_dptr(xs), _dptr(planes), pm.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                  xs.shape[0], T, D, L, K, float(inv_temp), _dptr(P))
+    if rc != 0:
+        raise ValueError("oracle_race_probs rejected its arguments")
+    return P.reshape(M, B, H, T, L << K)
+
+
+def race_probs_bwd(x, dP, planes, *, inv_temp: float, with_l1: bool = False):
+    """fp64 backward of race_probs: dP [M,B,H,T,S] -> (dx [M,B,T,H,D],
+    grad_inv_temp[, l1])."""
+    M, B, T, H, D = x.shape
+    planes = np.ascontiguousarray(np.asarray(planes, dtype=np.float64))
+    NP, L, K, _ = planes.shape
+    xs = to_streams(x)
+    dPs = np.ascontiguousarray(np.asarray(dP, dtype=np.float64).reshape(M * B * H, T, L << K))
+    pm = _plane_map(M, B, H, NP)
+    dx = np.zeros_like(xs)
+    git = np.zeros(2, dtype=np.float64)
+    rc = _lib().oracle_race_probs_bwd(_dptr(xs), _dptr(dPs), _dptr(planes),
+                                      pm.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), xs.shape[0], T, D, L, K,
+                                      float(inv_temp), _dptr(dx), _dptr(git), _dptr(git[1:]))
+    if rc != 0:
+        raise ValueError("oracle_race_probs_bwd rejected its arguments")
+    res = (from_streams(dx, M, B, H), float(git[0]))
     return res + (float(git[1]),) if with_l1 else res
 
 

@@ -40,6 +40,7 @@ EXPORTS = (
     "race_state_bytes", "race_fwd_workspace_bytes", "race_bwd_workspace_bytes",
     "race_fwd", "race_bwd",
     "race_fwd_ex_workspace_bytes", "race_fwd_ex", "race_bwd_ex",
+    "race_probs_bwd_workspace_bytes", "race_probs", "race_probs_bwd",
     "race_fwd_global_workspace_bytes", "race_bwd_global_workspace_bytes", "race_fwd_global", "race_bwd_global",
     "race_prefix_mean_workspace_bytes", "race_prefix_mean_fwd", "race_prefix_mean_bwd",
     "race_last_error", "race_abi_version",
@@ -66,6 +67,7 @@ def load():
         vp, sz, i64, dbl = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int64, ctypes.c_double
         dp = ctypes.POINTER(RaceDesc)
         for name in ("race_state_bytes", "race_fwd_workspace_bytes", "race_bwd_workspace_bytes", "race_fwd_ex_workspace_bytes",
+                     "race_probs_bwd_workspace_bytes",
                      "race_fwd_global_workspace_bytes", "race_bwd_global_workspace_bytes"):
             getattr(lib, name).argtypes = [dp]
             getattr(lib, name).restype = sz
@@ -73,6 +75,10 @@ def load():
         lib.race_fwd.restype = ctypes.c_int
         lib.race_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
         lib.race_bwd.restype = ctypes.c_int
+        lib.race_probs.argtypes = [dp, vp, vp, vp, vp]
+        lib.race_probs.restype = ctypes.c_int
+        lib.race_probs_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, sz, vp]
+        lib.race_probs_bwd.restype = ctypes.c_int
         lib.race_fwd_ex.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
         lib.race_fwd_ex.restype = ctypes.c_int
         lib.race_bwd_ex.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]

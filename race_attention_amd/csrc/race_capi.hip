@@ -311,6 +311,32 @@ template <typename T> int gn_bwd_dispatch(const race_desc *d, const Plan &p, con
     return fail(RACE_E_UNSUPPORTED, "bucket count / hash bits combination not compiled");
 }
 
+// Bucket probabilities (forward) and dP -> dx (backward)
+template <typename T, int SP, int KB> int probs_impl(const race_desc *d, const Plan &p, Args a, bool bwd,
+                                                     float *grad_inv_temp, hipStream_t s) {
+    const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
+    if (!bwd) {
+        k_probs<T, SP, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
+        return launched("race_probs");
+    }
+    k_probs<T, SP, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
+    if (sliced<T, KB>()) slice_sum<T>(p, d, a.dqpart, d->g_stride, a.dq, s);
+    if (grad_inv_temp) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, p.N * p.nseg * p.nslice, grad_inv_temp);
+    return launched("race_probs_bwd");
+}
+
+template <typename T>
+int probs_dispatch(const race_desc *d, const Plan &p, const Args &a, bool bwd, float *git, hipStream_t s) {
+#define X(TT_, SP_, KB_)                                                                                             \
+    if (std::is_same<T, TT_>::value && p.SP == SP_ && d->K == KB_) return probs_impl<TT_, SP_, KB_>(d, p, a, bwd, git, s);
+    RACE_FOR_COMBOS(X)
+#undef X
+    return fail(RACE_E_UNSUPPORTED, "bucket count / hash bits combination not compiled");
+}
+
+// workspace of race_probs_bwd: temperature partials, then fp32 dx partials (sliced)
+size_t probs_ws_core(const Plan &p) { return align16((size_t)p.N * p.nseg * p.nslice * sizeof(float)); }
+
 int check_gn(const race_desc *d) {
     if (d->causal != 1)
         return fail(RACE_E_UNSUPPORTED, "global normalisation is implemented for the causal operator only");
@@ -441,6 +467,47 @@ int race_bwd(const race_desc *d, const void *q, const void *k, const void *v, co
     hipStream_t s = (hipStream_t)stream;
     if (d->dtype == RACE_DTYPE_BF16) return bwd_dispatch<bf16>(d, p, a, grad_inv_temp, s);
     return bwd_dispatch<float>(d, p, a, grad_inv_temp, s);
+}
+
+size_t race_probs_bwd_workspace_bytes(const race_desc *d) {
+    Plan p;
+    if (make_plan(d, p) != RACE_OK) return 0;
+    ok();
+    return probs_ws_core(p) + p.part_bytes;
+}
+
+int race_probs(const race_desc *d, const void *x, const float *planes, float *P, void *stream) {
+    Plan p;
+    int rc = make_plan(d, p);
+    if (rc || (rc = check_tensor("x", x, d->q_stride, p.esize, d->T)) || (rc = check_den("P", P))) return rc;
+    if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
+    Args a = base_args(d, p, planes);
+    a.q = x;
+    a.probs = P;
+    hipStream_t s = (hipStream_t)stream;
+    if (d->dtype == RACE_DTYPE_BF16) return probs_dispatch<bf16>(d, p, a, false, nullptr, s);
+    return probs_dispatch<float>(d, p, a, false, nullptr, s);
+}
+
+int race_probs_bwd(const race_desc *d, const void *x, const float *planes, const float *dP, void *dx,
+                   float *grad_inv_temp, void *ws, size_t ws_bytes, void *stream) {
+    Plan p;
+    int rc = make_plan(d, p);
+    if (rc || (rc = check_tensor("x", x, d->q_stride, p.esize, d->T)) || (rc = check_den("dP", dP)) ||
+        (rc = check_tensor("dx", dx, d->g_stride, p.esize, d->T)))
+        return rc;
+    if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
+    const size_t need = probs_ws_core(p) + p.part_bytes;
+    if (!ws || ws_bytes < need) return fail(RACE_E_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, need);
+    Args a = base_args(d, p, planes);
+    a.q = x;
+    a.dq = dx;
+    a.dprobs = dP;
+    a.tpart = (float *)ws;
+    a.dqpart = p.parts ? (float *)((char *)ws + probs_ws_core(p)) : nullptr;
+    hipStream_t s = (hipStream_t)stream;
+    if (d->dtype == RACE_DTYPE_BF16) return probs_dispatch<bf16>(d, p, a, true, grad_inv_temp, s);
+    return probs_dispatch<float>(d, p, a, true, grad_inv_temp, s);
 }
 
 size_t race_fwd_ex_workspace_bytes(const race_desc *d) {

@@ -75,6 +75,10 @@ struct Args {
     // per-token key weights [B][T] on P_K (non-causal padding mask; nullable).
     // Non-causal F1 also writes den [N][T] when den is set and reads dden.
     const float *kw;
+    // bucket probabilities as an output: probs [N][T][S] fp32 (k_probs) and
+    // their upstream gradient dprobs (k_probs_bwd; x in q, dx in dq)
+    float *probs;
+    const float *dprobs;
 };
 
 constexpr int SROW = D + 1;  // state row: D values of B (or U) then A (or alpha)
@@ -1913,6 +1917,124 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     }
     const float ts = block_sum<NTH>(tsum, sRed);
     if (threadIdx.x == 0) a.tpart[((int64_t)(a.M * a.B * a.H + n) * a.nseg + seg) * a.nslice + z] = ts;
+}
+
+// =====================================================================
+// Bucket probabilities as an output (for hybrid consumers): P[n][t][s],
+// s = l*2^K + r, fp32, from one input x (q's pointer and strides); and the
+// backward dP -> dx (dq's pointer and strides; sliced instantiations write
+// fp32 partials) with the temperature-gradient partials.
+// =====================================================================
+template <typename T, int SP> struct ProbsL {
+    static constexpr int NW_ = SP / WB;
+    static constexpr int LDN = NatL<T, true>::LD, LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>();
+    static constexpr size_t oX = 0;
+    static constexpr size_t oPl = align16(oX + sizeof(T) * TT * LDN);
+    static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
+    static constexpr size_t oPlT = align16(oPlLo + sizeof(T) * NCOL * LDN);
+    static constexpr size_t oDproj = align16(oPlT + sizeof(T) * D * LDDP);
+    static constexpr size_t oSig = align16(oDproj + sizeof(T) * TT * LDDP);  // sp, sm, th
+    static constexpr size_t oRed = align16(oSig + sizeof(float) * 3 * TT * LDC);
+    static constexpr size_t oHash = align16(oRed + sizeof(float) * 64 * NW_);
+    static constexpr size_t oShare = align16(oHash + HashOps<T, 4>::bytes);
+    template <int KB> static constexpr size_t bytes() {
+        return align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
+    }
+};
+
+// the lane's 4 buckets (s0 .. s0+3) of token row p (S fp32 per row)
+__device__ __forceinline__ void store_row4(float *row, int s0, int S, const f32x4 &v) {
+    if ((S & 3) == 0) {
+        if (s0 < S) *reinterpret_cast<f32x4 *>(row + s0) = v;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (s0 + e < S) row[s0 + e] = v[e];
+    }
+}
+__device__ __forceinline__ f32x4 load_row4(const float *row, int s0, int S) {
+    f32x4 v = zero4();
+    if ((S & 3) == 0) {
+        if (s0 < S) v = *reinterpret_cast<const f32x4 *>(row + s0);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (s0 + e < S) v[e] = row[s0 + e];
+    }
+    return v;
+}
+
+template <typename T, int SP, int KB, bool BWD>
+__global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
+    using Ly = ProbsL<T, SP>;
+    using NL = NatL<T, true>;
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDC = Ly::LDC, LDDP = Ly::LDDP;
+    __shared__ __align__(16) unsigned char smem[Ly::template bytes<KB>()];
+    T *sX = (T *)(smem + Ly::oX), *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
+    T *sPlT = (T *)(smem + Ly::oPlT), *sDproj = (T *)(smem + Ly::oDproj);
+    float *sSp = (float *)(smem + Ly::oSig), *sSm = sSp + TT * LDC, *sTh = sSp + 2 * TT * LDC;
+    float *sRed = (float *)(smem + Ly::oRed), *sShare = (float *)(smem + Ly::oShare);
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
+              sg = z * SP + sw;
+    const int n = blockIdx.y, seg = blockIdx.x;
+    const int m = n / (a.B * a.H);
+    const int64_t ntiles = (a.T + TT - 1) / TT;
+    const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
+    const T *xp = (const T *)a.q + stream_off(a.sq, n, a.B, a.H);
+    T *dxp = BWD ? (T *)a.dq + stream_off(a.sg, n, a.B, a.H) : nullptr;
+    float *xpart = BWD && sliced<T, KB>() ? a.dqpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
+
+    HashOps<T, KB> ho;
+    WideHash<T, KB> wh;
+    if constexpr (BWD) {
+        if constexpr (KB <= 4)
+            ho.init((T *)(smem + Ly::oHash), NTH);
+        else
+            wh.init(sg);
+        zero_lds<T>(sDproj, TT * LDDP, NTH);
+    }
+    load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr,
+                            BWD ? sPlT : nullptr);
+    float tsum = 0.f;
+    Prefetch<T, NTH> px_;
+    for (int64_t jt = j0; jt < j1; ++jt) {
+        const int64_t t0 = jt * TT;
+        px_.issue(xp, a.sq.t, t0, a.T);
+        __syncthreads();  // the previous tile's readers of sX, sSig, sDproj are done
+        px_.template commit<NL>(sX, nullptr);
+        __syncthreads();
+        for (int q = w; q < 4; q += NW_)
+            project_tile<T, NL>(sX, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, BWD ? sTh : nullptr);
+        __syncthreads();
+        f32x4 P[2];
+        probs_st<KB>(sSp, sSm, sg, a.S, t0, a.T, P);
+        const int s0 = sg + 4 * g;
+        if constexpr (!BWD) {
+            for (int nt = 0; nt < 2; ++nt) {
+                const int64_t t = t0 + 16 * nt + i;
+                if (t < a.T) store_row4(a.probs + ((int64_t)n * a.T + t) * a.S, s0, a.S, P[nt]);
+            }
+        } else {
+            f32x4 dP[2];
+            for (int nt = 0; nt < 2; ++nt) {
+                const int64_t t = t0 + 16 * nt + i;
+                dP[nt] = t < a.T ? load_row4(a.dprobs + ((int64_t)n * a.T + t) * a.S, s0, a.S) : zero4();
+            }
+            if constexpr (KB <= 4) {
+                tsum += softhash_bwd<KB, T>(P, dP, sSp, sSm, sTh, sg, a.L, a.inv_temp, sDproj, ho);
+            } else {
+                softhash_share<KB, T>(P, dP, wh, sShare);
+                __syncthreads();
+                tsum += softhash_combine<KB, T, SP, NTH>(sShare, sSp, sSm, sTh, z, a.L, a.inv_temp, sDproj);
+            }
+            __syncthreads();
+            dx_store<T, NW_>(sDproj, sPlT, dxp, a.sg.t, t0, a.T, xpart);
+        }
+    }
+    if constexpr (BWD) {
+        const float ts = block_sum<NTH>(tsum, sRed);
+        if (threadIdx.x == 0) a.tpart[((int64_t)n * a.nseg + seg) * a.nslice + z] = ts;
+    }
 }
 
 // Sum of the per-slice fp32 partials [nslice][N][T][D] in slice order,

@@ -181,6 +181,78 @@ def race_attention(Qhf, Khf, Vhf, planes, *, L, K, causal, inv_temp, eps=1e-6):
     return RACEFunction.apply(Qhf, Khf, Vhf, planes, inv_temp, L, K, causal, eps)
 
 
+# ------------------------------------------------- bucket probabilities as an output
+def _probs_desc(x, planes, L, K, inv_temp):
+    if x.dim() != 5:
+        raise ValueError(f"expected x [M,B,T,H,D], got {tuple(x.shape)}")
+    if planes.shape[-3:] != (L, K, x.shape[-1]):
+        raise ValueError(f"planes trailing shape {tuple(planes.shape[-3:])} != (L, K, D)")
+    return make_desc(x, x, x, planes, L=L, K=K, causal=False, eps=1e-6, inv_temp=inv_temp)
+
+
+def race_probs_raw(x, planes, *, L, K, inv_temp):
+    """Bucket probabilities of x [M,B,T,H,D]: fp32 [M,B,H,T,L*2^K]."""
+    _require_gpu(x, planes)
+    x = _aligned(x)
+    planes = planes.to(device=x.device, dtype=torch.float32).contiguous()
+    M, B, T, H, _ = x.shape
+    lib = _lib.load()
+    d = _probs_desc(x, planes, L, K, inv_temp)
+    P = torch.empty((M, B, H, T, L << K), dtype=torch.float32, device=x.device)
+    _lib.check(lib.race_probs(ctypes.byref(d), _ptr(x), _ptr(planes), _ptr(P), _stream()), "race_probs")
+    return P
+
+
+def race_probs_bwd_raw(x, planes, dP, *, L, K, inv_temp, want_temp_grad=True):
+    """dP [M,B,H,T,S] -> (dx [M,B,T,H,D], grad_inv_temp or None)."""
+    _require_gpu(x, planes, dP)
+    x = _aligned(x)
+    planes = planes.to(device=x.device, dtype=torch.float32).contiguous()
+    M, B, T, H, _ = x.shape
+    if dP.shape != (M, B, H, T, L << K):
+        raise ValueError(f"dP must be [M,B,H,T,S] = {(M, B, H, T, L << K)}; got {tuple(dP.shape)}")
+    dP = dP.to(torch.float32).contiguous()
+    lib = _lib.load()
+    d = _probs_desc(x, planes, L, K, inv_temp)
+    dx = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    d.g_stride = _strides4(dx)
+    ws = torch.empty(max(lib.race_probs_bwd_workspace_bytes(ctypes.byref(d)), 16), dtype=torch.uint8, device=x.device)
+    git = torch.empty((), dtype=torch.float32, device=x.device) if want_temp_grad else None
+    rc = lib.race_probs_bwd(ctypes.byref(d), _ptr(x), _ptr(planes), _ptr(dP), _ptr(dx),
+                            _ptr(git) if git is not None else None, _ptr(ws), ctypes.c_size_t(ws.numel()), _stream())
+    _lib.check(rc, "race_probs_bwd")
+    return dx, git
+
+
+class RACEProbsFunction(torch.autograd.Function):
+    """Bucket probabilities as a differentiable output:
+    forward(x, planes, inv_temp, L, K) -> P [M,B,H,T,L*2^K] fp32; x and
+    inv_temp (a 0-dim tensor) receive gradients."""
+
+    @staticmethod
+    def forward(ctx, x, planes, inv_temp, L, K):
+        it = float(inv_temp)
+        P = race_probs_raw(x, planes, L=L, K=K, inv_temp=it)
+        ctx.save_for_backward(x, planes)
+        ctx.cfg = (L, K, it, torch.is_tensor(inv_temp))
+        return P
+
+    @staticmethod
+    def backward(ctx, dP):
+        x, planes = ctx.saved_tensors
+        L, K, it, is_t = ctx.cfg
+        want = is_t and ctx.needs_input_grad[2]
+        dx, git = race_probs_bwd_raw(x, planes, dP, L=L, K=K, inv_temp=it, want_temp_grad=want)
+        return (dx if ctx.needs_input_grad[0] else None, None, git if want else None, None, None)
+
+
+def race_bucket_probs(x, planes, *, L, K, inv_temp):
+    """Soft bucket probabilities of x [M,B,T,H,D] -> [M,B,H,T,L,2^K] fp32
+    (differentiable in x and a tensor inv_temp)."""
+    M, B, T, H, _ = x.shape
+    return RACEProbsFunction.apply(x, planes, inv_temp, L, K).view(M, B, H, T, L, 1 << K)
+
+
 # ------------------------------------------------- key weights and den (F1 extras)
 def _kmask_check(kmask, B, T, dev):
     if kmask is None:

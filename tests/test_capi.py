@@ -200,3 +200,15 @@ def test_ex_rejects_causal_extras_and_checks_pointers():
     assert lib.race_fwd_ex_workspace_bytes(ctypes.byref(d)) == lib.race_fwd_workspace_bytes(ctypes.byref(d))
     rc = lib.race_fwd_ex(ctypes.byref(d), p, p, p, p, None, p, p, p, p, 16, None)
     assert rc == -3 and "workspace" in _lib.last_error()
+
+
+def test_probs_argument_checks():
+    lib = _lib.load()
+    d = _desc(T=64)
+    p = ctypes.c_void_p(256)
+    assert lib.race_probs(ctypes.byref(d), None, p, p, None) == -1 and "x is NULL" in _lib.last_error()
+    assert lib.race_probs(ctypes.byref(d), p, p, None, None) == -1 and "P is NULL" in _lib.last_error()
+    need = lib.race_probs_bwd_workspace_bytes(ctypes.byref(d))
+    assert need == 8 * 2 * 4      # temperature partials: 8 streams x 2 segments (2 tiles), no slices
+    rc = lib.race_probs_bwd(ctypes.byref(d), p, p, p, p, None, p, need - 1, None)
+    assert rc == -3 and "workspace" in _lib.last_error()
