@@ -25,6 +25,10 @@ estimators with independent hyperplanes over Q/K/V expanded with stride 0,
 B=8, 12 heads, N=8192, d=64, bf16): 1024 buckets run as 8 bucket slices.
 The default (c4) line is the headline metric.
 
+--mode probs times the bucket probabilities as an output (race_probs +
+race_probs_bwd of Q, fp32 P [H,T,L*2^K] per step): HBM-bound, so its line
+reports GB/s of the compulsory bytes (read x, write P; read x and dP, write dx).
+
 --mode global times the globally normalised causal mode (CausalRACEAttention,
 misc/elsaa_causal_complete.py:438-586) on the same workload with beta = 1:
 race_fwd_global + race_bwd_global (the backward's first phase also runs the
@@ -70,8 +74,9 @@ def parse():
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="finish with a device-to-device copy of MIB MiB (PMC calibration)")
     ap.add_argument("--workload", choices=("c4", "c5"), default="c4")
-    ap.add_argument("--mode", choices=("f1", "global"), default="f1",
-                    help="f1: per-bucket normalisation (headline); global: one normaliser per token")
+    ap.add_argument("--mode", choices=("f1", "global", "probs"), default="f1",
+                    help="f1: per-bucket normalisation (headline); global: one normaliser per token; "
+                         "probs: the bucket probabilities of Q as an output, forward + backward")
     return ap.parse_args()
 
 
@@ -169,6 +174,74 @@ class GlobalStep(Step):
         if which in ("both", "bwd"):
             self.check(self.lib.race_bwd_global(ctypes.byref(self.d), *self.bargs, st), "race_bwd_global")
         self.d.phases = 0
+
+
+class ProbsStep:
+    """One race_probs + race_probs_bwd of x = Q (inv_temp 1/sqrt(d))."""
+
+    def __init__(self, q, planes, L, K):
+        import torch
+        from race_attention_amd import _lib
+        from race_attention_amd.functional import _probs_desc, _strides4
+        self.lib, self.check = _lib.load(), _lib.check
+        M, B, T, H, D = q.shape
+        self.planes = planes.float().contiguous()
+        self.d = _probs_desc(q, self.planes, L, K, 1.0 / math.sqrt(D))
+        self.P = torch.empty((M, B, H, T, L << K), dtype=torch.float32, device=q.device)
+        self.dP = torch.randn(self.P.shape, generator=torch.Generator(device=q.device).manual_seed(7),
+                              device=q.device)
+        self.dx = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        self.d.g_stride = _strides4(self.dx)
+        self.ws = torch.empty(max(self.lib.race_probs_bwd_workspace_bytes(ctypes.byref(self.d)), 16),
+                              dtype=torch.uint8, device=q.device)
+        self.git = torch.empty((), dtype=torch.float32, device=q.device)
+        P_ = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        self.fargs = (P_(q), P_(self.planes), P_(self.P))
+        self.bargs = (P_(q), P_(self.planes), P_(self.dP), P_(self.dx), P_(self.git), P_(self.ws),
+                      ctypes.c_size_t(self.ws.numel()))
+
+    def run(self, phases=0, which="both"):
+        import torch
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        if which in ("both", "fwd"):
+            self.check(self.lib.race_probs(ctypes.byref(self.d), *self.fargs, st), "race_probs")
+        if which in ("both", "bwd"):
+            self.check(self.lib.race_probs_bwd(ctypes.byref(self.d), *self.bargs, st), "race_probs_bwd")
+
+
+def probs_main(args, q, planes, L, K, wl, T, B, H, D, M):
+    """--mode probs: the two probability kernels, each timed with HIP events."""
+    import torch
+    step = ProbsStep(q, planes, L, K)
+    for _ in range(args.warmup):
+        step.run()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        ev[s][0].record()
+        step.run(which="fwd")
+        ev[s][1].record()
+        step.run(which="bwd")
+        ev[s][2].record()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    fwd = statistics.mean(ev[s][0].elapsed_time(ev[s][1]) for s in range(args.steps))
+    bwd = statistics.mean(ev[s][1].elapsed_time(ev[s][2]) for s in range(args.steps))
+    th = M * B * T * H
+    S = L << K
+    fb, bb = th * (D * 2 + S * 4), th * (D * 2 + S * 4 + D * 2)
+    res = {"metric": "bucket probabilities fwd+bwd tokens/s (HBM-bound)", "value": round(B * T / (ms / 1e3), 1),
+           "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16 in, fp32 P",
+           "data": "synthetic (unit-L2 N(0,1) Q, N(0,1) dP and hyperplanes)",
+           "config": {"workload": f"{wl}, bucket probabilities of Q: B={B} H={H} N={T} d={D} K={K} L={L} M={M}"},
+           "kernels": {"probs": {"ms": round(fwd, 4), "algorithmic_GBs": round(fb / (fwd * 1e-3) / 1e9, 1)},
+                       "probs_bwd": {"ms": round(bwd, 4), "algorithmic_GBs": round(bb / (bwd * 1e-3) / 1e9, 1)}},
+           "roofline": {"bound": "hbm", "kernel": "probs_bwd", "achieved": round(bb / (bwd * 1e-3) / 1e9, 1),
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(bb / (bwd * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "traffic": None}}
+    print(json.dumps(res), flush=True)
 
 
 def cpu_baseline_global(sample_T, H, D=64, L=8, K=4, reps=3):
@@ -311,6 +384,8 @@ def main():
         wl += ", global normalisation (F2, beta=1)"
     print(f"bench: generating inputs M={M} B={B} T={T} H={H} D={D} L={L} K={K}", file=sys.stderr, flush=True)
     q, k, v, do, planes = make_inputs(B, T, H, D, L, K, dev, M=M)
+    if args.mode == "probs":
+        return probs_main(args, q, planes, L, K, wl, T, B, H, D, M)
     step = (GlobalStep if args.mode == "global" else Step)(q, k, v, do, planes, L, K)
     for _ in range(args.warmup):
         step.run()

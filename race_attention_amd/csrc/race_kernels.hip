@@ -1997,11 +1997,12 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
                             BWD ? sPlT : nullptr);
     float tsum = 0.f;
     Prefetch<T, NTH> px_;
+    if (j0 < j1) px_.issue(xp, a.sq.t, j0 * TT, a.T);
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
-        px_.issue(xp, a.sq.t, t0, a.T);
         __syncthreads();  // the previous tile's readers of sX, sSig, sDproj are done
         px_.template commit<NL>(sX, nullptr);
+        if (jt + 1 < j1) px_.issue(xp, a.sq.t, t0 + TT, a.T);  // next tile, in flight during this one
         __syncthreads();
         for (int q = w; q < 4; q += NW_)
             project_tile<T, NL>(sX, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, BWD ? sTh : nullptr);
