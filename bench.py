@@ -35,6 +35,14 @@ race_fwd_global + race_bwd_global (the backward's first phase also runs the
 per-token prologue kernel).  Its CPU baseline is the fp64 C restatement under
 oracle/ (the reference's F2 CPU path is aten einsums), on a bounded sample.
 
+--workload c3-step / c5-step time one full training step of the models of
+BASELINE configs[2] and configs[4] with RACE blocks (forward, backward,
+AdamW; bf16 autocast over fp32 weights): the ViT encoder (6 layers, d=384,
+6 heads, MLP 1536, non-causal K=2 L=5 M=1, batch 64 x 785 tokens of 28x28
+images, 10 classes) and the GPT decoder (12 layers, d=768, 12 heads, MLP
+3072, vocab 50257, causal K=8 L=4 M=2, batch 8 x 8192 token ids).  Value is
+tokens/s of the step.
+
 --copy-calib MIB ends the run with one device-to-device copy of MIB MiB, the
 known-size kernel against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters
 are scaled when the HBM traffic of the operator's kernels is measured.
@@ -73,7 +81,7 @@ def parse():
     ap.add_argument("--max-n", action="store_true", help="also bisect the longest sequence that fits in HBM")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="finish with a device-to-device copy of MIB MiB (PMC calibration)")
-    ap.add_argument("--workload", choices=("c4", "c5"), default="c4")
+    ap.add_argument("--workload", choices=("c4", "c5", "c3-step", "c5-step"), default="c4")
     ap.add_argument("--mode", choices=("f1", "global", "probs"), default="f1",
                     help="f1: per-bucket normalisation (headline); global: one normaliser per token; "
                          "probs: the bucket probabilities of Q as an output, forward + backward")
@@ -244,6 +252,62 @@ def probs_main(args, q, planes, L, K, wl, T, B, H, D, M):
     print(json.dumps(res), flush=True)
 
 
+def model_step_main(args):
+    """--workload c3-step / c5-step: one training step of the full model."""
+    import torch
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    if args.workload == "c3-step":
+        from race_attention_amd.vit import VisionTransformer
+        cfg = dict(img_size=28, patch_size=1, num_channels=1, embed_dim=384, num_heads=6, transformer_units=6,
+                   drop_rate=0.1, qkv_bias=False, K=2, L=5, M=1, num_classes=10)
+        model = VisionTransformer(cfg).to(dev)
+        B, T = 64, 28 * 28 + 1
+        x = torch.randn(B, 1, 28, 28, device=dev)
+        y = torch.randint(0, 10, (B,), device=dev)
+        loss_fn = lambda out: torch.nn.functional.cross_entropy(out.float(), y)  # noqa: E731
+        wl = "C3 ViT training step (6 RACE blocks, d=384, 6 heads, K=2 L=5 M=1, non-causal), AdamW"
+    else:
+        from race_attention_amd.lm import LMModel
+        cfg = dict(vocab_size=50257, context_length=8192, emb_dim=768, n_heads=12, n_layers=12, drop_rate=0.1,
+                   qkv_bias=False, K=8, L=4, M=2)
+        model = LMModel(cfg).to(dev)
+        B, T = 8, 8192
+        x = torch.randint(0, 50257, (B, T), device=dev)
+        y = torch.randint(0, 50257, (B, T), device=dev)
+        loss_fn = lambda out: torch.nn.functional.cross_entropy(out.flatten(0, 1), y.flatten())  # noqa: E731
+        wl = "C5 GPT training step (12 causal RACE blocks, d=768, 12 heads, K=8 L=4 M=2, vocab 50257), AdamW"
+    opt = torch.optim.AdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1)
+    print(f"bench: {wl}: {sum(p.numel() for p in model.parameters())} parameters", file=sys.stderr, flush=True)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            out = model(x)
+        loss_fn(out).backward()
+        opt.step()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    print("bench: warm-up done", file=sys.stderr, flush=True)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    res = {"metric": "training step tokens/s (full model, RACE attention)", "value": round(B * T / (ms / 1e3), 1),
+           "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+           "gpu_ms_per_step": round(e0.elapsed_time(e1) / args.steps, 4),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16 autocast, fp32 weights",
+           "data": "synthetic (N(0,1) images / uniform token ids, random-init weights)",
+           "config": {"workload": wl, "global_batch": B, "seq_len": T}}
+    print(json.dumps(res), flush=True)
+
+
 def cpu_baseline_global(sample_T, H, D=64, L=8, K=4, reps=3):
     """The fp64 C restatement (oracle/race_oracle.c) of the globally normalised
     mode, fwd+bwd, on one batch row of H heads x sample_T tokens (OpenMP over
@@ -373,6 +437,8 @@ def main():
               "not part of this build", file=sys.stderr)
         sys.exit(2)
     import torch
+    if args.workload in ("c3-step", "c5-step"):
+        return model_step_main(args)
     dev = torch.device("cuda:0")
     if args.workload == "c5":
         M, B, T, H, D, L, K = 2, 8, 8192, 12, 64, 4, 8

@@ -1,8 +1,9 @@
 """Non-causal RACE modules with the reference API of misc/vit.py.
 
 Drop-in replacements for misc/vit.py's BatchedACE (:888-979), RACEAttention
-(:994-1039), RACEAttentionWithDenom (:1441-1543) and RACEBlock (:1040-1068):
-same arguments, buffer/parameter names
+(:994-1039), RACEAttentionWithDenom (:1441-1543), RACEBlock (:1040-1068),
+PatchEmbedding (:247-256) and VisionTransformer with RACE blocks
+(:4918-4982): same arguments, buffer/parameter names
 (planes_T, protos_T, logit_temp) and shapes; the attention core runs in the
 HIP library.  The learnable temperature is exp(logit_temp) clamped to
 [1e-2, temp_max] (temp_max 20 as misc/vit.py:923; the notebooks, misc/mlm.py
@@ -130,3 +131,47 @@ class RACEBlock(nn.Module):
         h = x
         x = self.ff(self.norm2(x))
         return self.drop(x) + h
+
+
+class PatchEmbedding(nn.Module):
+    """Non-overlapping patches -> tokens (misc/vit.py:247-256): [B,C,H,W] -> [B,N,d]."""
+
+    def __init__(self, cfg):
+        super().__init__()
+        self.patch_embed = nn.Conv2d(cfg["num_channels"], cfg["embed_dim"], kernel_size=cfg["patch_size"],
+                                     stride=cfg["patch_size"])
+
+    def forward(self, x):
+        return self.patch_embed(x).flatten(2).transpose(1, 2)
+
+
+class VisionTransformer(nn.Module):
+    """ViT with non-causal RACE blocks (misc/vit.py:4918-4982, attn_type "race"):
+    patch embedding, CLS token, learned positions, cfg["transformer_units"]
+    RACEBlocks, LayerNorm + Linear head on the CLS token.  cfg keys as the
+    reference's VISION_CONFIG: img_size, patch_size, num_channels, embed_dim,
+    num_heads, transformer_units, drop_rate, qkv_bias, K, L, M, num_classes."""
+
+    def __init__(self, cfg, attn_type="race", device='cpu'):
+        super().__init__()
+        if attn_type != "race":
+            raise ValueError("this build implements the RACE blocks only (attn_type='race')")
+        self.patch_embedding = PatchEmbedding(cfg)
+        G = cfg["img_size"] // cfg["patch_size"]
+        assert G * cfg["patch_size"] == cfg["img_size"], "img_size must be divisible by patch_size"
+        d = cfg["embed_dim"]
+        self.cls_token = nn.Parameter(torch.zeros(1, 1, d))
+        self.pos_embed = nn.Parameter(torch.zeros(1, G * G + 1, d))
+        nn.init.trunc_normal_(self.cls_token, std=0.02)
+        nn.init.trunc_normal_(self.pos_embed, std=0.02)
+        self.transformer_layers = nn.Sequential(*[RACEBlock(cfg, device) for _ in range(cfg["transformer_units"])])
+        self.mlp_head = nn.Sequential(nn.LayerNorm(d), nn.Linear(d, cfg["num_classes"]))
+
+    def forward(self, x):
+        x = self.patch_embedding(x)
+        B = x.shape[0]
+        x = torch.cat([self.cls_token.expand(B, -1, -1), x], dim=1)
+        x = x + self.pos_embed[:, :x.size(1), :]
+        x = self.transformer_layers(x)
+        return self.mlp_head(x[:, 0])
+

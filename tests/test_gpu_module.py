@@ -148,3 +148,59 @@ def test_causal_race_block(dev, monkeypatch):
     rp = dict(ref.named_parameters())
     pairs += [("d" + n, p.grad, rp[n].grad) for n, p in blk.named_parameters()]
     _check("race.RACEBlock", pairs, TOL[torch.float32])
+
+
+def _ref_copy(model):
+    return copy.deepcopy(model).double()
+
+
+def test_vision_transformer_step(dev, monkeypatch):
+    """vit.VisionTransformer (misc/vit.py:4918-4982) with RACE blocks, fp32 on
+    the GPU, against its fp64 CPU copy whose attention core is the oracle:
+    logits and every parameter gradient of a cross-entropy loss."""
+    import race_attention_amd.vit as rv
+    cfg = dict(img_size=12, patch_size=2, num_channels=1, embed_dim=128, num_heads=2, transformer_units=2,
+               drop_rate=0.0, qkv_bias=False, K=2, L=5, M=1, num_classes=10)
+    torch.manual_seed(21)
+    m = rv.VisionTransformer(cfg)
+    ref = _ref_copy(m)
+    g = torch.Generator().manual_seed(22)
+    x = torch.randn(3, 1, 12, 12, generator=g)
+    y = torch.randint(0, 10, (3,), generator=g)
+    md = m.to(dev)
+    out = md(x.to(dev))
+    torch.nn.functional.cross_entropy(out, y.to(dev)).backward()
+    torch.cuda.synchronize()
+    monkeypatch.setattr(rv, "race_attention", _oracle_attention)
+    out_r = ref(x.double())
+    torch.nn.functional.cross_entropy(out_r, y).backward()
+    monkeypatch.undo()
+    rp = dict(ref.named_parameters())
+    pairs = [("logits", out, out_r)] + [("d" + n, p.grad, rp[n].grad) for n, p in md.named_parameters()]
+    _check("vit.VisionTransformer", pairs, TOL[torch.float32])
+
+
+def test_lm_model_step(dev, monkeypatch):
+    """lm.LMModel (misc/lm.py:37-74) with causal RACE blocks, fp32 on the
+    GPU, against its fp64 CPU copy with the oracle attention core."""
+    import race_attention_amd.lm as rl
+    import race_attention_amd.race as rr
+    cfg = dict(vocab_size=300, context_length=96, emb_dim=128, n_heads=2, n_layers=2, drop_rate=0.0, qkv_bias=False,
+               K=2, L=4, M=2)
+    torch.manual_seed(31)
+    m = rl.LMModel(cfg)
+    ref = _ref_copy(m)
+    g = torch.Generator().manual_seed(32)
+    ids = torch.randint(0, 300, (2, 96), generator=g)
+    tgt = torch.randint(0, 300, (2, 96), generator=g)
+    md = m.to(dev)
+    out = md(ids.to(dev))
+    torch.nn.functional.cross_entropy(out.flatten(0, 1), tgt.to(dev).flatten()).backward()
+    torch.cuda.synchronize()
+    monkeypatch.setattr(rr, "race_attention", _oracle_attention)
+    out_r = ref(ids)
+    torch.nn.functional.cross_entropy(out_r.flatten(0, 1), tgt.flatten()).backward()
+    monkeypatch.undo()
+    rp = dict(ref.named_parameters())
+    pairs = [("logits", out, out_r)] + [("d" + n, p.grad, rp[n].grad) for n, p in md.named_parameters()]
+    _check("lm.LMModel", pairs, TOL[torch.float32])
