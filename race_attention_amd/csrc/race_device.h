@@ -224,6 +224,16 @@ __device__ __forceinline__ void mma16(f32x4 &c, const Frag4<float> &a, const Fra
     for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[e], b.v[e], c, 0, 0, 0);
 }
 
+// -f (sign bits of the 8 bf16 values flipped): a product C + A (-B) subtracts
+__device__ __forceinline__ Frag<bf16> neg_frag(const Frag<bf16> &f) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 u = __builtin_bit_cast(u32x4, f.v);
+    u ^= 0x80008000u;
+    Frag<bf16> r;
+    r.v = __builtin_bit_cast(bf16x8, u);
+    return r;
+}
+
 // fp64 -> fp32 as its own rounding step (kept from being fused with a
 // following fp32 -> bf16 conversion into a double -> bf16 one, which the
 // compiler expands into a multi-instruction round-to-odd sequence)

@@ -13,9 +13,11 @@
 //             k_bwd_scan    exclusive segment suffixes
 //             k_bwd_out     reverse walk: dK, dV            reads Q, K, V, dO
 // The reverse walk needs the forward state at every tile start: it subtracts
-// each tile's (A, B) sums -- recomputed with exactly the code of k_fwd_reduce,
-// so bit-identical -- from the segment's end state in fp64.  The non-causal
-// operator runs the same kernels with full-sequence sums and no triangles.
+// each tile's (A, B) sums from the segment's end state -- A in fp64, B in
+// fp64 for fp32 inputs (recomputed with exactly the code of k_fwd_reduce, so
+// bit-identical) and in fp32 MFMA accumulators for bf16, whose B reaches the
+// products only as a bf16 operand.  The non-causal operator runs the same
+// kernels with full-sequence sums and no triangles.
 //
 // Inside a workgroup wave w owns buckets [16w, 16w+16): the workgroup has
 // SP/16 waves.  Per-bucket elementwise work (probabilities, W = P_Q/(A+eps),
@@ -945,8 +947,10 @@ template <typename T, int SP> struct FwdReduceL {
 };
 
 // The tile's (A, B) sums -- tot (lane: bucket 4g + e) and dB^T (d-row) --
-// from the wave's token operand Pf.  k_bwd_out subtracts exactly these values
-// (same operands, same instructions) to walk the forward state backwards.
+// from the wave's token operand Pf.  In the fp32 instantiations k_bwd_out
+// subtracts exactly these values (same operands, same instructions) from the
+// fp64 state to walk it backwards; bf16 accumulates B in fp32 MFMA
+// accumulators instead (k_fwd_reduce adds, k_bwd_out subtracts).
 template <typename T>
 __device__ __forceinline__ void tile_sums(const Frag<T> &Pf, const Consts<T> &cst, const T *sVt, f32x4 &tot,
                                           f32x4 (&dB)[4]) {
@@ -964,7 +968,7 @@ template <typename T, int SP, int KB>
 __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     using Ly = FwdReduceL<T, SP>;
     using NL = NatL<T, true>;
-    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDC = Ly::LDC;
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDC = Ly::LDC, LDT = ldp_of<T>(TT);
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
@@ -984,11 +988,16 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
     load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
+    // segment sums: A in fp64; B in fp64 for fp32 inputs, and for bf16 in
+    // fp32 MFMA accumulators (bf16 uses B only through bf16 operands)
+    constexpr bool BM = is_bf16<T>();
     double accB[4][4], accA[4];
+    f32x4 accBm[4];
     for (int e = 0; e < 4; ++e) {
         accA[e] = 0.0;
         for (int md = 0; md < 4; ++md) accB[md][e] = 0.0;
     }
+    for (int md = 0; md < 4; ++md) accBm[md] = zero4();
 
     wait_state_loads();
     Prefetch<T, NTH> pk_;
@@ -1021,16 +1030,24 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
                 for (int e = 0; e < 4; ++e) PK[nt][e] *= wt;
             }
         const Frag<T> Pf = token_operand<T>(PK, cst);
-        f32x4 tot, dB[4];
-        tile_sums<T>(Pf, cst, sVt, tot, dB);
-        for (int e = 0; e < 4; ++e) {
-            accA[e] += (double)tot[e];
-            for (int md = 0; md < 4; ++md) accB[md][e] += (double)dB[md][e];
+        if constexpr (BM) {
+            f32x4 tot = zero4();
+            mma(tot, Pf, cst.ones());
+            for (int md = 0; md < 4; ++md) mma(accBm[md], ld_frag_pi(sVt + (16 * md + i) * LDT), Pf);
+            for (int e = 0; e < 4; ++e) accA[e] += (double)tot[e];
+        } else {
+            f32x4 tot, dB[4];
+            tile_sums<T>(Pf, cst, sVt, tot, dB);
+            for (int e = 0; e < 4; ++e) {
+                accA[e] += (double)tot[e];
+                for (int md = 0; md < 4; ++md) accB[md][e] += (double)dB[md][e];
+            }
         }
     }
     double *out = a.fdelta + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     for (int md = 0; md < 4; ++md)
-        for (int e = 0; e < 4; ++e) out[sidx(sg + i, 16 * md + 4 * g + e)] = accB[md][e];
+        for (int e = 0; e < 4; ++e)
+            out[sidx(sg + i, 16 * md + 4 * g + e)] = BM ? (double)accBm[md][e] : accB[md][e];
     if (i == 0)
         for (int e = 0; e < 4; ++e) out[sidx(sg + 4 * g + e, D)] = accA[e];
 }
@@ -1715,14 +1732,24 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     const float *rs = a.rstate + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     const double *fs = a.fstate + ((int64_t)n * (a.nseg + 1) + seg + 1) * a.Spad * SROW;
     f32x4 Ut[4];  // U^T[d = 16md + 4g + e][s = sw + i]
+    // Forward state, walked back from the segment end.  B only feeds the
+    // G product's operand: bf16 carries it in fp32 MFMA accumulators and
+    // subtracts the tile sums on the matrix core (Bm); fp32 walks it in fp64
+    // (Be).  A stays fp64: A(t) is far below the segment-end value early in
+    // a sequence.
+    constexpr bool BM = is_bf16<T>();
     double Be[4][4], Ae[4];
+    f32x4 Bm[4];
     float al[4];
     constexpr bool FSTATE = CAUSAL && !GN;
     for (int md = 0; md < 4; ++md)
         for (int e = 0; e < 4; ++e) {
             const int64_t r = sidx(sg + i, 16 * md + 4 * g + e);
             Ut[md][e] = rs[r];
-            Be[md][e] = FSTATE ? fs[r] : 0.0;
+            if constexpr (BM)
+                Bm[md][e] = FSTATE ? (float)fs[r] : 0.f;
+            else
+                Be[md][e] = FSTATE ? fs[r] : 0.0;
         }
     for (int e = 0; e < 4; ++e) {
         al[e] = rs[sidx(sg + 4 * g + e, D)];
@@ -1828,10 +1855,18 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 f32x4 PQ[2], Acum[2], W[2], tot, dB[4];
                 probs_st<KB>(sSpQ, sSmQ, sg, a.S, t0, a.T, PQ);
                 // forward state at the tile start: end state minus this tile's sums
-                tile_sums<T>(Pf, cst, sVt, tot, dB);
-                for (int e = 0; e < 4; ++e) {
-                    Ae[e] -= (double)tot[e];
-                    for (int md = 0; md < 4; ++md) Be[md][e] -= (double)dB[md][e];
+                if constexpr (BM) {
+                    tot = zero4();
+                    mma(tot, Pf, cst.ones());
+                    const Frag<T> Pn = neg_frag(Pf);
+                    for (int md = 0; md < 4; ++md) mma(Bm[md], ld_frag_pi(sVt + (16 * md + i) * LDT), Pn);
+                    for (int e = 0; e < 4; ++e) Ae[e] -= (double)tot[e];
+                } else {
+                    tile_sums<T>(Pf, cst, sVt, tot, dB);
+                    for (int e = 0; e < 4; ++e) {
+                        Ae[e] -= (double)tot[e];
+                        for (int md = 0; md < 4; ++md) Be[md][e] -= (double)dB[md][e];
+                    }
                 }
                 for (int nt = 0; nt < 2; ++nt) {
                     Acum[nt] = zero4();
@@ -1852,12 +1887,16 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             if constexpr (!GN) {
                 Frag<T> Bf[2];
                 for (int kk = 0; kk < 2; ++kk) {
-                    f32x4 b0, b1;
-                    for (int e = 0; e < 4; ++e) {
-                        b0[e] = narrow(Be[2 * kk][e]);
-                        b1[e] = narrow(Be[2 * kk + 1][e]);
+                    if constexpr (BM) {
+                        Bf[kk] = frag_acc<T>(Bm[2 * kk], Bm[2 * kk + 1]);
+                    } else {
+                        f32x4 b0, b1;
+                        for (int e = 0; e < 4; ++e) {
+                            b0[e] = narrow(Be[2 * kk][e]);
+                            b1[e] = narrow(Be[2 * kk + 1][e]);
+                        }
+                        Bf[kk] = frag_acc<T>(b0, b1);
                     }
-                    Bf[kk] = frag_acc<T>(b0, b1);
                 }
                 for (int nt = 0; nt < 2; ++nt) {
                     f32x4 G = zero4();
