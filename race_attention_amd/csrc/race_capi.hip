@@ -182,7 +182,7 @@ template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Pla
     if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
     const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
-        k_fwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
+        k_fwd_scan<<<dim3((elems + SCAN_THREADS - 1) / SCAN_THREADS, (unsigned)p.N), SCAN_THREADS, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
     if (run_phase(d, RACE_PHASE_OUT)) {
         if (d->causal)
             k_fwd_out<T, SP, true, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
@@ -211,7 +211,7 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
     }
     const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
-        k_bwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.rstate, a.rdelta, p.nseg, elems,
+        k_bwd_scan<<<dim3((elems + SCAN_THREADS - 1) / SCAN_THREADS, (unsigned)p.N), SCAN_THREADS, 0, s>>>(a.rstate, a.rdelta, p.nseg, elems,
                                                                             d->causal);
     if (run_phase(d, RACE_PHASE_OUT)) {
         if (d->causal)
@@ -234,7 +234,7 @@ template <typename T, int SP, int KB> int gn_fwd_impl(const race_desc *d, const 
     if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
     const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
-        k_fwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
+        k_fwd_scan<<<dim3((elems + SCAN_THREADS - 1) / SCAN_THREADS, (unsigned)p.N), SCAN_THREADS, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
     if (run_phase(d, RACE_PHASE_OUT)) {
         k_fwd_out<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) {
@@ -258,7 +258,7 @@ int gn_bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_beta, hip
     }
     const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
-        k_bwd_scan<<<dim3((elems + 255) / 256, (unsigned)p.N), 256, 0, s>>>(a.rstate, a.rdelta, p.nseg, elems, 1);
+        k_bwd_scan<<<dim3((elems + SCAN_THREADS - 1) / SCAN_THREADS, (unsigned)p.N), SCAN_THREADS, 0, s>>>(a.rstate, a.rdelta, p.nseg, elems, 1);
     if (run_phase(d, RACE_PHASE_OUT)) {
         k_bwd_out<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) {

@@ -1053,15 +1053,34 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
 }
 
 // exclusive prefix over segments; [nseg] receives the total
-__global__ void k_fwd_scan(double *fstate, const double *fdelta, int nseg, int elems) {
+// (one thread per state element of one stream, segments in order; the loads
+// of SCAN_BATCH segments are issued together so that many are in flight)
+constexpr int SCAN_BATCH = 16;
+constexpr int SCAN_THREADS = 64;
+__global__ __launch_bounds__(SCAN_THREADS) void k_fwd_scan(double *fstate, const double *fdelta, int nseg,
+                                                           int elems) {
     const int n = blockIdx.y, e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= elems) return;
+    const double *src = fdelta + (int64_t)n * nseg * elems + e;
+    double *dst = fstate + (int64_t)n * (nseg + 1) * elems + e;
     double acc = 0.0;
-    for (int s = 0; s < nseg; ++s) {
-        fstate[((int64_t)n * (nseg + 1) + s) * elems + e] = acc;
-        acc += fdelta[((int64_t)n * nseg + s) * elems + e];
+    int s = 0;
+    for (; s + SCAN_BATCH <= nseg; s += SCAN_BATCH) {
+        double v[SCAN_BATCH];
+#pragma unroll
+        for (int j = 0; j < SCAN_BATCH; ++j) v[j] = src[(int64_t)(s + j) * elems];
+#pragma unroll
+        for (int j = 0; j < SCAN_BATCH; ++j) {
+            dst[(int64_t)(s + j) * elems] = acc;
+            acc += v[j];
+        }
     }
-    fstate[((int64_t)n * (nseg + 1) + nseg) * elems + e] = acc;
+    for (; s < nseg; ++s) {
+        const double v = src[(int64_t)s * elems];
+        dst[(int64_t)s * elems] = acc;
+        acc += v;
+    }
+    dst[(int64_t)nseg * elems] = acc;
 }
 
 // =====================================================================
@@ -1583,18 +1602,33 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
 }
 
 // exclusive suffix over segments (causal) or totals (non-causal)
-__global__ void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int elems, int causal) {
+__global__ __launch_bounds__(SCAN_THREADS) void k_bwd_scan(float *rstate, const float *rdelta, int nseg, int elems,
+                                                           int causal) {
     const int n = blockIdx.y, e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= elems) return;
+    const float *src = rdelta + (int64_t)n * nseg * elems + e;
+    float *dst = rstate + (int64_t)n * nseg * elems + e;
     double acc = 0.0;
-    if (causal) {
-        for (int s = nseg - 1; s >= 0; --s) {
-            rstate[((int64_t)n * nseg + s) * elems + e] = (float)acc;
-            acc += rdelta[((int64_t)n * nseg + s) * elems + e];
+    if (causal) {  // segments in reverse order
+        int s = nseg;
+        for (; s >= SCAN_BATCH; s -= SCAN_BATCH) {
+            float v[SCAN_BATCH];
+#pragma unroll
+            for (int j = 0; j < SCAN_BATCH; ++j) v[j] = src[(int64_t)(s - 1 - j) * elems];
+#pragma unroll
+            for (int j = 0; j < SCAN_BATCH; ++j) {
+                dst[(int64_t)(s - 1 - j) * elems] = (float)acc;
+                acc += v[j];
+            }
+        }
+        for (; s > 0; --s) {
+            const float v = src[(int64_t)(s - 1) * elems];
+            dst[(int64_t)(s - 1) * elems] = (float)acc;
+            acc += v;
         }
     } else {
-        for (int s = 0; s < nseg; ++s) acc += rdelta[((int64_t)n * nseg + s) * elems + e];
-        for (int s = 0; s < nseg; ++s) rstate[((int64_t)n * nseg + s) * elems + e] = (float)acc;
+        for (int s = 0; s < nseg; ++s) acc += src[(int64_t)s * elems];
+        for (int s = 0; s < nseg; ++s) dst[(int64_t)s * elems] = (float)acc;
     }
 }
 
