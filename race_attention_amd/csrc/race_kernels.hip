@@ -1854,8 +1854,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 m_tile<T, NL>(q - 8, sV, sG, sX, sY);
         }
         __syncthreads();
-        f32x4 PKr[2];  // operand-rounded P_K (fp32 P_K is rebuilt for the softmax backward)
-        probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PKr);
+        f32x4 PKraw[2], PKr[2];  // fp32 P_K (kept for the softmax backward), operand-rounded P_K
+        probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PKraw);
+        PKr[0] = PKraw[0];
+        PKr[1] = PKraw[1];
         float kwt[2] = {1.f, 1.f};  // non-causal key weights: P_K' = w_t P_K
         if constexpr (!CAUSAL) {
             if (kwp)
@@ -1972,12 +1974,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             }
         }
         {
-            f32x4 PK[2];
-            probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PK);
             if constexpr (KB <= 4) {
-                tsum += softhash_bwd<KB, T>(PK, dPK, sSpK, sSmK, sThK, sg, a.L, a.inv_temp, sDproj, ho);
+                tsum += softhash_bwd<KB, T>(PKraw, dPK, sSpK, sSmK, sThK, sg, a.L, a.inv_temp, sDproj, ho);
             } else {
-                softhash_share<KB, T>(PK, dPK, wh, sShare);
+                softhash_share<KB, T>(PKraw, dPK, wh, sShare);
                 __syncthreads();
                 tsum += softhash_combine<KB, T, SP, NTH>(sShare, sSpK, sSmK, sThK, z, a.L, a.inv_temp, sDproj);
             }
