@@ -561,22 +561,26 @@ template <typename T, int KB> struct HashOps {
     static constexpr int LDI = ldp_of<T>(W_);
     static constexpr size_t bytes = sizeof(T) * 16 * LDI;
     const T *a;
-    // row r: 1 = corner k of local table tl, 2 = sum of tl, 0 = unused;
-    // de = slot of tl's sum row in the row's lane group
+    // row r = 4g + e (lane group g, slot e of the product's accumulator):
+    // 1 = corner k of local table tl, 2 = sum of tl, 0 = unused; de = slot of
+    // tl's sum row in the row's lane group.  The corners are spread over the
+    // lane groups so that every lane has at most one corner per pair of
+    // slots: K = 4 puts corner k = g in slot 0 (one pass over the slots),
+    // K = 3 corner k = g (g < 3) of tables 0 and 1 in slots 0 and 2.
     __host__ __device__ static constexpr int kind_of(int r, int &k, int &tl, int &de) {
         const int g = r >> 2, e = r & 3;
         k = 0;
         if constexpr (KB == 4) {
             tl = 0;
-            de = g == 0 ? 3 : 1;
-            if (g == 0) return e < 3 ? (k = e, 1) : 2;
-            if (g == 1) return e == 0 ? (k = 3, 1) : (e == 1 ? 2 : 0);
-            return 0;
+            de = 1;
+            k = g;
+            return e == 0 ? 1 : (e == 1 ? 2 : 0);
         } else if constexpr (KB == 3) {
-            tl = g;
-            de = 3;
-            if (g >= 2) return 0;
-            return e < 3 ? (k = e, 1) : 2;
+            tl = e >> 1;
+            de = (e & 2) | 1;
+            k = g;
+            if (g == 3) return 0;
+            return (e & 1) ? 2 : 1;
         } else if constexpr (KB == 2) {
             tl = g;
             de = 2;
@@ -607,6 +611,28 @@ template <typename T, int KB> struct HashOps {
         return o;
     }
 };
+
+// Every (table, corner) pair of the wave's 16 buckets has exactly one corner
+// row, whose sum slot de (same lane group) holds the sum row of its table.
+template <int KB> constexpr bool hash_rows_valid() {
+    constexpr int NTAB = 16 >> KB > 0 ? 16 >> KB : 1;
+    for (int tl = 0; tl < NTAB; ++tl)
+        for (int kk = 0; kk < KB; ++kk) {
+            int found = 0;
+            for (int r = 0; r < 16; ++r) {
+                int k = 0, t = 0, de = 0;
+                if (HashOps<float, KB>::kind_of(r, k, t, de) == 1 && t == tl && k == kk) {
+                    ++found;
+                    int k2 = 0, t2 = 0, de2 = 0;
+                    if (HashOps<float, KB>::kind_of((r & ~3) | de, k2, t2, de2) != 2 || t2 != tl) return false;
+                }
+            }
+            if (found != 1) return false;
+        }
+    return true;
+}
+static_assert(hash_rows_valid<1>() && hash_rows_valid<2>() && hash_rows_valid<3>() && hash_rows_valid<4>(),
+              "softmax-backward row layout");
 
 // Token-direction operand of the wave's bucket-row tiles X[2] (lane holds
 // X[s = 4g + e][t = 16nt + i]): each tile is transposed on the matrix core
@@ -802,9 +828,7 @@ __device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const f
             if (kind == 1 && l < L) {
                 float sum;
                 if constexpr (KB == 4)
-                    sum = g == 0 ? X[3] : X[1];
-                else if constexpr (KB == 3)
-                    sum = X[3];
+                    sum = X[1];
                 else if constexpr (KB == 2)
                     sum = X[2];
                 else
