@@ -36,7 +36,9 @@ template <typename T> __host__ __device__ constexpr int ld_of(int n) { return n 
 template <typename T> __host__ __device__ constexpr int ldp_of(int n) { return n + 4; }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+// wave index, uniform: read from the wave's first lane so that values derived
+// from it (bucket ranges, task indices) live in scalar registers
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 // ------------------------------------------------------------ conversions
 __device__ __forceinline__ float to_f32(float x) { return x; }
