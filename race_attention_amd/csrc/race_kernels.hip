@@ -1858,6 +1858,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         // loop head, and the wait placed there also waits for the previous
         // tile's stores.
         const int64_t tn = (jr > j0 ? jr - 1 : jr) * TT;
+        __syncthreads();
+        // issued after the barrier: the previous tile's dK stores have had
+        // the barrier's time to drain from the memory pipeline
         pk_.issue(kp, a.sk.t, tn, a.T);
         if constexpr (CAUSAL) {
             pv_.issue(1, vp, a.sv.t, tn, a.T);
@@ -1868,7 +1871,6 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             if (kwp) pt_.issue(kwp, nullptr, tn, a.T);
         }
         if constexpr (GN) pt_.issue(rdp, gdp, tn, a.T);
-        __syncthreads();
         for (int q = w; q < NTASK; q += NW_) {
             if (q < 4)
                 project_tile<T, NL>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpK, sSmK, sThK);
