@@ -288,18 +288,21 @@ __device__ __forceinline__ float row_sum(float x) {
 
 // ------------------------------------------------------------ sigmoids
 __device__ __forceinline__ float rcp_f(float x) { return __builtin_amdgcn_rcpf(x); }
-// stable pair (sigmoid(x), sigmoid(-x)) from one exp and one reciprocal
-__device__ __forceinline__ void sigmoid_pair(float x, float &sp, float &sm) {
-    const float e = __expf(-fabsf(x));
-    const float p = rcp_f(1.0f + e);
-    const float q = e * p;
-    sp = x >= 0.f ? p : q;
-    sm = x >= 0.f ? q : p;
+// (sigmoid(y), sigmoid(-y)) from z = -y log2(e): e = 2^z, sigmoid(y) = 1/(1+e),
+// sigmoid(-y) = e/(1+e).  z is capped at 64, so e, 1+e and the reciprocal stay
+// normal: for y < -44.36 sigmoid(y) reads 1/(1 + 2^64) instead of something
+// smaller (absolute error < 6e-20) and sigmoid(-y) reads 1.  No branch or
+// select on the sign of y.
+__device__ __forceinline__ void sigmoid_pair_l2(float z, float &sp, float &sm) {
+    const float e = __builtin_amdgcn_exp2f(fminf(z, 64.f));
+    sp = rcp_f(1.0f + e);
+    sm = e * sp;
 }
-// tanh(x) = sign(x) (1 - e) / (1 + e), e = exp(-2|x|); absolute error ~1e-7
+// tanh(x) = 1 - 2 / (1 + e^{2x}): e^{2x} overflowing to +inf gives 1 and
+// underflowing to 0 gives -1; absolute error ~1e-7
 __device__ __forceinline__ float tanh_fast(float x) {
-    const float e = __expf(-2.f * fabsf(x));
-    return copysignf((1.f - e) * rcp_f(1.f + e), x);
+    const float e = __builtin_amdgcn_exp2f(x * 2.8853900817779268f);  // 2 log2(e)
+    return fmaf(-2.f, rcp_f(1.f + e), 1.f);
 }
 
 } // namespace race

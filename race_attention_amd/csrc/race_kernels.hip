@@ -409,12 +409,15 @@ __device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mc, in
         if constexpr (is_bf16<T>()) mma(acc, NL::frag(pllo, 16 * mc + li(), kp), x);
     }
     const int t = 16 * nt + li(), c0 = 16 * mc + 4 * lg();
+    // the corner pair (sigmoid(2u), sigmoid(-2u)), u = th inv_temp, from
+    // z = -2u log2(e) = th * zc
+    const float zc = -2.8853900817779268f * inv_temp;
     f32x4 a, b, th;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         th[e] = tanh_fast(acc[e]);
         float x, y;
-        sigmoid_pair(2.f * th[e] * inv_temp, x, y);
+        sigmoid_pair_l2(th[e] * zc, x, y);
         a[e] = x;
         b[e] = y;
     }
@@ -1526,6 +1529,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             else
                 m_tile<T, NL>(q - 8, sV, sG, sX, nullptr);
         }
+        // dQ of the previous tile, from the dproj rows its softmax backward
+        // left in LDS: independent of the projections, so the two overlap;
+        // the next write of sDproj is two barriers away
+        if (jt > j0) dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart);
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2], tot;
         Frag<T> Pf;
@@ -1611,11 +1618,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             tsum += softhash_combine<KB, T, SP, NTH>(sShare, sSpQ, sSmQ, sThQ, z, a.L, a.inv_temp, sDproj);
         }
         __syncthreads();
-        // after the last barrier only dx_store runs, which reads neither the
-        // token tiles nor X: the next tile's rows can go to LDS now
+        // the next tile's rows go to LDS after the tile's last barrier; its
+        // dQ is stored in the next iteration (or after the loop)
         commit();
-        dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0, a.T, xpart);
     }
+    if (j0 < j1) dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, (j1 - 1) * TT, a.T, xpart);
     float *out = a.rdelta + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     for (int md = 0; md < 4; ++md)
         for (int e = 0; e < 4; ++e) out[sidx(sg + i, 16 * md + 4 * g + e)] = Ut[md][e];
@@ -1879,6 +1886,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             else
                 m_tile<T, NL>(q - 8, sV, sG, sX, sY);
         }
+        // dK of the tile after this one (walking down), from the dproj rows its
+        // softmax backward left in LDS: independent of the projections, so the
+        // two overlap; the next write of sDproj is two barriers away
+        if (jr + 1 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart);
         __syncthreads();
         f32x4 PKraw[2], PKr[2];  // fp32 P_K (kept for the softmax backward), operand-rounded P_K
         probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PKraw);
@@ -2009,11 +2020,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             }
         }
         __syncthreads();
-        // after the last barrier only dx_store runs, which reads neither the
-        // token tiles nor X / Y: the next tile's rows can go to LDS now
+        // the next tile's rows go to LDS after the tile's last barrier; its
+        // dK is stored in the next iteration (or after the loop)
         commit();
-        dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0, a.T, xpart);
     }
+    if (j0 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, j0 * TT, a.T, xpart);
     const float ts = block_sum<NTH>(tsum, sRed);
     if (threadIdx.x == 0) a.tpart[((int64_t)(a.M * a.B * a.H + n) * a.nseg + seg) * a.nslice + z] = ts;
 }
