@@ -286,6 +286,21 @@ __device__ __forceinline__ float row_sum(float x) {
     return x;
 }
 
+// row_sum of an fp64 value (both 32-bit halves move with the same pattern)
+template <int CTRL> __device__ __forceinline__ double dpp_d(double x) {
+    const long long b = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(b & 0xffffffffll), CTRL, 0xF, 0xF, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, 0xF, 0xF, true);
+    return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+}
+__device__ __forceinline__ double row_sum_f64(double x) {
+    x += dpp_d<0xB1>(x);
+    x += dpp_d<0x4E>(x);
+    x += dpp_d<0x141>(x);
+    x += dpp_d<0x140>(x);
+    return x;
+}
+
 // ------------------------------------------------------------ sigmoids
 __device__ __forceinline__ float rcp_f(float x) { return __builtin_amdgcn_rcpf(x); }
 // (sigmoid(y), sigmoid(-y)) from z = -y log2(e): e = 2^z, sigmoid(y) = 1/(1+e),

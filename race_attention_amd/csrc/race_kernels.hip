@@ -773,13 +773,14 @@ __device__ float softhash_combine(const float *share, const float *sp, const flo
     return tsum;
 }
 
-// Inclusive token suffix Y and token totals of a bucket-row tile pair on the
-// matrix cores; bf16 splits X into two bf16 parts (fp32-accurate sums).
+// Inclusive token suffix Y (plus y0, the lane's per-bucket carry) and token
+// totals of a bucket-row tile pair on the matrix cores; bf16 splits X into two
+// bf16 parts (fp32-accurate sums).
 template <typename T>
 __device__ void suffix_totals(const f32x4 (&X)[2], const Consts<T> &cst, const SufOps<T> &suf, const PairOps<T> &po,
-                              f32x4 (&Y)[2], f32x4 &tot) {
-    Y[0] = zero4();
-    Y[1] = zero4();
+                              const f32x4 &y0, f32x4 (&Y)[2], f32x4 &tot) {
+    Y[0] = y0;
+    Y[1] = y0;
     tot = zero4();
     auto add = [&](const Frag<T> &F) {
 #pragma unroll
@@ -1301,11 +1302,10 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             }
         } else {
             // W = P_Q / (A(t) + eps)
+            float ae[4];
+            for (int e = 0; e < 4; ++e) ae[e] = (float)a0[e] + a.eps;
             for (int nt = 0; nt < 2; ++nt)
-                for (int e = 0; e < 4; ++e) {
-                    const float A = (float)a0[e] + (CAUSAL ? Acum[nt][e] : 0.f);
-                    W[nt][e] = PQ[nt][e] * rcp(A + a.eps);
-                }
+                for (int e = 0; e < 4; ++e) W[nt][e] = PQ[nt][e] * rcp(CAUSAL ? ae[e] + Acum[nt][e] : ae[e]);
             if constexpr (!CAUSAL) {
                 if (want_den)  // this wave's share of den(t) = sum_s P_Q A_s
                     for (int nt = 0; nt < 2; ++nt) {
@@ -1550,19 +1550,20 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             mma(tot, Pf, cst.ones());
         }
         f32x4 Ag[2];  // GN: A_s(t)
-        float rd[2], gd[2];
+        float rd[2], gd[2], ae[4];  // ae: A at the tile start (+ eps unless GN)
+        for (int e = 0; e < 4; ++e) ae[e] = GN ? (float)a0[e] : (float)a0[e] + a.eps;
         for (int nt = 0; nt < 2; ++nt) {
             if constexpr (GN) {
                 rd[nt] = sTok[16 * nt + i];
                 gd[nt] = sTok[TT + 16 * nt + i];
             }
             for (int e = 0; e < 4; ++e) {
-                const float A = (float)a0[e] + (CAUSAL ? Acum[nt][e] : 0.f);
+                const float A = CAUSAL ? ae[e] + Acum[nt][e] : ae[e];
                 if constexpr (GN) {
                     Ag[nt][e] = A;
                     inv[nt][e] = rd[nt];
                 } else {
-                    inv[nt][e] = rcp(A + a.eps);
+                    inv[nt][e] = rcp(A);
                 }
                 W[nt][e] = PQ[nt][e] * inv[nt][e];
             }
@@ -1598,11 +1599,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
                 }
             }
         }
-        {
-            f32x4 tdA;
-            totals_of(dA, tdA);
-            for (int e = 0; e < 4; ++e) al[e] += (double)tdA[e];
-        }
+        // the lane's share of the segment's dA totals (summed over the row's
+        // lanes after the walk)
+        for (int e = 0; e < 4; ++e) al[e] += (double)(dA[0][e] + dA[1][e]);
         // U^T[d][s] += sum_t g[t][d] W[t][s]; carry B^T[d][s] += sum_t V[t][d] P_K[t][s]
         for (int md = 0; md < 4; ++md) {
             mma(Ut[md], ld_frag_pi(sGt + (16 * md + i) * LDT), Wf);
@@ -1626,6 +1625,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     float *out = a.rdelta + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     for (int md = 0; md < 4; ++md)
         for (int e = 0; e < 4; ++e) out[sidx(sg + i, 16 * md + 4 * g + e)] = Ut[md][e];
+    for (int e = 0; e < 4; ++e) al[e] = row_sum_f64(al[e]);
     if (i == 0)
         for (int e = 0; e < 4; ++e) out[sidx(sg + 4 * g + e, D)] = (float)al[e];
     const float ts = block_sum<NTH>(tsum, sRed);
@@ -1805,7 +1805,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     constexpr bool BM = is_bf16<T>();
     double Be[4][4], Ae[4];
     f32x4 Bm[4];
-    float al[4];
+    f32x4 al;
     constexpr bool FSTATE = CAUSAL && !GN;
     for (int md = 0; md < 4; ++md)
         for (int e = 0; e < 4; ++e) {
@@ -1945,9 +1945,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                     Acum[nt] = zero4();
                     mma(Acum[nt], Pf, cst.tri_op(nt));
                 }
+                float ae[4];
+                for (int e = 0; e < 4; ++e) ae[e] = (float)Ae[e] + a.eps;
                 for (int nt = 0; nt < 2; ++nt)
                     for (int e = 0; e < 4; ++e) {
-                        const float inv = rcp((float)Ae[e] + Acum[nt][e] + a.eps);
+                        const float inv = rcp(ae[e] + Acum[nt][e]);
                         W[nt][e] = PQ[nt][e] * inv;
                         Wi[nt][e] = W[nt][e] * inv;
                     }
@@ -1981,15 +1983,14 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             }
             // ---- dP_K[tau][s] = alpha(tau) + sum_d U[s][d] v_tau[d] + sum_{t >= tau} W[t][s] M[tau][t]
             {
-                f32x4 alpha[2], tdA;
-                suffix_totals<T>(dA, cst, sufo, po, alpha, tdA);
+                f32x4 alpha[2], tdA;  // alpha(tau): the suffix from this tile on
+                suffix_totals<T>(dA, cst, sufo, po, al, alpha, tdA);
                 const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
                 for (int nt = 0; nt < 2; ++nt) {
-                    f32x4 c = zero4();
-                    mma(c, u0, NL::frag_pi(sV, 16 * nt + i, 0));
-                    mma(c, u1, NL::frag_pi(sV, 16 * nt + i, 1));
-                    mma(c, Wf, ld_frag_pi(sY + (16 * nt + i) * LDT));
-                    for (int e = 0; e < 4; ++e) dPK[nt][e] = c[e] + alpha[nt][e] + al[e];
+                    dPK[nt] = alpha[nt];
+                    mma(dPK[nt], u0, NL::frag_pi(sV, 16 * nt + i, 0));
+                    mma(dPK[nt], u1, NL::frag_pi(sV, 16 * nt + i, 1));
+                    mma(dPK[nt], Wf, ld_frag_pi(sY + (16 * nt + i) * LDT));
                 }
                 for (int e = 0; e < 4; ++e) al[e] += tdA[e];
             }
