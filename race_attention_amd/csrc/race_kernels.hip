@@ -427,12 +427,12 @@ __device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mc, in
 }
 
 // Bucket probabilities of the wave's 16 buckets in bucket-row layout:
-// P[nt][e] = P[t = 16nt + i][s = sw + 4g + e]; zero for s >= S or t0 + t >= T.
+// P[nt][e] = P[t = 16nt + i][s = sw + 4g + e]; zero for s >= S or t >= nv (nv:
+// the tile's rows that exist, tile_rows).
 // For K >= 2 the 4 buckets of a lane share one table and differ in the two
 // lowest corner bits: P = hi * (bit1 ? s+ : s-) * (bit0 ? s+ : s-).
 template <int KB>
-__device__ __forceinline__ void probs_st(const float *sp, const float *sm, int sw, int S, int64_t t0, int64_t Tn,
-                                         f32x4 (&P)[2]) {
+__device__ __forceinline__ void probs_st(const float *sp, const float *sm, int sw, int S, int nv, f32x4 (&P)[2]) {
     constexpr int LDC = ld_of<float>(NCOL);
     constexpr int R = 1 << KB;
     const int g = lg(), i = li();
@@ -440,7 +440,7 @@ __device__ __forceinline__ void probs_st(const float *sp, const float *sm, int s
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int t = 16 * nt + i;
-        const bool tv = t0 + t < Tn;
+        const bool tv = t < nv;
         if constexpr (KB == 1) {
             // tables s0/2 and s0/2 + 1; corner r = 1 is sigmoid(+2u)
             const bool v01 = tv && s0 < S, v23 = tv && s0 + 2 < S;
@@ -460,9 +460,15 @@ __device__ __forceinline__ void probs_st(const float *sp, const float *sm, int s
                 fp[k] = pp[k];
                 fm[k] = pm[k];
             }
-            float hi = v ? 1.f : 0.f;
+            float hi;
+            if constexpr (KB == 2) {
+                hi = v ? 1.f : 0.f;
+            } else {
+                hi = ((r0 >> (KB - 1)) & 1) ? fp[0] : fm[0];
 #pragma unroll
-            for (int k = 0; k < KB - 2; ++k) hi *= ((r0 >> (KB - 1 - k)) & 1) ? fp[k] : fm[k];
+                for (int k = 1; k < KB - 2; ++k) hi *= ((r0 >> (KB - 1 - k)) & 1) ? fp[k] : fm[k];
+                hi = v ? hi : 0.f;
+            }
             const float h0 = hi * fm[KB - 2], h1 = hi * fp[KB - 2];
             P[nt][0] = h0 * fm[KB - 1];
             P[nt][1] = h0 * fp[KB - 1];
@@ -1007,6 +1013,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
     const int64_t ntiles = (a.T + TT - 1) / TT;
+    const int lastv = (int)(a.T - (ntiles - 1) * TT);  // rows of the last tile
     const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
@@ -1051,7 +1058,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
         for (int q = w; q < 4; q += NW_) project_tile<T, NL>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, nullptr);
         __syncthreads();
         f32x4 PK[2];
-        probs_st<KB>(sSp, sSm, sg, a.S, t0, a.T, PK);
+        probs_st<KB>(sSp, sSm, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
         if (kwp)  // P_K' = w_t P_K
             for (int nt = 0; nt < 2; ++nt) {
                 const float wt = sTok[16 * nt + i];
@@ -1215,6 +1222,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
     const int64_t ntiles = (a.T + TT - 1) / TT;
+    const int lastv = (int)(a.T - (ntiles - 1) * TT);  // rows of the last tile
     const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
     const T *qp = (const T *)a.q + stream_off(a.sq, n, a.B, a.H);
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
@@ -1276,9 +1284,9 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
         Frag<T> Pf;
-        probs_st<KB>(sSpQ, sSmQ, sg, a.S, t0, a.T, PQ);
+        probs_st<KB>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
         if constexpr (CAUSAL) {
-            probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PK);
+            probs_st<KB>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
             Pf = token_operand<T>(PK, cst);
@@ -1418,6 +1426,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
     const int64_t ntiles = (a.T + TT - 1) / TT;
+    const int lastv = (int)(a.T - (ntiles - 1) * TT);  // rows of the last tile
     const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
     const T *qp = (const T *)a.q + stream_off(a.sq, n, a.B, a.H);
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
@@ -1536,9 +1545,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2], tot;
         Frag<T> Pf;
-        probs_st<KB>(sSpQ, sSmQ, sg, a.S, t0, a.T, PQ);
+        probs_st<KB>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
         if constexpr (CAUSAL) {
-            probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PK);
+            probs_st<KB>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
             Pf = token_operand<T>(PK, cst, po);
@@ -1673,31 +1682,45 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     static constexpr int NW_ = SP / WB;
     static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>(),
                          LDS_ = sw_ld<T, SP>();
+    // token block: one tile's staged rows (K, Q, V, dO natural; V, dO
+    // transposed; GN: rden, gden [2][TT]; non-causal: key weights [TT])
     static constexpr size_t oK = 0;
     static constexpr size_t oQ = align16(oK + sizeof(T) * TT * LDN);
     static constexpr size_t oV = align16(oQ + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oG = align16(oV + sizeof(T) * TT * LDN);
     static constexpr size_t oVt = align16(oG + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oGt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oX = align16(oGt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oY = align16(oX + (CAUSAL ? sizeof(T) * TT * LDT : 0));
-    static constexpr size_t oPts = align16(oY + (CAUSAL ? sizeof(T) * TT * LDT : 0));
-    static constexpr size_t oWts = align16(oPts + sizeof(T) * TT * LDS_);
-    static constexpr size_t oUT = align16(oWts + (CAUSAL ? sizeof(T) * TT * LDS_ : 0));
-    static constexpr size_t oDproj = align16(oUT + sizeof(T) * D * LDS_);
-    static constexpr size_t oPl = align16(oDproj + sizeof(T) * TT * LDDP);
-    static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oPlT = align16(oPlLo + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oSig = align16(oPlT + sizeof(T) * D * LDDP);  // K sp, K sm, K th, Q sp, Q sm
-    static constexpr size_t oRed = align16(oSig + sizeof(float) * (CAUSAL ? 5 : 3) * TT * LDC);
-    static constexpr size_t oCst = align16(oRed + sizeof(float) * 64 * NW_);
-    static constexpr size_t oHash = align16(oCst + Consts<T>::bytes);
-    static constexpr size_t oSuf = align16(oHash + HashOps<T, 4>::bytes);
-    static constexpr size_t oPair = align16(oSuf + (CAUSAL ? SufOps<T>::bytes : 0));
-    static constexpr size_t oShare = align16(oPair + PairOps<T>::bytes);
-    static constexpr size_t oTok = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
-    // GN: rden, gden [2][TT]; non-causal: key weights [TT]
-    static constexpr size_t bytes = align16(oTok + (GN || !CAUSAL ? sizeof(float) * 2 * TT : 0));
+    static constexpr size_t oTok = align16(oGt + (CAUSAL ? sizeof(T) * D * LDT : 0));
+    static constexpr size_t TB = align16(oTok + (GN || !CAUSAL ? sizeof(float) * 2 * TT : 0));
+    // the rest, relative to its start
+    static constexpr size_t rX = 0;
+    static constexpr size_t rY = align16(rX + (CAUSAL ? sizeof(T) * TT * LDT : 0));
+    static constexpr size_t rPts = align16(rY + (CAUSAL ? sizeof(T) * TT * LDT : 0));
+    static constexpr size_t rWts = align16(rPts + sizeof(T) * TT * LDS_);
+    static constexpr size_t rUT = align16(rWts + (CAUSAL ? sizeof(T) * TT * LDS_ : 0));
+    static constexpr size_t rDproj = align16(rUT + sizeof(T) * D * LDS_);
+    static constexpr size_t rPl = align16(rDproj + sizeof(T) * TT * LDDP);
+    static constexpr size_t rPlLo = align16(rPl + sizeof(T) * NCOL * LDN);
+    static constexpr size_t rPlT = align16(rPlLo + sizeof(T) * NCOL * LDN);
+    static constexpr size_t rSig = align16(rPlT + sizeof(T) * D * LDDP);  // K sp, K sm, K th, Q sp, Q sm
+    static constexpr size_t rRed = align16(rSig + sizeof(float) * (CAUSAL ? 5 : 3) * TT * LDC);
+    static constexpr size_t rCst = align16(rRed + sizeof(float) * 64 * NW_);
+    static constexpr size_t rHash = align16(rCst + Consts<T>::bytes);
+    static constexpr size_t rSuf = align16(rHash + HashOps<T, 4>::bytes);
+    static constexpr size_t rPair = align16(rSuf + (CAUSAL ? SufOps<T>::bytes : 0));
+    static constexpr size_t rShare = align16(rPair + PairOps<T>::bytes);
+    static constexpr size_t rEnd = align16(rShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
+    // two token blocks when they cost no workgroup per CU (160 KiB of LDS):
+    // the next tile's rows then go to the other block while this tile still
+    // reads its own, and the barrier ahead of that commit goes away
+    static constexpr size_t LDS_CU = 160 * 1024;
+    static constexpr int NB = LDS_CU / (2 * TB + rEnd) >= LDS_CU / (TB + rEnd) ? 2 : 1;
+    static constexpr size_t R0 = NB * TB;
+    static constexpr size_t oX = R0 + rX, oY = R0 + rY, oPts = R0 + rPts, oWts = R0 + rWts, oUT = R0 + rUT,
+                            oDproj = R0 + rDproj, oPl = R0 + rPl, oPlLo = R0 + rPlLo, oPlT = R0 + rPlT,
+                            oSig = R0 + rSig, oRed = R0 + rRed, oCst = R0 + rCst, oHash = R0 + rHash, oSuf = R0 + rSuf,
+                            oPair = R0 + rPair, oShare = R0 + rShare;
+    static constexpr size_t bytes = R0 + rEnd;
 };
 
 template <typename T, int SP, bool CAUSAL>
@@ -1746,8 +1769,19 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                   LDS_ = Ly::LDS_;
     constexpr int NTASK = CAUSAL ? 14 : 4;  // K projection (4), Q projection (4), X and Y tiles (6)
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
-    T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sV = (T *)(smem + Ly::oV);
-    T *sG = (T *)(smem + Ly::oG), *sVt = (T *)(smem + Ly::oVt), *sGt = (T *)(smem + Ly::oGt);
+    // this tile's token block (block jr & 1 of two; block 0 of one)
+    T *sQ, *sK, *sV, *sG, *sVt, *sGt;
+    float *sTok;
+    auto use_block = [&](int b) {
+        unsigned char *tb = smem + b * Ly::TB;
+        sK = (T *)(tb + Ly::oK);
+        sQ = (T *)(tb + Ly::oQ);
+        sV = (T *)(tb + Ly::oV);
+        sG = (T *)(tb + Ly::oG);
+        sVt = (T *)(tb + Ly::oVt);
+        sGt = (T *)(tb + Ly::oGt);
+        sTok = (float *)(tb + Ly::oTok);
+    };
     T *sX = (T *)(smem + Ly::oX), *sY = (T *)(smem + Ly::oY);
     T *sPts = (T *)(smem + Ly::oPts), *sWts = (T *)(smem + Ly::oWts), *sUT = (T *)(smem + Ly::oUT);
     T *sDproj = (T *)(smem + Ly::oDproj);
@@ -1761,6 +1795,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
     const int64_t ntiles = (a.T + TT - 1) / TT;
+    const int lastv = (int)(a.T - (ntiles - 1) * TT);  // rows of the last tile
     const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
     const T *qp = (const T *)a.q + stream_off(a.sq, n, a.B, a.H);
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
@@ -1770,7 +1805,6 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     T *dvp = (T *)a.dv + stream_off(a.sg, n, a.B, a.H);
     float *xpart = sliced<T, KB>() ? a.dkpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
     float *vpart = sliced<T, KB>() ? a.dvpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
-    float *sTok = (float *)(smem + Ly::oTok);
     const float *rdp = GN ? a.rden + (int64_t)n * a.T : nullptr, *gdp = GN ? a.gden + (int64_t)n * a.T : nullptr;
     const float *kwp = !CAUSAL && a.kw ? a.kw + (int64_t)((n / a.H) % a.B) * a.T : nullptr;
 
@@ -1827,22 +1861,23 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     Prefetch<T, NTH> pq_, pk_, pvn_;  // pvn_: non-causal V (natural only)
     PrefetchT<T, NTH, 2> pg_, pv_;   // causal dO and V (natural and transposed)
     TokPre pt_;
-    // The next tile's rows are committed to LDS right after a tile's last
-    // barrier and before its dK stores: that commit waits (vmcnt) on loads
-    // issued a tile earlier, never on the stores just issued.
-    auto commit = [&]() {
+    // Writes the prefetched rows to token block b.
+    auto commit = [&](int b) {
+        unsigned char *tb = smem + b * Ly::TB;
+        float *tok = (float *)(tb + Ly::oTok);
         wait_vmem();
-        pk_.template commit<NL>(sK, nullptr);
+        pk_.template commit<NL>((T *)(tb + Ly::oK), nullptr);
         if constexpr (CAUSAL) {
-            pv_.template commit<NL>(1, sV, sVt);
-            pq_.template commit<NL>(sQ, nullptr);
-            pg_.template commit<NL>(0, sG, sGt);
+            pv_.template commit<NL>(1, (T *)(tb + Ly::oV), (T *)(tb + Ly::oVt));
+            pq_.template commit<NL>((T *)(tb + Ly::oQ), nullptr);
+            pg_.template commit<NL>(0, (T *)(tb + Ly::oG), (T *)(tb + Ly::oGt));
         } else {
-            pvn_.template commit<NL>(sV, nullptr);
-            if (kwp) pt_.commit(sTok);
+            pvn_.template commit<NL>((T *)(tb + Ly::oV), nullptr);
+            if (kwp) pt_.commit(tok);
         }
-        if constexpr (GN) pt_.commit(sTok);
+        if constexpr (GN) pt_.commit(tok);
     };
+    constexpr int NB = Ly::NB;
     if (j0 < j1) {
         const int64_t tl = (j1 - 1) * TT;
         pk_.issue(kp, a.sk.t, tl, a.T);
@@ -1855,10 +1890,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             if (kwp) pt_.issue(kwp, nullptr, tl, a.T);
         }
         if constexpr (GN) pt_.issue(rdp, gdp, tl, a.T);
-        commit();
+        commit(NB == 2 ? (int)((j1 - 1) & 1) : 0);
     }
     for (int64_t jr = j1 - 1; jr >= j0; --jr) {
         const int64_t t0 = jr * TT;
+        use_block(NB == 2 ? (int)(jr & 1) : 0);
         // next tile's rows (walking down); the last tile reloads itself (loads
         // stay in range).  Issue and commit run every iteration: a commit under
         // a condition leaves the prefetch registers possibly pending at the
@@ -1892,7 +1928,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         if (jr + 1 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart);
         __syncthreads();
         f32x4 PKraw[2], PKr[2];  // fp32 P_K (kept for the softmax backward), operand-rounded P_K
-        probs_st<KB>(sSpK, sSmK, sg, a.S, t0, a.T, PKraw);
+        probs_st<KB>(sSpK, sSmK, sg, a.S, jr + 1 < ntiles ? TT : lastv, PKraw);
         PKr[0] = PKraw[0];
         PKr[1] = PKraw[1];
         float kwt[2] = {1.f, 1.f};  // non-causal key weights: P_K' = w_t P_K
@@ -1914,7 +1950,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             Frag<T> Wf;
             if constexpr (GN) {
                 f32x4 PQ[2], W[2];
-                probs_st<KB>(sSpQ, sSmQ, sg, a.S, t0, a.T, PQ);
+                probs_st<KB>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
                 for (int nt = 0; nt < 2; ++nt) {
                     const float rd = sTok[16 * nt + i], gd = sTok[TT + 16 * nt + i];
                     for (int e = 0; e < 4; ++e) {
@@ -1926,7 +1962,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 Wf = token_operand<T>(W, cst, po);
             } else {
                 f32x4 PQ[2], Acum[2], W[2], tot, dB[4];
-                probs_st<KB>(sSpQ, sSmQ, sg, a.S, t0, a.T, PQ);
+                probs_st<KB>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
                 // forward state at the tile start: end state minus this tile's sums
                 if constexpr (BM) {
                     tot = zero4();
@@ -1958,6 +1994,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             }
             store_ut<T, SP>(sUT, sw, Ut, cst, po);
             __syncthreads();  // all waves' P_K, W, U rows in LDS
+            // two token blocks: the next tile's rows go to the other block now
+            // (its last readers finished before this tile's first barrier)
+            if constexpr (NB == 2) commit((int)((jr + 1) & 1));
             // ---- dA = -W G/(A+eps), G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
             if constexpr (!GN) {
                 Frag<T> Bf[2];
@@ -2000,6 +2039,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T, vpart);
         } else {
             __syncthreads();  // all waves' P_K rows in LDS
+            if constexpr (NB == 2) commit((int)((jr + 1) & 1));
             // non-causal: dV^T = U^T P_K^T; dP_K = alpha + v . U (totals)
             for (int q = w; q < 8; q += NW_)
                 dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, nullptr, nullptr, dvp, a.sg.t, t0, a.T, vpart);
@@ -2020,12 +2060,18 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 tsum += softhash_combine<KB, T, SP, NTH>(sShare, sSpK, sSmK, sThK, z, a.L, a.inv_temp, sDproj);
             }
         }
-        __syncthreads();
-        // the next tile's rows go to LDS after the tile's last barrier; its
-        // dK is stored in the next iteration (or after the loop)
-        commit();
+        // one token block: the next tile's rows go to it after the tile's
+        // last barrier.  The tile's dK is stored in the next iteration (or
+        // after the loop).
+        if constexpr (NB == 1) {
+            __syncthreads();
+            commit(0);
+        }
     }
-    if (j0 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, j0 * TT, a.T, xpart);
+    if (j0 < j1) {
+        if constexpr (NB == 2) __syncthreads();  // every wave's dproj rows of the last tile
+        dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, j0 * TT, a.T, xpart);
+    }
     const float ts = block_sum<NTH>(tsum, sRed);
     if (threadIdx.x == 0) a.tpart[((int64_t)(a.M * a.B * a.H + n) * a.nseg + seg) * a.nslice + z] = ts;
 }
@@ -2090,6 +2136,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
     const int64_t ntiles = (a.T + TT - 1) / TT;
+    const int lastv = (int)(a.T - (ntiles - 1) * TT);  // rows of the last tile
     const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
     const T *xp = (const T *)a.q + stream_off(a.sq, n, a.B, a.H);
     T *dxp = BWD ? (T *)a.dq + stream_off(a.sg, n, a.B, a.H) : nullptr;
@@ -2119,7 +2166,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
             project_tile<T, NL>(sX, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, BWD ? sTh : nullptr);
         __syncthreads();
         f32x4 P[2];
-        probs_st<KB>(sSp, sSm, sg, a.S, t0, a.T, P);
+        probs_st<KB>(sSp, sSm, sg, a.S, jt + 1 < ntiles ? TT : lastv, P);
         const int s0 = sg + 4 * g;
         if constexpr (!BWD) {
             for (int nt = 0; nt < 2; ++nt) {
