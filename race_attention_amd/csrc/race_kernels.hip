@@ -1377,29 +1377,42 @@ __device__ void gn_token_terms(const T *sG, const T *sO, const float *sIn, float
 template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr int NW_ = SP / WB;
     static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>();
+    // token block: one tile's staged rows (Q, K, V, dO natural; V, dO
+    // transposed; GN: the O tile and (den, dden) [2][TT]; non-causal: dden [TT])
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
     static constexpr size_t oV = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oG = align16(oV + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oVt = align16(oG + sizeof(T) * TT * LDN);
     static constexpr size_t oGt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oX = align16(oGt + sizeof(T) * D * LDT);
-    static constexpr size_t oDproj = align16(oX + (CAUSAL ? sizeof(T) * TT * LDT : 0));
-    static constexpr size_t oPl = align16(oDproj + sizeof(T) * TT * LDDP);
-    static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oPlT = align16(oPlLo + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oSig = align16(oPlT + sizeof(T) * D * LDDP);  // Q sp, Q sm, Q th, K sp, K sm
-    static constexpr size_t oRed = align16(oSig + sizeof(float) * 5 * TT * LDC);
-    static constexpr size_t oCst = align16(oRed + sizeof(float) * 64 * NW_);
-    static constexpr size_t oHash = align16(oCst + Consts<T>::bytes);
-    static constexpr size_t oPair = align16(oHash + HashOps<T, 4>::bytes);
-    static constexpr size_t oShare = align16(oPair + PairOps<T>::bytes);
-    static constexpr size_t oTok = align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
-    // GN: staged (den, dden) [2][TT], computed (rd, gd) [2][TT], the O tile;
-    // non-causal: staged dden [TT]
-    static constexpr size_t oTokIn = align16(oTok + (GN ? sizeof(float) * 2 * TT : 0));
-    static constexpr size_t oO = align16(oTokIn + (GN || !CAUSAL ? sizeof(float) * 2 * TT : 0));
-    static constexpr size_t bytes = align16(oO + (GN ? sizeof(T) * TT * LDN : 0));
+    static constexpr size_t oO = align16(oGt + sizeof(T) * D * LDT);
+    static constexpr size_t oTokIn = align16(oO + (GN ? sizeof(T) * TT * LDN : 0));
+    static constexpr size_t TB = align16(oTokIn + (GN || !CAUSAL ? sizeof(float) * 2 * TT : 0));
+    // the rest, relative to its start
+    static constexpr size_t rX = 0;
+    static constexpr size_t rDproj = align16(rX + (CAUSAL ? sizeof(T) * TT * LDT : 0));
+    static constexpr size_t rPl = align16(rDproj + sizeof(T) * TT * LDDP);
+    static constexpr size_t rPlLo = align16(rPl + sizeof(T) * NCOL * LDN);
+    static constexpr size_t rPlT = align16(rPlLo + sizeof(T) * NCOL * LDN);
+    static constexpr size_t rSig = align16(rPlT + sizeof(T) * D * LDDP);  // Q sp, Q sm, Q th, K sp, K sm
+    static constexpr size_t rRed = align16(rSig + sizeof(float) * 5 * TT * LDC);
+    static constexpr size_t rCst = align16(rRed + sizeof(float) * 64 * NW_);
+    static constexpr size_t rHash = align16(rCst + Consts<T>::bytes);
+    static constexpr size_t rPair = align16(rHash + HashOps<T, 4>::bytes);
+    static constexpr size_t rShare = align16(rPair + PairOps<T>::bytes);
+    static constexpr size_t rTok = align16(rShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
+    // GN: the computed (rd, gd) [2][TT]
+    static constexpr size_t rEnd = align16(rTok + (GN ? sizeof(float) * 2 * TT : 0));
+    // two token blocks when they cost no workgroup per CU (160 KiB of LDS):
+    // the next tile's rows then go to the other block while this tile still
+    // reads its own, and the barrier ahead of that commit goes away
+    static constexpr size_t LDS_CU = 160 * 1024;
+    static constexpr int NB = LDS_CU / (2 * TB + rEnd) >= LDS_CU / (TB + rEnd) ? 2 : 1;
+    static constexpr size_t R0 = NB * TB;
+    static constexpr size_t oX = R0 + rX, oDproj = R0 + rDproj, oPl = R0 + rPl, oPlLo = R0 + rPlLo, oPlT = R0 + rPlT,
+                            oSig = R0 + rSig, oRed = R0 + rRed, oCst = R0 + rCst, oHash = R0 + rHash, oPair = R0 + rPair,
+                            oShare = R0 + rShare, oTok = R0 + rTok;
+    static constexpr size_t bytes = R0 + rEnd;
 };
 
 // GN (global normalisation, causal only): with rd = 1/max(den, eps) and
@@ -1413,8 +1426,20 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     constexpr int NTASK = CAUSAL ? 11 : 4;  // Q projection (4), K projection (4), X tiles (3)
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
-    T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sV = (T *)(smem + Ly::oV);
-    T *sG = (T *)(smem + Ly::oG), *sVt = (T *)(smem + Ly::oVt), *sGt = (T *)(smem + Ly::oGt);
+    // this tile's token block (block jt & 1 of two; block 0 of one)
+    T *sQ, *sK, *sV, *sG, *sVt, *sGt, *sO;
+    float *sTokIn;
+    auto use_block = [&](int b) {
+        unsigned char *tb = smem + b * Ly::TB;
+        sQ = (T *)(tb + Ly::oQ);
+        sK = (T *)(tb + Ly::oK);
+        sV = (T *)(tb + Ly::oV);
+        sG = (T *)(tb + Ly::oG);
+        sVt = (T *)(tb + Ly::oVt);
+        sGt = (T *)(tb + Ly::oGt);
+        sO = (T *)(tb + Ly::oO);
+        sTokIn = (float *)(tb + Ly::oTokIn);
+    };
     T *sX = (T *)(smem + Ly::oX), *sDproj = (T *)(smem + Ly::oDproj);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo), *sPlT = (T *)(smem + Ly::oPlT);
     float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
@@ -1434,8 +1459,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     const T *gp = (const T *)a.dout + stream_off(a.sdo, n, a.B, a.H);
     T *dqp = (T *)a.dq + stream_off(a.sg, n, a.B, a.H);
     float *xpart = sliced<T, KB>() ? a.dqpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
-    float *sTok = (float *)(smem + Ly::oTok), *sTokIn = (float *)(smem + Ly::oTokIn);
-    T *sO = (T *)(smem + Ly::oO);
+    float *sTok = (float *)(smem + Ly::oTok);
     const T *op = GN ? (const T *)a.out + stream_off(a.so, n, a.B, a.H) : nullptr;
     const float *denp = GN ? a.den + (int64_t)n * a.T : nullptr;
     const float *ddp = (GN || !CAUSAL) && a.dden ? a.dden + (int64_t)n * a.T : nullptr;
@@ -1476,24 +1500,25 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     Prefetch<T, NTH> pq_, pk_, po_;  // po_: GN's O tile
     PrefetchT<T, NTH, NP> pg_, pv_;
     TokPre pt_;
-    // The next tile's rows are committed to LDS right after a tile's last
-    // barrier and before its dQ stores: that commit waits (vmcnt) on loads
-    // issued a tile earlier, never on the stores just issued.
-    auto commit = [&]() {
+    // Writes the prefetched rows to token block b.
+    auto commit = [&](int b) {
+        unsigned char *tb = smem + b * Ly::TB;
+        float *tin = (float *)(tb + Ly::oTokIn);
         wait_vmem();
-        pq_.template commit<NL>(sQ, nullptr);
-        pg_.template commit<NL>(0, sG, sGt);
+        pq_.template commit<NL>((T *)(tb + Ly::oQ), nullptr);
+        pg_.template commit<NL>(0, (T *)(tb + Ly::oG), (T *)(tb + Ly::oGt));
         if constexpr (CAUSAL) {
-            pk_.template commit<NL>(sK, nullptr);
-            pv_.template commit<NL>(1, sV, sVt);
+            pk_.template commit<NL>((T *)(tb + Ly::oK), nullptr);
+            pv_.template commit<NL>(1, (T *)(tb + Ly::oV), (T *)(tb + Ly::oVt));
         }
         if constexpr (GN) {
-            po_.template commit<NL>(sO, nullptr);
-            pt_.commit(sTokIn);
+            po_.template commit<NL>((T *)(tb + Ly::oO), nullptr);
+            pt_.commit(tin);
         } else if constexpr (!CAUSAL) {
-            if (ddp) pt_.commit(sTokIn);
+            if (ddp) pt_.commit(tin);
         }
     };
+    constexpr int NB = Ly::NB;
     if (j0 < j1) {
         pq_.issue(qp, a.sq.t, j0 * TT, a.T);
         pg_.issue(0, gp, a.sdo.t, j0 * TT, a.T);
@@ -1507,28 +1532,39 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         } else if constexpr (!CAUSAL) {
             if (ddp) pt_.issue(ddp, nullptr, j0 * TT, a.T);
         }
-        commit();
+        commit(NB == 2 ? (int)(j0 & 1) : 0);
     }
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
+        use_block(NB == 2 ? (int)(jt & 1) : 0);
         // next tile's rows; the last tile reloads itself (loads stay in range).
         // Issue and commit run every iteration: a commit under a condition
         // leaves the prefetch registers possibly pending at the loop head, and
         // the wait placed there also waits for the previous tile's stores.
         const int64_t tn = (jt + 1 < j1 ? jt + 1 : jt) * TT;
-        pq_.issue(qp, a.sq.t, tn, a.T);
-        pg_.issue(0, gp, a.sdo.t, tn, a.T);
-        if constexpr (CAUSAL) {
-            pk_.issue(kp, a.sk.t, tn, a.T);
-            pv_.issue(1, vp, a.sv.t, tn, a.T);
-        }
-        if constexpr (GN) {
-            po_.issue(op, a.so.t, tn, a.T);
-            pt_.issue(denp, ddp, tn, a.T);
-        } else if constexpr (!CAUSAL) {
-            if (ddp) pt_.issue(ddp, nullptr, tn, a.T);
-        }
+        auto issue = [&]() {
+            pq_.issue(qp, a.sq.t, tn, a.T);
+            pg_.issue(0, gp, a.sdo.t, tn, a.T);
+            if constexpr (CAUSAL) {
+                pk_.issue(kp, a.sk.t, tn, a.T);
+                pv_.issue(1, vp, a.sv.t, tn, a.T);
+            }
+            if constexpr (GN) {
+                po_.issue(op, a.so.t, tn, a.T);
+                pt_.issue(denp, ddp, tn, a.T);
+            } else if constexpr (!CAUSAL) {
+                if (ddp) pt_.issue(ddp, nullptr, tn, a.T);
+            }
+        };
+        // one token block: loads issued ahead of the barrier; two: after it,
+        // with the previous tile's dQ stores issued next, so that both have
+        // the whole tile to complete before the commit's wait at its end
+        if constexpr (NB == 1) issue();
         __syncthreads();
+        if constexpr (NB == 2) {
+            issue();
+            if (jt > j0) dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart);
+        }
         if constexpr (GN) gn_token_terms<T, NL, NW_>(sG, sO, sTokIn, sTok, a.eps, rdw, gdw, t0, a.T);
         for (int q = w; q < NTASK; q += NW_) {
             if (q < 4)
@@ -1538,10 +1574,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             else
                 m_tile<T, NL>(q - 8, sV, sG, sX, nullptr);
         }
-        // dQ of the previous tile, from the dproj rows its softmax backward
-        // left in LDS: independent of the projections, so the two overlap;
-        // the next write of sDproj is two barriers away
-        if (jt > j0) dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart);
+        // one token block: dQ of the previous tile, from the dproj rows its
+        // softmax backward left in LDS, after the projections (they overlap);
+        // the next write of sDproj is a barrier away
+        if constexpr (NB == 1)
+            if (jt > j0) dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart);
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2], tot;
         Frag<T> Pf;
@@ -1625,12 +1662,17 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             __syncthreads();
             tsum += softhash_combine<KB, T, SP, NTH>(sShare, sSpQ, sSmQ, sThQ, z, a.L, a.inv_temp, sDproj);
         }
-        __syncthreads();
-        // the next tile's rows go to LDS after the tile's last barrier; its
-        // dQ is stored in the next iteration (or after the loop)
-        commit();
+        // The next tile's rows go to the other token block (its last readers
+        // finished before this tile's first barrier), or with one block to it
+        // after a barrier.  The tile's dQ is stored in the next iteration (or
+        // after the loop).
+        if constexpr (NB == 1) __syncthreads();
+        commit(NB == 2 ? (int)((jt + 1) & 1) : 0);
     }
-    if (j0 < j1) dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, (j1 - 1) * TT, a.T, xpart);
+    if (j0 < j1) {
+        if constexpr (NB == 2) __syncthreads();  // every wave's dproj rows of the last tile
+        dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, (j1 - 1) * TT, a.T, xpart);
+    }
     float *out = a.rdelta + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     for (int md = 0; md < 4; ++md)
         for (int e = 0; e < 4; ++e) out[sidx(sg + i, 16 * md + 4 * g + e)] = Ut[md][e];
