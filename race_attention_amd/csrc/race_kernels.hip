@@ -1748,7 +1748,10 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     static constexpr size_t rRed = align16(rSig + sizeof(float) * (CAUSAL ? 5 : 3) * TT * LDC);
     static constexpr size_t rCst = align16(rRed + sizeof(float) * 64 * NW_);
     static constexpr size_t rHash = align16(rCst + Consts<T>::bytes);
-    static constexpr size_t rSuf = align16(rHash + HashOps<T, 4>::bytes);
+    // causal: Sc2^T [tau][t] of the last tile, for the dV tiles of the next
+    // iteration (with two token blocks)
+    static constexpr size_t rSc2 = align16(rHash + HashOps<T, 4>::bytes);
+    static constexpr size_t rSuf = align16(rSc2 + (CAUSAL ? sizeof(T) * TT * LDT : 0));
     static constexpr size_t rPair = align16(rSuf + (CAUSAL ? SufOps<T>::bytes : 0));
     static constexpr size_t rShare = align16(rPair + PairOps<T>::bytes);
     static constexpr size_t rEnd = align16(rShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
@@ -1761,20 +1764,39 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     static constexpr size_t oX = R0 + rX, oY = R0 + rY, oPts = R0 + rPts, oWts = R0 + rWts, oUT = R0 + rUT,
                             oDproj = R0 + rDproj, oPl = R0 + rPl, oPlLo = R0 + rPlLo, oPlT = R0 + rPlT,
                             oSig = R0 + rSig, oRed = R0 + rRed, oCst = R0 + rCst, oHash = R0 + rHash, oSuf = R0 + rSuf,
-                            oPair = R0 + rPair, oShare = R0 + rShare;
+                            oPair = R0 + rPair, oShare = R0 + rShare, oSc2 = R0 + rSc2;
     static constexpr size_t bytes = R0 + rEnd;
 };
 
-template <typename T, int SP, bool CAUSAL>
+// Sc2 output tile r = (mt, nt) in {(0,0), (1,0), (1,1)} (the (0,1) tile is
+// zero), masked to t >= tau and stored transposed: sc2[tau][t].
+template <typename T, int SP> __device__ void sc2_tile(int r, const T *Wts, const T *Pts, T *sc2) {
+    constexpr int LDT = ldp_of<T>(TT);
+    const int g = lg(), i = li(), mt = r == 0 ? 0 : 1, nt = r == 2 ? 1 : 0;
+    const T *pw = sw_frag_ptr<T, SP>(Wts, 16 * mt + i), *pp = sw_frag_ptr<T, SP>(Pts, 16 * nt + i);
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kp = 0; kp < SP / 32; ++kp) mma(acc, ld_frag(pw + 32 * kp), ld_frag(pp + 32 * kp));
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (16 * mt + 4 * g + e < 16 * nt + i) acc[e] = 0.f;  // keep t >= tau
+    store4<T>(sc2 + (16 * nt + i) * LDT + 16 * mt + 4 * g, acc);
+}
+
+// SC2 (causal): Sc2 read from its LDS copy sc2 (sc2_tile) instead of being
+// recomputed from Wts.
+template <typename T, int SP, bool CAUSAL, bool SC2 = false>
 __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts, const T *sGt, T *dvp, int64_t st,
-                        int64_t t0, int64_t Tn, float *part) {
+                        int64_t t0, int64_t Tn, float *part, const T *sc2 = nullptr) {
     constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
     const T *pu = sw_frag_ptr<T, SP>(sUT, 16 * md + i), *pp = sw_frag_ptr<T, SP>(Pts, 16 * nt + i);
     f32x4 acc = zero4();
 #pragma unroll
     for (int kp = 0; kp < SP / 32; ++kp) mma(acc, ld_frag(pu + 32 * kp), ld_frag(pp + 32 * kp));
-    if constexpr (CAUSAL) {
+    if constexpr (CAUSAL && SC2) {
+        mma(acc, ld_frag_pi(sGt + (16 * md + i) * LDT), ld_frag_pi(sc2 + (16 * nt + i) * LDT));
+    } else if constexpr (CAUSAL) {
         f32x4 Sc2[2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
@@ -1826,7 +1848,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     };
     T *sX = (T *)(smem + Ly::oX), *sY = (T *)(smem + Ly::oY);
     T *sPts = (T *)(smem + Ly::oPts), *sWts = (T *)(smem + Ly::oWts), *sUT = (T *)(smem + Ly::oUT);
-    T *sDproj = (T *)(smem + Ly::oDproj);
+    T *sDproj = (T *)(smem + Ly::oDproj), *sSc2 = (T *)(smem + Ly::oSc2);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo), *sPlT = (T *)(smem + Ly::oPlT);
     float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
     float *sSpK = sSig, *sSmK = sSig + TT * LDC, *sThK = sSig + 2 * TT * LDC;
@@ -1868,6 +1890,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     if constexpr (CAUSAL) {
         zero_lds<T>(sX, TT * LDT, NTH);
         zero_lds<T>(sY, TT * LDT, NTH);
+        zero_lds<T>(sSc2, TT * LDT, NTH);  // its (t < 16 <= tau) block stays zero
     }
     // reverse carries (U, alpha) after the segment; forward state at the segment end
     const float *rs = a.rstate + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
@@ -1920,6 +1943,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         if constexpr (GN) pt_.commit(tok);
     };
     constexpr int NB = Ly::NB;
+    // causal with two token blocks: a tile's dV is stored in the next
+    // iteration, from Sc2 rows computed once in LDS
+    constexpr bool SCN = CAUSAL && NB == 2;
     if (j0 < j1) {
         const int64_t tl = (j1 - 1) * TT;
         pk_.issue(kp, a.sk.t, tl, a.T);
@@ -1968,6 +1994,16 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         // softmax backward left in LDS: independent of the projections, so the
         // two overlap; the next write of sDproj is two barriers away
         if (jr + 1 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart);
+        // causal, two token blocks: dV of that tile too, from its U, P_K and
+        // Sc2 rows and its dO tile (still in its block: the next commit there
+        // is after this tile's third barrier)
+        if constexpr (SCN)
+            if (jr + 1 < j1) {
+                const T *gtn = (const T *)(smem + ((jr + 1) & 1) * Ly::TB + Ly::oGt);
+                for (int q = w; q < 8; q += NW_)
+                    dv_tile<T, SP, CAUSAL, true>(q >> 1, q & 1, sUT, sPts, nullptr, gtn, dvp, a.sg.t, t0 + TT, a.T,
+                                                 vpart, sSc2);
+            }
         __syncthreads();
         f32x4 PKraw[2], PKr[2];  // fp32 P_K (kept for the softmax backward), operand-rounded P_K
         probs_st<KB>(sSpK, sSmK, sg, a.S, jr + 1 < ntiles ? TT : lastv, PKraw);
@@ -2077,8 +2113,14 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             }
             // ---- U^T[d][s] += sum_t g[t][d] W[t][s]  (the dV tiles read the LDS copy of U)
             for (int md = 0; md < 4; ++md) mma(Ut[md], ld_frag_pi(sGt + (16 * md + i) * LDT), Wf);
-            for (int q = w; q < 8; q += NW_)
-                dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T, vpart);
+            if constexpr (SCN) {
+                // the tile's three Sc2 blocks, once each, for its dV tiles in
+                // the next iteration
+                for (int r = w; r < 3; r += NW_) sc2_tile<T, SP>(r, sWts, sPts, sSc2);
+            } else {
+                for (int q = w; q < 8; q += NW_)
+                    dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T, vpart);
+            }
         } else {
             __syncthreads();  // all waves' P_K rows in LDS
             if constexpr (NB == 2) commit((int)((jr + 1) & 1));
@@ -2111,8 +2153,14 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         }
     }
     if (j0 < j1) {
-        if constexpr (NB == 2) __syncthreads();  // every wave's dproj rows of the last tile
+        if constexpr (NB == 2) __syncthreads();  // every wave's dproj (and Sc2) rows of the last tile
         dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, j0 * TT, a.T, xpart);
+        if constexpr (SCN) {
+            const T *gtn = (const T *)(smem + (j0 & 1) * Ly::TB + Ly::oGt);
+            for (int q = w; q < 8; q += NW_)
+                dv_tile<T, SP, CAUSAL, true>(q >> 1, q & 1, sUT, sPts, nullptr, gtn, dvp, a.sg.t, j0 * TT, a.T, vpart,
+                                             sSc2);
+        }
     }
     const float ts = block_sum<NTH>(tsum, sRed);
     if (threadIdx.x == 0) a.tpart[((int64_t)(a.M * a.B * a.H + n) * a.nseg + seg) * a.nslice + z] = ts;
