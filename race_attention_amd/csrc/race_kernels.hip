@@ -1148,7 +1148,15 @@ template <typename T, int SP, bool CAUSAL, bool GN> struct FwdOutL {
     static constexpr size_t oCst = align16(oPlLo + sizeof(T) * NCOL * LDN);
     // [NW_][TT] per-wave den shares (GN; non-causal F1 when den is requested)
     static constexpr size_t oDen = align16(oCst + Consts<T>::bytes);
-    static constexpr size_t bytes = align16(oDen + (GN || !CAUSAL ? sizeof(float) * NW_ * TT : 0));
+    static constexpr size_t bytes1 = align16(oDen + (GN || !CAUSAL ? sizeof(float) * NW_ * TT : 0));
+    // causal, when it costs no workgroup per CU (160 KiB of LDS): a second
+    // transposed V tile and the tile's Sc^T [t][t'] blocks, computed once
+    static constexpr size_t oVt2 = bytes1;
+    static constexpr size_t oSc = align16(oVt2 + sizeof(T) * D * LDT);
+    static constexpr size_t bytes2 = align16(oSc + sizeof(T) * TT * LDT);
+    static constexpr size_t LDS_CU = 160 * 1024;
+    static constexpr bool SCN = CAUSAL && LDS_CU / bytes2 >= LDS_CU / bytes1;
+    static constexpr size_t bytes = SCN ? bytes2 : bytes1;
 };
 
 // Output tile (d = 16md.., t = 16nt..).  With sDen set, den is summed from
@@ -1188,6 +1196,59 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
 #pragma unroll
         for (int w = 0; w < NW_; ++w) dn += sDen[w * TT + t];
         if (GN && !part) {
+            const float r = 1.0f / fmaxf(dn, eps);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) O[e] *= r;
+        }
+        if (md == 0 && g == 0 && t0 + t < Tn) den[t0 + t] = dn;
+    }
+    if (t0 + t < Tn) {
+        if (part)
+            store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, O);
+        else
+            buf_st4<T>(tile_rsrc(op + t0 * st, st, Tn - t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T)), O);
+    }
+}
+
+// Sc block r = (mt, nt) in {(0,0), (0,1), (1,1)} of Sc[t'][t] = sum_s P_K[t'][s]
+// W[t][s] (the (1,0) block is zero), masked to t' <= t, stored as
+// sc[t][t'] (row t, t' contiguous).
+template <typename T, int SP> __device__ void sc_fwd_tile(int r, const T *Pts, const T *Wts, T *sc) {
+    constexpr int LDT = ldp_of<T>(TT);
+    const int g = lg(), i = li(), mt = r == 2 ? 1 : 0, nt = r == 0 ? 0 : 1;
+    const T *pp = sw_frag_ptr<T, SP>(Pts, 16 * mt + i), *pw = sw_frag_ptr<T, SP>(Wts, 16 * nt + i);
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kp = 0; kp < SP / 32; ++kp) mma(acc, ld_frag(pp + 32 * kp), ld_frag(pw + 32 * kp));
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (16 * mt + 4 * g + e > 16 * nt + i) acc[e] = 0.f;  // keep t' <= t
+    store4<T>(sc + (16 * nt + i) * LDT + 16 * mt + 4 * g, acc);
+}
+// Output tile (md, nt) in two steps: the carried-state part W B_start, then
+// the in-tile part V^T Sc from the Sc rows, the den terms and the store (as
+// fwd_out_tile).
+template <typename T, int SP> __device__ f32x4 fwd_out_partial(int md, int nt, const T *sBT, const T *Wts) {
+    const int i = li();
+    const T *pb = sw_frag_ptr<T, SP>(sBT, 16 * md + i), *pw = sw_frag_ptr<T, SP>(Wts, 16 * nt + i);
+    f32x4 O = zero4();
+#pragma unroll
+    for (int kp = 0; kp < SP / 32; ++kp) mma(O, ld_frag(pb + 32 * kp), ld_frag(pw + 32 * kp));
+    return O;
+}
+template <typename T, int SP, bool GN>
+__device__ void fwd_out_final(int md, int nt, f32x4 O, const T *sVt, const T *sc, T *op, int64_t st, int64_t t0,
+                              int64_t Tn, float *part, const float *sDen, float *den, float eps) {
+    constexpr int LDT = ldp_of<T>(TT);
+    const int g = lg(), i = li();
+    mma(O, ld_frag_pi(sVt + (16 * md + i) * LDT), ld_frag_pi(sc + (16 * nt + i) * LDT));
+    const int t = 16 * nt + i;
+    if (GN && sDen != nullptr) {
+        constexpr int NW_ = SP / WB;
+        float dn = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW_; ++w) dn += sDen[w * TT + t];
+        if (!part) {
             const float r = 1.0f / fmaxf(dn, eps);
 #pragma unroll
             for (int e = 0; e < 4; ++e) O[e] *= r;
@@ -1258,6 +1319,105 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             pk_.issue(kp, a.sk.t, j0 * TT, a.T);
             pv_.issue(0, vp, a.sv.t, j0 * TT, a.T);
         }
+    }
+    if constexpr (Ly::SCN) {
+        // Per tile: commit barrier, projections, barrier, probabilities and
+        // rows, barrier, Sc blocks and the carried-state part of O, barrier,
+        // then the next tile's rows (Q/K alias the P_K / W rows, now read;
+        // V^T goes to the other buffer) and the rest of O.
+        T *sSc = (T *)(smem + Ly::oSc);
+        zero_lds<T>(sSc, TT * LDT, NTH);  // its (t < 16 <= t') block stays zero
+        auto vt_of = [&](int64_t j) { return (T *)(smem + ((j & 1) ? Ly::oVt2 : Ly::oVt)); };
+        auto commit = [&](int64_t j) {  // the prefetched rows, V^T to the buffer of tile j
+            wait_vmem();
+            pq_.template commit<NL>(sQ, nullptr);
+            pk_.template commit<NL>(sK, nullptr);
+            pv_.template commit<NL>(0, nullptr, vt_of(j));
+        };
+        if (j0 < j1) commit(j0);
+        constexpr int NQ = (8 + NW_ - 1) / NW_;  // output tiles per wave
+        for (int64_t jt = j0; jt < j1; ++jt) {
+            const int64_t t0 = jt * TT;
+            // next tile's rows; the last tile reloads itself (loads stay in
+            // range, issue and commit unconditional)
+            const int64_t tn = (jt + 1 < j1 ? jt + 1 : jt) * TT;
+            sVt = vt_of(jt);
+            __syncthreads();  // this tile's rows in LDS; the previous tile's O rows are done
+            pq_.issue(qp, a.sq.t, tn, a.T);
+            pk_.issue(kp, a.sk.t, tn, a.T);
+            pv_.issue(0, vp, a.sv.t, tn, a.T);
+            for (int q = w; q < 8; q += NW_) {
+                if (q < 4)
+                    project_tile<T, NL>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+                else
+                    project_tile<T, NL>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
+            }
+            __syncthreads();
+            f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
+            Frag<T> Pf;
+            probs_st<KB>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
+            if constexpr (CAUSAL) {
+                probs_st<KB>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
+                for (int nt = 0; nt < 2; ++nt)
+                    for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
+                Pf = token_operand<T>(PK, cst);
+                for (int nt = 0; nt < 2; ++nt) {
+                    Acum[nt] = zero4();
+                    mma(Acum[nt], Pf, cst.tri_op(nt));
+                }
+                tot = zero4();
+                mma(tot, Pf, cst.ones());
+            }
+            if constexpr (GN) {
+                // W = P_Q; this wave's share of den(t) = sum_s P_Q A_s(t)
+                for (int nt = 0; nt < 2; ++nt) {
+                    float dp = 0.f;
+                    for (int e = 0; e < 4; ++e) {
+                        dp += PQ[nt][e] * ((float)a0[e] + Acum[nt][e]);
+                        W[nt][e] = PQ[nt][e];
+                    }
+                    dp = xor32_sum(xor16_sum(dp));
+                    if (g == 0) sDen[w * TT + 16 * nt + i] = dp;
+                }
+            } else {
+                // W = P_Q / (A(t) + eps)
+                float ae[4];
+                for (int e = 0; e < 4; ++e) ae[e] = (float)a0[e] + a.eps;
+                for (int nt = 0; nt < 2; ++nt)
+                    for (int e = 0; e < 4; ++e) W[nt][e] = PQ[nt][e] * rcp(CAUSAL ? ae[e] + Acum[nt][e] : ae[e]);
+                if constexpr (!CAUSAL) {
+                    if (want_den)  // this wave's share of den(t) = sum_s P_Q A_s
+                        for (int nt = 0; nt < 2; ++nt) {
+                            float dp = 0.f;
+                            for (int e = 0; e < 4; ++e) dp += PQ[nt][e] * (float)a0[e];
+                            dp = xor32_sum(xor16_sum(dp));
+                            if (g == 0) sDen[w * TT + 16 * nt + i] = dp;
+                        }
+                }
+            }
+            store_ts<T, SP>(sWts, sw, W);
+            store_ts<T, SP>(sPts, sw, PK);
+            store_ds<T, SP>(sBT, sw, Bc);
+            __syncthreads();
+            for (int r = w; r < 3; r += NW_) sc_fwd_tile<T, SP>(r, sPts, sWts, sSc);
+            f32x4 Op[NQ];
+#pragma unroll
+            for (int k = 0; k < NQ; ++k)
+                if (w + k * NW_ < 8) Op[k] = fwd_out_partial<T, SP>((w + k * NW_) >> 1, (w + k * NW_) & 1, sBT, sWts);
+            // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
+            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, ld_frag_pi(sVt + (16 * md + i) * LDT));
+            for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
+            __syncthreads();  // Sc rows in LDS; the P_K / W / B rows are read
+            commit(jt + 1);
+#pragma unroll
+            for (int k = 0; k < NQ; ++k) {
+                const int q = w + k * NW_;
+                if (q < 8)
+                    fwd_out_final<T, SP, GN>(q >> 1, q & 1, Op[k], sVt, sSc, op, a.so.t, t0, a.T, opart, sDen, denp,
+                                             a.eps);
+            }
+        }
+        return;
     }
     for (int64_t jt = j0; jt < j1; ++jt) {
         const int64_t t0 = jt * TT;
