@@ -2151,9 +2151,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 m_tile<T, NL>(q - 8, sV, sG, sX, sY);
         }
         // dK of the tile after this one (walking down), from the dproj rows its
-        // softmax backward left in LDS: independent of the projections, so the
-        // two overlap; the next write of sDproj is two barriers away
-        if (jr + 1 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart);
+        // softmax backward left in LDS, independent of the projections and the
+        // probabilities it runs beside; the next write of sDproj is after the
+        // third barrier
+        if constexpr (!SCN)
+            if (jr + 1 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart);
         // causal, two token blocks: dV of that tile too, from its U, P_K and
         // Sc2 rows and its dO tile (still in its block: the next commit there
         // is after this tile's third barrier)
@@ -2165,6 +2167,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                                                  vpart, sSc2);
             }
         __syncthreads();
+        if constexpr (SCN)
+            if (jr + 1 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart);
         f32x4 PKraw[2], PKr[2];  // fp32 P_K (kept for the softmax backward), operand-rounded P_K
         probs_st<KB>(sSpK, sSmK, sg, a.S, jr + 1 < ntiles ? TT : lastv, PKraw);
         PKr[0] = PKraw[0];
