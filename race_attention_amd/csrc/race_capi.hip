@@ -35,13 +35,19 @@ int ok() {
     return RACE_OK;
 }
 
-constexpr int64_t kTargetBlocks = 2048;  // workgroups per scan phase (256 CUs x 8)
+constexpr int64_t kTargetBlocks = 2048;  // workgroups per forward phase (256 CUs x 8)
+// The backward's tile kernels hold one workgroup per CU (LDS): fewer, longer
+// segments there amortise each workgroup's set-up (state rows, planes,
+// constant tables, the first tile's load) over more tiles.  A backward
+// segment is fmul forward segments, so its boundaries are forward ones.
+constexpr int64_t kTargetBlocksBwd = 512;
 
 struct Plan {
     int SP = 0, S = 0, R = 0, nslice = 1, Spad = 0;
     bool parts = false;  // fp32 partial outputs + slice sum (sliced<T, KB>() instantiations)
     int64_t N = 0, ntiles = 0;
     int nseg = 0, tps = 0;
+    int fnseg = 0, fmul = 1;  // forward segments; forward segments per segment of this plan
     size_t esize = 0;
     size_t state_bytes = 0, fws = 0, bws = 0;
     size_t fws_core = 0, bws_core = 0, part_bytes = 0;  // partial-output buffers follow the core
@@ -65,7 +71,7 @@ void slice_plan(int dtype, int K, int S, int &SP, int &nslice) {
     nslice = (S + SP - 1) / SP;
 }
 
-int make_plan(const race_desc *d, Plan &p) {
+int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
     if (!d) return fail(RACE_E_INVALID, "descriptor is NULL");
     if (d->dtype != RACE_DTYPE_F32 && d->dtype != RACE_DTYPE_BF16)
         return fail(RACE_E_INVALID, "dtype %d is not RACE_DTYPE_F32 or RACE_DTYPE_BF16", d->dtype);
@@ -102,10 +108,22 @@ int make_plan(const race_desc *d, Plan &p) {
     const int64_t nseg = (p.ntiles + p.tps - 1) / p.tps;
     if (nseg > (1 << 30)) return fail(RACE_E_UNSUPPORTED, "too many segments");
     p.nseg = (int)nseg;
+    p.fnseg = p.nseg;
     p.esize = d->dtype == RACE_DTYPE_BF16 ? 2 : 4;
     const size_t blk = (size_t)p.Spad * SROW;
-    p.state_bytes = (size_t)p.N * (p.nseg + 1) * blk * sizeof(double);
-    p.fws_core = align16((size_t)p.N * p.nseg * blk * sizeof(double));
+    p.state_bytes = (size_t)p.N * (p.fnseg + 1) * blk * sizeof(double);
+    p.fws_core = align16((size_t)p.N * p.fnseg * blk * sizeof(double));
+    if (bwd && d->seg_tiles <= 0) {
+        // backward segments of fmul forward ones (one segment when that
+        // covers the sequence); explicit seg_tiles keeps the forward's
+        const int64_t m = (int64_t)p.fnseg * p.N * p.nslice / kTargetBlocksBwd;
+        if (m > 1) {
+            const int64_t tb = (int64_t)p.tps * m;
+            p.fmul = m < p.fnseg ? (int)m : p.fnseg;
+            p.tps = (int)(tb < p.ntiles ? tb : p.ntiles);
+            p.nseg = (int)((p.ntiles + p.tps - 1) / p.tps);
+        }
+    }
     p.bws_core = 2 * (size_t)p.N * p.nseg * blk * sizeof(float) +
                  align16(2 * (size_t)p.N * p.nseg * p.nslice * sizeof(float));
     p.part_bytes = p.parts ? (size_t)p.nslice * p.N * d->T * D * sizeof(float) : 0;
@@ -157,6 +175,8 @@ Args base_args(const race_desc *d, const Plan &p, const float *planes) {
     a.inv_temp = d->inv_temp;
     a.nseg = p.nseg;
     a.tps = p.tps;
+    a.fnseg = p.fnseg;
+    a.fmul = p.fmul;
     a.nslice = p.nslice;
     a.Spad = p.Spad;
     return a;
@@ -426,7 +446,7 @@ size_t race_fwd_workspace_bytes(const race_desc *d) {
 
 size_t race_bwd_workspace_bytes(const race_desc *d) {
     Plan p;
-    if (make_plan(d, p) != RACE_OK) return 0;
+    if (make_plan(d, p, true) != RACE_OK) return 0;
     ok();
     return p.bws;
 }
@@ -460,7 +480,7 @@ int race_bwd(const race_desc *d, const void *q, const void *k, const void *v, co
              const void *dout, const void *state, void *dq, void *dk, void *dv, float *grad_inv_temp, void *ws,
              size_t ws_bytes, void *stream) {
     Plan p;
-    int rc = make_plan(d, p);
+    int rc = make_plan(d, p, true);
     if (rc) return rc;
     Args a;
     if ((rc = bwd_args(d, p, q, k, v, planes, dout, state, dq, dk, dv, ws, ws_bytes, a))) return rc;
@@ -552,7 +572,7 @@ int race_bwd_ex(const race_desc *d, const void *q, const void *k, const void *v,
                 const float *kmask, const void *dout, const float *dden, const void *state, void *dq, void *dk,
                 void *dv, float *grad_inv_temp, void *ws, size_t ws_bytes, void *stream) {
     Plan p;
-    int rc = make_plan(d, p);
+    int rc = make_plan(d, p, true);
     if (rc) return rc;
     if (d->causal && (kmask || dden))
         return fail(RACE_E_UNSUPPORTED, "key weights and den are implemented for the non-causal operator");
@@ -575,7 +595,7 @@ size_t race_fwd_global_workspace_bytes(const race_desc *d) {
 
 size_t race_bwd_global_workspace_bytes(const race_desc *d) {
     Plan p;
-    if (make_plan(d, p) != RACE_OK) return 0;
+    if (make_plan(d, p, true) != RACE_OK) return 0;
     ok();
     return p.gbws;
 }
@@ -612,7 +632,7 @@ int race_bwd_global(const race_desc *d, const void *q, const void *k, const void
                     const void *out, const float *den, const void *dout, const float *dden, const void *state,
                     void *dq, void *dk, void *dv, float *grad_beta, void *ws, size_t ws_bytes, void *stream) {
     Plan p;
-    int rc = make_plan(d, p);
+    int rc = make_plan(d, p, true);
     if (rc || (rc = check_gn(d))) return rc;
     if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
         (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) ||

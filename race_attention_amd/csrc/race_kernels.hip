@@ -58,8 +58,11 @@ struct Args {
     int64_t T;
     float eps, inv_temp;
     int nseg, tps;   // segments per stream, tiles per segment
+    // forward segments (fstate rows per stream - 1) and forward segments per
+    // segment: the backward's segment s starts at forward boundary s * fmul
+    int fnseg, fmul;
     int nslice, Spad;  // bucket slices (grid z) of SP buckets each; Spad = nslice * SP
-    double *fstate;  // [N][nseg+1][Spad][D+1] exclusive segment prefixes; [nseg] = totals
+    double *fstate;  // [N][fnseg+1][Spad][D+1] exclusive forward-segment prefixes; [fnseg] = totals
     double *fdelta;  // [N][nseg][Spad][D+1]
     float *rdelta;   // [N][nseg][Spad][D+1]  per-segment (U, alpha) sums
     float *rstate;   // [N][nseg][Spad][D+1]  exclusive suffixes (non-causal: totals)
@@ -1301,7 +1304,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
     // carried state: causal = prefix at the segment start, non-causal = totals.
     // B in bucket-row layout: lane holds B[s = sw + 4g + e][d = 16md + i]
-    const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * a.Spad * SROW;
+    const double *st = a.fstate + ((int64_t)n * (a.fnseg + 1) + (CAUSAL ? seg * a.fmul : a.fnseg)) * a.Spad * SROW;
     f32x4 Bc[4];
     double a0[4];
     for (int e = 0; e < 4; ++e) {
@@ -1642,7 +1645,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     zero_lds<T>(sDproj, TT * LDDP, NTH);
     if constexpr (CAUSAL) zero_lds<T>(sX, TT * LDT, NTH);
     // forward state in d-row layout: lane holds B^T[d = 16md + 4g + e][s = sw + i]
-    const double *st = a.fstate + ((int64_t)n * (a.nseg + 1) + (CAUSAL ? seg : a.nseg)) * a.Spad * SROW;
+    const double *st = a.fstate + ((int64_t)n * (a.fnseg + 1) + (CAUSAL ? seg * a.fmul : a.fnseg)) * a.Spad * SROW;
     f32x4 Bt[4], Ut[4];
     double a0[4], al[4];
     for (int md = 0; md < 4; ++md) {
@@ -2054,7 +2057,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     }
     // reverse carries (U, alpha) after the segment; forward state at the segment end
     const float *rs = a.rstate + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
-    const double *fs = a.fstate + ((int64_t)n * (a.nseg + 1) + seg + 1) * a.Spad * SROW;
+    const double *fs =
+        a.fstate + ((int64_t)n * (a.fnseg + 1) + min((seg + 1) * a.fmul, a.fnseg)) * a.Spad * SROW;
     f32x4 Ut[4];  // U^T[d = 16md + 4g + e][s = sw + i]
     // Forward state, walked back from the segment end.  B only feeds the
     // G product's operand: bf16 carries it in fp32 MFMA accumulators and

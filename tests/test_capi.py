@@ -56,7 +56,12 @@ def test_plan_sizes_c4():
     # N=8 streams, 256 segments (+1 total), 128 buckets x 65 fp64
     assert sb == 8 * 257 * 128 * 65 * 8
     assert lib.race_fwd_workspace_bytes(ctypes.byref(d)) == 8 * 256 * 128 * 65 * 8
-    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) >= 2 * 8 * 256 * 128 * 65 * 4
+    # the backward runs 64 segments of 4 forward ones (512 workgroups): (U, alpha)
+    # sums and suffixes fp32, and the [2][N][nseg][nslice] temperature partials
+    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 64 * 128 * 65 * 4 + 2 * 8 * 64 * 4
+    # an explicit seg_tiles keeps the forward's segmentation in the backward
+    d.seg_tiles = 128
+    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 256 * 128 * 65 * 4 + 2 * 8 * 256 * 4
 
 
 @pytest.mark.parametrize("field,value,code,msg", [
@@ -103,7 +108,9 @@ def test_sliced_plans(dtype, K, L, M, B, H, T, spad):
     nseg = sb // (N * row * 8) - 1
     part = (spad // (32 if dtype == _lib.RACE_DTYPE_F32 else 128)) * N * T * 64 * 4
     assert fw >= N * nseg * row * 8 + part
-    assert bw >= 2 * N * nseg * row * 4 + 3 * part
+    # the backward runs between 1 and nseg segments (whole forward segments)
+    nslice = spad // (32 if dtype == _lib.RACE_DTYPE_F32 else 128)
+    assert 2 * N * row * 4 + 3 * part <= bw <= 2 * N * nseg * row * 4 + 2 * N * nseg * nslice * 4 + 16 + 3 * part
 
 
 def test_null_and_misaligned_pointers_rejected():
