@@ -56,7 +56,8 @@ typedef struct race_desc {
     int64_t o_stride[4];      /* forward output */
     int64_t do_stride[4];     /* upstream gradient */
     int64_t g_stride[4];      /* dq, dk, dv */
-    int32_t seg_tiles;        /* 32-token tiles per scan segment; 0 = automatic */
+    int32_t seg_tiles;        /* 32-token tiles per scan segment, forward and backward; 0 = automatic
+                                 (the backward then joins whole forward segments into fewer ones) */
     int32_t phases;           /* 0 = run every kernel of the call; otherwise a bitmask of
                                  RACE_PHASE_* to run a subset (per-kernel timing); subsets of
                                  one call must be enqueued in phase order on one stream */
