@@ -1908,8 +1908,10 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     static constexpr size_t rPlLo = align16(rPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t rPlT = align16(rPlLo + sizeof(T) * NCOL * LDN);
     static constexpr size_t rSig = align16(rPlT + sizeof(T) * D * LDDP);  // K sp, K sm, K th, Q sp, Q sm
-    static constexpr size_t rRed = align16(rSig + sizeof(float) * (CAUSAL ? 5 : 3) * TT * LDC);
-    static constexpr size_t rCst = align16(rRed + sizeof(float) * 64 * NW_);
+    // the end-of-kernel block sum's scratch [64 * NW_] reuses the sigmoid rows
+    static_assert(64 * NW_ <= (CAUSAL ? 5 : 3) * TT * LDC, "block-sum scratch inside the sigmoid rows");
+    static constexpr size_t rRed = rSig;
+    static constexpr size_t rCst = align16(rSig + sizeof(float) * (CAUSAL ? 5 : 3) * TT * LDC);
     static constexpr size_t rHash = align16(rCst + Consts<T>::bytes);
     // causal: Sc2^T [tau][t] of the last tile, for the dV tiles of the next
     // iteration (with two token blocks)
