@@ -100,7 +100,8 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
     if (d->seg_tiles > 0) {
         tps = d->seg_tiles;
     } else {
-        int64_t nseg = (kTargetBlocks + p.N - 1) / p.N;
+        const int64_t per = p.N * p.nslice;  // workgroups per segment index
+        int64_t nseg = (kTargetBlocks + per - 1) / per;
         if (nseg > p.ntiles) nseg = p.ntiles;
         tps = (p.ntiles + nseg - 1) / nseg;
     }

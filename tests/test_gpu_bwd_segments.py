@@ -2,8 +2,9 @@
 joins fmul forward segments into one (fewer, longer workgroups; its
 boundaries are forward boundaries, so it reads the forward state rows
 s * fmul and min((s + 1) * fmul, fnseg)).  At B=1, H=4, N=8192 the forward
-runs 256 one-tile segments per stream and the backward 128 two-tile (bf16)
-or 32 eight-tile (fp32, four bucket slices) segments.
+runs 256 one-tile segments per stream (bf16; fp32, with four bucket slices,
+128 two-tile ones) and the backward 128 two-tile (bf16) or 32 eight-tile
+(fp32) segments.
 
 Checked: the auto plan against the same backward on the forward's
 segmentation (explicit seg_tiles), and against the fp64 oracle for F1
@@ -22,9 +23,8 @@ pytestmark = pytest.mark.gpu
 B, T, H, L, K = 1, 8192, 4, 8, 4
 
 
-def _bwd_ws(q, dtype_id, causal, seg):
+def _desc(dtype_id, causal, seg):
     from race_attention_amd import _lib
-    lib = _lib.load()
     d = _lib.RaceDesc()
     d.M, d.B, d.T, d.H, d.D = 1, B, T, H, 64
     d.L, d.K, d.causal, d.dtype = L, K, causal, dtype_id
@@ -35,7 +35,23 @@ def _bwd_ws(q, dtype_id, causal, seg):
         arr[2] = H * 64
         arr[3] = 64
     d.seg_tiles = seg
-    return lib.race_bwd_workspace_bytes(ctypes.byref(d))
+    return d
+
+
+def _bwd_ws(dtype_id, causal, seg):
+    from race_attention_amd import _lib
+    return _lib.load().race_bwd_workspace_bytes(ctypes.byref(_desc(dtype_id, causal, seg)))
+
+
+def _fwd_tps(dtype_id, causal):
+    """Tiles per segment of the automatic forward plan, from its state size
+    ([N][nseg+1][Spad][D+1] fp64)."""
+    from race_attention_amd import _lib
+    sb = _lib.load().race_state_bytes(ctypes.byref(_desc(dtype_id, causal, 0)))
+    spad = 128
+    nseg = sb // (H * spad * 65 * 8) - 1
+    ntiles = T // 32
+    return -(-ntiles // nseg)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
@@ -45,14 +61,15 @@ def test_coarser_backward_segments(dev, dtype, causal):
     from race_attention_amd import _lib
     from race_attention_amd.functional import race_bwd_raw, race_fwd_raw
     did = _lib.RACE_DTYPE_BF16 if dtype == torch.bfloat16 else _lib.RACE_DTYPE_F32
-    # the auto backward plan has fewer segments than the forward's (one tile each here)
-    assert _bwd_ws(None, did, int(causal), 0) < _bwd_ws(None, did, int(causal), 1)
+    tps = _fwd_tps(did, int(causal))  # explicit, the backward keeps the forward's segments
+    # the auto backward plan has fewer segments than the forward's
+    assert _bwd_ws(did, int(causal), 0) < _bwd_ws(did, int(causal), tps)
     q, k, v, do, planes = make_case(B=B, T=T, H=H, L=L, K=K, dtype=dtype, seed=11, unit=dtype == torch.bfloat16)
     it = 1.0 / math.sqrt(64) if causal else 0.8
     qd, kd, vd, dod, pd = [x.to(dev) for x in (q, k, v, do, planes)]
     out, st = race_fwd_raw(qd, kd, vd, pd, L=L, K=K, causal=causal, inv_temp=it)
     auto = race_bwd_raw(qd, kd, vd, pd, dod, st, L=L, K=K, causal=causal, inv_temp=it)
-    fine = race_bwd_raw(qd, kd, vd, pd, dod, st, L=L, K=K, causal=causal, inv_temp=it, seg_tiles=1)
+    fine = race_bwd_raw(qd, kd, vd, pd, dod, st, L=L, K=K, causal=causal, inv_temp=it, seg_tiles=tps)
     torch.cuda.synchronize()
     pl = planes.double().numpy()
     ref = ro.race_backward(to64(q), to64(k), to64(v), to64(do), pl, causal=causal, inv_temp=it, with_l1=True)
