@@ -924,6 +924,23 @@ template <typename T, class NL = NatL<T, false>> __device__ void m_tile(int q, c
     }
 }
 
+// Block r of X (as m_tile) and, from the same product, its transposed copy
+// Y[tau][t] (one 2-byte store per element): no second product.
+template <typename T, class NL = NatL<T, false>>
+__device__ void m_tile_xy(int r, const T *sV, const T *sG, T *X, T *Y) {
+    constexpr int LDT = ldp_of<T>(TT);
+    const int g = lg(), i = li();
+    const int mt = r == 2 ? 1 : 0, nt = r == 0 ? 0 : 1;
+    f32x4 acc = zero4();
+    nat_mma<NL>(acc, sV, 16 * mt, sG, 16 * nt);  // [tau = 16mt+4g+e][t = 16nt+i]
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (16 * mt + 4 * g + e > 16 * nt + i) acc[e] = 0.f;
+    store4<T>(X + (16 * nt + i) * LDT + 16 * mt + 4 * g, acc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Y[(16 * mt + 4 * g + e) * LDT + 16 * nt + i] = from_f32<T>(acc[e]);
+}
+
 template <typename T> __device__ void zero_lds(T *p, int n, int nth) {
     for (int idx = threadIdx.x; idx < n; idx += nth) p[idx] = from_f32<T>(0.f);
 }
@@ -1996,7 +2013,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     using NL = NatL<T, true>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
                   LDS_ = Ly::LDS_;
-    constexpr int NTASK = CAUSAL ? 14 : 4;  // K projection (4), Q projection (4), X and Y tiles (6)
+    constexpr int NTASK = CAUSAL ? 11 : 4;  // K projection (4), Q projection (4), X and Y blocks (3)
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     // this tile's token block (block jr & 1 of two; block 0 of one)
     T *sQ, *sK, *sV, *sG, *sVt, *sGt;
@@ -2154,7 +2171,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             else if (q < 8)
                 project_tile<T, NL>(sQ, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
             else
-                m_tile<T, NL>(q - 8, sV, sG, sX, sY);
+                m_tile_xy<T, NL>(q - 8, sV, sG, sX, sY);
         }
         // dK of the tile after this one (walking down), from the dproj rows its
         // softmax backward left in LDS, independent of the projections and the
