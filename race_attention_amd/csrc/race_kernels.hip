@@ -1965,20 +1965,16 @@ template <typename T, int SP> __device__ void sc2_tile(int r, const T *Wts, cons
     store4<T>(sc2 + (16 * nt + i) * LDT + 16 * mt + 4 * g, acc);
 }
 
-// SC2 (causal): Sc2 read from its LDS copy sc2 (sc2_tile) instead of being
-// recomputed from Wts.
-template <typename T, int SP, bool CAUSAL, bool SC2 = false>
+template <typename T, int SP, bool CAUSAL>
 __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts, const T *sGt, T *dvp, int64_t st,
-                        int64_t t0, int64_t Tn, float *part, const T *sc2 = nullptr) {
+                        int64_t t0, int64_t Tn, float *part) {
     constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
     const T *pu = sw_frag_ptr<T, SP>(sUT, 16 * md + i), *pp = sw_frag_ptr<T, SP>(Pts, 16 * nt + i);
     f32x4 acc = zero4();
 #pragma unroll
     for (int kp = 0; kp < SP / 32; ++kp) mma(acc, ld_frag(pu + 32 * kp), ld_frag(pp + 32 * kp));
-    if constexpr (CAUSAL && SC2) {
-        mma(acc, ld_frag_pi(sGt + (16 * md + i) * LDT), ld_frag_pi(sc2 + (16 * nt + i) * LDT));
-    } else if constexpr (CAUSAL) {
+    if constexpr (CAUSAL) {
         f32x4 Sc2[2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
@@ -1994,6 +1990,32 @@ __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts
         }
         mma(acc, ld_frag_pi(sGt + (16 * md + i) * LDT), frag_acc<T>(Sc2[0], Sc2[1]));
     }
+    const int t = 16 * nt + i;
+    if (t0 + t < Tn) {
+        if (part)
+            store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, acc);
+        else
+            store4<T>(at_bytes(dvp + t0 * st, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
+    }
+}
+
+// dV tile (md, nt) in two steps: the carried part U P_K (over all buckets,
+// from the U and P_K rows), then, once the tile's Sc2 rows exist (sc2_tile),
+// the in-tile part g^T Sc2 and the store.
+template <typename T, int SP> __device__ f32x4 dv_part(int md, int nt, const T *sUT, const T *Pts) {
+    const int i = li();
+    const T *pu = sw_frag_ptr<T, SP>(sUT, 16 * md + i), *pp = sw_frag_ptr<T, SP>(Pts, 16 * nt + i);
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kp = 0; kp < SP / 32; ++kp) mma(acc, ld_frag(pu + 32 * kp), ld_frag(pp + 32 * kp));
+    return acc;
+}
+template <typename T>
+__device__ void dv_finish(int md, int nt, f32x4 acc, const T *sGt, const T *sc2, T *dvp, int64_t st, int64_t t0,
+                          int64_t Tn, float *part) {
+    constexpr int LDT = ldp_of<T>(TT);
+    const int g = lg(), i = li();
+    mma(acc, ld_frag_pi(sGt + (16 * md + i) * LDT), ld_frag_pi(sc2 + (16 * nt + i) * LDT));
     const int t = 16 * nt + i;
     if (t0 + t < Tn) {
         if (part)
@@ -2129,6 +2151,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     // causal with two token blocks: a tile's dV is stored in the next
     // iteration, from Sc2 rows computed once in LDS
     constexpr bool SCN = CAUSAL && NB == 2;
+    constexpr int NQD = (8 + NW_ - 1) / NW_;  // dV tiles per wave
+    f32x4 dvacc[NQD];                          // SCN: carried part of the last tile's dV tiles
+#pragma unroll
+    for (int k = 0; k < NQD; ++k) dvacc[k] = zero4();
     if (j0 < j1) {
         const int64_t tl = (j1 - 1) * TT;
         pk_.issue(kp, a.sk.t, tl, a.T);
@@ -2179,15 +2205,18 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         // third barrier
         if constexpr (!SCN)
             if (jr + 1 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart);
-        // causal, two token blocks: dV of that tile too, from its U, P_K and
-        // Sc2 rows and its dO tile (still in its block: the next commit there
-        // is after this tile's third barrier)
+        // causal, two token blocks: dV of that tile too, its carried part
+        // (computed last iteration) plus the in-tile part from its Sc2 rows and
+        // its dO tile (still in its block: the next commit there is after this
+        // tile's third barrier)
         if constexpr (SCN)
             if (jr + 1 < j1) {
                 const T *gtn = (const T *)(smem + ((jr + 1) & 1) * Ly::TB + Ly::oGt);
-                for (int q = w; q < 8; q += NW_)
-                    dv_tile<T, SP, CAUSAL, true>(q >> 1, q & 1, sUT, sPts, nullptr, gtn, dvp, a.sg.t, t0 + TT, a.T,
-                                                 vpart, sSc2);
+#pragma unroll
+                for (int k = 0; k < NQD; ++k)
+                    if (w + k * NW_ < 8)
+                        dv_finish<T>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gtn, sSc2, dvp, a.sg.t, t0 + TT,
+                                     a.T, vpart);
             }
         __syncthreads();
         if constexpr (SCN)
@@ -2304,6 +2333,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 // the tile's three Sc2 blocks, once each, for its dV tiles in
                 // the next iteration
                 for (int r = w; r < 3; r += NW_) sc2_tile<T, SP>(r, sWts, sPts, sSc2);
+                // and the carried part of its dV tiles (U and P_K rows of this tile)
+#pragma unroll
+                for (int k = 0; k < NQD; ++k)
+                    if (w + k * NW_ < 8) dvacc[k] = dv_part<T, SP>((w + k * NW_) >> 1, (w + k * NW_) & 1, sUT, sPts);
             } else {
                 for (int q = w; q < 8; q += NW_)
                     dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T, vpart);
@@ -2344,9 +2377,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, j0 * TT, a.T, xpart);
         if constexpr (SCN) {
             const T *gtn = (const T *)(smem + (j0 & 1) * Ly::TB + Ly::oGt);
-            for (int q = w; q < 8; q += NW_)
-                dv_tile<T, SP, CAUSAL, true>(q >> 1, q & 1, sUT, sPts, nullptr, gtn, dvp, a.sg.t, j0 * TT, a.T, vpart,
-                                             sSc2);
+#pragma unroll
+            for (int k = 0; k < NQD; ++k)
+                if (w + k * NW_ < 8)
+                    dv_finish<T>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gtn, sSc2, dvp, a.sg.t, j0 * TT, a.T,
+                                 vpart);
         }
     }
     const float ts = block_sum<NTH>(tsum, sRed);
