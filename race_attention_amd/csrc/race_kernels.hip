@@ -2200,9 +2200,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 m_tile_xy<T, NL>(q - 8, sV, sG, sX, sY);
         }
         // dK of the tile after this one (walking down), from the dproj rows its
-        // softmax backward left in LDS, independent of the projections and the
-        // probabilities it runs beside; the next write of sDproj is after the
-        // third barrier
+        // softmax backward left in LDS: with one token block beside the
+        // projections, with two (below) beside the probabilities, after the
+        // second barrier; the next write of sDproj is after the third
         if constexpr (!SCN)
             if (jr + 1 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart);
         // causal, two token blocks: dV of that tile too, its carried part
