@@ -864,6 +864,43 @@ template <typename T, int N> __device__ __forceinline__ void store_ts(T *dst, in
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) store4<T>(p + 16 * sw_ld<T, N>() * nt, X[nt]);
 }
+// The wave's token operand of what store_ts wrote (bucket s = sw + i, k =
+// token t in pi order: 4g + j, then 16 + 4g + j), read back with two LDS
+// transpose loads (ds_read_b64_tr_b16: in each 16-lane group, lane 4e + q
+// reads 4 elements and lane 4q' + c receives element c of lanes q' + 4e,
+// e = 0..3).  bf16 only; the values are the ones store_ts rounded.
+template <int N> __device__ __forceinline__ Frag<bf16> ts_operand_tr(const bf16 *base, int sw) {
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    const int g = lg(), p = li();
+    const int c = sw + 4 * (p & 3);
+    const bf16 *a = base + sw_off<bf16, N>(4 * g + (p >> 2), c);
+    const bf16 *b = base + sw_off<bf16, N>(16 + 4 * g + (p >> 2), c);
+    const v4s ra = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)a);
+    const v4s rb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)b);
+    const bf16x4 x = __builtin_bit_cast(bf16x4, ra), y = __builtin_bit_cast(bf16x4, rb);
+    Frag<bf16> f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f.v[j] = x[j];
+        f.v[j + 4] = y[j];
+    }
+    return f;
+}
+// token operand of a bucket-row tile pair X that the wave also stores to its
+// [t][s] rows: bf16 stores first and reads the operand back transposed
+template <typename T, int N>
+__device__ __forceinline__ Frag<T> store_ts_operand(T *dst, int sw, const f32x4 (&X)[2], const Consts<T> &cst,
+                                                    const PairOps<T> &po) {
+    if constexpr (is_bf16<T>()) {
+        store_ts<T, N>(dst, sw, X);
+        return ts_operand_tr<N>(dst, sw);
+    } else {
+        const Frag<T> f = token_operand<T>(X, cst, po);
+        store_ts<T, N>(dst, sw, X);
+        return f;
+    }
+}
 // bucket-row [s][d] carry (lane holds [s = sw + 4g + e][d = 16md + i]) ->
 // [d][s] LDS array (s contiguous)
 template <typename T, int N> __device__ __forceinline__ void store_ds(T *dst, int sw, const f32x4 (&X)[4]) {
@@ -2235,8 +2272,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         }
         for (int nt = 0; nt < 2; ++nt)
             for (int e = 0; e < 4; ++e) PKr[nt][e] = as_operand<T>(PKr[nt][e]);
-        const Frag<T> Pf = token_operand<T>(PKr, cst, po);
-        store_ts<T, SP>(sPts, sw, PKr);
+        const Frag<T> Pf = store_ts_operand<T, SP>(sPts, sw, PKr, cst, po);
         f32x4 dPK[2];
         if constexpr (CAUSAL) {
             f32x4 Wi[2];  // W / (A + eps), the factor of dA
@@ -2252,8 +2288,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                         dA[nt][e] = gd * PQ[nt][e];
                     }
                 }
-                store_ts<T, SP>(sWts, sw, W);
-                Wf = token_operand<T>(W, cst, po);
+                Wf = store_ts_operand<T, SP>(sWts, sw, W, cst, po);
             } else {
                 f32x4 PQ[2], Acum[2], W[2], tot, dB[4];
                 probs_st<KB>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
@@ -2283,8 +2318,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                         W[nt][e] = PQ[nt][e] * inv;
                         Wi[nt][e] = W[nt][e] * inv;
                     }
-                store_ts<T, SP>(sWts, sw, W);
-                Wf = token_operand<T>(W, cst, po);
+                Wf = store_ts_operand<T, SP>(sWts, sw, W, cst, po);
             }
             store_ut<T, SP>(sUT, sw, Ut, cst, po);
             __syncthreads();  // all waves' P_K, W, U rows in LDS
