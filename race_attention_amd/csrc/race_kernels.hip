@@ -890,13 +890,12 @@ template <int N> __device__ __forceinline__ Frag<bf16> ts_operand_tr(const bf16 
 // token operand of a bucket-row tile pair X that the wave also stores to its
 // [t][s] rows: bf16 stores first and reads the operand back transposed
 template <typename T, int N>
-__device__ __forceinline__ Frag<T> store_ts_operand(T *dst, int sw, const f32x4 (&X)[2], const Consts<T> &cst,
-                                                    const PairOps<T> &po) {
+__device__ __forceinline__ Frag<T> store_ts_operand(T *dst, int sw, const f32x4 (&X)[2], const Consts<T> &cst) {
     if constexpr (is_bf16<T>()) {
         store_ts<T, N>(dst, sw, X);
         return ts_operand_tr<N>(dst, sw);
     } else {
-        const Frag<T> f = token_operand<T>(X, cst, po);
+        const Frag<T> f = token_operand<T>(X, cst);
         store_ts<T, N>(dst, sw, X);
         return f;
     }
@@ -1417,7 +1416,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
                 probs_st<KB>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
                 for (int nt = 0; nt < 2; ++nt)
                     for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
-                Pf = token_operand<T>(PK, cst);
+                Pf = store_ts_operand<T, SP>(sPts, sw, PK, cst);
                 for (int nt = 0; nt < 2; ++nt) {
                     Acum[nt] = zero4();
                     mma(Acum[nt], Pf, cst.tri_op(nt));
@@ -1453,7 +1452,6 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
                 }
             }
             store_ts<T, SP>(sWts, sw, W);
-            store_ts<T, SP>(sPts, sw, PK);
             store_ds<T, SP>(sBT, sw, Bc);
             __syncthreads();
             for (int r = w; r < 3; r += NW_) sc_fwd_tile<T, SP>(r, sPts, sWts, sSc);
@@ -2272,7 +2270,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         }
         for (int nt = 0; nt < 2; ++nt)
             for (int e = 0; e < 4; ++e) PKr[nt][e] = as_operand<T>(PKr[nt][e]);
-        const Frag<T> Pf = store_ts_operand<T, SP>(sPts, sw, PKr, cst, po);
+        const Frag<T> Pf = store_ts_operand<T, SP>(sPts, sw, PKr, cst);
         f32x4 dPK[2];
         if constexpr (CAUSAL) {
             f32x4 Wi[2];  // W / (A + eps), the factor of dA
@@ -2288,7 +2286,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                         dA[nt][e] = gd * PQ[nt][e];
                     }
                 }
-                Wf = store_ts_operand<T, SP>(sWts, sw, W, cst, po);
+                Wf = store_ts_operand<T, SP>(sWts, sw, W, cst);
             } else {
                 f32x4 PQ[2], Acum[2], W[2], tot, dB[4];
                 probs_st<KB>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
@@ -2318,7 +2316,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                         W[nt][e] = PQ[nt][e] * inv;
                         Wi[nt][e] = W[nt][e] * inv;
                     }
-                Wf = store_ts_operand<T, SP>(sWts, sw, W, cst, po);
+                Wf = store_ts_operand<T, SP>(sWts, sw, W, cst);
             }
             store_ut<T, SP>(sUT, sw, Ut, cst, po);
             __syncthreads();  // all waves' P_K, W, U rows in LDS
