@@ -523,18 +523,6 @@ template <typename T> struct Consts {
     __device__ __forceinline__ Frag<T> ones() const { return ld_frag_pi(tri + (TT - 1) * LDT); }
     __device__ __forceinline__ Frag4<T> ident() const { return ld_frag16(id + li() * LDI); }
 };
-// suf[t][tau] = (tau >= t): column t = 16nt + i of a token suffix
-template <typename T> struct SufOps {
-    static constexpr int LDT = ldp_of<T>(TT);
-    static constexpr size_t bytes = sizeof(T) * TT * LDT;
-    const T *suf;
-    __device__ __forceinline__ void init(T *buf, int nth) {
-        for (int idx = threadIdx.x; idx < TT * LDT; idx += nth)
-            buf[idx] = from_f32<T>(idx % LDT >= idx / LDT ? 1.f : 0.f);
-        suf = buf;
-    }
-    __device__ __forceinline__ Frag<T> op(int nt) const { return ld_frag_pi(suf + (16 * nt + li()) * LDT); }
-};
 // bf16 pairwise transposes: id[n][k] = (k == n), 32 x 32.  With the pair
 // operand A = frag_acc(X0, X1) of two bucket-row tiles, A . lo() = X0^T and
 // A . hi() = X1^T: every k slot holds data, none is zero padding.
@@ -673,16 +661,6 @@ __device__ __forceinline__ Frag<T> token_operand(const f32x4 (&X)[2], const Cons
     else
         return token_operand<T>(X, cst);
 }
-// bf16 parts of a tile pair: hi = bf16(X), lo = bf16(X - hi); hi + lo holds
-// X to ~2^-16 relative, so products of both keep fp32 accuracy
-__device__ __forceinline__ void split_pair(const f32x4 &x0, const f32x4 &x1, Frag<bf16> &hi, Frag<bf16> &lo) {
-    hi = frag_acc<bf16>(x0, x1);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        lo.v[j] = (bf16)(x0[j] - (float)hi.v[j]);
-        lo.v[j + 4] = (bf16)(x1[j] - (float)hi.v[j + 4]);
-    }
-}
 
 // c += A . X^T over the wave's 16 buckets, X a bucket-row tile taken as the B
 // operand (column t, k = s); bf16 runs A . hi + A . lo as one 32-deep product
@@ -783,26 +761,15 @@ __device__ float softhash_combine(const float *share, const float *sp, const flo
 }
 
 // Inclusive token suffix Y (plus y0, the lane's per-bucket carry) and token
-// totals of a bucket-row tile pair on the matrix cores; bf16 splits X into two
-// bf16 parts (fp32-accurate sums).
-template <typename T>
-__device__ void suffix_totals(const f32x4 (&X)[2], const Consts<T> &cst, const SufOps<T> &suf, const PairOps<T> &po,
-                              const f32x4 &y0, f32x4 (&Y)[2], f32x4 &tot) {
-    Y[0] = y0;
-    Y[1] = y0;
-    tot = zero4();
-    auto add = [&](const Frag<T> &F) {
+// totals of a bucket-row tile pair (lane holds X[s = 4g + e][t = 16nt + i]):
+// fp32 scans and sums over the 16 lanes of each row (DPP), tile 1 first.
+__device__ __forceinline__ void suffix_totals(const f32x4 (&X)[2], const f32x4 &y0, f32x4 (&Y)[2], f32x4 &tot) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) mma(Y[nt], F, suf.op(nt));
-        mma(tot, F, cst.ones());
-    };
-    if constexpr (is_bf16<T>()) {
-        Frag<bf16> hi, lo;
-        split_pair(X[0], X[1], hi, lo);
-        add(transpose_pair(hi, po));
-        add(transpose_pair(lo, po));
-    } else {
-        add(token_operand<T>(X, cst));
+    for (int e = 0; e < 4; ++e) {
+        const float t0 = row_sum(X[0][e]), t1 = row_sum(X[1][e]);
+        Y[1][e] = y0[e] + row_suffix(X[1][e]);
+        Y[0][e] = (y0[e] + t1) + row_suffix(X[0][e]);
+        tot[e] = t0 + t1;
     }
 }
 // token totals only (lane: bucket 4g + e), fp32 row sums over the 16 lanes
@@ -1968,8 +1935,7 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     // causal: Sc2^T [tau][t] of the last tile, for the dV tiles of the next
     // iteration (with two token blocks)
     static constexpr size_t rSc2 = align16(rHash + HashOps<T, 4>::bytes);
-    static constexpr size_t rSuf = align16(rSc2 + (CAUSAL ? sizeof(T) * TT * LDT : 0));
-    static constexpr size_t rPair = align16(rSuf + (CAUSAL ? SufOps<T>::bytes : 0));
+    static constexpr size_t rPair = align16(rSc2 + (CAUSAL ? sizeof(T) * TT * LDT : 0));
     static constexpr size_t rShare = align16(rPair + PairOps<T>::bytes);
     static constexpr size_t rEnd = align16(rShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
     // two token blocks when they cost no workgroup per CU (160 KiB of LDS):
@@ -1980,7 +1946,7 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     static constexpr size_t R0 = NB * TB;
     static constexpr size_t oX = R0 + rX, oY = R0 + rY, oPts = R0 + rPts, oWts = R0 + rWts, oUT = R0 + rUT,
                             oDproj = R0 + rDproj, oPl = R0 + rPl, oPlLo = R0 + rPlLo, oPlT = R0 + rPlT,
-                            oSig = R0 + rSig, oRed = R0 + rRed, oCst = R0 + rCst, oHash = R0 + rHash, oSuf = R0 + rSuf,
+                            oSig = R0 + rSig, oRed = R0 + rRed, oCst = R0 + rCst, oHash = R0 + rHash,
                             oPair = R0 + rPair, oShare = R0 + rShare, oSc2 = R0 + rSc2;
     static constexpr size_t bytes = R0 + rEnd;
 };
@@ -2122,8 +2088,6 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         wh.init(sg);
     PairOps<T> po;
     po.init((T *)(smem + Ly::oPair), NTH);
-    SufOps<T> sufo;
-    if constexpr (CAUSAL) sufo.init((T *)(smem + Ly::oSuf), NTH);
     load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
     zero_lds<T>(sDproj, TT * LDDP, NTH);
     if constexpr (CAUSAL) {
@@ -2349,7 +2313,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             // ---- dP_K[tau][s] = alpha(tau) + sum_d U[s][d] v_tau[d] + sum_{t >= tau} W[t][s] M[tau][t]
             {
                 f32x4 alpha[2], tdA;  // alpha(tau): the suffix from this tile on
-                suffix_totals<T>(dA, cst, sufo, po, al, alpha, tdA);
+                suffix_totals(dA, al, alpha, tdA);
                 const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
                 for (int nt = 0; nt < 2; ++nt) {
                     dPK[nt] = alpha[nt];
