@@ -16,7 +16,7 @@ from the timed region itself.  The CPU baseline times the reference's own CPU
 path (aten + kernels/cpu/race_pref.cpp compiled from source) on a bounded
 sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--seq N] [--no-cpu-baseline] [--max-n]
+    python bench.py [--steps K] [--warmup W] [--seq N] [--no-cpu-baseline] [--no-max-n]
                     [--copy-calib MIB] [--workload c4|c5] [--mode f1|global]
 
 --workload c5 times the attention core of BASELINE configs[4] instead (the
@@ -78,7 +78,8 @@ def parse():
     ap.add_argument("--heads", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=65536, help="tokens of one head per timed CPU run")
-    ap.add_argument("--max-n", action="store_true", help="also bisect the longest sequence that fits in HBM")
+    ap.add_argument("--no-max-n", dest="max_n", action="store_false",
+                    help="skip the bisection of the longest sequence that fits in HBM (run by default for c4 f1)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="finish with a device-to-device copy of MIB MiB (PMC calibration)")
     ap.add_argument("--workload", choices=("c4", "c5", "c3-step", "c5-step"), default="c4")
@@ -339,6 +340,31 @@ def algorithmic_bytes(name, tok_heads, D, esize, mode="f1"):
     return units.get(name, 0) * unit
 
 
+def mfma_figures(ms, tok_heads, D, L, K, workload, T):
+    """Matrix-core figures of the aggregation kernel (k_fwd_reduce: the
+    segment sums S = P_K^T [V, 1] with the K projection that feeds them).
+    algorithmic: 2 S (d+1) + 2 d L K flops per token-head over the kernel's
+    HIP-event time, against the dense bf16 peak.  counter: the share of
+    SIMD cycles the matrix cores were busy (SQ_VALU_MFMA_BUSY_CYCLES over the
+    launch's SIMD cycles), read from the committed rocprofv3 summary of the
+    same kernel and workload when there is one (every issued MFMA counts,
+    including transposes and hi/lo splits)."""
+    S = L << K
+    per_th = 2 * S * (D + 1) + 2 * D * L * K
+    tf = tok_heads * per_th / (ms * 1e-3) / 1e12
+    out = {"kernel": "fwd_reduce", "what": "bucket aggregation P_K^T [V, 1] per segment (+ K projection)",
+           "algorithmic_flops_per_token_head": per_th, "algorithmic_achieved": round(tf, 2),
+           "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "algorithmic_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 5),
+           "counter_busy_frac": None}
+    cfile = os.path.join(ROOT, "profiles", f"mfma_fwd_reduce_{workload}.txt")
+    if os.path.exists(cfile) and (workload != "c4" or T == 1 << 20):
+        for ln in open(cfile):
+            if ln.startswith("mfma_busy_frac"):
+                out["counter_busy_frac"] = float(ln.split("=")[1])
+                out["counter_source"] = os.path.relpath(cfile, ROOT)
+    return out
+
+
 def cpu_baseline(sample_T, H_full, D=64, L=8, K=4, reps=16):
     """Reference CPU path (aten + race_pref.cpp from source) on one head of
     sample_T tokens of the same workload, run reps times (default 16 x 65536
@@ -407,8 +433,8 @@ def max_seq_bisect(H, D, L, K, dev, limit_tokens=1 << 27):
             torch.cuda.synchronize()
             del st
             return True
-        except (torch.cuda.OutOfMemoryError, RuntimeError):
-            return False
+        except torch.cuda.OutOfMemoryError:
+            return False  # only an allocation failure means "does not fit"; anything else fails the run
         finally:
             del bufs
             torch.cuda.empty_cache()
@@ -505,6 +531,8 @@ def main():
                            "frac": round(value / (tokens / (all_bytes / (HBM_PEAK_GBS * 1e9))), 4)},
         "kernels": kernels,
     }
+    if "fwd_reduce" in per and args.mode == "f1":
+        res["mfma"] = mfma_figures(per["fwd_reduce"], tok_heads, D, L, K, args.workload, T)
     if args.copy_calib:
         n = args.copy_calib << 20
         src = torch.ones(n, dtype=torch.uint8, device=dev)
@@ -513,10 +541,15 @@ def main():
         torch.cuda.synchronize()
         res["copy_calib_bytes"] = n
         del src, dst
-    if args.max_n:
+    if args.max_n and args.workload == "c4" and args.mode == "f1":
         del step, q, k, v, do
         torch.cuda.empty_cache()
+        print("bench: max-N bisection", file=sys.stderr, flush=True)
+        t_mx = time.perf_counter()
         res["max_seq_len_fwd_bwd"] = max_seq_bisect(H, D, L, K, dev)
+        res["max_seq_len_note"] = (f"longest N (multiple of 2^16) whose layer fwd+bwd (B=1 H={H} d={D} K={K} L={L} "
+                                   "bf16: separate Q, K, V, dO, O, dQ, dK, dV, state, workspace) allocates and runs "
+                                   f"in this GPU's HBM; bisection took {time.perf_counter() - t_mx:.1f} s")
     if not args.no_cpu_baseline:
         print("bench: CPU baseline", file=sys.stderr, flush=True)
         if args.mode == "global":

@@ -136,6 +136,11 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
     return RACE_OK;
 }
 
+// Largest token stride (elements) whose lane byte offsets inside a 32-token
+// tile, ((TT - 1) * stride + D) * esize, fit the kernels' 32-bit offsets and
+// the 2^31 - 1 byte record size of k_fwd_out's buffer stores.
+int64_t max_token_stride(size_t esize) { return (0x7FFFFFFFll / (int64_t)esize - D) / (TT - 1); }
+
 int check_tensor(const char *name, const void *ptr, const int64_t *st, size_t esize, int64_t T) {
     if (!ptr) return fail(RACE_E_INVALID, "%s is NULL", name);
     if ((uintptr_t)ptr % 16) return fail(RACE_E_INVALID, "%s is not 16-byte aligned", name);
@@ -147,8 +152,26 @@ int check_tensor(const char *name, const void *ptr, const int64_t *st, size_t es
     }
     if (T > 1 && st[2] < D)
         return fail(RACE_E_INVALID, "%s token stride %lld overlaps rows", name, (long long)st[2]);
-    if (st[2] >= (int64_t(1) << 26))  // lane offsets within a 32-token tile are 32-bit
-        return fail(RACE_E_UNSUPPORTED, "%s token stride %lld exceeds 2^26 elements", name, (long long)st[2]);
+    if (st[2] > max_token_stride(esize))  // lane byte offsets within a 32-token tile are 32-bit
+        return fail(RACE_E_UNSUPPORTED, "%s token stride %lld exceeds %lld elements (32-bit tile offsets)", name,
+                    (long long)st[2], (long long)max_token_stride(esize));
+    return RACE_OK;
+}
+
+// A tensor the call writes: as check_tensor, and no two (m, b, t, h) rows
+// may share memory through a zero stride or heads closer than D elements
+// (workgroups of different streams would race on the same rows).
+int check_out(const char *name, const void *ptr, const int64_t *st, size_t esize, const race_desc *d) {
+    int rc = check_tensor(name, ptr, st, esize, d->T);
+    if (rc) return rc;
+    const int64_t sz[4] = {d->M, d->B, d->T, d->H};
+    static const char *dim[4] = {"M", "B", "T", "H"};
+    for (int j = 0; j < 4; ++j)
+        if (sz[j] > 1 && st[j] == 0)
+            return fail(RACE_E_INVALID, "%s is written but has stride 0 over %s (size %lld)", name, dim[j],
+                        (long long)sz[j]);
+    if (d->H > 1 && st[3] < D)
+        return fail(RACE_E_INVALID, "%s head stride %lld overlaps rows (< D)", name, (long long)st[3]);
     return RACE_OK;
 }
 
@@ -378,8 +401,8 @@ int bwd_args(const race_desc *d, const Plan &p, const void *q, const void *k, co
     if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
         (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) ||
         (rc = check_tensor("dout", dout, d->do_stride, p.esize, d->T)) ||
-        (rc = check_tensor("dq", dq, d->g_stride, p.esize, d->T)) || (rc = check_tensor("dk", dk, d->g_stride, p.esize, d->T)) ||
-        (rc = check_tensor("dv", dv, d->g_stride, p.esize, d->T)))
+        (rc = check_out("dq", dq, d->g_stride, p.esize, d)) || (rc = check_out("dk", dk, d->g_stride, p.esize, d)) ||
+        (rc = check_out("dv", dv, d->g_stride, p.esize, d)))
         return rc;
     if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
     if (!state) return fail(RACE_E_INVALID, "state is NULL");
@@ -458,7 +481,7 @@ int race_fwd(const race_desc *d, const void *q, const void *k, const void *v, co
     int rc = make_plan(d, p);
     if (rc) return rc;
     if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
-        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) || (rc = check_tensor("out", out, d->o_stride, p.esize, d->T)))
+        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) || (rc = check_out("out", out, d->o_stride, p.esize, d)))
         return rc;
     if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
     if (!state) return fail(RACE_E_INVALID, "state is NULL");
@@ -515,7 +538,7 @@ int race_probs_bwd(const race_desc *d, const void *x, const float *planes, const
     Plan p;
     int rc = make_plan(d, p);
     if (rc || (rc = check_tensor("x", x, d->q_stride, p.esize, d->T)) || (rc = check_den("dP", dP)) ||
-        (rc = check_tensor("dx", dx, d->g_stride, p.esize, d->T)))
+        (rc = check_out("dx", dx, d->g_stride, p.esize, d)))
         return rc;
     if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
     const size_t need = probs_ws_core(p) + p.part_bytes;
@@ -546,7 +569,7 @@ int race_fwd_ex(const race_desc *d, const void *q, const void *k, const void *v,
     if (d->causal && (kmask || den))
         return fail(RACE_E_UNSUPPORTED, "key weights and den are implemented for the non-causal operator");
     if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
-        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) || (rc = check_tensor("out", out, d->o_stride, p.esize, d->T)) ||
+        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) || (rc = check_out("out", out, d->o_stride, p.esize, d)) ||
         (kmask && (rc = check_den("kmask", kmask))) || (den && (rc = check_den("den", den))))
         return rc;
     if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
@@ -607,7 +630,7 @@ int race_fwd_global(const race_desc *d, const void *q, const void *k, const void
     int rc = make_plan(d, p);
     if (rc || (rc = check_gn(d))) return rc;
     if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
-        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) || (rc = check_tensor("out", out, d->o_stride, p.esize, d->T)) ||
+        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) || (rc = check_out("out", out, d->o_stride, p.esize, d)) ||
         (rc = check_den("den", den)))
         return rc;
     if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
@@ -639,8 +662,8 @@ int race_bwd_global(const race_desc *d, const void *q, const void *k, const void
         (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) ||
         (rc = check_tensor("out", out, d->o_stride, p.esize, d->T)) ||
         (rc = check_tensor("dout", dout, d->do_stride, p.esize, d->T)) ||
-        (rc = check_tensor("dq", dq, d->g_stride, p.esize, d->T)) || (rc = check_tensor("dk", dk, d->g_stride, p.esize, d->T)) ||
-        (rc = check_tensor("dv", dv, d->g_stride, p.esize, d->T)) || (rc = check_den("den", den)) ||
+        (rc = check_out("dq", dq, d->g_stride, p.esize, d)) || (rc = check_out("dk", dk, d->g_stride, p.esize, d)) ||
+        (rc = check_out("dv", dv, d->g_stride, p.esize, d)) || (rc = check_den("den", den)) ||
         (dden && (rc = check_den("dden", dden))))
         return rc;
     if (!planes) return fail(RACE_E_INVALID, "planes is NULL");

@@ -10,6 +10,15 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X) and the built HIP library")
+    config.addinivalue_line("markers", "timing: asserts measured cycle ratios; always collected last")
+
+
+def pytest_collection_modifyitems(session, config, items):
+    """Tests that assert timing ratios run after every other test (stable
+    order otherwise): a timing outlier on some box must not stop a -x run
+    before the parity tests."""
+    items[:] = ([it for it in items if it.get_closest_marker("timing") is None] +
+                [it for it in items if it.get_closest_marker("timing") is not None])
 
 
 def gpu_available() -> bool:

@@ -36,3 +36,37 @@ def make_case(M=1, B=1, T=64, H=2, D=64, L=8, K=4, dtype=torch.bfloat16, seed=0,
 
 def to64(x: torch.Tensor) -> np.ndarray:
     return x.detach().to(torch.float64).cpu().numpy()
+
+
+def run_gpu(q, k, v, do, planes, *, L, K, causal, inv_temp, dev, seg_tiles=0, eps=1e-6):
+    from race_attention_amd.functional import race_bwd_raw, race_fwd_raw
+    qd, kd, vd, dod, pd = [x.to(dev) for x in (q, k, v, do, planes)]
+    out, state = race_fwd_raw(qd, kd, vd, pd, L=L, K=K, causal=causal, inv_temp=inv_temp, seg_tiles=seg_tiles,
+                              eps=eps)
+    dq, dk, dv, git = race_bwd_raw(qd, kd, vd, pd, dod, state, L=L, K=K, causal=causal, inv_temp=inv_temp,
+                                   seg_tiles=seg_tiles, eps=eps)
+    torch.cuda.synchronize()
+    return out.cpu(), dq.cpu(), dk.cpu(), dv.cpu(), float(git.cpu())
+
+
+def run_oracle(q, k, v, do, planes, *, causal, inv_temp, eps=1e-6):
+    from oracle import race_oracle as ro
+    o = ro.race_forward(to64(q), to64(k), to64(v), planes.double().numpy(), causal=causal, inv_temp=inv_temp,
+                        eps=eps)
+    dq, dk, dv, git, gabs = ro.race_backward(to64(q), to64(k), to64(v), to64(do), planes.double().numpy(),
+                                             causal=causal, inv_temp=inv_temp, with_l1=True, eps=eps)
+    return o, dq, dk, dv, git, gabs
+
+
+def compare(case_name, gpu, ref, tol):
+    """relerr = max|a-b|/max|b| per tensor.  d(inv_temp) is one sum over all
+    tokens: fp32 compares |a-b|/|b|; bf16 compares |a-b| against the l1 mass
+    sum|du*th| of its terms (ref[5]), the analogue of the max-norm metric for
+    a reduction whose terms cancel."""
+    names = ("out", "dq", "dk", "dv")
+    errs = {nm: relerr(to64(a), b) for nm, a, b in zip(names, gpu[:4], ref[:4])}
+    scale = abs(ref[4]) if (tol < 1e-3 or len(ref) < 6) else ref[5]
+    errs["dinv_temp"] = abs(gpu[4] - ref[4]) / (scale + 1e-30)
+    print(f"[{case_name}] " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
+    for nm, e in errs.items():
+        assert e <= tol, f"{case_name}: {nm} relerr {e:.3e} > {tol:.1e}"

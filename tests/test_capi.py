@@ -44,6 +44,7 @@ def _desc(**kw):
     for j in range(4):
         d.q_stride[j] = d.k_stride[j] = d.v_stride[j] = d.o_stride[j] = d.do_stride[j] = d.g_stride[j] = 0
     d.q_stride[2] = d.k_stride[2] = d.v_stride[2] = d.o_stride[2] = d.do_stride[2] = d.g_stride[2] = 512
+    d.q_stride[3] = d.k_stride[3] = d.v_stride[3] = d.o_stride[3] = d.do_stride[3] = d.g_stride[3] = 64
     for k, v in kw.items():
         setattr(d, k, v)
     return d
@@ -131,6 +132,59 @@ def test_workspace_too_small_rejected():
     p = ctypes.c_void_p(256)
     rc = lib.race_fwd(ctypes.byref(d), p, p, p, p, p, p, p, 16, None)
     assert rc == -3 and "workspace" in _lib.last_error()
+
+
+def _max_stride(esize):
+    # ((32 - 1) * stride + 64) * esize <= 2^31 - 1, rounded down to a 16-byte multiple
+    m = ((2 ** 31 - 1) // esize - 64) // 31
+    return m - m % (16 // esize)
+
+
+@pytest.mark.parametrize("dtype,esize", [(_lib.RACE_DTYPE_BF16, 2), (_lib.RACE_DTYPE_F32, 4)])
+def test_token_stride_byte_bound(dtype, esize):
+    """Lane byte offsets inside a 32-token tile are 32-bit: the largest token
+    stride whose tile spans at most 2^31 - 1 bytes is accepted (the call then
+    stops at the too-small workspace), the next 16-byte multiple is rejected."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    for which in ("q_stride", "o_stride"):
+        d = _desc(T=64, H=1, dtype=dtype)
+        getattr(d, which)[2] = _max_stride(esize)
+        rc = lib.race_fwd(ctypes.byref(d), p, p, p, p, p, p, p, 16, None)
+        assert rc == -3 and "workspace" in _lib.last_error()
+        getattr(d, which)[2] = _max_stride(esize) + 16 // esize
+        rc = lib.race_fwd(ctypes.byref(d), p, p, p, p, p, p, p, 16, None)
+        assert rc == -2 and "32-bit tile offsets" in _lib.last_error()
+
+
+@pytest.mark.parametrize("field,j,value,msg", [
+    ("o_stride", 3, 0, "stride 0 over H"),
+    ("o_stride", 3, 32, "head stride"),
+    ("g_stride", 0, 0, "stride 0 over M"),
+    ("g_stride", 1, 0, "stride 0 over B"),
+])
+def test_written_tensors_must_not_alias(field, j, value, msg):
+    """Outputs with a zero stride over a dimension of size > 1, or heads
+    closer than D elements, would have workgroups of different streams write
+    the same rows: rejected (inputs may alias, e.g. the stride-0 M expand)."""
+    lib = _lib.load()
+    d = _desc(T=64, M=2, B=2)
+    for f in ("q_stride", "k_stride", "v_stride", "o_stride", "do_stride", "g_stride"):
+        getattr(d, f)[0], getattr(d, f)[1] = 2 * 64 * 512, 64 * 512
+    getattr(d, field)[j] = value
+    p = ctypes.c_void_p(256)
+    if field == "o_stride":
+        rc = lib.race_fwd(ctypes.byref(d), p, p, p, p, p, p, p, 16, None)
+    else:
+        rc = lib.race_bwd(ctypes.byref(d), p, p, p, p, p, p, p, p, p, None, p, 16, None)
+    assert rc == -1 and msg in _lib.last_error()
+    # inputs may share rows: a stride-0 M expand of q is accepted
+    d = _desc(T=64, M=2, B=2)
+    for f in ("k_stride", "v_stride", "o_stride", "do_stride", "g_stride"):
+        getattr(d, f)[0], getattr(d, f)[1] = 2 * 64 * 512, 64 * 512
+    d.q_stride[0], d.q_stride[1] = 0, 64 * 512
+    rc = lib.race_fwd(ctypes.byref(d), p, p, p, p, p, p, p, 16, None)
+    assert rc == -3
 
 
 def test_prefix_mean_argument_checks():

@@ -18,6 +18,7 @@ import numpy as np
 import pytest
 import torch
 
+import longseq
 from helpers import TOL, relerr, to64
 
 pytestmark = pytest.mark.gpu
@@ -100,3 +101,30 @@ def test_c4_full_size(dev, oracle):
     print(f"[C4 last token] causal-vs-noncausal={e_nc:.2e} causal-vs-fp64={e_np:.2e} "
           f"noncausal-vs-fp64={e_nc_np:.2e}", flush=True)
     assert max(e_nc, e_np, e_nc_np) <= TOL[torch.bfloat16]
+
+
+def test_c4_backward_suffix(dev):
+    """dO zero before the last T0 tokens: the reverse carries (U, alpha) of
+    every earlier token -- 63 of the backward's 64 joined segments -- are
+    constants of the last T0 tokens; dK and dV at sampled early tokens against
+    the fp64 closed form (tests/longseq.py), dQ exactly zero there."""
+    from race_attention_amd.functional import race_bwd_raw, race_fwd_raw
+    it = 1.0 / math.sqrt(D)
+    q, k, v, _, planes = _inputs(dev)
+    g = torch.Generator(device=dev).manual_seed(31)
+    do = torch.zeros(1, B, T, H, D, device=dev, dtype=torch.bfloat16)
+    do[:, :, T - T0:] = torch.randn(1, B, T0, H, D, device=dev, generator=g).to(torch.bfloat16)
+    pd = planes.to(dev)
+    _, state = race_fwd_raw(q, k, v, pd, L=L, K=K, causal=True, inv_temp=it)
+    dq, dk, dv, _ = race_bwd_raw(q, k, v, pd, do, state, L=L, K=K, causal=True, inv_temp=it)
+    torch.cuda.synchronize()
+    assert torch.isfinite(dk).all() and torch.isfinite(dv).all()
+    assert not dq[:, :, :T - T0].any(), "dq nonzero before the last T0 tokens"
+    taus = longseq.sample_taus(T, T0)
+    pl0 = planes[0].double().to(dev)
+    for h in (0, 3, 7):
+        dK_ref, dV_ref = longseq.suffix_reference(q, k, v, do, h, pl0, it, L, K, T0, EPS, taus)
+        e_k = relerr(to64(dk[0, 0, taus, h]), dK_ref.cpu().numpy())
+        e_v = relerr(to64(dv[0, 0, taus, h]), dV_ref.cpu().numpy())
+        print(f"[C4 suffix h={h}, {len(taus)} early tokens] dk={e_k:.2e} dv={e_v:.2e}", flush=True)
+        assert max(e_k, e_v) <= TOL[torch.bfloat16]

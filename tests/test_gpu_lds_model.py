@@ -19,7 +19,9 @@ sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 import lds_layouts as L  # noqa: E402
 from lds_model import R128_PASSES, ways  # noqa: E402
 
-pytestmark = pytest.mark.gpu
+# cycle-ratio thresholds: collected after every parity test (tests/conftest.py),
+# so that a timing outlier under pytest -x cannot leave a parity test unrun
+pytestmark = [pytest.mark.gpu, pytest.mark.timing]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 OPS = {"r32": 0, "r64": 1, "r128": 2, "w32": 3, "w64": 4, "w128": 5, "rpi": 6}

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import TOL, make_case, relerr, to64
+from helpers import TOL, compare, make_case, relerr, run_gpu, run_oracle, to64
 
 pytestmark = pytest.mark.gpu
 
@@ -113,40 +113,6 @@ def test_mfma_fragment_layout(dev, dtype):
     assert relerr(Ct.cpu(), ref.T) < tol
 
 
-def _run_gpu(q, k, v, do, planes, *, L, K, causal, inv_temp, dev, seg_tiles=0, eps=1e-6):
-    from race_attention_amd.functional import race_bwd_raw, race_fwd_raw
-    qd, kd, vd, dod, pd = [x.to(dev) for x in (q, k, v, do, planes)]
-    out, state = race_fwd_raw(qd, kd, vd, pd, L=L, K=K, causal=causal, inv_temp=inv_temp, seg_tiles=seg_tiles,
-                              eps=eps)
-    dq, dk, dv, git = race_bwd_raw(qd, kd, vd, pd, dod, state, L=L, K=K, causal=causal, inv_temp=inv_temp,
-                                   seg_tiles=seg_tiles, eps=eps)
-    torch.cuda.synchronize()
-    return out.cpu(), dq.cpu(), dk.cpu(), dv.cpu(), float(git.cpu())
-
-
-def _run_oracle(q, k, v, do, planes, *, causal, inv_temp, eps=1e-6):
-    from oracle import race_oracle as ro
-    o = ro.race_forward(to64(q), to64(k), to64(v), planes.double().numpy(), causal=causal, inv_temp=inv_temp,
-                        eps=eps)
-    dq, dk, dv, git, gabs = ro.race_backward(to64(q), to64(k), to64(v), to64(do), planes.double().numpy(),
-                                             causal=causal, inv_temp=inv_temp, with_l1=True, eps=eps)
-    return o, dq, dk, dv, git, gabs
-
-
-def _compare(case_name, gpu, ref, tol):
-    """relerr = max|a-b|/max|b| per tensor.  d(inv_temp) is one sum over all
-    tokens: fp32 compares |a-b|/|b|; bf16 compares |a-b| against the l1 mass
-    sum|du*th| of its terms (ref[5]), the analogue of the max-norm metric for
-    a reduction whose terms cancel."""
-    names = ("out", "dq", "dk", "dv")
-    errs = {nm: relerr(to64(a), b) for nm, a, b in zip(names, gpu[:4], ref[:4])}
-    scale = abs(ref[4]) if (tol < 1e-3 or len(ref) < 6) else ref[5]
-    errs["dinv_temp"] = abs(gpu[4] - ref[4]) / (scale + 1e-30)
-    print(f"[{case_name}] " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
-    for nm, e in errs.items():
-        assert e <= tol, f"{case_name}: {nm} relerr {e:.3e} > {tol:.1e}"
-
-
 CASES = [
     # name, dict(make_case kwargs), causal, inv_temp (None -> 1/sqrt(D)), seg_tiles
     ("causal_bf16_K4L8", dict(B=2, T=200, H=3, L=8, K=4), True, None, 0),
@@ -199,9 +165,9 @@ def test_parity_small(dev, name, kw, causal, it, seg):
     q, k, v, do, planes = make_case(seed=zlib.crc32(name.encode()) % 1000, **kw)
     L, K = kw["L"], kw["K"]
     inv_temp = it if it is not None else 1.0 / math.sqrt(q.shape[-1])
-    gpu = _run_gpu(q, k, v, do, planes, L=L, K=K, causal=causal, inv_temp=inv_temp, dev=dev, seg_tiles=seg, eps=eps)
-    ref = _run_oracle(q, k, v, do, planes, causal=causal, inv_temp=inv_temp, eps=eps)
-    _compare(name, gpu, ref, TOL[q.dtype])
+    gpu = run_gpu(q, k, v, do, planes, L=L, K=K, causal=causal, inv_temp=inv_temp, dev=dev, seg_tiles=seg, eps=eps)
+    ref = run_oracle(q, k, v, do, planes, causal=causal, inv_temp=inv_temp, eps=eps)
+    compare(name, gpu, ref, TOL[q.dtype])
 
 
 def test_strided_fused_qkv_layout(dev):
@@ -218,8 +184,8 @@ def test_strided_fused_qkv_layout(dev):
     out, st = race_fwd_raw(*views, planes.to(dev), L=L, K=K, causal=True, inv_temp=it)
     dq, dk, dv, git = race_bwd_raw(*views, planes.to(dev), do.to(dev), st, L=L, K=K, causal=True, inv_temp=it)
     cpu = [qkv[:, :, j * H:(j + 1) * H].unsqueeze(0) for j in range(3)]
-    ref = _run_oracle(*cpu, do, planes, causal=True, inv_temp=it)
-    _compare("fused_qkv", (out.cpu(), dq.cpu(), dk.cpu(), dv.cpu(), float(git.cpu())), ref, 2e-2)
+    ref = run_oracle(*cpu, do, planes, causal=True, inv_temp=it)
+    compare("fused_qkv", (out.cpu(), dq.cpu(), dk.cpu(), dv.cpu(), float(git.cpu())), ref, 2e-2)
 
 
 def test_golden_fixture(dev):
@@ -232,15 +198,15 @@ def test_golden_fixture(dev):
         q, k, v, do = [torch.from_numpy(f(s)).to(dtype) for s in ("q", "k", "v", "do")]
         planes = torch.from_numpy(f("planes")).float()
         L, K, causal, it = int(f("L")), int(f("K")), bool(f("causal")), float(f("inv_temp"))
-        gpu = _run_gpu(q, k, v, do, planes, L=L, K=K, causal=causal, inv_temp=it, dev=dev)
+        gpu = run_gpu(q, k, v, do, planes, L=L, K=K, causal=causal, inv_temp=it, dev=dev)
         ref = (f("out"), f("dq"), f("dk"), f("dv"), float(f("dinv_temp")), float(f("dinv_temp_l1")))
-        _compare("golden_" + nm, gpu, ref, TOL[dtype])
+        compare("golden_" + nm, gpu, ref, TOL[dtype])
 
 
 def test_deterministic(dev):
     q, k, v, do, planes = make_case(B=1, T=333, H=2, L=8, K=4, seed=3)
-    a = _run_gpu(q, k, v, do, planes, L=8, K=4, causal=True, inv_temp=0.125, dev=dev)
-    b = _run_gpu(q, k, v, do, planes, L=8, K=4, causal=True, inv_temp=0.125, dev=dev)
+    a = run_gpu(q, k, v, do, planes, L=8, K=4, causal=True, inv_temp=0.125, dev=dev)
+    b = run_gpu(q, k, v, do, planes, L=8, K=4, causal=True, inv_temp=0.125, dev=dev)
     for x, y in zip(a[:4], b[:4]):
         assert torch.equal(x, y)
     assert a[4] == b[4]
@@ -249,18 +215,18 @@ def test_deterministic(dev):
 def test_config_c1(dev):
     """C1: non-causal fp32, B=1 H=4 N=4096 d=64 K=2 L=5 M=1, tau = exp(0) = 1, N(0,1) inputs."""
     q, k, v, do, planes = make_case(B=1, T=4096, H=4, L=5, K=2, dtype=torch.float32, unit=False, seed=11)
-    gpu = _run_gpu(q, k, v, do, planes, L=5, K=2, causal=False, inv_temp=1.0, dev=dev)
-    ref = _run_oracle(q, k, v, do, planes, causal=False, inv_temp=1.0)
-    _compare("C1", gpu, ref, 1e-4)
+    gpu = run_gpu(q, k, v, do, planes, L=5, K=2, causal=False, inv_temp=1.0, dev=dev)
+    ref = run_oracle(q, k, v, do, planes, causal=False, inv_temp=1.0)
+    compare("C1", gpu, ref, 1e-4)
 
 
 def test_config_c2(dev):
     """C2: causal bf16, B=2 H=8 N=16384 d=64 K=4 L=8 M=1, unit-L2 rows."""
     q, k, v, do, planes = make_case(B=2, T=16384, H=8, L=8, K=4, seed=12)
     it = 1.0 / 8.0
-    gpu = _run_gpu(q, k, v, do, planes, L=8, K=4, causal=True, inv_temp=it, dev=dev)
-    ref = _run_oracle(q, k, v, do, planes, causal=True, inv_temp=it)
-    _compare("C2", gpu, ref, 2e-2)
+    gpu = run_gpu(q, k, v, do, planes, L=8, K=4, causal=True, inv_temp=it, dev=dev)
+    ref = run_oracle(q, k, v, do, planes, causal=True, inv_temp=it)
+    compare("C2", gpu, ref, 2e-2)
 
 
 def test_config_c5_attention(dev):
@@ -271,9 +237,9 @@ def test_config_c5_attention(dev):
     M, B, T, H, L, K = 2, 8, 8192, 12, 4, 8
     q, k, v, do, planes = make_case(M=M, B=B, T=T, H=H, L=L, K=K, seed=21, share_planes=False)
     it = 1.0 / 8.0
-    out, dq, dk, dv, _ = _run_gpu(q, k, v, do, planes, L=L, K=K, causal=True, inv_temp=it, dev=dev)
+    out, dq, dk, dv, _ = run_gpu(q, k, v, do, planes, L=L, K=K, causal=True, inv_temp=it, dev=dev)
     sub = lambda x: x[:, :1, :, :2]  # noqa: E731
-    ref = _run_oracle(sub(q), sub(k), sub(v), sub(do), planes, causal=True, inv_temp=it)
+    ref = run_oracle(sub(q), sub(k), sub(v), sub(do), planes, causal=True, inv_temp=it)
     errs = {nm: relerr(to64(sub(a)), b) for nm, a, b in zip(("out", "dq", "dk", "dv"), (out, dq, dk, dv), ref[:4])}
     print("[C5 attention] " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
     for x in (out, dq, dk, dv):
