@@ -184,6 +184,29 @@ int race_prefix_mean_bwd(const float *w, const float *v, const float *gE,
                          int64_t D, double eps, void *ws, size_t ws_bytes,
                          void *stream);
 
+/* ---------------------------------------------------------------------
+ * No-allocation forward.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory or pass workspaces (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same semantics and kernels as race_fwd, but the forward's segment state and
+ * segment sums live in a file-scope device array of the library of
+ * RACE_NOALLOC_SCRATCH_BYTES bytes per GPU (held until the process ends), so
+ * the caller passes only inputs and outputs; there is no state for a later
+ * race_bwd (forward only, e.g. inference).
+ *   - seg_tiles = 0 picks the default segmentation, coarsened until it fits
+ *     the array; an explicit seg_tiles is used as given (results are then
+ *     bit-identical to race_fwd with the same descriptor).
+ *   - A call whose scratch would exceed the array (fp32 or K > 4 inputs write
+ *     per-slice fp32 partial outputs of nslice * M*B*H * T * D * 4 bytes)
+ *     returns RACE_E_UNSUPPORTED and names the bytes it needs.
+ *   - Every call on one GPU shares that GPU's array: calls that overlap on
+ *     one GPU (concurrent streams or threads) race and must be serialised by
+ *     the caller.  Nothing in the array needs clearing between calls.
+ * --------------------------------------------------------------------- */
+#define RACE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int race_fwd_noalloc(const race_desc *d, const void *q, const void *k, const void *v,
+                     const float *planes, void *out, void *stream);
+
 /* Message for the last failing call on this thread ("" if none). */
 const char *race_last_error(void);
 

@@ -43,6 +43,7 @@ EXPORTS = (
     "race_probs_bwd_workspace_bytes", "race_probs", "race_probs_bwd",
     "race_fwd_global_workspace_bytes", "race_bwd_global_workspace_bytes", "race_fwd_global", "race_bwd_global",
     "race_prefix_mean_workspace_bytes", "race_prefix_mean_fwd", "race_prefix_mean_bwd",
+    "race_fwd_noalloc",
     "race_last_error", "race_abi_version",
 )
 
@@ -93,6 +94,8 @@ def load():
         lib.race_prefix_mean_fwd.restype = ctypes.c_int
         lib.race_prefix_mean_bwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, dbl, vp, sz, vp]
         lib.race_prefix_mean_bwd.restype = ctypes.c_int
+        lib.race_fwd_noalloc.argtypes = [dp, vp, vp, vp, vp, vp, vp]
+        lib.race_fwd_noalloc.restype = ctypes.c_int
         lib.race_last_error.argtypes = []
         lib.race_last_error.restype = ctypes.c_char_p
         lib.race_abi_version.argtypes = []

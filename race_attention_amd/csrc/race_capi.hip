@@ -8,6 +8,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -447,6 +448,65 @@ int pm_check(const void *a, const char *na, int64_t NS, int64_t T, int64_t D) {
     return RACE_OK;
 }
 
+// ---------------------------------------------------------------- no-allocation forward
+// race_fwd_noalloc keeps the forward's segment sums and segment state in one
+// file-scope device array instead of caller buffers.  In host code `scratch`
+// names a host-side stand-in: kernels get the device address that
+// hipGetSymbolAddress returns for the current device (each GPU holds its own
+// copy of the array), looked up once per device and cached.
+static __device__ __align__(256) unsigned char scratch[RACE_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+constexpr int kMaxDevices = 64;
+void *g_scratch_ptr[kMaxDevices];
+
+int scratch_address(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(RACE_E_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(RACE_E_UNSUPPORTED, "device ordinal %d >= %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(RACE_E_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return RACE_OK;
+}
+
+constexpr size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+size_t noalloc_need(const Plan &p) { return align256(p.state_bytes) + p.fws; }
+
+// Plan of the no-allocation forward: the descriptor's seg_tiles if set, else
+// the default segmentation, coarsened (longer segments) until the state and
+// the segment sums fit the scratch array.  Returns RACE_E_UNSUPPORTED with the
+// bytes needed when even one segment per stream does not fit.
+int noalloc_plan(const race_desc *d, race_desc &dd, Plan &p) {
+    dd = *d;
+    int rc = make_plan(&dd, p);
+    if (rc) return rc;
+    if (d->seg_tiles <= 0 && noalloc_need(p) > RACE_NOALLOC_SCRATCH_BYTES) {
+        // state (nseg + 1 rows) and sums (nseg rows) of N * Spad * (D+1) fp64 each
+        const size_t row = (size_t)p.N * p.Spad * SROW * sizeof(double);
+        const size_t fixed = p.part_bytes + row + 512;
+        const int64_t nseg = fixed < RACE_NOALLOC_SCRATCH_BYTES
+                                 ? (int64_t)((RACE_NOALLOC_SCRATCH_BYTES - fixed) / (2 * row)) : 0;
+        if (nseg >= 1) {
+            dd.seg_tiles = (int32_t)((p.ntiles + nseg - 1) / nseg);
+            if ((rc = make_plan(&dd, p))) return rc;
+        }
+    }
+    if (noalloc_need(p) > RACE_NOALLOC_SCRATCH_BYTES)
+        return fail(RACE_E_UNSUPPORTED,
+                    "race_fwd_noalloc: this call needs %zu bytes of scratch (state %zu, segment sums and partial "
+                    "outputs %zu); the no-allocation forward holds %zu -- use race_fwd with caller buffers",
+                    noalloc_need(p), p.state_bytes, p.fws, (size_t)RACE_NOALLOC_SCRATCH_BYTES);
+    return RACE_OK;
+}
+
 } // namespace
 } // namespace race
 
@@ -754,6 +814,31 @@ int race_prefix_mean_bwd(const float *w, const float *v, const float *gE, float 
     k_pm_rscan<<<dim3((elems + 255) / 256, (unsigned)NS), 256, 0, s>>>(rstate, rdelta, nseg, elems);
     k_pm_bw_rev<<<grid, 64, 0, s>>>(w, v, gE, invA, alpha, rstate, gW, gV, T, (int)D, tseg, nseg);
     return launched("race_prefix_mean_bwd");
+}
+
+int race_fwd_noalloc(const race_desc *d, const void *q, const void *k, const void *v, const float *planes,
+                     void *out, void *stream) {
+    race_desc dd;
+    Plan p;
+    int rc = noalloc_plan(d, dd, p);
+    if (rc) return rc;
+    if ((rc = check_tensor("q", q, d->q_stride, p.esize, d->T)) || (rc = check_tensor("k", k, d->k_stride, p.esize, d->T)) ||
+        (rc = check_tensor("v", v, d->v_stride, p.esize, d->T)) || (rc = check_out("out", out, d->o_stride, p.esize, d)))
+        return rc;
+    if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
+    void *base = nullptr;
+    if ((rc = scratch_address(&base))) return rc;
+    Args a = base_args(&dd, p, planes);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    a.fstate = (double *)base;
+    a.fdelta = (double *)((char *)base + align256(p.state_bytes));
+    a.opart = p.parts ? (float *)((char *)a.fdelta + p.fws_core) : nullptr;
+    hipStream_t s = (hipStream_t)stream;
+    if (d->dtype == RACE_DTYPE_BF16) return fwd_dispatch<bf16>(&dd, p, a, s);
+    return fwd_dispatch<float>(&dd, p, a, s);
 }
 
 const char *race_last_error(void) { return g_err.c_str(); }
