@@ -416,11 +416,25 @@ def cpu_baseline(sample_T, H_full, D=64, L=8, K=4, reps=16):
             "host_cpus": os.cpu_count(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
 
-def max_seq_bisect(H, D, L, K, dev, limit_tokens=1 << 27):
-    """Longest T (multiple of 2^16) for which one layer's fwd+bwd fits in HBM:
+def max_seq_bisect(H, D, L, K, dev, step=1 << 16):
+    """Longest T (multiple of step) for which one layer's fwd+bwd fits in HBM:
     separate Q, K, V, dO inputs, O, dQ, dK, dV outputs, the forward state and
-    the workspace, all allocated and the step run once."""
+    the workspace, all allocated and the step run once.  The candidate comes
+    from the free HBM and the library's own size queries; it is then confirmed
+    by running at T (stepping down while that runs out of memory) and by T +
+    step running out of memory (stepping up while it does not).  Only an
+    allocation failure counts as "does not fit"; any other error fails the run."""
     import torch
+    from race_attention_amd import _lib
+    from race_attention_amd.functional import make_desc
+    lib = _lib.load()
+
+    def need(T):
+        x = torch.empty((1, 1, T, H, D), dtype=torch.bfloat16, device="meta")  # shapes and strides only
+        d = make_desc(x, x, x, torch.empty(1, L, K, D), L=L, K=K, causal=True, eps=1e-6, inv_temp=0.125)
+        ref = ctypes.byref(d)
+        return (8 * T * H * D * 2 + lib.race_state_bytes(ref) +
+                max(lib.race_fwd_workspace_bytes(ref), lib.race_bwd_workspace_bytes(ref)))
 
     def fits(T):
         bufs = None
@@ -439,19 +453,24 @@ def max_seq_bisect(H, D, L, K, dev, limit_tokens=1 << 27):
             del bufs
             torch.cuda.empty_cache()
 
-    lo, hi = 1 << 20, None
-    T = lo
-    while T <= limit_tokens and fits(T):
-        lo = T
-        T *= 2
-    hi = T
-    while hi - lo > (1 << 16):
-        mid = (lo + hi) // 2 // (1 << 16) * (1 << 16)
-        if fits(mid):
-            lo = mid
-        else:
-            hi = mid
-    return lo
+    torch.cuda.empty_cache()
+    free = torch.cuda.mem_get_info(dev)[0]
+    T = step
+    while need(T + step) <= free:
+        T += step if need(2 * T) > free else T
+    T = T // step * step
+    tries = 0
+    while not fits(T):  # fragmentation or allocator overhead: step down
+        T -= step
+        tries += 1
+        if T <= 0 or tries > 64:
+            raise RuntimeError("max-N search: no fitting length found")
+    while fits(T + step):  # the estimate was conservative: step up
+        T += step
+        tries += 1
+        if tries > 64:
+            break
+    return T
 
 
 def main():

@@ -61,6 +61,10 @@ typedef struct race_desc {
     int32_t phases;           /* 0 = run every kernel of the call; otherwise a bitmask of
                                  RACE_PHASE_* to run a subset (per-kernel timing); subsets of
                                  one call must be enqueued in phase order on one stream */
+    const float *inv_temp_ptr; /* nullable: a device fp32 scalar read by the kernels in place of
+                                 inv_temp (a learnable temperature, misc/vit.py:923, stays on the
+                                 GPU: no host read per call); it must hold a finite value when
+                                 the call's kernels run.  NULL: the inv_temp field is used. */
 } race_desc;
 
 /* Bytes of the forward->backward state buffer (per-segment prefix carries,
@@ -210,7 +214,7 @@ int race_fwd_noalloc(const race_desc *d, const void *q, const void *k, const voi
 /* Message for the last failing call on this thread ("" if none). */
 const char *race_last_error(void);
 
-/* ABI version (increments on incompatible changes). */
+/* ABI version (increments on incompatible changes; 3 added inv_temp_ptr). */
 int race_abi_version(void);
 
 #ifdef __cplusplus

@@ -32,6 +32,7 @@ class RaceDesc(ctypes.Structure):
         ("q_stride", I64x4), ("k_stride", I64x4), ("v_stride", I64x4),
         ("o_stride", I64x4), ("do_stride", I64x4), ("g_stride", I64x4),
         ("seg_tiles", ctypes.c_int32), ("phases", ctypes.c_int32),
+        ("inv_temp_ptr", ctypes.c_void_p),
     ]
 
 

@@ -85,8 +85,10 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
     if (d->L * d->K > NCOL)
         return fail(RACE_E_UNSUPPORTED, "L*K=%d projection columns unsupported (L*K <= %d)", d->L * d->K, NCOL);
     if (!(d->eps >= 0.f) || d->eps > 1e30f) return fail(RACE_E_INVALID, "eps must be finite and >= 0");
-    if (!(d->inv_temp == d->inv_temp) || d->inv_temp > 1e30f || d->inv_temp < -1e30f)
+    if (!d->inv_temp_ptr && (!(d->inv_temp == d->inv_temp) || d->inv_temp > 1e30f || d->inv_temp < -1e30f))
         return fail(RACE_E_INVALID, "inv_temp must be finite");
+    if (d->inv_temp_ptr && (uintptr_t)d->inv_temp_ptr % 4)
+        return fail(RACE_E_INVALID, "inv_temp_ptr is not 4-byte aligned");
     if (d->planes_m_stride < 0) return fail(RACE_E_INVALID, "planes_m_stride must be >= 0");
     if (d->phases < 0 || d->phases > 7) return fail(RACE_E_INVALID, "phases must be a RACE_PHASE_* bitmask");
     p.R = 1 << d->K;
@@ -198,6 +200,7 @@ Args base_args(const race_desc *d, const Plan &p, const float *planes) {
     a.T = d->T;
     a.eps = d->eps;
     a.inv_temp = d->inv_temp;
+    a.inv_temp_ptr = d->inv_temp_ptr;
     a.nseg = p.nseg;
     a.tps = p.tps;
     a.fnseg = p.fnseg;
@@ -843,6 +846,6 @@ int race_fwd_noalloc(const race_desc *d, const void *q, const void *k, const voi
 
 const char *race_last_error(void) { return g_err.c_str(); }
 
-int race_abi_version(void) { return 2; }
+int race_abi_version(void) { return 3; }
 
 } // extern "C"

@@ -277,6 +277,8 @@ __device__ __forceinline__ float row_suffix(float x) {
     x += dpp_f<0x108>(x);
     return x;
 }
+// lane 0 of each row in every lane of that row (row_newbcast:0, gfx90a and later)
+__device__ __forceinline__ float row_bcast0(float x) { return dpp_f<0x150>(x); }
 // total of a row in every lane of it (quad swaps, half-row mirror, row mirror)
 __device__ __forceinline__ float row_sum(float x) {
     x += dpp_f<0xB1>(x);  // quad_perm [1,0,3,2]

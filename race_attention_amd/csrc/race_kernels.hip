@@ -57,6 +57,7 @@ struct Args {
     int M, B, H, L, K, R, S;
     int64_t T;
     float eps, inv_temp;
+    const float *inv_temp_ptr;  // nullable device scalar replacing inv_temp (read at kernel start)
     int nseg, tps;   // segments per stream, tiles per segment
     // forward segments (fstate rows per stream - 1) and forward segments per
     // segment: the backward's segment s starts at forward boundary s * fmul
@@ -762,14 +763,16 @@ __device__ float softhash_combine(const float *share, const float *sp, const flo
 
 // Inclusive token suffix Y (plus y0, the lane's per-bucket carry) and token
 // totals of a bucket-row tile pair (lane holds X[s = 4g + e][t = 16nt + i]):
-// fp32 scans and sums over the 16 lanes of each row (DPP), tile 1 first.
+// fp32 suffix scans over the 16 lanes of each row (DPP), tile 1 first; a
+// row's total is its suffix at lane 0, broadcast to the row.
 __device__ __forceinline__ void suffix_totals(const f32x4 (&X)[2], const f32x4 &y0, f32x4 (&Y)[2], f32x4 &tot) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const float t0 = row_sum(X[0][e]), t1 = row_sum(X[1][e]);
-        Y[1][e] = y0[e] + row_suffix(X[1][e]);
-        Y[0][e] = (y0[e] + t1) + row_suffix(X[0][e]);
-        tot[e] = t0 + t1;
+        const float s1 = row_suffix(X[1][e]), t1 = row_bcast0(s1);
+        const float s0 = row_suffix(X[0][e]);
+        Y[1][e] = y0[e] + s1;
+        Y[0][e] = (y0[e] + t1) + s0;
+        tot[e] = row_bcast0(s0) + t1;
     }
 }
 // token totals only (lane: bucket 4g + e), fp32 row sums over the 16 lanes
@@ -944,6 +947,27 @@ __device__ void m_tile_xy(int r, const T *sV, const T *sG, T *X, T *Y) {
     for (int e = 0; e < 4; ++e) Y[(16 * mt + 4 * g + e) * LDT + 16 * nt + i] = from_f32<T>(acc[e]);
 }
 
+// The G term's in-tile operand, built by each wave in registers: blocks
+// C[tau][t] = v_tau . g_t (tau <= t) of the tile as the B operand with k = tau
+// (pi order) and n = t for token half nt -- the values m_tile stores, without
+// the shared task, its barrier phase or LDS round trip.
+template <typename T, class NL>
+__device__ __forceinline__ void x_operands(const T *sV, const T *sG, Frag<T> (&X)[2]) {
+    const int g = lg(), i = li();
+    f32x4 c00 = zero4(), c01 = zero4(), c11 = zero4();
+    nat_mma<NL>(c00, sV, 0, sG, 0);    // [tau = 4g + e][t = i]
+    nat_mma<NL>(c01, sV, 0, sG, 16);   // [tau = 4g + e][t = 16 + i]: all tau <= t
+    nat_mma<NL>(c11, sV, 16, sG, 16);  // [tau = 16 + 4g + e][t = 16 + i]
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (4 * g + e > i) {
+            c00[e] = 0.f;
+            c11[e] = 0.f;
+        }
+    X[0] = frag_acc<T>(c00, zero4());
+    X[1] = frag_acc<T>(c01, c11);
+}
+
 template <typename T> __device__ void zero_lds(T *p, int n, int nth) {
     for (int idx = threadIdx.x; idx < n; idx += nth) p[idx] = from_f32<T>(0.f);
 }
@@ -969,6 +993,13 @@ __device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64
     }
 }
 
+// Workgroups per CU of a backward tile kernel with nw waves and `bytes` of
+// LDS: the kernels need more than 128 VGPRs, so at most 2 waves per SIMD
+// (8 per CU) run, whatever the LDS allows.
+__host__ __device__ constexpr size_t bwd_wgs_per_cu(int nw, size_t bytes) {
+    return (160 * 1024 / bytes) < (size_t)(8 / nw) ? 160 * 1024 / bytes : (size_t)(8 / nw);
+}
+
 // Sum of a per-thread value over the workgroup in a fixed order.
 template <int NTH> __device__ float block_sum(float v, float *scratch) {
     scratch[threadIdx.x] = v;
@@ -990,17 +1021,22 @@ __device__ __forceinline__ int64_t sidx(int s, int d) { return (int64_t)s * SROW
 // =====================================================================
 // k_fwd_reduce: per-segment (A, B) sums (fp64 over fp32 tile sums).
 // =====================================================================
+// Tiles are processed in groups of GT: one barrier after the group's rows are
+// committed (the 4 GT projection tasks then spread over the waves) and one
+// after the projections; V^T and the key weights alternate between two
+// buffers so the next group's commit can start while waves still read them.
 template <typename T, int SP> struct FwdReduceL {
     static constexpr int NW_ = SP / WB;
+    static constexpr int GT = 2;  // tiles per barrier group
     static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL);
-    static constexpr size_t oK = 0;
-    static constexpr size_t oVt = align16(oK + sizeof(T) * TT * LDN);
-    static constexpr size_t oPl = align16(oVt + sizeof(T) * D * LDT);
+    static constexpr size_t oK = 0;                                          // [GT][TT][LDN]
+    static constexpr size_t oVt = align16(oK + sizeof(T) * GT * TT * LDN);   // [2][GT][D][LDT]
+    static constexpr size_t oPl = align16(oVt + sizeof(T) * 2 * GT * D * LDT);
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oSig = align16(oPlLo + sizeof(T) * NCOL * LDN);
-    static constexpr size_t oCst = align16(oSig + sizeof(float) * 2 * TT * LDC);
-    static constexpr size_t oTok = align16(oCst + Consts<T>::bytes);  // key weights [TT] (+ unused [TT])
-    static constexpr size_t bytes = align16(oTok + sizeof(float) * 2 * TT);
+    static constexpr size_t oSig = align16(oPlLo + sizeof(T) * NCOL * LDN);  // [GT][sp, sm][TT][LDC]
+    static constexpr size_t oCst = align16(oSig + sizeof(float) * GT * 2 * TT * LDC);
+    static constexpr size_t oTok = align16(oCst + Consts<T>::bytes);  // key weights [2][GT][2 * TT]
+    static constexpr size_t bytes = align16(oTok + sizeof(float) * 2 * GT * 2 * TT);
 };
 
 // The tile's (A, B) sums -- tot (lane: bucket 4g + e) and dB^T (d-row) --
@@ -1023,31 +1059,32 @@ __device__ __forceinline__ void tile_sums(const Frag<T> &Pf, const Consts<T> &cs
 
 template <typename T, int SP, int KB>
 __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
+    if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     using Ly = FwdReduceL<T, SP>;
     using NL = NatL<T, true>;
-    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDC = Ly::LDC, LDT = ldp_of<T>(TT);
+    constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDC = Ly::LDC, LDT = ldp_of<T>(TT), LDN = Ly::LDN, GT = Ly::GT;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
-    T *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
+    T *sK = (T *)(smem + Ly::oK), *sVt0 = (T *)(smem + Ly::oVt);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
-    float *sSp = (float *)(smem + Ly::oSig), *sSm = sSp + TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
+    float *sSig = (float *)(smem + Ly::oSig), *sTok0 = (float *)(smem + Ly::oTok);
+    const int w = wave_id(), i = li(), g = lg(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
               sg = z * SP + sw;
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
     const int64_t ntiles = (a.T + TT - 1) / TT;
-    const int lastv = (int)(a.T - (ntiles - 1) * TT);  // rows of the last tile
     const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
+    const int64_t send = min(a.T, j1 * TT);  // the segment's tokens end here (tiles past it load nothing)
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
-    float *sTok = (float *)(smem + Ly::oTok);
     const float *kwp = a.kw ? a.kw + (int64_t)((n / a.H) % a.B) * a.T : nullptr;  // batch row's key weights
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
     load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
     // segment sums: A in fp64; B in fp64 for fp32 inputs, and for bf16 in
-    // fp32 MFMA accumulators (bf16 uses B only through bf16 operands)
+    // fp32 MFMA accumulators (bf16 uses B only through bf16 operands).  Tile
+    // sums are added tile by tile in token order.
     constexpr bool BM = is_bf16<T>();
     double accB[4][4], accA[4];
     f32x4 accBm[4];
@@ -1058,47 +1095,67 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     for (int md = 0; md < 4; ++md) accBm[md] = zero4();
 
     wait_state_loads();
-    Prefetch<T, NTH> pk_;
-    PrefetchT<T, NTH, 1> pv_;
-    TokPre pt_;
-    if (j0 < j1) {
-        pk_.issue(kp, a.sk.t, j0 * TT, a.T);
-        pv_.issue(0, vp, a.sv.t, j0 * TT, a.T);
-        if (kwp) pt_.issue(kwp, nullptr, j0 * TT, a.T);
-    }
-    for (int64_t jt = j0; jt < j1; ++jt) {
-        const int64_t t0 = jt * TT;
-        __syncthreads();
-        pk_.template commit<NL>(sK, nullptr);
-        pv_.template commit<NL>(0, nullptr, sVt);
-        if (kwp) pt_.commit(sTok);
-        if (jt + 1 < j1) {
-            pk_.issue(kp, a.sk.t, t0 + TT, a.T);
-            pv_.issue(0, vp, a.sv.t, t0 + TT, a.T);
-            if (kwp) pt_.issue(kwp, nullptr, t0 + TT, a.T);
+    Prefetch<T, NTH> pk_[GT];
+    PrefetchT<T, NTH, 1> pv_[GT];
+    TokPre pt_[GT];
+    auto issue = [&](int64_t jg) {
+#pragma unroll
+        for (int u = 0; u < GT; ++u) {
+            const int64_t t0 = (jg + u) * TT;
+            pk_[u].issue(kp, a.sk.t, t0, send);
+            pv_[u].issue(0, vp, a.sv.t, t0, send);
+            if (kwp) pt_[u].issue(kwp, nullptr, t0, send);
         }
-        __syncthreads();
-        for (int q = w; q < 4; q += NW_) project_tile<T, NL>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, nullptr);
-        __syncthreads();
-        f32x4 PK[2];
-        probs_st<KB>(sSp, sSm, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
-        if (kwp)  // P_K' = w_t P_K
-            for (int nt = 0; nt < 2; ++nt) {
-                const float wt = sTok[16 * nt + i];
-                for (int e = 0; e < 4; ++e) PK[nt][e] *= wt;
-            }
-        const Frag<T> Pf = token_operand<T>(PK, cst);
-        if constexpr (BM) {
-            f32x4 tot = zero4();
-            mma(tot, Pf, cst.ones());
-            for (int md = 0; md < 4; ++md) mma(accBm[md], ld_frag_pi(sVt + (16 * md + i) * LDT), Pf);
-            for (int e = 0; e < 4; ++e) accA[e] += (double)tot[e];
-        } else {
-            f32x4 tot, dB[4];
-            tile_sums<T>(Pf, cst, sVt, tot, dB);
-            for (int e = 0; e < 4; ++e) {
-                accA[e] += (double)tot[e];
-                for (int md = 0; md < 4; ++md) accB[md][e] += (double)dB[md][e];
+    };
+    if (j0 < j1) issue(j0);
+    int b = 0;
+    for (int64_t jg = j0; jg < j1; jg += GT, b ^= 1) {
+        // commit the group's rows (V^T and key weights to buffer b: the
+        // group before last read the other one, and its readers passed the
+        // last barrier), then start the next group's loads
+        T *sVt = sVt0 + b * GT * D * LDT;
+        float *sTok = sTok0 + b * GT * 2 * TT;
+        wait_vmem();
+#pragma unroll
+        for (int u = 0; u < GT; ++u) {
+            pk_[u].template commit<NL>(sK + u * TT * LDN, nullptr);
+            pv_[u].template commit<NL>(0, nullptr, sVt + u * D * LDT);
+            if (kwp) pt_[u].commit(sTok + u * 2 * TT);
+        }
+        if (jg + GT < j1) issue(jg + GT);
+        __syncthreads();  // the group's rows in LDS; the last group's sigmoid rows are read
+        for (int q = w; q < 4 * GT; q += NW_) {
+            float *sp = sSig + (q >> 2) * 2 * TT * LDC;
+            project_tile<T, NL>(sK + (q >> 2) * TT * LDN, sPl, sPlLo, (q >> 1) & 1, q & 1, a.inv_temp, sp,
+                                sp + TT * LDC, nullptr);
+        }
+        __syncthreads();  // sigmoid rows in LDS
+#pragma unroll
+        for (int u = 0; u < GT; ++u) {
+            const int64_t jt = jg + u;
+            if (jt >= j1) break;
+            const float *sp = sSig + u * 2 * TT * LDC;
+            const T *vt = sVt + u * D * LDT;
+            f32x4 PK[2];
+            probs_st<KB>(sp, sp + TT * LDC, sg, a.S, tile_rows(jt * TT, a.T), PK);
+            if (kwp)  // P_K' = w_t P_K
+                for (int nt = 0; nt < 2; ++nt) {
+                    const float wt = sTok[u * 2 * TT + 16 * nt + i];
+                    for (int e = 0; e < 4; ++e) PK[nt][e] *= wt;
+                }
+            const Frag<T> Pf = token_operand<T>(PK, cst);
+            if constexpr (BM) {
+                f32x4 tot = zero4();
+                mma(tot, Pf, cst.ones());
+                for (int md = 0; md < 4; ++md) mma(accBm[md], ld_frag_pi(vt + (16 * md + i) * LDT), Pf);
+                for (int e = 0; e < 4; ++e) accA[e] += (double)tot[e];
+            } else {
+                f32x4 tot, dB[4];
+                tile_sums<T>(Pf, cst, vt, tot, dB);
+                for (int e = 0; e < 4; ++e) {
+                    accA[e] += (double)tot[e];
+                    for (int md = 0; md < 4; ++md) accB[md][e] += (double)dB[md][e];
+                }
             }
         }
     }
@@ -1290,6 +1347,7 @@ __device__ void fwd_out_final(int md, int nt, f32x4 O, const T *sVt, const T *sc
 // divided by den(t) = sum over all buckets of P_Q A_s(t), clamped below at eps.
 template <typename T, int SP, bool CAUSAL, int KB, bool GN>
 __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(Args a) {
+    if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
     using Ly = FwdOutL<T, SP, CAUSAL, GN>;
     using NL = typename Ly::NL;
@@ -1381,8 +1439,6 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             probs_st<KB>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
             if constexpr (CAUSAL) {
                 probs_st<KB>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
-                for (int nt = 0; nt < 2; ++nt)
-                    for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
                 Pf = store_ts_operand<T, SP>(sPts, sw, PK, cst);
                 for (int nt = 0; nt < 2; ++nt) {
                     Acum[nt] = zero4();
@@ -1571,8 +1627,8 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr size_t oTokIn = align16(oO + (GN ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t TB = align16(oTokIn + (GN || !CAUSAL ? sizeof(float) * 2 * TT : 0));
     // the rest, relative to its start
-    static constexpr size_t rX = 0;
-    static constexpr size_t rDproj = align16(rX + (CAUSAL ? sizeof(T) * TT * LDT : 0));
+    static constexpr size_t rX = 0;  // (the in-tile v.g^T blocks live in each wave's registers)
+    static constexpr size_t rDproj = rX;
     static constexpr size_t rPl = align16(rDproj + sizeof(T) * TT * LDDP);
     static constexpr size_t rPlLo = align16(rPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t rPlT = align16(rPlLo + sizeof(T) * NCOL * LDN);
@@ -1589,7 +1645,7 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     // the next tile's rows then go to the other block while this tile still
     // reads its own, and the barrier ahead of that commit goes away
     static constexpr size_t LDS_CU = 160 * 1024;
-    static constexpr int NB = LDS_CU / (2 * TB + rEnd) >= LDS_CU / (TB + rEnd) ? 2 : 1;
+    static constexpr int NB = bwd_wgs_per_cu(NW_, 2 * TB + rEnd) >= bwd_wgs_per_cu(NW_, TB + rEnd) ? 2 : 1;
     static constexpr size_t R0 = NB * TB;
     static constexpr size_t oX = R0 + rX, oDproj = R0 + rDproj, oPl = R0 + rPl, oPlLo = R0 + rPlLo, oPlT = R0 + rPlT,
                             oSig = R0 + rSig, oRed = R0 + rRed, oCst = R0 + rCst, oHash = R0 + rHash, oPair = R0 + rPair,
@@ -1602,11 +1658,12 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
 // W = P_Q rd, dP_Q = G rd + gd A_s(t), dA = gd P_Q.
 template <typename T, int SP, bool CAUSAL, int KB, bool GN>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
+    if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
     using Ly = BwdReduceL<T, SP, CAUSAL, KB, GN>;
     using NL = NatL<T, true>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
-    constexpr int NTASK = CAUSAL ? 11 : 4;  // Q projection (4), K projection (4), X tiles (3)
+    constexpr int NTASK = CAUSAL ? 8 : 4;  // Q projection (4), K projection (4)
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     // this tile's token block (block jt & 1 of two; block 0 of one)
     T *sQ, *sK, *sV, *sG, *sVt, *sGt, *sO;
@@ -1622,7 +1679,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         sO = (T *)(tb + Ly::oO);
         sTokIn = (float *)(tb + Ly::oTokIn);
     };
-    T *sX = (T *)(smem + Ly::oX), *sDproj = (T *)(smem + Ly::oDproj);
+    T *sDproj = (T *)(smem + Ly::oDproj);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo), *sPlT = (T *)(smem + Ly::oPlT);
     float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sThQ = sSig + 2 * TT * LDC;
@@ -1662,7 +1719,6 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     po.init((T *)(smem + Ly::oPair), NTH);
     load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
     zero_lds<T>(sDproj, TT * LDDP, NTH);
-    if constexpr (CAUSAL) zero_lds<T>(sX, TT * LDT, NTH);
     // forward state in d-row layout: lane holds B^T[d = 16md + 4g + e][s = sw + i]
     const double *st = a.fstate + ((int64_t)n * (a.fnseg + 1) + (CAUSAL ? seg * a.fmul : a.fnseg)) * a.Spad * SROW;
     f32x4 Bt[4], Ut[4];
@@ -1751,10 +1807,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         for (int q = w; q < NTASK; q += NW_) {
             if (q < 4)
                 project_tile<T, NL>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, sThQ);
-            else if (q < 8)
-                project_tile<T, NL>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
             else
-                m_tile<T, NL>(q - 8, sV, sG, sX, nullptr);
+                project_tile<T, NL>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
         }
         // one token block: dQ of the previous tile, from the dproj rows its
         // softmax backward left in LDS, after the projections (they overlap);
@@ -1767,8 +1821,6 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         probs_st<KB>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
         if constexpr (CAUSAL) {
             probs_st<KB>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
-            for (int nt = 0; nt < 2; ++nt)
-                for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
             Pf = token_operand<T>(PK, cst, po);
             for (int nt = 0; nt < 2; ++nt) {
                 Acum[nt] = zero4();
@@ -1801,11 +1853,13 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         f32x4 dPQ[2], dA[2];
         {
             const Frag<T> b0 = frag_acc<T>(Bt[0], Bt[1]), b1 = frag_acc<T>(Bt[2], Bt[3]);
+            Frag<T> Xop[2];
+            if constexpr (CAUSAL) x_operands<T, NL>(sV, sG, Xop);
             for (int nt = 0; nt < 2; ++nt) {
                 f32x4 G = zero4();
                 mma(G, b0, NL::frag_pi(sG, 16 * nt + i, 0));
                 mma(G, b1, NL::frag_pi(sG, 16 * nt + i, 1));
-                if constexpr (CAUSAL) mma(G, Pf, ld_frag_pi(sX + (16 * nt + i) * LDT));
+                if constexpr (CAUSAL) mma(G, Pf, Xop[nt]);
                 // dP_Q = G/(A+eps); dA = -W G/(A+eps).  GN: dP_Q = G rd + gd A; dA = gd P_Q
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (GN) {
@@ -1942,7 +1996,7 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     // the next tile's rows then go to the other block while this tile still
     // reads its own, and the barrier ahead of that commit goes away
     static constexpr size_t LDS_CU = 160 * 1024;
-    static constexpr int NB = LDS_CU / (2 * TB + rEnd) >= LDS_CU / (TB + rEnd) ? 2 : 1;
+    static constexpr int NB = bwd_wgs_per_cu(NW_, 2 * TB + rEnd) >= bwd_wgs_per_cu(NW_, TB + rEnd) ? 2 : 1;
     static constexpr size_t R0 = NB * TB;
     static constexpr size_t oX = R0 + rX, oY = R0 + rY, oPts = R0 + rPts, oWts = R0 + rWts, oUT = R0 + rUT,
                             oDproj = R0 + rDproj, oPl = R0 + rPl, oPlLo = R0 + rPlLo, oPlT = R0 + rPlT,
@@ -2031,6 +2085,7 @@ __device__ void dv_finish(int md, int nt, f32x4 acc, const T *sGt, const T *sc2,
 // neither the forward state nor G.
 template <typename T, int SP, bool CAUSAL, int KB, bool GN>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
+    if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
     using Ly = BwdOutL<T, SP, CAUSAL, KB, GN>;
     using NL = NatL<T, true>;
@@ -2232,8 +2287,6 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                     for (int e = 0; e < 4; ++e) PKr[nt][e] *= kwt[nt];
                 }
         }
-        for (int nt = 0; nt < 2; ++nt)
-            for (int e = 0; e < 4; ++e) PKr[nt][e] = as_operand<T>(PKr[nt][e]);
         const Frag<T> Pf = store_ts_operand<T, SP>(sPts, sw, PKr, cst);
         f32x4 dPK[2];
         if constexpr (CAUSAL) {
@@ -2431,6 +2484,7 @@ __device__ __forceinline__ f32x4 load_row4(const float *row, int s0, int S) {
 
 template <typename T, int SP, int KB, bool BWD>
 __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
+    if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     using Ly = ProbsL<T, SP>;
     using NL = NatL<T, true>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDC = Ly::LDC, LDDP = Ly::LDDP;

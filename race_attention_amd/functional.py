@@ -75,7 +75,16 @@ def make_desc(q, k, v, planes, *, L, K, causal, eps, inv_temp, seg_tiles=0):
         raise TypeError(f"unsupported dtype {q.dtype} (bf16 or fp32)")
     d.dtype = _DTYPES[q.dtype]
     d.eps = float(eps)
-    d.inv_temp = float(inv_temp)
+    if torch.is_tensor(inv_temp) and inv_temp.is_cuda:
+        # a device temperature stays on the GPU: the kernels read it through
+        # inv_temp_ptr (no host synchronisation); the descriptor keeps the
+        # fp32 scalar alive until the call has been enqueued
+        t = inv_temp.detach().to(device=q.device, dtype=torch.float32).reshape(()).contiguous()
+        d.inv_temp = 1.0
+        d.inv_temp_ptr = t.data_ptr()
+        d._temp_keep = t
+    else:
+        d.inv_temp = float(inv_temp)
     if planes.dim() == 3:
         d.planes_m_stride = 0
     elif planes.dim() == 4 and planes.size(0) == 1:
@@ -146,6 +155,18 @@ def race_bwd_raw(q, k, v, planes, dout, state, *, L, K, causal, eps=1e-6, inv_te
     return dq, dk, dv, git
 
 
+def _temp_value(temp, x):
+    """The temperature an autograd Function runs with: a python float as is; a
+    tensor as an fp32 0-dim device copy taken now (read in-kernel, so the
+    forward never waits for the GPU, and the backward sees the forward's value
+    even if the source is updated in place meanwhile)."""
+    if torch.is_tensor(temp):
+        if temp.is_cuda:
+            return temp.detach().to(device=x.device, dtype=torch.float32).reshape(()).clone()
+        return float(temp)
+    return float(temp)
+
+
 class RACEFunction(torch.autograd.Function):
     """Autograd Function of the RACE operator (F1 semantics).
 
@@ -156,7 +177,7 @@ class RACEFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, Qhf, Khf, Vhf, planes, inv_temp, L, K, causal, eps):
-        it = float(inv_temp) if torch.is_tensor(inv_temp) else float(inv_temp)
+        it = _temp_value(inv_temp, Qhf)
         out, state = race_fwd_raw(Qhf, Khf, Vhf, planes, L=L, K=K, causal=causal, eps=eps, inv_temp=it)
         ctx.save_for_backward(Qhf, Khf, Vhf, planes, state)
         ctx.cfg = (L, K, causal, eps, it)
@@ -231,7 +252,7 @@ class RACEProbsFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, planes, inv_temp, L, K):
-        it = float(inv_temp)
+        it = _temp_value(inv_temp, x)
         P = race_probs_raw(x, planes, L=L, K=K, inv_temp=it)
         ctx.save_for_backward(x, planes)
         ctx.cfg = (L, K, it, torch.is_tensor(inv_temp))
@@ -329,7 +350,7 @@ class RACEExFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, Q, Kx, V, planes, inv_temp, kmask, L, K, eps, want_den):
-        it = float(inv_temp)
+        it = _temp_value(inv_temp, Q)
         out, den, state = race_fwd_ex_raw(Q, Kx, V, planes, L=L, K=K, inv_temp=it, kmask=kmask,
                                           want_den=want_den, eps=eps)
         ctx.save_for_backward(Q, Kx, V, planes, kmask if kmask is not None else torch.empty(0), state)
@@ -439,7 +460,7 @@ class RACEGlobalFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, Q, Kx, V, planes, beta, L, K, floor):
-        b = float(beta)
+        b = _temp_value(beta, Q)
         out, den, state = race_global_fwd_raw(Q, Kx, V, planes, L=L, K=K, beta=b, floor=floor)
         ctx.save_for_backward(Q, Kx, V, planes, out, den, state)
         ctx.cfg = (L, K, floor, b)

@@ -39,12 +39,14 @@ extern "C" int probe_mfma(int bf16, const void *A, const void *B, float *C, floa
     return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
 }
 
-// Row (16-lane) DPP scans: out[0..63] prefix, [64..127] suffix, [128..191] row sum.
+// Row (16-lane) DPP scans: out[0..63] prefix, [64..127] suffix, [128..191] row
+// sum, [192..255] lane 0 of the row broadcast to the row.
 __global__ __launch_bounds__(64) void k_probe_rows(const float *x, float *out) {
     const float v = x[threadIdx.x];
     out[threadIdx.x] = row_prefix(v);
     out[64 + threadIdx.x] = row_suffix(v);
     out[128 + threadIdx.x] = row_sum(v);
+    out[192 + threadIdx.x] = row_bcast0(v);
 }
 
 // MFMA chain with pi-ordered k: X = A . Bm^T (32 x 16, two tiles) kept in

@@ -27,13 +27,14 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.race_abi_version() == 2
+    assert lib.race_abi_version() == 3
 
 
 def test_desc_layout_matches_header():
     # int64 x5, int32 x4, float x2, int64, 6 x int64[4], int32 x2
-    assert ctypes.sizeof(_lib.RaceDesc) == 5 * 8 + 4 * 4 + 2 * 4 + 8 + 6 * 32 + 2 * 4  # seg_tiles, phases
+    assert ctypes.sizeof(_lib.RaceDesc) == 5 * 8 + 4 * 4 + 2 * 4 + 8 + 6 * 32 + 2 * 4 + 8  # ..., inv_temp_ptr
     assert _lib.RaceDesc.planes_m_stride.offset == 64
+    assert _lib.RaceDesc.inv_temp_ptr.offset == 272
 
 
 def _desc(**kw):
@@ -63,6 +64,18 @@ def test_plan_sizes_c4():
     # an explicit seg_tiles keeps the forward's segmentation in the backward
     d.seg_tiles = 128
     assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 256 * 128 * 65 * 4 + 2 * 8 * 256 * 4
+
+
+def test_device_temperature_skips_host_value_check():
+    """With inv_temp_ptr set the float field is not read (a device scalar is
+    validated by its producer); a misaligned pointer is rejected."""
+    lib = _lib.load()
+    d = _desc(T=64, inv_temp=float("nan"))
+    assert lib.race_state_bytes(ctypes.byref(d)) == 0 and "inv_temp" in _lib.last_error()
+    d.inv_temp_ptr = 256
+    assert lib.race_state_bytes(ctypes.byref(d)) > 0
+    d.inv_temp_ptr = 258
+    assert lib.race_state_bytes(ctypes.byref(d)) == 0 and "inv_temp_ptr" in _lib.last_error()
 
 
 @pytest.mark.parametrize("field,value,code,msg", [

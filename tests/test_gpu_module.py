@@ -9,7 +9,7 @@ import copy
 import pytest
 import torch
 
-from helpers import TOL, relerr
+from helpers import TOL, make_case, relerr
 
 pytestmark = pytest.mark.gpu
 
@@ -204,3 +204,43 @@ def test_lm_model_step(dev, monkeypatch):
     rp = dict(ref.named_parameters())
     pairs = [("logits", out, out_r)] + [("d" + n, p.grad, rp[n].grad) for n, p in md.named_parameters()]
     _check("lm.LMModel", pairs, TOL[torch.float32])
+
+
+def test_device_temperature_bit_identical(dev):
+    """A temperature passed as a device tensor (read in-kernel through
+    inv_temp_ptr) gives the same bits as the same value passed as a float,
+    forward and backward, including d(inv_temp)."""
+    from race_attention_amd.functional import race_bwd_raw, race_fwd_raw
+    q, k, v, do, planes = make_case(B=2, T=150, H=3, L=5, K=2, dtype=torch.bfloat16, unit=False, seed=41)
+    qd, kd, vd, dod, pd = [x.to(dev) for x in (q, k, v, do, planes)]
+    it_t = torch.tensor(0.8125, device=dev)
+    for causal in (False, True):
+        o1, s1 = race_fwd_raw(qd, kd, vd, pd, L=5, K=2, causal=causal, inv_temp=0.8125)
+        o2, s2 = race_fwd_raw(qd, kd, vd, pd, L=5, K=2, causal=causal, inv_temp=it_t)
+        g1 = race_bwd_raw(qd, kd, vd, pd, dod, s1, L=5, K=2, causal=causal, inv_temp=0.8125)
+        g2 = race_bwd_raw(qd, kd, vd, pd, dod, s2, L=5, K=2, causal=causal, inv_temp=it_t)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2)
+        for a, b in zip(g1, g2):
+            assert torch.equal(a, b)
+
+
+def test_learnable_temperature_no_host_sync(dev):
+    """The non-causal module with its learnable temperature runs forward and
+    backward without a device-to-host synchronisation (torch raises on one in
+    sync-debug mode "error")."""
+    from race_attention_amd.vit import RACEBlock
+    torch.manual_seed(0)
+    cfg = dict(embed_dim=128, drop_rate=0.0, num_heads=2, qkv_bias=False, L=5, K=2, M=1)
+    blk = RACEBlock(cfg).to(dev)
+    x = torch.randn(2, 77, 128, device=dev, requires_grad=True)
+    blk(x).sum().backward()  # warm-up: first-call work outside the checked region
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        y = blk(x)
+        y.sum().backward()
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    assert torch.isfinite(blk.att.ace.logit_temp.grad).all()

@@ -60,10 +60,10 @@ def test_mfma_chain16(dev, dtype):
 
 
 def test_dpp_row_scans(dev):
-    """16-lane row prefix/suffix/total helpers (in-bounds, one wave)."""
+    """16-lane row prefix/suffix/total/broadcast helpers (in-bounds, one wave)."""
     lib = _probe_lib()
     x = torch.randn(64, generator=torch.Generator().manual_seed(2)).to(dev)
-    out = torch.zeros(192, device=dev)
+    out = torch.zeros(256, device=dev)
     assert lib.probe_rows(x.data_ptr(), out.data_ptr()) == 0
     rows = x.cpu().double().view(4, 16)
     pre = torch.cumsum(rows, 1).reshape(-1)
@@ -72,7 +72,8 @@ def test_dpp_row_scans(dev):
     o = out.cpu().double()
     assert torch.allclose(o[:64], pre, atol=1e-5)
     assert torch.allclose(o[64:128], suf, atol=1e-5)
-    assert torch.allclose(o[128:], tot, atol=1e-5)
+    assert torch.allclose(o[128:192], tot, atol=1e-5)
+    assert torch.equal(o[192:], rows[:, :1].expand(4, 16).reshape(-1))  # row_newbcast:0
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
