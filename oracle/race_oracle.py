@@ -49,7 +49,9 @@ def build() -> None:
 def _lib():
     global _LIB
     if _LIB is None:
-        path = os.path.join(HERE, "liborace.so")
+        # RACE_ORACLE_LIB selects another build of the same source (the
+        # sanitizer builds of `make -C oracle sanitize`)
+        path = os.environ.get("RACE_ORACLE_LIB") or os.path.join(HERE, "liborace.so")
         if not os.path.exists(path):
             subprocess.check_call(["make", "-s", "-C", HERE, "liborace.so"])
         lib = ctypes.CDLL(path)

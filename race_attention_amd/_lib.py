@@ -10,7 +10,9 @@ import os
 import threading
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "librace_attention.so")
+# RACE_ATTENTION_LIB selects another build of the library (e.g. the host-side
+# sanitizer build of `python race_attention_amd/build.py --sanitize`)
+LIB_PATH = os.environ.get("RACE_ATTENTION_LIB") or os.path.join(HERE, "librace_attention.so")
 
 RACE_OK = 0
 RACE_DTYPE_F32 = 0

@@ -20,8 +20,18 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = True) -> str:
-    cmd = [HIPCC] + FLAGS + [SRC, "-o", OUT + ".tmp"]
+# host-side sanitizer build (device code unchanged): -fsanitize applies to the
+# host compilation only, through -Xarch_host
+SAN_OUT = os.path.join(HERE, "_san", "librace_attention_asan.so")
+SAN_FLAGS = ["-g", "-fno-omit-frame-pointer", "-Xarch_host", "-fsanitize=address",
+             "-Xarch_host", "-fsanitize=undefined"]
+
+
+def build(verbose: bool = True, sanitize: bool = False) -> str:
+    out = SAN_OUT if sanitize else OUT
+    if sanitize:
+        os.makedirs(os.path.dirname(out), exist_ok=True)
+    cmd = [HIPCC] + FLAGS + (SAN_FLAGS if sanitize else []) + [SRC, "-o", out + ".tmp"]
     if verbose:
         print("build:", " ".join(cmd), flush=True)
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
@@ -31,9 +41,9 @@ def build(verbose: bool = True) -> str:
         raise RuntimeError("hipcc failed building librace_attention.so")
     if verbose and msgs:
         print("\n".join(msgs))
-    os.replace(OUT + ".tmp", OUT)
-    return OUT
+    os.replace(out + ".tmp", out)
+    return out
 
 
 if __name__ == "__main__":
-    build()
+    build(sanitize="--sanitize" in sys.argv)
