@@ -52,6 +52,7 @@ struct Plan {
     size_t esize = 0;
     size_t state_bytes = 0, fws = 0, bws = 0;
     size_t fws_core = 0, bws_core = 0, part_bytes = 0;  // partial-output buffers follow the core
+    size_t xpart_bytes = 0;  // sliced dX partials (dproj columns), one buffer each for dQ and dK
     // global normalisation: den partials after the forward workspace; rden
     // and gden [N][T] after the backward workspace
     size_t gfws = 0, gbws = 0, tok_bytes = 0;
@@ -131,8 +132,9 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
     p.bws_core = 2 * (size_t)p.N * p.nseg * blk * sizeof(float) +
                  align16(2 * (size_t)p.N * p.nseg * p.nslice * sizeof(float));
     p.part_bytes = p.parts ? (size_t)p.nslice * p.N * d->T * D * sizeof(float) : 0;
-    p.fws = p.fws_core + p.part_bytes;        // partial O
-    p.bws = p.bws_core + 3 * p.part_bytes;    // partial dQ, dK, dV
+    p.xpart_bytes = p.parts ? align16((size_t)p.nslice * p.N * d->T * xcols_of(p.SP, d->K) * p.esize) : 0;
+    p.fws = p.fws_core + p.part_bytes;                         // partial O
+    p.bws = p.bws_core + 2 * p.xpart_bytes + p.part_bytes;     // dproj columns for dQ, dK; partial dV
     p.tok_bytes = align16((size_t)p.N * d->T * sizeof(float));
     p.gfws = p.fws + (p.parts ? p.nslice * p.tok_bytes : 0);
     p.gbws = p.bws + 2 * p.tok_bytes;
@@ -225,6 +227,17 @@ void slice_sum(const Plan &p, const race_desc *d, const float *part, const int64
                                                                 Strides{st[0], st[1], st[2], st[3]}, (T *)out);
 }
 
+// dX (dQ, dK, the probability backward's dx) of sliced instantiations from
+// the slices' dproj columns
+template <typename T>
+void dx_finish(const Plan &p, const race_desc *d, const void *part, const Args &a, const int64_t *st, void *out,
+               hipStream_t s) {
+    const int64_t waves = p.N * ((d->T + 15) / 16);  // one wave per 16 tokens of a stream
+    k_dx_finish<T><<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(
+        (const T *)part, p.nslice, xcols_of(p.SP, d->K), p.SP, d->K, d->L, a.planes, a.planes_m_stride, (int)d->B,
+        (int)d->H, p.N, d->T, Strides{st[0], st[1], st[2], st[3]}, (T *)out);
+}
+
 template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
     const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
     if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
@@ -255,7 +268,7 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
             k_bwd_reduce<T, SP, true, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         else
             k_bwd_reduce<T, SP, false, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
-        if (sliced<T, KB>()) slice_sum<T>(p, d, a.dqpart, d->g_stride, a.dq, s);
+        if (sliced<T, KB>()) dx_finish<T>(p, d, a.dqpart, a, d->g_stride, a.dq, s);
     }
     const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
@@ -267,7 +280,7 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
         else
             k_bwd_out<T, SP, false, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) {
-            slice_sum<T>(p, d, a.dkpart, d->g_stride, a.dk, s);
+            dx_finish<T>(p, d, a.dkpart, a, d->g_stride, a.dk, s);
             slice_sum<T>(p, d, a.dvpart, d->g_stride, a.dv, s);
         }
         if (grad_inv_temp) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, 2 * p.N * p.nseg * p.nslice, grad_inv_temp);
@@ -302,7 +315,7 @@ int gn_bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_beta, hip
     const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
         k_bwd_reduce<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
-        if (sliced<T, KB>()) slice_sum<T>(p, d, a.dqpart, d->g_stride, a.dq, s);
+        if (sliced<T, KB>()) dx_finish<T>(p, d, a.dqpart, a, d->g_stride, a.dq, s);
     }
     const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
@@ -310,7 +323,7 @@ int gn_bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_beta, hip
     if (run_phase(d, RACE_PHASE_OUT)) {
         k_bwd_out<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) {
-            slice_sum<T>(p, d, a.dkpart, d->g_stride, a.dk, s);
+            dx_finish<T>(p, d, a.dkpart, a, d->g_stride, a.dk, s);
             slice_sum<T>(p, d, a.dvpart, d->g_stride, a.dv, s);
         }
         if (grad_beta) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, 2 * p.N * p.nseg * p.nslice, grad_beta);
@@ -368,7 +381,7 @@ template <typename T, int SP, int KB> int probs_impl(const race_desc *d, const P
         return launched("race_probs");
     }
     k_probs<T, SP, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
-    if (sliced<T, KB>()) slice_sum<T>(p, d, a.dqpart, d->g_stride, a.dq, s);
+    if (sliced<T, KB>()) dx_finish<T>(p, d, a.dqpart, a, d->g_stride, a.dq, s);
     if (grad_inv_temp) k_temp_sum<<<1, 256, 0, s>>>(a.tpart, p.N * p.nseg * p.nslice, grad_inv_temp);
     return launched("race_probs_bwd");
 }
@@ -427,10 +440,9 @@ int bwd_args(const race_desc *d, const Plan &p, const void *q, const void *k, co
     a.tpart = a.rstate + blk;
     if (p.parts) {
         float *part = (float *)((char *)ws + p.bws_core);
-        const size_t pe = p.part_bytes / sizeof(float);
         a.dqpart = part;
-        a.dkpart = part + pe;
-        a.dvpart = part + 2 * pe;
+        a.dkpart = (char *)part + p.xpart_bytes;
+        a.dvpart = (float *)((char *)part + 2 * p.xpart_bytes);
     }
     return RACE_OK;
 }
@@ -580,7 +592,7 @@ size_t race_probs_bwd_workspace_bytes(const race_desc *d) {
     Plan p;
     if (make_plan(d, p) != RACE_OK) return 0;
     ok();
-    return probs_ws_core(p) + p.part_bytes;
+    return probs_ws_core(p) + p.xpart_bytes;
 }
 
 int race_probs(const race_desc *d, const void *x, const float *planes, float *P, void *stream) {
@@ -604,14 +616,14 @@ int race_probs_bwd(const race_desc *d, const void *x, const float *planes, const
         (rc = check_out("dx", dx, d->g_stride, p.esize, d)))
         return rc;
     if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
-    const size_t need = probs_ws_core(p) + p.part_bytes;
+    const size_t need = probs_ws_core(p) + p.xpart_bytes;
     if (!ws || ws_bytes < need) return fail(RACE_E_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, need);
     Args a = base_args(d, p, planes);
     a.q = x;
     a.dq = dx;
     a.dprobs = dP;
     a.tpart = (float *)ws;
-    a.dqpart = p.parts ? (float *)((char *)ws + probs_ws_core(p)) : nullptr;
+    a.dqpart = p.parts ? (char *)ws + probs_ws_core(p) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     if (d->dtype == RACE_DTYPE_BF16) return probs_dispatch<bf16>(d, p, a, true, grad_inv_temp, s);
     return probs_dispatch<float>(d, p, a, true, grad_inv_temp, s);
@@ -748,10 +760,9 @@ int race_bwd_global(const race_desc *d, const void *q, const void *k, const void
     a.tpart = a.rstate + blk;
     if (p.parts) {
         float *part = (float *)((char *)ws + p.bws_core);
-        const size_t pe = p.part_bytes / sizeof(float);
         a.dqpart = part;
-        a.dkpart = part + pe;
-        a.dvpart = part + 2 * pe;
+        a.dkpart = (char *)part + p.xpart_bytes;
+        a.dvpart = (float *)((char *)part + 2 * p.xpart_bytes);
     }
     a.out = const_cast<void *>(out);  // read only (the GN per-token terms)
     a.den = const_cast<float *>(den);

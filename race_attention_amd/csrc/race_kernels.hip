@@ -69,7 +69,11 @@ struct Args {
     float *rstate;   // [N][nseg][Spad][D+1]  exclusive suffixes (non-causal: totals)
     float *tpart;    // [2][N][nseg][nslice] partial sums of dU*th
     // sliced() instantiations: per-slice fp32 partial outputs [nslice][N][T][D], summed by k_slice_sum
-    float *opart, *dqpart, *dkpart, *dvpart;
+    float *opart, *dvpart;
+    // sliced dX outputs (dQ, dK; the probability backward's dx): each slice's
+    // dproj columns, T [nslice][N][T][xcols], multiplied by planes^T and
+    // summed over slices by k_dx_finish
+    void *dqpart, *dkpart;
     // global normalisation (GN instantiations; eps is the floor of den):
     // den [N][T] output (sliced: per-slice partials denpart [nslice][N][T]);
     // backward: den and dden (dL/d den, nullable) in, and per-token
@@ -96,6 +100,15 @@ __host__ __device__ constexpr int threads_of(int SP) { return 64 * (SP / WB); }
 // directly and never read blockIdx.z.
 template <typename T, int KB> __host__ __device__ constexpr bool sliced() {
     return !std::is_same<T, bf16>::value || KB > 4;
+}
+
+// Row width (elements, a power of 2) of the sliced dX partials: the
+// projection columns one slice's tables span -- SP / 2^KB tables of KB
+// columns, or KB columns of a table wider than the slice -- rounded up.
+__host__ __device__ constexpr int xcols_of(int SP, int KB) {
+    const int c = (1 << KB) <= SP ? (SP >> KB) * KB : KB;
+    const int m = c < NCOL ? c : NCOL;
+    return m <= 8 ? 8 : (m <= 16 ? 16 : 32);
 }
 
 __device__ __forceinline__ int64_t stream_off(const Strides &s, int n, int B, int H) {
@@ -430,6 +443,33 @@ __device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mc, in
     if (sth) *reinterpret_cast<f32x4 *>(sth + t * LDC + c0) = th;
 }
 
+// Projection columns a workgroup needs: the K columns of every table its
+// bucket slice [z SP, (z+1) SP) touches, as 16-column blocks pb0 .. pb0+nb-1
+// (one task per block and 16-token half).  A slice of part of a table (bf16
+// with K >= 5) or of a few tables (fp32) projects one block instead of all
+// of them; C4's single slice of 8 tables of 4 bits needs both.
+struct PlaneBlocks {
+    int pb0, lg;  // first block; log2 of the tasks per projected tensor (1: one block, 2: both)
+    // full: every column block (compile-time constants; the unsliced
+    // instantiations, whose task loops then specialise per iteration)
+    __device__ __forceinline__ PlaneBlocks(int z, int SP, int KB, int L, bool full) {
+        if (full) {
+            pb0 = 0;
+            lg = 2;
+            return;
+        }
+        const int l0 = (z * SP) >> KB;
+        const int l1 = (min((z + 1) * SP, L << KB) - 1) >> KB;
+        pb0 = __builtin_amdgcn_readfirstlane((l0 * KB) >> 4);
+        lg = __builtin_amdgcn_readfirstlane(((((l1 + 1) * KB) - 1) >> 4) - pb0 + 1);  // blocks: 1 or 2
+    }
+    __device__ __forceinline__ int tasks() const { return 2 << (lg - 1); }  // per projected tensor
+    __device__ __forceinline__ int task(int q) const { return q & (tasks() - 1); }   // task within its tensor
+    __device__ __forceinline__ int tensor(int q) const { return q >> lg; }          // which tensor
+    // column block of task r < tasks() (token half r & 1)
+    __device__ __forceinline__ int mc(int r) const { return pb0 + (r >> 1); }
+};
+
 // Bucket probabilities of the wave's 16 buckets in bucket-row layout:
 // P[nt][e] = P[t = 16nt + i][s = sw + 4g + e]; zero for s >= S or t >= nv (nv:
 // the tile's rows that exist, tile_rows).
@@ -480,6 +520,25 @@ __device__ __forceinline__ void probs_st(const float *sp, const float *sm, int s
             P[nt][3] = h1 * fp[KB - 1];
         }
     }
+}
+
+// Operand of 8 consecutive k values (k = 8g .. 8g+7 of lane (g, i)), the
+// layout ld_frag reads from k-contiguous rows, from registers.
+template <typename T> __device__ __forceinline__ Frag<T> frag_seq(const float (&v)[8]);
+template <> __device__ __forceinline__ Frag<bf16> frag_seq<bf16>(const float (&v)[8]) {
+    Frag<bf16> f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.v[j] = (bf16)v[j];
+    return f;
+}
+template <> __device__ __forceinline__ Frag<float> frag_seq<float>(const float (&v)[8]) {
+    Frag<float> f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f.lo[j] = v[j];
+        f.hi[j] = v[4 + j];
+    }
+    return f;
 }
 
 // ------------------------------------------------------------ constant operands
@@ -974,9 +1033,19 @@ template <typename T> __device__ void zero_lds(T *p, int n, int nth) {
 
 // dX for the tile: dX^T = planes^T dproj^T, 8 tiles over the workgroup's waves,
 // stored straight to rows t0.. (< T) of dst.
-// part != nullptr: fp32 partial of this bucket slice, rows t0.. of a [T][D] block.
-template <typename T, int NW_>
-__device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64_t t0, int64_t Tn, float *part) {
+// part != nullptr (bucket slices): this slice's dproj columns c0 .. c0 + XC - 1
+// instead, rows t0.. of a [T][XC] block -- the product with planes^T and the
+// sum over slices happen in k_dx_finish, on the same operand values.
+template <typename T, int NW_, int XC = 8>
+__device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64_t t0, int64_t Tn, T *part,
+                         int c0 = 0) {
+    if (part) {
+        for (int idx = threadIdx.x; idx < TT * XC; idx += 64 * NW_) {
+            const int t = idx / XC, c = idx % XC;
+            if (t0 + t < Tn) part[(t0 + t) * XC + c] = c0 + c < NCOL ? dproj[sw_off<T, NCOL>(t, c0 + c)] : from_f32<T>(0.f);
+        }
+        return;
+    }
     const int g = lg(), i = li(), w = wave_id();
     T *base = dst + t0 * st;
     for (int q = w; q < 8; q += NW_) {
@@ -984,12 +1053,7 @@ __device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64
         f32x4 acc = zero4();
         mma(acc, ld_frag(sw_frag_ptr<T, NCOL>(plt, 16 * md + i)), ld_frag(sw_frag_ptr<T, NCOL>(dproj, 16 * nt + i)));
         const int t = 16 * nt + i;
-        if (t0 + t < Tn) {
-            if (part)
-                store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, acc);
-            else
-                store4<T>(at_bytes(base, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
-        }
+        if (t0 + t < Tn) store4<T>(at_bytes(base, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
     }
 }
 
@@ -1069,6 +1133,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     float *sSig = (float *)(smem + Ly::oSig), *sTok0 = (float *)(smem + Ly::oTok);
     const int w = wave_id(), i = li(), g = lg(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
               sg = z * SP + sw;
+    const PlaneBlocks pbk(z, SP, KB, a.L, !sliced<T, KB>());  // projection columns of this slice
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -1124,10 +1189,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
         }
         if (jg + GT < j1) issue(jg + GT);
         __syncthreads();  // the group's rows in LDS; the last group's sigmoid rows are read
-        for (int q = w; q < 4 * GT; q += NW_) {
-            float *sp = sSig + (q >> 2) * 2 * TT * LDC;
-            project_tile<T, NL>(sK + (q >> 2) * TT * LDN, sPl, sPlLo, (q >> 1) & 1, q & 1, a.inv_temp, sp,
-                                sp + TT * LDC, nullptr);
+        for (int q = w; q < pbk.tasks() * GT; q += NW_) {
+            const int u = pbk.tensor(q), r = pbk.task(q);
+            float *sp = sSig + u * 2 * TT * LDC;
+            project_tile<T, NL>(sK + u * TT * LDN, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sp, sp + TT * LDC,
+                                nullptr);
         }
         __syncthreads();  // sigmoid rows in LDS
 #pragma unroll
@@ -1360,6 +1426,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sSpK = sSig + 2 * TT * LDC, *sSmK = sSig + 3 * TT * LDC;
     const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
               sg = z * SP + sw;
+    const PlaneBlocks pbk(z, SP, KB, a.L, !sliced<T, KB>());  // projection columns of this slice
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -1427,11 +1494,12 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             pq_.issue(qp, a.sq.t, tn, a.T);
             pk_.issue(kp, a.sk.t, tn, a.T);
             pv_.issue(0, vp, a.sv.t, tn, a.T);
-            for (int q = w; q < 8; q += NW_) {
-                if (q < 4)
-                    project_tile<T, NL>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+            for (int q = w; q < 2 * pbk.tasks(); q += NW_) {
+                const int r = pbk.task(q);
+                if (q < pbk.tasks())
+                    project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
                 else
-                    project_tile<T, NL>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
+                    project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr);
             }
             __syncthreads();
             f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
@@ -1513,11 +1581,12 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             }
         }
         __syncthreads();
-        for (int q = w; q < (CAUSAL ? 8 : 4); q += NW_) {
-            if (q < 4)
-                project_tile<T, NL>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+        for (int q = w; q < (CAUSAL ? 2 : 1) * pbk.tasks(); q += NW_) {
+            const int r = pbk.task(q);
+            if (q < pbk.tasks())
+                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
             else
-                project_tile<T, NL>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
+                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr);
         }
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
@@ -1663,7 +1732,6 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     using Ly = BwdReduceL<T, SP, CAUSAL, KB, GN>;
     using NL = NatL<T, true>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
-    constexpr int NTASK = CAUSAL ? 8 : 4;  // Q projection (4), K projection (4)
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     // this tile's token block (block jt & 1 of two; block 0 of one)
     T *sQ, *sK, *sV, *sG, *sVt, *sGt, *sO;
@@ -1686,6 +1754,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     float *sSpK = sSig + 3 * TT * LDC, *sSmK = sSig + 4 * TT * LDC;
     const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
               sg = z * SP + sw;
+    const PlaneBlocks pbk(z, SP, KB, a.L, !sliced<T, KB>());  // projection columns of this slice
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -1697,7 +1766,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
     const T *gp = (const T *)a.dout + stream_off(a.sdo, n, a.B, a.H);
     T *dqp = (T *)a.dq + stream_off(a.sg, n, a.B, a.H);
-    float *xpart = sliced<T, KB>() ? a.dqpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
+    constexpr int XC = xcols_of(SP, KB);
+    T *xpart = sliced<T, KB>() ? (T *)a.dqpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * XC : nullptr;
+    const int xc0 = ((z * SP) >> KB) * KB;  // first projection column of the slice's tables
     float *sTok = (float *)(smem + Ly::oTok);
     const T *op = GN ? (const T *)a.out + stream_off(a.so, n, a.B, a.H) : nullptr;
     const float *denp = GN ? a.den + (int64_t)n * a.T : nullptr;
@@ -1801,20 +1872,21 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         __syncthreads();
         if constexpr (NB == 2) {
             issue();
-            if (jt > j0) dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart);
+            if (jt > j0) dx_store<T, NW_, XC>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
         }
         if constexpr (GN) gn_token_terms<T, NL, NW_>(sG, sO, sTokIn, sTok, a.eps, rdw, gdw, t0, a.T);
-        for (int q = w; q < NTASK; q += NW_) {
-            if (q < 4)
-                project_tile<T, NL>(sQ, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, sThQ);
+        for (int q = w; q < (CAUSAL ? 2 : 1) * pbk.tasks(); q += NW_) {
+            const int r = pbk.task(q);
+            if (q < pbk.tasks())
+                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, sThQ);
             else
-                project_tile<T, NL>(sK, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpK, sSmK, nullptr);
+                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr);
         }
         // one token block: dQ of the previous tile, from the dproj rows its
         // softmax backward left in LDS, after the projections (they overlap);
         // the next write of sDproj is a barrier away
         if constexpr (NB == 1)
-            if (jt > j0) dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart);
+            if (jt > j0) dx_store<T, NW_, XC>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2], tot;
         Frag<T> Pf;
@@ -1907,7 +1979,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     }
     if (j0 < j1) {
         if constexpr (NB == 2) __syncthreads();  // every wave's dproj rows of the last tile
-        dx_store<T, NW_>(sDproj, sPlT, dqp, a.sg.t, (j1 - 1) * TT, a.T, xpart);
+        dx_store<T, NW_, XC>(sDproj, sPlT, dqp, a.sg.t, (j1 - 1) * TT, a.T, xpart, xc0);
     }
     float *out = a.rdelta + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     for (int md = 0; md < 4; ++md)
@@ -2091,7 +2163,6 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     using NL = NatL<T, true>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
                   LDS_ = Ly::LDS_;
-    constexpr int NTASK = CAUSAL ? 11 : 4;  // K projection (4), Q projection (4), X and Y blocks (3)
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     // this tile's token block (block jr & 1 of two; block 0 of one)
     T *sQ, *sK, *sV, *sG, *sVt, *sGt;
@@ -2115,6 +2186,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     float *sSpQ = sSig + 3 * TT * LDC, *sSmQ = sSig + 4 * TT * LDC;
     const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
               sg = z * SP + sw;
+    const PlaneBlocks pbk(z, SP, KB, a.L, !sliced<T, KB>());  // projection columns of this slice
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
@@ -2127,7 +2199,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     const T *gp = (const T *)a.dout + stream_off(a.sdo, n, a.B, a.H);
     T *dkp = (T *)a.dk + stream_off(a.sg, n, a.B, a.H);
     T *dvp = (T *)a.dv + stream_off(a.sg, n, a.B, a.H);
-    float *xpart = sliced<T, KB>() ? a.dkpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
+    constexpr int XC = xcols_of(SP, KB);
+    T *xpart = sliced<T, KB>() ? (T *)a.dkpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * XC : nullptr;
+    const int xc0 = ((z * SP) >> KB) * KB;  // first projection column of the slice's tables
     float *vpart = sliced<T, KB>() ? a.dvpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
     const float *rdp = GN ? a.rden + (int64_t)n * a.T : nullptr, *gdp = GN ? a.gden + (int64_t)n * a.T : nullptr;
     const float *kwp = !CAUSAL && a.kw ? a.kw + (int64_t)((n / a.H) % a.B) * a.T : nullptr;
@@ -2245,20 +2319,21 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             if (kwp) pt_.issue(kwp, nullptr, tn, a.T);
         }
         if constexpr (GN) pt_.issue(rdp, gdp, tn, a.T);
-        for (int q = w; q < NTASK; q += NW_) {
-            if (q < 4)
-                project_tile<T, NL>(sK, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSpK, sSmK, sThK);
-            else if (q < 8)
-                project_tile<T, NL>(sQ, sPl, sPlLo, (q - 4) >> 1, q & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+        for (int q = w; q < (CAUSAL ? 2 * pbk.tasks() + 3 : pbk.tasks()); q += NW_) {
+            const int r = pbk.task(q);
+            if (q < pbk.tasks())
+                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, sThK);
+            else if (q < 2 * pbk.tasks())
+                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
             else
-                m_tile_xy<T, NL>(q - 8, sV, sG, sX, sY);
+                m_tile_xy<T, NL>(q - 2 * pbk.tasks(), sV, sG, sX, sY);
         }
         // dK of the tile after this one (walking down), from the dproj rows its
         // softmax backward left in LDS: with one token block beside the
         // projections, with two (below) beside the probabilities, after the
         // second barrier; the next write of sDproj is after the third
         if constexpr (!SCN)
-            if (jr + 1 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart);
+            if (jr + 1 < j1) dx_store<T, NW_, XC>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
         // causal, two token blocks: dV of that tile too, its carried part
         // (computed last iteration) plus the in-tile part from its Sc2 rows and
         // its dO tile (still in its block: the next commit there is after this
@@ -2274,7 +2349,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             }
         __syncthreads();
         if constexpr (SCN)
-            if (jr + 1 < j1) dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart);
+            if (jr + 1 < j1) dx_store<T, NW_, XC>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
         f32x4 PKraw[2], PKr[2];  // fp32 P_K (kept for the softmax backward), operand-rounded P_K
         probs_st<KB>(sSpK, sSmK, sg, a.S, jr + 1 < ntiles ? TT : lastv, PKraw);
         PKr[0] = PKraw[0];
@@ -2423,7 +2498,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     }
     if (j0 < j1) {
         if constexpr (NB == 2) __syncthreads();  // every wave's dproj (and Sc2) rows of the last tile
-        dx_store<T, NW_>(sDproj, sPlT, dkp, a.sg.t, j0 * TT, a.T, xpart);
+        dx_store<T, NW_, XC>(sDproj, sPlT, dkp, a.sg.t, j0 * TT, a.T, xpart, xc0);
         if constexpr (SCN) {
             const T *gtn = (const T *)(smem + (j0 & 1) * Ly::TB + Ly::oGt);
 #pragma unroll
@@ -2495,6 +2570,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
     float *sRed = (float *)(smem + Ly::oRed), *sShare = (float *)(smem + Ly::oShare);
     const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
               sg = z * SP + sw;
+    const PlaneBlocks pbk(z, SP, KB, a.L, !sliced<T, KB>());  // projection columns of this slice
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
     const int64_t ntiles = (a.T + TT - 1) / TT;
@@ -2502,7 +2578,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
     const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
     const T *xp = (const T *)a.q + stream_off(a.sq, n, a.B, a.H);
     T *dxp = BWD ? (T *)a.dq + stream_off(a.sg, n, a.B, a.H) : nullptr;
-    float *xpart = BWD && sliced<T, KB>() ? a.dqpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
+    constexpr int XC = xcols_of(SP, KB);
+    T *xpart = BWD && sliced<T, KB>() ? (T *)a.dqpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * XC : nullptr;
+    const int xc0 = ((z * SP) >> KB) * KB;  // first projection column of the slice's tables
 
     HashOps<T, KB> ho;
     WideHash<T, KB> wh;
@@ -2524,8 +2602,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
         px_.template commit<NL>(sX, nullptr);
         if (jt + 1 < j1) px_.issue(xp, a.sq.t, t0 + TT, a.T);  // next tile, in flight during this one
         __syncthreads();
-        for (int q = w; q < 4; q += NW_)
-            project_tile<T, NL>(sX, sPl, sPlLo, q >> 1, q & 1, a.inv_temp, sSp, sSm, BWD ? sTh : nullptr);
+        for (int q = w; q < pbk.tasks(); q += NW_) {
+            project_tile<T, NL>(sX, sPl, sPlLo, pbk.mc(q), q & 1, a.inv_temp, sSp, sSm, BWD ? sTh : nullptr);
+        }
         __syncthreads();
         f32x4 P[2];
         probs_st<KB>(sSp, sSm, sg, a.S, jt + 1 < ntiles ? TT : lastv, P);
@@ -2549,7 +2628,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
                 tsum += softhash_combine<KB, T, SP, NTH>(sShare, sSp, sSm, sTh, z, a.L, a.inv_temp, sDproj);
             }
             __syncthreads();
-            dx_store<T, NW_>(sDproj, sPlT, dxp, a.sg.t, t0, a.T, xpart);
+            dx_store<T, NW_, XC>(sDproj, sPlT, dxp, a.sg.t, t0, a.T, xpart, xc0);
         }
     }
     if constexpr (BWD) {
@@ -2571,6 +2650,60 @@ __global__ void k_slice_sum(const float *part, int nslice, int64_t N, int64_t Tn
     f32x4 acc = *reinterpret_cast<const f32x4 *>(part + row);
     for (int z = 1; z < nslice; ++z) acc += *reinterpret_cast<const f32x4 *>(part + z * zs + row);
     store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc);
+}
+
+// dX of sliced instantiations: out[n][t][:] = sum over slices z (in order)
+// of part[z][n][t][:] . planes[m][c0(z) ..][:] -- per slice one product of
+// its dproj columns with planes^T on the matrix cores, the same operands
+// (bf16 for bf16 inputs) and fp32 accumulation as dx_store's unsliced path.
+// part rows hold XC columns; slice z's columns start at c0(z) = l0(z) K,
+// l0(z) = (z SP) >> K, and end at its last table's (at most L K).  One wave
+// per 16 tokens of a stream: lane (g, i) holds token i, columns 8g .. 8g+7.
+template <typename T>
+__global__ __launch_bounds__(256) void k_dx_finish(const T *part, int nslice, int XC, int SP, int KB, int L,
+                                                   const float *planes, int64_t planes_m_stride, int B, int H,
+                                                   int64_t N, int64_t Tn, Strides so, T *out) {
+    const int64_t wv = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;  // over N * ceil(T / 16)
+    const int64_t nblk = (Tn + 15) / 16;
+    if (wv >= N * nblk) return;  // whole waves
+    const int64_t n = wv / nblk, t0 = (wv % nblk) * 16;
+    const int g = lg(), i = li();
+    const float *pl = planes + (n / (B * H)) * planes_m_stride;
+    const int LK = L * KB;
+    // planes^T operand of each 16-wide d block: column c = 8g + j, d = 16md + i
+    Frag<T> pt[4];
+#pragma unroll
+    for (int md = 0; md < 4; ++md) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = 8 * g + j < LK ? pl[(int64_t)(8 * g + j) * D + 16 * md + i] : 0.f;
+        pt[md] = frag_seq<T>(v);
+    }
+    f32x4 acc[4] = {zero4(), zero4(), zero4(), zero4()};
+    const int64_t t = t0 + i;
+    for (int z = 0; z < nslice; ++z) {
+        const int c0 = ((z * SP) >> KB) * KB;
+        const int c1 = min(LK, ((((z + 1) * SP - 1) >> KB) + 1) * KB);
+        const T *row = part + ((int64_t)z * N * Tn + n * Tn + t) * XC;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = 8 * g + j;
+            v[j] = (t < Tn && c >= c0 && c < c1) ? to_f32(row[c - c0]) : 0.f;
+        }
+        const Frag<T> a = frag_seq<T>(v);
+#pragma unroll
+        for (int md = 0; md < 4; ++md) mma(acc[md], a, pt[md]);
+    }
+    // lane (g, i) holds dX[t0 + 4g + e][16md + i]
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int64_t tt = t0 + 4 * g + e;
+        if (tt < Tn)
+#pragma unroll
+            for (int md = 0; md < 4; ++md)
+                out[stream_off(so, (int)n, B, H) + tt * so.t + 16 * md + i] = from_f32<T>(acc[md][e]);
+    }
 }
 
 // den [N][T] = sum of the per-slice partials [nslice][N][T], in slice order.

@@ -120,11 +120,19 @@ def test_sliced_plans(dtype, K, L, M, B, H, T, spad):
     row = spad * 65
     assert sb > 0 and sb % (N * row * 8) == 0
     nseg = sb // (N * row * 8) - 1
-    part = (spad // (32 if dtype == _lib.RACE_DTYPE_F32 else 128)) * N * T * 64 * 4
+    SP = 32 if dtype == _lib.RACE_DTYPE_F32 else 128
+    part = (spad // SP) * N * T * 64 * 4
     assert fw >= N * nseg * row * 8 + part
-    # the backward runs between 1 and nseg segments (whole forward segments)
-    nslice = spad // (32 if dtype == _lib.RACE_DTYPE_F32 else 128)
-    assert 2 * N * row * 4 + 3 * part <= bw <= 2 * N * nseg * row * 4 + 2 * N * nseg * nslice * 4 + 16 + 3 * part
+    # the backward runs between 1 and nseg segments (whole forward segments);
+    # dQ and dK go through each slice's dproj columns: SP / 2^K tables of K
+    # columns (K columns of a wider table), rounded up to 8, 16 or 32
+    nslice = spad // SP
+    cols = (SP >> K) * K if (1 << K) <= SP else K
+    xc = next(c for c in (8, 16, 32) if c >= min(cols, 32))
+    es = 4 if dtype == _lib.RACE_DTYPE_F32 else 2
+    xpart = -(-(nslice * N * T * xc * es) // 16) * 16
+    lo, hi = 2 * N * row * 4, 2 * N * nseg * row * 4 + 2 * N * nseg * nslice * 4 + 16
+    assert lo + part + 2 * xpart <= bw <= hi + part + 2 * xpart
 
 
 def test_null_and_misaligned_pointers_rejected():
