@@ -232,7 +232,7 @@ void slice_sum(const Plan &p, const race_desc *d, const float *part, const int64
 template <typename T>
 void dx_finish(const Plan &p, const race_desc *d, const void *part, const Args &a, const int64_t *st, void *out,
                hipStream_t s) {
-    const int64_t waves = p.N * ((d->T + 15) / 16);  // one wave per 16 tokens of a stream
+    const int64_t waves = p.N * ((d->T + 16 * DXF_BLK - 1) / (16 * DXF_BLK));  // one wave per 64 tokens
     k_dx_finish<T><<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(
         (const T *)part, p.nslice, xcols_of(p.SP, d->K), p.SP, d->K, d->L, a.planes, a.planes_m_stride, (int)d->B,
         (int)d->H, p.N, d->T, Strides{st[0], st[1], st[2], st[3]}, (T *)out);

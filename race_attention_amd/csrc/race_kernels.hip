@@ -2658,15 +2658,17 @@ __global__ void k_slice_sum(const float *part, int nslice, int64_t N, int64_t Tn
 // (bf16 for bf16 inputs) and fp32 accumulation as dx_store's unsliced path.
 // part rows hold XC columns; slice z's columns start at c0(z) = l0(z) K,
 // l0(z) = (z SP) >> K, and end at its last table's (at most L K).  One wave
-// per 16 tokens of a stream: lane (g, i) holds token i, columns 8g .. 8g+7.
+// per DXF_BLK 16-token blocks of a stream (the planes^T operand is loaded
+// once per wave): lane (g, i) holds token i, columns 8g .. 8g+7.
+constexpr int DXF_BLK = 4;
 template <typename T>
 __global__ __launch_bounds__(256) void k_dx_finish(const T *part, int nslice, int XC, int SP, int KB, int L,
                                                    const float *planes, int64_t planes_m_stride, int B, int H,
                                                    int64_t N, int64_t Tn, Strides so, T *out) {
-    const int64_t wv = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;  // over N * ceil(T / 16)
-    const int64_t nblk = (Tn + 15) / 16;
+    const int64_t wv = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;  // over N * ceil(T / 64)
+    const int64_t nblk = (Tn + 16 * DXF_BLK - 1) / (16 * DXF_BLK);
     if (wv >= N * nblk) return;  // whole waves
-    const int64_t n = wv / nblk, t0 = (wv % nblk) * 16;
+    const int64_t n = wv / nblk, tw = (wv % nblk) * 16 * DXF_BLK;
     const int g = lg(), i = li();
     const float *pl = planes + (n / (B * H)) * planes_m_stride;
     const int LK = L * KB;
@@ -2679,6 +2681,9 @@ __global__ __launch_bounds__(256) void k_dx_finish(const T *part, int nslice, in
         for (int j = 0; j < 8; ++j) v[j] = 8 * g + j < LK ? pl[(int64_t)(8 * g + j) * D + 16 * md + i] : 0.f;
         pt[md] = frag_seq<T>(v);
     }
+    for (int tb = 0; tb < DXF_BLK; ++tb) {
+    const int64_t t0 = tw + 16 * tb;
+    if (t0 >= Tn) break;
     f32x4 acc[4] = {zero4(), zero4(), zero4(), zero4()};
     const int64_t t = t0 + i;
     for (int z = 0; z < nslice; ++z) {
@@ -2703,6 +2708,7 @@ __global__ __launch_bounds__(256) void k_dx_finish(const T *part, int nslice, in
 #pragma unroll
             for (int md = 0; md < 4; ++md)
                 out[stream_off(so, (int)n, B, H) + tt * so.t + 16 * md + i] = from_f32<T>(acc[md][e]);
+    }
     }
 }
 
