@@ -120,6 +120,15 @@ __host__ __device__ constexpr size_t align16(size_t x) { return (x + 15) & ~(siz
 __host__ __device__ constexpr size_t cmax(size_t a, size_t b) { return a > b ? a : b; }
 
 template <typename T> constexpr bool is_bf16() { return sizeof(T) == 2; }
+// Register type of A (the per-bucket sum of P_K) walked forward through a
+// segment from its fp64 start value, one fp32 tile total at a time: fp32 for
+// bf16 inputs, fp64 for fp32 inputs.  Each addition of a positive total
+// rounds once, so n tiles bound the relative error by n 2^-24 (3e-5 for the
+// 512-tile backward segments at 2^20 tokens; the rounding errors of a sum of
+// positive terms grow as sqrt(n) in practice), below the 2^-9 of the bf16
+// operands that the quotients P/(A + eps) feed.  The reverse walk of
+// k_bwd_out subtracts from a segment-end value and stays fp64 for both.
+template <typename T> using CarryA = std::conditional_t<is_bf16<T>(), float, double>;
 
 __device__ __forceinline__ int lg() { return (threadIdx.x & 63) >> 4; }
 __device__ __forceinline__ int li() { return threadIdx.x & 15; }
@@ -1451,10 +1460,10 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     // B in bucket-row layout: lane holds B[s = sw + 4g + e][d = 16md + i]
     const double *st = a.fstate + ((int64_t)n * (a.fnseg + 1) + (CAUSAL ? seg * a.fmul : a.fnseg)) * a.Spad * SROW;
     f32x4 Bc[4];
-    double a0[4];
+    CarryA<T> a0[4];  // A at the tile start
     for (int e = 0; e < 4; ++e) {
         for (int md = 0; md < 4; ++md) Bc[md][e] = (float)st[sidx(sg + 4 * g + e, 16 * md + i)];
-        a0[e] = st[sidx(sg + 4 * g + e, D)];
+        a0[e] = (CarryA<T>)st[sidx(sg + 4 * g + e, D)];
     }
     if constexpr (!CAUSAL) store_ds<T, SP>(sBT, sw, Bc);  // constant totals
 
@@ -1552,7 +1561,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
                 if (w + k * NW_ < 8) Op[k] = fwd_out_partial<T, SP>((w + k * NW_) >> 1, (w + k * NW_) & 1, sBT, sWts);
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
             for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, ld_frag_pi(sVt + (16 * md + i) * LDT));
-            for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
+            for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
             __syncthreads();  // Sc rows in LDS; the P_K / W / B rows are read
             commit(jt + 1);
 #pragma unroll
@@ -1643,7 +1652,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         if constexpr (CAUSAL) {
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
             for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, ld_frag_pi(sVt + (16 * md + i) * LDT));
-            for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
+            for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
         }
     }
 }
@@ -1793,13 +1802,14 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     // forward state in d-row layout: lane holds B^T[d = 16md + 4g + e][s = sw + i]
     const double *st = a.fstate + ((int64_t)n * (a.fnseg + 1) + (CAUSAL ? seg * a.fmul : a.fnseg)) * a.Spad * SROW;
     f32x4 Bt[4], Ut[4];
-    double a0[4], al[4];
+    CarryA<T> a0[4];  // A at the tile start
+    double al[4];
     for (int md = 0; md < 4; ++md) {
         Ut[md] = zero4();
         for (int e = 0; e < 4; ++e) Bt[md][e] = (float)st[sidx(sg + i, 16 * md + 4 * g + e)];
     }
     for (int e = 0; e < 4; ++e) {
-        a0[e] = st[sidx(sg + 4 * g + e, D)];
+        a0[e] = (CarryA<T>)st[sidx(sg + 4 * g + e, D)];
         al[e] = 0.0;
     }
     float tsum = 0.f;
@@ -1962,7 +1972,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
             if constexpr (CAUSAL) mma(Bt[md], ld_frag_pi(sVt + (16 * md + i) * LDT), Pf);
         }
         if constexpr (CAUSAL)
-            for (int e = 0; e < 4; ++e) a0[e] += (double)tot[e];
+            for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
         if constexpr (KB <= 4) {
             tsum += softhash_bwd<KB, T>(PQ, dPQ, sSpQ, sSmQ, sThQ, sg, a.L, a.inv_temp, sDproj, ho);
         } else {

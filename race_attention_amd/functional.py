@@ -61,6 +61,19 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _no_rows(x: torch.Tensor) -> bool:
+    """True for an [M,B,T,H,D] tensor with no (m, b, t, h) rows: an empty
+    batch or sequence.  The operator then has nothing to compute, and the raw
+    calls return empty outputs (and a zero temperature gradient) without a
+    launch, as torch's own ops do on empty tensors; the C ABI itself requires
+    M, B, T, H >= 1."""
+    return x.dim() == 5 and x.shape[:4].numel() == 0
+
+
+def _zero_grad_scalar(want, dev):
+    return torch.zeros((), dtype=torch.float32, device=dev) if want else None
+
+
 def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
@@ -111,6 +124,8 @@ def race_fwd_raw(q, k, v, planes, *, L, K, causal, eps=1e-6, inv_temp, seg_tiles
     """Forward only: returns (out [M,B,T,H,D] contiguous, state for race_bwd_raw)."""
     _require_gpu(q, k, v, planes)
     _check_inputs(q, k, v, planes, L, K)
+    if _no_rows(q):
+        return torch.empty(q.shape, dtype=q.dtype, device=q.device), torch.empty(0, dtype=torch.uint8, device=q.device)
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     planes = planes.to(device=q.device, dtype=torch.float32).contiguous()
     lib = _lib.load()
@@ -133,6 +148,9 @@ def race_bwd_raw(q, k, v, planes, dout, state, *, L, K, causal, eps=1e-6, inv_te
                  want_temp_grad=True):
     """Backward: returns (dq, dk, dv, grad_inv_temp (0-dim fp32 tensor or None))."""
     _require_gpu(q, k, v, planes, dout, state)
+    if _no_rows(q):
+        e = [torch.empty(q.shape, dtype=q.dtype, device=q.device) for _ in range(3)]
+        return e[0], e[1], e[2], _zero_grad_scalar(want_temp_grad, q.device)
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     dout = _aligned(dout.to(q.dtype))
     planes = planes.to(device=q.device, dtype=torch.float32).contiguous()
@@ -217,6 +235,9 @@ def race_probs_raw(x, planes, *, L, K, inv_temp):
     x = _aligned(x)
     planes = planes.to(device=x.device, dtype=torch.float32).contiguous()
     M, B, T, H, _ = x.shape
+    if _no_rows(x):
+        _probs_desc(x, planes, L, K, inv_temp)  # argument checks only
+        return torch.empty((M, B, H, T, L << K), dtype=torch.float32, device=x.device)
     lib = _lib.load()
     d = _probs_desc(x, planes, L, K, inv_temp)
     P = torch.empty((M, B, H, T, L << K), dtype=torch.float32, device=x.device)
@@ -232,6 +253,8 @@ def race_probs_bwd_raw(x, planes, dP, *, L, K, inv_temp, want_temp_grad=True):
     M, B, T, H, _ = x.shape
     if dP.shape != (M, B, H, T, L << K):
         raise ValueError(f"dP must be [M,B,H,T,S] = {(M, B, H, T, L << K)}; got {tuple(dP.shape)}")
+    if _no_rows(x):
+        return torch.empty(x.shape, dtype=x.dtype, device=x.device), _zero_grad_scalar(want_temp_grad, x.device)
     dP = dP.to(torch.float32).contiguous()
     lib = _lib.load()
     d = _probs_desc(x, planes, L, K, inv_temp)
@@ -292,10 +315,12 @@ def race_fwd_ex_raw(q, k, v, planes, *, L, K, inv_temp, kmask=None, want_den=Fal
     planes = planes.to(device=q.device, dtype=torch.float32).contiguous()
     M, B, T, H, _ = q.shape
     kmask = _kmask_check(kmask, B, T, q.device)
-    lib = _lib.load()
-    d = make_desc(q, k, v, planes, L=L, K=K, causal=False, eps=eps, inv_temp=inv_temp, seg_tiles=seg_tiles)
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     den = torch.empty((M, B, H, T), dtype=torch.float32, device=q.device) if want_den else None
+    if _no_rows(q):
+        return out, den, torch.empty(0, dtype=torch.uint8, device=q.device)
+    lib = _lib.load()
+    d = make_desc(q, k, v, planes, L=L, K=K, causal=False, eps=eps, inv_temp=inv_temp, seg_tiles=seg_tiles)
     d.o_stride = _strides4(out)
     sb = lib.race_state_bytes(ctypes.byref(d))
     if sb == 0:
@@ -315,6 +340,9 @@ def race_bwd_ex_raw(q, k, v, planes, dout, dden, state, *, L, K, inv_temp, kmask
                     want_temp_grad=True):
     """Backward of race_fwd_ex_raw: returns (dq, dk, dv, grad_inv_temp or None)."""
     _require_gpu(q, k, v, planes, state)
+    if _no_rows(q):
+        e = [torch.empty(q.shape, dtype=q.dtype, device=q.device) for _ in range(3)]
+        return e[0], e[1], e[2], _zero_grad_scalar(want_temp_grad, q.device)
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     M, B, T, H, _ = q.shape
     dout = _aligned(dout.to(q.dtype)) if dout is not None else torch.zeros(q.shape, dtype=q.dtype, device=q.device)
@@ -394,11 +422,15 @@ def race_global_fwd_raw(q, k, v, planes, *, L, K, beta, floor=1e-6, seg_tiles=0)
     """F2 forward: returns (out [M,B,T,H,D], den [M,B,H,T] fp32, state)."""
     _require_gpu(q, k, v, planes)
     _check_inputs(q, k, v, planes, L, K)
+    M, B, T, H, _ = q.shape
+    if _no_rows(q):
+        return (torch.empty(q.shape, dtype=q.dtype, device=q.device),
+                torch.empty((M, B, H, T), dtype=torch.float32, device=q.device),
+                torch.empty(0, dtype=torch.uint8, device=q.device))
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     planes = planes.to(device=q.device, dtype=torch.float32).contiguous()
     lib = _lib.load()
     d = make_desc(q, k, v, planes, L=L, K=K, causal=True, eps=floor, inv_temp=beta, seg_tiles=seg_tiles)
-    M, B, T, H, _ = q.shape
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     den = torch.empty((M, B, H, T), dtype=torch.float32, device=q.device)
     d.o_stride = _strides4(out)
@@ -419,6 +451,9 @@ def race_global_bwd_raw(q, k, v, planes, out, den, dout, dden, state, *, L, K, b
     """F2 backward: returns (dq, dk, dv, grad_beta (0-dim fp32 tensor or None)).
     dden (gradient of den, [M,B,H,T]) may be None."""
     _require_gpu(q, k, v, planes, out, den, dout, state)
+    if _no_rows(q):
+        e = [torch.empty(q.shape, dtype=q.dtype, device=q.device) for _ in range(3)]
+        return e[0], e[1], e[2], _zero_grad_scalar(want_beta_grad, q.device)
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     out = _aligned(out)
     dout = _aligned(dout.to(q.dtype))
@@ -498,8 +533,10 @@ def prefix_mean_fwd(w: torch.Tensor, v: torch.Tensor, eps: float = 1e-6) -> torc
         raise ValueError("shapes must be [NS,T] and [NS,T,D] with matching NS and T")
     w, v = w.contiguous(), v.contiguous()
     NS, T, D = v.shape
-    lib = _lib.load()
     E = torch.empty_like(v)
+    if v.numel() == 0:  # race_pref.cpp returns its empty output too
+        return E
+    lib = _lib.load()
     wb = lib.race_prefix_mean_workspace_bytes(NS, T, D)
     ws = torch.empty(max(wb, 16), dtype=torch.uint8, device=v.device)
     rc = lib.race_prefix_mean_fwd(_ptr(w), _ptr(v), _ptr(E), NS, T, D, float(eps), _ptr(ws),
@@ -513,9 +550,11 @@ def prefix_mean_bwd(w, v, gE, eps: float = 1e-6):
     _require_gpu(w, v, gE)
     w, v, gE = w.contiguous(), v.contiguous(), gE.contiguous().to(torch.float32)
     NS, T, D = v.shape
-    lib = _lib.load()
     gW = torch.empty_like(w)
     gV = torch.empty_like(v)
+    if v.numel() == 0:
+        return gW.zero_(), gV
+    lib = _lib.load()
     wb = lib.race_prefix_mean_workspace_bytes(NS, T, D)
     ws = torch.empty(max(wb, 16), dtype=torch.uint8, device=v.device)
     rc = lib.race_prefix_mean_bwd(_ptr(w), _ptr(v), _ptr(gE), _ptr(gW), _ptr(gV), NS, T, D, float(eps),
