@@ -802,29 +802,41 @@ __device__ void softhash_share(const f32x4 (&P)[2], const f32x4 (&dP)[2], const 
 }
 
 // after the shares are visible: du -> dproj for the slice's tables; returns
-// this thread's part of sum du * th
+// this thread's part of sum du * th.  Each (token, table, bit) item's sum over
+// the table's waves is split between two neighbouring lanes (half the waves
+// each, in order) and joined with a DPP swap, so every wave of the workgroup
+// takes part and the dependent chain of LDS reads is half as long.
 template <int KB, typename T, int SP, int NTH>
 __device__ float softhash_combine(const float *share, const float *sp, const float *sm, const float *sth, int z, int L,
                                   float inv_temp, T *dproj) {
     constexpr int LDC = ld_of<float>(NCOL), R = 1 << KB, NW_ = SP / WB;
     constexpr int NTAB = SP >= R ? SP / R : 1;          // tables (or one table part) in the slice
     constexpr int WPT = (R / WB) < NW_ ? R / WB : NW_;  // waves per table in the slice
+    constexpr int SPLIT = WPT % 2 == 0 ? 2 : 1, WPL = WPT / SPLIT, ITEMS = TT * NTAB * KB;
     const int l0 = (z * SP) >> KB;
     float tsum = 0.f;
-    for (int idx = threadIdx.x; idx < TT * NTAB * KB; idx += NTH) {
-        const int t = idx / (NTAB * KB), r = idx % (NTAB * KB), tl = r / KB, k = r % KB;
-        const int l = l0 + tl;
-        if (l >= L) continue;
+    for (int base = 0; base < ITEMS * SPLIT; base += NTH) {  // the same trip count in every lane
+        const int idx = base + (int)threadIdx.x, item = idx / SPLIT, half = idx % SPLIT;
+        const int t = item / (NTAB * KB), r = item % (NTAB * KB), tl = r / KB, k = r % KB;
+        const bool live = item < ITEMS && l0 + tl < L;
         float sx = 0.f, sd = 0.f;
-        for (int ww = tl * WPT; ww < (tl + 1) * WPT; ++ww) {
-            sx += share[(ww * TT + t) * (KB + 1) + k];
-            sd += share[(ww * TT + t) * (KB + 1) + KB];
+        if (live)
+            for (int u = 0; u < WPL; ++u) {
+                const int ww = tl * WPT + half * WPL + u;
+                sx += share[(ww * TT + t) * (KB + 1) + k];
+                sd += share[(ww * TT + t) * (KB + 1) + KB];
+            }
+        if constexpr (SPLIT == 2) {  // lanes 2m and 2m + 1 hold one item
+            sx += dpp_f<0xB1>(sx);
+            sd += dpp_f<0xB1>(sd);
         }
-        const int col = l * KB + k;
-        const float th = sth[t * LDC + col];
-        const float du = sx - sd * (sp[t * LDC + col] - sm[t * LDC + col]);
-        tsum += du * th;
-        dproj[sw_off<T, NCOL>(t, col)] = from_f32<T>(du * inv_temp * (1.f - th * th));
+        if (live && half == 0) {
+            const int col = (l0 + tl) * KB + k;
+            const float th = sth[t * LDC + col];
+            const float du = sx - sd * (sp[t * LDC + col] - sm[t * LDC + col]);
+            tsum += du * th;
+            dproj[sw_off<T, NCOL>(t, col)] = from_f32<T>(du * inv_temp * (1.f - th * th));
+        }
     }
     return tsum;
 }
