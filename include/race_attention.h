@@ -45,7 +45,7 @@ extern "C" {
  * dimensions of a [M,B,T,H,D] tensor whose D dimension is contiguous; a zero
  * M stride expresses the reference's M-fold expand (misc/race.py:167-168). */
 typedef struct race_desc {
-    int64_t M, B, T, H, D;    /* estimators, batch, tokens, heads, head dim (D = 64) */
+    int64_t M, B, T, H, D;    /* estimators, batch, tokens (T <= 2^35), heads, head dim (D = 64) */
     int32_t L, K;             /* hash tables, hash bits per table (R = 2^K buckets) */
     int32_t causal;           /* 1: prefix (causal) aggregation, 0: full sequence */
     int32_t dtype;            /* RACE_DTYPE_F32 or RACE_DTYPE_BF16 for q/k/v/out/grads */

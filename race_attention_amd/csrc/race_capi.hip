@@ -81,6 +81,9 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
         return fail(RACE_E_INVALID, "M, B, T, H must be >= 1 (got %lld, %lld, %lld, %lld)", (long long)d->M,
                     (long long)d->B, (long long)d->T, (long long)d->H);
     if (d->D != D) return fail(RACE_E_UNSUPPORTED, "head dim D=%lld unsupported (this build: D=64)", (long long)d->D);
+    // the kernels count tiles of 32 tokens in 32-bit integers
+    if (d->T > (1ll << 35))
+        return fail(RACE_E_UNSUPPORTED, "T=%lld tokens per sequence unsupported (T <= 2^35)", (long long)d->T);
     if (d->L < 1 || d->K < 1) return fail(RACE_E_INVALID, "L and K must be >= 1 (got L=%d K=%d)", d->L, d->K);
     if (d->K > 8) return fail(RACE_E_UNSUPPORTED, "K=%d hash bits unsupported (K <= 8)", d->K);
     if (d->L * d->K > NCOL)
@@ -238,14 +241,34 @@ void dx_finish(const Plan &p, const race_desc *d, const void *part, const Args &
         (int)d->H, p.N, d->T, Strides{st[0], st[1], st[2], st[3]}, (T *)out);
 }
 
+// Whole-tile instantiations (template flag AL of the tile kernels): compiled
+// for the causal bf16 slices of 128 buckets at 4 and 8 hash bits, and used
+// when every tile holds TT tokens (T % TT == 0) and every bucket of every
+// slice is one of the S buckets, so no load, store or probability needs a
+// row or bucket guard.  Elsewhere the template argument is false and both
+// branches below launch the same kernel.
+template <typename T, int SP, int KB> constexpr bool al_compiled() {
+    return std::is_same<T, bf16>::value && SP == 128 && (KB == 4 || KB == 8);
+}
+bool whole_tiles(const race_desc *d, const Plan &p) { return d->T % TT == 0 && p.S == p.Spad; }
+
 template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
     const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
-    if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
+    constexpr bool ALC = al_compiled<T, SP, KB>();
+    const bool al = ALC && whole_tiles(d, p);
+    if (run_phase(d, RACE_PHASE_REDUCE)) {
+        if (al)
+            k_fwd_reduce<T, SP, KB, ALC><<<grid, threads_of(SP), 0, s>>>(a);
+        else
+            k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
+    }
     const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
         k_fwd_scan<<<dim3((elems + SCAN_THREADS - 1) / SCAN_THREADS, (unsigned)p.N), SCAN_THREADS, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
     if (run_phase(d, RACE_PHASE_OUT)) {
-        if (d->causal)
+        if (d->causal && al)
+            k_fwd_out<T, SP, true, KB, false, ALC><<<grid, threads_of(SP), 0, s>>>(a);
+        else if (d->causal)
             k_fwd_out<T, SP, true, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         else
             k_fwd_out<T, SP, false, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
@@ -263,8 +286,12 @@ template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Pla
 template <typename T, int SP, int KB>
 int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hipStream_t s) {
     const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
+    constexpr bool ALC = al_compiled<T, SP, KB>();
+    const bool al = ALC && whole_tiles(d, p);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
-        if (d->causal)
+        if (d->causal && al)
+            k_bwd_reduce<T, SP, true, KB, false, ALC><<<grid, threads_of(SP), 0, s>>>(a);
+        else if (d->causal)
             k_bwd_reduce<T, SP, true, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         else
             k_bwd_reduce<T, SP, false, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
@@ -275,7 +302,9 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
         k_bwd_scan<<<dim3((elems + SCAN_THREADS - 1) / SCAN_THREADS, (unsigned)p.N), SCAN_THREADS, 0, s>>>(a.rstate, a.rdelta, p.nseg, elems,
                                                                             d->causal);
     if (run_phase(d, RACE_PHASE_OUT)) {
-        if (d->causal)
+        if (d->causal && al)
+            k_bwd_out<T, SP, true, KB, false, ALC><<<grid, threads_of(SP), 0, s>>>(a);
+        else if (d->causal)
             k_bwd_out<T, SP, true, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         else
             k_bwd_out<T, SP, false, KB, false><<<grid, threads_of(SP), 0, s>>>(a);

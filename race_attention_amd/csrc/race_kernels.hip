@@ -282,12 +282,18 @@ __device__ __forceinline__ void nat_mma(f32x4 &acc, const T *A, int rA, const T 
 // Chunks of 16 bytes, or of 8 bytes when 16-byte chunks would leave some of
 // the workgroup's threads without one (every wave shares the staging work).
 // rows of the tile at t0 that exist (0 .. TT), as a wave-uniform 32-bit count
+// (32-bit compares on the two halves of Tn - t0: the scalar unit has no
+// 64-bit ordered compare, and a vector one would cost VALU work per tile)
 __device__ __forceinline__ int tile_rows(int64_t t0, int64_t Tn) {
-    const int64_t r = Tn - t0;
-    return r < 0 ? 0 : (r > TT ? TT : (int)r);
+    const uint64_t r = (uint64_t)(Tn - t0);
+    const int32_t hi = (int32_t)(r >> 32);
+    const uint32_t lo = (uint32_t)r;
+    return hi < 0 ? 0 : ((hi > 0 || lo >= (uint32_t)TT) ? TT : (int)lo);
 }
 
-template <typename T, int NTH> struct Prefetch {
+// AL (whole tiles): the launch guarantees that every tile issued holds TT
+// rows, so the loads need no row guards.
+template <typename T, int NTH, bool AL = false> struct Prefetch {
     static constexpr int CB = (TT * D * (int)sizeof(T) / 16 >= NTH) ? 16 : 8;
     typedef typename ChunkOf<CB>::type chunk_t;
     static constexpr int EPC = CB / sizeof(T), CPR = D / EPC, CHUNKS = TT * CPR;
@@ -297,7 +303,7 @@ template <typename T, int NTH> struct Prefetch {
     // 32-bit (the host bounds 32 * token stride below 2^31)
     __device__ __forceinline__ void issue(const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn) {
         const T *base = src + t0 * st;
-        const int rem = tile_rows(t0, Tn);
+        const int rem = AL ? TT : tile_rows(t0, Tn);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int idx = threadIdx.x + j * NTH, t = idx / CPR, c = idx % CPR;
@@ -334,7 +340,7 @@ template <typename T, int NTH> struct Prefetch {
 // written as packed token pairs to consecutive LDS words (few bank conflicts)
 // while each token row is still read in 32-byte runs.  NPART tensors share
 // the workgroup: this one uses threads [part*NTH/NPART, (part+1)*NTH/NPART).
-template <typename T, int NTH, int NPART> struct PrefetchT {
+template <typename T, int NTH, int NPART, bool AL = false> struct PrefetchT {
     static constexpr int NT = NTH / NPART;
     static constexpr int EPC = 8 / sizeof(T), CPR = D / EPC, TASKS = (TT / 2) * CPR;
     static constexpr int PER = (TASKS + NT - 1) / NT;
@@ -347,7 +353,7 @@ template <typename T, int NTH, int NPART> struct PrefetchT {
     }
     __device__ __forceinline__ void issue(int part, const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn) {
         const T *base = src + t0 * st;
-        const int rem = tile_rows(t0, Tn);
+        const int rem = AL ? TT : tile_rows(t0, Tn);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             int tp, c;
@@ -484,8 +490,10 @@ struct PlaneBlocks {
 // the tile's rows that exist, tile_rows).
 // For K >= 2 the 4 buckets of a lane share one table and differ in the two
 // lowest corner bits: P = hi * (bit1 ? s+ : s-) * (bit0 ? s+ : s-).
-template <int KB>
-__device__ __forceinline__ void probs_st(const float *sp, const float *sm, int sw, int S, int nv, f32x4 (&P)[2]) {
+// FULL: every token of the tile exists and every bucket of the wave is below
+// S (no validity masks; the whole-tile instantiations, AL).
+template <int KB, bool FULL>
+__device__ __forceinline__ void probs_st_(const float *sp, const float *sm, int sw, int S, int nv, f32x4 (&P)[2]) {
     constexpr int LDC = ld_of<float>(NCOL);
     constexpr int R = 1 << KB;
     const int g = lg(), i = li();
@@ -493,18 +501,18 @@ __device__ __forceinline__ void probs_st(const float *sp, const float *sm, int s
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int t = 16 * nt + i;
-        const bool tv = t < nv;
+        const bool tv = FULL || t < nv;
         if constexpr (KB == 1) {
             // tables s0/2 and s0/2 + 1; corner r = 1 is sigmoid(+2u)
-            const bool v01 = tv && s0 < S, v23 = tv && s0 + 2 < S;
+            const bool v01 = FULL || (tv && s0 < S), v23 = FULL || (tv && s0 + 2 < S);
             const int l0 = v01 ? s0 >> 1 : 0, l1 = v23 ? (s0 >> 1) + 1 : 0;
             P[nt][0] = v01 ? sm[t * LDC + l0] : 0.f;
             P[nt][1] = v01 ? sp[t * LDC + l0] : 0.f;
             P[nt][2] = v23 ? sm[t * LDC + l1] : 0.f;
             P[nt][3] = v23 ? sp[t * LDC + l1] : 0.f;
         } else {
-            const bool v = tv && s0 < S;
-            const int l = s0 < S ? s0 >> KB : 0;
+            const bool v = FULL || (tv && s0 < S);
+            const int l = (FULL || s0 < S) ? s0 >> KB : 0;
             const int r0 = s0 & (R - 1);
             const float *pp = sp + t * LDC + l * KB, *pm = sm + t * LDC + l * KB;
             float fp[KB], fm[KB];
@@ -529,6 +537,10 @@ __device__ __forceinline__ void probs_st(const float *sp, const float *sm, int s
             P[nt][3] = h1 * fp[KB - 1];
         }
     }
+}
+template <int KB, bool AL = false>
+__device__ __forceinline__ void probs_st(const float *sp, const float *sm, int sw, int S, int nv, f32x4 (&P)[2]) {
+    probs_st_<KB, AL>(sp, sm, sw, S, nv, P);
 }
 
 // Operand of 8 consecutive k values (k = 8g .. 8g+7 of lane (g, i)), the
@@ -1057,13 +1069,13 @@ template <typename T> __device__ void zero_lds(T *p, int n, int nth) {
 // part != nullptr (bucket slices): this slice's dproj columns c0 .. c0 + XC - 1
 // instead, rows t0.. of a [T][XC] block -- the product with planes^T and the
 // sum over slices happen in k_dx_finish, on the same operand values.
-template <typename T, int NW_, int XC = 8>
+template <typename T, int NW_, int XC = 8, bool AL = false>
 __device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64_t t0, int64_t Tn, T *part,
                          int c0 = 0) {
     if (part) {
         for (int idx = threadIdx.x; idx < TT * XC; idx += 64 * NW_) {
             const int t = idx / XC, c = idx % XC;
-            if (t0 + t < Tn) part[(t0 + t) * XC + c] = c0 + c < NCOL ? dproj[sw_off<T, NCOL>(t, c0 + c)] : from_f32<T>(0.f);
+            if (AL || t < tile_rows(t0, Tn)) part[(t0 + t) * XC + c] = c0 + c < NCOL ? dproj[sw_off<T, NCOL>(t, c0 + c)] : from_f32<T>(0.f);
         }
         return;
     }
@@ -1074,7 +1086,7 @@ __device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64
         f32x4 acc = zero4();
         mma(acc, ld_frag(sw_frag_ptr<T, NCOL>(plt, 16 * md + i)), ld_frag(sw_frag_ptr<T, NCOL>(dproj, 16 * nt + i)));
         const int t = 16 * nt + i;
-        if (t0 + t < Tn) store4<T>(at_bytes(base, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
+        if (AL || t < tile_rows(t0, Tn)) store4<T>(at_bytes(base, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
     }
 }
 
@@ -1142,7 +1154,7 @@ __device__ __forceinline__ void tile_sums(const Frag<T> &Pf, const Consts<T> &cs
     }
 }
 
-template <typename T, int SP, int KB>
+template <typename T, int SP, int KB, bool AL = false>
 __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     using Ly = FwdReduceL<T, SP>;
@@ -1158,9 +1170,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
-    const int64_t ntiles = (a.T + TT - 1) / TT;
-    const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
-    const int64_t send = min(a.T, j1 * TT);  // the segment's tokens end here (tiles past it load nothing)
+    const int ntiles = (int)((a.T + TT - 1) / TT);  // the host bounds T by 2^35
+    const int j0 = seg * a.tps, j1 = min(ntiles, j0 + a.tps);
+    const int64_t send = min(a.T, (int64_t)j1 * TT);  // the segment's tokens end here (tiles past it load nothing)
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
     const float *kwp = a.kw ? a.kw + (int64_t)((n / a.H) % a.B) * a.T : nullptr;  // batch row's key weights
@@ -1181,13 +1193,15 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     for (int md = 0; md < 4; ++md) accBm[md] = zero4();
 
     wait_state_loads();
-    Prefetch<T, NTH> pk_[GT];
-    PrefetchT<T, NTH, 1> pv_[GT];
+    Prefetch<T, NTH, AL> pk_[GT];
+    PrefetchT<T, NTH, 1, AL> pv_[GT];
     TokPre pt_[GT];
-    auto issue = [&](int64_t jg) {
+    auto issue = [&](int jg) {
 #pragma unroll
         for (int u = 0; u < GT; ++u) {
-            const int64_t t0 = (jg + u) * TT;
+            // AL loads whole tiles without row guards: a group's tile past
+            // the segment reloads the segment's last tile (unused)
+            const int64_t t0 = (int64_t)(AL ? min(jg + u, j1 - 1) : jg + u) * TT;
             pk_[u].issue(kp, a.sk.t, t0, send);
             pv_[u].issue(0, vp, a.sv.t, t0, send);
             if (kwp) pt_[u].issue(kwp, nullptr, t0, send);
@@ -1195,7 +1209,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     };
     if (j0 < j1) issue(j0);
     int b = 0;
-    for (int64_t jg = j0; jg < j1; jg += GT, b ^= 1) {
+    for (int jg = j0; jg < j1; jg += GT, b ^= 1) {
         // commit the group's rows (V^T and key weights to buffer b: the
         // group before last read the other one, and its readers passed the
         // last barrier), then start the next group's loads
@@ -1219,12 +1233,12 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
         __syncthreads();  // sigmoid rows in LDS
 #pragma unroll
         for (int u = 0; u < GT; ++u) {
-            const int64_t jt = jg + u;
+            const int jt = jg + u;
             if (jt >= j1) break;
             const float *sp = sSig + u * 2 * TT * LDC;
             const T *vt = sVt + u * D * LDT;
             f32x4 PK[2];
-            probs_st<KB>(sp, sp + TT * LDC, sg, a.S, tile_rows(jt * TT, a.T), PK);
+            probs_st<KB, AL>(sp, sp + TT * LDC, sg, a.S, tile_rows((int64_t)jt * TT, a.T), PK);
             if (kwp)  // P_K' = w_t P_K
                 for (int nt = 0; nt < 2; ++nt) {
                     const float wt = sTok[u * 2 * TT + 16 * nt + i];
@@ -1330,7 +1344,7 @@ template <typename T, int SP, bool CAUSAL, bool GN> struct FwdOutL {
 // the waves' shares (sDen [NW_][TT]) and the md == 0 tiles write it (sliced
 // instantiations: this slice's den share, a partial).  GN also divides the
 // tile's numerator by max(den, eps) (sliced: the numerator is the partial).
-template <typename T, int SP, bool CAUSAL, bool GN = false>
+template <typename T, int SP, bool CAUSAL, bool GN = false, bool AL = false>
 __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T *Wts, const T *sVt, T *op,
                              int64_t st, int64_t t0, int64_t Tn, float *part, const float *sDen = nullptr,
                              float *den = nullptr, float eps = 0.f) {
@@ -1367,9 +1381,9 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
 #pragma unroll
             for (int e = 0; e < 4; ++e) O[e] *= r;
         }
-        if (md == 0 && g == 0 && t0 + t < Tn) den[t0 + t] = dn;
+        if (md == 0 && g == 0 && (AL || t < tile_rows(t0, Tn))) den[t0 + t] = dn;
     }
-    if (t0 + t < Tn) {
+    if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
             store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, O);
         else
@@ -1403,7 +1417,7 @@ template <typename T, int SP> __device__ f32x4 fwd_out_partial(int md, int nt, c
     for (int kp = 0; kp < SP / 32; ++kp) mma(O, ld_frag(pb + 32 * kp), ld_frag(pw + 32 * kp));
     return O;
 }
-template <typename T, int SP, bool GN>
+template <typename T, int SP, bool GN, bool AL = false>
 __device__ void fwd_out_final(int md, int nt, f32x4 O, const T *sVt, const T *sc, T *op, int64_t st, int64_t t0,
                               int64_t Tn, float *part, const float *sDen, float *den, float eps) {
     constexpr int LDT = ldp_of<T>(TT);
@@ -1420,9 +1434,9 @@ __device__ void fwd_out_final(int md, int nt, f32x4 O, const T *sVt, const T *sc
 #pragma unroll
             for (int e = 0; e < 4; ++e) O[e] *= r;
         }
-        if (md == 0 && g == 0 && t0 + t < Tn) den[t0 + t] = dn;
+        if (md == 0 && g == 0 && (AL || t < tile_rows(t0, Tn))) den[t0 + t] = dn;
     }
-    if (t0 + t < Tn) {
+    if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
             store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, O);
         else
@@ -1432,7 +1446,7 @@ __device__ void fwd_out_final(int md, int nt, f32x4 O, const T *sVt, const T *sc
 
 // GN: global normalisation (causal only) -- W = P_Q, and the output is
 // divided by den(t) = sum over all buckets of P_Q A_s(t), clamped below at eps.
-template <typename T, int SP, bool CAUSAL, int KB, bool GN>
+template <typename T, int SP, bool CAUSAL, int KB, bool GN, bool AL = false>
 __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(Args a) {
     if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
@@ -1451,9 +1465,9 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
-    const int64_t ntiles = (a.T + TT - 1) / TT;
-    const int lastv = (int)(a.T - (ntiles - 1) * TT);  // rows of the last tile
-    const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
+    const int ntiles = (int)((a.T + TT - 1) / TT);  // the host bounds T by 2^35
+    const int lastv = (int)(a.T - (int64_t)(ntiles - 1) * TT);  // rows of the last tile
+    const int j0 = seg * a.tps, j1 = min(ntiles, j0 + a.tps);
     const T *qp = (const T *)a.q + stream_off(a.sq, n, a.B, a.H);
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
@@ -1480,13 +1494,13 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     if constexpr (!CAUSAL) store_ds<T, SP>(sBT, sw, Bc);  // constant totals
 
     wait_state_loads();
-    Prefetch<T, NTH> pq_, pk_;
-    PrefetchT<T, NTH, 1> pv_;
+    Prefetch<T, NTH, AL> pq_, pk_;
+    PrefetchT<T, NTH, 1, AL> pv_;
     if (j0 < j1) {
-        pq_.issue(qp, a.sq.t, j0 * TT, a.T);
+        pq_.issue(qp, a.sq.t, (int64_t)j0 * TT, a.T);
         if constexpr (CAUSAL) {
-            pk_.issue(kp, a.sk.t, j0 * TT, a.T);
-            pv_.issue(0, vp, a.sv.t, j0 * TT, a.T);
+            pk_.issue(kp, a.sk.t, (int64_t)j0 * TT, a.T);
+            pv_.issue(0, vp, a.sv.t, (int64_t)j0 * TT, a.T);
         }
     }
     if constexpr (Ly::SCN) {
@@ -1496,8 +1510,8 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         // V^T goes to the other buffer) and the rest of O.
         T *sSc = (T *)(smem + Ly::oSc);
         zero_lds<T>(sSc, TT * LDT, NTH);  // its (t < 16 <= t') block stays zero
-        auto vt_of = [&](int64_t j) { return (T *)(smem + ((j & 1) ? Ly::oVt2 : Ly::oVt)); };
-        auto commit = [&](int64_t j) {  // the prefetched rows, V^T to the buffer of tile j
+        auto vt_of = [&](int j) { return (T *)(smem + ((j & 1) ? Ly::oVt2 : Ly::oVt)); };
+        auto commit = [&](int j) {  // the prefetched rows, V^T to the buffer of tile j
             wait_vmem();
             pq_.template commit<NL>(sQ, nullptr);
             pk_.template commit<NL>(sK, nullptr);
@@ -1505,11 +1519,11 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         };
         if (j0 < j1) commit(j0);
         constexpr int NQ = (8 + NW_ - 1) / NW_;  // output tiles per wave
-        for (int64_t jt = j0; jt < j1; ++jt) {
-            const int64_t t0 = jt * TT;
+        for (int jt = j0; jt < j1; ++jt) {
+            const int64_t t0 = (int64_t)jt * TT;
             // next tile's rows; the last tile reloads itself (loads stay in
             // range, issue and commit unconditional)
-            const int64_t tn = (jt + 1 < j1 ? jt + 1 : jt) * TT;
+            const int64_t tn = (int64_t)(jt + 1 < j1 ? jt + 1 : jt) * TT;
             sVt = vt_of(jt);
             __syncthreads();  // this tile's rows in LDS; the previous tile's O rows are done
             pq_.issue(qp, a.sq.t, tn, a.T);
@@ -1525,9 +1539,9 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             __syncthreads();
             f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
             Frag<T> Pf;
-            probs_st<KB>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
+            probs_st<KB, AL>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
             if constexpr (CAUSAL) {
-                probs_st<KB>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
+                probs_st<KB, AL>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
                 Pf = store_ts_operand<T, SP>(sPts, sw, PK, cst);
                 for (int nt = 0; nt < 2; ++nt) {
                     Acum[nt] = zero4();
@@ -1580,14 +1594,14 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             for (int k = 0; k < NQ; ++k) {
                 const int q = w + k * NW_;
                 if (q < 8)
-                    fwd_out_final<T, SP, GN>(q >> 1, q & 1, Op[k], sVt, sSc, op, a.so.t, t0, a.T, opart, sDen, denp,
+                    fwd_out_final<T, SP, GN, AL>(q >> 1, q & 1, Op[k], sVt, sSc, op, a.so.t, t0, a.T, opart, sDen, denp,
                                              a.eps);
             }
         }
         return;
     }
-    for (int64_t jt = j0; jt < j1; ++jt) {
-        const int64_t t0 = jt * TT;
+    for (int jt = j0; jt < j1; ++jt) {
+        const int64_t t0 = (int64_t)jt * TT;
         __syncthreads();  // previous tile's readers of sVt / sPts / sWts / sBT are done
         pq_.template commit<NL>(sQ, nullptr);
         if constexpr (CAUSAL) {
@@ -1612,9 +1626,9 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
         Frag<T> Pf;
-        probs_st<KB>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
+        probs_st<KB, AL>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
         if constexpr (CAUSAL) {
-            probs_st<KB>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
+            probs_st<KB, AL>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
             Pf = token_operand<T>(PK, cst);
@@ -1659,7 +1673,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         }
         __syncthreads();
         for (int q = w; q < 8; q += NW_)
-            fwd_out_tile<T, SP, CAUSAL, GN>(q >> 1, q & 1, sBT, sPts, sWts, sVt, op, a.so.t, t0, a.T, opart, sDen,
+            fwd_out_tile<T, SP, CAUSAL, GN, AL>(q >> 1, q & 1, sBT, sPts, sWts, sVt, op, a.so.t, t0, a.T, opart, sDen,
                                             denp, a.eps);
         if constexpr (CAUSAL) {
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
@@ -1694,7 +1708,7 @@ __device__ void gn_token_terms(const T *sG, const T *sO, const float *sIn, float
         if (c == 0) {
             sOut[t] = rd;
             sOut[TT + t] = gd;
-            if (rdw && t0 + t < Tn) {
+            if (rdw && t < tile_rows(t0, Tn)) {
                 rdw[t0 + t] = rd;
                 gdw[t0 + t] = gd;
             }
@@ -1746,7 +1760,7 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
 // GN (global normalisation, causal only): with rd = 1/max(den, eps) and
 // gd = dL/d den per token (gn_token_terms, from the O and dO tiles),
 // W = P_Q rd, dP_Q = G rd + gd A_s(t), dA = gd P_Q.
-template <typename T, int SP, bool CAUSAL, int KB, bool GN>
+template <typename T, int SP, bool CAUSAL, int KB, bool GN, bool AL = false>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
@@ -1779,9 +1793,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
-    const int64_t ntiles = (a.T + TT - 1) / TT;
-    const int lastv = (int)(a.T - (ntiles - 1) * TT);  // rows of the last tile
-    const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
+    const int ntiles = (int)((a.T + TT - 1) / TT);  // the host bounds T by 2^35
+    const int lastv = (int)(a.T - (int64_t)(ntiles - 1) * TT);  // rows of the last tile
+    const int j0 = seg * a.tps, j1 = min(ntiles, j0 + a.tps);
     const T *qp = (const T *)a.q + stream_off(a.sq, n, a.B, a.H);
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
@@ -1828,8 +1842,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
 
     wait_state_loads();
     constexpr int NP = CAUSAL ? 2 : 1;  // transposed tiles: dO (and V)
-    Prefetch<T, NTH> pq_, pk_, po_;  // po_: GN's O tile
-    PrefetchT<T, NTH, NP> pg_, pv_;
+    Prefetch<T, NTH, AL> pq_, pk_, po_;  // po_: GN's O tile
+    PrefetchT<T, NTH, NP, AL> pg_, pv_;
     TokPre pt_;
     // Writes the prefetched rows to token block b.
     auto commit = [&](int b) {
@@ -1851,28 +1865,28 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     };
     constexpr int NB = Ly::NB;
     if (j0 < j1) {
-        pq_.issue(qp, a.sq.t, j0 * TT, a.T);
-        pg_.issue(0, gp, a.sdo.t, j0 * TT, a.T);
+        pq_.issue(qp, a.sq.t, (int64_t)j0 * TT, a.T);
+        pg_.issue(0, gp, a.sdo.t, (int64_t)j0 * TT, a.T);
         if constexpr (CAUSAL) {
-            pk_.issue(kp, a.sk.t, j0 * TT, a.T);
-            pv_.issue(1, vp, a.sv.t, j0 * TT, a.T);
+            pk_.issue(kp, a.sk.t, (int64_t)j0 * TT, a.T);
+            pv_.issue(1, vp, a.sv.t, (int64_t)j0 * TT, a.T);
         }
         if constexpr (GN) {
-            po_.issue(op, a.so.t, j0 * TT, a.T);
-            pt_.issue(denp, ddp, j0 * TT, a.T);
+            po_.issue(op, a.so.t, (int64_t)j0 * TT, a.T);
+            pt_.issue(denp, ddp, (int64_t)j0 * TT, a.T);
         } else if constexpr (!CAUSAL) {
-            if (ddp) pt_.issue(ddp, nullptr, j0 * TT, a.T);
+            if (ddp) pt_.issue(ddp, nullptr, (int64_t)j0 * TT, a.T);
         }
         commit(NB == 2 ? (int)(j0 & 1) : 0);
     }
-    for (int64_t jt = j0; jt < j1; ++jt) {
-        const int64_t t0 = jt * TT;
+    for (int jt = j0; jt < j1; ++jt) {
+        const int64_t t0 = (int64_t)jt * TT;
         use_block(NB == 2 ? (int)(jt & 1) : 0);
         // next tile's rows; the last tile reloads itself (loads stay in range).
         // Issue and commit run every iteration: a commit under a condition
         // leaves the prefetch registers possibly pending at the loop head, and
         // the wait placed there also waits for the previous tile's stores.
-        const int64_t tn = (jt + 1 < j1 ? jt + 1 : jt) * TT;
+        const int64_t tn = (int64_t)(jt + 1 < j1 ? jt + 1 : jt) * TT;
         auto issue = [&]() {
             pq_.issue(qp, a.sq.t, tn, a.T);
             pg_.issue(0, gp, a.sdo.t, tn, a.T);
@@ -1894,7 +1908,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         __syncthreads();
         if constexpr (NB == 2) {
             issue();
-            if (jt > j0) dx_store<T, NW_, XC>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
+            if (jt > j0) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
         }
         if constexpr (GN) gn_token_terms<T, NL, NW_>(sG, sO, sTokIn, sTok, a.eps, rdw, gdw, t0, a.T);
         for (int q = w; q < (CAUSAL ? 2 : 1) * pbk.tasks(); q += NW_) {
@@ -1908,13 +1922,13 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
         // softmax backward left in LDS, after the projections (they overlap);
         // the next write of sDproj is a barrier away
         if constexpr (NB == 1)
-            if (jt > j0) dx_store<T, NW_, XC>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
+            if (jt > j0) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2], tot;
         Frag<T> Pf;
-        probs_st<KB>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
+        probs_st<KB, AL>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
         if constexpr (CAUSAL) {
-            probs_st<KB>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
+            probs_st<KB, AL>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
             Pf = token_operand<T>(PK, cst, po);
             for (int nt = 0; nt < 2; ++nt) {
                 Acum[nt] = zero4();
@@ -2001,7 +2015,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     }
     if (j0 < j1) {
         if constexpr (NB == 2) __syncthreads();  // every wave's dproj rows of the last tile
-        dx_store<T, NW_, XC>(sDproj, sPlT, dqp, a.sg.t, (j1 - 1) * TT, a.T, xpart, xc0);
+        dx_store<T, NW_, XC, AL>(sDproj, sPlT, dqp, a.sg.t, (int64_t)(j1 - 1) * TT, a.T, xpart, xc0);
     }
     float *out = a.rdelta + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     for (int md = 0; md < 4; ++md)
@@ -2114,7 +2128,7 @@ template <typename T, int SP> __device__ void sc2_tile(int r, const T *Wts, cons
     store4<T>(sc2 + (16 * nt + i) * LDT + 16 * mt + 4 * g, acc);
 }
 
-template <typename T, int SP, bool CAUSAL>
+template <typename T, int SP, bool CAUSAL, bool AL = false>
 __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts, const T *sGt, T *dvp, int64_t st,
                         int64_t t0, int64_t Tn, float *part) {
     constexpr int LDT = ldp_of<T>(TT);
@@ -2140,7 +2154,7 @@ __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts
         mma(acc, ld_frag_pi(sGt + (16 * md + i) * LDT), frag_acc<T>(Sc2[0], Sc2[1]));
     }
     const int t = 16 * nt + i;
-    if (t0 + t < Tn) {
+    if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
             store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, acc);
         else
@@ -2159,14 +2173,14 @@ template <typename T, int SP> __device__ f32x4 dv_part(int md, int nt, const T *
     for (int kp = 0; kp < SP / 32; ++kp) mma(acc, ld_frag(pu + 32 * kp), ld_frag(pp + 32 * kp));
     return acc;
 }
-template <typename T>
+template <typename T, bool AL = false>
 __device__ void dv_finish(int md, int nt, f32x4 acc, const T *sGt, const T *sc2, T *dvp, int64_t st, int64_t t0,
                           int64_t Tn, float *part) {
     constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
     mma(acc, ld_frag_pi(sGt + (16 * md + i) * LDT), ld_frag_pi(sc2 + (16 * nt + i) * LDT));
     const int t = 16 * nt + i;
-    if (t0 + t < Tn) {
+    if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
             store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, acc);
         else
@@ -2177,7 +2191,7 @@ __device__ void dv_finish(int md, int nt, f32x4 acc, const T *sGt, const T *sc2,
 // GN (global normalisation, causal only): W = P_Q rd and dA = gd P_Q per
 // token (rd = 1/max(den, eps), gd = dL/d den), so the reverse walk needs
 // neither the forward state nor G.
-template <typename T, int SP, bool CAUSAL, int KB, bool GN>
+template <typename T, int SP, bool CAUSAL, int KB, bool GN, bool AL = false>
 __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
@@ -2212,9 +2226,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
 
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
-    const int64_t ntiles = (a.T + TT - 1) / TT;
-    const int lastv = (int)(a.T - (ntiles - 1) * TT);  // rows of the last tile
-    const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
+    const int ntiles = (int)((a.T + TT - 1) / TT);  // the host bounds T by 2^35
+    const int lastv = (int)(a.T - (int64_t)(ntiles - 1) * TT);  // rows of the last tile
+    const int j0 = seg * a.tps, j1 = min(ntiles, j0 + a.tps);
     const T *qp = (const T *)a.q + stream_off(a.sq, n, a.B, a.H);
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
@@ -2278,8 +2292,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     float tsum = 0.f;
 
     wait_state_loads();
-    Prefetch<T, NTH> pq_, pk_, pvn_;  // pvn_: non-causal V (natural only)
-    PrefetchT<T, NTH, 2> pg_, pv_;   // causal dO and V (natural and transposed)
+    Prefetch<T, NTH, AL> pq_, pk_, pvn_;  // pvn_: non-causal V (natural only)
+    PrefetchT<T, NTH, 2, AL> pg_, pv_;   // causal dO and V (natural and transposed)
     TokPre pt_;
     // Writes the prefetched rows to token block b.
     auto commit = [&](int b) {
@@ -2306,7 +2320,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
 #pragma unroll
     for (int k = 0; k < NQD; ++k) dvacc[k] = zero4();
     if (j0 < j1) {
-        const int64_t tl = (j1 - 1) * TT;
+        const int64_t tl = (int64_t)(j1 - 1) * TT;
         pk_.issue(kp, a.sk.t, tl, a.T);
         if constexpr (CAUSAL) {
             pv_.issue(1, vp, a.sv.t, tl, a.T);
@@ -2319,15 +2333,15 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         if constexpr (GN) pt_.issue(rdp, gdp, tl, a.T);
         commit(NB == 2 ? (int)((j1 - 1) & 1) : 0);
     }
-    for (int64_t jr = j1 - 1; jr >= j0; --jr) {
-        const int64_t t0 = jr * TT;
+    for (int jr = j1 - 1; jr >= j0; --jr) {
+        const int64_t t0 = (int64_t)jr * TT;
         use_block(NB == 2 ? (int)(jr & 1) : 0);
         // next tile's rows (walking down); the last tile reloads itself (loads
         // stay in range).  Issue and commit run every iteration: a commit under
         // a condition leaves the prefetch registers possibly pending at the
         // loop head, and the wait placed there also waits for the previous
         // tile's stores.
-        const int64_t tn = (jr > j0 ? jr - 1 : jr) * TT;
+        const int64_t tn = (int64_t)(jr > j0 ? jr - 1 : jr) * TT;
         __syncthreads();
         // issued after the barrier: the previous tile's dK stores have had
         // the barrier's time to drain from the memory pipeline
@@ -2355,7 +2369,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         // projections, with two (below) beside the probabilities, after the
         // second barrier; the next write of sDproj is after the third
         if constexpr (!SCN)
-            if (jr + 1 < j1) dx_store<T, NW_, XC>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
+            if (jr + 1 < j1) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
         // causal, two token blocks: dV of that tile too, its carried part
         // (computed last iteration) plus the in-tile part from its Sc2 rows and
         // its dO tile (still in its block: the next commit there is after this
@@ -2366,14 +2380,14 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
 #pragma unroll
                 for (int k = 0; k < NQD; ++k)
                     if (w + k * NW_ < 8)
-                        dv_finish<T>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gtn, sSc2, dvp, a.sg.t, t0 + TT,
+                        dv_finish<T, AL>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gtn, sSc2, dvp, a.sg.t, t0 + TT,
                                      a.T, vpart);
             }
         __syncthreads();
         if constexpr (SCN)
-            if (jr + 1 < j1) dx_store<T, NW_, XC>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
+            if (jr + 1 < j1) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
         f32x4 PKraw[2], PKr[2];  // fp32 P_K (kept for the softmax backward), operand-rounded P_K
-        probs_st<KB>(sSpK, sSmK, sg, a.S, jr + 1 < ntiles ? TT : lastv, PKraw);
+        probs_st<KB, AL>(sSpK, sSmK, sg, a.S, jr + 1 < ntiles ? TT : lastv, PKraw);
         PKr[0] = PKraw[0];
         PKr[1] = PKraw[1];
         float kwt[2] = {1.f, 1.f};  // non-causal key weights: P_K' = w_t P_K
@@ -2392,7 +2406,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             Frag<T> Wf;
             if constexpr (GN) {
                 f32x4 PQ[2], W[2];
-                probs_st<KB>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
+                probs_st<KB, AL>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
                 for (int nt = 0; nt < 2; ++nt) {
                     const float rd = sTok[16 * nt + i], gd = sTok[TT + 16 * nt + i];
                     for (int e = 0; e < 4; ++e) {
@@ -2403,7 +2417,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                 Wf = store_ts_operand<T, SP>(sWts, sw, W, cst);
             } else {
                 f32x4 PQ[2], Acum[2], W[2], tot, dB[4];
-                probs_st<KB>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
+                probs_st<KB, AL>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
                 // forward state at the tile start: end state minus this tile's sums
                 if constexpr (BM) {
                     tot = zero4();
@@ -2485,14 +2499,14 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
                     if (w + k * NW_ < 8) dvacc[k] = dv_part<T, SP>((w + k * NW_) >> 1, (w + k * NW_) & 1, sUT, sPts);
             } else {
                 for (int q = w; q < 8; q += NW_)
-                    dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T, vpart);
+                    dv_tile<T, SP, CAUSAL, AL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T, vpart);
             }
         } else {
             __syncthreads();  // all waves' P_K rows in LDS
             if constexpr (NB == 2) commit((int)((jr + 1) & 1));
             // non-causal: dV^T = U^T P_K^T; dP_K = alpha + v . U (totals)
             for (int q = w; q < 8; q += NW_)
-                dv_tile<T, SP, CAUSAL>(q >> 1, q & 1, sUT, sPts, nullptr, nullptr, dvp, a.sg.t, t0, a.T, vpart);
+                dv_tile<T, SP, CAUSAL, AL>(q >> 1, q & 1, sUT, sPts, nullptr, nullptr, dvp, a.sg.t, t0, a.T, vpart);
             const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
             for (int nt = 0; nt < 2; ++nt) {
                 f32x4 c = zero4();
@@ -2520,13 +2534,13 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
     }
     if (j0 < j1) {
         if constexpr (NB == 2) __syncthreads();  // every wave's dproj (and Sc2) rows of the last tile
-        dx_store<T, NW_, XC>(sDproj, sPlT, dkp, a.sg.t, j0 * TT, a.T, xpart, xc0);
+        dx_store<T, NW_, XC, AL>(sDproj, sPlT, dkp, a.sg.t, (int64_t)j0 * TT, a.T, xpart, xc0);
         if constexpr (SCN) {
             const T *gtn = (const T *)(smem + (j0 & 1) * Ly::TB + Ly::oGt);
 #pragma unroll
             for (int k = 0; k < NQD; ++k)
                 if (w + k * NW_ < 8)
-                    dv_finish<T>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gtn, sSc2, dvp, a.sg.t, j0 * TT, a.T,
+                    dv_finish<T, AL>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gtn, sSc2, dvp, a.sg.t, (int64_t)j0 * TT, a.T,
                                  vpart);
         }
     }
@@ -2595,9 +2609,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
     const PlaneBlocks pbk(z, SP, KB, a.L, !sliced<T, KB>());  // projection columns of this slice
     const int n = blockIdx.y, seg = blockIdx.x;
     const int m = n / (a.B * a.H);
-    const int64_t ntiles = (a.T + TT - 1) / TT;
-    const int lastv = (int)(a.T - (ntiles - 1) * TT);  // rows of the last tile
-    const int64_t j0 = (int64_t)seg * a.tps, j1 = min(ntiles, j0 + a.tps);
+    const int ntiles = (int)((a.T + TT - 1) / TT);  // the host bounds T by 2^35
+    const int lastv = (int)(a.T - (int64_t)(ntiles - 1) * TT);  // rows of the last tile
+    const int j0 = seg * a.tps, j1 = min(ntiles, j0 + a.tps);
     const T *xp = (const T *)a.q + stream_off(a.sq, n, a.B, a.H);
     T *dxp = BWD ? (T *)a.dq + stream_off(a.sg, n, a.B, a.H) : nullptr;
     constexpr int XC = xcols_of(SP, KB);
@@ -2617,9 +2631,9 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
                             BWD ? sPlT : nullptr);
     float tsum = 0.f;
     Prefetch<T, NTH> px_;
-    if (j0 < j1) px_.issue(xp, a.sq.t, j0 * TT, a.T);
-    for (int64_t jt = j0; jt < j1; ++jt) {
-        const int64_t t0 = jt * TT;
+    if (j0 < j1) px_.issue(xp, a.sq.t, (int64_t)j0 * TT, a.T);
+    for (int jt = j0; jt < j1; ++jt) {
+        const int64_t t0 = (int64_t)jt * TT;
         __syncthreads();  // the previous tile's readers of sX, sSig, sDproj are done
         px_.template commit<NL>(sX, nullptr);
         if (jt + 1 < j1) px_.issue(xp, a.sq.t, t0 + TT, a.T);  // next tile, in flight during this one

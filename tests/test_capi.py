@@ -84,6 +84,7 @@ def test_device_temperature_skips_host_value_check():
     ("L", 9, -2, "projection columns"),
     ("L", 0, -1, "L and K"),
     ("T", 0, -1, "must be >= 1"),
+    ("T", (1 << 35) + 1, -2, "T <= 2^35"),
     ("dtype", 7, -1, "dtype"),
 ])
 def test_invalid_descriptors_rejected(field, value, code, msg):
