@@ -591,6 +591,9 @@ template <typename T> struct Consts {
     static constexpr int LDT = ldp_of<T>(TT), LDI = ldp_of<T>(16);
     static constexpr size_t bytes = sizeof(T) * (TT * LDT + 16 * LDI);
     const T *tri, *id;
+    // bf16: the prefix and total operands in registers (cache(), once the
+    // table is visible), so the tile loops do not read them from LDS
+    Frag<T> tri0_, tri1_, ones_;
     __device__ __forceinline__ void init(T *buf, int nth) {
         T *t = buf, *d = buf + TT * LDT;
         for (int idx = threadIdx.x; idx < TT * LDT; idx += nth)
@@ -600,8 +603,25 @@ template <typename T> struct Consts {
         tri = t;
         id = d;
     }
-    __device__ __forceinline__ Frag<T> tri_op(int nt) const { return ld_frag_pi(tri + (16 * nt + li()) * LDT); }
-    __device__ __forceinline__ Frag<T> ones() const { return ld_frag_pi(tri + (TT - 1) * LDT); }
+    __device__ __forceinline__ void cache() {
+        if constexpr (is_bf16<T>()) {
+            tri0_ = ld_frag_pi(tri + li() * LDT);
+            tri1_ = ld_frag_pi(tri + (16 + li()) * LDT);
+            ones_ = ld_frag_pi(tri + (TT - 1) * LDT);
+        }
+    }
+    __device__ __forceinline__ Frag<T> tri_op(int nt) const {
+        if constexpr (is_bf16<T>())
+            return nt ? tri1_ : tri0_;
+        else
+            return ld_frag_pi(tri + (16 * nt + li()) * LDT);
+    }
+    __device__ __forceinline__ Frag<T> ones() const {
+        if constexpr (is_bf16<T>())
+            return ones_;
+        else
+            return ld_frag_pi(tri + (TT - 1) * LDT);
+    }
     __device__ __forceinline__ Frag4<T> ident() const { return ld_frag16(id + li() * LDI); }
 };
 // bf16 pairwise transposes: id[n][k] = (k == n), 32 x 32.  With the pair
@@ -611,6 +631,7 @@ template <typename T> struct PairOps {
     static constexpr int LDT = ldp_of<T>(TT);
     static constexpr size_t bytes = is_bf16<T>() ? sizeof(T) * TT * LDT : 0;
     const T *id = nullptr;
+    Frag<T> lo_, hi_;  // in registers after cache()
     __device__ __forceinline__ void init(T *buf, int nth) {
         if constexpr (is_bf16<T>()) {
             for (int idx = threadIdx.x; idx < TT * LDT; idx += nth)
@@ -618,8 +639,14 @@ template <typename T> struct PairOps {
             id = buf;
         }
     }
-    __device__ __forceinline__ Frag<T> lo() const { return ld_frag_pi(id + li() * LDT); }
-    __device__ __forceinline__ Frag<T> hi() const { return ld_frag_pi(id + (16 + li()) * LDT); }
+    __device__ __forceinline__ void cache() {
+        if constexpr (is_bf16<T>()) {
+            lo_ = ld_frag_pi(id + li() * LDT);
+            hi_ = ld_frag_pi(id + (16 + li()) * LDT);
+        }
+    }
+    __device__ __forceinline__ Frag<T> lo() const { return lo_; }
+    __device__ __forceinline__ Frag<T> hi() const { return hi_; }
 };
 
 // 16-deep constant A operand of mma16_x: bf16 holds the row's 16 k values
@@ -683,14 +710,14 @@ template <typename T, int KB> struct HashOps {
         }
         a = buf;
     }
-    __device__ __forceinline__ OpX<T> op() const {
-        OpX<T> o;
+    OpX<T> op_;  // in registers after cache()
+    __device__ __forceinline__ void cache() {
         if constexpr (is_bf16<T>())
-            o.f = ld_frag_pi(a + li() * LDI);
+            op_.f = ld_frag_pi(a + li() * LDI);
         else
-            o.f = ld_frag16(a + li() * LDI);
-        return o;
+            op_.f = ld_frag16(a + li() * LDI);
     }
+    __device__ __forceinline__ OpX<T> op() const { return op_; }
 };
 
 // Every (table, corner) pair of the wave's 16 buckets has exactly one corner
@@ -887,6 +914,22 @@ __device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const f
     constexpr int LDC = ld_of<float>(NCOL);
     const int g = lg(), i = li(), l0 = sw >> KB;
     const OpX<T> A = ho.op();
+    // the corner rows' tanh(u) = sp - sm and th, read ahead of the products
+    // (column 0 stands in for tables past L, whose results are dropped)
+    float tu[2][4], th[2][4];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            int k = 0, tl = 0, de = 0;
+            const int kind = HashOps<T, KB>::kind_of(4 * g + e, k, tl, de);
+            const int l = l0 + tl, c = l < L ? l * KB + k : 0, t = 16 * nt + i;
+            tu[nt][e] = th[nt][e] = 0.f;
+            if (kind == 1) {
+                tu[nt][e] = sp[t * LDC + c] - sm[t * LDC + c];
+                th[nt][e] = sth[t * LDC + c];
+            }
+        }
     float tsum = 0.f;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -908,11 +951,9 @@ __device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const f
                     sum = X[2];
                 else
                     sum = X[(e & 2) | 1];
-                const float tu = sp[t * LDC + col] - sm[t * LDC + col];
-                const float du = X[e] - sum * tu;
-                const float th = sth[t * LDC + col];
-                tsum += du * th;
-                dproj[sw_off<T, NCOL>(t, col)] = from_f32<T>(du * inv_temp * (1.f - th * th));
+                const float du = X[e] - sum * tu[nt][e];
+                tsum += du * th[nt][e];
+                dproj[sw_off<T, NCOL>(t, col)] = from_f32<T>(du * inv_temp * (1.f - th[nt][e] * th[nt][e]));
             }
         }
     }
@@ -1180,6 +1221,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
     load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
+    __syncthreads();  // the constant tables in LDS; their operands to registers
+    cst.cache();
     // segment sums: A in fp64; B in fp64 for fp32 inputs, and for bf16 in
     // fp32 MFMA accumulators (bf16 uses B only through bf16 operands).  Tile
     // sums are added tile by tile in token order.
@@ -1482,6 +1525,8 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
     load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
+    __syncthreads();  // the constant tables in LDS; their operands to registers
+    cst.cache();
     // carried state: causal = prefix at the segment start, non-causal = totals.
     // B in bucket-row layout: lane holds B[s = sw + 4g + e][d = 16md + i]
     const double *st = a.fstate + ((int64_t)n * (a.fnseg + 1) + (CAUSAL ? seg * a.fmul : a.fnseg)) * a.Spad * SROW;
@@ -1761,7 +1806,7 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
 // gd = dL/d den per token (gn_token_terms, from the O and dO tiles),
 // W = P_Q rd, dP_Q = G rd + gd A_s(t), dA = gd P_Q.
 template <typename T, int SP, bool CAUSAL, int KB, bool GN, bool AL = false>
-__global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
+__global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
     using Ly = BwdReduceL<T, SP, CAUSAL, KB, GN>;
@@ -1825,6 +1870,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_reduce(Args a) {
     po.init((T *)(smem + Ly::oPair), NTH);
     load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, sPlT);
     zero_lds<T>(sDproj, TT * LDDP, NTH);
+    __syncthreads();  // the constant tables in LDS; their operands to registers
+    cst.cache();
+    if constexpr (KB <= 4) ho.cache();
+    po.cache();
     // forward state in d-row layout: lane holds B^T[d = 16md + 4g + e][s = sw + i]
     const double *st = a.fstate + ((int64_t)n * (a.fnseg + 1) + (CAUSAL ? seg * a.fmul : a.fnseg)) * a.Spad * SROW;
     f32x4 Bt[4], Ut[4];
@@ -2192,7 +2241,7 @@ __device__ void dv_finish(int md, int nt, f32x4 acc, const T *sGt, const T *sc2,
 // token (rd = 1/max(den, eps), gd = dL/d den), so the reverse walk needs
 // neither the forward state nor G.
 template <typename T, int SP, bool CAUSAL, int KB, bool GN, bool AL = false>
-__global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
+__global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
     using Ly = BwdOutL<T, SP, CAUSAL, KB, GN>;
@@ -2260,6 +2309,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         zero_lds<T>(sY, TT * LDT, NTH);
         zero_lds<T>(sSc2, TT * LDT, NTH);  // its (t < 16 <= tau) block stays zero
     }
+    __syncthreads();  // the constant tables in LDS; their operands to registers
+    cst.cache();
+    if constexpr (KB <= 4) ho.cache();
+    po.cache();
     // reverse carries (U, alpha) after the segment; forward state at the segment end
     const float *rs = a.rstate + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     const double *fs =
@@ -2355,7 +2408,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
             if (kwp) pt_.issue(kwp, nullptr, tn, a.T);
         }
         if constexpr (GN) pt_.issue(rdp, gdp, tn, a.T);
-        for (int q = w; q < (CAUSAL ? 2 * pbk.tasks() + 3 : pbk.tasks()); q += NW_) {
+        // the three masked v.g^T blocks: here, or (two token blocks, every
+        // projection task on a wave of its own) in the next phase, whose
+        // bucket work leaves issue slots to fill
+        constexpr bool MT2 = SCN;
+        for (int q = w; q < (CAUSAL ? 2 * pbk.tasks() + (MT2 ? 0 : 3) : pbk.tasks()); q += NW_) {
             const int r = pbk.task(q);
             if (q < pbk.tasks())
                 project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, sThK);
@@ -2386,6 +2443,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_bwd_out(Args a) {
         __syncthreads();
         if constexpr (SCN)
             if (jr + 1 < j1) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
+        if constexpr (MT2)  // X and Y are read after the next barrier
+            for (int q = w; q < 3; q += NW_) m_tile_xy<T, NL>(q, sV, sG, sX, sY);
         f32x4 PKraw[2], PKr[2];  // fp32 P_K (kept for the softmax backward), operand-rounded P_K
         probs_st<KB, AL>(sSpK, sSmK, sg, a.S, jr + 1 < ntiles ? TT : lastv, PKraw);
         PKr[0] = PKraw[0];
@@ -2629,6 +2688,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
     }
     load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr,
                             BWD ? sPlT : nullptr);
+    if constexpr (BWD && KB <= 4) {
+        __syncthreads();  // the hash table in LDS; its operand to registers
+        ho.cache();
+    }
     float tsum = 0.f;
     Prefetch<T, NTH> px_;
     if (j0 < j1) px_.issue(xp, a.sq.t, (int64_t)j0 * TT, a.T);
