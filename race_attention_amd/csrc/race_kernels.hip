@@ -392,6 +392,71 @@ template <typename T, int NTH, int NPART, bool AL = false> struct PrefetchT {
     }
 };
 
+// Two token tiles staged like PrefetchT (natural and/or transposed), the
+// first by the workgroup's first half of waves and the second by the other
+// half.  The tensor is chosen per wave (scalar selects of the source and
+// destinations), so every lane takes part and no lane mask is needed.
+template <typename T, int NTH, bool AL = false> struct PrefetchT2 {
+    static constexpr int NT = NTH / 2;
+    static constexpr int EPC = 8 / sizeof(T), CPR = D / EPC, TASKS = (TT / 2) * CPR;
+    static_assert(NT % 64 == 0 && TASKS % NT == 0, "whole waves per tensor, whole tasks per lane");
+    static constexpr int PER = TASKS / NT;
+    uint2 v[PER][2];
+    __device__ __forceinline__ static bool second() { return wave_id() >= NT / 64; }
+    __device__ __forceinline__ static void task_of(int j, int &tp, int &c) {
+        const int task = ((int)threadIdx.x & (NT - 1)) + j * NT;
+        tp = (task >> 2) & 15;
+        c = (task & 3) + 4 * (task >> 6);
+    }
+    __device__ __forceinline__ void issue(const T *__restrict__ src0, int64_t st0, const T *__restrict__ src1,
+                                          int64_t st1, int64_t t0, int64_t Tn) {
+        const bool sc = second();
+        const int64_t st = sc ? st1 : st0;
+        const T *base = (sc ? src1 : src0) + t0 * st;
+        const int rem = AL ? TT : tile_rows(t0, Tn);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            int tp, c;
+            task_of(j, tp, c);
+            const uint32_t off = tile_off(2 * tp, st, c * EPC, sizeof(T));
+            if constexpr (AL) {
+                v[j][0] = ld_at<uint2>(base, off);
+                v[j][1] = ld_at<uint2>(base, off + (uint32_t)st * (uint32_t)sizeof(T));
+            } else {
+                v[j][0] = uint2{0, 0};
+                v[j][1] = uint2{0, 0};
+                if (2 * tp < rem) v[j][0] = ld_at<uint2>(base, off);
+                if (2 * tp + 1 < rem) v[j][1] = ld_at<uint2>(base, off + (uint32_t)st * (uint32_t)sizeof(T));
+            }
+        }
+    }
+    template <class NL = NatL<T, false>>
+    __device__ __forceinline__ void commit(T *nat0, T *trn0, T *nat1, T *trn1) const {
+        constexpr int LDT = ldp_of<T>(TT);
+        const bool sc = second();
+        T *nat = sc ? nat1 : nat0, *trn = sc ? trn1 : trn0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            int tp, c;
+            task_of(j, tp, c);
+            *reinterpret_cast<uint2 *>(nat + NL::off(2 * tp, c * EPC)) = v[j][0];
+            *reinterpret_cast<uint2 *>(nat + NL::off(2 * tp + 1, c * EPC)) = v[j][1];
+            const uint2 a = v[j][0], b = v[j][1];
+            uint32_t *row = reinterpret_cast<uint32_t *>(trn + (c * EPC) * LDT + 2 * tp);
+            constexpr int RW = LDT * (int)sizeof(T) / 4;
+            if constexpr (sizeof(T) == 2) {
+                row[0 * RW] = (a.x & 0xFFFFu) | (b.x << 16);
+                row[1 * RW] = (a.x >> 16) | (b.x & 0xFFFF0000u);
+                row[2 * RW] = (a.y & 0xFFFFu) | (b.y << 16);
+                row[3 * RW] = (a.y >> 16) | (b.y & 0xFFFF0000u);
+            } else {
+                *reinterpret_cast<uint2 *>(row) = uint2{a.x, b.x};
+                *reinterpret_cast<uint2 *>(row + RW) = uint2{a.y, b.y};
+            }
+        }
+    }
+};
+
 // Per-token fp32 pair (a[t], b[t]) of a 32-token tile (the GN backward's
 // den and dden, or rden and gden), loaded by wave 0 with the token tiles and
 // committed to LDS as [2][TT] with them; zero past the sequence end and for
@@ -429,16 +494,31 @@ __device__ void load_planes(const float *__restrict__ planes, int LK, T *pl, T *
 // One 16x16 tile (rows c = 16mc.., columns t = 16nt..) of planes . X^T, then
 // th = tanh and the sigmoid pair of 2*th*inv_temp, stored as sp/sm/sth
 // [TT][ld_of<float>(NCOL)] (lane writes its 4 consecutive c of token t).
+// The planes operands of one 16-column block (rows 16 mc.. of pl / pllo),
+// held in registers by a wave whose projection task keeps that block on
+// every tile.
+template <typename T> struct PlaneOps {
+    Frag<T> hi[D / 32], lo[D / 32];
+    template <class NL> __device__ __forceinline__ void load(const T *pl, const T *pllo, int mc) {
+#pragma unroll
+        for (int kp = 0; kp < D / 32; ++kp) {
+            hi[kp] = NL::frag(pl, 16 * mc + li(), kp);
+            if constexpr (is_bf16<T>()) lo[kp] = NL::frag(pllo, 16 * mc + li(), kp);
+        }
+    }
+};
+
+// pc: the block's operands in registers (mc is then that block), or null
 template <typename T, class NL = NatL<T, false>>
 __device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mc, int nt, float inv_temp, float *sp,
-                             float *sm, float *sth) {
+                             float *sm, float *sth, const PlaneOps<T> *pc = nullptr) {
     constexpr int LDC = ld_of<float>(NCOL);
     f32x4 acc = zero4();
 #pragma unroll
     for (int kp = 0; kp < D / 32; ++kp) {
         const Frag<T> x = NL::frag(sx, 16 * nt + li(), kp);
-        mma(acc, NL::frag(pl, 16 * mc + li(), kp), x);
-        if constexpr (is_bf16<T>()) mma(acc, NL::frag(pllo, 16 * mc + li(), kp), x);
+        mma(acc, pc ? pc->hi[kp] : NL::frag(pl, 16 * mc + li(), kp), x);
+        if constexpr (is_bf16<T>()) mma(acc, pc ? pc->lo[kp] : NL::frag(pllo, 16 * mc + li(), kp), x);
     }
     const int t = 16 * nt + li(), c0 = 16 * mc + 4 * lg();
     // the corner pair (sigmoid(2u), sigmoid(-2u)), u = th inv_temp, from
@@ -772,15 +852,18 @@ __device__ __forceinline__ Frag<T> token_operand(const f32x4 (&X)[2], const Cons
 
 // c += A . X^T over the wave's 16 buckets, X a bucket-row tile taken as the B
 // operand (column t, k = s); bf16 runs A . hi + A . lo as one 32-deep product
-// (A duplicated in OpX, X split into its two bf16 parts), fp32 accuracy.
+// (A duplicated in OpX, X split into its two bf16 parts, hi + lo within
+// 2^-16 of x), fp32 accuracy.
 template <typename T> __device__ __forceinline__ void mma16_x(f32x4 &c, const OpX<T> &A, const f32x4 &x) {
     if constexpr (is_bf16<T>()) {
+        // hi: x truncated to its upper 16 bits (exact as bf16, no rounding
+        // step); lo: the exact remainder x - hi, rounded to bf16
         Frag<bf16> hl;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const bf16 h = (bf16)x[j];
-            hl.v[j] = h;
-            hl.v[j + 4] = (bf16)(x[j] - (float)h);
+            const uint32_t u = __float_as_uint(x[j]) & 0xFFFF0000u;
+            hl.v[j] = __builtin_bit_cast(bf16, (unsigned short)(u >> 16));
+            hl.v[j + 4] = (bf16)(x[j] - __uint_as_float(u));
         }
         mma(c, A.f, hl);
     } else {
@@ -1223,6 +1306,10 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
     __syncthreads();  // the constant tables in LDS; their operands to registers
     cst.cache();
+    // whole-tile instantiations: each wave has at most one projection task,
+    // the same column block on every tile, whose planes stay in registers
+    PlaneOps<T> pcw;
+    if constexpr (AL) pcw.template load<NL>(sPl, sPlLo, pbk.mc(pbk.task(w)));
     // segment sums: A in fp64; B in fp64 for fp32 inputs, and for bf16 in
     // fp32 MFMA accumulators (bf16 uses B only through bf16 operands).  Tile
     // sums are added tile by tile in token order.
@@ -1271,7 +1358,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
             const int u = pbk.tensor(q), r = pbk.task(q);
             float *sp = sSig + u * 2 * TT * LDC;
             project_tile<T, NL>(sK + u * TT * LDN, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sp, sp + TT * LDC,
-                                nullptr);
+                                nullptr, (AL && q == w) ? &pcw : nullptr);
         }
         __syncthreads();  // sigmoid rows in LDS
 #pragma unroll
@@ -1527,6 +1614,10 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     load_planes<T, NTH, NL>(a.planes + m * a.planes_m_stride, a.L * a.K, sPl, is_bf16<T>() ? sPlLo : nullptr, nullptr);
     __syncthreads();  // the constant tables in LDS; their operands to registers
     cst.cache();
+    // whole-tile instantiations: each wave has at most one projection task,
+    // the same column block on every tile, whose planes stay in registers
+    PlaneOps<T> pcw;
+    if constexpr (AL) pcw.template load<NL>(sPl, sPlLo, pbk.mc(pbk.task(w)));
     // carried state: causal = prefix at the segment start, non-causal = totals.
     // B in bucket-row layout: lane holds B[s = sw + 4g + e][d = 16md + i]
     const double *st = a.fstate + ((int64_t)n * (a.fnseg + 1) + (CAUSAL ? seg * a.fmul : a.fnseg)) * a.Spad * SROW;
@@ -1577,9 +1668,11 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             for (int q = w; q < 2 * pbk.tasks(); q += NW_) {
                 const int r = pbk.task(q);
                 if (q < pbk.tasks())
-                    project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+                    project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
+                                        (AL && q == w) ? &pcw : nullptr);
                 else
-                    project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr);
+                    project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
+                                        (AL && q == w) ? &pcw : nullptr);
             }
             __syncthreads();
             f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
@@ -1664,9 +1757,11 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         for (int q = w; q < (CAUSAL ? 2 : 1) * pbk.tasks(); q += NW_) {
             const int r = pbk.task(q);
             if (q < pbk.tasks())
-                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
+                                    (AL && q == w) ? &pcw : nullptr);
             else
-                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr);
+                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
+                                    (AL && q == w) ? &pcw : nullptr);
         }
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
@@ -1874,6 +1969,10 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     cst.cache();
     if constexpr (KB <= 4) ho.cache();
     po.cache();
+    // whole-tile instantiations: each wave has at most one projection task,
+    // the same column block on every tile, whose planes stay in registers
+    PlaneOps<T> pcw;
+    if constexpr (AL) pcw.template load<NL>(sPl, sPlLo, pbk.mc(pbk.task(w)));
     // forward state in d-row layout: lane holds B^T[d = 16md + 4g + e][s = sw + i]
     const double *st = a.fstate + ((int64_t)n * (a.fnseg + 1) + (CAUSAL ? seg * a.fmul : a.fnseg)) * a.Spad * SROW;
     f32x4 Bt[4], Ut[4];
@@ -1892,7 +1991,8 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     wait_state_loads();
     constexpr int NP = CAUSAL ? 2 : 1;  // transposed tiles: dO (and V)
     Prefetch<T, NTH, AL> pq_, pk_, po_;  // po_: GN's O tile
-    PrefetchT<T, NTH, NP, AL> pg_, pv_;
+    PrefetchT<T, NTH, NP, AL> pg_;  // non-causal dO
+    PrefetchT2<T, NTH, AL> pgv_;     // causal dO (first half of the waves) and V
     TokPre pt_;
     // Writes the prefetched rows to token block b.
     auto commit = [&](int b) {
@@ -1900,10 +2000,11 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         float *tin = (float *)(tb + Ly::oTokIn);
         wait_vmem();
         pq_.template commit<NL>((T *)(tb + Ly::oQ), nullptr);
-        pg_.template commit<NL>(0, (T *)(tb + Ly::oG), (T *)(tb + Ly::oGt));
         if constexpr (CAUSAL) {
             pk_.template commit<NL>((T *)(tb + Ly::oK), nullptr);
-            pv_.template commit<NL>(1, (T *)(tb + Ly::oV), (T *)(tb + Ly::oVt));
+            pgv_.template commit<NL>((T *)(tb + Ly::oG), (T *)(tb + Ly::oGt), (T *)(tb + Ly::oV), (T *)(tb + Ly::oVt));
+        } else {
+            pg_.template commit<NL>(0, (T *)(tb + Ly::oG), (T *)(tb + Ly::oGt));
         }
         if constexpr (GN) {
             po_.template commit<NL>((T *)(tb + Ly::oO), nullptr);
@@ -1915,10 +2016,11 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     constexpr int NB = Ly::NB;
     if (j0 < j1) {
         pq_.issue(qp, a.sq.t, (int64_t)j0 * TT, a.T);
-        pg_.issue(0, gp, a.sdo.t, (int64_t)j0 * TT, a.T);
         if constexpr (CAUSAL) {
             pk_.issue(kp, a.sk.t, (int64_t)j0 * TT, a.T);
-            pv_.issue(1, vp, a.sv.t, (int64_t)j0 * TT, a.T);
+            pgv_.issue(gp, a.sdo.t, vp, a.sv.t, (int64_t)j0 * TT, a.T);
+        } else {
+            pg_.issue(0, gp, a.sdo.t, (int64_t)j0 * TT, a.T);
         }
         if constexpr (GN) {
             po_.issue(op, a.so.t, (int64_t)j0 * TT, a.T);
@@ -1938,10 +2040,11 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         const int64_t tn = (int64_t)(jt + 1 < j1 ? jt + 1 : jt) * TT;
         auto issue = [&]() {
             pq_.issue(qp, a.sq.t, tn, a.T);
-            pg_.issue(0, gp, a.sdo.t, tn, a.T);
             if constexpr (CAUSAL) {
                 pk_.issue(kp, a.sk.t, tn, a.T);
-                pv_.issue(1, vp, a.sv.t, tn, a.T);
+                pgv_.issue(gp, a.sdo.t, vp, a.sv.t, tn, a.T);
+            } else {
+                pg_.issue(0, gp, a.sdo.t, tn, a.T);
             }
             if constexpr (GN) {
                 po_.issue(op, a.so.t, tn, a.T);
@@ -1963,9 +2066,11 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         for (int q = w; q < (CAUSAL ? 2 : 1) * pbk.tasks(); q += NW_) {
             const int r = pbk.task(q);
             if (q < pbk.tasks())
-                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, sThQ);
+                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, sThQ,
+                                    (AL && q == w) ? &pcw : nullptr);
             else
-                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr);
+                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
+                                    (AL && q == w) ? &pcw : nullptr);
         }
         // one token block: dQ of the previous tile, from the dproj rows its
         // softmax backward left in LDS, after the projections (they overlap);
@@ -2313,6 +2418,10 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     cst.cache();
     if constexpr (KB <= 4) ho.cache();
     po.cache();
+    // whole-tile instantiations: each wave has at most one projection task,
+    // the same column block on every tile, whose planes stay in registers
+    PlaneOps<T> pcw;
+    if constexpr (AL) pcw.template load<NL>(sPl, sPlLo, pbk.mc(pbk.task(w)));
     // reverse carries (U, alpha) after the segment; forward state at the segment end
     const float *rs = a.rstate + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     const double *fs =
@@ -2346,7 +2455,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
 
     wait_state_loads();
     Prefetch<T, NTH, AL> pq_, pk_, pvn_;  // pvn_: non-causal V (natural only)
-    PrefetchT<T, NTH, 2, AL> pg_, pv_;   // causal dO and V (natural and transposed)
+    PrefetchT2<T, NTH, AL> pgv_;         // causal dO (first half of the waves) and V, natural and transposed
     TokPre pt_;
     // Writes the prefetched rows to token block b.
     auto commit = [&](int b) {
@@ -2355,9 +2464,8 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         wait_vmem();
         pk_.template commit<NL>((T *)(tb + Ly::oK), nullptr);
         if constexpr (CAUSAL) {
-            pv_.template commit<NL>(1, (T *)(tb + Ly::oV), (T *)(tb + Ly::oVt));
             pq_.template commit<NL>((T *)(tb + Ly::oQ), nullptr);
-            pg_.template commit<NL>(0, (T *)(tb + Ly::oG), (T *)(tb + Ly::oGt));
+            pgv_.template commit<NL>((T *)(tb + Ly::oG), (T *)(tb + Ly::oGt), (T *)(tb + Ly::oV), (T *)(tb + Ly::oVt));
         } else {
             pvn_.template commit<NL>((T *)(tb + Ly::oV), nullptr);
             if (kwp) pt_.commit(tok);
@@ -2376,9 +2484,8 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         const int64_t tl = (int64_t)(j1 - 1) * TT;
         pk_.issue(kp, a.sk.t, tl, a.T);
         if constexpr (CAUSAL) {
-            pv_.issue(1, vp, a.sv.t, tl, a.T);
             pq_.issue(qp, a.sq.t, tl, a.T);
-            pg_.issue(0, gp, a.sdo.t, tl, a.T);
+            pgv_.issue(gp, a.sdo.t, vp, a.sv.t, tl, a.T);
         } else {
             pvn_.issue(vp, a.sv.t, tl, a.T);
             if (kwp) pt_.issue(kwp, nullptr, tl, a.T);
@@ -2400,9 +2507,8 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         // the barrier's time to drain from the memory pipeline
         pk_.issue(kp, a.sk.t, tn, a.T);
         if constexpr (CAUSAL) {
-            pv_.issue(1, vp, a.sv.t, tn, a.T);
             pq_.issue(qp, a.sq.t, tn, a.T);
-            pg_.issue(0, gp, a.sdo.t, tn, a.T);
+            pgv_.issue(gp, a.sdo.t, vp, a.sv.t, tn, a.T);
         } else {
             pvn_.issue(vp, a.sv.t, tn, a.T);
             if (kwp) pt_.issue(kwp, nullptr, tn, a.T);
@@ -2415,9 +2521,11 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         for (int q = w; q < (CAUSAL ? 2 * pbk.tasks() + (MT2 ? 0 : 3) : pbk.tasks()); q += NW_) {
             const int r = pbk.task(q);
             if (q < pbk.tasks())
-                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, sThK);
+                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, sThK,
+                                    (AL && q == w) ? &pcw : nullptr);
             else if (q < 2 * pbk.tasks())
-                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr);
+                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
+                                    (AL && q == w) ? &pcw : nullptr);
             else
                 m_tile_xy<T, NL>(q - 2 * pbk.tasks(), sV, sG, sX, sY);
         }
