@@ -340,7 +340,9 @@ template <typename T, int NTH, bool AL = false> struct Prefetch {
 // written as packed token pairs to consecutive LDS words (few bank conflicts)
 // while each token row is still read in 32-byte runs.  NPART tensors share
 // the workgroup: this one uses threads [part*NTH/NPART, (part+1)*NTH/NPART).
-template <typename T, int NTH, int NPART, bool AL = false> struct PrefetchT {
+// TRN = false: natural rows only (bf16 reads the token operands from them
+// with LDS transpose loads, col_operand).
+template <typename T, int NTH, int NPART, bool AL = false, bool TRN = true> struct PrefetchT {
     static constexpr int NT = NTH / NPART;
     static constexpr int EPC = 8 / sizeof(T), CPR = D / EPC, TASKS = (TT / 2) * CPR;
     static constexpr int PER = (TASKS + NT - 1) / NT;
@@ -375,6 +377,7 @@ template <typename T, int NTH, int NPART, bool AL = false> struct PrefetchT {
                 *reinterpret_cast<uint2 *>(nat + NL::off(2 * tp, c * EPC)) = v[j][0];
                 *reinterpret_cast<uint2 *>(nat + NL::off(2 * tp + 1, c * EPC)) = v[j][1];
             }
+            if constexpr (!TRN) continue;
             // element q of a chunk: bf16 -> 16-bit half q of the 64-bit chunk; fp32 -> word q
             const uint2 a = v[j][0], b = v[j][1];
             uint32_t *row = reinterpret_cast<uint32_t *>(trn + (c * EPC) * LDT + 2 * tp);
@@ -396,7 +399,9 @@ template <typename T, int NTH, int NPART, bool AL = false> struct PrefetchT {
 // first by the workgroup's first half of waves and the second by the other
 // half.  The tensor is chosen per wave (scalar selects of the source and
 // destinations), so every lane takes part and no lane mask is needed.
-template <typename T, int NTH, bool AL = false> struct PrefetchT2 {
+// TRN: also write the transposed rows (fp32; bf16 reads its token operands
+// from the natural rows with LDS transpose loads, col_operand).
+template <typename T, int NTH, bool AL = false, bool TRN = true> struct PrefetchT2 {
     static constexpr int NT = NTH / 2;
     static constexpr int EPC = 8 / sizeof(T), CPR = D / EPC, TASKS = (TT / 2) * CPR;
     static_assert(NT % 64 == 0 && TASKS % NT == 0, "whole waves per tensor, whole tasks per lane");
@@ -441,6 +446,7 @@ template <typename T, int NTH, bool AL = false> struct PrefetchT2 {
             task_of(j, tp, c);
             *reinterpret_cast<uint2 *>(nat + NL::off(2 * tp, c * EPC)) = v[j][0];
             *reinterpret_cast<uint2 *>(nat + NL::off(2 * tp + 1, c * EPC)) = v[j][1];
+            if constexpr (!TRN) continue;
             const uint2 a = v[j][0], b = v[j][1];
             uint32_t *row = reinterpret_cast<uint32_t *>(trn + (c * EPC) * LDT + 2 * tp);
             constexpr int RW = LDT * (int)sizeof(T) / 4;
@@ -1073,6 +1079,35 @@ template <int N> __device__ __forceinline__ Frag<bf16> ts_operand_tr(const bf16 
     }
     return f;
 }
+// The pi-order token operand of column d = 16 md + i of a staged token tile
+// (k = token t: 4g + j, then 16 + 4g + j), the operand ld_frag_pi reads from a
+// transposed [D][TT] tile's row d.  bf16 reads it from the natural rows with
+// two LDS transpose loads: lane (g, p) reads columns 16 md + 4(p & 3) .. +3 of
+// row 4g + (p >> 2) (and row 16 + ...), runs of 4 columns that the natural
+// layout keeps contiguous; fp32 reads the transposed rows trn.
+template <typename T, class NL, bool NAT = is_bf16<T>()>
+__device__ __forceinline__ Frag<T> col_operand(const T *nat, const T *trn, int md) {
+    if constexpr (NAT) {
+        static_assert(is_bf16<T>(), "transpose loads of 16-bit elements");
+        typedef short v4s __attribute__((ext_vector_type(4)));
+        typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        const int g = lg(), p = li(), d0 = 16 * md + 4 * (p & 3);
+        const bf16 *a = nat + NL::off(4 * g + (p >> 2), d0);
+        const bf16 *b = nat + NL::off(16 + 4 * g + (p >> 2), d0);
+        const v4s ra = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)a);
+        const v4s rb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)b);
+        const bf16x4 x = __builtin_bit_cast(bf16x4, ra), y = __builtin_bit_cast(bf16x4, rb);
+        Frag<bf16> f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f.v[j] = x[j];
+            f.v[j + 4] = y[j];
+        }
+        return f;
+    } else {
+        return ld_frag_pi(trn + (16 * md + li()) * ldp_of<T>(TT));
+    }
+}
 // token operand of a bucket-row tile pair X that the wave also stores to its
 // [t][s] rows: bf16 stores first and reads the operand back transposed
 template <typename T, int N>
@@ -1251,8 +1286,11 @@ template <typename T, int SP> struct FwdReduceL {
     static constexpr int GT = 2;  // tiles per barrier group
     static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL);
     static constexpr size_t oK = 0;                                          // [GT][TT][LDN]
-    static constexpr size_t oVt = align16(oK + sizeof(T) * GT * TT * LDN);   // [2][GT][D][LDT]
-    static constexpr size_t oPl = align16(oVt + sizeof(T) * 2 * GT * D * LDT);
+    // V tiles [2][GT]: bf16 natural rows (token operands by transpose loads,
+    // col_operand), fp32 transposed [D][LDT]
+    static constexpr int VTE = is_bf16<T>() ? TT * LDN : D * LDT;  // elements per tile
+    static constexpr size_t oVt = align16(oK + sizeof(T) * GT * TT * LDN);
+    static constexpr size_t oPl = align16(oVt + sizeof(T) * 2 * GT * VTE);
     static constexpr size_t oPlLo = align16(oPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t oSig = align16(oPlLo + sizeof(T) * NCOL * LDN);  // [GT][sp, sm][TT][LDC]
     static constexpr size_t oCst = align16(oSig + sizeof(float) * GT * 2 * TT * LDC);
@@ -1324,7 +1362,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
 
     wait_state_loads();
     Prefetch<T, NTH, AL> pk_[GT];
-    PrefetchT<T, NTH, 1, AL> pv_[GT];
+    PrefetchT<T, NTH, 1, AL, !is_bf16<T>()> pv_[GT];
     TokPre pt_[GT];
     auto issue = [&](int jg) {
 #pragma unroll
@@ -1343,13 +1381,13 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
         // commit the group's rows (V^T and key weights to buffer b: the
         // group before last read the other one, and its readers passed the
         // last barrier), then start the next group's loads
-        T *sVt = sVt0 + b * GT * D * LDT;
+        T *sVt = sVt0 + b * GT * Ly::VTE;
         float *sTok = sTok0 + b * GT * 2 * TT;
         wait_vmem();
 #pragma unroll
         for (int u = 0; u < GT; ++u) {
             pk_[u].template commit<NL>(sK + u * TT * LDN, nullptr);
-            pv_[u].template commit<NL>(0, nullptr, sVt + u * D * LDT);
+            pv_[u].template commit<NL>(0, is_bf16<T>() ? sVt + u * Ly::VTE : nullptr, is_bf16<T>() ? nullptr : sVt + u * Ly::VTE);
             if (kwp) pt_[u].commit(sTok + u * 2 * TT);
         }
         if (jg + GT < j1) issue(jg + GT);
@@ -1366,7 +1404,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
             const int jt = jg + u;
             if (jt >= j1) break;
             const float *sp = sSig + u * 2 * TT * LDC;
-            const T *vt = sVt + u * D * LDT;
+            const T *vt = sVt + u * Ly::VTE;
             f32x4 PK[2];
             probs_st<KB, AL>(sp, sp + TT * LDC, sg, a.S, tile_rows((int64_t)jt * TT, a.T), PK);
             if (kwp)  // P_K' = w_t P_K
@@ -1378,7 +1416,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
             if constexpr (BM) {
                 f32x4 tot = zero4();
                 mma(tot, Pf, cst.ones());
-                for (int md = 0; md < 4; ++md) mma(accBm[md], ld_frag_pi(vt + (16 * md + i) * LDT), Pf);
+                for (int md = 0; md < 4; ++md) mma(accBm[md], col_operand<T, NL>(vt, vt, md), Pf);
                 for (int e = 0; e < 4; ++e) accA[e] += (double)tot[e];
             } else {
                 f32x4 tot, dB[4];
@@ -1444,8 +1482,13 @@ template <typename T, int SP, bool CAUSAL, bool GN> struct FwdOutL {
     static constexpr bool ALIAS = sw_ld<T, SP>() >= NatL<T, true>::LD;
     using NL = NatL<T, ALIAS>;
     static constexpr int LDN = NL::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDS_ = sw_ld<T, SP>();
+    // the V tile: natural rows, its token operands read with transpose loads
+    // (bf16 F1), or transposed (fp32, and the global normalisation, whose
+    // registers are at the 4-waves-per-SIMD limit)
+    static constexpr bool VNAT = is_bf16<T>() && !GN;
+    static constexpr size_t VTB = VNAT ? sizeof(T) * TT * LDN : sizeof(T) * D * LDT;
     static constexpr size_t oVt = 0;
-    static constexpr size_t oSig = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));  // Q sp, Q sm, K sp, K sm
+    static constexpr size_t oSig = align16(oVt + (CAUSAL ? VTB : 0));  // Q sp, Q sm, K sp, K sm
     static constexpr size_t oPts = align16(oSig + sizeof(float) * (CAUSAL ? 4 : 2) * TT * LDC);
     static constexpr size_t oWts = align16(oPts + (CAUSAL ? sizeof(T) * TT * LDS_ : 0));
     static constexpr size_t oBT = align16(oWts + sizeof(T) * TT * LDS_);
@@ -1463,7 +1506,7 @@ template <typename T, int SP, bool CAUSAL, bool GN> struct FwdOutL {
     // causal, when it costs no workgroup per CU (160 KiB of LDS): a second
     // transposed V tile and the tile's Sc^T [t][t'] blocks, computed once
     static constexpr size_t oVt2 = bytes1;
-    static constexpr size_t oSc = align16(oVt2 + sizeof(T) * D * LDT);
+    static constexpr size_t oSc = align16(oVt2 + VTB);
     static constexpr size_t bytes2 = align16(oSc + sizeof(T) * TT * LDT);
     static constexpr size_t LDS_CU = 160 * 1024;
     static constexpr bool SCN = CAUSAL && LDS_CU / bytes2 >= LDS_CU / bytes1;
@@ -1474,7 +1517,8 @@ template <typename T, int SP, bool CAUSAL, bool GN> struct FwdOutL {
 // the waves' shares (sDen [NW_][TT]) and the md == 0 tiles write it (sliced
 // instantiations: this slice's den share, a partial).  GN also divides the
 // tile's numerator by max(den, eps) (sliced: the numerator is the partial).
-template <typename T, int SP, bool CAUSAL, bool GN = false, bool AL = false>
+template <typename T, int SP, bool CAUSAL, bool GN = false, bool AL = false, class NL = NatL<T, true>,
+          bool VNAT = is_bf16<T>()>
 __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T *Wts, const T *sVt, T *op,
                              int64_t st, int64_t t0, int64_t Tn, float *part, const float *sDen = nullptr,
                              float *den = nullptr, float eps = 0.f) {
@@ -1498,7 +1542,7 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
                     if (16 * mt + 4 * g + e > 16 * nt + i) Sc[mt][e] = 0.f;  // keep t' <= t
             }
         }
-        mma(O, ld_frag_pi(sVt + (16 * md + i) * LDT), frag_acc<T>(Sc[0], Sc[1]));
+        mma(O, col_operand<T, NL, VNAT>(sVt, sVt, md), frag_acc<T>(Sc[0], Sc[1]));
     }
     const int t = 16 * nt + i;
     if (GN || !CAUSAL ? sDen != nullptr : false) {
@@ -1547,12 +1591,12 @@ template <typename T, int SP> __device__ f32x4 fwd_out_partial(int md, int nt, c
     for (int kp = 0; kp < SP / 32; ++kp) mma(O, ld_frag(pb + 32 * kp), ld_frag(pw + 32 * kp));
     return O;
 }
-template <typename T, int SP, bool GN, bool AL = false>
+template <typename T, int SP, bool GN, bool AL = false, class NL = NatL<T, true>, bool VNAT = is_bf16<T>()>
 __device__ void fwd_out_final(int md, int nt, f32x4 O, const T *sVt, const T *sc, T *op, int64_t st, int64_t t0,
                               int64_t Tn, float *part, const float *sDen, float *den, float eps) {
     constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
-    mma(O, ld_frag_pi(sVt + (16 * md + i) * LDT), ld_frag_pi(sc + (16 * nt + i) * LDT));
+    mma(O, col_operand<T, NL, VNAT>(sVt, sVt, md), ld_frag_pi(sc + (16 * nt + i) * LDT));
     const int t = 16 * nt + i;
     if (GN && sDen != nullptr) {
         constexpr int NW_ = SP / WB;
@@ -1582,6 +1626,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
     using Ly = FwdOutL<T, SP, CAUSAL, GN>;
     using NL = typename Ly::NL;
+    constexpr bool VNAT = Ly::VNAT;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC, LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
@@ -1631,7 +1676,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 
     wait_state_loads();
     Prefetch<T, NTH, AL> pq_, pk_;
-    PrefetchT<T, NTH, 1, AL> pv_;
+    PrefetchT<T, NTH, 1, AL, !VNAT> pv_;  // V: natural rows (VNAT) or transposed
     if (j0 < j1) {
         pq_.issue(qp, a.sq.t, (int64_t)j0 * TT, a.T);
         if constexpr (CAUSAL) {
@@ -1651,7 +1696,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             wait_vmem();
             pq_.template commit<NL>(sQ, nullptr);
             pk_.template commit<NL>(sK, nullptr);
-            pv_.template commit<NL>(0, nullptr, vt_of(j));
+            pv_.template commit<NL>(0, VNAT ? vt_of(j) : nullptr, VNAT ? nullptr : vt_of(j));
         };
         if (j0 < j1) commit(j0);
         constexpr int NQ = (8 + NW_ - 1) / NW_;  // output tiles per wave
@@ -1724,7 +1769,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             for (int k = 0; k < NQ; ++k)
                 if (w + k * NW_ < 8) Op[k] = fwd_out_partial<T, SP>((w + k * NW_) >> 1, (w + k * NW_) & 1, sBT, sWts);
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
-            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, ld_frag_pi(sVt + (16 * md + i) * LDT));
+            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, col_operand<T, NL, VNAT>(sVt, sVt, md));
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
             __syncthreads();  // Sc rows in LDS; the P_K / W / B rows are read
             commit(jt + 1);
@@ -1732,7 +1777,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             for (int k = 0; k < NQ; ++k) {
                 const int q = w + k * NW_;
                 if (q < 8)
-                    fwd_out_final<T, SP, GN, AL>(q >> 1, q & 1, Op[k], sVt, sSc, op, a.so.t, t0, a.T, opart, sDen, denp,
+                    fwd_out_final<T, SP, GN, AL, NL, VNAT>(q >> 1, q & 1, Op[k], sVt, sSc, op, a.so.t, t0, a.T, opart, sDen, denp,
                                              a.eps);
             }
         }
@@ -1744,7 +1789,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         pq_.template commit<NL>(sQ, nullptr);
         if constexpr (CAUSAL) {
             pk_.template commit<NL>(sK, nullptr);
-            pv_.template commit<NL>(0, nullptr, sVt);
+            pv_.template commit<NL>(0, VNAT ? sVt : nullptr, VNAT ? nullptr : sVt);
         }
         if (jt + 1 < j1) {
             pq_.issue(qp, a.sq.t, t0 + TT, a.T);
@@ -1813,11 +1858,11 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         }
         __syncthreads();
         for (int q = w; q < 8; q += NW_)
-            fwd_out_tile<T, SP, CAUSAL, GN, AL>(q >> 1, q & 1, sBT, sPts, sWts, sVt, op, a.so.t, t0, a.T, opart, sDen,
+            fwd_out_tile<T, SP, CAUSAL, GN, AL, NL, VNAT>(q >> 1, q & 1, sBT, sPts, sWts, sVt, op, a.so.t, t0, a.T, opart, sDen,
                                             denp, a.eps);
         if constexpr (CAUSAL) {
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
-            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, ld_frag_pi(sVt + (16 * md + i) * LDT));
+            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, col_operand<T, NL, VNAT>(sVt, sVt, md));
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
         }
     }
@@ -1992,7 +2037,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     constexpr int NP = CAUSAL ? 2 : 1;  // transposed tiles: dO (and V)
     Prefetch<T, NTH, AL> pq_, pk_, po_;  // po_: GN's O tile
     PrefetchT<T, NTH, NP, AL> pg_;  // non-causal dO
-    PrefetchT2<T, NTH, AL> pgv_;     // causal dO (first half of the waves) and V
+    PrefetchT2<T, NTH, AL, !is_bf16<T>()> pgv_;  // causal dO (first half of the waves) and V
     TokPre pt_;
     // Writes the prefetched rows to token block b.
     auto commit = [&](int b) {
@@ -2148,8 +2193,8 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         for (int e = 0; e < 4; ++e) al[e] += (double)(dA[0][e] + dA[1][e]);
         // U^T[d][s] += sum_t g[t][d] W[t][s]; carry B^T[d][s] += sum_t V[t][d] P_K[t][s]
         for (int md = 0; md < 4; ++md) {
-            mma(Ut[md], ld_frag_pi(sGt + (16 * md + i) * LDT), Wf);
-            if constexpr (CAUSAL) mma(Bt[md], ld_frag_pi(sVt + (16 * md + i) * LDT), Pf);
+            mma(Ut[md], col_operand<T, NL>(sG, sGt, md), Wf);
+            if constexpr (CAUSAL) mma(Bt[md], col_operand<T, NL>(sV, sVt, md), Pf);
         }
         if constexpr (CAUSAL)
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
@@ -2282,8 +2327,9 @@ template <typename T, int SP> __device__ void sc2_tile(int r, const T *Wts, cons
     store4<T>(sc2 + (16 * nt + i) * LDT + 16 * mt + 4 * g, acc);
 }
 
-template <typename T, int SP, bool CAUSAL, bool AL = false>
-__device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts, const T *sGt, T *dvp, int64_t st,
+template <typename T, int SP, bool CAUSAL, bool AL = false, class NL = NatL<T, true>>
+__device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts, const T *sG, const T *sGt, T *dvp,
+                        int64_t st,
                         int64_t t0, int64_t Tn, float *part) {
     constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
@@ -2305,7 +2351,7 @@ __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts
                     if (16 * mt + 4 * g + e < 16 * nt + i) Sc2[mt][e] = 0.f;  // keep t >= tau
             }
         }
-        mma(acc, ld_frag_pi(sGt + (16 * md + i) * LDT), frag_acc<T>(Sc2[0], Sc2[1]));
+        mma(acc, col_operand<T, NL>(sG, sGt, md), frag_acc<T>(Sc2[0], Sc2[1]));
     }
     const int t = 16 * nt + i;
     if ((AL || t < tile_rows(t0, Tn))) {
@@ -2327,12 +2373,13 @@ template <typename T, int SP> __device__ f32x4 dv_part(int md, int nt, const T *
     for (int kp = 0; kp < SP / 32; ++kp) mma(acc, ld_frag(pu + 32 * kp), ld_frag(pp + 32 * kp));
     return acc;
 }
-template <typename T, bool AL = false>
-__device__ void dv_finish(int md, int nt, f32x4 acc, const T *sGt, const T *sc2, T *dvp, int64_t st, int64_t t0,
+template <typename T, bool AL = false, class NL = NatL<T, true>>
+__device__ void dv_finish(int md, int nt, f32x4 acc, const T *sG, const T *sGt, const T *sc2, T *dvp, int64_t st,
+                          int64_t t0,
                           int64_t Tn, float *part) {
     constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
-    mma(acc, ld_frag_pi(sGt + (16 * md + i) * LDT), ld_frag_pi(sc2 + (16 * nt + i) * LDT));
+    mma(acc, col_operand<T, NL>(sG, sGt, md), ld_frag_pi(sc2 + (16 * nt + i) * LDT));
     const int t = 16 * nt + i;
     if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
@@ -2455,7 +2502,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
 
     wait_state_loads();
     Prefetch<T, NTH, AL> pq_, pk_, pvn_;  // pvn_: non-causal V (natural only)
-    PrefetchT2<T, NTH, AL> pgv_;         // causal dO (first half of the waves) and V, natural and transposed
+    PrefetchT2<T, NTH, AL, !is_bf16<T>()> pgv_;  // causal dO (first half of the waves) and V
     TokPre pt_;
     // Writes the prefetched rows to token block b.
     auto commit = [&](int b) {
@@ -2542,10 +2589,11 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         if constexpr (SCN)
             if (jr + 1 < j1) {
                 const T *gtn = (const T *)(smem + ((jr + 1) & 1) * Ly::TB + Ly::oGt);
+                const T *gnn = (const T *)(smem + ((jr + 1) & 1) * Ly::TB + Ly::oG);
 #pragma unroll
                 for (int k = 0; k < NQD; ++k)
                     if (w + k * NW_ < 8)
-                        dv_finish<T, AL>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gtn, sSc2, dvp, a.sg.t, t0 + TT,
+                        dv_finish<T, AL>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gnn, gtn, sSc2, dvp, a.sg.t, t0 + TT,
                                      a.T, vpart);
             }
         __syncthreads();
@@ -2590,7 +2638,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                     tot = zero4();
                     mma(tot, Pf, cst.ones());
                     const Frag<T> Pn = neg_frag(Pf);
-                    for (int md = 0; md < 4; ++md) mma(Bm[md], ld_frag_pi(sVt + (16 * md + i) * LDT), Pn);
+                    for (int md = 0; md < 4; ++md) mma(Bm[md], col_operand<T, NL>(sV, sVt, md), Pn);
                     for (int e = 0; e < 4; ++e) Ae[e] -= (double)tot[e];
                 } else {
                     tile_sums<T>(Pf, cst, sVt, tot, dB);
@@ -2655,7 +2703,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                 for (int e = 0; e < 4; ++e) al[e] += tdA[e];
             }
             // ---- U^T[d][s] += sum_t g[t][d] W[t][s]  (the dV tiles read the LDS copy of U)
-            for (int md = 0; md < 4; ++md) mma(Ut[md], ld_frag_pi(sGt + (16 * md + i) * LDT), Wf);
+            for (int md = 0; md < 4; ++md) mma(Ut[md], col_operand<T, NL>(sG, sGt, md), Wf);
             if constexpr (SCN) {
                 // the tile's three Sc2 blocks, once each, for its dV tiles in
                 // the next iteration
@@ -2666,14 +2714,14 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                     if (w + k * NW_ < 8) dvacc[k] = dv_part<T, SP>((w + k * NW_) >> 1, (w + k * NW_) & 1, sUT, sPts);
             } else {
                 for (int q = w; q < 8; q += NW_)
-                    dv_tile<T, SP, CAUSAL, AL>(q >> 1, q & 1, sUT, sPts, sWts, sGt, dvp, a.sg.t, t0, a.T, vpart);
+                    dv_tile<T, SP, CAUSAL, AL>(q >> 1, q & 1, sUT, sPts, sWts, sG, sGt, dvp, a.sg.t, t0, a.T, vpart);
             }
         } else {
             __syncthreads();  // all waves' P_K rows in LDS
             if constexpr (NB == 2) commit((int)((jr + 1) & 1));
             // non-causal: dV^T = U^T P_K^T; dP_K = alpha + v . U (totals)
             for (int q = w; q < 8; q += NW_)
-                dv_tile<T, SP, CAUSAL, AL>(q >> 1, q & 1, sUT, sPts, nullptr, nullptr, dvp, a.sg.t, t0, a.T, vpart);
+                dv_tile<T, SP, CAUSAL, AL>(q >> 1, q & 1, sUT, sPts, nullptr, nullptr, nullptr, dvp, a.sg.t, t0, a.T, vpart);
             const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
             for (int nt = 0; nt < 2; ++nt) {
                 f32x4 c = zero4();
@@ -2704,10 +2752,11 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         dx_store<T, NW_, XC, AL>(sDproj, sPlT, dkp, a.sg.t, (int64_t)j0 * TT, a.T, xpart, xc0);
         if constexpr (SCN) {
             const T *gtn = (const T *)(smem + (j0 & 1) * Ly::TB + Ly::oGt);
+            const T *gnn = (const T *)(smem + (j0 & 1) * Ly::TB + Ly::oG);
 #pragma unroll
             for (int k = 0; k < NQD; ++k)
                 if (w + k * NW_ < 8)
-                    dv_finish<T, AL>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gtn, sSc2, dvp, a.sg.t, (int64_t)j0 * TT, a.T,
+                    dv_finish<T, AL>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gnn, gtn, sSc2, dvp, a.sg.t, (int64_t)j0 * TT, a.T,
                                  vpart);
         }
     }
