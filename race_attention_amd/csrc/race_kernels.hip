@@ -298,6 +298,8 @@ template <typename T, int NTH, bool AL = false> struct Prefetch {
     typedef typename ChunkOf<CB>::type chunk_t;
     static constexpr int EPC = CB / sizeof(T), CPR = D / EPC, CHUNKS = TT * CPR;
     static constexpr int PER = (CHUNKS + NTH - 1) / NTH;
+    // whole tiles whose chunks every thread shares evenly
+    static constexpr bool WHOLE = AL && CHUNKS % NTH == 0;
     chunk_t v[PER];
     // tile base src + t0 * st is uniform; the lane offset t * st + c * EPC is
     // 32-bit (the host bounds 32 * token stride below 2^31)
@@ -307,6 +309,10 @@ template <typename T, int NTH, bool AL = false> struct Prefetch {
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int idx = threadIdx.x + j * NTH, t = idx / CPR, c = idx % CPR;
+            if constexpr (WHOLE) {  // every lane loads: no branch, counted waits stay exact
+                v[j] = ld_at<chunk_t>(base, tile_off(t, st, c * EPC, sizeof(T)));
+                continue;
+            }
             v[j] = chunk_t{};
             if (idx < CHUNKS && t < rem) v[j] = ld_at<chunk_t>(base, tile_off(t, st, c * EPC, sizeof(T)));
         }
@@ -316,7 +322,7 @@ template <typename T, int NTH, bool AL = false> struct Prefetch {
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int idx = threadIdx.x + j * NTH, t = idx / CPR, c = idx % CPR;
-            if (idx >= CHUNKS) continue;
+            if (!WHOLE && idx >= CHUNKS) continue;
             if (nat) {
                 if constexpr (NL::P && CB == 16) {  // two runs of 4 elements
                     *reinterpret_cast<uint2 *>(nat + NL::off(t, c * EPC)) = uint2{v[j].x, v[j].y};
@@ -1361,36 +1367,12 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     for (int md = 0; md < 4; ++md) accBm[md] = zero4();
 
     wait_state_loads();
-    Prefetch<T, NTH, AL> pk_[GT];
-    PrefetchT<T, NTH, 1, AL, !is_bf16<T>()> pv_[GT];
-    TokPre pt_[GT];
-    auto issue = [&](int jg) {
-#pragma unroll
-        for (int u = 0; u < GT; ++u) {
-            // AL loads whole tiles without row guards: a group's tile past
-            // the segment reloads the segment's last tile (unused)
-            const int64_t t0 = (int64_t)(AL ? min(jg + u, j1 - 1) : jg + u) * TT;
-            pk_[u].issue(kp, a.sk.t, t0, send);
-            pv_[u].issue(0, vp, a.sv.t, t0, send);
-            if (kwp) pt_[u].issue(kwp, nullptr, t0, send);
-        }
-    };
-    if (j0 < j1) issue(j0);
-    int b = 0;
-    for (int jg = j0; jg < j1; jg += GT, b ^= 1) {
-        // commit the group's rows (V^T and key weights to buffer b: the
-        // group before last read the other one, and its readers passed the
-        // last barrier), then start the next group's loads
-        T *sVt = sVt0 + b * GT * Ly::VTE;
-        float *sTok = sTok0 + b * GT * 2 * TT;
-        wait_vmem();
-#pragma unroll
-        for (int u = 0; u < GT; ++u) {
-            pk_[u].template commit<NL>(sK + u * TT * LDN, nullptr);
-            pv_[u].template commit<NL>(0, is_bf16<T>() ? sVt + u * Ly::VTE : nullptr, is_bf16<T>() ? nullptr : sVt + u * Ly::VTE);
-            if (kwp) pt_[u].commit(sTok + u * 2 * TT);
-        }
-        if (jg + GT < j1) issue(jg + GT);
+    // The group's work once its rows are in LDS (K tiles; V tiles and key
+    // weights in buffer b): projections, then each tile's probabilities and
+    // sums.
+    auto work = [&](int jg, int b) {
+        const T *sVt = sVt0 + b * GT * Ly::VTE;
+        const float *sTok = sTok0 + b * GT * 2 * TT;
         __syncthreads();  // the group's rows in LDS; the last group's sigmoid rows are read
         for (int q = w; q < pbk.tasks() * GT; q += NW_) {
             const int u = pbk.tensor(q), r = pbk.task(q);
@@ -1426,6 +1408,83 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
                     for (int md = 0; md < 4; ++md) accB[md][e] += (double)dB[md][e];
                 }
             }
+        }
+    };
+    constexpr bool TWO = AL && is_bf16<T>();
+    if (TWO && !kwp) {
+        // Whole tiles, bf16 (natural V rows), no key weights: two groups'
+        // loads in flight.  Register sets A and B alternate; a set is
+        // committed and at once reloaded with the group two ahead, so each
+        // group's loads have two groups of work to arrive.  Every lane issues
+        // the same loads each time (tiles past the segment reload its last
+        // one), so the compiler's counted waits at a commit cover only the
+        // older set.
+        using PF = Prefetch<T, NTH, true>;
+        PF ka[GT], va[GT], kb[GT], vb[GT];
+        auto issue2 = [&](PF (&pk)[GT], PF (&pv)[GT], int jg) {
+#pragma unroll
+            for (int u = 0; u < GT; ++u) {
+                const int64_t t0 = (int64_t)min(jg + u, j1 - 1) * TT;
+                pk[u].issue(kp, a.sk.t, t0, send);
+                pv[u].issue(vp, a.sv.t, t0, send);
+            }
+        };
+        // K tiles are read only by the projections, which every wave has
+        // finished at the previous group's second barrier; V buffer b was
+        // last read by the group before last.
+        auto commit2 = [&](const PF (&pk)[GT], const PF (&pv)[GT], int b) {
+            T *sVt = sVt0 + b * GT * Ly::VTE;
+#pragma unroll
+            for (int u = 0; u < GT; ++u) {
+                pk[u].template commit<NL>(sK + u * TT * LDN, nullptr);
+                pv[u].template commit<NL>(sVt + u * Ly::VTE, nullptr);
+            }
+        };
+        if (j0 < j1) {
+            issue2(ka, va, j0);
+            issue2(kb, vb, j0 + GT);
+        }
+        for (int jg = j0; jg < j1; jg += 2 * GT) {
+            commit2(ka, va, 0);
+            issue2(ka, va, jg + 2 * GT);
+            work(jg, 0);
+            commit2(kb, vb, 1);  // unconditional: the same pending sets at the loop head on every path
+            issue2(kb, vb, jg + 3 * GT);
+            if (jg + GT < j1) work(jg + GT, 1);
+        }
+    } else {
+        Prefetch<T, NTH, AL> pk_[GT];
+        PrefetchT<T, NTH, 1, AL, !is_bf16<T>()> pv_[GT];
+        TokPre pt_[GT];
+        auto issue = [&](int jg) {
+#pragma unroll
+            for (int u = 0; u < GT; ++u) {
+                // AL loads whole tiles without row guards: a group's tile past
+                // the segment reloads the segment's last tile (unused)
+                const int64_t t0 = (int64_t)(AL ? min(jg + u, j1 - 1) : jg + u) * TT;
+                pk_[u].issue(kp, a.sk.t, t0, send);
+                pv_[u].issue(0, vp, a.sv.t, t0, send);
+                if (kwp) pt_[u].issue(kwp, nullptr, t0, send);
+            }
+        };
+        if (j0 < j1) issue(j0);
+        int b = 0;
+        for (int jg = j0; jg < j1; jg += GT, b ^= 1) {
+            // commit the group's rows (V^T and key weights to buffer b: the
+            // group before last read the other one, and its readers passed the
+            // last barrier), then start the next group's loads
+            T *sVt = sVt0 + b * GT * Ly::VTE;
+            float *sTok = sTok0 + b * GT * 2 * TT;
+            wait_vmem();
+#pragma unroll
+            for (int u = 0; u < GT; ++u) {
+                pk_[u].template commit<NL>(sK + u * TT * LDN, nullptr);
+                pv_[u].template commit<NL>(0, is_bf16<T>() ? sVt + u * Ly::VTE : nullptr,
+                                           is_bf16<T>() ? nullptr : sVt + u * Ly::VTE);
+                if (kwp) pt_[u].commit(sTok + u * 2 * TT);
+            }
+            if (jg + GT < j1) issue(jg + GT);
+            work(jg, b);
         }
     }
     double *out = a.fdelta + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
@@ -1698,18 +1757,24 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             pk_.template commit<NL>(sK, nullptr);
             pv_.template commit<NL>(0, VNAT ? vt_of(j) : nullptr, VNAT ? nullptr : vt_of(j));
         };
-        if (j0 < j1) commit(j0);
-        constexpr int NQ = (8 + NW_ - 1) / NW_;  // output tiles per wave
-        for (int jt = j0; jt < j1; ++jt) {
-            const int64_t t0 = (int64_t)jt * TT;
-            // next tile's rows; the last tile reloads itself (loads stay in
-            // range, issue and commit unconditional)
-            const int64_t tn = (int64_t)(jt + 1 < j1 ? jt + 1 : jt) * TT;
-            sVt = vt_of(jt);
-            __syncthreads();  // this tile's rows in LDS; the previous tile's O rows are done
+        // The rows of tile j + 1 are loaded from the commit of tile j on
+        // (the registers are free then), a tile and a phase ahead of their
+        // own commit.  The last tile's commit writes rows nobody reads.
+        auto issue = [&](int j) {
+            const int64_t tn = (int64_t)min(j, j1 - 1) * TT;
             pq_.issue(qp, a.sq.t, tn, a.T);
             pk_.issue(kp, a.sk.t, tn, a.T);
             pv_.issue(0, vp, a.sv.t, tn, a.T);
+        };
+        if (j0 < j1) {
+            commit(j0);
+            issue(j0 + 1);
+        }
+        constexpr int NQ = (8 + NW_ - 1) / NW_;  // output tiles per wave
+        for (int jt = j0; jt < j1; ++jt) {
+            const int64_t t0 = (int64_t)jt * TT;
+            sVt = vt_of(jt);
+            __syncthreads();  // this tile's rows in LDS; the previous tile's O rows are done
             for (int q = w; q < 2 * pbk.tasks(); q += NW_) {
                 const int r = pbk.task(q);
                 if (q < pbk.tasks())
@@ -1773,6 +1838,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
             __syncthreads();  // Sc rows in LDS; the P_K / W / B rows are read
             commit(jt + 1);
+            if (jt + 2 < j1) issue(jt + 2);
 #pragma unroll
             for (int k = 0; k < NQ; ++k) {
                 const int q = w + k * NW_;
