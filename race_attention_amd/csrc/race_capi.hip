@@ -236,6 +236,15 @@ template <typename T>
 void dx_finish(const Plan &p, const race_desc *d, const void *part, const Args &a, const int64_t *st, void *out,
                hipStream_t s) {
     const int64_t waves = p.N * ((d->T + 16 * DXF_BLK - 1) / (16 * DXF_BLK));  // one wave per 64 tokens
+    if constexpr (std::is_same<T, bf16>::value) {
+        // 8-bit hashes, slices of 128 buckets: two slices per table, 8 columns each
+        if (d->K == 8 && p.SP == 128 && xcols_of(p.SP, d->K) == 8 && d->L <= 4 && p.nslice == 2 * d->L) {
+            k_dx_finish8<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(
+                (const bf16 *)part, d->L, a.planes, a.planes_m_stride, (int)d->B, (int)d->H, p.N, d->T,
+                Strides{st[0], st[1], st[2], st[3]}, (bf16 *)out);
+            return;
+        }
+    }
     k_dx_finish<T><<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(
         (const T *)part, p.nslice, xcols_of(p.SP, d->K), p.SP, d->K, d->L, a.planes, a.planes_m_stride, (int)d->B,
         (int)d->H, p.N, d->T, Strides{st[0], st[1], st[2], st[3]}, (T *)out);

@@ -3034,6 +3034,62 @@ __global__ __launch_bounds__(256) void k_dx_finish(const T *part, int nslice, in
     }
 }
 
+// dX for bf16 8-bit hashes in slices of 128 buckets: two slices per table
+// (slice z holds table z >> 1's 8 columns, one 16-byte row per token), at
+// most 4 tables.  Lane (g, i) takes token i and table g's columns, from slice
+// 2g in one product and slice 2g + 1 in a second, so a 16-wide d block costs
+// two products instead of one per slice (fp32 accumulation as above; the
+// tables' sums meet inside each product).
+__global__ __launch_bounds__(256) void k_dx_finish8(const bf16 *part, int L, const float *planes,
+                                                    int64_t planes_m_stride, int B, int H, int64_t N, int64_t Tn,
+                                                    Strides so, bf16 *out) {
+    const int64_t wv = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;  // over N * ceil(T / 64)
+    const int64_t nblk = (Tn + 16 * DXF_BLK - 1) / (16 * DXF_BLK);
+    if (wv >= N * nblk) return;  // whole waves
+    const int64_t n = wv / nblk, tw = (wv % nblk) * 16 * DXF_BLK;
+    const int g = lg(), i = li();
+    const bool live = g < L;  // table g exists
+    const float *pl = planes + (n / (B * H)) * planes_m_stride;
+    // planes^T operand of each 16-wide d block: column c = 8g + j, d = 16md + i
+    Frag<bf16> pt[4];
+#pragma unroll
+    for (int md = 0; md < 4; ++md) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = live ? pl[(int64_t)(8 * g + j) * D + 16 * md + i] : 0.f;
+        pt[md] = frag_seq<bf16>(v);
+    }
+    const int64_t zs = N * Tn * 8;  // elements per slice
+    for (int tb = 0; tb < DXF_BLK; ++tb) {
+        const int64_t t0 = tw + 16 * tb;
+        if (t0 >= Tn) break;
+        const int64_t t = t0 + i;
+        Frag<bf16> ae, ao;
+        ae.v = bf16x8{};
+        ao.v = bf16x8{};
+        if (live && t < Tn) {
+            const bf16 *row = part + 2 * g * zs + (n * Tn + t) * 8;
+            ae = *reinterpret_cast<const Frag<bf16> *>(row);
+            ao = *reinterpret_cast<const Frag<bf16> *>(row + zs);
+        }
+        f32x4 acc[4] = {zero4(), zero4(), zero4(), zero4()};
+#pragma unroll
+        for (int md = 0; md < 4; ++md) {
+            mma(acc[md], ae, pt[md]);
+            mma(acc[md], ao, pt[md]);
+        }
+        // lane (g, i) holds dX[t0 + 4g + e][16md + i]
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t tt = t0 + 4 * g + e;
+            if (tt < Tn)
+#pragma unroll
+                for (int md = 0; md < 4; ++md)
+                    out[stream_off(so, (int)n, B, H) + tt * so.t + 16 * md + i] = from_f32<bf16>(acc[md][e]);
+        }
+    }
+}
+
 // den [N][T] = sum of the per-slice partials [nslice][N][T], in slice order.
 __global__ void k_den_sum(const float *denpart, int nslice, int64_t NT, float *den) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
