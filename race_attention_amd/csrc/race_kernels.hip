@@ -2959,6 +2959,12 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
     }
 }
 
+// Partials are read once: nontemporal loads keep them from displacing other
+// lines in the caches (measured faster).
+__device__ __forceinline__ f32x4 part4(const float *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+}
+
 // Sum of the per-slice fp32 partials [nslice][N][T][D] in slice order,
 // written to the strided output (4 consecutive d per thread).
 template <typename T>
@@ -2969,8 +2975,8 @@ __global__ void k_slice_sum(const float *part, int nslice, int64_t N, int64_t Tn
     const int64_t n = idx / per, r = idx % per, t = r / (D / 4);
     const int d0 = 4 * (int)(r % (D / 4));
     const int64_t row = (n * Tn + t) * D + d0, zs = N * Tn * D;
-    f32x4 acc = *reinterpret_cast<const f32x4 *>(part + row);
-    for (int z = 1; z < nslice; ++z) acc += *reinterpret_cast<const f32x4 *>(part + z * zs + row);
+    f32x4 acc = part4(part + row);
+    for (int z = 1; z < nslice; ++z) acc += part4(part + z * zs + row);
     store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc);
 }
 
@@ -3111,10 +3117,10 @@ __global__ void k_slice_sum_gn(const float *part, const float *denpart, int nsli
     const int64_t n = idx / per, r = idx % per, t = r / (D / 4);
     const int d0 = 4 * (int)(r % (D / 4));
     const int64_t row = (n * Tn + t) * D + d0, zs = N * Tn * D, nt = n * Tn + t;
-    f32x4 acc = *reinterpret_cast<const f32x4 *>(part + row);
+    f32x4 acc = part4(part + row);
     float dn = denpart[nt];
     for (int z = 1; z < nslice; ++z) {
-        acc += *reinterpret_cast<const f32x4 *>(part + z * zs + row);
+        acc += part4(part + z * zs + row);
         dn += denpart[z * N * Tn + nt];
     }
     const float rc = 1.0f / fmaxf(dn, eps);
