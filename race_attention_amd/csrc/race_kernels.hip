@@ -520,8 +520,14 @@ template <typename T> struct PlaneOps {
     }
 };
 
-// pc: the block's operands in registers (mc is then that block), or null
-template <typename T, class NL = NatL<T, false>>
+// pc: the block's operands in registers (mc is then that block), or null.
+// PAIR: instead of the corner pair of each column, write the products of
+// corner pairs of the lane's 4 columns (a nibble: columns c0 .. c0+3, c0 = 4q;
+// 8- and 4-bit tables are whole nibbles), the index's high bit choosing the
+// first column's factor (1: sigmoid(2u)):
+//   sp[c0 + j] = f(c0, j >> 1) f(c0 + 1, j & 1),  sm[c0 + j] = f(c0 + 2, j >> 1) f(c0 + 3, j & 1),
+// so probs_st_ forms a bucket probability from two or four products.
+template <typename T, class NL = NatL<T, false>, bool PAIR = false>
 __device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mc, int nt, float inv_temp, float *sp,
                              float *sm, float *sth, const PlaneOps<T> *pc = nullptr) {
     constexpr int LDC = ld_of<float>(NCOL);
@@ -545,9 +551,39 @@ __device__ void project_tile(const T *sx, const T *pl, const T *pllo, int mc, in
         a[e] = x;
         b[e] = y;
     }
+    if constexpr (PAIR) {
+        f32x4 hp, lp;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            hp[j] = ((j & 2) ? a[0] : b[0]) * ((j & 1) ? a[1] : b[1]);
+            lp[j] = ((j & 2) ? a[2] : b[2]) * ((j & 1) ? a[3] : b[3]);
+        }
+        a = hp;
+        b = lp;
+    }
     *reinterpret_cast<f32x4 *>(sp + t * LDC + c0) = a;
     *reinterpret_cast<f32x4 *>(sm + t * LDC + c0) = b;
     if (sth) *reinterpret_cast<f32x4 *>(sth + t * LDC + c0) = th;
+}
+
+// Tables whose corner probabilities can be formed from nibble pair products
+// (project_tile's PAIR rows): 4 and 8 bits.
+template <int KB> constexpr bool pair_tables() { return KB == 4 || KB == 8; }
+
+// tanh(u) = sigmoid(2u) - sigmoid(-2u) of column c of token row t: from the
+// corner pair (sp - sm), or (PAIR) from the nibble's pair products, whose
+// halves sum to one column's factor times (sigmoid(2u') + sigmoid(-2u')) = 1
+// of the other column in the pair.
+template <bool PAIR>
+__device__ __forceinline__ float corner_tanh(const float *sp, const float *sm, int t, int c) {
+    constexpr int LDC = ld_of<float>(NCOL);
+    if constexpr (PAIR) {
+        const int m = c & 3;
+        const f32x4 h = *reinterpret_cast<const f32x4 *>((m < 2 ? sp : sm) + t * LDC + (c & ~3));
+        return (m & 1) ? (h[1] + h[3]) - (h[0] + h[2]) : (h[2] + h[3]) - (h[0] + h[1]);
+    } else {
+        return sp[t * LDC + c] - sm[t * LDC + c];
+    }
 }
 
 // Projection columns a workgroup needs: the K columns of every table its
@@ -584,12 +620,35 @@ struct PlaneBlocks {
 // lowest corner bits: P = hi * (bit1 ? s+ : s-) * (bit0 ? s+ : s-).
 // FULL: every token of the tile exists and every bucket of the wave is below
 // S (no validity masks; the whole-tile instantiations, AL).
-template <int KB, bool FULL>
+// PAIR: sp/sm hold project_tile's PAIR rows (4 or 8 bits).  The lane's 4
+// buckets r0 .. r0+3 (r0 = 4g in a 16-bucket run) differ in the last
+// nibble's two low bits: P = sp[n + (r >> 2 & 3)] sm[n + (r & 3)] over the
+// table's last nibble n, times (8 bits) the first nibble's two products,
+// which the wave's buckets share.
+template <int KB, bool FULL, bool PAIR = false>
 __device__ __forceinline__ void probs_st_(const float *sp, const float *sm, int sw, int S, int nv, f32x4 (&P)[2]) {
     constexpr int LDC = ld_of<float>(NCOL);
     constexpr int R = 1 << KB;
     const int g = lg(), i = li();
     const int s0 = sw + 4 * g;
+    static_assert(!PAIR || pair_tables<KB>(), "pair rows of 4- and 8-bit tables");
+    if constexpr (PAIR) {
+        const bool sv = FULL || s0 < S;
+        const int l = sv ? s0 >> KB : 0, r0 = s0 & (R - 1);
+        const int n1 = l * KB + KB - 4;  // the table's last nibble
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const int t = 16 * nt + i;
+            const bool v = sv && (FULL || t < nv);
+            float hi = sp[t * LDC + n1 + ((r0 >> 2) & 3)];
+            if constexpr (KB == 8) hi *= sp[t * LDC + l * KB + (r0 >> 6)] * sm[t * LDC + l * KB + ((r0 >> 4) & 3)];
+            if constexpr (!FULL) hi = v ? hi : 0.f;
+            const f32x4 lo = *reinterpret_cast<const f32x4 *>(sm + t * LDC + n1);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) P[nt][e] = hi * lo[e];
+        }
+        return;
+    }
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int t = 16 * nt + i;
@@ -630,9 +689,9 @@ __device__ __forceinline__ void probs_st_(const float *sp, const float *sm, int 
         }
     }
 }
-template <int KB, bool AL = false>
+template <int KB, bool AL = false, bool PAIR = false>
 __device__ __forceinline__ void probs_st(const float *sp, const float *sm, int sw, int S, int nv, f32x4 (&P)[2]) {
-    probs_st_<KB, AL>(sp, sm, sw, S, nv, P);
+    probs_st_<KB, AL, PAIR>(sp, sm, sw, S, nv, P);
 }
 
 // Operand of 8 consecutive k values (k = 8g .. 8g+7 of lane (g, i)), the
@@ -940,7 +999,7 @@ __device__ void softhash_share(const f32x4 (&P)[2], const f32x4 (&dP)[2], const 
 // the table's waves is split between two neighbouring lanes (half the waves
 // each, in order) and joined with a DPP swap, so every wave of the workgroup
 // takes part and the dependent chain of LDS reads is half as long.
-template <int KB, typename T, int SP, int NTH>
+template <int KB, typename T, int SP, int NTH, bool PAIR = false>
 __device__ float softhash_combine(const float *share, const float *sp, const float *sm, const float *sth, int z, int L,
                                   float inv_temp, T *dproj) {
     constexpr int LDC = ld_of<float>(NCOL), R = 1 << KB, NW_ = SP / WB;
@@ -967,7 +1026,7 @@ __device__ float softhash_combine(const float *share, const float *sp, const flo
         if (live && half == 0) {
             const int col = (l0 + tl) * KB + k;
             const float th = sth[t * LDC + col];
-            const float du = sx - sd * (sp[t * LDC + col] - sm[t * LDC + col]);
+            const float du = sx - sd * corner_tanh<PAIR>(sp, sm, t, col);
             tsum += du * th;
             dproj[sw_off<T, NCOL>(t, col)] = from_f32<T>(du * inv_temp * (1.f - th * th));
         }
@@ -1003,7 +1062,7 @@ __device__ __forceinline__ void totals_of(const f32x4 (&X)[2], f32x4 &tot) {
 //        = sum_table pd c_k - (sum_table pd) tanh(u_k),  pd = P dP,
 // since sum_table P c_k = sigmoid(2u_k) - sigmoid(-2u_k) = tanh(u_k) (= sp - sm);
 //   dproj = du * inv_temp * (1 - th^2).
-template <int KB, typename T>
+template <int KB, typename T, bool PAIR = false>
 __device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const float *sp, const float *sm,
                               const float *sth, int sw, int L, float inv_temp, T *dproj, const HashOps<T, KB> &ho) {
     constexpr int LDC = ld_of<float>(NCOL);
@@ -1021,7 +1080,7 @@ __device__ float softhash_bwd(const f32x4 (&P)[2], const f32x4 (&dP)[2], const f
             const int l = l0 + tl, c = l < L ? l * KB + k : 0, t = 16 * nt + i;
             tu[nt][e] = th[nt][e] = 0.f;
             if (kind == 1) {
-                tu[nt][e] = sp[t * LDC + c] - sm[t * LDC + c];
+                tu[nt][e] = corner_tanh<PAIR>(sp, sm, t, c);
                 th[nt][e] = sth[t * LDC + c];
             }
         }
@@ -1327,6 +1386,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     using Ly = FwdReduceL<T, SP>;
     using NL = NatL<T, true>;
+    constexpr bool PR = pair_tables<KB>();  // K's sigmoid rows as pair products
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDC = Ly::LDC, LDT = ldp_of<T>(TT), LDN = Ly::LDN, GT = Ly::GT;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sK = (T *)(smem + Ly::oK), *sVt0 = (T *)(smem + Ly::oVt);
@@ -1377,7 +1437,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
         for (int q = w; q < pbk.tasks() * GT; q += NW_) {
             const int u = pbk.tensor(q), r = pbk.task(q);
             float *sp = sSig + u * 2 * TT * LDC;
-            project_tile<T, NL>(sK + u * TT * LDN, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sp, sp + TT * LDC,
+            project_tile<T, NL, PR>(sK + u * TT * LDN, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sp, sp + TT * LDC,
                                 nullptr, (AL && q == w) ? &pcw : nullptr);
         }
         __syncthreads();  // sigmoid rows in LDS
@@ -1388,7 +1448,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
             const float *sp = sSig + u * 2 * TT * LDC;
             const T *vt = sVt + u * Ly::VTE;
             f32x4 PK[2];
-            probs_st<KB, AL>(sp, sp + TT * LDC, sg, a.S, tile_rows((int64_t)jt * TT, a.T), PK);
+            probs_st<KB, AL, PR>(sp, sp + TT * LDC, sg, a.S, tile_rows((int64_t)jt * TT, a.T), PK);
             if (kwp)  // P_K' = w_t P_K
                 for (int nt = 0; nt < 2; ++nt) {
                     const float wt = sTok[u * 2 * TT + 16 * nt + i];
@@ -1686,6 +1746,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     using Ly = FwdOutL<T, SP, CAUSAL, GN>;
     using NL = typename Ly::NL;
     constexpr bool VNAT = Ly::VNAT;
+    constexpr bool PR = pair_tables<KB>();  // Q's and K's sigmoid rows as pair products
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC, LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
@@ -1778,18 +1839,18 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             for (int q = w; q < 2 * pbk.tasks(); q += NW_) {
                 const int r = pbk.task(q);
                 if (q < pbk.tasks())
-                    project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
+                    project_tile<T, NL, PR>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
                                         (AL && q == w) ? &pcw : nullptr);
                 else
-                    project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
+                    project_tile<T, NL, PR>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
                                         (AL && q == w) ? &pcw : nullptr);
             }
             __syncthreads();
             f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
             Frag<T> Pf;
-            probs_st<KB, AL>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
+            probs_st<KB, AL, PR>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
             if constexpr (CAUSAL) {
-                probs_st<KB, AL>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
+                probs_st<KB, AL, PR>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
                 Pf = store_ts_operand<T, SP>(sPts, sw, PK, cst);
                 for (int nt = 0; nt < 2; ++nt) {
                     Acum[nt] = zero4();
@@ -1868,18 +1929,18 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         for (int q = w; q < (CAUSAL ? 2 : 1) * pbk.tasks(); q += NW_) {
             const int r = pbk.task(q);
             if (q < pbk.tasks())
-                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
+                project_tile<T, NL, PR>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
                                     (AL && q == w) ? &pcw : nullptr);
             else
-                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
+                project_tile<T, NL, PR>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
                                     (AL && q == w) ? &pcw : nullptr);
         }
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
         Frag<T> Pf;
-        probs_st<KB, AL>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
+        probs_st<KB, AL, PR>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
         if constexpr (CAUSAL) {
-            probs_st<KB, AL>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
+            probs_st<KB, AL, PR>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
             Pf = token_operand<T>(PK, cst);
@@ -2017,6 +2078,10 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
     using Ly = BwdReduceL<T, SP, CAUSAL, KB, GN>;
     using NL = NatL<T, true>;
+    // K's sigmoid rows as pair products, as in the forward kernels (the walk of
+    // the forward state needs the same P_K); Q's stay corner pairs, which its
+    // softmax backward reads directly
+    constexpr bool PR = pair_tables<KB>();
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     // this tile's token block (block jt & 1 of two; block 0 of one)
@@ -2180,7 +2245,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
                 project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, sThQ,
                                     (AL && q == w) ? &pcw : nullptr);
             else
-                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
+                project_tile<T, NL, PR>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
                                     (AL && q == w) ? &pcw : nullptr);
         }
         // one token block: dQ of the previous tile, from the dproj rows its
@@ -2193,7 +2258,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         Frag<T> Pf;
         probs_st<KB, AL>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
         if constexpr (CAUSAL) {
-            probs_st<KB, AL>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
+            probs_st<KB, AL, PR>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
             Pf = token_operand<T>(PK, cst, po);
             for (int nt = 0; nt < 2; ++nt) {
                 Acum[nt] = zero4();
@@ -2464,6 +2529,9 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
     using Ly = BwdOutL<T, SP, CAUSAL, KB, GN>;
     using NL = NatL<T, true>;
+    // Q's and K's sigmoid rows as pair products (K's as in the forward kernels:
+    // the walk back of the forward state subtracts the same P_K)
+    constexpr bool PR = pair_tables<KB>();
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
                   LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
@@ -2634,10 +2702,10 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         for (int q = w; q < (CAUSAL ? 2 * pbk.tasks() + (MT2 ? 0 : 3) : pbk.tasks()); q += NW_) {
             const int r = pbk.task(q);
             if (q < pbk.tasks())
-                project_tile<T, NL>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, sThK,
+                project_tile<T, NL, PR>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, sThK,
                                     (AL && q == w) ? &pcw : nullptr);
             else if (q < 2 * pbk.tasks())
-                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
+                project_tile<T, NL, PR>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
                                     (AL && q == w) ? &pcw : nullptr);
             else
                 m_tile_xy<T, NL>(q - 2 * pbk.tasks(), sV, sG, sX, sY);
@@ -2668,7 +2736,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         if constexpr (MT2)  // X and Y are read after the next barrier
             for (int q = w; q < 3; q += NW_) m_tile_xy<T, NL>(q, sV, sG, sX, sY);
         f32x4 PKraw[2], PKr[2];  // fp32 P_K (kept for the softmax backward), operand-rounded P_K
-        probs_st<KB, AL>(sSpK, sSmK, sg, a.S, jr + 1 < ntiles ? TT : lastv, PKraw);
+        probs_st<KB, AL, PR>(sSpK, sSmK, sg, a.S, jr + 1 < ntiles ? TT : lastv, PKraw);
         PKr[0] = PKraw[0];
         PKr[1] = PKraw[1];
         float kwt[2] = {1.f, 1.f};  // non-causal key weights: P_K' = w_t P_K
@@ -2687,7 +2755,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
             Frag<T> Wf;
             if constexpr (GN) {
                 f32x4 PQ[2], W[2];
-                probs_st<KB, AL>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
+                probs_st<KB, AL, PR>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
                 for (int nt = 0; nt < 2; ++nt) {
                     const float rd = sTok[16 * nt + i], gd = sTok[TT + 16 * nt + i];
                     for (int e = 0; e < 4; ++e) {
@@ -2698,7 +2766,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                 Wf = store_ts_operand<T, SP>(sWts, sw, W, cst);
             } else {
                 f32x4 PQ[2], Acum[2], W[2], tot, dB[4];
-                probs_st<KB, AL>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
+                probs_st<KB, AL, PR>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
                 // forward state at the tile start: end state minus this tile's sums
                 if constexpr (BM) {
                     tot = zero4();
@@ -2798,11 +2866,11 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         }
         {
             if constexpr (KB <= 4) {
-                tsum += softhash_bwd<KB, T>(PKraw, dPK, sSpK, sSmK, sThK, sg, a.L, a.inv_temp, sDproj, ho);
+                tsum += softhash_bwd<KB, T, PR>(PKraw, dPK, sSpK, sSmK, sThK, sg, a.L, a.inv_temp, sDproj, ho);
             } else {
                 softhash_share<KB, T>(PKraw, dPK, wh, sShare);
                 __syncthreads();
-                tsum += softhash_combine<KB, T, SP, NTH>(sShare, sSpK, sSmK, sThK, z, a.L, a.inv_temp, sDproj);
+                tsum += softhash_combine<KB, T, SP, NTH, PR>(sShare, sSpK, sSmK, sThK, z, a.L, a.inv_temp, sDproj);
             }
         }
         // one token block: the next tile's rows go to it after the tile's
