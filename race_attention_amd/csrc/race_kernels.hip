@@ -1710,6 +1710,21 @@ template <typename T, int SP> __device__ f32x4 fwd_out_partial(int md, int nt, c
     for (int kp = 0; kp < SP / 32; ++kp) mma(O, ld_frag(pb + 32 * kp), ld_frag(pw + 32 * kp));
     return O;
 }
+// Output tiles (md, 0) and (md, 1): their carried-state parts from one read
+// of the B^T operand.
+template <typename T, int SP> __device__ void fwd_out_partial2(int md, const T *sBT, const T *Wts, f32x4 (&O)[2]) {
+    const int i = li();
+    const T *pb = sw_frag_ptr<T, SP>(sBT, 16 * md + i), *pw0 = sw_frag_ptr<T, SP>(Wts, i),
+            *pw1 = sw_frag_ptr<T, SP>(Wts, 16 + i);
+    O[0] = zero4();
+    O[1] = zero4();
+#pragma unroll
+    for (int kp = 0; kp < SP / 32; ++kp) {
+        const Frag<T> b = ld_frag(pb + 32 * kp);
+        mma(O[0], b, ld_frag(pw0 + 32 * kp));
+        mma(O[1], b, ld_frag(pw1 + 32 * kp));
+    }
+}
 template <typename T, int SP, bool GN, bool AL = false, class NL = NatL<T, true>, bool VNAT = is_bf16<T>()>
 __device__ void fwd_out_final(int md, int nt, f32x4 O, const T *sVt, const T *sc, T *op, int64_t st, int64_t t0,
                               int64_t Tn, float *part, const float *sDen, float *den, float eps) {
@@ -1832,6 +1847,10 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             issue(j0 + 1);
         }
         constexpr int NQ = (8 + NW_ - 1) / NW_;  // output tiles per wave
+        // 8 waves writing the output directly: half of them take two output
+        // tiles each (fewer LDS operand reads); with fp32 slice partials the
+        // stores are better spread over all waves (measured)
+        constexpr bool OPAIR = NW_ == 8 && !sliced<T, KB>();
         for (int jt = j0; jt < j1; ++jt) {
             const int64_t t0 = (int64_t)jt * TT;
             sVt = vt_of(jt);
@@ -1889,23 +1908,38 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             store_ts<T, SP>(sWts, sw, W);
             store_ds<T, SP>(sBT, sw, Bc);
             __syncthreads();
-            for (int r = w; r < 3; r += NW_) sc_fwd_tile<T, SP>(r, sPts, sWts, sSc);
-            f32x4 Op[NQ];
+            f32x4 Op[NQ > 2 ? NQ : 2];
+            if constexpr (OPAIR) {
+                // waves 0-3: the output tiles (md = w, nt = 0, 1), one B^T
+                // operand for both; waves 4-6: the Sc blocks
+                if (w < 4) fwd_out_partial2<T, SP>(w, sBT, sWts, Op);
+                else if (w < 7) sc_fwd_tile<T, SP>(w - 4, sPts, sWts, sSc);
+            } else {
+                for (int r = w; r < 3; r += NW_) sc_fwd_tile<T, SP>(r, sPts, sWts, sSc);
 #pragma unroll
-            for (int k = 0; k < NQ; ++k)
-                if (w + k * NW_ < 8) Op[k] = fwd_out_partial<T, SP>((w + k * NW_) >> 1, (w + k * NW_) & 1, sBT, sWts);
+                for (int k = 0; k < NQ; ++k)
+                    if (w + k * NW_ < 8) Op[k] = fwd_out_partial<T, SP>((w + k * NW_) >> 1, (w + k * NW_) & 1, sBT, sWts);
+            }
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
             for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, col_operand<T, NL, VNAT>(sVt, sVt, md));
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
             __syncthreads();  // Sc rows in LDS; the P_K / W / B rows are read
             commit(jt + 1);
             if (jt + 2 < j1) issue(jt + 2);
+            if constexpr (OPAIR) {
+                if (w < 4)
 #pragma unroll
-            for (int k = 0; k < NQ; ++k) {
-                const int q = w + k * NW_;
-                if (q < 8)
-                    fwd_out_final<T, SP, GN, AL, NL, VNAT>(q >> 1, q & 1, Op[k], sVt, sSc, op, a.so.t, t0, a.T, opart, sDen, denp,
-                                             a.eps);
+                    for (int nt = 0; nt < 2; ++nt)
+                        fwd_out_final<T, SP, GN, AL, NL, VNAT>(w, nt, Op[nt], sVt, sSc, op, a.so.t, t0, a.T, opart, sDen,
+                                                               denp, a.eps);
+            } else {
+#pragma unroll
+                for (int k = 0; k < NQ; ++k) {
+                    const int q = w + k * NW_;
+                    if (q < 8)
+                        fwd_out_final<T, SP, GN, AL, NL, VNAT>(q >> 1, q & 1, Op[k], sVt, sSc, op, a.so.t, t0, a.T, opart,
+                                                               sDen, denp, a.eps);
+                }
             }
         }
         return;
