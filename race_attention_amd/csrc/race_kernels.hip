@@ -272,6 +272,17 @@ template <typename T, bool SW> struct NatL {
             return ld_frag_pi(base + r * LD + 32 * h);
     }
 };
+// Plain token rows for tiles read only by LDS transpose loads (col_operand,
+// bf16): row r at r * LD, k in natural order.  LD = D + 16 puts the rows of a
+// 4-row group 8 dwords apart modulo the 32 banks of 8-byte accesses, so the 4
+// rows x 4 runs of 8 bytes that one 16-lane pass of a transpose load reads
+// fall on 32 distinct banks (the swizzled pi-order rows put them on 16).
+template <typename T> struct TrL {
+    static constexpr bool P = false;
+    static constexpr int LD = D + 16;
+    __device__ __forceinline__ static int off(int r, int k) { return r * LD + k; }
+};
+
 // acc += A[rA .. rA+15][:] * B[rB .. rB+15][:]^T over all D of two natural arrays
 template <class NL, typename T>
 __device__ __forceinline__ void nat_mma(f32x4 &acc, const T *A, int rA, const T *B, int rB) {
@@ -1387,6 +1398,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     using Ly = FwdReduceL<T, SP>;
     using NL = NatL<T, true>;
     constexpr bool PR = pair_tables<KB>();  // K's sigmoid rows as pair products
+    using VL = TrL<T>;                      // V rows: read only by transpose loads
+    static_assert(!is_bf16<T>() || TrL<T>::LD <= NatL<T, true>::LD, "V rows within the tile buffer");
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDC = Ly::LDC, LDT = ldp_of<T>(TT), LDN = Ly::LDN, GT = Ly::GT;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sK = (T *)(smem + Ly::oK), *sVt0 = (T *)(smem + Ly::oVt);
@@ -1458,7 +1471,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
             if constexpr (BM) {
                 f32x4 tot = zero4();
                 mma(tot, Pf, cst.ones());
-                for (int md = 0; md < 4; ++md) mma(accBm[md], col_operand<T, NL>(vt, vt, md), Pf);
+                for (int md = 0; md < 4; ++md) mma(accBm[md], col_operand<T, VL>(vt, vt, md), Pf);
                 for (int e = 0; e < 4; ++e) accA[e] += (double)tot[e];
             } else {
                 f32x4 tot, dB[4];
@@ -1497,7 +1510,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
 #pragma unroll
             for (int u = 0; u < GT; ++u) {
                 pk[u].template commit<NL>(sK + u * TT * LDN, nullptr);
-                pv[u].template commit<NL>(sVt + u * Ly::VTE, nullptr);
+                pv[u].template commit<VL>(sVt + u * Ly::VTE, nullptr);
             }
         };
         if (j0 < j1) {
@@ -1539,7 +1552,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
 #pragma unroll
             for (int u = 0; u < GT; ++u) {
                 pk_[u].template commit<NL>(sK + u * TT * LDN, nullptr);
-                pv_[u].template commit<NL>(0, is_bf16<T>() ? sVt + u * Ly::VTE : nullptr,
+                pv_[u].template commit<VL>(0, is_bf16<T>() ? sVt + u * Ly::VTE : nullptr,
                                            is_bf16<T>() ? nullptr : sVt + u * Ly::VTE);
                 if (kwp) pt_[u].commit(sTok + u * 2 * TT);
             }
@@ -1605,7 +1618,7 @@ template <typename T, int SP, bool CAUSAL, bool GN> struct FwdOutL {
     // (bf16 F1), or transposed (fp32, and the global normalisation, whose
     // registers are at the 4-waves-per-SIMD limit)
     static constexpr bool VNAT = is_bf16<T>() && !GN;
-    static constexpr size_t VTB = VNAT ? sizeof(T) * TT * LDN : sizeof(T) * D * LDT;
+    static constexpr size_t VTB = VNAT ? sizeof(T) * TT * TrL<T>::LD : sizeof(T) * D * LDT;
     static constexpr size_t oVt = 0;
     static constexpr size_t oSig = align16(oVt + (CAUSAL ? VTB : 0));  // Q sp, Q sm, K sp, K sm
     static constexpr size_t oPts = align16(oSig + sizeof(float) * (CAUSAL ? 4 : 2) * TT * LDC);
@@ -1762,6 +1775,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     using NL = typename Ly::NL;
     constexpr bool VNAT = Ly::VNAT;
     constexpr bool PR = pair_tables<KB>();  // Q's and K's sigmoid rows as pair products
+    using VL = TrL<T>;                      // V rows (VNAT): read only by transpose loads
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC, LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     T *sQ = (T *)(smem + Ly::oQ), *sK = (T *)(smem + Ly::oK), *sVt = (T *)(smem + Ly::oVt);
@@ -1811,12 +1825,26 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 
     wait_state_loads();
     Prefetch<T, NTH, AL> pq_, pk_;
-    PrefetchT<T, NTH, 1, AL, !VNAT> pv_;  // V: natural rows (VNAT) or transposed
+    // V: plain rows read by transpose loads (VNAT; staged row by row, 16
+    // lanes per row, conflict-free) or transposed rows
+    std::conditional_t<VNAT, Prefetch<T, NTH, AL>, PrefetchT<T, NTH, 1, AL, true>> pv_;
+    auto v_issue = [&](int64_t t0) {
+        if constexpr (VNAT)
+            pv_.issue(vp, a.sv.t, t0, a.T);
+        else
+            pv_.issue(0, vp, a.sv.t, t0, a.T);
+    };
+    auto v_commit = [&](T *buf) {
+        if constexpr (VNAT)
+            pv_.template commit<VL>(buf, nullptr);
+        else
+            pv_.template commit<NL>(0, nullptr, buf);
+    };
     if (j0 < j1) {
         pq_.issue(qp, a.sq.t, (int64_t)j0 * TT, a.T);
         if constexpr (CAUSAL) {
             pk_.issue(kp, a.sk.t, (int64_t)j0 * TT, a.T);
-            pv_.issue(0, vp, a.sv.t, (int64_t)j0 * TT, a.T);
+            v_issue((int64_t)j0 * TT);
         }
     }
     if constexpr (Ly::SCN) {
@@ -1831,7 +1859,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             wait_vmem();
             pq_.template commit<NL>(sQ, nullptr);
             pk_.template commit<NL>(sK, nullptr);
-            pv_.template commit<NL>(0, VNAT ? vt_of(j) : nullptr, VNAT ? nullptr : vt_of(j));
+            v_commit(vt_of(j));
         };
         // The rows of tile j + 1 are loaded from the commit of tile j on
         // (the registers are free then), a tile and a phase ahead of their
@@ -1840,7 +1868,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             const int64_t tn = (int64_t)min(j, j1 - 1) * TT;
             pq_.issue(qp, a.sq.t, tn, a.T);
             pk_.issue(kp, a.sk.t, tn, a.T);
-            pv_.issue(0, vp, a.sv.t, tn, a.T);
+            v_issue(tn);
         };
         if (j0 < j1) {
             commit(j0);
@@ -1921,7 +1949,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
                     if (w + k * NW_ < 8) Op[k] = fwd_out_partial<T, SP>((w + k * NW_) >> 1, (w + k * NW_) & 1, sBT, sWts);
             }
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
-            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, col_operand<T, NL, VNAT>(sVt, sVt, md));
+            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, col_operand<T, VL, VNAT>(sVt, sVt, md));
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
             __syncthreads();  // Sc rows in LDS; the P_K / W / B rows are read
             commit(jt + 1);
@@ -1930,14 +1958,14 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
                 if (w < 4)
 #pragma unroll
                     for (int nt = 0; nt < 2; ++nt)
-                        fwd_out_final<T, SP, GN, AL, NL, VNAT>(w, nt, Op[nt], sVt, sSc, op, a.so.t, t0, a.T, opart, sDen,
+                        fwd_out_final<T, SP, GN, AL, VL, VNAT>(w, nt, Op[nt], sVt, sSc, op, a.so.t, t0, a.T, opart, sDen,
                                                                denp, a.eps);
             } else {
 #pragma unroll
                 for (int k = 0; k < NQ; ++k) {
                     const int q = w + k * NW_;
                     if (q < 8)
-                        fwd_out_final<T, SP, GN, AL, NL, VNAT>(q >> 1, q & 1, Op[k], sVt, sSc, op, a.so.t, t0, a.T, opart,
+                        fwd_out_final<T, SP, GN, AL, VL, VNAT>(q >> 1, q & 1, Op[k], sVt, sSc, op, a.so.t, t0, a.T, opart,
                                                                sDen, denp, a.eps);
                 }
             }
@@ -1950,13 +1978,13 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         pq_.template commit<NL>(sQ, nullptr);
         if constexpr (CAUSAL) {
             pk_.template commit<NL>(sK, nullptr);
-            pv_.template commit<NL>(0, VNAT ? sVt : nullptr, VNAT ? nullptr : sVt);
+            v_commit(sVt);
         }
         if (jt + 1 < j1) {
             pq_.issue(qp, a.sq.t, t0 + TT, a.T);
             if constexpr (CAUSAL) {
                 pk_.issue(kp, a.sk.t, t0 + TT, a.T);
-                pv_.issue(0, vp, a.sv.t, t0 + TT, a.T);
+                v_issue(t0 + TT);
             }
         }
         __syncthreads();
@@ -2019,11 +2047,11 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         }
         __syncthreads();
         for (int q = w; q < 8; q += NW_)
-            fwd_out_tile<T, SP, CAUSAL, GN, AL, NL, VNAT>(q >> 1, q & 1, sBT, sPts, sWts, sVt, op, a.so.t, t0, a.T, opart, sDen,
+            fwd_out_tile<T, SP, CAUSAL, GN, AL, VL, VNAT>(q >> 1, q & 1, sBT, sPts, sWts, sVt, op, a.so.t, t0, a.T, opart, sDen,
                                             denp, a.eps);
         if constexpr (CAUSAL) {
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
-            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, col_operand<T, NL, VNAT>(sVt, sVt, md));
+            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, col_operand<T, VL, VNAT>(sVt, sVt, md));
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
         }
     }
