@@ -206,9 +206,27 @@ template <> __device__ __forceinline__ void buf_st4<bf16>(__amdgpu_buffer_rsrc_t
     for (int e = 0; e < 4; ++e) o[e] = (bf16)v[e];
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o), r, (int)off, 0, 0);
 }
+// Base of the token tile that starts at t0 (a multiple of TT) of a tensor with
+// token stride st.  The host bounds TT * st * sizeof(T) below 2^32 and T by
+// 2^35, so the offset is one 32 x 32-bit product of the tile index and the
+// tile's byte stride: two scalar multiplies per tile where a 64-bit
+// t0 * st * sizeof(T) takes a dozen scalar instructions.
+template <typename T> __device__ __forceinline__ T *tile_ptr(T *src, int64_t st, int64_t t0) {
+    const uint32_t tb = (uint32_t)st * (uint32_t)(TT * sizeof(T));
+    const uint64_t off = (uint64_t)(uint32_t)((uint64_t)t0 / TT) * tb;
+    using C = std::conditional_t<std::is_const<T>::value, const char, char>;  // pointer arithmetic keeps the global loads
+    return reinterpret_cast<T *>(reinterpret_cast<C *>(src) + off);
+}
 // byte offset of element (t, d) of a token tile
 __device__ __forceinline__ uint32_t tile_off(int t, int64_t st, int d, int esize) {
     return ((uint32_t)t * (uint32_t)st + (uint32_t)d) * (uint32_t)esize;
+}
+
+// Element (t, d) of the tile at t0 of a [T][D] fp32 partial block (bucket
+// slices): a uniform tile base and a 32-bit lane offset that stays the same
+// on every tile.
+__device__ __forceinline__ float *part_at(float *part, int64_t t0, int t, int d) {
+    return at_bytes(part + t0 * D, (uint32_t)(t * D + d) * (uint32_t)sizeof(float));
 }
 
 template <int B> struct ChunkOf;
@@ -315,7 +333,7 @@ template <typename T, int NTH, bool AL = false> struct Prefetch {
     // tile base src + t0 * st is uniform; the lane offset t * st + c * EPC is
     // 32-bit (the host bounds 32 * token stride below 2^31)
     __device__ __forceinline__ void issue(const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn) {
-        const T *base = src + t0 * st;
+        const T *base = tile_ptr(src, st, t0);
         const int rem = AL ? TT : tile_rows(t0, Tn);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
@@ -371,7 +389,7 @@ template <typename T, int NTH, int NPART, bool AL = false, bool TRN = true> stru
         return local >= 0 && local < NT && task < TASKS;
     }
     __device__ __forceinline__ void issue(int part, const T *__restrict__ src, int64_t st, int64_t t0, int64_t Tn) {
-        const T *base = src + t0 * st;
+        const T *base = tile_ptr(src, st, t0);
         const int rem = AL ? TT : tile_rows(t0, Tn);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
@@ -434,7 +452,7 @@ template <typename T, int NTH, bool AL = false, bool TRN = true> struct Prefetch
                                           int64_t st1, int64_t t0, int64_t Tn) {
         const bool sc = second();
         const int64_t st = sc ? st1 : st0;
-        const T *base = (sc ? src1 : src0) + t0 * st;
+        const T *base = tile_ptr(sc ? src1 : src0, st, t0);
         const int rem = AL ? TT : tile_rows(t0, Tn);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
@@ -1308,6 +1326,17 @@ template <typename T, int NW_, int XC = 8, bool AL = false>
 __device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64_t t0, int64_t Tn, T *part,
                          int c0 = 0) {
     if (part) {
+        if constexpr (is_bf16<T>() && XC == 8) {
+            if ((c0 & 7) == 0) {
+                // the 8 columns are one 16-byte granule of each swizzled dproj
+                // row (c0 + 8 <= NCOL): one 16-byte copy per token
+                const int t = threadIdx.x;
+                if (t < TT && (AL || t < tile_rows(t0, Tn)))
+                    *reinterpret_cast<uint4 *>(at_bytes(part + t0 * XC, (uint32_t)(t * XC) * (uint32_t)sizeof(T))) =
+                        *reinterpret_cast<const uint4 *>(dproj + sw_off<T, NCOL>(t, c0));
+                return;
+            }
+        }
         for (int idx = threadIdx.x; idx < TT * XC; idx += 64 * NW_) {
             const int t = idx / XC, c = idx % XC;
             if (AL || t < tile_rows(t0, Tn)) part[(t0 + t) * XC + c] = c0 + c < NCOL ? dproj[sw_off<T, NCOL>(t, c0 + c)] : from_f32<T>(0.f);
@@ -1315,7 +1344,7 @@ __device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64
         return;
     }
     const int g = lg(), i = li(), w = wave_id();
-    T *base = dst + t0 * st;
+    T *base = tile_ptr(dst, st, t0);
     for (int q = w; q < 8; q += NW_) {
         const int md = q >> 1, nt = q & 1;
         f32x4 acc = zero4();
@@ -1691,9 +1720,9 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
     }
     if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
-            store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, O);
+            store4<float>(part_at(part, t0, t, 16 * md + 4 * g), O);
         else
-            buf_st4<T>(tile_rsrc(op + t0 * st, st, Tn - t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T)), O);
+            buf_st4<T>(tile_rsrc(tile_ptr(op, st, t0), st, AL ? (int64_t)TT : Tn - t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T)), O);
     }
 }
 
@@ -1759,9 +1788,9 @@ __device__ void fwd_out_final(int md, int nt, f32x4 O, const T *sVt, const T *sc
     }
     if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
-            store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, O);
+            store4<float>(part_at(part, t0, t, 16 * md + 4 * g), O);
         else
-            buf_st4<T>(tile_rsrc(op + t0 * st, st, Tn - t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T)), O);
+            buf_st4<T>(tile_rsrc(tile_ptr(op, st, t0), st, AL ? (int64_t)TT : Tn - t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T)), O);
     }
 }
 
@@ -2549,9 +2578,9 @@ __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts
     const int t = 16 * nt + i;
     if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
-            store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, acc);
+            store4<float>(part_at(part, t0, t, 16 * md + 4 * g), acc);
         else
-            store4<T>(at_bytes(dvp + t0 * st, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
+            store4<T>(at_bytes(tile_ptr(dvp, st, t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
     }
 }
 
@@ -2576,9 +2605,9 @@ __device__ void dv_finish(int md, int nt, f32x4 acc, const T *sG, const T *sGt, 
     const int t = 16 * nt + i;
     if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
-            store4<float>(part + (t0 + t) * D + 16 * md + 4 * g, acc);
+            store4<float>(part_at(part, t0, t, 16 * md + 4 * g), acc);
         else
-            store4<T>(at_bytes(dvp + t0 * st, tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
+            store4<T>(at_bytes(tile_ptr(dvp, st, t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
     }
 }
 
