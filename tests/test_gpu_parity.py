@@ -171,6 +171,25 @@ def test_parity_small(dev, name, kw, causal, it, seg):
     compare(name, gpu, ref, TOL[q.dtype])
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_t1_reference_eps_out_dv(dev, dtype):
+    """T=1 at the reference eps (1e-6): out and dV are well conditioned there
+    (out = sum_l v . P_Q P_K / (P_K + eps), dV its transpose), so they are
+    checked to the usual bars; dQ and dK carry the factor eps/(P + eps) and are
+    covered at eps=0.5 by the *_T1_eps cases."""
+    fp32 = dtype == torch.float32
+    L, K = (5, 2) if fp32 else (8, 4)
+    q, k, v, do, planes = make_case(T=1, H=2, L=L, K=K, dtype=dtype, unit=not fp32, seed=21)
+    it = 1.0 if fp32 else 1.0 / math.sqrt(q.shape[-1])
+    gpu = run_gpu(q, k, v, do, planes, L=L, K=K, causal=True, inv_temp=it, dev=dev)
+    ref = run_oracle(q, k, v, do, planes, causal=True, inv_temp=it)
+    tol = TOL[dtype]
+    for nm, a, b in (("out", gpu[0], ref[0]), ("dv", gpu[3], ref[3])):
+        e = relerr(to64(a), b)
+        print(f"[T1 {dtype}] {nm}={e:.2e}", flush=True)
+        assert e <= tol, f"T=1 {nm} relerr {e:.3e} > {tol:.1e}"
+
+
 def test_strided_fused_qkv_layout(dev):
     """Q, K, V as views into one [B, T, 3*H, D] projection (token stride 3*H*D)."""
     B, T, H, D, L, K = 2, 120, 2, 64, 8, 4
