@@ -146,7 +146,9 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
 
 // Largest token stride (elements) whose lane byte offsets inside a 32-token
 // tile, ((TT - 1) * stride + D) * esize, fit the kernels' 32-bit offsets and
-// the 2^31 - 1 byte record size of k_fwd_out's buffer stores.
+// the 2^31 - 1 byte record size of k_fwd_out's buffer stores.  It also keeps a
+// tile's byte stride TT * stride * esize below 2^32, which the kernels' tile
+// base addresses (tile index times that stride, a 32 x 32-bit product) need.
 int64_t max_token_stride(size_t esize) { return (0x7FFFFFFFll / (int64_t)esize - D) / (TT - 1); }
 
 int check_tensor(const char *name, const void *ptr, const int64_t *st, size_t esize, int64_t T) {

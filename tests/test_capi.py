@@ -168,6 +168,9 @@ def test_token_stride_byte_bound(dtype, esize):
     stride whose tile spans at most 2^31 - 1 bytes is accepted (the call then
     stops at the too-small workspace), the next 16-byte multiple is rejected."""
     lib = _lib.load()
+    # the accepted stride also keeps a tile's byte stride (32 rows) below
+    # 2^32, the bound of the kernels' 32 x 32-bit tile base offsets
+    assert 32 * _max_stride(esize) * esize < 2 ** 32
     p = ctypes.c_void_p(256)
     for which in ("q_stride", "o_stride"):
         d = _desc(T=64, H=1, dtype=dtype)
