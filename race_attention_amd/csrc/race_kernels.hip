@@ -1912,14 +1912,24 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             const int64_t t0 = (int64_t)jt * TT;
             sVt = vt_of(jt);
             __syncthreads();  // this tile's rows in LDS; the previous tile's O rows are done
-            for (int q = w; q < 2 * pbk.tasks(); q += NW_) {
-                const int r = pbk.task(q);
-                if (q < pbk.tasks())
-                    project_tile<T, NL, PR>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
-                                        (AL && q == w) ? &pcw : nullptr);
-                else
-                    project_tile<T, NL, PR>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
-                                        (AL && q == w) ? &pcw : nullptr);
+            if constexpr (AL) {
+                // whole tiles: at most one task per wave (Q first), one code path
+                if (2 * pbk.tasks() >= NW_ || w < 2 * pbk.tasks()) {
+                    const bool isq = w < pbk.tasks();
+                    const int r = pbk.task(w);
+                    project_tile<T, NL, PR>(isq ? sQ : sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp,
+                                            isq ? sSpQ : sSpK, isq ? sSmQ : sSmK, nullptr, &pcw);
+                }
+            } else {
+                for (int q = w; q < 2 * pbk.tasks(); q += NW_) {
+                    const int r = pbk.task(q);
+                    if (q < pbk.tasks())
+                        project_tile<T, NL, PR>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
+                                                (AL && q == w) ? &pcw : nullptr);
+                    else
+                        project_tile<T, NL, PR>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
+                                                (AL && q == w) ? &pcw : nullptr);
+                }
             }
             __syncthreads();
             f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
@@ -2790,16 +2800,28 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         // projection task on a wave of its own) in the next phase, whose
         // bucket work leaves issue slots to fill
         constexpr bool MT2 = SCN;
-        for (int q = w; q < (CAUSAL ? 2 * pbk.tasks() + (MT2 ? 0 : 3) : pbk.tasks()); q += NW_) {
-            const int r = pbk.task(q);
-            if (q < pbk.tasks())
-                project_tile<T, NL, PR>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, sThK,
-                                    (AL && q == w) ? &pcw : nullptr);
-            else if (q < 2 * pbk.tasks())
-                project_tile<T, NL, PR>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
-                                    (AL && q == w) ? &pcw : nullptr);
-            else
-                m_tile_xy<T, NL>(q - 2 * pbk.tasks(), sV, sG, sX, sY);
+        if constexpr (AL && MT2) {
+            // whole tiles: at most one task per wave, K (first half) or Q --
+            // one code path on scalar-selected rows, which the compiler can
+            // interleave with the rest of the phase (unsliced: every wave)
+            if (2 * pbk.tasks() >= NW_ || w < 2 * pbk.tasks()) {
+                const bool isk = w < pbk.tasks();
+                const int r = pbk.task(w);
+                project_tile<T, NL, PR>(isk ? sK : sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, isk ? sSpK : sSpQ,
+                                        isk ? sSmK : sSmQ, isk ? sThK : nullptr, &pcw);
+            }
+        } else {
+            for (int q = w; q < (CAUSAL ? 2 * pbk.tasks() + (MT2 ? 0 : 3) : pbk.tasks()); q += NW_) {
+                const int r = pbk.task(q);
+                if (q < pbk.tasks())
+                    project_tile<T, NL, PR>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, sThK,
+                                            (AL && q == w) ? &pcw : nullptr);
+                else if (q < 2 * pbk.tasks())
+                    project_tile<T, NL, PR>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
+                                            (AL && q == w) ? &pcw : nullptr);
+                else
+                    m_tile_xy<T, NL>(q - 2 * pbk.tasks(), sV, sG, sX, sY);
+            }
         }
         // dK of the tile after this one (walking down), from the dproj rows its
         // softmax backward left in LDS: with one token block beside the
