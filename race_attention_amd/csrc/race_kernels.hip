@@ -2497,6 +2497,15 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_bwd_scan(float *rstate, const 
 // =====================================================================
 template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     static constexpr int NW_ = SP / WB;
+    // the configuration of the whole-tile 4-bit instantiation (bf16, 128-bucket
+    // slices, causal F1): it projects a tile in the previous tile's last phase,
+    // so K's sigmoid rows are double-buffered, and the transposed V / dO rows,
+    // which bf16 never reads, take no LDS.  (8-bit slices measured faster with
+    // the projections in a phase of their own: only half of their waves have a
+    // projection task, and their last phase already ends at the wide-table
+    // barrier.)
+    static constexpr bool P2L = is_bf16<T>() && SP == 128 && CAUSAL && !GN && KB == 4;
+    static constexpr int NSIG = P2L ? 8 : (CAUSAL ? 5 : 3);  // sigmoid row arrays
     static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>(),
                          LDS_ = sw_ld<T, SP>();
     // token block: one tile's staged rows (K, Q, V, dO natural; V, dO
@@ -2506,8 +2515,8 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     static constexpr size_t oV = align16(oQ + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oG = align16(oV + sizeof(T) * TT * LDN);
     static constexpr size_t oVt = align16(oG + (CAUSAL ? sizeof(T) * TT * LDN : 0));
-    static constexpr size_t oGt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oTok = align16(oGt + (CAUSAL ? sizeof(T) * D * LDT : 0));
+    static constexpr size_t oGt = align16(oVt + (CAUSAL && !P2L ? sizeof(T) * D * LDT : 0));
+    static constexpr size_t oTok = align16(oGt + (CAUSAL && !P2L ? sizeof(T) * D * LDT : 0));
     static constexpr size_t TB = align16(oTok + (GN || !CAUSAL ? sizeof(float) * 2 * TT : 0));
     // the rest, relative to its start
     static constexpr size_t rX = 0;
@@ -2519,11 +2528,12 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdOutL {
     static constexpr size_t rPl = align16(rDproj + sizeof(T) * TT * LDDP);
     static constexpr size_t rPlLo = align16(rPl + sizeof(T) * NCOL * LDN);
     static constexpr size_t rPlT = align16(rPlLo + sizeof(T) * NCOL * LDN);
-    static constexpr size_t rSig = align16(rPlT + sizeof(T) * D * LDDP);  // K sp, K sm, K th, Q sp, Q sm
+    // K sp, K sm, K th, Q sp, Q sm (P2L: then K sp, K sm, K th of odd tiles)
+    static constexpr size_t rSig = align16(rPlT + sizeof(T) * D * LDDP);
     // the end-of-kernel block sum's scratch [64 * NW_] reuses the sigmoid rows
     static_assert(64 * NW_ <= (CAUSAL ? 5 : 3) * TT * LDC, "block-sum scratch inside the sigmoid rows");
     static constexpr size_t rRed = rSig;
-    static constexpr size_t rCst = align16(rSig + sizeof(float) * (CAUSAL ? 5 : 3) * TT * LDC);
+    static constexpr size_t rCst = align16(rSig + sizeof(float) * NSIG * TT * LDC);
     static constexpr size_t rHash = align16(rCst + Consts<T>::bytes);
     // causal: Sc2^T [tau][t] of the last tile, for the dV tiles of the next
     // iteration (with two token blocks)
@@ -2762,7 +2772,58 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     f32x4 dvacc[NQD];                          // SCN: carried part of the last tile's dV tiles
 #pragma unroll
     for (int k = 0; k < NQD; ++k) dvacc[k] = zero4();
-    if (j0 < j1) {
+    // Whole 4-bit tiles (P2): two barriers per tile instead of three.  The Q and K
+    // rows of tile j - 1 are committed in tile j's second phase and projected
+    // at the end of its last phase, into the Q rows (read only in the second
+    // phase) and K rows of the other parity (K's are also read by the
+    // softmax backward of the last phase); V and dO are committed in the last
+    // phase as before.  Each prefetch set is reloaded right after its commit,
+    // a tile ahead, and its commit waits on it by count (every lane issues the
+    // same branch-free loads), not on the stores issued since.
+    constexpr bool P2 = AL && SCN && Ly::P2L;
+    // the three masked v.g^T blocks: with the projections, or (two token
+    // blocks, every projection task on a wave of its own) in the next phase,
+    // whose bucket work leaves issue slots to fill
+    constexpr bool MT2 = SCN;
+    static_assert(!Ly::P2L || !AL || SCN, "the 4-bit whole-tile instantiation runs the two-barrier walk");
+    auto commit_qk = [&](int b) {
+        unsigned char *tb = smem + b * Ly::TB;
+        pk_.template commit<NL>((T *)(tb + Ly::oK), nullptr);
+        pq_.template commit<NL>((T *)(tb + Ly::oQ), nullptr);
+    };
+    auto commit_vg = [&](int b) {
+        unsigned char *tb = smem + b * Ly::TB;
+        pgv_.template commit<NL>((T *)(tb + Ly::oG), (T *)(tb + Ly::oGt), (T *)(tb + Ly::oV), (T *)(tb + Ly::oVt));
+    };
+    auto issue_qk = [&](int64_t tq) {
+        pk_.issue(kp, a.sk.t, tq, a.T);
+        pq_.issue(qp, a.sq.t, tq, a.T);
+    };
+    auto issue_vg = [&](int64_t tq) { pgv_.issue(gp, a.sdo.t, vp, a.sv.t, tq, a.T); };
+    // the wave's projection task (at most one: K in the first half, Q) of the
+    // tile in token block b, into the Q rows and the K rows of parity par
+    auto project2 = [&](int b, int par) {
+        unsigned char *tb = smem + b * Ly::TB;
+        if (2 * pbk.tasks() >= NW_ || w < 2 * pbk.tasks()) {
+            const bool isk = w < pbk.tasks();
+            const int r = pbk.task(w);
+            float *kr = sSig + (par ? 5 : 0) * TT * LDC;
+            project_tile<T, NL, PR>(isk ? (const T *)(tb + Ly::oK) : (const T *)(tb + Ly::oQ), sPl, sPlLo, pbk.mc(r),
+                                    r & 1, a.inv_temp, isk ? kr : sSpQ, isk ? kr + TT * LDC : sSmQ,
+                                    isk ? kr + 2 * TT * LDC : nullptr, &pcw);
+        }
+    };
+    if (P2 && j0 < j1) {
+        const int64_t tl = (int64_t)(j1 - 1) * TT, tl2 = (int64_t)max(j1 - 2, j0) * TT;
+        issue_qk(tl);
+        issue_vg(tl);
+        commit_qk((j1 - 1) & 1);
+        commit_vg((j1 - 1) & 1);
+        issue_qk(tl2);
+        issue_vg(tl2);
+        __syncthreads();
+        project2((j1 - 1) & 1, (j1 - 1) & 1);
+    } else if (j0 < j1) {
         const int64_t tl = (int64_t)(j1 - 1) * TT;
         pk_.issue(kp, a.sk.t, tl, a.T);
         if constexpr (CAUSAL) {
@@ -2784,66 +2845,84 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         // loop head, and the wait placed there also waits for the previous
         // tile's stores.
         const int64_t tn = (int64_t)(jr > j0 ? jr - 1 : jr) * TT;
+        if constexpr (P2) {
+            sSpK = sSig + ((jr & 1) ? 5 : 0) * TT * LDC;  // this tile's K rows
+            sSmK = sSpK + TT * LDC;
+            sThK = sSpK + 2 * TT * LDC;
+        } else {
+            __syncthreads();
+            // issued after the barrier: the previous tile's dK stores have had
+            // the barrier's time to drain from the memory pipeline
+            pk_.issue(kp, a.sk.t, tn, a.T);
+            if constexpr (CAUSAL) {
+                pq_.issue(qp, a.sq.t, tn, a.T);
+                pgv_.issue(gp, a.sdo.t, vp, a.sv.t, tn, a.T);
+            } else {
+                pvn_.issue(vp, a.sv.t, tn, a.T);
+                if (kwp) pt_.issue(kwp, nullptr, tn, a.T);
+            }
+            if constexpr (GN) pt_.issue(rdp, gdp, tn, a.T);
+            if constexpr (AL && MT2) {
+                // whole tiles: at most one task per wave, K (first half) or Q --
+                // one code path on scalar-selected rows, which the compiler can
+                // interleave with the rest of the phase
+                if (w < 2 * pbk.tasks()) {
+                    const bool isk = w < pbk.tasks();
+                    const int r = pbk.task(w);
+                    project_tile<T, NL, PR>(isk ? sK : sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp,
+                                            isk ? sSpK : sSpQ, isk ? sSmK : sSmQ, isk ? sThK : nullptr, &pcw);
+                }
+            } else {
+                for (int q = w; q < (CAUSAL ? 2 * pbk.tasks() + (MT2 ? 0 : 3) : pbk.tasks()); q += NW_) {
+                    const int r = pbk.task(q);
+                    if (q < pbk.tasks())
+                        project_tile<T, NL, PR>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, sThK,
+                                                (AL && q == w) ? &pcw : nullptr);
+                    else if (q < 2 * pbk.tasks())
+                        project_tile<T, NL, PR>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
+                                                (AL && q == w) ? &pcw : nullptr);
+                    else
+                        m_tile_xy<T, NL>(q - 2 * pbk.tasks(), sV, sG, sX, sY);
+                }
+            }
+            // dK of the tile after this one (walking down), from the dproj rows its
+            // softmax backward left in LDS: with one token block beside the
+            // projections, with two (below) beside the probabilities, after the
+            // second barrier; the next write of sDproj is after the third
+            if constexpr (!SCN)
+                if (jr + 1 < j1) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
+            // causal, two token blocks: dV of that tile too, its carried part
+            // (computed last iteration) plus the in-tile part from its Sc2 rows and
+            // its dO tile (still in its block: the next commit there is after this
+            // tile's third barrier)
+            if constexpr (SCN)
+                if (jr + 1 < j1) {
+                    const T *gtn = (const T *)(smem + ((jr + 1) & 1) * Ly::TB + Ly::oGt);
+                    const T *gnn = (const T *)(smem + ((jr + 1) & 1) * Ly::TB + Ly::oG);
+#pragma unroll
+                    for (int k = 0; k < NQD; ++k)
+                        if (w + k * NW_ < 8)
+                            dv_finish<T, AL>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gnn, gtn, sSc2, dvp,
+                                             a.sg.t, t0 + TT, a.T, vpart);
+                }
+        }
         __syncthreads();
-        // issued after the barrier: the previous tile's dK stores have had
-        // the barrier's time to drain from the memory pipeline
-        pk_.issue(kp, a.sk.t, tn, a.T);
-        if constexpr (CAUSAL) {
-            pq_.issue(qp, a.sq.t, tn, a.T);
-            pgv_.issue(gp, a.sdo.t, vp, a.sv.t, tn, a.T);
-        } else {
-            pvn_.issue(vp, a.sv.t, tn, a.T);
-            if (kwp) pt_.issue(kwp, nullptr, tn, a.T);
-        }
-        if constexpr (GN) pt_.issue(rdp, gdp, tn, a.T);
-        // the three masked v.g^T blocks: here, or (two token blocks, every
-        // projection task on a wave of its own) in the next phase, whose
-        // bucket work leaves issue slots to fill
-        constexpr bool MT2 = SCN;
-        if constexpr (AL && MT2) {
-            // whole tiles: at most one task per wave, K (first half) or Q --
-            // one code path on scalar-selected rows, which the compiler can
-            // interleave with the rest of the phase (unsliced: every wave)
-            if (2 * pbk.tasks() >= NW_ || w < 2 * pbk.tasks()) {
-                const bool isk = w < pbk.tasks();
-                const int r = pbk.task(w);
-                project_tile<T, NL, PR>(isk ? sK : sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, isk ? sSpK : sSpQ,
-                                        isk ? sSmK : sSmQ, isk ? sThK : nullptr, &pcw);
-            }
-        } else {
-            for (int q = w; q < (CAUSAL ? 2 * pbk.tasks() + (MT2 ? 0 : 3) : pbk.tasks()); q += NW_) {
-                const int r = pbk.task(q);
-                if (q < pbk.tasks())
-                    project_tile<T, NL, PR>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, sThK,
-                                            (AL && q == w) ? &pcw : nullptr);
-                else if (q < 2 * pbk.tasks())
-                    project_tile<T, NL, PR>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, nullptr,
-                                            (AL && q == w) ? &pcw : nullptr);
-                else
-                    m_tile_xy<T, NL>(q - 2 * pbk.tasks(), sV, sG, sX, sY);
-            }
-        }
-        // dK of the tile after this one (walking down), from the dproj rows its
-        // softmax backward left in LDS: with one token block beside the
-        // projections, with two (below) beside the probabilities, after the
-        // second barrier; the next write of sDproj is after the third
-        if constexpr (!SCN)
-            if (jr + 1 < j1) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
-        // causal, two token blocks: dV of that tile too, its carried part
-        // (computed last iteration) plus the in-tile part from its Sc2 rows and
-        // its dO tile (still in its block: the next commit there is after this
-        // tile's third barrier)
-        if constexpr (SCN)
+        if constexpr (P2) {
+            // tile j - 1's Q and K rows, then the loads of tile j - 2's; the
+            // dV tiles of tile j + 1 (its dO rows stay until this tile's last
+            // phase)
+            commit_qk((jr + 1) & 1);
+            issue_qk((int64_t)max(jr - 2, j0) * TT);
             if (jr + 1 < j1) {
                 const T *gtn = (const T *)(smem + ((jr + 1) & 1) * Ly::TB + Ly::oGt);
                 const T *gnn = (const T *)(smem + ((jr + 1) & 1) * Ly::TB + Ly::oG);
 #pragma unroll
                 for (int k = 0; k < NQD; ++k)
                     if (w + k * NW_ < 8)
-                        dv_finish<T, AL>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gnn, gtn, sSc2, dvp, a.sg.t, t0 + TT,
-                                     a.T, vpart);
+                        dv_finish<T, AL>((w + k * NW_) >> 1, (w + k * NW_) & 1, dvacc[k], gnn, gtn, sSc2, dvp, a.sg.t,
+                                         t0 + TT, a.T, vpart);
             }
-        __syncthreads();
+        }
         if constexpr (SCN)
             if (jr + 1 < j1) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
         if constexpr (MT2)  // X and Y are read after the next barrier
@@ -2911,8 +2990,15 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
             store_ut<T, SP>(sUT, sw, Ut, cst, po);
             __syncthreads();  // all waves' P_K, W, U rows in LDS
             // two token blocks: the next tile's rows go to the other block now
-            // (its last readers finished before this tile's first barrier)
-            if constexpr (NB == 2) commit((int)((jr + 1) & 1));
+            // (its last readers finished before this tile's first barrier);
+            // P2: its V and dO rows (the dV tiles of tile j + 1 read them
+            // before this barrier), then the loads of tile j - 2's
+            if constexpr (P2) {
+                commit_vg((jr + 1) & 1);
+                issue_vg((int64_t)max(jr - 2, j0) * TT);
+            } else if constexpr (NB == 2) {
+                commit((int)((jr + 1) & 1));
+            }
             // ---- dA = -W G/(A+eps), G[s][t] = sum_d B_start[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
             if constexpr (!GN) {
                 Frag<T> Bf[2];
@@ -2986,6 +3072,9 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                 tsum += softhash_combine<KB, T, SP, NTH, PR>(sShare, sSpK, sSmK, sThK, z, a.L, a.inv_temp, sDproj);
             }
         }
+        // P2: tile j - 1's projections (its Q and K rows arrived in the second
+        // phase), for the next iteration
+        if constexpr (P2) project2((jr + 1) & 1, (jr + 1) & 1);
         // one token block: the next tile's rows go to it after the tile's
         // last barrier.  The tile's dK is stored in the next iteration (or
         // after the loop).
