@@ -201,7 +201,7 @@ int race_prefix_mean_bwd(const float *w, const float *v, const float *gE,
  *     the array; an explicit seg_tiles is used as given (results are then
  *     bit-identical to race_fwd with the same descriptor).
  *   - A call whose scratch would exceed the array (fp32 or K > 4 inputs write
- *     per-slice fp32 partial outputs of nslice * M*B*H * T * D * 4 bytes)
+ *     per-slice partial outputs of nslice * M*B*H * T * D * element-size bytes)
  *     returns RACE_E_UNSUPPORTED and names the bytes it needs.
  *   - Every call on one GPU shares that GPU's array: calls that overlap on
  *     one GPU (concurrent streams or threads) race and must be serialised by

@@ -45,7 +45,7 @@ constexpr int64_t kTargetBlocksBwd = 512;
 
 struct Plan {
     int SP = 0, S = 0, R = 0, nslice = 1, Spad = 0;
-    bool parts = false;  // fp32 partial outputs + slice sum (sliced<T, KB>() instantiations)
+    bool parts = false;  // partial outputs + slice sum (sliced<T, KB>() instantiations)
     int64_t N = 0, ntiles = 0;
     int nseg = 0, tps = 0;
     int fnseg = 0, fmul = 1;  // forward segments; forward segments per segment of this plan
@@ -134,7 +134,7 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
     }
     p.bws_core = 2 * (size_t)p.N * p.nseg * blk * sizeof(float) +
                  align16(2 * (size_t)p.N * p.nseg * p.nslice * sizeof(float));
-    p.part_bytes = p.parts ? (size_t)p.nslice * p.N * d->T * D * sizeof(float) : 0;
+    p.part_bytes = p.parts ? align16((size_t)p.nslice * p.N * d->T * D * p.esize) : 0;
     p.xpart_bytes = p.parts ? align16((size_t)p.nslice * p.N * d->T * xcols_of(p.SP, d->K) * p.esize) : 0;
     p.fws = p.fws_core + p.part_bytes;                         // partial O
     p.bws = p.bws_core + 2 * p.xpart_bytes + p.part_bytes;     // dproj columns for dQ, dK; partial dV
@@ -226,9 +226,9 @@ int launched(const char *what) {
 bool run_phase(const race_desc *d, int ph) { return d->phases == 0 || (d->phases & ph); }
 
 template <typename T>
-void slice_sum(const Plan &p, const race_desc *d, const float *part, const int64_t *st, void *out, hipStream_t s) {
+void slice_sum(const Plan &p, const race_desc *d, const void *part, const int64_t *st, void *out, hipStream_t s) {
     const int64_t n4 = p.N * d->T * (D / 4);
-    k_slice_sum<T><<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(part, p.nslice, p.N, d->T, (int)d->B, (int)d->H,
+    k_slice_sum<T><<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>((const T *)part, p.nslice, p.N, d->T, (int)d->B, (int)d->H,
                                                                 Strides{st[0], st[1], st[2], st[3]}, (T *)out);
 }
 
@@ -341,7 +341,7 @@ template <typename T, int SP, int KB> int gn_fwd_impl(const race_desc *d, const 
         if (sliced<T, KB>()) {
             const int64_t n4 = p.N * d->T * (D / 4);
             k_slice_sum_gn<T><<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(
-                a.opart, a.denpart, p.nslice, p.N, d->T, (int)d->B, (int)d->H, strides_of(d->o_stride), (T *)a.out,
+                (const T *)a.opart, a.denpart, p.nslice, p.N, d->T, (int)d->B, (int)d->H, strides_of(d->o_stride), (T *)a.out,
                 a.den, d->eps);
         }
     }
@@ -482,7 +482,7 @@ int bwd_args(const race_desc *d, const Plan &p, const void *q, const void *k, co
         float *part = (float *)((char *)ws + p.bws_core);
         a.dqpart = part;
         a.dkpart = (char *)part + p.xpart_bytes;
-        a.dvpart = (float *)((char *)part + 2 * p.xpart_bytes);
+        a.dvpart = (char *)part + 2 * p.xpart_bytes;
     }
     return RACE_OK;
 }
@@ -609,7 +609,7 @@ int race_fwd(const race_desc *d, const void *q, const void *k, const void *v, co
     a.out = out;
     a.fstate = (double *)state;
     a.fdelta = (double *)ws;
-    a.opart = p.parts ? (float *)((char *)ws + p.fws_core) : nullptr;
+    a.opart = p.parts ? (void *)((char *)ws + p.fws_core) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     if (d->dtype == RACE_DTYPE_BF16) return fwd_dispatch<bf16>(d, p, a, s);
     return fwd_dispatch<float>(d, p, a, s);
@@ -700,7 +700,7 @@ int race_fwd_ex(const race_desc *d, const void *q, const void *k, const void *v,
     a.den = den;
     a.fstate = (double *)state;
     a.fdelta = (double *)ws;
-    a.opart = p.parts ? (float *)((char *)ws + p.fws_core) : nullptr;
+    a.opart = p.parts ? (void *)((char *)ws + p.fws_core) : nullptr;
     a.denpart = p.parts && den ? (float *)((char *)ws + p.fws) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     if (d->dtype == RACE_DTYPE_BF16) return fwd_dispatch<bf16>(d, p, a, s);
@@ -760,7 +760,7 @@ int race_fwd_global(const race_desc *d, const void *q, const void *k, const void
     a.den = den;
     a.fstate = (double *)state;
     a.fdelta = (double *)ws;
-    a.opart = p.parts ? (float *)((char *)ws + p.fws_core) : nullptr;
+    a.opart = p.parts ? (void *)((char *)ws + p.fws_core) : nullptr;
     a.denpart = p.parts ? (float *)((char *)ws + p.fws) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     if (d->dtype == RACE_DTYPE_BF16) return gn_fwd_dispatch<bf16>(d, p, a, s);
@@ -802,7 +802,7 @@ int race_bwd_global(const race_desc *d, const void *q, const void *k, const void
         float *part = (float *)((char *)ws + p.bws_core);
         a.dqpart = part;
         a.dkpart = (char *)part + p.xpart_bytes;
-        a.dvpart = (float *)((char *)part + 2 * p.xpart_bytes);
+        a.dvpart = (char *)part + 2 * p.xpart_bytes;
     }
     a.out = const_cast<void *>(out);  // read only (the GN per-token terms)
     a.den = const_cast<float *>(den);
@@ -889,7 +889,7 @@ int race_fwd_noalloc(const race_desc *d, const void *q, const void *k, const voi
     a.out = out;
     a.fstate = (double *)base;
     a.fdelta = (double *)((char *)base + align256(p.state_bytes));
-    a.opart = p.parts ? (float *)((char *)a.fdelta + p.fws_core) : nullptr;
+    a.opart = p.parts ? (void *)((char *)a.fdelta + p.fws_core) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     if (d->dtype == RACE_DTYPE_BF16) return fwd_dispatch<bf16>(&dd, p, a, s);
     return fwd_dispatch<float>(&dd, p, a, s);

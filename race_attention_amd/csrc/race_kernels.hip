@@ -68,8 +68,9 @@ struct Args {
     float *rdelta;   // [N][nseg][Spad][D+1]  per-segment (U, alpha) sums
     float *rstate;   // [N][nseg][Spad][D+1]  exclusive suffixes (non-causal: totals)
     float *tpart;    // [2][N][nseg][nslice] partial sums of dU*th
-    // sliced() instantiations: per-slice fp32 partial outputs [nslice][N][T][D], summed by k_slice_sum
-    float *opart, *dvpart;
+    // sliced() instantiations: per-slice partial outputs [nslice][N][T][D] in the element type (bf16 or
+    // fp32), summed in fp32 by k_slice_sum
+    void *opart, *dvpart;
     // sliced dX outputs (dQ, dK; the probability backward's dx): each slice's
     // dproj columns, T [nslice][N][T][xcols], multiplied by planes^T and
     // summed over slices by k_dx_finish
@@ -96,8 +97,9 @@ constexpr int WB = 16;       // buckets per wave
 __host__ __device__ constexpr int threads_of(int SP) { return 64 * (SP / WB); }
 
 // Instantiations that may run several bucket slices (fp32, and bf16 with more
-// than 4 hash bits) write fp32 partial outputs; the others write the outputs
-// directly and never read blockIdx.z.
+// than 4 hash bits) write partial outputs in the element type, summed in fp32
+// by k_slice_sum; the others write the outputs directly and never read
+// blockIdx.z.
 template <typename T, int KB> __host__ __device__ constexpr bool sliced() {
     return !std::is_same<T, bf16>::value || KB > 4;
 }
@@ -222,11 +224,11 @@ __device__ __forceinline__ uint32_t tile_off(int t, int64_t st, int d, int esize
     return ((uint32_t)t * (uint32_t)st + (uint32_t)d) * (uint32_t)esize;
 }
 
-// Element (t, d) of the tile at t0 of a [T][D] fp32 partial block (bucket
+// Element (t, d) of the tile at t0 of a [T][D] partial block (bucket
 // slices): a uniform tile base and a 32-bit lane offset that stays the same
 // on every tile.
-__device__ __forceinline__ float *part_at(float *part, int64_t t0, int t, int d) {
-    return at_bytes(part + t0 * D, (uint32_t)(t * D + d) * (uint32_t)sizeof(float));
+template <typename P> __device__ __forceinline__ P *part_at(P *part, int64_t t0, int t, int d) {
+    return at_bytes(part + t0 * D, (uint32_t)(t * D + d) * (uint32_t)sizeof(P));
 }
 
 template <int B> struct ChunkOf;
@@ -1681,7 +1683,7 @@ template <typename T, int SP, bool CAUSAL, bool GN> struct FwdOutL {
 template <typename T, int SP, bool CAUSAL, bool GN = false, bool AL = false, class NL = NatL<T, true>,
           bool VNAT = is_bf16<T>()>
 __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T *Wts, const T *sVt, T *op,
-                             int64_t st, int64_t t0, int64_t Tn, float *part, const float *sDen = nullptr,
+                             int64_t st, int64_t t0, int64_t Tn, T *part, const float *sDen = nullptr,
                              float *den = nullptr, float eps = 0.f) {
     constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
@@ -1720,7 +1722,7 @@ __device__ void fwd_out_tile(int md, int nt, const T *sBT, const T *Pts, const T
     }
     if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
-            store4<float>(part_at(part, t0, t, 16 * md + 4 * g), O);
+            store4<T>(part_at(part, t0, t, 16 * md + 4 * g), O);
         else
             buf_st4<T>(tile_rsrc(tile_ptr(op, st, t0), st, AL ? (int64_t)TT : Tn - t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T)), O);
     }
@@ -1769,7 +1771,7 @@ template <typename T, int SP> __device__ void fwd_out_partial2(int md, const T *
 }
 template <typename T, int SP, bool GN, bool AL = false, class NL = NatL<T, true>, bool VNAT = is_bf16<T>()>
 __device__ void fwd_out_final(int md, int nt, f32x4 O, const T *sVt, const T *sc, T *op, int64_t st, int64_t t0,
-                              int64_t Tn, float *part, const float *sDen, float *den, float eps) {
+                              int64_t Tn, T *part, const float *sDen, float *den, float eps) {
     constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
     mma(O, col_operand<T, NL, VNAT>(sVt, sVt, md), ld_frag_pi(sc + (16 * nt + i) * LDT));
@@ -1788,7 +1790,7 @@ __device__ void fwd_out_final(int md, int nt, f32x4 O, const T *sVt, const T *sc
     }
     if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
-            store4<float>(part_at(part, t0, t, 16 * md + 4 * g), O);
+            store4<T>(part_at(part, t0, t, 16 * md + 4 * g), O);
         else
             buf_st4<T>(tile_rsrc(tile_ptr(op, st, t0), st, AL ? (int64_t)TT : Tn - t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T)), O);
     }
@@ -1825,7 +1827,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     const T *kp = (const T *)a.k + stream_off(a.sk, n, a.B, a.H);
     const T *vp = (const T *)a.v + stream_off(a.sv, n, a.B, a.H);
     T *op = (T *)a.out + stream_off(a.so, n, a.B, a.H);
-    float *opart = sliced<T, KB>() ? a.opart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
+    T *opart = sliced<T, KB>() ? (T *)a.opart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
     const bool want_den = GN || (!CAUSAL && a.den);
     float *sDen = want_den ? (float *)(smem + Ly::oDen) : nullptr;
     float *denp = !want_den       ? nullptr
@@ -2572,7 +2574,7 @@ template <typename T, int SP> __device__ void sc2_tile(int r, const T *Wts, cons
 template <typename T, int SP, bool CAUSAL, bool AL = false, class NL = NatL<T, true>>
 __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts, const T *sG, const T *sGt, T *dvp,
                         int64_t st,
-                        int64_t t0, int64_t Tn, float *part) {
+                        int64_t t0, int64_t Tn, T *part) {
     constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
     const T *pu = sw_frag_ptr<T, SP>(sUT, 16 * md + i), *pp = sw_frag_ptr<T, SP>(Pts, 16 * nt + i);
@@ -2598,7 +2600,7 @@ __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts
     const int t = 16 * nt + i;
     if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
-            store4<float>(part_at(part, t0, t, 16 * md + 4 * g), acc);
+            store4<T>(part_at(part, t0, t, 16 * md + 4 * g), acc);
         else
             store4<T>(at_bytes(tile_ptr(dvp, st, t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
     }
@@ -2618,14 +2620,14 @@ template <typename T, int SP> __device__ f32x4 dv_part(int md, int nt, const T *
 template <typename T, bool AL = false, class NL = NatL<T, true>>
 __device__ void dv_finish(int md, int nt, f32x4 acc, const T *sG, const T *sGt, const T *sc2, T *dvp, int64_t st,
                           int64_t t0,
-                          int64_t Tn, float *part) {
+                          int64_t Tn, T *part) {
     constexpr int LDT = ldp_of<T>(TT);
     const int g = lg(), i = li();
     mma(acc, col_operand<T, NL>(sG, sGt, md), ld_frag_pi(sc2 + (16 * nt + i) * LDT));
     const int t = 16 * nt + i;
     if ((AL || t < tile_rows(t0, Tn))) {
         if (part)
-            store4<float>(part_at(part, t0, t, 16 * md + 4 * g), acc);
+            store4<T>(part_at(part, t0, t, 16 * md + 4 * g), acc);
         else
             store4<T>(at_bytes(tile_ptr(dvp, st, t0), tile_off(t, st, 16 * md + 4 * g, sizeof(T))), acc);
     }
@@ -2684,7 +2686,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     constexpr int XC = xcols_of(SP, KB);
     T *xpart = sliced<T, KB>() ? (T *)a.dkpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * XC : nullptr;
     const int xc0 = ((z * SP) >> KB) * KB;  // first projection column of the slice's tables
-    float *vpart = sliced<T, KB>() ? a.dvpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
+    T *vpart = sliced<T, KB>() ? (T *)a.dvpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
     const float *rdp = GN ? a.rden + (int64_t)n * a.T : nullptr, *gdp = GN ? a.gden + (int64_t)n * a.T : nullptr;
     const float *kwp = !CAUSAL && a.kw ? a.kw + (int64_t)((n / a.H) % a.B) * a.T : nullptr;
 
@@ -3230,15 +3232,20 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
 }
 
 // Partials are read once: nontemporal loads keep them from displacing other
-// lines in the caches (measured faster).
+// lines in the caches (measured faster).  4 consecutive elements as fp32.
 __device__ __forceinline__ f32x4 part4(const float *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
 }
+__device__ __forceinline__ f32x4 part4(const bf16 *p) {
+    const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+    return f32x4{__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xFFFF0000u), __uint_as_float(u[1] << 16),
+                 __uint_as_float(u[1] & 0xFFFF0000u)};
+}
 
-// Sum of the per-slice fp32 partials [nslice][N][T][D] in slice order,
-// written to the strided output (4 consecutive d per thread).
+// Sum of the per-slice partials [nslice][N][T][D] (element type T) in slice
+// order, in fp32, written to the strided output (4 consecutive d per thread).
 template <typename T>
-__global__ void k_slice_sum(const float *part, int nslice, int64_t N, int64_t Tn, int B, int H, Strides so, T *out) {
+__global__ void k_slice_sum(const T *part, int nslice, int64_t N, int64_t Tn, int B, int H, Strides so, T *out) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over N * T * D/4
     const int64_t per = Tn * (D / 4);
     if (idx >= N * per) return;
@@ -3379,7 +3386,7 @@ __global__ void k_den_sum(const float *denpart, int nslice, int64_t NT, float *d
 // numerator partials) / max(den, eps), den = sum of the slices' den partials
 // [nslice][N][T] (slice order), also written to den [N][T].
 template <typename T>
-__global__ void k_slice_sum_gn(const float *part, const float *denpart, int nslice, int64_t N, int64_t Tn, int B,
+__global__ void k_slice_sum_gn(const T *part, const float *denpart, int nslice, int64_t N, int64_t Tn, int B,
                                int H, Strides so, T *out, float *den, float eps) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over N * T * D/4
     const int64_t per = Tn * (D / 4);

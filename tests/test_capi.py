@@ -114,15 +114,16 @@ def _plan(**kw):
 ])
 def test_sliced_plans(dtype, K, L, M, B, H, T, spad):
     """Bucket counts beyond one workgroup run as slices: the state holds every
-    (padded) bucket, and the workspaces add fp32 per-slice partial outputs
-    (O forward; dQ, dK, dV backward)."""
+    (padded) bucket, and the workspaces add per-slice partial outputs in the
+    element type (O forward; dQ, dK, dV backward)."""
     sb, fw, bw = _plan(dtype=dtype, K=K, L=L, M=M, B=B, H=H, T=T)
     N = M * B * H
     row = spad * 65
     assert sb > 0 and sb % (N * row * 8) == 0
     nseg = sb // (N * row * 8) - 1
     SP = 32 if dtype == _lib.RACE_DTYPE_F32 else 128
-    part = (spad // SP) * N * T * 64 * 4
+    es = 4 if dtype == _lib.RACE_DTYPE_F32 else 2
+    part = -(-((spad // SP) * N * T * 64 * es) // 16) * 16
     assert fw >= N * nseg * row * 8 + part
     # the backward runs between 1 and nseg segments (whole forward segments);
     # dQ and dK go through each slice's dproj columns: SP / 2^K tables of K
@@ -130,7 +131,6 @@ def test_sliced_plans(dtype, K, L, M, B, H, T, spad):
     nslice = spad // SP
     cols = (SP >> K) * K if (1 << K) <= SP else K
     xc = next(c for c in (8, 16, 32) if c >= min(cols, 32))
-    es = 4 if dtype == _lib.RACE_DTYPE_F32 else 2
     xpart = -(-(nslice * N * T * xc * es) // 16) * 16
     lo, hi = 2 * N * row * 4, 2 * N * nseg * row * 4 + 2 * N * nseg * nslice * 4 + 16
     assert lo + part + 2 * xpart <= bw <= hi + part + 2 * xpart
