@@ -115,6 +115,9 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
     p.tps = (int)(tps < p.ntiles ? tps : p.ntiles);
     const int64_t nseg = (p.ntiles + p.tps - 1) / p.tps;
     if (nseg > (1 << 30)) return fail(RACE_E_UNSUPPORTED, "too many segments");
+    if (p.parts && (nseg * p.N + 7) / 8 * 8 * p.nslice > 0x7FFFFFFFll)  // the sliced launches' 1-D grid
+        return fail(RACE_E_UNSUPPORTED, "too many segments x streams x bucket slices (%lld)",
+                    (long long)(nseg * p.N * p.nslice));
     p.nseg = (int)nseg;
     p.fnseg = p.nseg;
     p.esize = d->dtype == RACE_DTYPE_BF16 ? 2 : 4;
@@ -225,6 +228,13 @@ int launched(const char *what) {
 
 bool run_phase(const race_desc *d, int ph) { return d->phases == 0 || (d->phases & ph); }
 
+// Launch grid of the tile kernels (their wg_pos): (nseg, N) unsliced; sliced,
+// 1-D over blocks of 8 (segment, stream) groups times the slices.
+dim3 tile_grid(const Plan &p) {
+    if (!p.parts) return dim3((unsigned)p.nseg, (unsigned)p.N, 1);
+    return dim3((unsigned)(((int64_t)p.nseg * p.N + 7) / 8 * 8 * p.nslice), 1, 1);
+}
+
 template <typename T>
 void slice_sum(const Plan &p, const race_desc *d, const void *part, const int64_t *st, void *out, hipStream_t s) {
     const int64_t n4 = p.N * d->T * (D / 4);
@@ -264,7 +274,7 @@ template <typename T, int SP, int KB> constexpr bool al_compiled() {
 bool whole_tiles(const race_desc *d, const Plan &p) { return d->T % TT == 0 && p.S == p.Spad; }
 
 template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
-    const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
+    const dim3 grid = tile_grid(p);
     constexpr bool ALC = al_compiled<T, SP, KB>();
     const bool al = ALC && whole_tiles(d, p);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
@@ -296,7 +306,7 @@ template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Pla
 
 template <typename T, int SP, int KB>
 int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hipStream_t s) {
-    const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
+    const dim3 grid = tile_grid(p);
     constexpr bool ALC = al_compiled<T, SP, KB>();
     const bool al = ALC && whole_tiles(d, p);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
@@ -331,7 +341,7 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
 // Global normalisation (causal): the F1 reduce and scan kernels, then the GN
 // readout; its den partials (sliced) are summed with the numerators.
 template <typename T, int SP, int KB> int gn_fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
-    const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
+    const dim3 grid = tile_grid(p);
     if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
     const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
@@ -352,7 +362,7 @@ template <typename T, int SP, int KB> int gn_fwd_impl(const race_desc *d, const 
 // (1/max(den, eps) and dL/d den, from out, dout, den, dden) that k_bwd_out reads.
 template <typename T, int SP, int KB>
 int gn_bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_beta, hipStream_t s) {
-    const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
+    const dim3 grid = tile_grid(p);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
         k_bwd_reduce<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) dx_finish<T>(p, d, a.dqpart, a, d->g_stride, a.dq, s);
@@ -415,7 +425,7 @@ template <typename T> int gn_bwd_dispatch(const race_desc *d, const Plan &p, con
 // Bucket probabilities (forward) and dP -> dx (backward)
 template <typename T, int SP, int KB> int probs_impl(const race_desc *d, const Plan &p, Args a, bool bwd,
                                                      float *grad_inv_temp, hipStream_t s) {
-    const dim3 grid(p.nseg, (unsigned)p.N, (unsigned)p.nslice);
+    const dim3 grid = tile_grid(p);
     if (!bwd) {
         k_probs<T, SP, KB, false><<<grid, threads_of(SP), 0, s>>>(a);
         return launched("race_probs");

@@ -98,8 +98,7 @@ __host__ __device__ constexpr int threads_of(int SP) { return 64 * (SP / WB); }
 
 // Instantiations that may run several bucket slices (fp32, and bf16 with more
 // than 4 hash bits) write partial outputs in the element type, summed in fp32
-// by k_slice_sum; the others write the outputs directly and never read
-// blockIdx.z.
+// by k_slice_sum; the others write the outputs directly and run one slice.
 template <typename T, int KB> __host__ __device__ constexpr bool sliced() {
     return !std::is_same<T, bf16>::value || KB > 4;
 }
@@ -116,6 +115,23 @@ __host__ __device__ constexpr int xcols_of(int SP, int KB) {
 __device__ __forceinline__ int64_t stream_off(const Strides &s, int n, int B, int H) {
     const int h = n % H, b = (n / H) % B, m = n / (H * B);
     return (int64_t)m * s.m + (int64_t)b * s.b + (int64_t)h * s.h;
+}
+
+// Workgroup coordinates (segment, stream, bucket slice).  Unsliced launches
+// are (nseg, N).  The bucket slices of one (segment, stream) read the same
+// token tiles, so sliced launches are 1-D with a group's slices 8 workgroups
+// apart: gfx950 hands workgroups to its 8 XCDs round-robin, so the slices of
+// a group share one XCD's L2 and start together.  Groups past nseg * N (the
+// blocks of 8 groups are whole) exit at once.
+struct WgPos {
+    int seg, n, z;
+    bool live;
+};
+__device__ __forceinline__ WgPos wg_pos(int nseg, int N, int nslice, bool sl) {
+    if (!sl) return WgPos{(int)blockIdx.x, (int)blockIdx.y, 0, true};
+    const int L = (int)blockIdx.x, per = 8 * nslice, r = L % per;
+    const int grp = (L / per) * 8 + (r & 7);
+    return WgPos{grp % nseg, grp / nseg, r >> 3, (int64_t)grp < (int64_t)nseg * N};
 }
 
 __host__ __device__ constexpr size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -1436,11 +1452,13 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     T *sK = (T *)(smem + Ly::oK), *sVt0 = (T *)(smem + Ly::oVt);
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
     float *sSig = (float *)(smem + Ly::oSig), *sTok0 = (float *)(smem + Ly::oTok);
-    const int w = wave_id(), i = li(), g = lg(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
+    const WgPos wp = wg_pos(a.nseg, a.M * a.B * a.H, a.nslice, sliced<T, KB>());
+    if (!wp.live) return;
+    const int w = wave_id(), i = li(), g = lg(), sw = WB * w, z = wp.z,
               sg = z * SP + sw;
     const PlaneBlocks pbk(z, SP, KB, a.L, !sliced<T, KB>());  // projection columns of this slice
 
-    const int n = blockIdx.y, seg = blockIdx.x;
+    const int n = wp.n, seg = wp.seg;
     const int m = n / (a.B * a.H);
     const int ntiles = (int)((a.T + TT - 1) / TT);  // the host bounds T by 2^35
     const int j0 = seg * a.tps, j1 = min(ntiles, j0 + a.tps);
@@ -1814,11 +1832,13 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     T *sPl = (T *)(smem + Ly::oPl), *sPlLo = (T *)(smem + Ly::oPlLo);
     float *sSig = (float *)(smem + Ly::oSig);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sSpK = sSig + 2 * TT * LDC, *sSmK = sSig + 3 * TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
+    const WgPos wp = wg_pos(a.nseg, a.M * a.B * a.H, a.nslice, sliced<T, KB>());
+    if (!wp.live) return;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = wp.z,
               sg = z * SP + sw;
     const PlaneBlocks pbk(z, SP, KB, a.L, !sliced<T, KB>());  // projection columns of this slice
 
-    const int n = blockIdx.y, seg = blockIdx.x;
+    const int n = wp.n, seg = wp.seg;
     const int m = n / (a.B * a.H);
     const int ntiles = (int)((a.T + TT - 1) / TT);  // the host bounds T by 2^35
     const int lastv = (int)(a.T - (int64_t)(ntiles - 1) * TT);  // rows of the last tile
@@ -2206,11 +2226,13 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
     float *sSpQ = sSig, *sSmQ = sSig + TT * LDC, *sThQ = sSig + 2 * TT * LDC;
     float *sSpK = sSig + 3 * TT * LDC, *sSmK = sSig + 4 * TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
+    const WgPos wp = wg_pos(a.nseg, a.M * a.B * a.H, a.nslice, sliced<T, KB>());
+    if (!wp.live) return;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = wp.z,
               sg = z * SP + sw;
     const PlaneBlocks pbk(z, SP, KB, a.L, !sliced<T, KB>());  // projection columns of this slice
 
-    const int n = blockIdx.y, seg = blockIdx.x;
+    const int n = wp.n, seg = wp.seg;
     const int m = n / (a.B * a.H);
     const int ntiles = (int)((a.T + TT - 1) / TT);  // the host bounds T by 2^35
     const int lastv = (int)(a.T - (int64_t)(ntiles - 1) * TT);  // rows of the last tile
@@ -2668,11 +2690,13 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     float *sSig = (float *)(smem + Ly::oSig), *sRed = (float *)(smem + Ly::oRed);
     float *sSpK = sSig, *sSmK = sSig + TT * LDC, *sThK = sSig + 2 * TT * LDC;
     float *sSpQ = sSig + 3 * TT * LDC, *sSmQ = sSig + 4 * TT * LDC;
-    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
+    const WgPos wp = wg_pos(a.nseg, a.M * a.B * a.H, a.nslice, sliced<T, KB>());
+    if (!wp.live) return;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = wp.z,
               sg = z * SP + sw;
     const PlaneBlocks pbk(z, SP, KB, a.L, !sliced<T, KB>());  // projection columns of this slice
 
-    const int n = blockIdx.y, seg = blockIdx.x;
+    const int n = wp.n, seg = wp.seg;
     const int m = n / (a.B * a.H);
     const int ntiles = (int)((a.T + TT - 1) / TT);  // the host bounds T by 2^35
     const int lastv = (int)(a.T - (int64_t)(ntiles - 1) * TT);  // rows of the last tile
@@ -3158,10 +3182,12 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
     T *sPlT = (T *)(smem + Ly::oPlT), *sDproj = (T *)(smem + Ly::oDproj);
     float *sSp = (float *)(smem + Ly::oSig), *sSm = sSp + TT * LDC, *sTh = sSp + 2 * TT * LDC;
     float *sRed = (float *)(smem + Ly::oRed), *sShare = (float *)(smem + Ly::oShare);
-    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = sliced<T, KB>() ? (int)blockIdx.z : 0,
+    const WgPos wp = wg_pos(a.nseg, a.M * a.B * a.H, a.nslice, sliced<T, KB>());
+    if (!wp.live) return;
+    const int w = wave_id(), g = lg(), i = li(), sw = WB * w, z = wp.z,
               sg = z * SP + sw;
     const PlaneBlocks pbk(z, SP, KB, a.L, !sliced<T, KB>());  // projection columns of this slice
-    const int n = blockIdx.y, seg = blockIdx.x;
+    const int n = wp.n, seg = wp.seg;
     const int m = n / (a.B * a.H);
     const int ntiles = (int)((a.T + TT - 1) / TT);  // the host bounds T by 2^35
     const int lastv = (int)(a.T - (int64_t)(ntiles - 1) * TT);  // rows of the last tile
