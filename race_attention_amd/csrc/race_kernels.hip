@@ -1926,10 +1926,9 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             issue(j0 + 1);
         }
         constexpr int NQ = (8 + NW_ - 1) / NW_;  // output tiles per wave
-        // 8 waves writing the output directly: half of them take two output
-        // tiles each (fewer LDS operand reads); with fp32 slice partials the
-        // stores are better spread over all waves (measured)
-        constexpr bool OPAIR = NW_ == 8 && !sliced<T, KB>();
+        // 8 waves: half of them take two output tiles each (fewer LDS operand
+        // reads), for the output and for the slices' partials alike
+        constexpr bool OPAIR = NW_ == 8;
         for (int jt = j0; jt < j1; ++jt) {
             const int64_t t0 = (int64_t)jt * TT;
             sVt = vt_of(jt);
