@@ -42,6 +42,17 @@ constexpr int64_t kTargetBlocks = 2048;  // workgroups per forward phase (256 CU
 // constant tables, the first tile's load) over more tiles.  A backward
 // segment is fmul forward segments, so its boundaries are forward ones.
 constexpr int64_t kTargetBlocksBwd = 512;
+// Longest segment, forward or backward, in 32-token tiles (8192 tokens).
+// The bf16 kernels carry B in fp32 MFMA accumulators through a segment:
+// k_fwd_reduce and k_bwd_reduce add tile sums from the segment's start,
+// and k_bwd_out re-derives B(t) by subtracting them from the fp64 state at
+// the segment's end.  Those roundings are relative to the state the walk
+// starts from, while B(t) early in a sequence can be far below it (V with a
+// non-zero mean makes |B| grow linearly in t), so the walk length must not
+// grow with T: long sequences add segments instead.  At 256 tiles the
+// walks' error stays below the bf16 operand rounding of B (measured: dK of
+// the first tokens equals that of one-tile walks; it grows from 512 tiles).
+constexpr int64_t kMaxSegTiles = 256;
 
 struct Plan {
     int SP = 0, S = 0, R = 0, nslice = 1, Spad = 0;
@@ -73,7 +84,15 @@ void slice_plan(int dtype, int K, int S, int &SP, int &nslice) {
     nslice = (S + SP - 1) / SP;
 }
 
-int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
+// Work-items of a 1-D launch: the dispatch packet counts them in 32 bits.
+constexpr int64_t kMaxWorkItems = 0xFFFFFFFFll;
+
+// bwd: the backward's plan (longer segments of whole forward ones, at most
+// kMaxSegTiles); it rejects an explicit seg_tiles above kMaxSegTiles.
+// walks: the automatic plan of a call whose state a backward may walk (every
+// call but the no-allocation forward and the probability outputs) caps its
+// segments at kMaxSegTiles.
+int make_plan(const race_desc *d, Plan &p, bool bwd = false, bool walks = true) {
     if (!d) return fail(RACE_E_INVALID, "descriptor is NULL");
     if (d->dtype != RACE_DTYPE_F32 && d->dtype != RACE_DTYPE_BF16)
         return fail(RACE_E_INVALID, "dtype %d is not RACE_DTYPE_F32 or RACE_DTYPE_BF16", d->dtype);
@@ -105,19 +124,27 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
     p.ntiles = (d->T + TT - 1) / TT;
     int64_t tps;
     if (d->seg_tiles > 0) {
+        if (bwd && d->seg_tiles > kMaxSegTiles)
+            return fail(RACE_E_UNSUPPORTED,
+                        "seg_tiles=%d exceeds %lld tiles: the backward's fp32 walks of the forward state are "
+                        "bounded by the segment length", d->seg_tiles, (long long)kMaxSegTiles);
         tps = d->seg_tiles;
     } else {
         const int64_t per = p.N * p.nslice;  // workgroups per segment index
         int64_t nseg = (kTargetBlocks + per - 1) / per;
         if (nseg > p.ntiles) nseg = p.ntiles;
         tps = (p.ntiles + nseg - 1) / nseg;
+        if (walks && tps > kMaxSegTiles) tps = kMaxSegTiles;
     }
     p.tps = (int)(tps < p.ntiles ? tps : p.ntiles);
     const int64_t nseg = (p.ntiles + p.tps - 1) / p.tps;
     if (nseg > (1 << 30)) return fail(RACE_E_UNSUPPORTED, "too many segments");
-    if (p.parts && (nseg * p.N + 7) / 8 * 8 * p.nslice > 0x7FFFFFFFll)  // the sliced launches' 1-D grid
-        return fail(RACE_E_UNSUPPORTED, "too many segments x streams x bucket slices (%lld)",
-                    (long long)(nseg * p.N * p.nslice));
+    // the tile kernels' grids: (nseg, N) of threads_of(SP)-thread workgroups,
+    // or (sliced) 1-D over whole blocks of 8 (segment, stream) groups x slices
+    const int64_t wgs = p.parts ? (nseg * p.N + 7) / 8 * 8 * p.nslice : nseg;
+    if (wgs * threads_of(p.SP) > kMaxWorkItems)
+        return fail(RACE_E_UNSUPPORTED, "%lld segments x %lld streams x %d bucket slices exceed one launch's 2^32 "
+                    "work-items", (long long)nseg, (long long)p.N, p.nslice);
     p.nseg = (int)nseg;
     p.fnseg = p.nseg;
     p.esize = d->dtype == RACE_DTYPE_BF16 ? 2 : 4;
@@ -127,7 +154,8 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
     if (bwd && d->seg_tiles <= 0) {
         // backward segments of fmul forward ones (one segment when that
         // covers the sequence); explicit seg_tiles keeps the forward's
-        const int64_t m = (int64_t)p.fnseg * p.N * p.nslice / kTargetBlocksBwd;
+        int64_t m = (int64_t)p.fnseg * p.N * p.nslice / kTargetBlocksBwd;
+        if (walks && m > kMaxSegTiles / p.tps) m = kMaxSegTiles / p.tps;
         if (m > 1) {
             const int64_t tb = (int64_t)p.tps * m;
             p.fmul = m < p.fnseg ? (int)m : p.fnseg;
@@ -137,6 +165,10 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false) {
     }
     p.bws_core = 2 * (size_t)p.N * p.nseg * blk * sizeof(float) +
                  align16(2 * (size_t)p.N * p.nseg * p.nslice * sizeof(float));
+    // k_dx_finish runs one 64-lane wave per 64 tokens of a stream
+    if (p.parts && (p.N * ((d->T + 16 * DXF_BLK - 1) / (16 * DXF_BLK)) + 3) / 4 * 256 > kMaxWorkItems)
+        return fail(RACE_E_UNSUPPORTED, "M*B*H*T=%lld token-heads exceed one dX launch's 2^32 work-items",
+                    (long long)(p.N * d->T));
     p.part_bytes = p.parts ? align16((size_t)p.nslice * p.N * d->T * D * p.esize) : 0;
     p.xpart_bytes = p.parts ? align16((size_t)p.nslice * p.N * d->T * xcols_of(p.SP, d->K) * p.esize) : 0;
     p.fws = p.fws_core + p.part_bytes;                         // partial O
@@ -238,7 +270,7 @@ dim3 tile_grid(const Plan &p) {
 template <typename T>
 void slice_sum(const Plan &p, const race_desc *d, const void *part, const int64_t *st, void *out, hipStream_t s) {
     const int64_t n4 = p.N * d->T * (D / 4);
-    k_slice_sum<T><<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>((const T *)part, p.nslice, p.N, d->T, (int)d->B, (int)d->H,
+    k_slice_sum<T><<<elem_blocks(n4), ELEM_THREADS, 0, s>>>((const T *)part, p.nslice, p.N, d->T, (int)d->B, (int)d->H,
                                                                 Strides{st[0], st[1], st[2], st[3]}, (T *)out);
 }
 
@@ -297,7 +329,7 @@ template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Pla
             slice_sum<T>(p, d, a.opart, d->o_stride, a.out, s);
             if (a.den) {
                 const int64_t nt = p.N * d->T;
-                k_den_sum<<<(unsigned)((nt + 255) / 256), 256, 0, s>>>(a.denpart, p.nslice, nt, a.den);
+                k_den_sum<<<elem_blocks(nt), ELEM_THREADS, 0, s>>>(a.denpart, p.nslice, nt, a.den);
             }
         }
     }
@@ -350,7 +382,7 @@ template <typename T, int SP, int KB> int gn_fwd_impl(const race_desc *d, const 
         k_fwd_out<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) {
             const int64_t n4 = p.N * d->T * (D / 4);
-            k_slice_sum_gn<T><<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(
+            k_slice_sum_gn<T><<<elem_blocks(n4), ELEM_THREADS, 0, s>>>(
                 (const T *)a.opart, a.denpart, p.nslice, p.N, d->T, (int)d->B, (int)d->H, strides_of(d->o_stride), (T *)a.out,
                 a.den, d->eps);
         }
@@ -550,8 +582,9 @@ size_t noalloc_need(const Plan &p) { return align256(p.state_bytes) + p.fws; }
 // the segment sums fit the scratch array.  Returns RACE_E_UNSUPPORTED with the
 // bytes needed when even one segment per stream does not fit.
 int noalloc_plan(const race_desc *d, race_desc &dd, Plan &p) {
+    if (!d) return fail(RACE_E_INVALID, "descriptor is NULL");
     dd = *d;
-    int rc = make_plan(&dd, p);
+    int rc = make_plan(&dd, p, false, false);
     if (rc) return rc;
     if (d->seg_tiles <= 0 && noalloc_need(p) > RACE_NOALLOC_SCRATCH_BYTES) {
         // state (nseg + 1 rows) and sums (nseg rows) of N * Spad * (D+1) fp64 each
@@ -561,7 +594,7 @@ int noalloc_plan(const race_desc *d, race_desc &dd, Plan &p) {
                                  ? (int64_t)((RACE_NOALLOC_SCRATCH_BYTES - fixed) / (2 * row)) : 0;
         if (nseg >= 1) {
             dd.seg_tiles = (int32_t)((p.ntiles + nseg - 1) / nseg);
-            if ((rc = make_plan(&dd, p))) return rc;
+            if ((rc = make_plan(&dd, p, false, false))) return rc;
         }
     }
     if (noalloc_need(p) > RACE_NOALLOC_SCRATCH_BYTES)
@@ -640,14 +673,14 @@ int race_bwd(const race_desc *d, const void *q, const void *k, const void *v, co
 
 size_t race_probs_bwd_workspace_bytes(const race_desc *d) {
     Plan p;
-    if (make_plan(d, p) != RACE_OK) return 0;
+    if (make_plan(d, p, false, false) != RACE_OK) return 0;
     ok();
     return probs_ws_core(p) + p.xpart_bytes;
 }
 
 int race_probs(const race_desc *d, const void *x, const float *planes, float *P, void *stream) {
     Plan p;
-    int rc = make_plan(d, p);
+    int rc = make_plan(d, p, false, false);
     if (rc || (rc = check_tensor("x", x, d->q_stride, p.esize, d->T)) || (rc = check_den("P", P))) return rc;
     if (!planes) return fail(RACE_E_INVALID, "planes is NULL");
     Args a = base_args(d, p, planes);
@@ -661,7 +694,7 @@ int race_probs(const race_desc *d, const void *x, const float *planes, float *P,
 int race_probs_bwd(const race_desc *d, const void *x, const float *planes, const float *dP, void *dx,
                    float *grad_inv_temp, void *ws, size_t ws_bytes, void *stream) {
     Plan p;
-    int rc = make_plan(d, p);
+    int rc = make_plan(d, p, false, false);
     if (rc || (rc = check_tensor("x", x, d->q_stride, p.esize, d->T)) || (rc = check_den("dP", dP)) ||
         (rc = check_out("dx", dx, d->g_stride, p.esize, d)))
         return rc;

@@ -141,10 +141,10 @@ template <typename T> constexpr bool is_bf16() { return sizeof(T) == 2; }
 // Register type of A (the per-bucket sum of P_K) walked forward through a
 // segment from its fp64 start value, one fp32 tile total at a time: fp32 for
 // bf16 inputs, fp64 for fp32 inputs.  Each addition of a positive total
-// rounds once, so n tiles bound the relative error by n 2^-24 (3e-5 for the
-// 512-tile backward segments at 2^20 tokens; the rounding errors of a sum of
-// positive terms grow as sqrt(n) in practice), below the 2^-9 of the bf16
-// operands that the quotients P/(A + eps) feed.  The reverse walk of
+// rounds once, so n tiles bound the relative error by n 2^-24 (1.5e-5 for
+// the host's longest segment, 256 tiles, at any T; the rounding errors of a
+// sum of positive terms grow as sqrt(n) in practice), below the 2^-9 of the
+// bf16 operands that the quotients P/(A + eps) feed.  The reverse walk of
 // k_bwd_out subtracts from a segment-end value and stays fp64 for both.
 template <typename T> using CarryA = std::conditional_t<is_bf16<T>(), float, double>;
 
@@ -3267,19 +3267,32 @@ __device__ __forceinline__ f32x4 part4(const bf16 *p) {
                  __uint_as_float(u[1] & 0xFFFF0000u)};
 }
 
+// The element-wise kernels below run a grid-stride loop over their items:
+// their grids are capped at ELEM_BLOCKS workgroups of ELEM_THREADS (one pass
+// below N * T of about 2^26 token-heads), so a launch stays far below the
+// dispatch packet's 2^32 work-items at any size.
+constexpr int ELEM_THREADS = 256;
+constexpr int64_t ELEM_BLOCKS = 1 << 20;
+__host__ __device__ constexpr unsigned elem_blocks(int64_t items) {
+    const int64_t b = (items + ELEM_THREADS - 1) / ELEM_THREADS;
+    return (unsigned)(b < ELEM_BLOCKS ? (b > 0 ? b : 1) : ELEM_BLOCKS);
+}
+
 // Sum of the per-slice partials [nslice][N][T][D] (element type T) in slice
-// order, in fp32, written to the strided output (4 consecutive d per thread).
+// order, in fp32, written to the strided output (4 consecutive d per item).
 template <typename T>
-__global__ void k_slice_sum(const T *part, int nslice, int64_t N, int64_t Tn, int B, int H, Strides so, T *out) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over N * T * D/4
-    const int64_t per = Tn * (D / 4);
-    if (idx >= N * per) return;
-    const int64_t n = idx / per, r = idx % per, t = r / (D / 4);
-    const int d0 = 4 * (int)(r % (D / 4));
-    const int64_t row = (n * Tn + t) * D + d0, zs = N * Tn * D;
-    f32x4 acc = part4(part + row);
-    for (int z = 1; z < nslice; ++z) acc += part4(part + z * zs + row);
-    store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc);
+__global__ __launch_bounds__(ELEM_THREADS) void k_slice_sum(const T *part, int nslice, int64_t N, int64_t Tn, int B,
+                                                            int H, Strides so, T *out) {
+    const int64_t per = Tn * (D / 4), items = N * per;  // over N * T * D/4
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < items;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t n = idx / per, r = idx % per, t = r / (D / 4);
+        const int d0 = 4 * (int)(r % (D / 4));
+        const int64_t row = (n * Tn + t) * D + d0, zs = N * Tn * D;
+        f32x4 acc = part4(part + row);
+        for (int z = 1; z < nslice; ++z) acc += part4(part + z * zs + row);
+        store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc);
+    }
 }
 
 // dX of sliced instantiations: out[n][t][:] = sum over slices z (in order)
@@ -3399,35 +3412,38 @@ __global__ __launch_bounds__(256) void k_dx_finish8(const bf16 *part, int L, con
 }
 
 // den [N][T] = sum of the per-slice partials [nslice][N][T], in slice order.
-__global__ void k_den_sum(const float *denpart, int nslice, int64_t NT, float *den) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= NT) return;
-    float dn = denpart[idx];
-    for (int z = 1; z < nslice; ++z) dn += denpart[z * NT + idx];
-    den[idx] = dn;
+__global__ __launch_bounds__(ELEM_THREADS) void k_den_sum(const float *denpart, int nslice, int64_t NT, float *den) {
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < NT;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        float dn = denpart[idx];
+        for (int z = 1; z < nslice; ++z) dn += denpart[z * NT + idx];
+        den[idx] = dn;
+    }
 }
 
 // Global normalisation, sliced instantiations: out = (sum of the slices'
 // numerator partials) / max(den, eps), den = sum of the slices' den partials
 // [nslice][N][T] (slice order), also written to den [N][T].
 template <typename T>
-__global__ void k_slice_sum_gn(const T *part, const float *denpart, int nslice, int64_t N, int64_t Tn, int B,
-                               int H, Strides so, T *out, float *den, float eps) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over N * T * D/4
-    const int64_t per = Tn * (D / 4);
-    if (idx >= N * per) return;
-    const int64_t n = idx / per, r = idx % per, t = r / (D / 4);
-    const int d0 = 4 * (int)(r % (D / 4));
-    const int64_t row = (n * Tn + t) * D + d0, zs = N * Tn * D, nt = n * Tn + t;
-    f32x4 acc = part4(part + row);
-    float dn = denpart[nt];
-    for (int z = 1; z < nslice; ++z) {
-        acc += part4(part + z * zs + row);
-        dn += denpart[z * N * Tn + nt];
+__global__ __launch_bounds__(ELEM_THREADS) void k_slice_sum_gn(const T *part, const float *denpart, int nslice,
+                                                               int64_t N, int64_t Tn, int B, int H, Strides so, T *out,
+                                                               float *den, float eps) {
+    const int64_t per = Tn * (D / 4), items = N * per;  // over N * T * D/4
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < items;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t n = idx / per, r = idx % per, t = r / (D / 4);
+        const int d0 = 4 * (int)(r % (D / 4));
+        const int64_t row = (n * Tn + t) * D + d0, zs = N * Tn * D, nt = n * Tn + t;
+        f32x4 acc = part4(part + row);
+        float dn = denpart[nt];
+        for (int z = 1; z < nslice; ++z) {
+            acc += part4(part + z * zs + row);
+            dn += denpart[z * N * Tn + nt];
+        }
+        const float rc = 1.0f / fmaxf(dn, eps);
+        store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc * rc);
+        if (d0 == 0) den[nt] = dn;
     }
-    const float rc = 1.0f / fmaxf(dn, eps);
-    store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc * rc);
-    if (d0 == 0) den[nt] = dn;
 }
 
 // grad_inv_temp = sum of all partials, in a fixed order

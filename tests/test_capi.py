@@ -51,19 +51,82 @@ def _desc(**kw):
     return d
 
 
+def _state(N, rows, spad=128):
+    """State bytes: N x rows x spad buckets of 65 fp64 (B, A)."""
+    return N * rows * spad * 65 * 8
+
+
 def test_plan_sizes_c4():
     lib = _lib.load()
     d = _desc()
     sb = lib.race_state_bytes(ctypes.byref(d))
-    # N=8 streams, 256 segments (+1 total), 128 buckets x 65 fp64
-    assert sb == 8 * 257 * 128 * 65 * 8
+    # N=8 streams, 256 segments (+1 total), 128 buckets
+    assert sb == _state(8, 257)
     assert lib.race_fwd_workspace_bytes(ctypes.byref(d)) == 8 * 256 * 128 * 65 * 8
-    # the backward runs 64 segments of 4 forward ones (512 workgroups): (U, alpha)
-    # sums and suffixes fp32, and the [2][N][nseg][nslice] temperature partials
-    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 64 * 128 * 65 * 4 + 2 * 8 * 64 * 4
+    # the backward runs 128 segments of 2 forward ones (1024 workgroups; the
+    # 256-tile segment bound stops the joining there): (U, alpha) sums and
+    # suffixes fp32, and the [2][N][nseg][nslice] temperature partials
+    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 128 * 128 * 65 * 4 + 2 * 8 * 128 * 4
     # an explicit seg_tiles keeps the forward's segmentation in the backward
     d.seg_tiles = 128
     assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 256 * 128 * 65 * 4 + 2 * 8 * 256 * 4
+
+
+def test_segments_bounded_at_long_sequences():
+    """Segments, forward and backward, are at most 256 tiles at any T (this
+    bounds the backward's fp32 walks of the forward state): at T = 2^22 the
+    default plan runs 512 segments per stream instead of 256 of 512 tiles, and
+    the backward keeps them; at 37.5 M tokens (one layer's max-N in 288 GB)
+    4584 segments per stream."""
+    lib = _lib.load()
+    d = _desc(T=1 << 22)
+    assert lib.race_state_bytes(ctypes.byref(d)) == _state(8, 513)
+    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 512 * 128 * 65 * 4 + 2 * 8 * 512 * 4
+    d = _desc(T=37552128)
+    assert lib.race_state_bytes(ctypes.byref(d)) == _state(8, 37552128 // 8192 + 1)
+    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == (2 * 8 * 4584 * 128 * 65 * 4 +
+                                                              -(-2 * 8 * 4584 * 4 // 16) * 16)
+
+
+def test_explicit_segments_above_the_walk_bound_rejected():
+    """An explicit seg_tiles above 256 would lengthen the backward's walks:
+    the backward calls reject it.  A forward alone walks its segments only
+    upwards from an fp64 state row and accepts it, and so do the probability
+    outputs, which walk no state."""
+    lib = _lib.load()
+    d = _desc(seg_tiles=256)
+    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) > 0
+    d = _desc(seg_tiles=257)
+    assert lib.race_state_bytes(ctypes.byref(d)) > 0
+    assert lib.race_fwd_workspace_bytes(ctypes.byref(d)) > 0
+    assert lib.race_probs_bwd_workspace_bytes(ctypes.byref(d)) > 0
+    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 0 and "seg_tiles=257" in _lib.last_error()
+    assert lib.race_bwd_global_workspace_bytes(ctypes.byref(d)) == 0
+    p = ctypes.c_void_p(256)
+    rc = lib.race_bwd(ctypes.byref(d), p, p, p, p, p, p, p, p, p, None, p, 1 << 30, None)
+    assert rc == -2 and "seg_tiles" in _lib.last_error()
+    rc = lib.race_bwd_ex(ctypes.byref(d), p, p, p, p, None, p, None, p, p, p, p, None, p, 1 << 30, None)
+    assert rc == -2 and "seg_tiles" in _lib.last_error()
+
+
+def test_launch_grid_bound_in_work_items():
+    """A launch counts its work-items in 32 bits (the dispatch packet's grid
+    size): a plan whose tile grid would exceed 2^32 - 1 work-items is rejected
+    before any launch -- here 16.8 M sliced workgroups of 512 threads from an
+    explicit one-tile segmentation."""
+    lib = _lib.load()
+    d = _desc(K=8, L=4, M=1, B=1, H=64, T=1 << 20, seg_tiles=1)
+    assert lib.race_state_bytes(ctypes.byref(d)) == 0 and "2^32 work-items" in _lib.last_error()
+    rc = lib.race_fwd(ctypes.byref(d), None, None, None, None, None, None, None, 0, None)
+    assert rc == -2 and "2^32 work-items" in _lib.last_error()
+    d = _desc(K=8, L=4, M=1, B=1, H=64, T=1 << 20, seg_tiles=16)   # 1/16 of the workgroups
+    assert lib.race_state_bytes(ctypes.byref(d)) > 0
+
+
+def test_noalloc_null_descriptor_rejected():
+    lib = _lib.load()
+    rc = lib.race_fwd_noalloc(None, None, None, None, None, None, None)
+    assert rc == -1 and "descriptor is NULL" in _lib.last_error()
 
 
 def test_device_temperature_skips_host_value_check():
@@ -119,8 +182,8 @@ def test_sliced_plans(dtype, K, L, M, B, H, T, spad):
     sb, fw, bw = _plan(dtype=dtype, K=K, L=L, M=M, B=B, H=H, T=T)
     N = M * B * H
     row = spad * 65
-    assert sb > 0 and sb % (N * row * 8) == 0
-    nseg = sb // (N * row * 8) - 1
+    assert sb > 0 and sb % _state(N, 1, spad) == 0
+    nseg = sb // _state(N, 1, spad) - 1
     SP = 32 if dtype == _lib.RACE_DTYPE_F32 else 128
     es = 4 if dtype == _lib.RACE_DTYPE_F32 else 2
     part = -(-((spad // SP) * N * T * 64 * es) // 16) * 16
