@@ -156,6 +156,14 @@ CASES = [
     ("causal_fp32_K3L5_pad", dict(T=90, H=1, L=5, K=3, dtype=torch.float32, unit=False), True, 0.5, 0),
     ("noncausal_fp32_K5L3", dict(T=100, H=1, L=3, K=5, dtype=torch.float32, unit=False), False, 1.0, 2),
     ("causal_fp32_K8L2_16slices", dict(T=70, H=1, L=2, K=8, dtype=torch.float32, unit=False), True, 0.5, 0),
+    # Whole tiles (T a multiple of 32, every bucket real) run the unguarded
+    # whole-tile kernels; with an explicit seg_tiles the backward keeps the
+    # forward's segments, so these walk several backward segments with carries
+    # and prefetches across segment edges and a short last segment: K=8
+    # (33 tiles in 9 segments, the last of one tile) and K=4 (32 tiles in
+    # 11 segments, the last of two).
+    ("causal_bf16_K8L4_whole_seg4", dict(T=1056, H=2, L=4, K=8), True, None, 4),
+    ("causal_bf16_K4L8_whole_seg3", dict(T=1024, H=2, L=8, K=4), True, None, 3),
 ]
 
 

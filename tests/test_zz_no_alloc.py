@@ -3,8 +3,9 @@ device array (no caller workspace or state), against race_fwd through the C
 ABI: two calls in a row on one GPU (the second with a smaller input, so it
 runs on whatever the first left in the array), bit-identical to race_fwd with
 the same segmentation and within the bf16 bar of the oracle; the automatic
-segmentation coarsened to fit the array; fp32 with per-slice partial outputs
-in the array; and the size rejection (CPU)."""
+segmentation coarsened to fit the array; fp32 and bf16 K=8 with per-slice
+partial outputs in the array; replays of a captured HIP graph; and the size
+rejection (CPU)."""
 import ctypes
 import math
 
@@ -59,6 +60,71 @@ def test_noalloc_two_calls_match_race_fwd(dev):
         e = relerr(to64(out_na.cpu()), ref)
         print(f"[noalloc T={T} H={H}] out vs oracle {e:.2e}", flush=True)
         assert e <= TOL[torch.bfloat16]
+
+
+@pytest.mark.gpu
+def test_noalloc_two_calls_bf16_slices(dev):
+    """bf16 with 8-bit hashes (K=8, L=4: 1024 buckets in 8 slices) writes its
+    bf16 partial outputs into the array too: two calls in a row, the second
+    smaller, bit-identical to race_fwd with the same segmentation (explicit:
+    the default one's state and sums for 1024 buckets would exceed the array,
+    which the no-allocation forward answers with longer segments) and within
+    the bf16 bar of the oracle."""
+    for T, H, seg, seed in ((1500, 2, 8, 3), (600, 1, 4, 4)):
+        L, K = 4, 8
+        q, k, v, do, planes = make_case(B=1, T=T, H=H, L=L, K=K, seed=seed)
+        it = 1.0 / math.sqrt(64)
+        qd, kd, vd = [x.to(dev) for x in (q, k, v)]
+        pd = planes.to(dev).float().contiguous()
+        out_na, out = _both(qd, kd, vd, pd, L, K, True, it, seg)
+        print(f"[noalloc K=8 T={T} H={H} seg_tiles={seg}] bit-identical={torch.equal(out_na, out)}", flush=True)
+        assert torch.equal(out_na, out)
+        ref = run_oracle(q, k, v, do, planes, causal=True, inv_temp=it)[0]
+        e = relerr(to64(out_na.cpu()), ref)
+        print(f"[noalloc K=8 T={T} H={H}] out vs oracle {e:.2e}", flush=True)
+        assert e <= TOL[torch.bfloat16]
+
+
+@pytest.mark.gpu
+def test_noalloc_graph_capture_replays(dev):
+    """race_fwd_noalloc captured into a HIP graph (torch.cuda.CUDAGraph) after
+    one warm-up call, which looks the array's address up outside the capture:
+    three replays, each on new input values copied into the captured tensors
+    with eager work and a synchronisation before and after, are bit-identical
+    to race_fwd on the same inputs."""
+    from race_attention_amd import _lib
+    lib = _lib.load()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    L, K, T, H, it = 8, 4, 2000, 2, 0.125
+    q, k, v, _, planes = make_case(B=1, T=T, H=H, L=L, K=K, seed=41)
+    qd, kd, vd = [x.to(dev).contiguous() for x in (q, k, v)]
+    pd = planes.to(dev).float().contiguous()
+    out = torch.empty_like(qd)
+    d = _desc(qd, pd, L, K, True, it, 0)
+
+    def call():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(lib.race_fwd_noalloc(ctypes.byref(d), P(qd), P(kd), P(vd), P(pd), P(out), st),
+                   "race_fwd_noalloc")
+
+    call()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        gen = torch.Generator(device=dev).manual_seed(100 + rep)
+        for x in (qd, kd, vd):
+            x.copy_(torch.nn.functional.normalize(torch.randn(x.shape, device=dev, generator=gen), dim=-1))
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        _, ref = _both(qd, kd, vd, pd, L, K, True, it, 0)
+        print(f"[noalloc graph replay {rep}] bit-identical={torch.equal(got, ref)}", flush=True)
+        assert torch.equal(got, ref)
 
 
 @pytest.mark.gpu
