@@ -371,15 +371,26 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
 }
 
 // Global normalisation (causal): the F1 reduce and scan kernels, then the GN
-// readout; its den partials (sliced) are summed with the numerators.
+// readout; its den partials (sliced) are summed with the numerators.  Whole
+// tiles run the whole-tile instantiations, as F1 does.
 template <typename T, int SP, int KB> int gn_fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
     const dim3 grid = tile_grid(p);
-    if (run_phase(d, RACE_PHASE_REDUCE)) k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
+    constexpr bool ALC = al_compiled<T, SP, KB>();
+    // the segment sums are F1's (the same kernel): its whole-tile instantiation where it applies
+    if (run_phase(d, RACE_PHASE_REDUCE)) {
+        if (ALC && whole_tiles(d, p))
+            k_fwd_reduce<T, SP, KB, ALC><<<grid, threads_of(SP), 0, s>>>(a);
+        else
+            k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
+    }
     const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
         k_fwd_scan<<<dim3((elems + SCAN_THREADS - 1) / SCAN_THREADS, (unsigned)p.N), SCAN_THREADS, 0, s>>>(a.fstate, a.fdelta, p.nseg, elems);
     if (run_phase(d, RACE_PHASE_OUT)) {
-        k_fwd_out<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
+        if (ALC && whole_tiles(d, p))
+            k_fwd_out<T, SP, true, KB, true, ALC><<<grid, threads_of(SP), 0, s>>>(a);
+        else
+            k_fwd_out<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) {
             const int64_t n4 = p.N * d->T * (D / 4);
             k_slice_sum_gn<T><<<elem_blocks(n4), ELEM_THREADS, 0, s>>>(
@@ -395,15 +406,23 @@ template <typename T, int SP, int KB> int gn_fwd_impl(const race_desc *d, const 
 template <typename T, int SP, int KB>
 int gn_bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_beta, hipStream_t s) {
     const dim3 grid = tile_grid(p);
+    constexpr bool ALC = al_compiled<T, SP, KB>();
+    const bool al = ALC && whole_tiles(d, p);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
-        k_bwd_reduce<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
+        if (al)
+            k_bwd_reduce<T, SP, true, KB, true, ALC><<<grid, threads_of(SP), 0, s>>>(a);
+        else
+            k_bwd_reduce<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) dx_finish<T>(p, d, a.dqpart, a, d->g_stride, a.dq, s);
     }
     const int elems = p.Spad * SROW;
     if (run_phase(d, RACE_PHASE_SCAN))
         k_bwd_scan<<<dim3((elems + SCAN_THREADS - 1) / SCAN_THREADS, (unsigned)p.N), SCAN_THREADS, 0, s>>>(a.rstate, a.rdelta, p.nseg, elems, 1);
     if (run_phase(d, RACE_PHASE_OUT)) {
-        k_bwd_out<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
+        if (al)
+            k_bwd_out<T, SP, true, KB, true, ALC><<<grid, threads_of(SP), 0, s>>>(a);
+        else
+            k_bwd_out<T, SP, true, KB, true><<<grid, threads_of(SP), 0, s>>>(a);
         if (sliced<T, KB>()) {
             dx_finish<T>(p, d, a.dkpart, a, d->g_stride, a.dk, s);
             slice_sum<T>(p, d, a.dvpart, d->g_stride, a.dv, s);

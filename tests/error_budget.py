@@ -1,0 +1,200 @@
+"""bf16 error budget of the causal RACE operator: which roundings of the bf16
+kernels (race_attention_amd/csrc/race_kernels.hip) account for the error of
+out, dQ, dK and dV against the exact operator.
+
+A numpy fp64 restatement of the tile algorithm the kernels run (32-token
+tiles; the chunked forward and backward of the survey's Appendix B, i.e. the
+recurrence of kernels/cpu/race_pref.cpp:36-220 cut into tiles), in which every
+value the kernels round to bf16 passes through a switchable rounding:
+
+  P      P_K as an MFMA operand: every sum over tokens of P_K (A, B, the
+         in-tile triangles, dV) uses bf16 P_K (P_Q stays fp32 until it is
+         part of W);
+  W      W = P_Q / (A(t) + eps) as an operand (outputs, U, dP_K, Sc, Sc2);
+  B      the carried B_s at a tile start as an operand (O's carried part, G);
+  U      the carried U_s at a tile end as an operand (dP_K's v.U, dV);
+  tri    the in-tile 32 x 32 blocks Sc = tril(W P_K^T), Sc2 = triu(P_K W^T)
+         and M = tril(v g^T), stored or taken as bf16;
+  dproj  d(projection) rows (bf16 in LDS) and planes^T (bf16) in dX = dproj
+         planes;
+  out    the bf16 rounding of the outputs themselves (out, dQ, dK, dV).
+
+Everything else is exact here: the fp32-accurate projection (hi/lo split of
+the planes), the sigmoid factors, A's fp64 carries, fp32 accumulation (far
+below 2^-9), the softmax backward's hi/lo table sums.  The kernels' carries of
+B in fp32 are also taken as exact (their walk error is bounded by the segment
+length, see race_capi.hip kMaxSegTiles).
+
+With every rounding off the restatement equals the oracle (tests/
+test_error_budget.py pins it there).  `python tests/error_budget.py [T]`
+prints the error of each rounding alone and of all together; with --gpu (on a
+GPU) also the HIP operator's own error on the same inputs.
+"""
+from __future__ import annotations
+
+import itertools
+import sys
+
+import numpy as np
+
+TT = 32
+ROUNDINGS = ("P", "W", "B", "U", "tri", "dproj", "out")
+
+
+def bf16(x: np.ndarray) -> np.ndarray:
+    """Round to the nearest bf16 (ties to even), via fp32."""
+    x32 = np.ascontiguousarray(x, dtype=np.float32)
+    u = x32.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def corners(K: int) -> np.ndarray:
+    """c[r, k] = +1 iff bit (K-1-k) of r is set (itertools.product order, misc/race.py:54-58)."""
+    return np.array([[1.0 if (r >> (K - 1 - k)) & 1 else -1.0 for k in range(K)] for r in range(1 << K)])
+
+
+def soft_hash(x, planes, it):
+    """x [T, D], planes [L, K, D] -> P [T, L*R], th [T, L*K] (th = tanh(x . w))."""
+    L, K, D = planes.shape
+    th = np.tanh(x @ planes.reshape(L * K, D).T)
+    u = th.reshape(-1, L, K) * it
+    logits = np.einsum("tlk,rk->tlr", u, corners(K))
+    logits -= logits.max(-1, keepdims=True)
+    P = np.exp(logits)
+    P /= P.sum(-1, keepdims=True)
+    return P.reshape(x.shape[0], -1), th
+
+
+def soft_hash_bwd(P, dP, th, planes, it):
+    """dX [T, D] from dP [T, L*R] through the softmax over corners, tanh and the projection."""
+    L, K, D = planes.shape
+    P3, dP3 = P.reshape(-1, L, 1 << K), dP.reshape(-1, L, 1 << K)
+    dlog = P3 * (dP3 - (P3 * dP3).sum(-1, keepdims=True))
+    du = np.einsum("tlr,rk->tlk", dlog, corners(K)).reshape(-1, L * K)
+    return du * it * (1.0 - th * th)
+
+
+def stream(q, k, v, g, planes, it, eps, on=()):
+    """One causal stream: q, k, v, g [T, D] (bf16-valued fp64), planes [L, K, D].
+    Returns out, dq, dk, dv [T, D] with the roundings named in `on` applied."""
+    r = {name: (bf16 if name in on else (lambda x: x)) for name in ROUNDINGS}
+    T, D = q.shape
+    L, K, _ = planes.shape
+    PQ, thq = soft_hash(q, planes, it)
+    PK, thk = soft_hash(k, planes, it)
+    PKr = r["P"](PK)
+    S = PK.shape[1]
+    nt = (T + TT - 1) // TT
+    A0 = np.zeros((nt, S))      # A, B at each tile start (exact carries)
+    B0 = np.zeros((nt, S, D))
+    out = np.zeros((T, D))
+    W = np.zeros((T, S))
+    Wr = np.zeros((T, S))
+    Ac = np.zeros(S)
+    Bc = np.zeros((S, D))
+    for c in range(nt):
+        a, b = c * TT, min(T, c * TT + TT)
+        A0[c], B0[c] = Ac, Bc
+        pk, vv = PKr[a:b], v[a:b]
+        At = Ac + np.cumsum(pk, 0)                                   # A_s(t), t in the tile
+        W[a:b] = PQ[a:b] / (At + eps)
+        w = r["W"](W[a:b])
+        Wr[a:b] = w
+        Sc = r["tri"](np.tril(w @ pk.T))                             # Sc[t, t'] = sum_s W P_K, t' <= t
+        out[a:b] = w @ r["B"](Bc) + Sc @ vv
+        Bc = Bc + pk.T @ vv
+        Ac = Ac + pk.sum(0)
+    dq_proj = np.zeros((T, L * K))
+    dk_proj = np.zeros((T, L * K))
+    dv = np.zeros((T, D))
+    Uc = np.zeros((S, D))
+    alc = np.zeros(S)
+    for c in reversed(range(nt)):
+        a, b = c * TT, min(T, c * TT + TT)
+        pk, vv, gg, w = PKr[a:b], v[a:b], g[a:b], Wr[a:b]
+        At = A0[c] + np.cumsum(pk, 0)
+        inv = 1.0 / (At + eps)
+        M = r["tri"](np.triu(vv @ gg.T))                             # M[tau, t] = v_tau . g_t, tau <= t
+        G = gg @ r["B"](B0[c]).T + M.T @ pk                           # G[t, s] = g_t . B_s(t)
+        dPQ = G * inv
+        dA = -W[a:b] * dPQ                                            # fp32 W (Wi = W / (A + eps))
+        alpha = alc + np.cumsum(dA[::-1], 0)[::-1]                    # suffix from tau on
+        Ur = r["U"](Uc)
+        dPK = alpha + vv @ Ur.T + M @ w                               # sum_{t >= tau} M[tau, t] W[t, s]
+        Sc2 = r["tri"](np.triu(pk @ w.T))                             # Sc2[tau, t] = sum_s P_K W, t >= tau
+        dv[a:b] = pk @ Ur + Sc2 @ gg
+        Uc = Uc + w.T @ gg
+        alc = alc + dA.sum(0)
+        dq_proj[a:b] = soft_hash_bwd(PQ[a:b], dPQ, thq[a:b], planes, it)
+        dk_proj[a:b] = soft_hash_bwd(PK[a:b], dPK, thk[a:b], planes, it)
+    pl = planes.reshape(L * K, D)
+    dq = r["dproj"](dq_proj) @ r["dproj"](pl)
+    dk = r["dproj"](dk_proj) @ r["dproj"](pl)
+    return tuple(r["out"](x) for x in (out, dq, dk, dv))
+
+
+def run(q, k, v, g, planes, it, eps=1e-6, on=()):
+    """[M,B,T,H,D] arrays (bf16-valued), planes [1,L,K,D] -> out, dq, dk, dv of the same shape."""
+    res = [np.zeros_like(q) for _ in range(4)]
+    M, B, T, H, D = q.shape
+    for m, bb, h in itertools.product(range(M), range(B), range(H)):
+        o = stream(q[m, bb, :, h], k[m, bb, :, h], v[m, bb, :, h], g[m, bb, :, h], planes[0], it, eps, on)
+        for x, y in zip(res, o):
+            x[m, bb, :, h] = y
+    return tuple(res)
+
+
+def relerr(a, b):
+    return float(np.abs(a - b).max() / (np.abs(b).max() + 1e-30))
+
+
+def inputs(T=1024, H=4, shift=0.0, L=8, K=4, seed=0):
+    """Unit-norm Q, K; V = normalize(N(0,1) + shift); dO N(0,1); all bf16-valued."""
+    rng = np.random.default_rng(seed)
+    nrm = lambda x: x / np.linalg.norm(x, axis=-1, keepdims=True)  # noqa: E731
+    q, k = (bf16(nrm(rng.standard_normal((1, 1, T, H, 64)))) for _ in range(2))
+    v = bf16(nrm(rng.standard_normal((1, 1, T, H, 64)) + shift))
+    g = bf16(rng.standard_normal((1, 1, T, H, 64)))
+    planes = rng.standard_normal((1, L, K, 64)).astype(np.float32).astype(np.float64)
+    return q, k, v, g, planes
+
+
+def gpu_run(q, k, v, g, planes, it, eps=1e-6):
+    """The bf16 HIP operator on the same (bf16-valued) inputs."""
+    import torch
+    from race_attention_amd.functional import race_bwd_raw, race_fwd_raw
+    dev = torch.device("cuda:0")
+    L, K = planes.shape[1], planes.shape[2]
+    t = [torch.from_numpy(x).to(dev, torch.bfloat16) for x in (q, k, v, g)]
+    pd = torch.from_numpy(planes).float().to(dev)
+    out, st = race_fwd_raw(t[0], t[1], t[2], pd, L=L, K=K, causal=True, inv_temp=it, eps=eps)
+    dq, dk, dv, _ = race_bwd_raw(t[0], t[1], t[2], pd, t[3], st, L=L, K=K, causal=True, inv_temp=it, eps=eps)
+    torch.cuda.synchronize()
+    return tuple(x.double().cpu().numpy() for x in (out, dq, dk, dv))
+
+
+def table(T=1024, H=4, shifts=(0.0, 0.5), L=8, K=4, gpu=False):
+    it = 1.0 / 8.0
+    rows = []
+    for shift in shifts:
+        q, k, v, g, planes = inputs(T, H, shift, L, K)
+        exact = run(q, k, v, g, planes, it)
+        for on in [(x,) for x in ROUNDINGS] + [ROUNDINGS]:
+            got = run(q, k, v, g, planes, it, on=on)
+            rows.append((shift, "+".join(on) if len(on) > 1 else on[0],
+                         [relerr(a, b) for a, b in zip(got, exact)]))
+        if gpu:
+            got = gpu_run(q, k, v, g, planes, it)
+            rows.append((shift, "**GPU kernels**", [relerr(a, b) for a, b in zip(got, exact)]))
+    return rows
+
+
+if __name__ == "__main__":
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    T = int(args[0]) if args else 1024
+    print(f"bf16 roundings, causal K=4 L=8 d=64, T={T}, 4 streams; max|a-b|/max|b| against the exact operator")
+    print("| V mean shift | rounding | out | dq | dk | dv |")
+    print("|---|---|---|---|---|---|")
+    for shift, name, e in table(T=T, gpu="--gpu" in sys.argv):
+        print(f"| {shift} | {name} | " + " | ".join(f"{x:.1e}" for x in e) + " |", flush=True)

@@ -71,6 +71,12 @@ CASES = [
     ("gn_bf16_K8L4_seg", dict(T=300, H=1, L=4, K=8), 1.0, 2, 1e-6, True),
     ("gn_fp32_K4L8_4slices", dict(T=140, H=2, L=8, K=4, dtype=torch.float32, unit=False), 1.0, 0, 1e-6, True),
     ("gn_fp32_K8L2_16slices", dict(T=70, H=1, L=2, K=8, dtype=torch.float32, unit=False), 0.5, 0, 1e-6, True),
+    # whole tiles (T a multiple of 32, every bucket real): the unguarded whole-tile kernels, with the default
+    # segmentation and over explicit segments with a short last one
+    ("gn_bf16_K4L8_whole", dict(B=2, T=512, H=2, L=8, K=4), 1.0, 0, 1e-6, True),
+    ("gn_bf16_K4L8_whole_seg3", dict(T=1024, H=2, L=8, K=4), 0.7, 3, 1e-6, True),
+    ("gn_bf16_K8L4_whole_seg4", dict(T=1056, H=2, L=4, K=8), 1.0, 4, 1e-6, True),
+    ("gn_bf16_K8L4_whole_nodden", dict(T=256, H=1, L=4, K=8), 1.0, 0, 1e-6, False),
 ]
 
 
