@@ -968,6 +968,20 @@ __device__ __forceinline__ Frag<T> token_operand(const f32x4 (&X)[2], const Cons
         return token_operand<T>(X, cst);
 }
 
+// fp32-accurate bf16 pair operand of two accumulator tiles (the pi-order pair
+// of frag_acc): hi = each value truncated to its upper 16 bits (exact as
+// bf16, no rounding step), lo = the exact remainder rounded to bf16, so that
+// hi + lo is within 2^-16 of the value.
+__device__ __forceinline__ void frag_acc_hilo(const f32x4 &x0, const f32x4 &x1, Frag<bf16> &hi, Frag<bf16> &lo) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float x = j < 4 ? x0[j] : x1[j - 4];
+        const uint32_t u = __float_as_uint(x) & 0xFFFF0000u;
+        hi.v[j] = __builtin_bit_cast(bf16, (unsigned short)(u >> 16));
+        lo.v[j] = (bf16)(x - __uint_as_float(u));
+    }
+}
+
 // c += A . X^T over the wave's 16 buckets, X a bucket-row tile taken as the B
 // operand (column t, k = s); bf16 runs A . hi + A . lo as one 32-deep product
 // (A duplicated in OpX, X split into its two bf16 parts, hi + lo within
@@ -2414,13 +2428,28 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         // G[s][t] = g_t . B_s(t) = sum_d B[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
         f32x4 dPQ[2], dA[2];
         {
-            const Frag<T> b0 = frag_acc<T>(Bt[0], Bt[1]), b1 = frag_acc<T>(Bt[2], Bt[3]);
+            // The carried B enters G as an fp32-accurate operand pair (hi + lo, for bf16): with values
+            // of non-zero mean, B_s carries a component common to all buckets that the softmax
+            // backward of dQ cancels, so a one-part bf16 B would put 2^-9 of that component into dQ.
+            Frag<T> b0, b1, b0l, b1l;
+            if constexpr (is_bf16<T>()) {
+                frag_acc_hilo(Bt[0], Bt[1], b0, b0l);
+                frag_acc_hilo(Bt[2], Bt[3], b1, b1l);
+            } else {
+                b0 = frag_acc<T>(Bt[0], Bt[1]);
+                b1 = frag_acc<T>(Bt[2], Bt[3]);
+            }
             Frag<T> Xop[2];
             if constexpr (CAUSAL) x_operands<T, NL>(sV, sG, Xop);
             for (int nt = 0; nt < 2; ++nt) {
                 f32x4 G = zero4();
-                mma(G, b0, NL::frag_pi(sG, 16 * nt + i, 0));
-                mma(G, b1, NL::frag_pi(sG, 16 * nt + i, 1));
+                const Frag<T> g0 = NL::frag_pi(sG, 16 * nt + i, 0), g1 = NL::frag_pi(sG, 16 * nt + i, 1);
+                mma(G, b0, g0);
+                mma(G, b1, g1);
+                if constexpr (is_bf16<T>()) {
+                    mma(G, b0l, g0);
+                    mma(G, b1l, g1);
+                }
                 if constexpr (CAUSAL) mma(G, Pf, Xop[nt]);
                 // dP_Q = G/(A+eps); dA = -W G/(A+eps).  GN: dP_Q = G rd + gd A; dA = gd P_Q
                 for (int e = 0; e < 4; ++e) {

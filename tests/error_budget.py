@@ -11,7 +11,9 @@ value the kernels round to bf16 passes through a switchable rounding:
          in-tile triangles, dV) uses bf16 P_K (P_Q stays fp32 until it is
          part of W);
   W      W = P_Q / (A(t) + eps) as an operand (outputs, U, dP_K, Sc, Sc2);
-  B      the carried B_s at a tile start as an operand (O's carried part, G);
+  B      the carried B_s at a tile start as a bf16 operand: O's carried part and
+         the G of k_bwd_out (for dA).  (k_bwd_reduce's G, which feeds dQ, takes
+         B as an fp32-accurate hi + lo pair, so it is never rounded there);
   U      the carried U_s at a tile end as an operand (dP_K's v.U, dV);
   tri    the in-tile 32 x 32 blocks Sc = tril(W P_K^T), Sc2 = triu(P_K W^T)
          and M = tril(v g^T), stored or taken as bf16;
@@ -116,9 +118,9 @@ def stream(q, k, v, g, planes, it, eps, on=()):
         At = A0[c] + np.cumsum(pk, 0)
         inv = 1.0 / (At + eps)
         M = r["tri"](np.triu(vv @ gg.T))                             # M[tau, t] = v_tau . g_t, tau <= t
-        G = gg @ r["B"](B0[c]).T + M.T @ pk                           # G[t, s] = g_t . B_s(t)
-        dPQ = G * inv
-        dA = -W[a:b] * dPQ                                            # fp32 W (Wi = W / (A + eps))
+        tri_g = M.T @ pk                                              # in-tile part of G[t, s] = g_t . B_s(t)
+        dPQ = (gg @ B0[c].T + tri_g) * inv                            # k_bwd_reduce: hi + lo B
+        dA = -W[a:b] * (gg @ r["B"](B0[c]).T + tri_g) * inv           # k_bwd_out: bf16 B; fp32 W
         alpha = alc + np.cumsum(dA[::-1], 0)[::-1]                    # suffix from tau on
         Ur = r["U"](Uc)
         dPK = alpha + vv @ Ur.T + M @ w                               # sum_{t >= tau} M[tau, t] W[t, s]

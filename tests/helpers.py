@@ -16,13 +16,16 @@ TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
 
 
 def make_case(M=1, B=1, T=64, H=2, D=64, L=8, K=4, dtype=torch.bfloat16, seed=0, unit=True,
-              share_planes=True, expand_m=False):
+              share_planes=True, expand_m=False, v_shift=0.0):
     """Seeded Q, K, V, dO [M,B,T,H,D] (dtype, CPU), planes fp32 [NP,L,K,D].
     unit=True row-normalises Q, K, V (configs C2/C4); expand_m builds the M
-    estimators as an expand of one [B,T,H,D] tensor (stride 0 over M)."""
+    estimators as an expand of one [B,T,H,D] tensor (stride 0 over M);
+    v_shift adds a constant to every component of V before the
+    normalisation (values with a mean, whose B sums grow linearly in t)."""
     g = torch.Generator().manual_seed(seed)
     Mi = 1 if expand_m else M
     q, k, v = [torch.randn(Mi, B, T, H, D, generator=g) for _ in range(3)]
+    v = v + v_shift
     if unit:
         q, k, v = [torch.nn.functional.normalize(x, dim=-1) for x in (q, k, v)]
     do = torch.randn(M, B, T, H, D, generator=g)

@@ -77,6 +77,8 @@ CASES = [
     ("gn_bf16_K4L8_whole_seg3", dict(T=1024, H=2, L=8, K=4), 0.7, 3, 1e-6, True),
     ("gn_bf16_K8L4_whole_seg4", dict(T=1056, H=2, L=4, K=8), 1.0, 4, 1e-6, True),
     ("gn_bf16_K8L4_whole_nodden", dict(T=256, H=1, L=4, K=8), 1.0, 0, 1e-6, False),
+    # values with a mean (B grows linearly in t)
+    ("gn_bf16_K4L8_vmean", dict(T=2048, H=2, L=8, K=4, v_shift=0.5), 1.0, 0, 1e-6, True),
 ]
 
 

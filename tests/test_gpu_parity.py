@@ -164,6 +164,13 @@ CASES = [
     # 11 segments, the last of two).
     ("causal_bf16_K8L4_whole_seg4", dict(T=1056, H=2, L=4, K=8), True, None, 4),
     ("causal_bf16_K4L8_whole_seg3", dict(T=1024, H=2, L=8, K=4), True, None, 3),
+    # values with a mean (V = normalize(N(0,1) + 0.5)): B grows linearly in t, the case that exposes walks of
+    # the forward state that are too long, and the one where the bf16 B operand weighs most (error budget)
+    ("causal_bf16_K4L8_vmean", dict(T=2048, H=2, L=8, K=4, v_shift=0.5), True, None, 0),
+    ("causal_bf16_K4L8_vmean_seg256", dict(T=8192, H=1, L=8, K=4, v_shift=0.5), True, None, 256),
+    ("causal_bf16_K8L4_vmean", dict(T=1024, H=2, L=4, K=8, v_shift=0.5), True, None, 0),
+    ("causal_fp32_K4L8_vmean_seg", dict(T=1500, H=1, L=8, K=4, dtype=torch.float32, v_shift=0.5), True, None, 40),
+    ("noncausal_bf16_K4L8_vmean", dict(T=600, H=2, L=8, K=4, v_shift=0.5), False, 1.0, 0),
 ]
 
 
