@@ -170,7 +170,8 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false, bool walks = true) 
         return fail(RACE_E_UNSUPPORTED, "M*B*H*T=%lld token-heads exceed one dX launch's 2^32 work-items",
                     (long long)(p.N * d->T));
     p.part_bytes = p.parts ? align16((size_t)p.nslice * p.N * d->T * D * p.esize) : 0;
-    p.xpart_bytes = p.parts ? align16((size_t)p.nslice * p.N * d->T * xcols_of(p.SP, d->K) * p.esize) : 0;
+    const size_t xesize = xpart_f32(d->dtype == RACE_DTYPE_BF16, p.SP, d->K) ? sizeof(float) : p.esize;
+    p.xpart_bytes = p.parts ? align16((size_t)p.nslice * p.N * d->T * xcols_of(p.SP, d->K) * xesize) : 0;
     p.fws = p.fws_core + p.part_bytes;                         // partial O
     p.bws = p.bws_core + 2 * p.xpart_bytes + p.part_bytes;     // dproj columns for dQ, dK; partial dV
     p.tok_bytes = align16((size_t)p.N * d->T * sizeof(float));
@@ -281,10 +282,11 @@ void dx_finish(const Plan &p, const race_desc *d, const void *part, const Args &
                hipStream_t s) {
     const int64_t waves = p.N * ((d->T + 16 * DXF_BLK - 1) / (16 * DXF_BLK));  // one wave per 64 tokens
     if constexpr (std::is_same<T, bf16>::value) {
-        // 8-bit hashes, slices of 128 buckets: two slices per table, 8 columns each
-        if (d->K == 8 && p.SP == 128 && xcols_of(p.SP, d->K) == 8 && d->L <= 4 && p.nslice == 2 * d->L) {
+        // 8-bit hashes, slices of 128 buckets: two slices per table, 8 fp32
+        // columns each (the plan gives L <= 4 and 2L slices whenever this holds)
+        if (xpart_f32(true, p.SP, d->K)) {
             k_dx_finish8<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(
-                (const bf16 *)part, d->L, a.planes, a.planes_m_stride, (int)d->B, (int)d->H, p.N, d->T,
+                (const float *)part, d->L, a.planes, a.planes_m_stride, (int)d->B, (int)d->H, p.N, d->T,
                 Strides{st[0], st[1], st[2], st[3]}, (bf16 *)out);
             return;
         }

@@ -72,8 +72,8 @@ struct Args {
     // fp32), summed in fp32 by k_slice_sum
     void *opart, *dvpart;
     // sliced dX outputs (dQ, dK; the probability backward's dx): each slice's
-    // dproj columns, T [nslice][N][T][xcols], multiplied by planes^T and
-    // summed over slices by k_dx_finish
+    // dproj columns, [nslice][N][T][xcols] in the element type (fp32 where
+    // xpart_f32), multiplied by planes^T and summed over slices by k_dx_finish
     void *dqpart, *dkpart;
     // global normalisation (GN instantiations; eps is the floor of den):
     // den [N][T] output (sliced: per-slice partials denpart [nslice][N][T]);
@@ -112,6 +112,13 @@ __host__ __device__ constexpr int xcols_of(int SP, int KB) {
     return m <= 8 ? 8 : (m <= 16 ? 16 : 32);
 }
 
+// bf16 tables wider than a slice (8-bit hashes in 128-bucket slices: two
+// slices per table) split each (token, bit)'s du between two slices, whose
+// partial sums can cancel.  Those slices keep their d(projection) partials in
+// fp32 (8 columns, 32 bytes a token) and k_dx_finish8 adds a table's two
+// slices before any rounding.
+__host__ __device__ constexpr bool xpart_f32(bool bf, int SP, int KB) { return bf && (1 << KB) > SP; }
+
 __device__ __forceinline__ int64_t stream_off(const Strides &s, int n, int B, int H) {
     const int h = n % H, b = (n / H) % B, m = n / (H * B);
     return (int64_t)m * s.m + (int64_t)b * s.b + (int64_t)h * s.h;
@@ -138,6 +145,16 @@ __host__ __device__ constexpr size_t align16(size_t x) { return (x + 15) & ~(siz
 __host__ __device__ constexpr size_t cmax(size_t a, size_t b) { return a > b ? a : b; }
 
 template <typename T> constexpr bool is_bf16() { return sizeof(T) == 2; }
+
+// (slice z, stream n)'s [T][xcols] block of a sliced dX partial buffer
+template <typename T, int SP, int KB> __device__ __forceinline__ void *xpart_at(void *base, int z, int64_t n, const Args &a) {
+    const int64_t off = ((int64_t)z * a.M * a.B * a.H + n) * a.T * xcols_of(SP, KB);
+    if constexpr (xpart_f32(is_bf16<T>(), SP, KB))
+        return (float *)base + off;
+    else
+        return (T *)base + off;
+}
+
 // Register type of A (the per-bucket sum of P_K) walked forward through a
 // segment from its fp64 start value, one fp32 tile total at a time: fp32 for
 // bf16 inputs, fp64 for fp32 inputs.  Each addition of a positive total
@@ -1089,7 +1106,11 @@ __device__ float softhash_combine(const float *share, const float *sp, const flo
             const float th = sth[t * LDC + col];
             const float du = sx - sd * corner_tanh<PAIR>(sp, sm, t, col);
             tsum += du * th;
-            dproj[sw_off<T, NCOL>(t, col)] = from_f32<T>(du * inv_temp * (1.f - th * th));
+            const float dp = du * inv_temp * (1.f - th * th);
+            if constexpr (xpart_f32(is_bf16<T>(), SP, KB))
+                reinterpret_cast<float *>(dproj)[t * 8 + k] = dp;  // the slice's one table: [TT][8] fp32
+            else
+                dproj[sw_off<T, NCOL>(t, col)] = from_f32<T>(dp);
         }
     }
     return tsum;
@@ -1353,10 +1374,21 @@ template <typename T> __device__ void zero_lds(T *p, int n, int nth) {
 // stored straight to rows t0.. (< T) of dst.
 // part != nullptr (bucket slices): this slice's dproj columns c0 .. c0 + XC - 1
 // instead, rows t0.. of a [T][XC] block -- the product with planes^T and the
-// sum over slices happen in k_dx_finish, on the same operand values.
-template <typename T, int NW_, int XC = 8, bool AL = false>
-__device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64_t t0, int64_t Tn, T *part,
+// sum over slices happen in k_dx_finish, on the same operand values.  XF: the
+// rows are fp32 ([TT][8] at dproj's start, softhash_combine), copied as they are.
+template <typename T, int NW_, int XC = 8, bool AL = false, bool XF = false>
+__device__ void dx_store(const T *dproj, const T *plt, T *dst, int64_t st, int64_t t0, int64_t Tn, void *vpart,
                          int c0 = 0) {
+    if constexpr (XF) {
+        static_assert(XC == 8, "fp32 dproj partials are 8-column rows");
+        // two lanes a token, 16 bytes each: the tile's rows are 1 KB of contiguous partials
+        const int l = threadIdx.x, t = l >> 1;
+        if (l < 2 * TT && (AL || t < tile_rows(t0, Tn)))
+            *reinterpret_cast<f32x4 *>(at_bytes((float *)vpart + t0 * 8, (uint32_t)l * 16u)) =
+                *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(dproj) + 4 * l);
+        return;
+    }
+    T *part = (T *)vpart;
     if (part) {
         if constexpr (is_bf16<T>() && XC == 8) {
             if ((c0 & 7) == 0) {
@@ -2256,7 +2288,8 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     const T *gp = (const T *)a.dout + stream_off(a.sdo, n, a.B, a.H);
     T *dqp = (T *)a.dq + stream_off(a.sg, n, a.B, a.H);
     constexpr int XC = xcols_of(SP, KB);
-    T *xpart = sliced<T, KB>() ? (T *)a.dqpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * XC : nullptr;
+    constexpr bool XF = xpart_f32(is_bf16<T>(), SP, KB);
+    void *xpart = sliced<T, KB>() ? xpart_at<T, SP, KB>(a.dqpart, z, n, a) : nullptr;
     const int xc0 = ((z * SP) >> KB) * KB;  // first projection column of the slice's tables
     float *sTok = (float *)(smem + Ly::oTok);
     const T *op = GN ? (const T *)a.out + stream_off(a.so, n, a.B, a.H) : nullptr;
@@ -2374,7 +2407,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         __syncthreads();
         if constexpr (NB == 2) {
             issue();
-            if (jt > j0) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
+            if (jt > j0) dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
         }
         if constexpr (GN) gn_token_terms<T, NL, NW_>(sG, sO, sTokIn, sTok, a.eps, rdw, gdw, t0, a.T);
         for (int q = w; q < (CAUSAL ? 2 : 1) * pbk.tasks(); q += NW_) {
@@ -2390,7 +2423,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         // softmax backward left in LDS, after the projections (they overlap);
         // the next write of sDproj is a barrier away
         if constexpr (NB == 1)
-            if (jt > j0) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
+            if (jt > j0) dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2], tot;
         Frag<T> Pf;
@@ -2498,7 +2531,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     }
     if (j0 < j1) {
         if constexpr (NB == 2) __syncthreads();  // every wave's dproj rows of the last tile
-        dx_store<T, NW_, XC, AL>(sDproj, sPlT, dqp, a.sg.t, (int64_t)(j1 - 1) * TT, a.T, xpart, xc0);
+        dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dqp, a.sg.t, (int64_t)(j1 - 1) * TT, a.T, xpart, xc0);
     }
     float *out = a.rdelta + ((int64_t)n * a.nseg + seg) * a.Spad * SROW;
     for (int md = 0; md < 4; ++md)
@@ -2736,7 +2769,8 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     T *dkp = (T *)a.dk + stream_off(a.sg, n, a.B, a.H);
     T *dvp = (T *)a.dv + stream_off(a.sg, n, a.B, a.H);
     constexpr int XC = xcols_of(SP, KB);
-    T *xpart = sliced<T, KB>() ? (T *)a.dkpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * XC : nullptr;
+    constexpr bool XF = xpart_f32(is_bf16<T>(), SP, KB);
+    void *xpart = sliced<T, KB>() ? xpart_at<T, SP, KB>(a.dkpart, z, n, a) : nullptr;
     const int xc0 = ((z * SP) >> KB) * KB;  // first projection column of the slice's tables
     T *vpart = sliced<T, KB>() ? (T *)a.dvpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * D : nullptr;
     const float *rdp = GN ? a.rden + (int64_t)n * a.T : nullptr, *gdp = GN ? a.gden + (int64_t)n * a.T : nullptr;
@@ -2944,7 +2978,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
             // projections, with two (below) beside the probabilities, after the
             // second barrier; the next write of sDproj is after the third
             if constexpr (!SCN)
-                if (jr + 1 < j1) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
+                if (jr + 1 < j1) dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
             // causal, two token blocks: dV of that tile too, its carried part
             // (computed last iteration) plus the in-tile part from its Sc2 rows and
             // its dO tile (still in its block: the next commit there is after this
@@ -2978,7 +3012,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
             }
         }
         if constexpr (SCN)
-            if (jr + 1 < j1) dx_store<T, NW_, XC, AL>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
+            if (jr + 1 < j1) dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dkp, a.sg.t, t0 + TT, a.T, xpart, xc0);
         if constexpr (MT2)  // X and Y are read after the next barrier
             for (int q = w; q < 3; q += NW_) m_tile_xy<T, NL>(q, sV, sG, sX, sY);
         f32x4 PKraw[2], PKr[2];  // fp32 P_K (kept for the softmax backward), operand-rounded P_K
@@ -3139,7 +3173,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     }
     if (j0 < j1) {
         if constexpr (NB == 2) __syncthreads();  // every wave's dproj (and Sc2) rows of the last tile
-        dx_store<T, NW_, XC, AL>(sDproj, sPlT, dkp, a.sg.t, (int64_t)j0 * TT, a.T, xpart, xc0);
+        dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dkp, a.sg.t, (int64_t)j0 * TT, a.T, xpart, xc0);
         if constexpr (SCN) {
             const T *gtn = (const T *)(smem + (j0 & 1) * Ly::TB + Ly::oGt);
             const T *gnn = (const T *)(smem + (j0 & 1) * Ly::TB + Ly::oG);
@@ -3223,7 +3257,8 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
     const T *xp = (const T *)a.q + stream_off(a.sq, n, a.B, a.H);
     T *dxp = BWD ? (T *)a.dq + stream_off(a.sg, n, a.B, a.H) : nullptr;
     constexpr int XC = xcols_of(SP, KB);
-    T *xpart = BWD && sliced<T, KB>() ? (T *)a.dqpart + ((int64_t)z * a.M * a.B * a.H + n) * a.T * XC : nullptr;
+    constexpr bool XF = xpart_f32(is_bf16<T>(), SP, KB);
+    void *xpart = BWD && sliced<T, KB>() ? xpart_at<T, SP, KB>(a.dqpart, z, n, a) : nullptr;
     const int xc0 = ((z * SP) >> KB) * KB;  // first projection column of the slice's tables
 
     HashOps<T, KB> ho;
@@ -3276,7 +3311,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
                 tsum += softhash_combine<KB, T, SP, NTH>(sShare, sSp, sSm, sTh, z, a.L, a.inv_temp, sDproj);
             }
             __syncthreads();
-            dx_store<T, NW_, XC>(sDproj, sPlT, dxp, a.sg.t, t0, a.T, xpart, xc0);
+            dx_store<T, NW_, XC, false, XF>(sDproj, sPlT, dxp, a.sg.t, t0, a.T, xpart, xc0);
         }
     }
     if constexpr (BWD) {
@@ -3385,12 +3420,14 @@ __global__ __launch_bounds__(256) void k_dx_finish(const T *part, int nslice, in
 }
 
 // dX for bf16 8-bit hashes in slices of 128 buckets: two slices per table
-// (slice z holds table z >> 1's 8 columns, one 16-byte row per token), at
-// most 4 tables.  Lane (g, i) takes token i and table g's columns, from slice
-// 2g in one product and slice 2g + 1 in a second, so a 16-wide d block costs
-// two products instead of one per slice (fp32 accumulation as above; the
-// tables' sums meet inside each product).
-__global__ __launch_bounds__(256) void k_dx_finish8(const bf16 *part, int L, const float *planes,
+// (slice z holds table z >> 1's 8 columns as fp32 rows, 32 bytes a token), at
+// most 4 tables.  Lane (g, i) takes token i and table g's columns: the sum of
+// slices 2g and 2g + 1 in fp32 (partials that may cancel, added before any
+// rounding), as an fp32-accurate hi + lo bf16 pair (frag_acc_hilo), against
+// planes^T rounded to bf16 as in the unsliced kernels.  The product is dX^T:
+// lane (g, i) ends with d = 16 md + 4g .. + 3 of token i, one 8-byte store per
+// 16-wide d block (fp32 accumulation; the tables' sums meet inside each product).
+__global__ __launch_bounds__(256) void k_dx_finish8(const float *part, int L, const float *planes,
                                                     int64_t planes_m_stride, int B, int H, int64_t N, int64_t Tn,
                                                     Strides so, bf16 *out) {
     const int64_t wv = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;  // over N * ceil(T / 64)
@@ -3410,32 +3447,25 @@ __global__ __launch_bounds__(256) void k_dx_finish8(const bf16 *part, int L, con
         pt[md] = frag_seq<bf16>(v);
     }
     const int64_t zs = N * Tn * 8;  // elements per slice
+    bf16 *op = out + stream_off(so, (int)n, B, H);
     for (int tb = 0; tb < DXF_BLK; ++tb) {
         const int64_t t0 = tw + 16 * tb;
         if (t0 >= Tn) break;
         const int64_t t = t0 + i;
-        Frag<bf16> ae, ao;
-        ae.v = bf16x8{};
-        ao.v = bf16x8{};
+        f32x4 x0 = zero4(), x1 = zero4();
         if (live && t < Tn) {
-            const bf16 *row = part + 2 * g * zs + (n * Tn + t) * 8;
-            ae = *reinterpret_cast<const Frag<bf16> *>(row);
-            ao = *reinterpret_cast<const Frag<bf16> *>(row + zs);
+            const float *row = part + 2 * g * zs + (n * Tn + t) * 8;
+            x0 = *reinterpret_cast<const f32x4 *>(row) + *reinterpret_cast<const f32x4 *>(row + zs);
+            x1 = *reinterpret_cast<const f32x4 *>(row + 4) + *reinterpret_cast<const f32x4 *>(row + zs + 4);
         }
-        f32x4 acc[4] = {zero4(), zero4(), zero4(), zero4()};
+        Frag<bf16> hi, lo;
+        frag_acc_hilo(x0, x1, hi, lo);
 #pragma unroll
         for (int md = 0; md < 4; ++md) {
-            mma(acc[md], ae, pt[md]);
-            mma(acc[md], ao, pt[md]);
-        }
-        // lane (g, i) holds dX[t0 + 4g + e][16md + i]
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int64_t tt = t0 + 4 * g + e;
-            if (tt < Tn)
-#pragma unroll
-                for (int md = 0; md < 4; ++md)
-                    out[stream_off(so, (int)n, B, H) + tt * so.t + 16 * md + i] = from_f32<bf16>(acc[md][e]);
+            f32x4 acc = zero4();
+            mma(acc, pt[md], hi);
+            mma(acc, pt[md], lo);
+            if (t < Tn) store4<bf16>(op + t * so.t + 16 * md + 4 * g, acc);
         }
     }
 }

@@ -18,8 +18,18 @@ value the kernels round to bf16 passes through a switchable rounding:
   tri    the in-tile 32 x 32 blocks Sc = tril(W P_K^T), Sc2 = triu(P_K W^T)
          and M = tril(v g^T), stored or taken as bf16;
   dproj  d(projection) rows (bf16 in LDS) and planes^T (bf16) in dX = dproj
-         planes;
+         planes (8-bit hashes: the rows reach the product as an fp32-accurate
+         hi + lo pair, so only planes^T rounds there -- taken as the K <= 4 case
+         here, an upper bound);
   out    the bf16 rounding of the outputs themselves (out, dQ, dK, dV).
+
+One more switch is not a rounding of the current kernels: xpart rounds each
+128-bucket slice's partial d(projection) of a table wider than a slice (8-bit
+hashes, two slices per table) to bf16 before the slices are added, as bf16
+partials would.  The partials of a column can cancel (the softmax backward's
+mean term), so that rounding is relative to the partials, not the sum; the
+kernels keep them fp32 for that reason (race_kernels.hip xpart_f32).
+`python tests/error_budget.py --k8` prints the comparison.
 
 Everything else is exact here: the fp32-accurate projection (hi/lo split of
 the planes), the sigmoid factors, A's fp64 carries, fp32 accumulation (far
@@ -41,6 +51,7 @@ import numpy as np
 
 TT = 32
 ROUNDINGS = ("P", "W", "B", "U", "tri", "dproj", "out")
+SLICE = 128  # buckets per bf16 slice
 
 
 def bf16(x: np.ndarray) -> np.ndarray:
@@ -68,19 +79,34 @@ def soft_hash(x, planes, it):
     return P.reshape(x.shape[0], -1), th
 
 
-def soft_hash_bwd(P, dP, th, planes, it):
-    """dX [T, D] from dP [T, L*R] through the softmax over corners, tanh and the projection."""
+def soft_hash_bwd(P, dP, th, planes, it, xpart=None):
+    """d(projection) [T, L*K] from dP [T, L*R] through the softmax over corners
+    and tanh.  xpart (a rounding): tables wider than SLICE buckets are summed
+    from per-slice partials du_z = sum_{r in z} P dP c_r - (sum_{r in z} P dP)
+    tanh(u), each passed through xpart before the slices are added."""
     L, K, D = planes.shape
-    P3, dP3 = P.reshape(-1, L, 1 << K), dP.reshape(-1, L, 1 << K)
-    dlog = P3 * (dP3 - (P3 * dP3).sum(-1, keepdims=True))
-    du = np.einsum("tlr,rk->tlk", dlog, corners(K)).reshape(-1, L * K)
-    return du * it * (1.0 - th * th)
+    R = 1 << K
+    P3, dP3 = P.reshape(-1, L, R), dP.reshape(-1, L, R)
+    dth = it * (1.0 - th * th)
+    if xpart is None or R <= SLICE:
+        dlog = P3 * (dP3 - (P3 * dP3).sum(-1, keepdims=True))
+        du = np.einsum("tlr,rk->tlk", dlog, corners(K)).reshape(-1, L * K)
+        return du * dth
+    c, tu = corners(K), np.tanh(th.reshape(-1, L, K) * it)
+    out = np.zeros((P.shape[0], L, K))
+    for z in range(R // SLICE):
+        sl = slice(z * SLICE, (z + 1) * SLICE)
+        pd = P3[:, :, sl] * dP3[:, :, sl]
+        du = np.einsum("tlr,rk->tlk", pd, c[sl]) - pd.sum(-1, keepdims=True) * tu
+        out += xpart(du * dth.reshape(-1, L, K))
+    return out.reshape(-1, L * K)
 
 
 def stream(q, k, v, g, planes, it, eps, on=()):
     """One causal stream: q, k, v, g [T, D] (bf16-valued fp64), planes [L, K, D].
     Returns out, dq, dk, dv [T, D] with the roundings named in `on` applied."""
     r = {name: (bf16 if name in on else (lambda x: x)) for name in ROUNDINGS}
+    xp = bf16 if "xpart" in on else None
     T, D = q.shape
     L, K, _ = planes.shape
     PQ, thq = soft_hash(q, planes, it)
@@ -128,8 +154,8 @@ def stream(q, k, v, g, planes, it, eps, on=()):
         dv[a:b] = pk @ Ur + Sc2 @ gg
         Uc = Uc + w.T @ gg
         alc = alc + dA.sum(0)
-        dq_proj[a:b] = soft_hash_bwd(PQ[a:b], dPQ, thq[a:b], planes, it)
-        dk_proj[a:b] = soft_hash_bwd(PK[a:b], dPK, thk[a:b], planes, it)
+        dq_proj[a:b] = soft_hash_bwd(PQ[a:b], dPQ, thq[a:b], planes, it, xp)
+        dk_proj[a:b] = soft_hash_bwd(PK[a:b], dPK, thk[a:b], planes, it, xp)
     pl = planes.reshape(L * K, D)
     dq = r["dproj"](dq_proj) @ r["dproj"](pl)
     dk = r["dproj"](dk_proj) @ r["dproj"](pl)
@@ -176,13 +202,13 @@ def gpu_run(q, k, v, g, planes, it, eps=1e-6):
     return tuple(x.double().cpu().numpy() for x in (out, dq, dk, dv))
 
 
-def table(T=1024, H=4, shifts=(0.0, 0.5), L=8, K=4, gpu=False):
+def table(T=1024, H=4, shifts=(0.0, 0.5), L=8, K=4, gpu=False, sets=None):
     it = 1.0 / 8.0
     rows = []
     for shift in shifts:
         q, k, v, g, planes = inputs(T, H, shift, L, K)
         exact = run(q, k, v, g, planes, it)
-        for on in [(x,) for x in ROUNDINGS] + [ROUNDINGS]:
+        for on in sets or [(x,) for x in ROUNDINGS] + [ROUNDINGS]:
             got = run(q, k, v, g, planes, it, on=on)
             rows.append((shift, "+".join(on) if len(on) > 1 else on[0],
                          [relerr(a, b) for a, b in zip(got, exact)]))
@@ -194,9 +220,12 @@ def table(T=1024, H=4, shifts=(0.0, 0.5), L=8, K=4, gpu=False):
 
 if __name__ == "__main__":
     args = [a for a in sys.argv[1:] if not a.startswith("--")]
-    T = int(args[0]) if args else 1024
-    print(f"bf16 roundings, causal K=4 L=8 d=64, T={T}, 4 streams; max|a-b|/max|b| against the exact operator")
+    k8 = "--k8" in sys.argv
+    T = int(args[0]) if args else (512 if k8 else 1024)
+    L, K = (4, 8) if k8 else (8, 4)
+    sets = [("dproj",), ("xpart",), ROUNDINGS, ("xpart",) + ROUNDINGS] if k8 else None
+    print(f"bf16 roundings, causal K={K} L={L} d=64, T={T}, 4 streams; max|a-b|/max|b| against the exact operator")
     print("| V mean shift | rounding | out | dq | dk | dv |")
     print("|---|---|---|---|---|---|")
-    for shift, name, e in table(T=T, gpu="--gpu" in sys.argv):
+    for shift, name, e in table(T=T, L=L, K=K, gpu="--gpu" in sys.argv, sets=sets):
         print(f"| {shift} | {name} | " + " | ".join(f"{x:.1e}" for x in e) + " |", flush=True)

@@ -190,11 +190,13 @@ def test_sliced_plans(dtype, K, L, M, B, H, T, spad):
     assert fw >= N * nseg * row * 8 + part
     # the backward runs between 1 and nseg segments (whole forward segments);
     # dQ and dK go through each slice's dproj columns: SP / 2^K tables of K
-    # columns (K columns of a wider table), rounded up to 8, 16 or 32
+    # columns (K columns of a wider table), rounded up to 8, 16 or 32; bf16
+    # tables wider than a slice (K=8: two slices per table) keep them in fp32
     nslice = spad // SP
     cols = (SP >> K) * K if (1 << K) <= SP else K
     xc = next(c for c in (8, 16, 32) if c >= min(cols, 32))
-    xpart = -(-(nslice * N * T * xc * es) // 16) * 16
+    xes = 4 if (1 << K) > SP else es
+    xpart = -(-(nslice * N * T * xc * xes) // 16) * 16
     lo, hi = 2 * N * row * 4, 2 * N * nseg * row * 4 + 2 * N * nseg * nslice * 4 + 16
     assert lo + part + 2 * xpart <= bw <= hi + part + 2 * xpart
 

@@ -28,3 +28,22 @@ def test_bf16_rounding_is_exact_to_nearest_even():
     assert r[3] == 1.0 + 2 ** -6                  # tie: 1 + 2^-7 is odd, 1 + 2^-6 even
     assert r[4] == 1.0 + 2 ** -7                  # above the tie: up
     assert r[5] == -2.5
+
+
+def test_slice_partials_add_up_to_the_table():
+    """The softmax backward of a 256-bucket table as two 128-bucket slices'
+    partials, du_z = sum_{r in z} P dP c_r - (sum_{r in z} P dP) tanh(u), adds
+    up to the whole table's (sum_r P c_r = tanh(u) over a table): with no
+    rounding of the partials, the two forms agree to fp64 rounding."""
+    rng = np.random.default_rng(3)
+    T, L, K, it = 40, 4, 8, 0.125
+    planes = rng.standard_normal((L, K, 64))
+    x = rng.standard_normal((T, 64))
+    P, th = eb.soft_hash(x, planes, it)
+    dP = rng.standard_normal(P.shape) + 0.5
+    whole = eb.soft_hash_bwd(P, dP, th, planes, it)
+    parts = eb.soft_hash_bwd(P, dP, th, planes, it, xpart=lambda y: y)
+    assert np.abs(parts - whole).max() <= 1e-12 * np.abs(whole).max()
+    # a bf16 rounding of each partial is relative to the partials
+    rounded = eb.soft_hash_bwd(P, dP, th, planes, it, xpart=eb.bf16)
+    assert np.abs(rounded - whole).max() > 0
