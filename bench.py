@@ -137,6 +137,7 @@ class Step:
             _lib.check(-1, "race_state_bytes")
         self.state = torch.empty(sb, dtype=torch.uint8, device=q.device)
         self.ws = torch.empty(max(fw, bw), dtype=torch.uint8, device=q.device)
+        self.sizes = (sb, bw)  # state and backward-workspace bytes (scan_bytes)
         self.git = torch.empty((), dtype=torch.float32, device=q.device)
         self.check = _lib.check
         P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
@@ -340,6 +341,42 @@ def algorithmic_bytes(name, tok_heads, D, esize, mode="f1"):
     return units.get(name, 0) * unit
 
 
+def _a16(x):
+    return (x + 15) // 16 * 16
+
+
+def scan_bytes(state_bytes, bwd_ws_bytes, N, T, L, K, D=64):
+    """HBM bytes of the two bf16 F1 scans, from the library's buffer sizes.
+
+    k_fwd_scan reads the fp64 per-segment sums [N][fnseg][Spad][D+1] and
+    writes the exclusive prefixes [N][fnseg+1][Spad][D+1] (the state);
+    k_bwd_scan reads the fp32 (U, alpha) sums [N][nseg][Spad][D+1] and writes
+    their suffixes, the same size.  The segment counts follow from the sizes:
+    state = N (fnseg+1) Spad (D+1) 8 bytes; backward workspace = 2 N nseg
+    Spad (D+1) 4 + align16(8 N nseg nslice), plus, for bucket slices, the dV
+    partials [nslice][N][T][D] bf16 and the two dQ / dK d(projection) partial
+    buffers [nslice][N][T][8] (fp32 for 8-bit hashes).  Covers the
+    single-slice plans (K <= 4, L 2^K <= 128) and 8-bit hashes; None otherwise.
+    Returns (fwd_scan bytes, bwd_scan bytes, fnseg, nseg)."""
+    S = L << K
+    if K <= 4 and S <= 128:
+        spad = (S + 31) // 32 * 32
+        spad, nslice, parts = (128 if spad == 96 else spad), 1, 0
+    elif K == 8:
+        nslice = -(-S // 128)
+        spad = nslice * 128
+        parts = _a16(nslice * N * T * D * 2) + 2 * _a16(nslice * N * T * 8 * 4)
+    else:
+        return None
+    blk = spad * (D + 1)
+    fnseg = state_bytes // (N * blk * 8) - 1
+    nseg = (bwd_ws_bytes - parts) // (8 * N * blk + 8 * N * nslice)
+    if state_bytes != N * (fnseg + 1) * blk * 8 or \
+            bwd_ws_bytes != 8 * N * nseg * blk + _a16(8 * N * nseg * nslice) + parts:
+        return None
+    return (2 * fnseg + 1) * N * blk * 8, 2 * N * nseg * blk * 4, fnseg, nseg
+
+
 def mfma_figures(ms, tok_heads, D, L, K, workload, T):
     """Matrix-core figures of the aggregation kernel (k_fwd_reduce: the
     segment sums S = P_K^T [V, 1] with the K projection that feeds them).
@@ -521,10 +558,17 @@ def main():
 
     tok_heads = M * B * T * H  # token-streams: each (m, b, h) stream reads its own Q, K, V rows
     kernels = {}
+    sc = scan_bytes(*step.sizes, M * B * H, T, L, K, D) if args.mode == "f1" else None
     for name, t_ms in per.items():
         ab = algorithmic_bytes(name, tok_heads, D, 2, args.mode)
         kernels[name] = {"ms": round(t_ms, 4),
                          "algorithmic_GBs": round(ab / (t_ms * 1e-3) / 1e9, 1) if ab else None}
+        if sc and name in ("fwd_scan", "bwd_scan"):
+            # the scans move segment sums, not token rows: read the sums, write the prefixes
+            nb = sc[0] if name == "fwd_scan" else sc[1]
+            kernels[name].update(segments=sc[2] if name == "fwd_scan" else sc[3], bytes=nb,
+                                 GBs=round(nb / (t_ms * 1e-3) / 1e9, 1),
+                                 frac=round(nb / (t_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
     dom = max(per, key=per.get)
     ab = algorithmic_bytes(dom, tok_heads, D, 2, args.mode)
     achieved = ab / (per[dom] * 1e-3) / 1e9

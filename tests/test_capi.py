@@ -363,3 +363,26 @@ def test_probs_argument_checks():
     assert need == 8 * 2 * 4      # temperature partials: 8 streams x 2 segments (2 tiles), no slices
     rc = lib.race_probs_bwd(ctypes.byref(d), p, p, p, p, None, p, need - 1, None)
     assert rc == -3 and "workspace" in _lib.last_error()
+
+
+@pytest.mark.parametrize("K,L,M,B,H,T,fnseg,nseg", [
+    (4, 8, 1, 1, 8, 1 << 20, 256, 128),   # C4: 256 forward segments of 128 tiles, 128 backward ones of 256
+    (4, 8, 1, 1, 8, 1 << 22, 512, 512),   # every segment at the 256-tile bound
+    (8, 4, 2, 8, 12, 8192, 2, 1),          # C5: 8 slices; 2 forward segments, 1 backward
+    (2, 5, 1, 4, 3, 1000, None, None),     # 20 buckets, one 32-bucket slice
+])
+def test_bench_scan_bytes(K, L, M, B, H, T, fnseg, nseg):
+    """bench.py's scan byte model recovers the plan's segment counts from the
+    library's buffer sizes (the sizes must match its formulas exactly) and
+    counts each scan's reads and writes of segment rows."""
+    import bench
+    sb, _, bw = _plan(dtype=_lib.RACE_DTYPE_BF16, K=K, L=L, M=M, B=B, H=H, T=T)
+    N = M * B * H
+    got = bench.scan_bytes(sb, bw, N, T, L, K)
+    assert got is not None
+    fb, bb, fn, bn = got
+    if fnseg is not None:
+        assert (fn, bn) == (fnseg, nseg)
+    spad = -(-(L << K) // 128) * 128 if K > 4 else (L << K) + (-(L << K)) % 32
+    assert fb == (2 * fn + 1) * N * spad * 65 * 8
+    assert bb == 2 * N * bn * spad * 65 * 4
