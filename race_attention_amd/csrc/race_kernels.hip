@@ -1949,6 +1949,21 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         // rows, barrier, Sc blocks and the carried-state part of O, barrier,
         // then the next tile's rows (Q/K alias the P_K / W rows, now read;
         // V^T goes to the other buffer) and the rest of O.
+        // Whole 4-bit F1 tiles (QKP): every wave's planes are in registers, so
+        // Q and K take the planes' rows instead (same layout and size: NCOL =
+        // TT rows).  The next tile's rows are then committed in the third
+        // phase (this tile's projections are done by then), and the next
+        // tile's projections run at the end of the last phase, after the
+        // output tiles: three barriers per tile (probabilities and rows,
+        // barrier, Sc blocks, carried-state part of O and the next rows'
+        // commit, barrier, the rest of O and the next projections, barrier).
+        constexpr bool QKP = AL && KB == 4 && !GN;
+        static_assert(NCOL == TT, "Q and K rows in the planes' rows");
+        if constexpr (QKP) {
+            sQ = sPl;
+            sK = sPlLo;
+            __syncthreads();  // every wave has read its planes
+        }
         T *sSc = (T *)(smem + Ly::oSc);
         zero_lds<T>(sSc, TT * LDT, NTH);  // its (t < 16 <= t') block stays zero
         auto vt_of = [&](int j) { return (T *)(smem + ((j & 1) ? Ly::oVt2 : Ly::oVt)); };
@@ -1971,6 +1986,19 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             commit(j0);
             issue(j0 + 1);
         }
+        // whole tiles: at most one projection task per wave (Q first), one code path
+        auto project_al = [&]() {
+            if (2 * pbk.tasks() >= NW_ || w < 2 * pbk.tasks()) {
+                const bool isq = w < pbk.tasks();
+                const int r = pbk.task(w);
+                project_tile<T, NL, PR>(isq ? sQ : sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, isq ? sSpQ : sSpK,
+                                        isq ? sSmQ : sSmK, nullptr, &pcw);
+            }
+        };
+        if constexpr (QKP) {
+            __syncthreads();  // the first tile's rows in LDS
+            project_al();
+        }
         constexpr int NQ = (8 + NW_ - 1) / NW_;  // output tiles per wave
         // 8 waves: half of them take two output tiles each (fewer LDS operand
         // reads), for the output and for the slices' partials alike
@@ -1978,16 +2006,13 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         for (int jt = j0; jt < j1; ++jt) {
             const int64_t t0 = (int64_t)jt * TT;
             sVt = vt_of(jt);
-            __syncthreads();  // this tile's rows in LDS; the previous tile's O rows are done
-            if constexpr (AL) {
-                // whole tiles: at most one task per wave (Q first), one code path
-                if (2 * pbk.tasks() >= NW_ || w < 2 * pbk.tasks()) {
-                    const bool isq = w < pbk.tasks();
-                    const int r = pbk.task(w);
-                    project_tile<T, NL, PR>(isq ? sQ : sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp,
-                                            isq ? sSpQ : sSpK, isq ? sSmQ : sSmK, nullptr, &pcw);
-                }
+            if constexpr (QKP) {
+                // this tile's projections ran at the end of the last tile (or before the loop)
+            } else if constexpr (AL) {
+                __syncthreads();  // this tile's rows in LDS; the previous tile's O rows are done
+                project_al();
             } else {
+                __syncthreads();
                 for (int q = w; q < 2 * pbk.tasks(); q += NW_) {
                     const int r = pbk.task(q);
                     if (q < pbk.tasks())
@@ -2057,8 +2082,9 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
             for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, col_operand<T, VL, VNAT>(sVt, sVt, md));
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
+            if constexpr (QKP) commit(jt + 1);  // Q/K rows read by this tile's projections before the second barrier
             __syncthreads();  // Sc rows in LDS; the P_K / W / B rows are read
-            commit(jt + 1);
+            if constexpr (!QKP) commit(jt + 1);
             if (jt + 2 < j1) issue(jt + 2);
             if constexpr (OPAIR) {
                 if (w < 4)
@@ -2066,6 +2092,8 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
                     for (int nt = 0; nt < 2; ++nt)
                         fwd_out_final<T, SP, GN, AL, VL, VNAT>(w, nt, Op[nt], sVt, sSc, op, a.so.t, t0, a.T, opart, sDen,
                                                                denp, a.eps);
+                if constexpr (QKP)
+                    if (jt + 1 < j1) project_al();  // the next tile's rows, committed before the last barrier
             } else {
 #pragma unroll
                 for (int k = 0; k < NQ; ++k) {
