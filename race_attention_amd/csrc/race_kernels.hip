@@ -3222,7 +3222,13 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
 // backward dP -> dx (dq's pointer and strides; sliced instantiations write
 // fp32 partials) with the temperature-gradient partials.
 // =====================================================================
-template <typename T, int SP> struct ProbsL {
+// One layout for both directions, except the end-of-kernel block sum's
+// scratch [64 * NW_]: the backward reuses its sigmoid rows for it (the last
+// tile reads them before its last barrier), which brings it to 4 workgroups
+// per CU (backward 1.52 -> 1.38 ms at C4's shape, K=4); the forward, which has
+// no block sum, keeps a region of that size, since smaller forward layouts (4
+// or 6 workgroups per CU) measured 2.5% slower.
+template <typename T, int SP, bool BWD> struct ProbsL {
     static constexpr int NW_ = SP / WB;
     static constexpr int LDN = NatL<T, true>::LD, LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>();
     static constexpr size_t oX = 0;
@@ -3231,8 +3237,9 @@ template <typename T, int SP> struct ProbsL {
     static constexpr size_t oPlT = align16(oPlLo + sizeof(T) * NCOL * LDN);
     static constexpr size_t oDproj = align16(oPlT + sizeof(T) * D * LDDP);
     static constexpr size_t oSig = align16(oDproj + sizeof(T) * TT * LDDP);  // sp, sm, th
-    static constexpr size_t oRed = align16(oSig + sizeof(float) * 3 * TT * LDC);
-    static constexpr size_t oHash = align16(oRed + sizeof(float) * 64 * NW_);
+    static_assert(64 * NW_ <= 3 * TT * LDC, "block-sum scratch inside the sigmoid rows");
+    static constexpr size_t oRed = BWD ? oSig : align16(oSig + sizeof(float) * 3 * TT * LDC);
+    static constexpr size_t oHash = align16(oSig + sizeof(float) * 3 * TT * LDC + (BWD ? 0 : sizeof(float) * 64 * NW_));
     static constexpr size_t oShare = align16(oHash + HashOps<T, 4>::bytes);
     template <int KB> static constexpr size_t bytes() {
         return align16(oShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
@@ -3264,7 +3271,7 @@ __device__ __forceinline__ f32x4 load_row4(const float *row, int s0, int S) {
 template <typename T, int SP, int KB, bool BWD>
 __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
     if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
-    using Ly = ProbsL<T, SP>;
+    using Ly = ProbsL<T, SP, BWD>;
     using NL = NatL<T, true>;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDC = Ly::LDC, LDDP = Ly::LDDP;
     __shared__ __align__(16) unsigned char smem[Ly::template bytes<KB>()];
