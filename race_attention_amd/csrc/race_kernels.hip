@@ -1949,15 +1949,15 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         // rows, barrier, Sc blocks and the carried-state part of O, barrier,
         // then the next tile's rows (Q/K alias the P_K / W rows, now read;
         // V^T goes to the other buffer) and the rest of O.
-        // Whole 4-bit F1 tiles (QKP): every wave's planes are in registers, so
-        // Q and K take the planes' rows instead (same layout and size: NCOL =
-        // TT rows).  The next tile's rows are then committed in the third
+        // Whole 4-bit tiles (QKP; F1 and the global normalisation): every
+        // wave's planes are in registers, so Q and K take the planes' rows
+        // instead (same layout and size: NCOL = TT rows).  The next tile's rows are then committed in the third
         // phase (this tile's projections are done by then), and the next
         // tile's projections run at the end of the last phase, after the
         // output tiles: three barriers per tile (probabilities and rows,
         // barrier, Sc blocks, carried-state part of O and the next rows'
         // commit, barrier, the rest of O and the next projections, barrier).
-        constexpr bool QKP = AL && KB == 4 && !GN;
+        constexpr bool QKP = AL && KB == 4;
         static_assert(NCOL == TT, "Q and K rows in the planes' rows");
         if constexpr (QKP) {
             sQ = sPl;
