@@ -3459,9 +3459,11 @@ __global__ __launch_bounds__(256) void k_dx_finish(const T *part, int nslice, in
 // most 4 tables.  Lane (g, i) takes token i and table g's columns: the sum of
 // slices 2g and 2g + 1 in fp32 (partials that may cancel, added before any
 // rounding), as an fp32-accurate hi + lo bf16 pair (frag_acc_hilo), against
-// planes^T rounded to bf16 as in the unsliced kernels.  The product is dX^T:
-// lane (g, i) ends with d = 16 md + 4g .. + 3 of token i, one 8-byte store per
-// 16-wide d block (fp32 accumulation; the tables' sums meet inside each product).
+// planes^T rounded to bf16 as in the unsliced kernels.  The product is dX^T,
+// with row r of block md holding d = 4r + md: lane (g, i) ends with
+// d = 16g .. 16g + 15 of token i (acc[md][e] is d = 16g + 4e + md), stored as
+// two 16-byte pieces (fp32 accumulation; the tables' sums meet inside each
+// product).
 __global__ __launch_bounds__(256) void k_dx_finish8(const float *part, int L, const float *planes,
                                                     int64_t planes_m_stride, int B, int H, int64_t N, int64_t Tn,
                                                     Strides so, bf16 *out) {
@@ -3472,13 +3474,13 @@ __global__ __launch_bounds__(256) void k_dx_finish8(const float *part, int L, co
     const int g = lg(), i = li();
     const bool live = g < L;  // table g exists
     const float *pl = planes + (n / (B * H)) * planes_m_stride;
-    // planes^T operand of each 16-wide d block: column c = 8g + j, d = 16md + i
+    // planes^T operand of block md: column c = 8g + j, row i = d 4i + md
     Frag<bf16> pt[4];
 #pragma unroll
     for (int md = 0; md < 4; ++md) {
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = live ? pl[(int64_t)(8 * g + j) * D + 16 * md + i] : 0.f;
+        for (int j = 0; j < 8; ++j) v[j] = live ? pl[(int64_t)(8 * g + j) * D + 4 * i + md] : 0.f;
         pt[md] = frag_seq<bf16>(v);
     }
     const int64_t zs = N * Tn * 8;  // elements per slice
@@ -3495,12 +3497,21 @@ __global__ __launch_bounds__(256) void k_dx_finish8(const float *part, int L, co
         }
         Frag<bf16> hi, lo;
         frag_acc_hilo(x0, x1, hi, lo);
+        f32x4 acc[4];
 #pragma unroll
         for (int md = 0; md < 4; ++md) {
-            f32x4 acc = zero4();
-            mma(acc, pt[md], hi);
-            mma(acc, pt[md], lo);
-            if (t < Tn) store4<bf16>(op + t * so.t + 16 * md + 4 * g, acc);
+            acc[md] = zero4();
+            mma(acc[md], pt[md], hi);
+            mma(acc[md], pt[md], lo);
+        }
+        if (t < Tn) {
+            float v[8];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {  // d = 16g + 8h .. + 7
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = acc[j & 3][2 * h + (j >> 2)];
+                *reinterpret_cast<Frag<bf16> *>(op + t * so.t + 16 * g + 8 * h) = frag_seq<bf16>(v);
+            }
         }
     }
 }
