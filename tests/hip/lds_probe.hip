@@ -6,6 +6,7 @@
 
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef short v4s __attribute__((ext_vector_type(4)));
 
 template <int OP>
 __global__ __launch_bounds__(1024) void lds_probe_kernel(const int *offs, int iters, long long *cyc, unsigned *sink) {
@@ -32,6 +33,10 @@ __global__ __launch_bounds__(1024) void lds_probe_kernel(const int *offs, int it
                 const u32x2 a = *(u32x2 *)p, b = *(u32x2 *)(p + 32);
                 acc ^= a.x ^ a.y ^ b.x ^ b.y;
             }
+            if constexpr (OP == 7) {  // transpose load of 16-bit elements: 8 bytes at p
+                const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)p);
+                acc ^= (unsigned)(unsigned short)v.x ^ ((unsigned)(unsigned short)v.w << 16);
+            }
         }
         asm volatile("" ::: "memory");
     }
@@ -41,7 +46,7 @@ __global__ __launch_bounds__(1024) void lds_probe_kernel(const int *offs, int it
     sink[blockIdx.x * 1024 + threadIdx.x] = acc + lds[threadIdx.x];
 }
 
-// op: 0 r32, 1 r64, 2 r128, 3 w32, 4 w64, 5 w128, 6 pi-order pair read
+// op: 0 r32, 1 r64, 2 r128, 3 w32, 4 w64, 5 w128, 6 pi-order pair read, 7 ds_read_tr16_b64
 extern "C" int lds_probe(int op, const int *offs_dev, int iters, long long *cyc_dev, unsigned *sink_dev) {
     switch (op) {
     case 0: lds_probe_kernel<0><<<1, 1024>>>(offs_dev, iters, cyc_dev, sink_dev); break;
@@ -51,6 +56,7 @@ extern "C" int lds_probe(int op, const int *offs_dev, int iters, long long *cyc_
     case 4: lds_probe_kernel<4><<<1, 1024>>>(offs_dev, iters, cyc_dev, sink_dev); break;
     case 5: lds_probe_kernel<5><<<1, 1024>>>(offs_dev, iters, cyc_dev, sink_dev); break;
     case 6: lds_probe_kernel<6><<<1, 1024>>>(offs_dev, iters, cyc_dev, sink_dev); break;
+    case 7: lds_probe_kernel<7><<<1, 1024>>>(offs_dev, iters, cyc_dev, sink_dev); break;
     default: return -1;
     }
     return hipDeviceSynchronize() == hipSuccess ? 0 : -2;

@@ -84,3 +84,25 @@ def pi_row_store(nt, mt):
 def transposed_word_store(cw, q):
     """PrefetchT transposed commit: row 4c + q (c = (l & 3) + 4 cw), word tp = (l >> 2) & 15"""
     return [2 * ((4 * ((l & 3) + 4 * cw) + q) * PI_PITCH) + 4 * ((l >> 2) & 15) for l in range(64)]
+
+
+# ---- LDS transpose loads (ds_read_b64_tr_b16): lane (g, p) reads 4 elements,
+# columns c0 + 4(p & 3) of row 4g + (p >> 2), and row 16 + ... for the
+# operand's second half (race_kernels.hip col_operand, ts_operand_tr)
+TR_PITCH = D + 16  # natural token rows read only by transpose loads (race_kernels.hip TrL::LD)
+
+
+def tr_col_read(md, half, pitch_elems=TR_PITCH):
+    """col_operand: natural token rows, columns 16 md + 4(p & 3)"""
+    return lanes(lambda g, p: 2 * ((4 * g + (p >> 2) + half) * pitch_elems + 16 * md + 4 * (p & 3)))
+
+
+def tr_ts_read(n, sw, half):
+    """ts_operand_tr: swizzled [t][s] rows of n buckets, columns sw + 4(p & 3)"""
+    return lanes(lambda g, p: 2 * elem(n, 4 * g + (p >> 2) + half, sw + 4 * (p & 3)))
+
+
+def rebased(offs):
+    """the same banks inside the probe's 8 KiB slot (banks repeat every 256 bytes)"""
+    m = min(offs) // 256 * 256
+    return [o - m for o in offs]

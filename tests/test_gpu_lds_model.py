@@ -24,8 +24,8 @@ from lds_model import R128_PASSES, ways  # noqa: E402
 pytestmark = [pytest.mark.gpu, pytest.mark.timing]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-OPS = {"r32": 0, "r64": 1, "r128": 2, "w32": 3, "w64": 4, "w128": 5, "rpi": 6}
-SIZE = {"r32": 4, "r64": 8, "r128": 16, "w32": 4, "w64": 8, "w128": 16, "rpi": 8}
+OPS = {"r32": 0, "r64": 1, "r128": 2, "w32": 3, "w64": 4, "w128": 5, "rpi": 6, "rtr": 7}
+SIZE = {"r32": 4, "r64": 8, "r128": 16, "w32": 4, "w64": 8, "w128": 16, "rpi": 8, "rtr": 8}
 
 
 class Probe:
@@ -113,3 +113,24 @@ def test_kernel_patterns_measured(probe):
     for name, op, offs in old:
         assert ways(op, offs) >= 2
         assert probe.ratio(op, offs) > 1.3, name
+
+
+def test_transpose_load_patterns(probe):
+    """ds_read_b64_tr_b16 serves 32 lanes per pass (measured: lanes 0-31 share
+    one).  The kernels' two transpose-load operands -- col_operand over the
+    natural token rows (pitch D + 16) and ts_operand_tr over the swizzled
+    [t][s] bucket rows -- measure conflict-free; the token rows at an unpadded
+    pitch (D) and at D + 4 measure conflicted."""
+    got = _same_pass(probe, "rtr", 0)
+    print(f"[lds] ds_read_b64_tr_b16 lanes sharing a pass with lane 0: {got}", flush=True)
+    assert got == list(range(1, 32))
+    good = [(f"col_operand md={md} half={h}", L.tr_col_read(md, h)) for md in range(4) for h in (0, 16)]
+    good += [(f"ts_operand_tr SP=128 wave {w} half={h}", L.rebased(L.tr_ts_read(128, 16 * w, h)))
+             for w in (0, 3, 5) for h in (0, 16)]
+    bad = [(f"col_operand pitch {pe} md=0", L.tr_col_read(0, 0, pe)) for pe in (L.D, L.D + 4)]
+    for name, offs in good + bad:
+        print(f"[lds] {name:40s} measured cost x{probe.ratio('rtr', offs):.2f}", flush=True)
+    for name, offs in good:
+        assert probe.ratio("rtr", offs) < 1.08, name
+    for name, offs in bad:
+        assert probe.ratio("rtr", offs) > 1.3, name
