@@ -154,8 +154,10 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false, bool walks = true) 
     if (bwd && d->seg_tiles <= 0) {
         // backward segments of fmul forward ones (one segment when that
         // covers the sequence); explicit seg_tiles keeps the forward's
+        // (a segment is at most kMaxSegTiles long: m * tps tiles, or the whole
+        // sequence when that is shorter)
         int64_t m = (int64_t)p.fnseg * p.N * p.nslice / kTargetBlocksBwd;
-        if (walks && m > kMaxSegTiles / p.tps) m = kMaxSegTiles / p.tps;
+        if (walks && p.ntiles > kMaxSegTiles && m > kMaxSegTiles / p.tps) m = kMaxSegTiles / p.tps;
         if (m > 1) {
             const int64_t tb = (int64_t)p.tps * m;
             p.fmul = m < p.fnseg ? (int)m : p.fnseg;

@@ -386,3 +386,18 @@ def test_bench_scan_bytes(K, L, M, B, H, T, fnseg, nseg):
     spad = -(-(L << K) // 128) * 128 if K > 4 else (L << K) + (-(L << K)) % 32
     assert fb == (2 * fn + 1) * N * spad * 65 * 8
     assert bb == 2 * N * bn * spad * 65 * 4
+
+
+def test_backward_segments_cover_short_sequences_whole():
+    """The decoder core's shape (shared sketch: 96 streams of 8192 tokens, K=8,
+    L=4, 8 slices): the forward runs 3 segments of 86 tiles; the backward
+    covers each stream's 256 tiles in one segment -- within the 256-tile
+    bound -- rather than in 172 + 84 tiles."""
+    import bench
+    sb, _, bw = _plan(dtype=_lib.RACE_DTYPE_BF16, K=8, L=4, M=1, B=8, H=12, T=8192)
+    _, _, fnseg, nseg = bench.scan_bytes(sb, bw, 96, 8192, 4, 8)
+    assert (fnseg, nseg) == (3, 1)
+    # beyond the bound the backward segments stay within it: 2^16 tokens = 2048 tiles
+    sb, _, bw = _plan(dtype=_lib.RACE_DTYPE_BF16, K=8, L=4, M=1, B=8, H=12, T=1 << 16)
+    _, _, fnseg, nseg = bench.scan_bytes(sb, bw, 96, 1 << 16, 4, 8)
+    assert -(-2048 // nseg) <= 256, (fnseg, nseg)
