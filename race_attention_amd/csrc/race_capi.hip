@@ -272,6 +272,15 @@ dim3 tile_grid(const Plan &p) {
 
 template <typename T>
 void slice_sum(const Plan &p, const race_desc *d, const void *part, const int64_t *st, void *out, hipStream_t s) {
+    if constexpr (std::is_same<T, bf16>::value) {
+        if (p.nslice == 8) {  // the 8-bit slices of 4 tables
+            const int64_t n8 = p.N * d->T * (D / 8);
+            k_slice_sum8<8><<<elem_blocks(n8), ELEM_THREADS, 0, s>>>((const bf16 *)part, p.N, d->T, (int)d->B,
+                                                                     (int)d->H, Strides{st[0], st[1], st[2], st[3]},
+                                                                     (bf16 *)out);
+            return;
+        }
+    }
     const int64_t n4 = p.N * d->T * (D / 4);
     k_slice_sum<T><<<elem_blocks(n4), ELEM_THREADS, 0, s>>>((const T *)part, p.nslice, p.N, d->T, (int)d->B, (int)d->H,
                                                                 Strides{st[0], st[1], st[2], st[3]}, (T *)out);

@@ -3394,6 +3394,40 @@ __global__ __launch_bounds__(ELEM_THREADS) void k_slice_sum(const T *part, int n
     }
 }
 
+// The same for bf16 partials and a slice count NS known at compile time (8:
+// the 8-bit slices of 4 tables): 8 consecutive d per item, 16-byte loads of
+// every slice issued together, one 16-byte store.
+__device__ __forceinline__ void part8(const bf16 *p, f32x4 &lo, f32x4 &hi) {
+    const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    lo = f32x4{__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xFFFF0000u), __uint_as_float(u[1] << 16),
+               __uint_as_float(u[1] & 0xFFFF0000u)};
+    hi = f32x4{__uint_as_float(u[2] << 16), __uint_as_float(u[2] & 0xFFFF0000u), __uint_as_float(u[3] << 16),
+               __uint_as_float(u[3] & 0xFFFF0000u)};
+}
+template <int NS>
+__global__ __launch_bounds__(ELEM_THREADS) void k_slice_sum8(const bf16 *part, int64_t N, int64_t Tn, int B, int H,
+                                                             Strides so, bf16 *out) {
+    const int64_t per = Tn * (D / 8), items = N * per;  // over N * T * D/8
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < items;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t n = idx / per, r = idx % per, t = r / (D / 8);
+        const int d0 = 8 * (int)(r % (D / 8));
+        const int64_t row = (n * Tn + t) * D + d0, zs = N * Tn * D;
+        f32x4 lo[NS], hi[NS];
+#pragma unroll
+        for (int z = 0; z < NS; ++z) part8(part + z * zs + row, lo[z], hi[z]);
+        f32x4 a = lo[0], b = hi[0];
+#pragma unroll
+        for (int z = 1; z < NS; ++z) {
+            a += lo[z];
+            b += hi[z];
+        }
+        bf16 *o = out + stream_off(so, (int)n, B, H) + t * so.t + d0;
+        store4<bf16>(o, a);
+        store4<bf16>(o + 4, b);
+    }
+}
+
 // dX of sliced instantiations: out[n][t][:] = sum over slices z (in order)
 // of part[z][n][t][:] . planes[m][c0(z) ..][:] -- per slice one product of
 // its dproj columns with planes^T on the matrix cores, the same operands
