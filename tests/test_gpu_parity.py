@@ -171,6 +171,10 @@ CASES = [
     ("causal_bf16_K8L4_vmean", dict(T=1024, H=2, L=4, K=8, v_shift=0.5), True, None, 0),
     ("causal_fp32_K4L8_vmean_seg", dict(T=1500, H=1, L=8, K=4, dtype=torch.float32, v_shift=0.5), True, None, 40),
     ("noncausal_bf16_K4L8_vmean", dict(T=600, H=2, L=8, K=4, v_shift=0.5), False, 1.0, 0),
+    # 8-bit hashes with one table (2 slices: k_dx_finish8 with one live table) and three (6 slices: the
+    # generic slice sum), whole tiles and ragged
+    ("causal_bf16_K8L1_whole", dict(T=640, H=2, L=1, K=8), True, None, 0),
+    ("causal_bf16_K8L3_ragged", dict(T=333, H=2, L=3, K=8), True, None, 3),
 ]
 
 
