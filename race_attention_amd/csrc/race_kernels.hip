@@ -14,9 +14,9 @@
 //             k_bwd_out     reverse walk: dK, dV            reads Q, K, V, dO
 // The reverse walk needs the forward state at every tile start: it subtracts
 // each tile's (A, B) sums from the segment's end state -- A in fp64, B in
-// fp64 for fp32 inputs (recomputed with exactly the code of k_fwd_reduce, so
-// bit-identical) and in fp32 MFMA accumulators for bf16, whose B reaches the
-// products only as a bf16 operand.  The non-causal operator runs the same
+// fp64 (recomputed with exactly the code of k_fwd_reduce: bit-identical tile
+// sums), except in the whole-tile bf16 instantiations, which keep B in fp32
+// MFMA accumulators (see walk_f64).  The non-causal operator runs the same
 // kernels with full-sequence sums and no triangles.
 //
 // Inside a workgroup wave w owns buckets [16w, 16w+16): the workgroup has
@@ -999,6 +999,42 @@ __device__ __forceinline__ void frag_acc_hilo(const f32x4 &x0, const f32x4 &x1, 
     }
 }
 
+// Small tables -- bf16 with at most 3 hash bits, or 4 bits in at most 64
+// buckets: P_K, W and the carried U enter the products that sum them as
+// fp32-accurate pairs (the operand hi plus a second product with lo = the
+// remainder).  A table of few wide buckets at a low temperature has nearly
+// flat probabilities (P_s = 2^-K + a small variation); the softmax backward
+// of dQ and dK cancels what is common to a table's buckets, so a bf16 operand
+// alone would leave 2^-9 of P itself, not of its variation, in the gradients:
+// through A's prefix sums and totals, the in-tile G term and the B sums (P_K),
+// dP_K's in-tile term and the U sums (W), and dP_K's v . U term (U).  The
+// 4-bit, 128-bucket and wider instantiations average over more tables and
+// keep the single operands.
+template <typename T, int SP, int KB> __host__ __device__ constexpr bool hl_ops() {
+    return is_bf16<T>() && (KB <= 3 || (KB == 4 && SP <= 64));
+}
+// bf16 B state in fp64: k_fwd_reduce's segment sums and k_bwd_out's reverse
+// walk add the tiles' fp32 sums to fp64 totals instead of accumulating them
+// on the matrix core.  The walk derives B at a tile start as the state at the
+// segment end minus the later tiles' sums, so an fp32 walk carries an error
+// relative to the segment-end state; with a sharp softmax a bucket's B can
+// grow by orders of magnitude within a segment, and dA, whose factor
+// W / (A + eps) is largest where A (hence B) is smallest, takes that error as
+// it is.  Both sides change together: fp32 sums and an fp32 walk round the
+// same tile sums the same way, and their errors partly cancel.  The
+// whole-tile instantiations (4- and 8-bit, 128 buckets) keep the fp32
+// accumulators: they hold the registers of the two-wave occupancy of
+// k_bwd_out and the four-wave one of k_fwd_reduce.
+template <typename T, bool AL> __host__ __device__ constexpr bool walk_f64() { return is_bf16<T>() && !AL; }
+// R = X - bf16(X) (exact in fp32): the lo part of a tile pair whose hi part is
+// the round-to-nearest operand the kernels take from X
+__device__ __forceinline__ void lo_rem(const f32x4 (&X)[2], f32x4 (&R)[2]) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) R[nt][e] = X[nt][e] - as_operand<bf16>(X[nt][e]);
+}
+
 // c += A . X^T over the wave's 16 buckets, X a bucket-row tile taken as the B
 // operand (column t, k = s); bf16 runs A . hi + A . lo as one 32-deep product
 // (A duplicated in OpX, X split into its two bf16 parts, hi + lo within
@@ -1484,6 +1520,22 @@ __device__ __forceinline__ void tile_sums(const Frag<T> &Pf, const Consts<T> &cs
         mma(dB[md], ld_frag_pi(sVt + (16 * md + li()) * LDT), Pf);
     }
 }
+// bf16: the same sums from a V tile that col_operand reads (natural rows nat
+// or transposed rows trn, per VL), with HL the lo part Pl of P_K added
+template <class VL, bool HL>
+__device__ __forceinline__ void tile_sums_bf(const Frag<bf16> &Pf, const Frag<bf16> &Pl, const Consts<bf16> &cst,
+                                             const bf16 *nat, const bf16 *trn, f32x4 &tot, f32x4 (&dB)[4]) {
+    tot = zero4();
+    mma(tot, Pf, cst.ones());
+    if constexpr (HL) mma(tot, Pl, cst.ones());
+#pragma unroll
+    for (int md = 0; md < 4; ++md) {
+        const Frag<bf16> vo = col_operand<bf16, VL>(nat, trn, md);
+        dB[md] = zero4();
+        mma(dB[md], vo, Pf);
+        if constexpr (HL) mma(dB[md], vo, Pl);
+    }
+}
 
 template <typename T, int SP, int KB, bool AL = false>
 __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
@@ -1522,10 +1574,11 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
     // the same column block on every tile, whose planes stay in registers
     PlaneOps<T> pcw;
     if constexpr (AL) pcw.template load<NL>(sPl, sPlLo, pbk.mc(pbk.task(w)));
-    // segment sums: A in fp64; B in fp64 for fp32 inputs, and for bf16 in
-    // fp32 MFMA accumulators (bf16 uses B only through bf16 operands).  Tile
-    // sums are added tile by tile in token order.
-    constexpr bool BM = is_bf16<T>();
+    // segment sums: A in fp64; B in fp64, except in the whole-tile bf16
+    // instantiations' fp32 MFMA accumulators (walk_f64).  Tile sums are added
+    // tile by tile in token order.
+    constexpr bool HL = hl_ops<T, SP, KB>();  // P_K as a hi + lo pair
+    constexpr bool BM = is_bf16<T>() && !walk_f64<T, AL>();
     double accB[4][4], accA[4];
     f32x4 accBm[4];
     for (int e = 0; e < 4; ++e) {
@@ -1563,14 +1616,28 @@ __global__ __launch_bounds__(threads_of(SP)) void k_fwd_reduce(Args a) {
                     for (int e = 0; e < 4; ++e) PK[nt][e] *= wt;
                 }
             const Frag<T> Pf = token_operand<T>(PK, cst);
+            Frag<T> Pl;  // the lo part of P_K (HL)
+            if constexpr (HL) {
+                f32x4 R[2];
+                lo_rem(PK, R);
+                Pl = token_operand<T>(R, cst);
+            }
             if constexpr (BM) {
                 f32x4 tot = zero4();
                 mma(tot, Pf, cst.ones());
-                for (int md = 0; md < 4; ++md) mma(accBm[md], col_operand<T, VL>(vt, vt, md), Pf);
+                if constexpr (HL) mma(tot, Pl, cst.ones());
+                for (int md = 0; md < 4; ++md) {
+                    const Frag<T> vo = col_operand<T, VL>(vt, vt, md);
+                    mma(accBm[md], vo, Pf);
+                    if constexpr (HL) mma(accBm[md], vo, Pl);
+                }
                 for (int e = 0; e < 4; ++e) accA[e] += (double)tot[e];
             } else {
                 f32x4 tot, dB[4];
-                tile_sums<T>(Pf, cst, vt, tot, dB);
+                if constexpr (is_bf16<T>())
+                    tile_sums_bf<VL, HL>(Pf, Pl, cst, vt, vt, tot, dB);
+                else
+                    tile_sums<T>(Pf, cst, vt, tot, dB);
                 for (int e = 0; e < 4; ++e) {
                     accA[e] += (double)tot[e];
                     for (int md = 0; md < 4; ++md) accB[md][e] += (double)dB[md][e];
@@ -1870,6 +1937,7 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
     using NL = typename Ly::NL;
     constexpr bool VNAT = Ly::VNAT;
     constexpr bool PR = pair_tables<KB>();  // Q's and K's sigmoid rows as pair products
+    constexpr bool HL = hl_ops<T, SP, KB>();  // P_K as a hi + lo pair
     using VL = TrL<T>;                      // V rows (VNAT): read only by transpose loads
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDT = Ly::LDT, LDC = Ly::LDC, LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
@@ -2025,17 +2093,24 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
             }
             __syncthreads();
             f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
-            Frag<T> Pf;
+            Frag<T> Pf, Pl;  // Pl: the lo part of P_K (HL)
             probs_st<KB, AL, PR>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
             if constexpr (CAUSAL) {
                 probs_st<KB, AL, PR>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
                 Pf = store_ts_operand<T, SP>(sPts, sw, PK, cst);
+                if constexpr (HL) {
+                    f32x4 R[2];
+                    lo_rem(PK, R);
+                    Pl = token_operand<T>(R, cst);
+                }
                 for (int nt = 0; nt < 2; ++nt) {
                     Acum[nt] = zero4();
                     mma(Acum[nt], Pf, cst.tri_op(nt));
+                    if constexpr (HL) mma(Acum[nt], Pl, cst.tri_op(nt));
                 }
                 tot = zero4();
                 mma(tot, Pf, cst.ones());
+                if constexpr (HL) mma(tot, Pl, cst.ones());
             }
             if constexpr (GN) {
                 // W = P_Q; this wave's share of den(t) = sum_s P_Q A_s(t)
@@ -2080,7 +2155,11 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
                     if (w + k * NW_ < 8) Op[k] = fwd_out_partial<T, SP>((w + k * NW_) >> 1, (w + k * NW_) & 1, sBT, sWts);
             }
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
-            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, col_operand<T, VL, VNAT>(sVt, sVt, md));
+            for (int md = 0; md < 4; ++md) {
+                const Frag<T> vo = col_operand<T, VL, VNAT>(sVt, sVt, md);
+                mma(Bc[md], Pf, vo);
+                if constexpr (HL) mma(Bc[md], Pl, vo);
+            }
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
             if constexpr (QKP) commit(jt + 1);  // Q/K rows read by this tile's projections before the second barrier
             __syncthreads();  // Sc rows in LDS; the P_K / W / B rows are read
@@ -2133,19 +2212,26 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
         }
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], tot;
-        Frag<T> Pf;
+        Frag<T> Pf, Pl;  // Pl: the lo part of P_K (HL)
         probs_st<KB, AL, PR>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
         if constexpr (CAUSAL) {
             probs_st<KB, AL, PR>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
+            if constexpr (HL) {
+                f32x4 R[2];
+                lo_rem(PK, R);
+                Pl = token_operand<T>(R, cst);
+            }
             for (int nt = 0; nt < 2; ++nt)
                 for (int e = 0; e < 4; ++e) PK[nt][e] = as_operand<T>(PK[nt][e]);
             Pf = token_operand<T>(PK, cst);
             for (int nt = 0; nt < 2; ++nt) {
                 Acum[nt] = zero4();
                 mma(Acum[nt], Pf, cst.tri_op(nt));
+                if constexpr (HL) mma(Acum[nt], Pl, cst.tri_op(nt));
             }
             tot = zero4();
             mma(tot, Pf, cst.ones());
+            if constexpr (HL) mma(tot, Pl, cst.ones());
         }
         if constexpr (GN) {
             // W = P_Q; this wave's share of den(t) = sum_s P_Q A_s(t)
@@ -2185,7 +2271,11 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
                                             denp, a.eps);
         if constexpr (CAUSAL) {
             // carry: B[s][d] += sum_t P_K[t][s] V[t][d]
-            for (int md = 0; md < 4; ++md) mma(Bc[md], Pf, col_operand<T, VL, VNAT>(sVt, sVt, md));
+            for (int md = 0; md < 4; ++md) {
+                const Frag<T> vo = col_operand<T, VL, VNAT>(sVt, sVt, md);
+                mma(Bc[md], Pf, vo);
+                if constexpr (HL) mma(Bc[md], Pl, vo);
+            }
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
         }
     }
@@ -2278,6 +2368,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     // the forward state needs the same P_K); Q's stay corner pairs, which its
     // softmax backward reads directly
     constexpr bool PR = pair_tables<KB>();
+    constexpr bool HL = hl_ops<T, SP, KB>();  // P_K and W as hi + lo pairs
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     // this tile's token block (block jt & 1 of two; block 0 of one)
@@ -2454,17 +2545,24 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
             if (jt > j0) dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2], tot;
-        Frag<T> Pf;
+        Frag<T> Pf, Pl;  // Pl: the lo part of P_K (HL)
         probs_st<KB, AL>(sSpQ, sSmQ, sg, a.S, jt + 1 < ntiles ? TT : lastv, PQ);
         if constexpr (CAUSAL) {
             probs_st<KB, AL, PR>(sSpK, sSmK, sg, a.S, jt + 1 < ntiles ? TT : lastv, PK);
             Pf = token_operand<T>(PK, cst, po);
+            if constexpr (HL) {
+                f32x4 R[2];
+                lo_rem(PK, R);
+                Pl = token_operand<T>(R, cst, po);
+            }
             for (int nt = 0; nt < 2; ++nt) {
                 Acum[nt] = zero4();
                 mma(Acum[nt], Pf, cst.tri_op(nt));
+                if constexpr (HL) mma(Acum[nt], Pl, cst.tri_op(nt));
             }
             tot = zero4();
             mma(tot, Pf, cst.ones());
+            if constexpr (HL) mma(tot, Pl, cst.ones());
         }
         f32x4 Ag[2];  // GN: A_s(t)
         float rd[2], gd[2], ae[4];  // ae: A at the tile start (+ eps unless GN)
@@ -2486,6 +2584,12 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
             }
         }
         const Frag<T> Wf = token_operand<T>(W, cst, po);
+        Frag<T> Wl;  // the lo part of W (HL)
+        if constexpr (HL) {
+            f32x4 R[2];
+            lo_rem(W, R);
+            Wl = token_operand<T>(R, cst, po);
+        }
         // G[s][t] = g_t . B_s(t) = sum_d B[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
         f32x4 dPQ[2], dA[2];
         {
@@ -2512,6 +2616,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
                     mma(G, b1l, g1);
                 }
                 if constexpr (CAUSAL) mma(G, Pf, Xop[nt]);
+                if constexpr (CAUSAL && HL) mma(G, Pl, Xop[nt]);
                 // dP_Q = G/(A+eps); dA = -W G/(A+eps).  GN: dP_Q = G rd + gd A; dA = gd P_Q
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (GN) {
@@ -2538,8 +2643,14 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         for (int e = 0; e < 4; ++e) al[e] += (double)(dA[0][e] + dA[1][e]);
         // U^T[d][s] += sum_t g[t][d] W[t][s]; carry B^T[d][s] += sum_t V[t][d] P_K[t][s]
         for (int md = 0; md < 4; ++md) {
-            mma(Ut[md], col_operand<T, NL>(sG, sGt, md), Wf);
-            if constexpr (CAUSAL) mma(Bt[md], col_operand<T, NL>(sV, sVt, md), Pf);
+            const Frag<T> go = col_operand<T, NL>(sG, sGt, md);
+            mma(Ut[md], go, Wf);
+            if constexpr (HL) mma(Ut[md], go, Wl);
+            if constexpr (CAUSAL) {
+                const Frag<T> vo = col_operand<T, NL>(sV, sVt, md);
+                mma(Bt[md], vo, Pf);
+                if constexpr (HL) mma(Bt[md], vo, Pl);
+            }
         }
         if constexpr (CAUSAL)
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
@@ -2720,6 +2831,31 @@ __device__ void dv_tile(int md, int nt, const T *sUT, const T *Pts, const T *Wts
 // dV tile (md, nt) in two steps: the carried part U P_K (over all buckets,
 // from the U and P_K rows), then, once the tile's Sc2 rows exist (sc2_tile),
 // the in-tile part g^T Sc2 and the store.
+// The d-row carry U^T (lane: [d = 16md + 4g + e][s = sw + i]) as the operand
+// of acc[s][tau] += sum_d U[s][d] v_tau[d]; with HL an fp32-accurate hi + lo
+// pair
+template <typename T, bool HL> struct UOps {
+    Frag<T> u0, u1, u0l, u1l;
+    __device__ __forceinline__ explicit UOps(const f32x4 (&Ut)[4]) {
+        if constexpr (HL) {
+            frag_acc_hilo(Ut[0], Ut[1], u0, u0l);
+            frag_acc_hilo(Ut[2], Ut[3], u1, u1l);
+        } else {
+            u0 = frag_acc<T>(Ut[0], Ut[1]);
+            u1 = frag_acc<T>(Ut[2], Ut[3]);
+        }
+    }
+    // the tile's tokens tau = 16 nt + i
+    template <class NL> __device__ __forceinline__ void apply(f32x4 &acc, const T *sV, int nt) const {
+        const Frag<T> v0 = NL::frag_pi(sV, 16 * nt + li(), 0), v1 = NL::frag_pi(sV, 16 * nt + li(), 1);
+        mma(acc, u0, v0);
+        mma(acc, u1, v1);
+        if constexpr (HL) {
+            mma(acc, u0l, v0);
+            mma(acc, u1l, v1);
+        }
+    }
+};
 template <typename T, int SP> __device__ f32x4 dv_part(int md, int nt, const T *sUT, const T *Pts) {
     const int i = li();
     const T *pu = sw_frag_ptr<T, SP>(sUT, 16 * md + i), *pp = sw_frag_ptr<T, SP>(Pts, 16 * nt + i);
@@ -2756,6 +2892,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     // Q's and K's sigmoid rows as pair products (K's as in the forward kernels:
     // the walk back of the forward state subtracts the same P_K)
     constexpr bool PR = pair_tables<KB>();
+    constexpr bool HL = hl_ops<T, SP, KB>();  // P_K, W and U as hi + lo pairs
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
                   LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
@@ -2836,11 +2973,11 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         a.fstate + ((int64_t)n * (a.fnseg + 1) + min((seg + 1) * a.fmul, a.fnseg)) * a.Spad * SROW;
     f32x4 Ut[4];  // U^T[d = 16md + 4g + e][s = sw + i]
     // Forward state, walked back from the segment end.  B only feeds the
-    // G product's operand: bf16 carries it in fp32 MFMA accumulators and
-    // subtracts the tile sums on the matrix core (Bm); fp32 walks it in fp64
-    // (Be).  A stays fp64: A(t) is far below the segment-end value early in
-    // a sequence.
-    constexpr bool BM = is_bf16<T>();
+    // G product's operand: the whole-tile bf16 instantiations carry it in
+    // fp32 MFMA accumulators and subtract the tile sums on the matrix core
+    // (Bm); the others walk it in fp64 (Be, walk_f64).  A stays fp64: A(t)
+    // is far below the segment-end value early in a sequence.
+    constexpr bool BM = is_bf16<T>() && !walk_f64<T, AL>();
     double Be[4][4], Ae[4];
     f32x4 Bm[4];
     f32x4 al;
@@ -3060,7 +3197,21 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         if constexpr (CAUSAL) {
             f32x4 Wi[2];  // W / (A + eps), the factor of dA
             f32x4 dA[2];
-            Frag<T> Wf;
+            Frag<T> Wf, Pl, Wl;  // Pl, Wl: the lo parts of P_K and W (HL)
+            if constexpr (HL) {
+                f32x4 R[2];
+                lo_rem(PKr, R);
+                Pl = token_operand<T>(R, cst, po);
+            }
+            // W's operand, and with HL its lo part
+            auto w_operands = [&](const f32x4 (&W)[2]) {
+                Wf = store_ts_operand<T, SP>(sWts, sw, W, cst);
+                if constexpr (HL) {
+                    f32x4 R[2];
+                    lo_rem(W, R);
+                    Wl = token_operand<T>(R, cst, po);
+                }
+            };
             if constexpr (GN) {
                 f32x4 PQ[2], W[2];
                 probs_st<KB, AL, PR>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
@@ -3071,7 +3222,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                         dA[nt][e] = gd * PQ[nt][e];
                     }
                 }
-                Wf = store_ts_operand<T, SP>(sWts, sw, W, cst);
+                w_operands(W);
             } else {
                 f32x4 PQ[2], Acum[2], W[2], tot, dB[4];
                 probs_st<KB, AL, PR>(sSpQ, sSmQ, sg, a.S, jr + 1 < ntiles ? TT : lastv, PQ);
@@ -3079,11 +3230,19 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                 if constexpr (BM) {
                     tot = zero4();
                     mma(tot, Pf, cst.ones());
+                    if constexpr (HL) mma(tot, Pl, cst.ones());
                     const Frag<T> Pn = neg_frag(Pf);
-                    for (int md = 0; md < 4; ++md) mma(Bm[md], col_operand<T, NL>(sV, sVt, md), Pn);
+                    for (int md = 0; md < 4; ++md) {
+                        const Frag<T> vo = col_operand<T, NL>(sV, sVt, md);
+                        mma(Bm[md], vo, Pn);
+                        if constexpr (HL) mma(Bm[md], vo, neg_frag(Pl));
+                    }
                     for (int e = 0; e < 4; ++e) Ae[e] -= (double)tot[e];
                 } else {
-                    tile_sums<T>(Pf, cst, sVt, tot, dB);
+                    if constexpr (is_bf16<T>())
+                        tile_sums_bf<NL, HL>(Pf, Pl, cst, sV, sVt, tot, dB);
+                    else
+                        tile_sums<T>(Pf, cst, sVt, tot, dB);
                     for (int e = 0; e < 4; ++e) {
                         Ae[e] -= (double)tot[e];
                         for (int md = 0; md < 4; ++md) Be[md][e] -= (double)dB[md][e];
@@ -3092,6 +3251,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                 for (int nt = 0; nt < 2; ++nt) {
                     Acum[nt] = zero4();
                     mma(Acum[nt], Pf, cst.tri_op(nt));
+                    if constexpr (HL) mma(Acum[nt], Pl, cst.tri_op(nt));
                 }
                 float ae[4];
                 for (int e = 0; e < 4; ++e) ae[e] = (float)Ae[e] + a.eps;
@@ -3101,7 +3261,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                         W[nt][e] = PQ[nt][e] * inv;
                         Wi[nt][e] = W[nt][e] * inv;
                     }
-                Wf = store_ts_operand<T, SP>(sWts, sw, W, cst);
+                w_operands(W);
             }
             store_ut<T, SP>(sUT, sw, Ut, cst, po);
             __syncthreads();  // all waves' P_K, W, U rows in LDS
@@ -3134,7 +3294,9 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                     f32x4 G = zero4();
                     mma(G, Bf[0], NL::frag_pi(sG, 16 * nt + i, 0));
                     mma(G, Bf[1], NL::frag_pi(sG, 16 * nt + i, 1));
-                    mma(G, Pf, ld_frag_pi(sX + (16 * nt + i) * LDT));
+                    const Frag<T> xo = ld_frag_pi(sX + (16 * nt + i) * LDT);
+                    mma(G, Pf, xo);
+                    if constexpr (HL) mma(G, Pl, xo);
                     for (int e = 0; e < 4; ++e) dA[nt][e] = -Wi[nt][e] * G[e];
                 }
             }
@@ -3142,17 +3304,22 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
             {
                 f32x4 alpha[2], tdA;  // alpha(tau): the suffix from this tile on
                 suffix_totals(dA, al, alpha, tdA);
-                const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
+                const UOps<T, HL> uo(Ut);
                 for (int nt = 0; nt < 2; ++nt) {
                     dPK[nt] = alpha[nt];
-                    mma(dPK[nt], u0, NL::frag_pi(sV, 16 * nt + i, 0));
-                    mma(dPK[nt], u1, NL::frag_pi(sV, 16 * nt + i, 1));
-                    mma(dPK[nt], Wf, ld_frag_pi(sY + (16 * nt + i) * LDT));
+                    uo.template apply<NL>(dPK[nt], sV, nt);
+                    const Frag<T> yo = ld_frag_pi(sY + (16 * nt + i) * LDT);
+                    mma(dPK[nt], Wf, yo);
+                    if constexpr (HL) mma(dPK[nt], Wl, yo);
                 }
                 for (int e = 0; e < 4; ++e) al[e] += tdA[e];
             }
             // ---- U^T[d][s] += sum_t g[t][d] W[t][s]  (the dV tiles read the LDS copy of U)
-            for (int md = 0; md < 4; ++md) mma(Ut[md], col_operand<T, NL>(sG, sGt, md), Wf);
+            for (int md = 0; md < 4; ++md) {
+                const Frag<T> go = col_operand<T, NL>(sG, sGt, md);
+                mma(Ut[md], go, Wf);
+                if constexpr (HL) mma(Ut[md], go, Wl);
+            }
             if constexpr (SCN) {
                 // the tile's three Sc2 blocks, once each, for its dV tiles in
                 // the next iteration
@@ -3171,11 +3338,10 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
             // non-causal: dV^T = U^T P_K^T; dP_K = alpha + v . U (totals)
             for (int q = w; q < 8; q += NW_)
                 dv_tile<T, SP, CAUSAL, AL>(q >> 1, q & 1, sUT, sPts, nullptr, nullptr, nullptr, dvp, a.sg.t, t0, a.T, vpart);
-            const Frag<T> u0 = frag_acc<T>(Ut[0], Ut[1]), u1 = frag_acc<T>(Ut[2], Ut[3]);
+            const UOps<T, HL> uo(Ut);
             for (int nt = 0; nt < 2; ++nt) {
                 f32x4 c = zero4();
-                mma(c, u0, NL::frag_pi(sV, 16 * nt + i, 0));
-                mma(c, u1, NL::frag_pi(sV, 16 * nt + i, 1));
+                uo.template apply<NL>(c, sV, nt);
                 for (int e = 0; e < 4; ++e) dPK[nt][e] = (c[e] + al[e]) * kwt[nt];  // through the key weight
             }
         }

@@ -3,9 +3,9 @@ kernels (race_attention_amd/csrc/race_kernels.hip) account for the error of
 out, dQ, dK and dV against the exact operator.
 
 A numpy fp64 restatement of the tile algorithm the kernels run (32-token
-tiles; the chunked forward and backward of the survey's Appendix B, i.e. the
-recurrence of kernels/cpu/race_pref.cpp:36-220 cut into tiles), in which every
-value the kernels round to bf16 passes through a switchable rounding:
+tiles: the recurrence of kernels/cpu/race_pref.cpp:36-220 cut into tiles), in
+which every value the kernels round to bf16 passes through a switchable
+rounding:
 
   P      P_K as an MFMA operand: every sum over tokens of P_K (A, B, the
          in-tile triangles, dV) uses bf16 P_K (P_Q stays fp32 until it is
@@ -36,6 +36,13 @@ the planes), the sigmoid factors, A's fp64 carries, fp32 accumulation (far
 below 2^-9), the softmax backward's hi/lo table sums.  The kernels' carries of
 B in fp32 are also taken as exact (their walk error is bounded by the segment
 length, see race_capi.hip kMaxSegTiles).
+
+hl=True models the small-table instantiations (race_kernels.hip hl_ops: bf16
+with at most 3 hash bits, or 4 bits in at most 64 buckets), which take P_K,
+W and the carried U as fp32-accurate hi + lo operand pairs wherever a sum
+feeds the gradients' softmax backward: P_K in A, in B and in the in-tile G
+term; W in dP_K's in-tile term and in U; U in dP_K's v . U term.  P and W
+keep their rounding in the output triangles and dV, U in dV.
 
 With every rounding off the restatement equals the oracle (tests/
 test_error_budget.py pins it there).  `python tests/error_budget.py [T]`
@@ -102,9 +109,10 @@ def soft_hash_bwd(P, dP, th, planes, it, xpart=None):
     return out.reshape(-1, L * K)
 
 
-def stream(q, k, v, g, planes, it, eps, on=()):
+def stream(q, k, v, g, planes, it, eps, on=(), hl=False):
     """One causal stream: q, k, v, g [T, D] (bf16-valued fp64), planes [L, K, D].
-    Returns out, dq, dk, dv [T, D] with the roundings named in `on` applied."""
+    Returns out, dq, dk, dv [T, D] with the roundings named in `on` applied
+    (hl: the small-table operand pairs)."""
     r = {name: (bf16 if name in on else (lambda x: x)) for name in ROUNDINGS}
     xp = bf16 if "xpart" in on else None
     T, D = q.shape
@@ -112,6 +120,7 @@ def stream(q, k, v, g, planes, it, eps, on=()):
     PQ, thq = soft_hash(q, planes, it)
     PK, thk = soft_hash(k, planes, it)
     PKr = r["P"](PK)
+    PKx = PK if hl else PKr  # P_K in A, B and the in-tile G term
     S = PK.shape[1]
     nt = (T + TT - 1) // TT
     A0 = np.zeros((nt, S))      # A, B at each tile start (exact carries)
@@ -124,15 +133,15 @@ def stream(q, k, v, g, planes, it, eps, on=()):
     for c in range(nt):
         a, b = c * TT, min(T, c * TT + TT)
         A0[c], B0[c] = Ac, Bc
-        pk, vv = PKr[a:b], v[a:b]
-        At = Ac + np.cumsum(pk, 0)                                   # A_s(t), t in the tile
+        pk, px, vv = PKr[a:b], PKx[a:b], v[a:b]
+        At = Ac + np.cumsum(px, 0)                                   # A_s(t), t in the tile
         W[a:b] = PQ[a:b] / (At + eps)
         w = r["W"](W[a:b])
         Wr[a:b] = w
         Sc = r["tri"](np.tril(w @ pk.T))                             # Sc[t, t'] = sum_s W P_K, t' <= t
         out[a:b] = w @ r["B"](Bc) + Sc @ vv
-        Bc = Bc + pk.T @ vv
-        Ac = Ac + pk.sum(0)
+        Bc = Bc + px.T @ vv
+        Ac = Ac + px.sum(0)
     dq_proj = np.zeros((T, L * K))
     dk_proj = np.zeros((T, L * K))
     dv = np.zeros((T, D))
@@ -140,19 +149,20 @@ def stream(q, k, v, g, planes, it, eps, on=()):
     alc = np.zeros(S)
     for c in reversed(range(nt)):
         a, b = c * TT, min(T, c * TT + TT)
-        pk, vv, gg, w = PKr[a:b], v[a:b], g[a:b], Wr[a:b]
-        At = A0[c] + np.cumsum(pk, 0)
+        pk, px, vv, gg, w = PKr[a:b], PKx[a:b], v[a:b], g[a:b], Wr[a:b]
+        wx = W[a:b] if hl else w                                      # W in dP_K's in-tile term and U
+        At = A0[c] + np.cumsum(px, 0)
         inv = 1.0 / (At + eps)
         M = r["tri"](np.triu(vv @ gg.T))                             # M[tau, t] = v_tau . g_t, tau <= t
-        tri_g = M.T @ pk                                              # in-tile part of G[t, s] = g_t . B_s(t)
+        tri_g = M.T @ px                                              # in-tile part of G[t, s] = g_t . B_s(t)
         dPQ = (gg @ B0[c].T + tri_g) * inv                            # k_bwd_reduce: hi + lo B
         dA = -W[a:b] * (gg @ r["B"](B0[c]).T + tri_g) * inv           # k_bwd_out: bf16 B; fp32 W
         alpha = alc + np.cumsum(dA[::-1], 0)[::-1]                    # suffix from tau on
         Ur = r["U"](Uc)
-        dPK = alpha + vv @ Ur.T + M @ w                               # sum_{t >= tau} M[tau, t] W[t, s]
+        dPK = alpha + vv @ (Uc if hl else Ur).T + M @ wx              # sum_{t >= tau} M[tau, t] W[t, s]
         Sc2 = r["tri"](np.triu(pk @ w.T))                             # Sc2[tau, t] = sum_s P_K W, t >= tau
         dv[a:b] = pk @ Ur + Sc2 @ gg
-        Uc = Uc + w.T @ gg
+        Uc = Uc + wx.T @ gg
         alc = alc + dA.sum(0)
         dq_proj[a:b] = soft_hash_bwd(PQ[a:b], dPQ, thq[a:b], planes, it, xp)
         dk_proj[a:b] = soft_hash_bwd(PK[a:b], dPK, thk[a:b], planes, it, xp)
@@ -162,12 +172,12 @@ def stream(q, k, v, g, planes, it, eps, on=()):
     return tuple(r["out"](x) for x in (out, dq, dk, dv))
 
 
-def run(q, k, v, g, planes, it, eps=1e-6, on=()):
+def run(q, k, v, g, planes, it, eps=1e-6, on=(), hl=False):
     """[M,B,T,H,D] arrays (bf16-valued), planes [1,L,K,D] -> out, dq, dk, dv of the same shape."""
     res = [np.zeros_like(q) for _ in range(4)]
     M, B, T, H, D = q.shape
     for m, bb, h in itertools.product(range(M), range(B), range(H)):
-        o = stream(q[m, bb, :, h], k[m, bb, :, h], v[m, bb, :, h], g[m, bb, :, h], planes[0], it, eps, on)
+        o = stream(q[m, bb, :, h], k[m, bb, :, h], v[m, bb, :, h], g[m, bb, :, h], planes[0], it, eps, on, hl)
         for x, y in zip(res, o):
             x[m, bb, :, h] = y
     return tuple(res)

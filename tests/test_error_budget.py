@@ -47,3 +47,21 @@ def test_slice_partials_add_up_to_the_table():
     # a bf16 rounding of each partial is relative to the partials
     rounded = eb.soft_hash_bwd(P, dP, th, planes, it, xpart=eb.bf16)
     assert np.abs(rounded - whole).max() > 0
+
+
+def test_small_table_operand_pairs():
+    """Two-bit tables at the 1/sqrt(d) temperature: bucket probabilities are
+    nearly flat, and the softmax backward of dQ and dK cancels what a table's
+    buckets share.  With single bf16 operands for P_K, W and U the restatement's
+    dQ / dK error is at the bf16 bar; with the small-table instantiations' hi +
+    lo pairs (hl) it is a third of that.  hl without roundings is the exact
+    operator."""
+    q, k, v, g, planes = eb.inputs(T=608, H=2, L=5, K=2, seed=0)
+    it = 1.0 / 8.0
+    exact = eb.run(q, k, v, g, planes, it)
+    single = [eb.relerr(a, b) for a, b in zip(eb.run(q, k, v, g, planes, it, on=eb.ROUNDINGS), exact)]
+    pairs = [eb.relerr(a, b) for a, b in zip(eb.run(q, k, v, g, planes, it, on=eb.ROUNDINGS, hl=True), exact)]
+    assert max(single[1:3]) > 1.2e-2, single
+    assert max(pairs[1:3]) < 6e-3, pairs
+    none = eb.run(q, k, v, g, planes, it, hl=True)
+    assert max(eb.relerr(a, b) for a, b in zip(none, exact)) < 1e-11
