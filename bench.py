@@ -353,7 +353,7 @@ def scan_bytes(state_bytes, bwd_ws_bytes, N, T, L, K, D=64):
     k_bwd_scan reads the fp32 (U, alpha) sums [N][nseg][Spad][D+1] and writes
     their suffixes, the same size.  The segment counts follow from the sizes:
     state = N (fnseg+1) Spad (D+1) 8 bytes; backward workspace = 2 N nseg
-    Spad (D+1) 4 + align16(8 N nseg nslice), plus, for bucket slices, the dV
+    Spad (D+1) 4 + align16(16 N nseg nslice), plus, for bucket slices, the dV
     partials [nslice][N][T][D] bf16 and the two dQ / dK d(projection) partial
     buffers [nslice][N][T][8] (fp32 for 8-bit hashes).  Covers the
     single-slice plans (K <= 4, L 2^K <= 128) and 8-bit hashes; None otherwise.
@@ -370,9 +370,9 @@ def scan_bytes(state_bytes, bwd_ws_bytes, N, T, L, K, D=64):
         return None
     blk = spad * (D + 1)
     fnseg = state_bytes // (N * blk * 8) - 1
-    nseg = (bwd_ws_bytes - parts) // (8 * N * blk + 8 * N * nslice)
+    nseg = (bwd_ws_bytes - parts) // (8 * N * blk + 16 * N * nslice)
     if state_bytes != N * (fnseg + 1) * blk * 8 or \
-            bwd_ws_bytes != 8 * N * nseg * blk + _a16(8 * N * nseg * nslice) + parts:
+            bwd_ws_bytes != 8 * N * nseg * blk + _a16(16 * N * nseg * nslice) + parts:
         return None
     return (2 * fnseg + 1) * N * blk * 8, 2 * N * nseg * blk * 4, fnseg, nseg
 

@@ -59,9 +59,9 @@ typedef struct race_desc {
     int32_t seg_tiles;        /* 32-token tiles per scan segment, forward and backward; 0 = automatic
                                  (the backward then joins whole forward segments into fewer ones).
                                  Automatic segments are at most 256 tiles at any T, and the
-                                 backward calls reject an explicit value above 256: the bf16
-                                 kernels walk B in fp32 through a segment, so long sequences
-                                 add segments instead of lengthening the walks. */
+                                 backward calls reject an explicit value above 256: the
+                                 whole-tile bf16 kernels walk B in fp32 through a segment, so
+                                 long sequences add segments instead of lengthening the walks. */
     int32_t phases;           /* 0 = run every kernel of the call; otherwise a bitmask of
                                  RACE_PHASE_* to run a subset (per-kernel timing); subsets of
                                  one call must be enqueued in phase order on one stream */

@@ -166,7 +166,7 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false, bool walks = true) 
         }
     }
     p.bws_core = 2 * (size_t)p.N * p.nseg * blk * sizeof(float) +
-                 align16(2 * (size_t)p.N * p.nseg * p.nslice * sizeof(float));
+                 align16(2 * (size_t)p.N * p.nseg * p.nslice * sizeof(double));
     // k_dx_finish runs one 64-lane wave per 64 tokens of a stream
     if (p.parts && (p.N * ((d->T + 16 * DXF_BLK - 1) / (16 * DXF_BLK)) + 3) / 4 * 256 > kMaxWorkItems)
         return fail(RACE_E_UNSUPPORTED, "M*B*H*T=%lld token-heads exceed one dX launch's 2^32 work-items",
@@ -510,7 +510,7 @@ int probs_dispatch(const race_desc *d, const Plan &p, const Args &a, bool bwd, f
 }
 
 // workspace of race_probs_bwd: temperature partials, then fp32 dx partials (sliced)
-size_t probs_ws_core(const Plan &p) { return align16((size_t)p.N * p.nseg * p.nslice * sizeof(float)); }
+size_t probs_ws_core(const Plan &p) { return align16((size_t)p.N * p.nseg * p.nslice * sizeof(double)); }
 
 int check_gn(const race_desc *d) {
     if (d->causal != 1)
@@ -551,7 +551,7 @@ int bwd_args(const race_desc *d, const Plan &p, const void *q, const void *k, co
     const size_t blk = (size_t)p.N * p.nseg * p.Spad * SROW;
     a.rdelta = (float *)ws;
     a.rstate = a.rdelta + blk;
-    a.tpart = a.rstate + blk;
+    a.tpart = (double *)(a.rstate + blk);  // blk is even: 8-byte aligned
     if (p.parts) {
         float *part = (float *)((char *)ws + p.bws_core);
         a.dqpart = part;
@@ -737,7 +737,7 @@ int race_probs_bwd(const race_desc *d, const void *x, const float *planes, const
     a.q = x;
     a.dq = dx;
     a.dprobs = dP;
-    a.tpart = (float *)ws;
+    a.tpart = (double *)ws;
     a.dqpart = p.parts ? (char *)ws + probs_ws_core(p) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     if (d->dtype == RACE_DTYPE_BF16) return probs_dispatch<bf16>(d, p, a, true, grad_inv_temp, s);
@@ -872,7 +872,7 @@ int race_bwd_global(const race_desc *d, const void *q, const void *k, const void
     const size_t blk = (size_t)p.N * p.nseg * p.Spad * SROW;
     a.rdelta = (float *)ws;
     a.rstate = a.rdelta + blk;
-    a.tpart = a.rstate + blk;
+    a.tpart = (double *)(a.rstate + blk);  // blk is even: 8-byte aligned
     if (p.parts) {
         float *part = (float *)((char *)ws + p.bws_core);
         a.dqpart = part;

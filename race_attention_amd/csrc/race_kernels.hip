@@ -67,7 +67,7 @@ struct Args {
     double *fdelta;  // [N][nseg][Spad][D+1]
     float *rdelta;   // [N][nseg][Spad][D+1]  per-segment (U, alpha) sums
     float *rstate;   // [N][nseg][Spad][D+1]  exclusive suffixes (non-causal: totals)
-    float *tpart;    // [2][N][nseg][nslice] partial sums of dU*th
+    double *tpart;   // [2][N][nseg][nslice] partial sums of dU*th
     // sliced() instantiations: per-slice partial outputs [nslice][N][T][D] in the element type (bf16 or
     // fp32), summed in fp32 by k_slice_sum
     void *opart, *dvpart;
@@ -696,9 +696,15 @@ __device__ __forceinline__ void probs_st_(const float *sp, const float *sm, int 
     const int g = lg(), i = li();
     const int s0 = sw + 4 * g;
     static_assert(!PAIR || pair_tables<KB>(), "pair rows of 4- and 8-bit tables");
+    // Padding buckets (s >= S) read the last table's rows, which every slice
+    // holding padding projects (a slice's columns hold only its own tables:
+    // other rows of its LDS are left over from earlier work), and padding
+    // buckets and tokens are cleared by a select: a product with zero would
+    // keep a NaN or infinity of those rows.
+    const int lpad = (S >> KB) - 1;
     if constexpr (PAIR) {
         const bool sv = FULL || s0 < S;
-        const int l = sv ? s0 >> KB : 0, r0 = s0 & (R - 1);
+        const int l = sv ? s0 >> KB : lpad, r0 = s0 & (R - 1);
         const int n1 = l * KB + KB - 4;  // the table's last nibble
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
@@ -706,10 +712,9 @@ __device__ __forceinline__ void probs_st_(const float *sp, const float *sm, int 
             const bool v = sv && (FULL || t < nv);
             float hi = sp[t * LDC + n1 + ((r0 >> 2) & 3)];
             if constexpr (KB == 8) hi *= sp[t * LDC + l * KB + (r0 >> 6)] * sm[t * LDC + l * KB + ((r0 >> 4) & 3)];
-            if constexpr (!FULL) hi = v ? hi : 0.f;
             const f32x4 lo = *reinterpret_cast<const f32x4 *>(sm + t * LDC + n1);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) P[nt][e] = hi * lo[e];
+            for (int e = 0; e < 4; ++e) P[nt][e] = (FULL || v) ? hi * lo[e] : 0.f;
         }
         return;
     }
@@ -720,14 +725,14 @@ __device__ __forceinline__ void probs_st_(const float *sp, const float *sm, int 
         if constexpr (KB == 1) {
             // tables s0/2 and s0/2 + 1; corner r = 1 is sigmoid(+2u)
             const bool v01 = FULL || (tv && s0 < S), v23 = FULL || (tv && s0 + 2 < S);
-            const int l0 = v01 ? s0 >> 1 : 0, l1 = v23 ? (s0 >> 1) + 1 : 0;
+            const int l0 = v01 ? s0 >> 1 : lpad, l1 = v23 ? (s0 >> 1) + 1 : lpad;
             P[nt][0] = v01 ? sm[t * LDC + l0] : 0.f;
             P[nt][1] = v01 ? sp[t * LDC + l0] : 0.f;
             P[nt][2] = v23 ? sm[t * LDC + l1] : 0.f;
             P[nt][3] = v23 ? sp[t * LDC + l1] : 0.f;
         } else {
             const bool v = FULL || (tv && s0 < S);
-            const int l = (FULL || s0 < S) ? s0 >> KB : 0;
+            const int l = (FULL || s0 < S) ? s0 >> KB : lpad;
             const int r0 = s0 & (R - 1);
             const float *pp = sp + t * LDC + l * KB, *pm = sm + t * LDC + l * KB;
             float fp[KB], fm[KB];
@@ -736,20 +741,17 @@ __device__ __forceinline__ void probs_st_(const float *sp, const float *sm, int 
                 fp[k] = pp[k];
                 fm[k] = pm[k];
             }
-            float hi;
-            if constexpr (KB == 2) {
-                hi = v ? 1.f : 0.f;
-            } else {
+            float hi = 1.f;
+            if constexpr (KB > 2) {
                 hi = ((r0 >> (KB - 1)) & 1) ? fp[0] : fm[0];
 #pragma unroll
                 for (int k = 1; k < KB - 2; ++k) hi *= ((r0 >> (KB - 1 - k)) & 1) ? fp[k] : fm[k];
-                hi = v ? hi : 0.f;
             }
             const float h0 = hi * fm[KB - 2], h1 = hi * fp[KB - 2];
-            P[nt][0] = h0 * fm[KB - 1];
-            P[nt][1] = h0 * fp[KB - 1];
-            P[nt][2] = h1 * fm[KB - 1];
-            P[nt][3] = h1 * fp[KB - 1];
+            P[nt][0] = v ? h0 * fm[KB - 1] : 0.f;
+            P[nt][1] = v ? h0 * fp[KB - 1] : 0.f;
+            P[nt][2] = v ? h1 * fm[KB - 1] : 0.f;
+            P[nt][3] = v ? h1 * fp[KB - 1] : 0.f;
         }
     }
 }
@@ -1461,17 +1463,18 @@ __host__ __device__ constexpr size_t bwd_wgs_per_cu(int nw, size_t bytes) {
     return (160 * 1024 / bytes) < (size_t)(8 / nw) ? 160 * 1024 / bytes : (size_t)(8 / nw);
 }
 
-// Sum of a per-thread value over the workgroup in a fixed order.
-template <int NTH> __device__ float block_sum(float v, float *scratch) {
-    scratch[threadIdx.x] = v;
+// Sum of a per-thread value over the workgroup in a fixed order, in fp64 (the
+// temperature and beta gradients: one sum over every token, whose terms can
+// cancel by orders of magnitude): a butterfly within each wave (every lane
+// ends with the same value), then the waves in order.
+template <int NTH> __device__ double block_sum_f64(double v, float *scratch) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    double *red = reinterpret_cast<double *>(scratch);
+    if (lane_id() == 0) red[wave_id()] = v;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float s = 0.f;
-        for (int j = 0; j < NTH; ++j) s += scratch[j];
-        scratch[0] = s;
-    }
-    __syncthreads();
-    const float r = scratch[0];
+    double r = 0.0;
+    for (int j = 0; j < NTH / 64; ++j) r += red[j];
     __syncthreads();
     return r;
 }
@@ -2452,7 +2455,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         a0[e] = (CarryA<T>)st[sidx(sg + 4 * g + e, D)];
         al[e] = 0.0;
     }
-    float tsum = 0.f;
+    CarryA<T> tsum = 0;  // this thread's share of sum du * th
 
     wait_state_loads();
     constexpr int NP = CAUSAL ? 2 : 1;  // transposed tiles: dO (and V)
@@ -2678,7 +2681,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     for (int e = 0; e < 4; ++e) al[e] = row_sum_f64(al[e]);
     if (i == 0)
         for (int e = 0; e < 4; ++e) out[sidx(sg + 4 * g + e, D)] = (float)al[e];
-    const float ts = block_sum<NTH>(tsum, sRed);
+    const double ts = block_sum_f64<NTH>((double)tsum, sRed);
     if (threadIdx.x == 0) a.tpart[((int64_t)n * a.nseg + seg) * a.nslice + z] = ts;
 }
 
@@ -2996,7 +2999,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         Ae[e] = FSTATE ? fs[sidx(sg + 4 * g + e, D)] : 0.0;
     }
     if constexpr (!CAUSAL) store_ut<T, SP>(sUT, sw, Ut, cst, po);  // constant totals
-    float tsum = 0.f;
+    CarryA<T> tsum = 0;  // this thread's share of sum du * th
 
     wait_state_loads();
     Prefetch<T, NTH, AL> pq_, pk_, pvn_;  // pvn_: non-causal V (natural only)
@@ -3378,7 +3381,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                                  vpart);
         }
     }
-    const float ts = block_sum<NTH>(tsum, sRed);
+    const double ts = block_sum_f64<NTH>((double)tsum, sRed);
     if (threadIdx.x == 0) a.tpart[((int64_t)(a.M * a.B * a.H + n) * a.nseg + seg) * a.nslice + z] = ts;
 }
 
@@ -3477,7 +3480,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
         __syncthreads();  // the hash table in LDS; its operand to registers
         ho.cache();
     }
-    float tsum = 0.f;
+    CarryA<T> tsum = 0;  // this thread's share of sum du * th
     Prefetch<T, NTH> px_;
     if (j0 < j1) px_.issue(xp, a.sq.t, (int64_t)j0 * TT, a.T);
     for (int jt = j0; jt < j1; ++jt) {
@@ -3516,7 +3519,7 @@ __global__ __launch_bounds__(threads_of(SP)) void k_probs(Args a) {
         }
     }
     if constexpr (BWD) {
-        const float ts = block_sum<NTH>(tsum, sRed);
+        const double ts = block_sum_f64<NTH>((double)tsum, sRed);
         if (threadIdx.x == 0) a.tpart[((int64_t)n * a.nseg + seg) * a.nslice + z] = ts;
     }
 }
@@ -3752,7 +3755,7 @@ __global__ __launch_bounds__(ELEM_THREADS) void k_slice_sum_gn(const T *part, co
 }
 
 // grad_inv_temp = sum of all partials, in a fixed order
-__global__ void k_temp_sum(const float *tpart, int64_t count, float *out) {
+__global__ void k_temp_sum(const double *tpart, int64_t count, float *out) {
     __shared__ double red[256];
     double acc = 0.0;
     for (int64_t j = threadIdx.x; j < count; j += blockDim.x) acc += tpart[j];

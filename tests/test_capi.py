@@ -65,11 +65,11 @@ def test_plan_sizes_c4():
     assert lib.race_fwd_workspace_bytes(ctypes.byref(d)) == 8 * 256 * 128 * 65 * 8
     # the backward runs 128 segments of 2 forward ones (1024 workgroups; the
     # 256-tile segment bound stops the joining there): (U, alpha) sums and
-    # suffixes fp32, and the [2][N][nseg][nslice] temperature partials
-    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 128 * 128 * 65 * 4 + 2 * 8 * 128 * 4
+    # suffixes fp32, and the [2][N][nseg][nslice] temperature partials fp64
+    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 128 * 128 * 65 * 4 + 2 * 8 * 128 * 8
     # an explicit seg_tiles keeps the forward's segmentation in the backward
     d.seg_tiles = 128
-    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 256 * 128 * 65 * 4 + 2 * 8 * 256 * 4
+    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 256 * 128 * 65 * 4 + 2 * 8 * 256 * 8
 
 
 def test_segments_bounded_at_long_sequences():
@@ -81,11 +81,11 @@ def test_segments_bounded_at_long_sequences():
     lib = _lib.load()
     d = _desc(T=1 << 22)
     assert lib.race_state_bytes(ctypes.byref(d)) == _state(8, 513)
-    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 512 * 128 * 65 * 4 + 2 * 8 * 512 * 4
+    assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 8 * 512 * 128 * 65 * 4 + 2 * 8 * 512 * 8
     d = _desc(T=37552128)
     assert lib.race_state_bytes(ctypes.byref(d)) == _state(8, 37552128 // 8192 + 1)
     assert lib.race_bwd_workspace_bytes(ctypes.byref(d)) == (2 * 8 * 4584 * 128 * 65 * 4 +
-                                                              -(-2 * 8 * 4584 * 4 // 16) * 16)
+                                                              -(-2 * 8 * 4584 * 8 // 16) * 16)
 
 
 def test_explicit_segments_above_the_walk_bound_rejected():
@@ -197,7 +197,7 @@ def test_sliced_plans(dtype, K, L, M, B, H, T, spad):
     xc = next(c for c in (8, 16, 32) if c >= min(cols, 32))
     xes = 4 if (1 << K) > SP else es
     xpart = -(-(nslice * N * T * xc * xes) // 16) * 16
-    lo, hi = 2 * N * row * 4, 2 * N * nseg * row * 4 + 2 * N * nseg * nslice * 4 + 16
+    lo, hi = 2 * N * row * 4, 2 * N * nseg * row * 4 + 2 * N * nseg * nslice * 8 + 16
     assert lo + part + 2 * xpart <= bw <= hi + part + 2 * xpart
 
 
@@ -360,7 +360,7 @@ def test_probs_argument_checks():
     assert lib.race_probs(ctypes.byref(d), None, p, p, None) == -1 and "x is NULL" in _lib.last_error()
     assert lib.race_probs(ctypes.byref(d), p, p, None, None) == -1 and "P is NULL" in _lib.last_error()
     need = lib.race_probs_bwd_workspace_bytes(ctypes.byref(d))
-    assert need == 8 * 2 * 4      # temperature partials: 8 streams x 2 segments (2 tiles), no slices
+    assert need == 8 * 2 * 8      # fp64 temperature partials: 8 streams x 2 segments (2 tiles), no slices
     rc = lib.race_probs_bwd(ctypes.byref(d), p, p, p, p, None, p, need - 1, None)
     assert rc == -3 and "workspace" in _lib.last_error()
 
