@@ -1,4 +1,5 @@
-"""No kernel takes a value from LDS it has not written.
+"""No kernel takes a value from LDS, or from a workspace, state or output
+buffer, that it has not written.
 
 LDS keeps what the previous workgroup on a CU left there.  A bucket slice
 (bf16 with K >= 5: 128 of the L * 2^K buckets; fp32: 32) projects only the
@@ -16,7 +17,11 @@ first column block (bf16 K=5 L=5 and K=6 L=5, fp32 K=4 L=5 and K=2 L=9),
 through the F1 operator, the key-weight / den form, the global normalisation
 and the probability outputs (before the padding rows were read from a
 projected table, 8 of those 10 gave NaN); the rest cover the other
-instantiation families."""
+instantiation families.
+
+The same cases run once more with every buffer the wrappers allocate
+(outputs, state, workspaces) filled with all-ones bytes before use: every
+output element must still be the one of a call with fresh buffers."""
 import ctypes
 import os
 
@@ -135,3 +140,31 @@ def test_outputs_ignore_lds_leftovers(dev, monkeypatch, name, mode, kw, it, seg)
         print(f"[{name} output {j}] NaN after LDS fills {nan}; bit-identical {torch.equal(a, b)}", flush=True)
         assert torch.isfinite(a).all(), f"{name} output {j}: non-finite without the fill"
         assert torch.equal(a, b), f"{name} output {j}: {nan} NaN, differs after the LDS fills"
+
+
+def _poisoned_empty(real_empty):
+    def empty(*args, **kw):
+        x = real_empty(*args, **kw)
+        if x.numel():
+            x.reshape(-1).view(torch.uint8).fill_(255)
+        return x
+    return empty
+
+
+@pytest.mark.parametrize("name,mode,kw,it,seg", CASES, ids=[c[0] for c in CASES])
+def test_outputs_ignore_buffer_contents(dev, monkeypatch, name, mode, kw, it, seg):
+    import types
+
+    from race_attention_amd import functional as F
+    q, k, v, do, planes = [x.to(dev) for x in make_case(seed=11, **kw)]
+    clean = _calls(mode, q, k, v, do, planes, kw, it, seg, torch.Generator().manual_seed(5))
+    fake = types.SimpleNamespace(**{a: getattr(torch, a) for a in dir(torch) if not a.startswith("__")})
+    fake.empty = _poisoned_empty(torch.empty)
+    fake.empty_like = lambda t, **kw_: fake.empty(t.shape, dtype=kw_.get("dtype", t.dtype),
+                                                  device=kw_.get("device", t.device))
+    monkeypatch.setattr(F, "torch", fake)
+    poisoned = _calls(mode, q, k, v, do, planes, kw, it, seg, torch.Generator().manual_seed(5))
+    torch.cuda.synchronize()
+    for j, (a, b) in enumerate(zip(clean, poisoned)):
+        print(f"[{name} output {j}] bit-identical with poisoned buffers {torch.equal(a, b)}", flush=True)
+        assert torch.equal(a, b), f"{name} output {j}: differs when the buffers start as all-ones bytes"
