@@ -8,6 +8,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <cmath>
 #include <mutex>
 #include <string>
 #include <type_traits>
@@ -318,12 +319,25 @@ template <typename T, int SP, int KB> constexpr bool al_compiled() {
 }
 bool whole_tiles(const race_desc *d, const Plan &p) { return d->T % TT == 0 && p.S == p.Spad; }
 
+// The causal F1 operator walks the forward state B back through each backward
+// segment (k_bwd_out); its whole-tile bf16 instantiations do it in fp32, the
+// others in fp64 (race_kernels.hip walk_f64).  A table's logits differ by at
+// most 2 K |inv_temp| (|tanh| <= 1 per bit), so at most e^(2 K |inv_temp|)
+// separates its largest and smallest probability: above K |inv_temp| = 2
+// (e^4), or with a temperature on the device, whole tiles take the segment
+// sums from the generic k_fwd_reduce (fp64) and walk B in fp64 in the
+// whole-tile k_bwd_out.  The forward and the backward of one descriptor choose
+// alike.
+bool exact_walk(const race_desc *d) {
+    return d->causal && (d->inv_temp_ptr != nullptr || (double)d->K * std::fabs((double)d->inv_temp) > 2.0);
+}
+
 template <typename T, int SP, int KB> int fwd_impl(const race_desc *d, const Plan &p, Args a, hipStream_t s) {
     const dim3 grid = tile_grid(p);
     constexpr bool ALC = al_compiled<T, SP, KB>();
     const bool al = ALC && whole_tiles(d, p);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
-        if (al)
+        if (al && !exact_walk(d))
             k_fwd_reduce<T, SP, KB, ALC><<<grid, threads_of(SP), 0, s>>>(a);
         else
             k_fwd_reduce<T, SP, KB><<<grid, threads_of(SP), 0, s>>>(a);
@@ -368,7 +382,9 @@ int bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_inv_temp, hi
         k_bwd_scan<<<dim3((elems + SCAN_THREADS - 1) / SCAN_THREADS, (unsigned)p.N), SCAN_THREADS, 0, s>>>(a.rstate, a.rdelta, p.nseg, elems,
                                                                             d->causal);
     if (run_phase(d, RACE_PHASE_OUT)) {
-        if (d->causal && al)
+        if (d->causal && al && exact_walk(d))
+            k_bwd_out<T, SP, true, KB, false, ALC, true><<<grid, threads_of(SP), 0, s>>>(a);
+        else if (d->causal && al)
             k_bwd_out<T, SP, true, KB, false, ALC><<<grid, threads_of(SP), 0, s>>>(a);
         else if (d->causal)
             k_bwd_out<T, SP, true, KB, false><<<grid, threads_of(SP), 0, s>>>(a);

@@ -1015,18 +1015,22 @@ __device__ __forceinline__ void frag_acc_hilo(const f32x4 &x0, const f32x4 &x1, 
 template <typename T, int SP, int KB> __host__ __device__ constexpr bool hl_ops() {
     return is_bf16<T>() && (KB <= 3 || (KB == 4 && SP <= 64));
 }
-// bf16 B state in fp64: k_fwd_reduce's segment sums and k_bwd_out's reverse
-// walk add the tiles' fp32 sums to fp64 totals instead of accumulating them
-// on the matrix core.  The walk derives B at a tile start as the state at the
-// segment end minus the later tiles' sums, so an fp32 walk carries an error
-// relative to the segment-end state; with a sharp softmax a bucket's B can
-// grow by orders of magnitude within a segment, and dA, whose factor
-// W / (A + eps) is largest where A (hence B) is smallest, takes that error as
-// it is.  Both sides change together: fp32 sums and an fp32 walk round the
-// same tile sums the same way, and their errors partly cancel.  The
-// whole-tile instantiations (4- and 8-bit, 128 buckets) keep the fp32
-// accumulators: they hold the registers of the two-wave occupancy of
-// k_bwd_out and the four-wave one of k_fwd_reduce.
+// bf16 B state in fp64: k_fwd_reduce's segment sums and k_bwd_out's
+// reverse walk add the tiles' fp32 sums to fp64 totals instead of
+// accumulating them on the matrix core.  The walk derives B at a tile start
+// as the state at the segment end minus the later tiles' sums, so an fp32
+// walk carries an error relative to the segment-end state; with a sharp
+// softmax a bucket's B can grow by orders of magnitude within a segment, and
+// dA, whose factor W / (A + eps) is largest where A (hence B) is smallest,
+// takes that error as it is.  Both sides change together: fp32 sums and an
+// fp32 walk round the same tile sums the same way, and their errors partly
+// cancel.  Every bf16 instantiation but the whole-tile ones (4- and 8-bit,
+// 128 buckets), whose fp32 accumulators keep the registers of k_bwd_out's
+// two-wave and k_fwd_reduce's four-wave occupancy.  Where the bucket
+// probabilities can span a wide range, the host runs whole tiles through the
+// generic k_fwd_reduce and the whole-tile k_bwd_out with XW (race_capi.hip
+// exact_walk): their tile sums come from the same P_K and V operands in the
+// same order, so the fp64 walk subtracts exactly what the sums added.
 template <typename T, bool AL> __host__ __device__ constexpr bool walk_f64() { return is_bf16<T>() && !AL; }
 // R = X - bf16(X) (exact in fp32): the lo part of a tile pair whose hi part is
 // the round-to-nearest operand the kernels take from X
@@ -2886,7 +2890,7 @@ __device__ void dv_finish(int md, int nt, f32x4 acc, const T *sG, const T *sGt, 
 // GN (global normalisation, causal only): W = P_Q rd and dA = gd P_Q per
 // token (rd = 1/max(den, eps), gd = dL/d den), so the reverse walk needs
 // neither the forward state nor G.
-template <typename T, int SP, bool CAUSAL, int KB, bool GN, bool AL = false>
+template <typename T, int SP, bool CAUSAL, int KB, bool GN, bool AL = false, bool XW = walk_f64<T, AL>()>
 __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
@@ -2896,6 +2900,11 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     // the walk back of the forward state subtracts the same P_K)
     constexpr bool PR = pair_tables<KB>();
     constexpr bool HL = hl_ops<T, SP, KB>();  // P_K, W and U as hi + lo pairs
+    // every bf16 instantiation: W as a hi + lo pair in dP_K's in-tile term
+    // sum_{t >= tau} M[tau][t] W[t][s], the leading bf16 rounding of dK (with a
+    // value mean, v.g is large and the softmax backward cancels what a table's
+    // buckets share of it)
+    constexpr bool WM = is_bf16<T>();
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
                   LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
@@ -2980,7 +2989,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     // fp32 MFMA accumulators and subtract the tile sums on the matrix core
     // (Bm); the others walk it in fp64 (Be, walk_f64).  A stays fp64: A(t)
     // is far below the segment-end value early in a sequence.
-    constexpr bool BM = is_bf16<T>() && !walk_f64<T, AL>();
+    constexpr bool BM = is_bf16<T>() && !XW;  // the walk of B in fp64 (walk_f64)
     double Be[4][4], Ae[4];
     f32x4 Bm[4];
     f32x4 al;
@@ -3200,7 +3209,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
         if constexpr (CAUSAL) {
             f32x4 Wi[2];  // W / (A + eps), the factor of dA
             f32x4 dA[2];
-            Frag<T> Wf, Pl, Wl;  // Pl, Wl: the lo parts of P_K and W (HL)
+            Frag<T> Wf, Pl, Wl;  // Pl, Wl: the lo parts of P_K (HL) and W (HL, WM)
             if constexpr (HL) {
                 f32x4 R[2];
                 lo_rem(PKr, R);
@@ -3209,7 +3218,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
             // W's operand, and with HL its lo part
             auto w_operands = [&](const f32x4 (&W)[2]) {
                 Wf = store_ts_operand<T, SP>(sWts, sw, W, cst);
-                if constexpr (HL) {
+                if constexpr (HL || WM) {
                     f32x4 R[2];
                     lo_rem(W, R);
                     Wl = token_operand<T>(R, cst, po);
@@ -3313,7 +3322,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
                     uo.template apply<NL>(dPK[nt], sV, nt);
                     const Frag<T> yo = ld_frag_pi(sY + (16 * nt + i) * LDT);
                     mma(dPK[nt], Wf, yo);
-                    if constexpr (HL) mma(dPK[nt], Wl, yo);
+                    if constexpr (HL || WM) mma(dPK[nt], Wl, yo);
                 }
                 for (int e = 0; e < 4; ++e) al[e] += tdA[e];
             }

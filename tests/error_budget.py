@@ -10,7 +10,9 @@ rounding:
   P      P_K as an MFMA operand: every sum over tokens of P_K (A, B, the
          in-tile triangles, dV) uses bf16 P_K (P_Q stays fp32 until it is
          part of W);
-  W      W = P_Q / (A(t) + eps) as an operand (outputs, U, dP_K, Sc, Sc2);
+  W      W = P_Q / (A(t) + eps) as an operand (outputs, U, Sc, Sc2; dP_K's
+         in-tile term takes W as an fp32-accurate hi + lo pair in every bf16
+         instantiation, so W never rounds there);
   B      the carried B_s at a tile start as a bf16 operand: O's carried part and
          the G of k_bwd_out (for dA).  (k_bwd_reduce's G, which feeds dQ, takes
          B as an fp32-accurate hi + lo pair, so it is never rounded there);
@@ -41,8 +43,9 @@ hl=True models the small-table instantiations (race_kernels.hip hl_ops: bf16
 with at most 3 hash bits, or 4 bits in at most 64 buckets), which take P_K,
 W and the carried U as fp32-accurate hi + lo operand pairs wherever a sum
 feeds the gradients' softmax backward: P_K in A, in B and in the in-tile G
-term; W in dP_K's in-tile term and in U; U in dP_K's v . U term.  P and W
-keep their rounding in the output triangles and dV, U in dV.
+term; W in U (and, as in every instantiation, in dP_K's in-tile term); U in
+dP_K's v . U term.  P and W keep their rounding in the output triangles and
+dV, U in dV.
 
 With every rounding off the restatement equals the oracle (tests/
 test_error_budget.py pins it there).  `python tests/error_budget.py [T]`
@@ -150,7 +153,7 @@ def stream(q, k, v, g, planes, it, eps, on=(), hl=False):
     for c in reversed(range(nt)):
         a, b = c * TT, min(T, c * TT + TT)
         pk, px, vv, gg, w = PKr[a:b], PKx[a:b], v[a:b], g[a:b], Wr[a:b]
-        wx = W[a:b] if hl else w                                      # W in dP_K's in-tile term and U
+        wx = W[a:b] if hl else w                                      # W in U
         At = A0[c] + np.cumsum(px, 0)
         inv = 1.0 / (At + eps)
         M = r["tri"](np.triu(vv @ gg.T))                             # M[tau, t] = v_tau . g_t, tau <= t
@@ -159,7 +162,7 @@ def stream(q, k, v, g, planes, it, eps, on=(), hl=False):
         dA = -W[a:b] * (gg @ r["B"](B0[c]).T + tri_g) * inv           # k_bwd_out: bf16 B; fp32 W
         alpha = alc + np.cumsum(dA[::-1], 0)[::-1]                    # suffix from tau on
         Ur = r["U"](Uc)
-        dPK = alpha + vv @ (Uc if hl else Ur).T + M @ wx              # sum_{t >= tau} M[tau, t] W[t, s]
+        dPK = alpha + vv @ (Uc if hl else Ur).T + M @ W[a:b]          # sum_{t >= tau} M[tau, t] W[t, s]: a pair
         Sc2 = r["tri"](np.triu(pk @ w.T))                             # Sc2[tau, t] = sum_s P_K W, t >= tau
         dv[a:b] = pk @ Ur + Sc2 @ gg
         Uc = Uc + wx.T @ gg

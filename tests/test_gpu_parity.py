@@ -216,6 +216,47 @@ def test_parity_flat_tables(dev, name, kw, causal, it, seg):
     compare(name, gpu, ref, TOL[q.dtype])
 
 
+# Whole tiles at sharp temperatures over long segments, from a randomised sweep of long walks (old dK in the
+# comment): the whole-tile instantiations walk B in fp32 unless K |inv_temp| > 2 or the temperature is a
+# device scalar (race_capi.hip exact_walk), and then in fp64.
+SHARP_CASES = [
+    # name, make_case kwargs (with seed), inv_temp, seg_tiles
+    ("sharp_K8L1_whole_seg128", dict(T=9376, H=1, L=1, K=8, v_shift=0.5, seed=1036), 2.0, 128),  # dk 2.5e-1
+    ("sharp_K4L8_whole_seg64", dict(T=3648, H=1, L=8, K=4, v_shift=1.0, seed=1025), 2.0, 64),  # dk 3.4e-1
+    ("sharp_K4L8_whole_seg256", dict(T=14528, H=1, L=8, K=4, seed=1057), 2.0, 256),  # dk 4.1e-2
+    ("sharp_K4L8_whole_tau1", dict(T=13280, H=1, L=8, K=4, v_shift=1.0, seed=1035), 1.0, 256),  # dk 2.3e-2
+]
+
+
+@pytest.mark.parametrize("name,kw,it,seg", SHARP_CASES, ids=[c[0] for c in SHARP_CASES])
+def test_parity_sharp_whole_tiles(dev, name, kw, it, seg):
+    q, k, v, do, planes = make_case(**kw)
+    gpu = run_gpu(q, k, v, do, planes, L=kw["L"], K=kw["K"], causal=True, inv_temp=it, dev=dev, seg_tiles=seg)
+    ref = run_oracle(q, k, v, do, planes, causal=True, inv_temp=it)
+    compare(name, gpu, ref, TOL[q.dtype])
+
+
+def test_device_temperature_takes_the_exact_walk(dev):
+    """A device temperature (race_desc.inv_temp_ptr) runs the fp64 walk whatever its value: at the default
+    temperature its result is within the bar of the oracle and close to the host temperature's fp32 walk."""
+    from race_attention_amd.functional import race_bwd_raw, race_fwd_raw
+    q, k, v, do, planes = make_case(T=2048, H=2, L=8, K=4, v_shift=0.5, seed=77)
+    it = 0.125
+    ref = run_oracle(q, k, v, do, planes, causal=True, inv_temp=it)
+    host = run_gpu(q, k, v, do, planes, L=8, K=4, causal=True, inv_temp=it, dev=dev, seg_tiles=64)
+    t = torch.tensor(it, device=dev)
+    qd, kd, vd, dod, pd = [x.to(dev) for x in (q, k, v, do, planes)]
+    out, st = race_fwd_raw(qd, kd, vd, pd, L=8, K=4, causal=True, inv_temp=t, seg_tiles=64)
+    dq, dk, dv, git = race_bwd_raw(qd, kd, vd, pd, dod, st, L=8, K=4, causal=True, inv_temp=t, seg_tiles=64)
+    torch.cuda.synchronize()
+    devt = (out.cpu(), dq.cpu(), dk.cpu(), dv.cpu(), float(git.cpu()))
+    compare("device temperature, fp64 walk", devt, ref, TOL[q.dtype])
+    for nm, a, b in zip(("out", "dq", "dk", "dv"), devt[:4], host[:4]):
+        e = relerr(to64(a), to64(b))
+        print(f"[device vs host temperature] {nm} {e:.2e}", flush=True)
+        assert e < 1e-2, (nm, e)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
 def test_t1_reference_eps_out_dv(dev, dtype):
     """T=1 at the reference eps (1e-6): out and dV are well conditioned there
