@@ -2900,11 +2900,12 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_out(Args a) {
     // the walk back of the forward state subtracts the same P_K)
     constexpr bool PR = pair_tables<KB>();
     constexpr bool HL = hl_ops<T, SP, KB>();  // P_K, W and U as hi + lo pairs
-    // every bf16 instantiation: W as a hi + lo pair in dP_K's in-tile term
-    // sum_{t >= tau} M[tau][t] W[t][s], the leading bf16 rounding of dK (with a
-    // value mean, v.g is large and the softmax backward cancels what a table's
-    // buckets share of it)
-    constexpr bool WM = is_bf16<T>();
+    // bf16 tables of up to 7 bits: W as a hi + lo pair in dP_K's in-tile term
+    // sum_{t >= tau} M[tau][t] W[t][s], the leading bf16 rounding of dK there
+    // (with a value mean, v.g is large and the softmax backward cancels what a
+    // table's buckets share of it).  An 8-bit table's 256 buckets spread W, and
+    // the single operand costs it no more than the other roundings do.
+    constexpr bool WM = is_bf16<T>() && KB < 8;
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP,
                   LDS_ = Ly::LDS_;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
