@@ -2292,6 +2292,20 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 // k_bwd_reduce: forward walk.  dQ, and per-segment sums of
 // alpha = sum_t dA and U = sum_t W^T g.
 // =====================================================================
+// GN with every bucket of the stream in one workgroup (bf16, K <= 4): gd
+// comes from the kernel's own G instead of the stored output,
+//   gd = dden - [den >= eps] rd^2 sum_s P_Q[t][s] G[s][t]
+// (sum_s P_Q G = dO . num in exact arithmetic; the O tile is not read).
+// dP_Q = G rd + gd A then has sum_s P_Q dP_Q = dden den to fp32 rounding, as
+// the exact gradient has, so a token whose keys all carry one value (t = 0:
+// out = v_0, exact dq = 0 without dden) gets no gradient from the roundings
+// of O, of P_K or of the in-tile v.g products -- which do not cancel where
+// den is small, and there outweigh the true gradient.  The in-tile products
+// enter G rounded to bf16 exactly as k_bwd_out's in-tile dP_K term takes
+// them (the same MFMA, the same rounding), so its t = tau terms, alpha's
+// gd P_Q against W v.g, cancel as well.
+template <typename T, int KB> __host__ __device__ constexpr bool gn_own_gd() { return !sliced<T, KB>(); }
+
 // GN backward, per token of the tile: with dc = max(den, eps) and the
 // forward's out = num / dc,
 //   rd = 1 / dc,  gd = dL/d den = dden - [den >= eps] (dO . O) rd.
@@ -2324,8 +2338,10 @@ __device__ void gn_token_terms(const T *sG, const T *sO, const float *sIn, float
 template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr int NW_ = SP / WB;
     static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>();
+    static constexpr bool GO = GN && !gn_own_gd<T, KB>();  // gd from the O tile
+    static constexpr bool GC = GN && gn_own_gd<T, KB>();   // gd from the kernel's G
     // token block: one tile's staged rows (Q, K, V, dO natural; V, dO
-    // transposed; GN: the O tile and (den, dden) [2][TT]; non-causal: dden [TT])
+    // transposed; GN: (den, dden) [2][TT] and, GO, the O tile; non-causal: dden [TT])
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
     static constexpr size_t oV = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
@@ -2333,7 +2349,7 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr size_t oVt = align16(oG + sizeof(T) * TT * LDN);
     static constexpr size_t oGt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
     static constexpr size_t oO = align16(oGt + sizeof(T) * D * LDT);
-    static constexpr size_t oTokIn = align16(oO + (GN ? sizeof(T) * TT * LDN : 0));
+    static constexpr size_t oTokIn = align16(oO + (GO ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t TB = align16(oTokIn + (GN || !CAUSAL ? sizeof(float) * 2 * TT : 0));
     // the rest, relative to its start
     static constexpr size_t rX = 0;  // (the in-tile v.g^T blocks live in each wave's registers)
@@ -2348,8 +2364,9 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr size_t rPair = align16(rHash + HashOps<T, 4>::bytes);
     static constexpr size_t rShare = align16(rPair + PairOps<T>::bytes);
     static constexpr size_t rTok = align16(rShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
-    // GN: the computed (rd, gd) [2][TT]
-    static constexpr size_t rEnd = align16(rTok + (GN ? sizeof(float) * 2 * TT : 0));
+    // GN: the computed (rd, gd) [2][TT]; GC: the waves' shares of sum_s P_Q G [NW_][TT]
+    static constexpr size_t rGs = align16(rTok + (GN ? sizeof(float) * 2 * TT : 0));
+    static constexpr size_t rEnd = align16(rGs + (GC ? sizeof(float) * NW_ * TT : 0));
     // two token blocks when they cost no workgroup per CU (160 KiB of LDS):
     // the next tile's rows then go to the other block while this tile still
     // reads its own, and the barrier ahead of that commit goes away
@@ -2358,13 +2375,14 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr size_t R0 = NB * TB;
     static constexpr size_t oX = R0 + rX, oDproj = R0 + rDproj, oPl = R0 + rPl, oPlLo = R0 + rPlLo, oPlT = R0 + rPlT,
                             oSig = R0 + rSig, oRed = R0 + rRed, oCst = R0 + rCst, oHash = R0 + rHash, oPair = R0 + rPair,
-                            oShare = R0 + rShare, oTok = R0 + rTok;
+                            oShare = R0 + rShare, oTok = R0 + rTok, oGs = R0 + rGs;
     static constexpr size_t bytes = R0 + rEnd;
 };
 
 // GN (global normalisation, causal only): with rd = 1/max(den, eps) and
-// gd = dL/d den per token (gn_token_terms, from the O and dO tiles),
-// W = P_Q rd, dP_Q = G rd + gd A_s(t), dA = gd P_Q.
+// gd = dL/d den per token (GO: gn_token_terms, from the O and dO tiles; GC:
+// from sum_s P_Q G after the tile's G, gn_own_gd), W = P_Q rd,
+// dP_Q = G rd + gd A_s(t), dA = gd P_Q.
 template <typename T, int SP, bool CAUSAL, int KB, bool GN, bool AL = false>
 __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
@@ -2376,6 +2394,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     // softmax backward reads directly
     constexpr bool PR = pair_tables<KB>();
     constexpr bool HL = hl_ops<T, SP, KB>();  // P_K and W as hi + lo pairs
+    constexpr bool GO = Ly::GO, GC = Ly::GC;   // GN: gd from the O tile / from G
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     // this tile's token block (block jt & 1 of two; block 0 of one)
@@ -2417,8 +2436,8 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     constexpr bool XF = xpart_f32(is_bf16<T>(), SP, KB);
     void *xpart = sliced<T, KB>() ? xpart_at<T, SP, KB>(a.dqpart, z, n, a) : nullptr;
     const int xc0 = ((z * SP) >> KB) * KB;  // first projection column of the slice's tables
-    float *sTok = (float *)(smem + Ly::oTok);
-    const T *op = GN ? (const T *)a.out + stream_off(a.so, n, a.B, a.H) : nullptr;
+    float *sTok = (float *)(smem + Ly::oTok), *sGs = (float *)(smem + Ly::oGs);
+    const T *op = GO ? (const T *)a.out + stream_off(a.so, n, a.B, a.H) : nullptr;
     const float *denp = GN ? a.den + (int64_t)n * a.T : nullptr;
     const float *ddp = (GN || !CAUSAL) && a.dden ? a.dden + (int64_t)n * a.T : nullptr;
     // one bucket slice writes the per-token terms for k_bwd_out
@@ -2463,7 +2482,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
 
     wait_state_loads();
     constexpr int NP = CAUSAL ? 2 : 1;  // transposed tiles: dO (and V)
-    Prefetch<T, NTH, AL> pq_, pk_, po_;  // po_: GN's O tile
+    Prefetch<T, NTH, AL> pq_, pk_, po_;  // po_: the O tile (GO)
     PrefetchT<T, NTH, NP, AL> pg_;  // non-causal dO
     PrefetchT2<T, NTH, AL, !is_bf16<T>()> pgv_;  // causal dO (first half of the waves) and V
     TokPre pt_;
@@ -2480,7 +2499,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
             pg_.template commit<NL>(0, (T *)(tb + Ly::oG), (T *)(tb + Ly::oGt));
         }
         if constexpr (GN) {
-            po_.template commit<NL>((T *)(tb + Ly::oO), nullptr);
+            if constexpr (GO) po_.template commit<NL>((T *)(tb + Ly::oO), nullptr);
             pt_.commit(tin);
         } else if constexpr (!CAUSAL) {
             if (ddp) pt_.commit(tin);
@@ -2496,7 +2515,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
             pg_.issue(0, gp, a.sdo.t, (int64_t)j0 * TT, a.T);
         }
         if constexpr (GN) {
-            po_.issue(op, a.so.t, (int64_t)j0 * TT, a.T);
+            if constexpr (GO) po_.issue(op, a.so.t, (int64_t)j0 * TT, a.T);
             pt_.issue(denp, ddp, (int64_t)j0 * TT, a.T);
         } else if constexpr (!CAUSAL) {
             if (ddp) pt_.issue(ddp, nullptr, (int64_t)j0 * TT, a.T);
@@ -2520,7 +2539,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
                 pg_.issue(0, gp, a.sdo.t, tn, a.T);
             }
             if constexpr (GN) {
-                po_.issue(op, a.so.t, tn, a.T);
+                if constexpr (GO) po_.issue(op, a.so.t, tn, a.T);
                 pt_.issue(denp, ddp, tn, a.T);
             } else if constexpr (!CAUSAL) {
                 if (ddp) pt_.issue(ddp, nullptr, tn, a.T);
@@ -2535,7 +2554,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
             issue();
             if (jt > j0) dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
         }
-        if constexpr (GN) gn_token_terms<T, NL, NW_>(sG, sO, sTokIn, sTok, a.eps, rdw, gdw, t0, a.T);
+        if constexpr (GO) gn_token_terms<T, NL, NW_>(sG, sO, sTokIn, sTok, a.eps, rdw, gdw, t0, a.T);
         for (int q = w; q < (CAUSAL ? 2 : 1) * pbk.tasks(); q += NW_) {
             const int r = pbk.task(q);
             if (q < pbk.tasks())
@@ -2575,9 +2594,11 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         float rd[2], gd[2], ae[4];  // ae: A at the tile start (+ eps unless GN)
         for (int e = 0; e < 4; ++e) ae[e] = GN ? (float)a0[e] : (float)a0[e] + a.eps;
         for (int nt = 0; nt < 2; ++nt) {
-            if constexpr (GN) {
+            if constexpr (GO) {
                 rd[nt] = sTok[16 * nt + i];
                 gd[nt] = sTok[TT + 16 * nt + i];
+            } else if constexpr (GC) {
+                rd[nt] = 1.0f / fmaxf(sTokIn[16 * nt + i], a.eps);
             }
             for (int e = 0; e < 4; ++e) {
                 const float A = CAUSAL ? ae[e] + Acum[nt][e] : ae[e];
@@ -2598,7 +2619,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
             Wl = token_operand<T>(R, cst, po);
         }
         // G[s][t] = g_t . B_s(t) = sum_d B[s][d] g[t][d] + sum_{tau<=t} P_K[tau][s] M[tau][t]
-        f32x4 dPQ[2], dA[2];
+        f32x4 dPQ[2], dA[2], Gv[2];  // Gv: G, kept for GC's gd
         {
             // The carried B enters G as an fp32-accurate operand pair (hi + lo, for bf16): with values
             // of non-zero mean, B_s carries a component common to all buckets that the softmax
@@ -2624,6 +2645,15 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
                 }
                 if constexpr (CAUSAL) mma(G, Pf, Xop[nt]);
                 if constexpr (CAUSAL && HL) mma(G, Pl, Xop[nt]);
+                if constexpr (GC) {
+                    // this wave's share of sum_s P_Q G; dP_Q follows the barrier
+                    Gv[nt] = G;
+                    float p = 0.f;
+                    for (int e = 0; e < 4; ++e) p += PQ[nt][e] * G[e];
+                    p = xor32_sum(xor16_sum(p));
+                    if (g == 0) sGs[w * TT + 16 * nt + i] = p;
+                    continue;
+                }
                 // dP_Q = G/(A+eps); dA = -W G/(A+eps).  GN: dP_Q = G rd + gd A; dA = gd P_Q
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (GN) {
@@ -2647,7 +2677,8 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         }
         // the lane's share of the segment's dA totals (summed over the row's
         // lanes after the walk)
-        for (int e = 0; e < 4; ++e) al[e] += (double)(dA[0][e] + dA[1][e]);
+        if constexpr (!GC)
+            for (int e = 0; e < 4; ++e) al[e] += (double)(dA[0][e] + dA[1][e]);
         // U^T[d][s] += sum_t g[t][d] W[t][s]; carry B^T[d][s] += sum_t V[t][d] P_K[t][s]
         for (int md = 0; md < 4; ++md) {
             const Frag<T> go = col_operand<T, NL>(sG, sGt, md);
@@ -2661,6 +2692,26 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         }
         if constexpr (CAUSAL)
             for (int e = 0; e < 4; ++e) a0[e] += (CarryA<T>)tot[e];
+        if constexpr (GC) {
+            __syncthreads();  // every wave's share of sum_s P_Q G
+            for (int nt = 0; nt < 2; ++nt) {
+                const int t = 16 * nt + i;
+                float sq = 0.f;
+#pragma unroll
+                for (int v = 0; v < NW_; ++v) sq += sGs[v * TT + t];
+                const float dn = sTokIn[t];
+                gd[nt] = sTokIn[TT + t] - (dn >= a.eps ? rd[nt] * rd[nt] * sq : 0.f);
+                if (rdw && w == 0 && g == 0 && t < tile_rows(t0, a.T)) {
+                    rdw[t0 + t] = rd[nt];
+                    gdw[t0 + t] = gd[nt];
+                }
+                for (int e = 0; e < 4; ++e) {
+                    dPQ[nt][e] = Gv[nt][e] * inv[nt][e] + gd[nt] * Ag[nt][e];
+                    dA[nt][e] = gd[nt] * PQ[nt][e];
+                }
+            }
+            for (int e = 0; e < 4; ++e) al[e] += (double)(dA[0][e] + dA[1][e]);
+        }
         if constexpr (KB <= 4) {
             tsum += softhash_bwd<KB, T>(PQ, dPQ, sSpQ, sSmQ, sThQ, sg, a.L, a.inv_temp, sDproj, ho);
         } else {

@@ -93,6 +93,38 @@ def test_global_parity(dev, name, kw, beta, seg, floor, with_dden):
     _compare(name, gpu, ref, TOL[q.dtype])
 
 
+# Token 0 sees only its own key, so out_0 = v_0 whatever P_Q is, and with no
+# den gradient the exact dq_0 is zero.  Where den_0 is small (sharp beta, q_0
+# and k_0 in different buckets) any rounding that keeps dP_Q[0][s] from
+# cancelling shows up at full size in dq_0: the bf16 kernels with every bucket
+# in one workgroup (K <= 4) form dL/d den from their own G, sum_s P_Q G, for
+# which the cancellation holds to fp32 rounding.  Cases: T not a multiple of
+# 32 over several segments (and one whole-tile case), independent planes.
+FIRST_TOKEN_CASES = [
+    ("K4L6_beta2", dict(L=6, K=4), 2.0),
+    ("K4L5_beta3", dict(L=5, K=4), 3.0),
+    ("K4L8_beta4_whole", dict(L=8, K=4, T=1024), 4.0),
+    ("K3L8_beta3_pairs", dict(L=8, K=3), 3.0),
+    ("K2L5_beta4_pairs", dict(L=5, K=2), 4.0),
+    ("K1L7_beta3_pairs", dict(L=7, K=1), 3.0),
+]
+
+
+@pytest.mark.parametrize("name,kw,beta", FIRST_TOKEN_CASES, ids=[c[0] for c in FIRST_TOKEN_CASES])
+def test_global_first_token_gradient(dev, name, kw, beta):
+    args = dict(M=2, B=1, T=318, H=3, seed=58004, share_planes=False)
+    args.update(kw)
+    q, k, v, do, planes = make_case(**args)
+    gpu = _run_gpu(q, k, v, do, None, planes, L=kw["L"], K=kw["K"], beta=beta, dev=dev, seg_tiles=3)
+    ref = _run_oracle(q, k, v, do, None, planes, beta=beta)
+    scale = np.abs(ref[2]).max()
+    first = np.abs(to64(gpu[2])[:, :, 0]).max() / scale
+    print(f"[{name}] |dq_0| / max|dq| = {first:.2e}", flush=True)
+    assert np.abs(ref[2][:, :, 0]).max() <= 1e-12 * scale  # the oracle's zero
+    assert first <= 1e-5, f"{name}: dq at t = 0 is {first:.2e} of max|dq|"
+    _compare("first_token_" + name, gpu, ref, TOL[q.dtype])
+
+
 def test_global_deterministic(dev):
     q, k, v, do, planes = make_case(B=1, T=333, H=2, L=8, K=4, seed=3)
     dden = torch.randn(1, 1, 2, 333, generator=torch.Generator().manual_seed(1))
