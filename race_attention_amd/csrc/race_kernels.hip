@@ -2364,8 +2364,8 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr size_t rPair = align16(rHash + HashOps<T, 4>::bytes);
     static constexpr size_t rShare = align16(rPair + PairOps<T>::bytes);
     static constexpr size_t rTok = align16(rShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
-    // GN: the computed (rd, gd) [2][TT]; GC: the waves' shares of sum_s P_Q G [NW_][TT]
-    static constexpr size_t rGs = align16(rTok + (GN ? sizeof(float) * 2 * TT : 0));
+    // GO: the computed (rd, gd) [2][TT]; GC: the waves' shares of sum_s P_Q G [NW_][TT]
+    static constexpr size_t rGs = align16(rTok + (GO ? sizeof(float) * 2 * TT : 0));
     static constexpr size_t rEnd = align16(rGs + (GC ? sizeof(float) * NW_ * TT : 0));
     // two token blocks when they cost no workgroup per CU (160 KiB of LDS):
     // the next tile's rows then go to the other block while this tile still
