@@ -2634,6 +2634,22 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
             }
             Frag<T> Xop[2];
             if constexpr (CAUSAL) x_operands<T, NL>(sV, sG, Xop);
+            if constexpr (GO && is_bf16<T>()) {
+                // The stream's first token sees only its own key, so out_0 = v_0
+                // and dO.out_0 = dO.v_0 exactly: taken as G takes it (the rounded
+                // in-tile product, lane 0's first slot, the same in every wave
+                // and slice) rather than from the stored O, whose rounding does
+                // not cancel against G where den_0 is small
+                if (t0 == 0) {
+                    const float m00 = __builtin_bit_cast(
+                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, (float)Xop[0].v[0]), 0));
+                    if (i == 0) {
+                        const float dn = sTokIn[0];
+                        gd[0] = sTokIn[TT] - (dn >= a.eps ? m00 * rd[0] : 0.f);
+                        if (gdw && w == 0 && g == 0) gdw[0] = gd[0];  // after gn_token_terms' write, same lane
+                    }
+                }
+            }
             for (int nt = 0; nt < 2; ++nt) {
                 f32x4 G = zero4();
                 const Frag<T> g0 = NL::frag_pi(sG, 16 * nt + i, 0), g1 = NL::frag_pi(sG, 16 * nt + i, 1);

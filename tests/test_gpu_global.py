@@ -97,9 +97,11 @@ def test_global_parity(dev, name, kw, beta, seg, floor, with_dden):
 # den gradient the exact dq_0 is zero.  Where den_0 is small (sharp beta, q_0
 # and k_0 in different buckets) any rounding that keeps dP_Q[0][s] from
 # cancelling shows up at full size in dq_0: the bf16 kernels with every bucket
-# in one workgroup (K <= 4) form dL/d den from their own G, sum_s P_Q G, for
-# which the cancellation holds to fp32 rounding.  Cases: T not a multiple of
-# 32 over several segments (and one whole-tile case), independent planes.
+# in one workgroup (K <= 4) form dL/d den from their own G, sum_s P_Q G, and
+# the bucket-slice kernels (K >= 5) take token 0's dO . out as dO . v_0 rounded
+# as G rounds it; either way the cancellation holds to fp32 rounding.  Cases:
+# T not a multiple of 32 over several segments (and one whole-tile case),
+# independent planes.
 FIRST_TOKEN_CASES = [
     ("K4L6_beta2", dict(L=6, K=4), 2.0),
     ("K4L5_beta3", dict(L=5, K=4), 3.0),
@@ -107,6 +109,10 @@ FIRST_TOKEN_CASES = [
     ("K3L8_beta3_pairs", dict(L=8, K=3), 3.0),
     ("K2L5_beta4_pairs", dict(L=5, K=2), 4.0),
     ("K1L7_beta3_pairs", dict(L=7, K=1), 3.0),
+    ("K5L4_beta3_sliced", dict(L=4, K=5), 3.0),
+    ("K6L3_beta2_2slices", dict(L=3, K=6), 2.0),
+    ("K8L1_beta1_2slices", dict(L=1, K=8), 1.0),
+    ("K8L4_beta2_8slices_whole", dict(L=4, K=8, T=1024), 2.0),
 ]
 
 
