@@ -175,6 +175,113 @@ def stream(q, k, v, g, planes, it, eps, on=(), hl=False):
     return tuple(r["out"](x) for x in (out, dq, dk, dv))
 
 
+def stream_gn(q, k, v, g, h, planes, beta, floor, on=(), hl=False, own_gd=True, slice_parts=False):
+    """One causal stream of the globally normalised operator (F2): num = sum_s
+    P_Q B_s(t), den = sum_s P_Q A_s(t) over all tables, out = num / max(den,
+    floor); h [T] is the upstream gradient of den.  The same switches as
+    `stream`, placed where the GN kernels round:
+      forward   W = P_Q as an operand (outputs, Sc), den from fp32 P_Q and A;
+      backward  G with B as a hi + lo pair and the in-tile M rounded (tri);
+                gd = h - [den >= floor] rd^2 sum_s P_Q G (own_gd: bf16 with
+                K <= 4) or h - [den >= floor] rd dO.y with y the stored
+                output, except token 0, which takes dO.v_0 as G does (M[0, 0]);
+                W = P_Q rd as an operand in U, Sc2 and dV, an fp32-accurate
+                pair in dP_K's in-tile term for tables up to 7 bits.
+    slice_parts: the bucket-slice kernels round each 128-bucket slice's
+    numerator and dV (its own Sc, Sc2 blocks) to bf16 (as "out") before the
+    slices are summed (and the numerator divided).
+    Returns out, den, dq, dk, dv [T, D] ([T] for den)."""
+    r = {name: (bf16 if name in on else (lambda x: x)) for name in ROUNDINGS}
+    T, D = q.shape
+    L, K, _ = planes.shape
+    PQ, thq = soft_hash(q, planes, beta)
+    PK, thk = soft_hash(k, planes, beta)
+    PKr = r["P"](PK)
+    PKx = PK if hl else PKr  # P_K in A, B and the in-tile G term
+    S = PK.shape[1]
+    nt = (T + TT - 1) // TT
+    A0 = np.zeros((nt, S))
+    B0 = np.zeros((nt, S, D))
+    out = np.zeros((T, D))
+    den = np.zeros(T)
+    Ac = np.zeros(S)
+    Bc = np.zeros((S, D))
+    nz = (S + SLICE - 1) // SLICE if slice_parts else 1
+    for c in range(nt):
+        a, b = c * TT, min(T, c * TT + TT)
+        A0[c], B0[c] = Ac, Bc
+        pk, px, vv = PKr[a:b], PKx[a:b], v[a:b]
+        At = Ac + np.cumsum(px, 0)
+        den[a:b] = (PQ[a:b] * At).sum(1)
+        w = r["W"](PQ[a:b])
+        num = np.zeros((b - a, D))
+        for z in range(nz):
+            sl = slice(z * SLICE, (z + 1) * SLICE) if slice_parts else slice(0, S)
+            Sc = r["tri"](np.tril(w[:, sl] @ pk[:, sl].T))
+            part = w[:, sl] @ r["B"](Bc[sl]) + Sc @ vv
+            num += r["out"](part) if slice_parts else part
+        out[a:b] = num / np.maximum(den[a:b], floor)[:, None]
+        Bc = Bc + px.T @ vv
+        Ac = Ac + px.sum(0)
+    y = r["out"](out)
+    act = den >= floor
+    rd = 1.0 / np.maximum(den, floor)
+    dq_proj = np.zeros((T, L * K))
+    dk_proj = np.zeros((T, L * K))
+    dv = np.zeros((T, D))
+    Uc = np.zeros((S, D))
+    alc = np.zeros(S)
+    for c in reversed(range(nt)):
+        a, b = c * TT, min(T, c * TT + TT)
+        pk, px, vv, gg = PKr[a:b], PKx[a:b], v[a:b], g[a:b]
+        At = A0[c] + np.cumsum(px, 0)
+        M = r["tri"](np.triu(vv @ gg.T))
+        G = gg @ B0[c].T + M.T @ px
+        if own_gd:
+            gd = h[a:b] - act[a:b] * rd[a:b] ** 2 * (PQ[a:b] * G).sum(1)
+        else:
+            dot = (gg * y[a:b]).sum(1)
+            if a == 0:
+                dot[0] = M[0, 0]
+            gd = h[a:b] - act[a:b] * rd[a:b] * dot
+        dPQ = G * rd[a:b, None] + gd[:, None] * At
+        dA = gd[:, None] * PQ[a:b]
+        W = PQ[a:b] * rd[a:b, None]
+        w = r["W"](W)
+        wx = W if hl else w
+        alpha = alc + np.cumsum(dA[::-1], 0)[::-1]
+        Ur = r["U"](Uc)
+        dPK = alpha + vv @ (Uc if hl else Ur).T + M @ (W if (hl or K < 8) else w)
+        for z in range(nz):
+            sl = slice(z * SLICE, (z + 1) * SLICE) if slice_parts else slice(0, S)
+            Sc2 = r["tri"](np.triu(pk[:, sl] @ w[:, sl].T))
+            part = pk[:, sl] @ Ur[sl] + Sc2 @ gg
+            dv[a:b] += r["out"](part) if slice_parts else part
+        Uc = Uc + wx.T @ gg
+        alc = alc + dA.sum(0)
+        dq_proj[a:b] = soft_hash_bwd(PQ[a:b], dPQ, thq[a:b], planes, beta)
+        dk_proj[a:b] = soft_hash_bwd(PK[a:b], dPK, thk[a:b], planes, beta)
+    pl = planes.reshape(L * K, D)
+    dq = r["dproj"](dq_proj) @ r["dproj"](pl)
+    dk = r["dproj"](dk_proj) @ r["dproj"](pl)
+    return y, den, r["out"](dq), r["out"](dk), r["out"](dv)
+
+
+def run_gn(q, k, v, g, h, planes, beta, floor=1e-6, on=(), hl=False, own_gd=True, slice_parts=False):
+    """F2 over [M,B,T,H,D] arrays (h: [M,B,H,T] or None), planes [NP,L,K,D]
+    (NP = 1 or M) -> out, den [M,B,H,T], dq, dk, dv."""
+    M, B, T, H, D = q.shape
+    res = [np.zeros_like(q), np.zeros((M, B, H, T))] + [np.zeros_like(q) for _ in range(3)]
+    for m, bb, hh in itertools.product(range(M), range(B), range(H)):
+        hv = h[m, bb, hh] if h is not None else np.zeros(T)
+        o = stream_gn(q[m, bb, :, hh], k[m, bb, :, hh], v[m, bb, :, hh], g[m, bb, :, hh], hv,
+                      planes[m if planes.shape[0] > 1 else 0], beta, floor, on, hl, own_gd, slice_parts)
+        res[0][m, bb, :, hh], res[1][m, bb, hh] = o[0], o[1]
+        for x, y in zip(res[2:], o[2:]):
+            x[m, bb, :, hh] = y
+    return tuple(res)
+
+
 def run(q, k, v, g, planes, it, eps=1e-6, on=(), hl=False):
     """[M,B,T,H,D] arrays (bf16-valued), planes [1,L,K,D] -> out, dq, dk, dv of the same shape."""
     res = [np.zeros_like(q) for _ in range(4)]

@@ -65,3 +65,58 @@ def test_small_table_operand_pairs():
     assert max(pairs[1:3]) < 6e-3, pairs
     none = eb.run(q, k, v, g, planes, it, hl=True)
     assert max(eb.relerr(a, b) for a, b in zip(none, exact)) < 1e-11
+
+
+def _gn_case(K, L, T, seed, dden):
+    rng = np.random.default_rng(seed)
+    nrm = lambda x: x / np.linalg.norm(x, axis=-1, keepdims=True)  # noqa: E731
+    q, k, v = (eb.bf16(nrm(rng.standard_normal((2, 1, T, 2, 64)))) for _ in range(3))
+    g = eb.bf16(rng.standard_normal((2, 1, T, 2, 64)))
+    h = rng.standard_normal((2, 1, 2, T)) if dden else None
+    planes = rng.standard_normal((2, L, K, 64)).astype(np.float32).astype(np.float64)
+    return q, k, v, g, h, planes
+
+
+def test_gn_restatement_is_the_operator(oracle):
+    """The globally normalised restatement (stream_gn) with no rounding equals
+    the fp64 F2 oracle, out, den and every gradient, with either form of
+    dL/d den (the kernels' own sums, or dO . out with token 0 as dO . v_0) and
+    with the slice partials summed."""
+    for K, L, T, beta, dden in ((4, 8, 100, 1.0, True), (2, 5, 70, 3.0, False), (6, 3, 90, 2.0, True)):
+        q, k, v, g, h, planes = _gn_case(K, L, T, K, dden)
+        o, den = oracle.race_global_forward(q, k, v, planes, beta=beta)
+        dq, dk, dv, _ = oracle.race_global_backward(q, k, v, g, planes, dden=h, beta=beta)
+        for own_gd in (True, False):
+            got = eb.run_gn(q, k, v, g, h, planes, beta, own_gd=own_gd, slice_parts=K > 4)
+            for name, a, b in zip(("out", "den", "dq", "dk", "dv"), got, (o, den, dq, dk, dv)):
+                e = eb.relerr(a, b)
+                assert e < 1e-11, (K, own_gd, name, e)
+
+
+def test_gn_first_token_cancels_with_every_rounding():
+    """Token 0's dq is exactly zero without dden (out_0 = v_0).  With every
+    bf16 rounding on, both forms of dL/d den the kernels use keep it zero to
+    fp64 rounding: the kernels' own sum_s P_Q G, and dO . v_0 taken as G takes
+    it.  dO . y_0 with the stored bf16 output does not."""
+    q, k, v, g, _, planes = _gn_case(4, 6, 64, 7, False)
+    beta = 3.0
+    exact = eb.run_gn(q, k, v, g, None, planes, beta)
+    scale = np.abs(exact[2]).max()
+    for own_gd in (True, False):
+        got = eb.run_gn(q, k, v, g, None, planes, beta, on=eb.ROUNDINGS, own_gd=own_gd)
+        assert np.abs(got[2][:, :, 0]).max() <= 1e-12 * scale, own_gd
+    # the stored output at token 0: y_0 = bf16(out_0) against G's rounded dO . v_0
+    L, K = planes.shape[1], planes.shape[2]
+    worst = 0.0
+    for m in range(2):
+        for hh in range(2):
+            PQ, thq = eb.soft_hash(q[m, 0, :1, hh], planes[m], beta)
+            PK, _ = eb.soft_hash(k[m, 0, :1, hh], planes[m], beta)
+            PKr = eb.bf16(PK)
+            den0 = float((PQ * PKr).sum())
+            y0 = eb.bf16((eb.bf16(PQ) @ PKr.T)[0, 0] * v[m, 0, 0, hh] / den0)
+            m00 = eb.bf16(np.array(v[m, 0, 0, hh] @ g[m, 0, 0, hh]))
+            dP = PKr * (m00 - g[m, 0, 0, hh] @ y0) / den0
+            dq0 = eb.soft_hash_bwd(PQ, dP, thq, planes[m], beta) @ planes[m].reshape(L * K, 64)
+            worst = max(worst, float(np.abs(dq0).max()))
+    assert worst > 5e-4 * scale  # 1.4e-3 here, against 1e-16 for the two forms above
