@@ -169,9 +169,9 @@ int race_fwd_global(const race_desc *d, const void *q, const void *k,
  * (misc/elsaa_causal_complete.py:392-436) and the autograd of the module's
  * phi and division: out and den are the forward's outputs, dout the
  * gradient of out, dden (nullable = zero) the gradient of den, fp32 like den.
- * grad_beta (nullable, device fp32 scalar) receives dL/d(beta).  bf16 with
- * K <= 4 forms dL/d den from the kernel's bucket sums (sum_s P_Q dout.B_s)
- * and does not read out; the other configurations use dout.out. */
+ * grad_beta (nullable, device fp32 scalar) receives dL/d(beta).  dL/d den
+ * is formed from the kernels' bucket sums (sum_s P_Q dout.B_s; bucket slices:
+ * summed over the slices by a pre-pass), so out is validated but not read. */
 int race_bwd_global(const race_desc *d, const void *q, const void *k,
                     const void *v, const float *planes, const void *out,
                     const float *den, const void *dout, const float *dden,

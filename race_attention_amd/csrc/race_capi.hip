@@ -66,7 +66,8 @@ struct Plan {
     size_t fws_core = 0, bws_core = 0, part_bytes = 0;  // partial-output buffers follow the core
     size_t xpart_bytes = 0;  // sliced dX partials (dproj columns), one buffer each for dQ and dK
     // global normalisation: den partials after the forward workspace; rden
-    // and gden [N][T] after the backward workspace
+    // and gden [N][T] after the backward workspace, then (sliced) the slices'
+    // shares of sum_s P_Q dO.B_s [nslice][N][T]
     size_t gfws = 0, gbws = 0, tok_bytes = 0;
 };
 
@@ -179,7 +180,7 @@ int make_plan(const race_desc *d, Plan &p, bool bwd = false, bool walks = true) 
     p.bws = p.bws_core + 2 * p.xpart_bytes + p.part_bytes;     // dproj columns for dQ, dK; partial dV
     p.tok_bytes = align16((size_t)p.N * d->T * sizeof(float));
     p.gfws = p.fws + (p.parts ? p.nslice * p.tok_bytes : 0);
-    p.gbws = p.bws + 2 * p.tok_bytes;
+    p.gbws = p.bws + 2 * p.tok_bytes + (p.parts ? p.nslice * p.tok_bytes : 0);  // + the slices' gsum
     return RACE_OK;
 }
 
@@ -438,6 +439,16 @@ int gn_bwd_impl(const race_desc *d, const Plan &p, Args a, float *grad_beta, hip
     constexpr bool ALC = al_compiled<T, SP, KB>();
     const bool al = ALC && whole_tiles(d, p);
     if (run_phase(d, RACE_PHASE_REDUCE)) {
+        if constexpr (sliced<T, KB>()) {
+            // each slice's share of sum_s P_Q G per token, then rd and gd
+            if (al)
+                k_bwd_reduce<T, SP, true, KB, true, ALC, true><<<grid, threads_of(SP), 0, s>>>(a);
+            else
+                k_bwd_reduce<T, SP, true, KB, true, false, true><<<grid, threads_of(SP), 0, s>>>(a);
+            const int64_t nt = p.N * d->T;
+            k_gn_terms<<<elem_blocks(nt), ELEM_THREADS, 0, s>>>(a.gsum, p.nslice, nt, a.den, a.dden, d->eps, a.rden,
+                                                                a.gden);
+        }
         if (al)
             k_bwd_reduce<T, SP, true, KB, true, ALC><<<grid, threads_of(SP), 0, s>>>(a);
         else
@@ -900,6 +911,7 @@ int race_bwd_global(const race_desc *d, const void *q, const void *k, const void
     a.dden = dden;
     a.rden = (float *)((char *)ws + p.bws);
     a.gden = (float *)((char *)ws + p.bws + p.tok_bytes);
+    a.gsum = p.parts ? (float *)((char *)ws + p.bws + 2 * p.tok_bytes) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     if (d->dtype == RACE_DTYPE_BF16) return gn_bwd_dispatch<bf16>(d, p, a, grad_beta, s);
     return gn_bwd_dispatch<float>(d, p, a, grad_beta, s);

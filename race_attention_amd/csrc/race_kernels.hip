@@ -83,6 +83,9 @@ struct Args {
     float *den, *denpart;
     const float *dden;
     float *rden, *gden;
+    // bucket slices: each slice's share of sum_s P_Q G per token [nslice][N][T]
+    // (the k_bwd_reduce pre-pass), summed by k_gn_terms into rden / gden
+    float *gsum;
     // per-token key weights [B][T] on P_K (non-causal padding mask; nullable).
     // Non-causal F1 also writes den [N][T] when den is set and reads dden.
     const float *kw;
@@ -2292,10 +2295,9 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 // k_bwd_reduce: forward walk.  dQ, and per-segment sums of
 // alpha = sum_t dA and U = sum_t W^T g.
 // =====================================================================
-// GN with every bucket of the stream in one workgroup (bf16, K <= 4): gd
-// comes from the kernel's own G instead of the stored output,
-//   gd = dden - [den >= eps] rd^2 sum_s P_Q[t][s] G[s][t]
-// (sum_s P_Q G = dO . num in exact arithmetic; the O tile is not read).
+// GN: gd = dL/d den per token is formed from the kernels' own sums,
+//   gd = dden - [den >= eps] rd^2 S_t,   S_t = sum_s P_Q[t][s] G[s][t]
+// (S_t = dO . num in exact arithmetic; the stored output is not read).
 // dP_Q = G rd + gd A then has sum_s P_Q dP_Q = dden den to fp32 rounding, as
 // the exact gradient has, so a token whose keys all carry one value (t = 0:
 // out = v_0, exact dq = 0 without dden) gets no gradient from the roundings
@@ -2304,52 +2306,27 @@ __global__ __launch_bounds__(threads_of(SP), SP == 128 ? 4 : 1) void k_fwd_out(A
 // enter G rounded to bf16 exactly as k_bwd_out's in-tile dP_K term takes
 // them (the same MFMA, the same rounding), so its t = tau terms, alpha's
 // gd P_Q against W v.g, cancel as well.
+// With every bucket of the stream in one workgroup (bf16, K <= 4: GC) the
+// kernel sums S_t itself, over its waves, after the tile's G.  Bucket slices
+// (GS) take it from a pre-pass: the same kernel with GP set walks the tiles
+// as far as G and writes its slice's share of S_t; k_gn_terms adds the
+// shares and writes rd and gd per token for the second pass and k_bwd_out.
 template <typename T, int KB> __host__ __device__ constexpr bool gn_own_gd() { return !sliced<T, KB>(); }
-
-// GN backward, per token of the tile: with dc = max(den, eps) and the
-// forward's out = num / dc,
-//   rd = 1 / dc,  gd = dL/d den = dden - [den >= eps] (dO . O) rd.
-// dO and O are natural tiles of one layout (the dot product reads both at the
-// same physical offsets); den, dden come from sIn [2][TT].  Results go to
-// sOut [2][TT] and, when rdw is set, to rdw / gdw [t] for k_bwd_out.  A wave
-// takes 4 tokens per pass, 16 lanes x 4 d each.
-template <typename T, class NL, int NW_>
-__device__ void gn_token_terms(const T *sG, const T *sO, const float *sIn, float *sOut, float eps, float *rdw,
-                               float *gdw, int64_t t0, int64_t Tn) {
-    const int w = wave_id(), r = lane_id() >> 4, c = lane_id() & 15;
-    for (int tb = 4 * w; tb < TT; tb += 4 * NW_) {
-        const int t = tb + r;
-        const int o = NL::P ? sw_off<T, D>(t, 4 * c) : t * NL::LD + 4 * c;
-        const f32x4 g = load4<T>(sG + o), y = load4<T>(sO + o);
-        const float dot = row_sum(g[0] * y[0] + g[1] * y[1] + g[2] * y[2] + g[3] * y[3]);
-        const float dn = sIn[t], rd = 1.0f / fmaxf(dn, eps);
-        const float gd = sIn[TT + t] - (dn >= eps ? dot * rd : 0.f);
-        if (c == 0) {
-            sOut[t] = rd;
-            sOut[TT + t] = gd;
-            if (rdw && t < tile_rows(t0, Tn)) {
-                rdw[t0 + t] = rd;
-                gdw[t0 + t] = gd;
-            }
-        }
-    }
-}
 
 template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr int NW_ = SP / WB;
     static constexpr int LDN = NatL<T, true>::LD, LDT = ldp_of<T>(TT), LDC = ld_of<float>(NCOL), LDDP = sw_ld<T, NCOL>();
-    static constexpr bool GO = GN && !gn_own_gd<T, KB>();  // gd from the O tile
-    static constexpr bool GC = GN && gn_own_gd<T, KB>();   // gd from the kernel's G
+    static constexpr bool GS = GN && !gn_own_gd<T, KB>();  // gd per token from k_gn_terms
+    static constexpr bool GC = GN && gn_own_gd<T, KB>();   // gd from this kernel's own sums
     // token block: one tile's staged rows (Q, K, V, dO natural; V, dO
-    // transposed; GN: (den, dden) [2][TT] and, GO, the O tile; non-causal: dden [TT])
+    // transposed; GN: (den, dden) [2][TT], GS (den, gd); non-causal: dden [TT])
     static constexpr size_t oQ = 0;
     static constexpr size_t oK = align16(oQ + sizeof(T) * TT * LDN);
     static constexpr size_t oV = align16(oK + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oG = align16(oV + (CAUSAL ? sizeof(T) * TT * LDN : 0));
     static constexpr size_t oVt = align16(oG + sizeof(T) * TT * LDN);
     static constexpr size_t oGt = align16(oVt + (CAUSAL ? sizeof(T) * D * LDT : 0));
-    static constexpr size_t oO = align16(oGt + sizeof(T) * D * LDT);
-    static constexpr size_t oTokIn = align16(oO + (GO ? sizeof(T) * TT * LDN : 0));
+    static constexpr size_t oTokIn = align16(oGt + sizeof(T) * D * LDT);
     static constexpr size_t TB = align16(oTokIn + (GN || !CAUSAL ? sizeof(float) * 2 * TT : 0));
     // the rest, relative to its start
     static constexpr size_t rX = 0;  // (the in-tile v.g^T blocks live in each wave's registers)
@@ -2364,9 +2341,9 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr size_t rPair = align16(rHash + HashOps<T, 4>::bytes);
     static constexpr size_t rShare = align16(rPair + PairOps<T>::bytes);
     static constexpr size_t rTok = align16(rShare + (KB > 4 ? WideHash<T, KB>::bytes(NW_) : 0));
-    // GO: the computed (rd, gd) [2][TT]; GC: the waves' shares of sum_s P_Q G [NW_][TT]
-    static constexpr size_t rGs = align16(rTok + (GO ? sizeof(float) * 2 * TT : 0));
-    static constexpr size_t rEnd = align16(rGs + (GC ? sizeof(float) * NW_ * TT : 0));
+    // GN (GC, and GS's pre-pass): the waves' shares of sum_s P_Q G [NW_][TT]
+    static constexpr size_t rGs = rTok;
+    static constexpr size_t rEnd = align16(rGs + (GN ? sizeof(float) * NW_ * TT : 0));
     // two token blocks when they cost no workgroup per CU (160 KiB of LDS):
     // the next tile's rows then go to the other block while this tile still
     // reads its own, and the barrier ahead of that commit goes away
@@ -2375,15 +2352,16 @@ template <typename T, int SP, bool CAUSAL, int KB, bool GN> struct BwdReduceL {
     static constexpr size_t R0 = NB * TB;
     static constexpr size_t oX = R0 + rX, oDproj = R0 + rDproj, oPl = R0 + rPl, oPlLo = R0 + rPlLo, oPlT = R0 + rPlT,
                             oSig = R0 + rSig, oRed = R0 + rRed, oCst = R0 + rCst, oHash = R0 + rHash, oPair = R0 + rPair,
-                            oShare = R0 + rShare, oTok = R0 + rTok, oGs = R0 + rGs;
+                            oShare = R0 + rShare, oGs = R0 + rGs;
     static constexpr size_t bytes = R0 + rEnd;
 };
 
 // GN (global normalisation, causal only): with rd = 1/max(den, eps) and
-// gd = dL/d den per token (GO: gn_token_terms, from the O and dO tiles; GC:
-// from sum_s P_Q G after the tile's G, gn_own_gd), W = P_Q rd,
-// dP_Q = G rd + gd A_s(t), dA = gd P_Q.
-template <typename T, int SP, bool CAUSAL, int KB, bool GN, bool AL = false>
+// gd = dL/d den per token (GC: from sum_s P_Q G after the tile's G; GS: read,
+// as k_gn_terms wrote it from GP's shares), W = P_Q rd, dP_Q = G rd + gd A_s(t),
+// dA = gd P_Q.  GP: the GS pre-pass, which writes this slice's share of
+// sum_s P_Q G per token (gsum) and nothing else.
+template <typename T, int SP, bool CAUSAL, int KB, bool GN, bool AL = false, bool GP = false>
 __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     if (a.inv_temp_ptr) a.inv_temp = *a.inv_temp_ptr;  // uniform scalar load
     static_assert(CAUSAL || !GN, "global normalisation is causal only");
@@ -2394,11 +2372,12 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     // softmax backward reads directly
     constexpr bool PR = pair_tables<KB>();
     constexpr bool HL = hl_ops<T, SP, KB>();  // P_K and W as hi + lo pairs
-    constexpr bool GO = Ly::GO, GC = Ly::GC;   // GN: gd from the O tile / from G
+    constexpr bool GS = Ly::GS, GC = Ly::GC;   // GN: gd read per token / from this kernel's sums
+    static_assert(!GP || GS, "the pre-pass is the bucket-slice instantiations'");
     constexpr int NW_ = Ly::NW_, NTH = 64 * NW_, LDN = Ly::LDN, LDT = Ly::LDT, LDC = Ly::LDC, LDDP = Ly::LDDP;
     __shared__ __align__(16) unsigned char smem[Ly::bytes];
     // this tile's token block (block jt & 1 of two; block 0 of one)
-    T *sQ, *sK, *sV, *sG, *sVt, *sGt, *sO;
+    T *sQ, *sK, *sV, *sG, *sVt, *sGt;
     float *sTokIn;
     auto use_block = [&](int b) {
         unsigned char *tb = smem + b * Ly::TB;
@@ -2408,7 +2387,6 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         sG = (T *)(tb + Ly::oG);
         sVt = (T *)(tb + Ly::oVt);
         sGt = (T *)(tb + Ly::oGt);
-        sO = (T *)(tb + Ly::oO);
         sTokIn = (float *)(tb + Ly::oTokIn);
     };
     T *sDproj = (T *)(smem + Ly::oDproj);
@@ -2436,13 +2414,16 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
     constexpr bool XF = xpart_f32(is_bf16<T>(), SP, KB);
     void *xpart = sliced<T, KB>() ? xpart_at<T, SP, KB>(a.dqpart, z, n, a) : nullptr;
     const int xc0 = ((z * SP) >> KB) * KB;  // first projection column of the slice's tables
-    float *sTok = (float *)(smem + Ly::oTok), *sGs = (float *)(smem + Ly::oGs);
-    const T *op = GO ? (const T *)a.out + stream_off(a.so, n, a.B, a.H) : nullptr;
+    float *sGs = (float *)(smem + Ly::oGs);
     const float *denp = GN ? a.den + (int64_t)n * a.T : nullptr;
-    const float *ddp = (GN || !CAUSAL) && a.dden ? a.dden + (int64_t)n * a.T : nullptr;
-    // one bucket slice writes the per-token terms for k_bwd_out
-    float *rdw = GN && z == 0 ? a.rden + (int64_t)n * a.T : nullptr;
-    float *gdw = GN && z == 0 ? a.gden + (int64_t)n * a.T : nullptr;
+    // the second token row: dden (GS: gd, from k_gn_terms)
+    const float *ddp = GS && !GP       ? a.gden + (int64_t)n * a.T
+                       : (GN || !CAUSAL) && a.dden ? a.dden + (int64_t)n * a.T
+                                                   : nullptr;
+    float *gsp = GP ? a.gsum + ((int64_t)z * a.M * a.B * a.H + n) * a.T : nullptr;
+    // GC writes the per-token terms for k_bwd_out (GS: k_gn_terms does)
+    float *rdw = GC ? a.rden + (int64_t)n * a.T : nullptr;
+    float *gdw = GC ? a.gden + (int64_t)n * a.T : nullptr;
 
     Consts<T> cst;
     cst.init((T *)(smem + Ly::oCst), NTH);
@@ -2482,7 +2463,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
 
     wait_state_loads();
     constexpr int NP = CAUSAL ? 2 : 1;  // transposed tiles: dO (and V)
-    Prefetch<T, NTH, AL> pq_, pk_, po_;  // po_: the O tile (GO)
+    Prefetch<T, NTH, AL> pq_, pk_;
     PrefetchT<T, NTH, NP, AL> pg_;  // non-causal dO
     PrefetchT2<T, NTH, AL, !is_bf16<T>()> pgv_;  // causal dO (first half of the waves) and V
     TokPre pt_;
@@ -2499,7 +2480,6 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
             pg_.template commit<NL>(0, (T *)(tb + Ly::oG), (T *)(tb + Ly::oGt));
         }
         if constexpr (GN) {
-            if constexpr (GO) po_.template commit<NL>((T *)(tb + Ly::oO), nullptr);
             pt_.commit(tin);
         } else if constexpr (!CAUSAL) {
             if (ddp) pt_.commit(tin);
@@ -2515,7 +2495,6 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
             pg_.issue(0, gp, a.sdo.t, (int64_t)j0 * TT, a.T);
         }
         if constexpr (GN) {
-            if constexpr (GO) po_.issue(op, a.so.t, (int64_t)j0 * TT, a.T);
             pt_.issue(denp, ddp, (int64_t)j0 * TT, a.T);
         } else if constexpr (!CAUSAL) {
             if (ddp) pt_.issue(ddp, nullptr, (int64_t)j0 * TT, a.T);
@@ -2539,7 +2518,6 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
                 pg_.issue(0, gp, a.sdo.t, tn, a.T);
             }
             if constexpr (GN) {
-                if constexpr (GO) po_.issue(op, a.so.t, tn, a.T);
                 pt_.issue(denp, ddp, tn, a.T);
             } else if constexpr (!CAUSAL) {
                 if (ddp) pt_.issue(ddp, nullptr, tn, a.T);
@@ -2552,9 +2530,9 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         __syncthreads();
         if constexpr (NB == 2) {
             issue();
-            if (jt > j0) dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
+            if constexpr (!GP)
+                if (jt > j0) dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
         }
-        if constexpr (GO) gn_token_terms<T, NL, NW_>(sG, sO, sTokIn, sTok, a.eps, rdw, gdw, t0, a.T);
         for (int q = w; q < (CAUSAL ? 2 : 1) * pbk.tasks(); q += NW_) {
             const int r = pbk.task(q);
             if (q < pbk.tasks())
@@ -2567,7 +2545,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         // one token block: dQ of the previous tile, from the dproj rows its
         // softmax backward left in LDS, after the projections (they overlap);
         // the next write of sDproj is a barrier away
-        if constexpr (NB == 1)
+        if constexpr (NB == 1 && !GP)
             if (jt > j0) dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dqp, a.sg.t, t0 - TT, a.T, xpart, xc0);
         __syncthreads();
         f32x4 PQ[2], PK[2], Acum[2], W[2], inv[2], tot;
@@ -2594,12 +2572,8 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         float rd[2], gd[2], ae[4];  // ae: A at the tile start (+ eps unless GN)
         for (int e = 0; e < 4; ++e) ae[e] = GN ? (float)a0[e] : (float)a0[e] + a.eps;
         for (int nt = 0; nt < 2; ++nt) {
-            if constexpr (GO) {
-                rd[nt] = sTok[16 * nt + i];
-                gd[nt] = sTok[TT + 16 * nt + i];
-            } else if constexpr (GC) {
-                rd[nt] = 1.0f / fmaxf(sTokIn[16 * nt + i], a.eps);
-            }
+            if constexpr (GN) rd[nt] = 1.0f / fmaxf(sTokIn[16 * nt + i], a.eps);
+            if constexpr (GS) gd[nt] = sTokIn[TT + 16 * nt + i];
             for (int e = 0; e < 4; ++e) {
                 const float A = CAUSAL ? ae[e] + Acum[nt][e] : ae[e];
                 if constexpr (GN) {
@@ -2634,22 +2608,6 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
             }
             Frag<T> Xop[2];
             if constexpr (CAUSAL) x_operands<T, NL>(sV, sG, Xop);
-            if constexpr (GO && is_bf16<T>()) {
-                // The stream's first token sees only its own key, so out_0 = v_0
-                // and dO.out_0 = dO.v_0 exactly: taken as G takes it (the rounded
-                // in-tile product, lane 0's first slot, the same in every wave
-                // and slice) rather than from the stored O, whose rounding does
-                // not cancel against G where den_0 is small
-                if (t0 == 0) {
-                    const float m00 = __builtin_bit_cast(
-                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, (float)Xop[0].v[0]), 0));
-                    if (i == 0) {
-                        const float dn = sTokIn[0];
-                        gd[0] = sTokIn[TT] - (dn >= a.eps ? m00 * rd[0] : 0.f);
-                        if (gdw && w == 0 && g == 0) gdw[0] = gd[0];  // after gn_token_terms' write, same lane
-                    }
-                }
-            }
             for (int nt = 0; nt < 2; ++nt) {
                 f32x4 G = zero4();
                 const Frag<T> g0 = NL::frag_pi(sG, 16 * nt + i, 0), g1 = NL::frag_pi(sG, 16 * nt + i, 1);
@@ -2661,8 +2619,8 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
                 }
                 if constexpr (CAUSAL) mma(G, Pf, Xop[nt]);
                 if constexpr (CAUSAL && HL) mma(G, Pl, Xop[nt]);
-                if constexpr (GC) {
-                    // this wave's share of sum_s P_Q G; dP_Q follows the barrier
+                if constexpr (GC || GP) {
+                    // this wave's share of sum_s P_Q G (GC: dP_Q follows the barrier)
                     Gv[nt] = G;
                     float p = 0.f;
                     for (int e = 0; e < 4; ++e) p += PQ[nt][e] * G[e];
@@ -2693,13 +2651,15 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         }
         // the lane's share of the segment's dA totals (summed over the row's
         // lanes after the walk)
-        if constexpr (!GC)
+        if constexpr (!GC && !GP)
             for (int e = 0; e < 4; ++e) al[e] += (double)(dA[0][e] + dA[1][e]);
         // U^T[d][s] += sum_t g[t][d] W[t][s]; carry B^T[d][s] += sum_t V[t][d] P_K[t][s]
         for (int md = 0; md < 4; ++md) {
-            const Frag<T> go = col_operand<T, NL>(sG, sGt, md);
-            mma(Ut[md], go, Wf);
-            if constexpr (HL) mma(Ut[md], go, Wl);
+            if constexpr (!GP) {
+                const Frag<T> go = col_operand<T, NL>(sG, sGt, md);
+                mma(Ut[md], go, Wf);
+                if constexpr (HL) mma(Ut[md], go, Wl);
+            }
             if constexpr (CAUSAL) {
                 const Frag<T> vo = col_operand<T, NL>(sV, sVt, md);
                 mma(Bt[md], vo, Pf);
@@ -2728,7 +2688,17 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
             }
             for (int e = 0; e < 4; ++e) al[e] += (double)(dA[0][e] + dA[1][e]);
         }
-        if constexpr (KB <= 4) {
+        if constexpr (GP) {
+            __syncthreads();  // every wave's share of this slice's sum_s P_Q G
+            if (w == 0 && g == 0)
+                for (int nt = 0; nt < 2; ++nt) {
+                    const int t = 16 * nt + i;
+                    float sq = 0.f;
+#pragma unroll
+                    for (int v = 0; v < NW_; ++v) sq += sGs[v * TT + t];
+                    if (t < tile_rows(t0, a.T)) gsp[t0 + t] = sq;
+                }
+        } else if constexpr (KB <= 4) {
             tsum += softhash_bwd<KB, T>(PQ, dPQ, sSpQ, sSmQ, sThQ, sg, a.L, a.inv_temp, sDproj, ho);
         } else {
             softhash_share<KB, T>(PQ, dPQ, wh, sShare);
@@ -2742,6 +2712,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         if constexpr (NB == 1) __syncthreads();
         commit(NB == 2 ? (int)((jt + 1) & 1) : 0);
     }
+    if constexpr (GP) return;  // the pre-pass writes gsum only
     if (j0 < j1) {
         if constexpr (NB == 2) __syncthreads();  // every wave's dproj rows of the last tile
         dx_store<T, NW_, XC, AL, XF>(sDproj, sPlT, dqp, a.sg.t, (int64_t)(j1 - 1) * TT, a.T, xpart, xc0);
@@ -3828,6 +3799,21 @@ __global__ __launch_bounds__(ELEM_THREADS) void k_slice_sum_gn(const T *part, co
         const float rc = 1.0f / fmaxf(dn, eps);
         store4<T>(out + stream_off(so, (int)n, B, H) + t * so.t + d0, acc * rc);
         if (d0 == 0) den[nt] = dn;
+    }
+}
+
+// Bucket-slice GN backward: per token j = n T + t, the slices' shares of
+// S = sum_s P_Q G added in slice order, rd = 1 / max(den, eps) and
+// gd = dden - [den >= eps] rd^2 S, read by the second k_bwd_reduce pass and
+// by k_bwd_out.
+__global__ __launch_bounds__(ELEM_THREADS) void k_gn_terms(const float *gsum, int nslice, int64_t NT, const float *den,
+                                                           const float *dden, float eps, float *rden, float *gden) {
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < NT; j += (int64_t)gridDim.x * blockDim.x) {
+        float sq = gsum[j];
+        for (int z = 1; z < nslice; ++z) sq += gsum[z * NT + j];
+        const float dn = den[j], rd = 1.0f / fmaxf(dn, eps);
+        rden[j] = rd;
+        gden[j] = (dden ? dden[j] : 0.f) - (dn >= eps ? rd * rd * sq : 0.f);
     }
 }
 

@@ -182,9 +182,9 @@ def stream_gn(q, k, v, g, h, planes, beta, floor, on=(), hl=False, own_gd=True, 
     `stream`, placed where the GN kernels round:
       forward   W = P_Q as an operand (outputs, Sc), den from fp32 P_Q and A;
       backward  G with B as a hi + lo pair and the in-tile M rounded (tri);
-                gd = h - [den >= floor] rd^2 sum_s P_Q G (own_gd: bf16 with
-                K <= 4) or h - [den >= floor] rd dO.y with y the stored
-                output, except token 0, which takes dO.v_0 as G does (M[0, 0]);
+                gd = h - [den >= floor] rd^2 sum_s P_Q G, as the kernels form
+                it (own_gd; own_gd=False: h - [den >= floor] rd dO.y with y the
+                stored output, the form the kernels avoid);
                 W = P_Q rd as an operand in U, Sc2 and dV, an fp32-accurate
                 pair in dP_K's in-tile term for tables up to 7 bits.
     slice_parts: the bucket-slice kernels round each 128-bucket slice's
@@ -240,10 +240,7 @@ def stream_gn(q, k, v, g, h, planes, beta, floor, on=(), hl=False, own_gd=True, 
         if own_gd:
             gd = h[a:b] - act[a:b] * rd[a:b] ** 2 * (PQ[a:b] * G).sum(1)
         else:
-            dot = (gg * y[a:b]).sum(1)
-            if a == 0:
-                dot[0] = M[0, 0]
-            gd = h[a:b] - act[a:b] * rd[a:b] * dot
+            gd = h[a:b] - act[a:b] * rd[a:b] * (gg * y[a:b]).sum(1)
         dPQ = G * rd[a:b, None] + gd[:, None] * At
         dA = gd[:, None] * PQ[a:b]
         W = PQ[a:b] * rd[a:b, None]

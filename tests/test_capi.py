@@ -291,7 +291,8 @@ def test_prefix_mean_argument_checks():
 # ------------------------------------------------- global normalisation (F2)
 def test_global_workspace_sizes():
     """F2 adds per-token fp32 buffers: den partials per slice (sliced
-    instantiations, forward) and rden/gden (backward)."""
+    instantiations, forward), rden/gden (backward) and, sliced, each slice's
+    share of sum_s P_Q dO.B_s (backward)."""
     lib = _lib.load()
     d = _desc()
     N, T = 8, 1 << 20
@@ -301,6 +302,8 @@ def test_global_workspace_sizes():
     d = _desc(dtype=_lib.RACE_DTYPE_F32, T=4096)      # 4 slices of 32 buckets
     f1 = lib.race_fwd_workspace_bytes(ctypes.byref(d))
     assert lib.race_fwd_global_workspace_bytes(ctypes.byref(d)) == f1 + 4 * N * 4096 * 4
+    b1 = lib.race_bwd_workspace_bytes(ctypes.byref(d))
+    assert lib.race_bwd_global_workspace_bytes(ctypes.byref(d)) == b1 + (2 + 4) * N * 4096 * 4
 
 
 @pytest.mark.parametrize("field,value,code,msg", [

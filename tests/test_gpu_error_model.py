@@ -54,9 +54,8 @@ def test_gpu_error_is_the_modelled_rounding(dev, name, kw, hl):
 
 
 # The globally normalised operator (F2): the restatement's stream_gn, with
-# dL/d den from the kernel's own sums (own_gd: bf16, K <= 4) or from the
-# stored output (bucket slices, whose partial numerators and dV round per
-# slice).  beta up to 3 and an upstream den gradient in some cases; planes per
+# dL/d den from the kernels' own sums (in one workgroup, or over bucket
+# slices, whose partial numerators and dV round per slice).  beta up to 3 and an upstream den gradient in some cases; planes per
 # estimator.  8-bit slices are left out: there the restatement's output error
 # is an upper bound (its in-tile blocks round where the kernel's error is
 # smaller: 5.3e-3 modelled, 1.9e-3 measured on K=8 L=4).
@@ -66,7 +65,7 @@ GN_CASES = [
     ("gn_K4L8_vmean", dict(M=1, B=1, T=256, H=2, L=8, K=4, v_shift=0.5), 1.0, False, False, True, False, 0),
     ("gn_K4L6_beta2", dict(M=2, B=1, T=318, H=3, L=6, K=4, share_planes=False), 2.0, False, False, True, False, 3),
     ("gn_K2L5_pairs_beta3", dict(M=1, B=1, T=200, H=2, L=5, K=2), 3.0, True, True, True, False, 2),
-    ("gn_K6L3_slices", dict(M=2, B=1, T=318, H=3, L=3, K=6, share_planes=False), 2.0, False, False, False, True, 3),
+    ("gn_K6L3_slices", dict(M=2, B=1, T=318, H=3, L=3, K=6, share_planes=False), 2.0, False, False, True, True, 3),
 ]
 
 

@@ -96,10 +96,9 @@ def test_global_parity(dev, name, kw, beta, seg, floor, with_dden):
 # Token 0 sees only its own key, so out_0 = v_0 whatever P_Q is, and with no
 # den gradient the exact dq_0 is zero.  Where den_0 is small (sharp beta, q_0
 # and k_0 in different buckets) any rounding that keeps dP_Q[0][s] from
-# cancelling shows up at full size in dq_0: the bf16 kernels with every bucket
-# in one workgroup (K <= 4) form dL/d den from their own G, sum_s P_Q G, and
-# the bucket-slice kernels (K >= 5) take token 0's dO . out as dO . v_0 rounded
-# as G rounds it; either way the cancellation holds to fp32 rounding.  Cases:
+# cancelling shows up at full size in dq_0: the kernels form dL/d den from
+# their own G, sum_s P_Q G (bucket slices: summed over the slices by a
+# pre-pass), for which the cancellation holds to fp32 rounding.  Cases:
 # T not a multiple of 32 over several segments (and one whole-tile case),
 # independent planes.
 FIRST_TOKEN_CASES = [
