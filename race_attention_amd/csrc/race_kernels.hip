@@ -2536,7 +2536,7 @@ __global__ __launch_bounds__(threads_of(SP), 2) void k_bwd_reduce(Args a) {
         for (int q = w; q < (CAUSAL ? 2 : 1) * pbk.tasks(); q += NW_) {
             const int r = pbk.task(q);
             if (q < pbk.tasks())
-                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, sThQ,
+                project_tile<T, NL>(sQ, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpQ, sSmQ, GP ? nullptr : sThQ,
                                     (AL && q == w) ? &pcw : nullptr);
             else
                 project_tile<T, NL, PR>(sK, sPl, sPlLo, pbk.mc(r), r & 1, a.inv_temp, sSpK, sSmK, nullptr,
