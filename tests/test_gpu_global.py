@@ -130,6 +130,27 @@ def test_global_first_token_gradient(dev, name, kw, beta):
     _compare("first_token_" + name, gpu, ref, TOL[q.dtype])
 
 
+@pytest.mark.parametrize("kw", [dict(T=200, H=2, L=8, K=4), dict(T=150, H=2, L=3, K=6),
+                                dict(T=96, H=1, L=4, K=3, dtype=torch.float32, unit=False)],
+                         ids=["K4_one_workgroup", "K6_slices", "fp32_slices"])
+def test_global_backward_does_not_read_out(dev, kw):
+    """dL/d den comes from the kernels' own sums, so the backward's result is
+    the same, bit for bit, when the out argument holds NaN instead of the
+    forward's output."""
+    from race_attention_amd.functional import race_global_bwd_raw, race_global_fwd_raw
+    q, k, v, do, planes = [x.to(dev) for x in make_case(seed=9, **kw)]
+    M, B, T, H, _ = q.shape
+    dden = torch.randn(M, B, H, T, generator=torch.Generator().manual_seed(2)).to(dev)
+    L, K = kw["L"], kw["K"]
+    out, den, state = race_global_fwd_raw(q, k, v, planes, L=L, K=K, beta=2.0)
+    a = race_global_bwd_raw(q, k, v, planes, out, den, do, dden, state, L=L, K=K, beta=2.0)
+    b = race_global_bwd_raw(q, k, v, planes, torch.full_like(out, float("nan")), den, do, dden, state, L=L, K=K,
+                            beta=2.0)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
 def test_global_deterministic(dev):
     q, k, v, do, planes = make_case(B=1, T=333, H=2, L=8, K=4, seed=3)
     dden = torch.randn(1, 1, 2, 333, generator=torch.Generator().manual_seed(1))
